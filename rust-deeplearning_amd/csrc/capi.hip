@@ -1,0 +1,439 @@
+// capi.hip -- the extern "C" boundary of librdlquant.so (include/rdl_quant.h).
+//
+// Argument checks follow the reference's error behaviour
+// (rustml/quant/main/src/core/quantize.rs:208-213, 272-277, 333-338: K % 32 is
+// checked first and reported as QuantError::BlockAlignment) and add the
+// slice-length checks the reference leaves to a panic.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/rdl_quant.h"
+#include "rdl_internal.hpp"
+
+using rdl::FloatRec;
+using rdl::NativeRec;
+using rdl::WType;
+
+struct rdl_weight {
+    void* dev;
+    size_t len;
+    WType type;
+    size_t n, k;
+    bool owned;
+};
+
+namespace {
+
+thread_local std::string g_err;
+
+rdl_status fail(rdl_status st, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return st;
+}
+
+rdl_status ok() {
+    g_err.clear();
+    return RDL_OK;
+}
+
+#define HIP_TRY(expr)                                                                     \
+    do {                                                                                  \
+        hipError_t e_ = (expr);                                                           \
+        if (e_ != hipSuccess)                                                             \
+            return fail(RDL_ERR_HIP, "%s failed: %s", #expr, hipGetErrorString(e_));      \
+    } while (0)
+
+const char* type_name(WType t) {
+    switch (t) {
+        case WType::Q4_0: return "Q4_0";
+        case WType::Q4_1: return "Q4_1";
+        case WType::Q8_0: return "Q8_0";
+        case WType::Q4_K: return "Q4_K";
+    }
+    return "?";
+}
+
+bool valid_type(int32_t d) {
+    return d == RDL_DTYPE_Q4_0 || d == RDL_DTYPE_Q4_1 || d == RDL_DTYPE_Q8_0 || d == RDL_DTYPE_Q4_K;
+}
+
+// Visible gfx950 devices; 0 without a GPU.
+int count_devices() {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    int good = 0;
+    for (int i = 0; i < n; i++) {
+        hipDeviceProp_t p;
+        if (hipGetDeviceProperties(&p, i) == hipSuccess && strncmp(p.gcnArchName, "gfx950", 6) == 0)
+            good++;
+    }
+    return good;
+}
+
+rdl_status require_device() {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0)
+        return fail(RDL_ERR_NO_DEVICE, "no HIP device is visible");
+    int cur = 0;
+    if (hipGetDevice(&cur) != hipSuccess) return fail(RDL_ERR_NO_DEVICE, "hipGetDevice failed");
+    hipDeviceProp_t p;
+    if (hipGetDeviceProperties(&p, cur) != hipSuccess)
+        return fail(RDL_ERR_NO_DEVICE, "hipGetDeviceProperties failed");
+    if (strncmp(p.gcnArchName, "gfx950", 6) != 0)
+        return fail(RDL_ERR_NO_DEVICE, "device %d is %s, this library is built for gfx950", cur,
+                    p.gcnArchName);
+    return RDL_OK;
+}
+
+// Shape checks shared by every matmul entry point.
+rdl_status check_matmul(WType t, const float* x, size_t x_len, const uint8_t* w, size_t w_len,
+                        size_t m, size_t k, size_t n, const void* y, size_t y_len) {
+    const size_t be = rdl::block_elems(t);
+    if (k % be != 0)
+        return fail(RDL_ERR_BLOCK_ALIGNMENT, "in_features %zu not divisible by %s block size %zu", k,
+                    type_name(t), be);
+    // With no output rows or columns the reference never slices its inputs.
+    if (m == 0 || n == 0) return RDL_OK;
+    const size_t need_w = n * (k / be) * rdl::block_bytes(t);
+    if (w_len < need_w)
+        return fail(RDL_ERR_SHAPE_MISMATCH, "weight bytes: expected %zu, got %zu", need_w, w_len);
+    if (x_len < m * k)
+        return fail(RDL_ERR_SHAPE_MISMATCH, "input length: expected %zu, got %zu", m * k, x_len);
+    if (y_len < m * n)
+        return fail(RDL_ERR_SHAPE_MISMATCH, "output length: expected %zu, got %zu", m * n, y_len);
+    if ((m * k && !x) || (need_w && !w) || (m * n && !y))
+        return fail(RDL_ERR_NULL_POINTER, "NULL buffer with non-zero length");
+    return RDL_OK;
+}
+
+size_t rec_bytes(bool native, size_t m, size_t k) {
+    return m * (k / rdl::QK) * (native ? sizeof(NativeRec) : sizeof(FloatRec));
+}
+
+// Prepare activations and run the product on `s`; xrec must hold rec_bytes().
+rdl_status run_linear(WType t, bool native, const uint8_t* w_dev, size_t n, size_t k,
+                      const float* x_dev, size_t m, float* y_dev, void* xrec, hipStream_t s) {
+    if (m == 0 || n == 0) return RDL_OK;
+    // k == 0: no blocks; the GEMV then writes zeros (empty dot, as in the reference).
+    if (k == 0) {
+        HIP_TRY(rdl::launch_gemv(t, native, w_dev, n, k, xrec, m, y_dev, s));
+        return RDL_OK;
+    }
+    if (native)
+        HIP_TRY(rdl::launch_prep_native(x_dev, m, k, (NativeRec*)xrec, nullptr, nullptr, s));
+    else
+        HIP_TRY(rdl::launch_prep_float(x_dev, m, k, (FloatRec*)xrec, s));
+    HIP_TRY(rdl::launch_gemv(t, native, w_dev, n, k, xrec, m, y_dev, s));
+    return RDL_OK;
+}
+
+// RAII device buffer for the synchronous host entry points.
+struct DevBuf {
+    void* p = nullptr;
+    ~DevBuf() {
+        if (p) (void)hipFree(p);
+    }
+    hipError_t alloc(size_t bytes) { return hipMalloc(&p, bytes ? bytes : 4); }
+};
+
+rdl_status host_matmul(WType t, bool native, const float* x, size_t x_len, const uint8_t* w,
+                       size_t w_len, size_t m, size_t k, size_t n, float* y, size_t y_len) {
+    rdl_status st = check_matmul(t, x, x_len, w, w_len, m, k, n, y, y_len);
+    if (st != RDL_OK) return st;
+    if (m == 0 || n == 0) return ok();
+    if ((st = require_device()) != RDL_OK) return st;
+    const size_t wb = n * (k / rdl::block_elems(t)) * rdl::block_bytes(t);
+    DevBuf dx, dw, dy, dr;
+    HIP_TRY(dx.alloc(m * k * sizeof(float)));
+    HIP_TRY(dw.alloc(wb + 64));
+    HIP_TRY(dy.alloc(m * n * sizeof(float)));
+    HIP_TRY(dr.alloc(rec_bytes(native, m, k)));
+    HIP_TRY(hipMemcpy(dx.p, x, m * k * sizeof(float), hipMemcpyHostToDevice));
+    HIP_TRY(hipMemcpy(dw.p, w, wb, hipMemcpyHostToDevice));
+    st = run_linear(t, native, (const uint8_t*)dw.p, n, k, (const float*)dx.p, m, (float*)dy.p,
+                    dr.p, nullptr);
+    if (st != RDL_OK) return st;
+    HIP_TRY(hipMemcpy(y, dy.p, m * n * sizeof(float), hipMemcpyDeviceToHost));
+    return ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* rdl_status_string(rdl_status s) {
+    switch (s) {
+        case RDL_OK: return "ok";
+        case RDL_ERR_DTYPE_MISMATCH: return "dtype mismatch";
+        case RDL_ERR_SHAPE_MISMATCH: return "shape mismatch";
+        case RDL_ERR_BLOCK_ALIGNMENT: return "block alignment error";
+        case RDL_ERR_INVALID_DATA: return "invalid data";
+        case RDL_ERR_NULL_POINTER: return "null pointer";
+        case RDL_ERR_HIP: return "HIP runtime error";
+        case RDL_ERR_NO_DEVICE: return "no gfx950 device";
+        case RDL_ERR_UNSUPPORTED: return "unsupported shape";
+    }
+    return "unknown status";
+}
+
+const char* rdl_last_error(void) { return g_err.c_str(); }
+
+const char* rdl_version(void) { return "rdlquant 0.1.0 (gfx950)"; }
+
+int32_t rdl_device_count(void) { return count_devices(); }
+
+rdl_status rdl_matmul_f32_q8(const float* x, size_t x_len, const uint8_t* w, size_t w_len,
+                             size_t m, size_t k, size_t n, float* y, size_t y_len) {
+    return host_matmul(WType::Q8_0, false, x, x_len, w, w_len, m, k, n, y, y_len);
+}
+rdl_status rdl_matmul_f32_q4(const float* x, size_t x_len, const uint8_t* w, size_t w_len,
+                             size_t m, size_t k, size_t n, float* y, size_t y_len) {
+    return host_matmul(WType::Q4_0, false, x, x_len, w, w_len, m, k, n, y, y_len);
+}
+rdl_status rdl_matmul_f32_q4_native(const float* x, size_t x_len, const uint8_t* w, size_t w_len,
+                                    size_t m, size_t k, size_t n, float* y, size_t y_len) {
+    return host_matmul(WType::Q4_0, true, x, x_len, w, w_len, m, k, n, y, y_len);
+}
+rdl_status rdl_matmul_f32_q4_1(const float* x, size_t x_len, const uint8_t* w, size_t w_len,
+                               size_t m, size_t k, size_t n, float* y, size_t y_len) {
+    return host_matmul(WType::Q4_1, false, x, x_len, w, w_len, m, k, n, y, y_len);
+}
+rdl_status rdl_matmul_f32_q4_1_native(const float* x, size_t x_len, const uint8_t* w,
+                                      size_t w_len, size_t m, size_t k, size_t n, float* y,
+                                      size_t y_len) {
+    return host_matmul(WType::Q4_1, true, x, x_len, w, w_len, m, k, n, y, y_len);
+}
+rdl_status rdl_matmul_f32_q4_k(const float* x, size_t x_len, const uint8_t* w, size_t w_len,
+                               size_t m, size_t k, size_t n, float* y, size_t y_len) {
+    return host_matmul(WType::Q4_K, false, x, x_len, w, w_len, m, k, n, y, y_len);
+}
+
+rdl_status rdl_quantize_row_q8_0(const float* input, size_t input_len, uint8_t* output,
+                                 size_t output_len, float* scales, size_t scales_len) {
+    if (input_len % rdl::QK != 0)
+        return fail(RDL_ERR_BLOCK_ALIGNMENT, "Q8_0 requires element count divisible by 32, got %zu",
+                    input_len);
+    const size_t nb = input_len / rdl::QK;
+    if (output_len < nb * rdl::Q8_0_BYTES)
+        return fail(RDL_ERR_SHAPE_MISMATCH, "output bytes: expected %zu, got %zu",
+                    nb * rdl::Q8_0_BYTES, output_len);
+    if (scales_len < nb)
+        return fail(RDL_ERR_SHAPE_MISMATCH, "scales length: expected %zu, got %zu", nb, scales_len);
+    if (nb == 0) return ok();
+    if (!input || !output || !scales) return fail(RDL_ERR_NULL_POINTER, "NULL buffer");
+    rdl_status st = require_device();
+    if (st != RDL_OK) return st;
+    DevBuf dx, dq, ds, dr;
+    HIP_TRY(dx.alloc(input_len * sizeof(float)));
+    HIP_TRY(dq.alloc(nb * rdl::Q8_0_BYTES));
+    HIP_TRY(ds.alloc(nb * sizeof(float)));
+    HIP_TRY(dr.alloc(nb * sizeof(NativeRec)));
+    HIP_TRY(hipMemcpy(dx.p, input, input_len * sizeof(float), hipMemcpyHostToDevice));
+    HIP_TRY(rdl::launch_prep_native((const float*)dx.p, 1, input_len, (NativeRec*)dr.p,
+                                    (uint8_t*)dq.p, (float*)ds.p, nullptr));
+    HIP_TRY(hipMemcpy(output, dq.p, nb * rdl::Q8_0_BYTES, hipMemcpyDeviceToHost));
+    HIP_TRY(hipMemcpy(scales, ds.p, nb * sizeof(float), hipMemcpyDeviceToHost));
+    return ok();
+}
+
+rdl_status rdl_q4_0_q8_0_block_dots(const float* x, size_t x_len, const uint8_t* w, size_t w_len,
+                                    size_t m, size_t k, size_t n, int32_t* partials,
+                                    size_t partials_len) {
+    rdl_status st = check_matmul(WType::Q4_0, x, x_len, w, w_len, m, k, n, partials,
+                                 partials_len);
+    if (st != RDL_OK) return st;
+    const size_t nb = k / rdl::QK;
+    if (partials_len < m * n * nb)
+        return fail(RDL_ERR_SHAPE_MISMATCH, "partials length: expected %zu, got %zu", m * n * nb,
+                    partials_len);
+    if (m * n * nb == 0) return ok();
+    if ((st = require_device()) != RDL_OK) return st;
+    DevBuf dx, dw, dp, dr;
+    HIP_TRY(dx.alloc(m * k * sizeof(float)));
+    HIP_TRY(dw.alloc(n * nb * rdl::Q4_0_BYTES + 64));
+    HIP_TRY(dp.alloc(m * n * nb * sizeof(int32_t)));
+    HIP_TRY(dr.alloc(m * nb * sizeof(NativeRec)));
+    HIP_TRY(hipMemcpy(dx.p, x, m * k * sizeof(float), hipMemcpyHostToDevice));
+    HIP_TRY(hipMemcpy(dw.p, w, n * nb * rdl::Q4_0_BYTES, hipMemcpyHostToDevice));
+    HIP_TRY(rdl::launch_prep_native((const float*)dx.p, m, k, (NativeRec*)dr.p, nullptr, nullptr,
+                                    nullptr));
+    for (size_t r = 0; r < m; r++)
+        HIP_TRY(rdl::launch_q4_0_block_dots((const uint8_t*)dw.p, n, k,
+                                            (const NativeRec*)dr.p + r * nb,
+                                            (int32_t*)dp.p + r * n * nb, nullptr));
+    HIP_TRY(hipMemcpy(partials, dp.p, m * n * nb * sizeof(int32_t), hipMemcpyDeviceToHost));
+    return ok();
+}
+
+rdl_status rdl_weight_upload(const uint8_t* bytes, size_t len, int32_t dtype,
+                             size_t out_features, size_t in_features, rdl_weight** out) {
+    if (!out) return fail(RDL_ERR_NULL_POINTER, "out is NULL");
+    *out = nullptr;
+    if (!valid_type(dtype)) return fail(RDL_ERR_DTYPE_MISMATCH, "unsupported dtype %d", dtype);
+    const WType t = (WType)dtype;
+    const size_t be = rdl::block_elems(t);
+    if (in_features % be)
+        return fail(RDL_ERR_BLOCK_ALIGNMENT, "in_features %zu not divisible by %s block size %zu",
+                    in_features, type_name(t), be);
+    const size_t need = out_features * (in_features / be) * rdl::block_bytes(t);
+    if (len < need) return fail(RDL_ERR_SHAPE_MISMATCH, "weight bytes: expected %zu, got %zu", need, len);
+    if (need && !bytes) return fail(RDL_ERR_NULL_POINTER, "bytes is NULL");
+    rdl_status st = require_device();
+    if (st != RDL_OK) return st;
+    void* d = nullptr;
+    HIP_TRY(hipMalloc(&d, need + 64));
+    if (need) {
+        hipError_t e = hipMemcpy(d, bytes, need, hipMemcpyHostToDevice);
+        if (e != hipSuccess) {
+            (void)hipFree(d);
+            return fail(RDL_ERR_HIP, "hipMemcpy failed: %s", hipGetErrorString(e));
+        }
+    }
+    *out = new rdl_weight{d, need, t, out_features, in_features, true};
+    return ok();
+}
+
+rdl_status rdl_weight_wrap_device(const void* dev_bytes, size_t len, int32_t dtype,
+                                  size_t out_features, size_t in_features, rdl_weight** out) {
+    if (!out) return fail(RDL_ERR_NULL_POINTER, "out is NULL");
+    *out = nullptr;
+    if (!valid_type(dtype)) return fail(RDL_ERR_DTYPE_MISMATCH, "unsupported dtype %d", dtype);
+    const WType t = (WType)dtype;
+    const size_t be = rdl::block_elems(t);
+    if (in_features % be)
+        return fail(RDL_ERR_BLOCK_ALIGNMENT, "in_features %zu not divisible by %s block size %zu",
+                    in_features, type_name(t), be);
+    const size_t need = out_features * (in_features / be) * rdl::block_bytes(t);
+    if (len < need) return fail(RDL_ERR_SHAPE_MISMATCH, "weight bytes: expected %zu, got %zu", need, len);
+    if (need && !dev_bytes) return fail(RDL_ERR_NULL_POINTER, "dev_bytes is NULL");
+    if (t == WType::Q4_K && ((uintptr_t)dev_bytes & 15))
+        return fail(RDL_ERR_INVALID_DATA, "Q4_K device bytes must be 16-byte aligned");
+    if ((uintptr_t)dev_bytes & 3)
+        return fail(RDL_ERR_INVALID_DATA, "device bytes must be 4-byte aligned");
+    *out = new rdl_weight{const_cast<void*>(dev_bytes), need, t, out_features, in_features, false};
+    return ok();
+}
+
+rdl_status rdl_weight_free(rdl_weight* w) {
+    if (!w) return ok();
+    if (w->owned && w->dev) (void)hipFree(w->dev);
+    delete w;
+    return ok();
+}
+
+rdl_status rdl_linear_forward_dev(const rdl_weight* w, const float* x_dev, size_t m, float* y_dev,
+                                  int32_t mode, void* stream) {
+    if (!w) return fail(RDL_ERR_NULL_POINTER, "weight handle is NULL");
+    if (mode != RDL_MODE_FLOAT && mode != RDL_MODE_NATIVE)
+        return fail(RDL_ERR_INVALID_DATA, "unknown mode %d", mode);
+    if (m == 0 || w->n == 0) return ok();
+    if (!x_dev || !y_dev) return fail(RDL_ERR_NULL_POINTER, "NULL activation pointer");
+    // Linear::forward honours use_native_q4 only for Q4_0 / Q4_1 (linear.rs:128-153).
+    const bool native = mode == RDL_MODE_NATIVE && (w->type == WType::Q4_0 || w->type == WType::Q4_1);
+    hipStream_t s = (hipStream_t)stream;
+    void* rec = nullptr;
+    const size_t rb = rec_bytes(native, m, w->k);
+    if (rb) HIP_TRY(hipMallocAsync(&rec, rb, s));
+    rdl_status st = run_linear(w->type, native, (const uint8_t*)w->dev, w->n, w->k, x_dev, m, y_dev,
+                               rec, s);
+    if (rec) {
+        hipError_t e = hipFreeAsync(rec, s);
+        if (st == RDL_OK && e != hipSuccess)
+            return fail(RDL_ERR_HIP, "hipFreeAsync failed: %s", hipGetErrorString(e));
+    }
+    return st == RDL_OK ? ok() : st;
+}
+
+size_t rdl_activation_record_bytes(size_t m, size_t k, int32_t mode) {
+    return rec_bytes(mode == RDL_MODE_NATIVE, m, k);
+}
+
+rdl_status rdl_prepare_activations_dev(const float* x_dev, size_t m, size_t k, int32_t mode,
+                                       void* rec_dev, void* stream) {
+    if (mode != RDL_MODE_FLOAT && mode != RDL_MODE_NATIVE)
+        return fail(RDL_ERR_INVALID_DATA, "unknown mode %d", mode);
+    if (k % rdl::QK)
+        return fail(RDL_ERR_BLOCK_ALIGNMENT, "activation length %zu not divisible by 32", k);
+    if (m * k == 0) return ok();
+    if (!x_dev || !rec_dev) return fail(RDL_ERR_NULL_POINTER, "NULL device pointer");
+    if ((uintptr_t)rec_dev & 15) return fail(RDL_ERR_INVALID_DATA, "record buffer must be 16-byte aligned");
+    hipStream_t s = (hipStream_t)stream;
+    if (mode == RDL_MODE_NATIVE)
+        HIP_TRY(rdl::launch_prep_native(x_dev, m, k, (NativeRec*)rec_dev, nullptr, nullptr, s));
+    else
+        HIP_TRY(rdl::launch_prep_float(x_dev, m, k, (FloatRec*)rec_dev, s));
+    return ok();
+}
+
+rdl_status rdl_linear_prepared_dev(const rdl_weight* w, const void* rec_dev, size_t m, float* y_dev,
+                                   int32_t mode, void* stream) {
+    if (!w) return fail(RDL_ERR_NULL_POINTER, "weight handle is NULL");
+    if (mode != RDL_MODE_FLOAT && mode != RDL_MODE_NATIVE)
+        return fail(RDL_ERR_INVALID_DATA, "unknown mode %d", mode);
+    const bool native = mode == RDL_MODE_NATIVE;
+    if (native && w->type != WType::Q4_0 && w->type != WType::Q4_1)
+        return fail(RDL_ERR_DTYPE_MISMATCH, "native records apply to Q4_0 / Q4_1 weights only");
+    if (m == 0 || w->n == 0) return ok();
+    if (!y_dev || (w->k && !rec_dev)) return fail(RDL_ERR_NULL_POINTER, "NULL device pointer");
+    HIP_TRY(rdl::launch_gemv(w->type, native, (const uint8_t*)w->dev, w->n, w->k, rec_dev, m, y_dev,
+                             (hipStream_t)stream));
+    return ok();
+}
+
+rdl_status rdl_quantize_row_q8_0_dev(const float* x_dev, size_t n, uint8_t* out_dev,
+                                     float* scales_dev, void* stream) {
+    if (n % rdl::QK)
+        return fail(RDL_ERR_BLOCK_ALIGNMENT, "Q8_0 requires element count divisible by 32, got %zu", n);
+    if (n == 0) return ok();
+    if (!x_dev || !out_dev) return fail(RDL_ERR_NULL_POINTER, "NULL device pointer");
+    hipStream_t s = (hipStream_t)stream;
+    void* rec = nullptr;
+    HIP_TRY(hipMallocAsync(&rec, (n / rdl::QK) * sizeof(NativeRec), s));
+    hipError_t e = rdl::launch_prep_native(x_dev, 1, n, (NativeRec*)rec, out_dev, scales_dev, s);
+    hipError_t e2 = hipFreeAsync(rec, s);
+    HIP_TRY(e);
+    HIP_TRY(e2);
+    return ok();
+}
+
+rdl_status rdl_dequantize_rows_dev(const rdl_weight* w, const int32_t* row_ids_dev, size_t n_rows,
+                                   float* out_dev, void* stream) {
+    if (!w) return fail(RDL_ERR_NULL_POINTER, "weight handle is NULL");
+    if (w->type == WType::Q4_K)
+        return fail(RDL_ERR_DTYPE_MISMATCH, "row dequantization supports Q4_0, Q4_1, Q8_0");
+    if (n_rows == 0) return ok();
+    if (!row_ids_dev || !out_dev) return fail(RDL_ERR_NULL_POINTER, "NULL device pointer");
+    HIP_TRY(rdl::launch_dequant_rows(w->type, (const uint8_t*)w->dev, w->n, w->k, row_ids_dev,
+                                     n_rows, out_dev, (hipStream_t)stream));
+    return ok();
+}
+
+rdl_status rdl_q4_0_q8_0_block_dots_dev(const rdl_weight* w, const float* x_dev,
+                                        int32_t* partials_dev, void* stream) {
+    if (!w) return fail(RDL_ERR_NULL_POINTER, "weight handle is NULL");
+    if (w->type != WType::Q4_0) return fail(RDL_ERR_DTYPE_MISMATCH, "weight must be Q4_0");
+    if (w->n == 0 || w->k == 0) return ok();
+    if (!x_dev || !partials_dev) return fail(RDL_ERR_NULL_POINTER, "NULL device pointer");
+    hipStream_t s = (hipStream_t)stream;
+    void* rec = nullptr;
+    HIP_TRY(hipMallocAsync(&rec, rec_bytes(true, 1, w->k), s));
+    hipError_t e = rdl::launch_prep_native(x_dev, 1, w->k, (NativeRec*)rec, nullptr, nullptr, s);
+    if (e == hipSuccess)
+        e = rdl::launch_q4_0_block_dots((const uint8_t*)w->dev, w->n, w->k, (const NativeRec*)rec,
+                                        partials_dev, s);
+    hipError_t e2 = hipFreeAsync(rec, s);
+    HIP_TRY(e);
+    HIP_TRY(e2);
+    return ok();
+}
+
+}  // extern "C"

@@ -1,0 +1,93 @@
+// rdl_internal.hpp -- declarations shared by the HIP translation units of
+// librdlquant.so (kernels, launchers and the C ABI).  Not part of the ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace rdl {
+
+// GGUF block geometry (rustml/quant/main/src/api/types.rs:1-17,
+// rustml/gguf/main/src/api/types.rs:54-76).
+constexpr int QK = 32;          // elements per Q4_0 / Q4_1 / Q8_0 block
+constexpr int Q4_0_BYTES = 18;  // [f16 d][16 B nibbles]
+constexpr int Q4_1_BYTES = 20;  // [f16 d][f16 m][16 B nibbles]
+constexpr int Q8_0_BYTES = 34;  // [f16 d][32 x i8]
+constexpr int QK_K = 256;       // elements per Q4_K super-block
+constexpr int Q4_K_BYTES = 144; // [f16 d][f16 dmin][12 B scales][128 B nibbles]
+
+// ---------------------------------------------------------------------------
+// Prepared activations.
+//
+// The GEMV/GEMM kernels never read f32 activations directly: a small pass
+// converts each 32-element block of x into a record the integer dot units
+// (v_dot4_i32_i8) consume.
+//
+// FloatRec (float mode, 128 B): x_j ~= S * (a_j + b_j/256 + c_j/65536) with
+// S = amax/127 and signed 8-bit digits a, b, c (a 24-bit fixed-point code per
+// block; absolute error <= amax * 2^-23 per element).  A block dot against
+// integer weights q_j is then S * (A + (B + C/256)/256) with A = sum q_j a_j,
+// etc., computed exactly in int32.  sa/sb/sc are sum(a), sum(b), sum(c) (for
+// the Q4_0 "-8" offset) and xsum is sum(x_j) in f32 (for Q4_1/Q4_K minimums).
+// A block holding a NaN or Inf gets S = NaN, which makes every output it
+// touches NaN.
+//
+// NativeRec (native mode, 48 B): the Q8_0 quantization of the block exactly as
+// quantize_row_q8_0 (quantize.rs:164-193) produces it: q8 bytes, the
+// f16-rounded scale as f32, and sum(q8).
+// ---------------------------------------------------------------------------
+struct alignas(16) FloatRec {
+    int32_t a[8];
+    int32_t b[8];
+    int32_t c[8];
+    float S;
+    int32_t sa, sb, sc;
+    float xsum;
+    int32_t pad[3];
+};
+static_assert(sizeof(FloatRec) == 128, "FloatRec layout");
+
+struct alignas(16) NativeRec {
+    int32_t q[8];
+    float scale;
+    int32_t qsum;
+    int32_t pad[2];
+};
+static_assert(sizeof(NativeRec) == 48, "NativeRec layout");
+
+enum class WType : int { Q4_0 = 2, Q4_1 = 3, Q8_0 = 8, Q4_K = 12 };
+
+inline size_t block_elems(WType t) { return t == WType::Q4_K ? QK_K : QK; }
+inline size_t block_bytes(WType t) {
+    switch (t) {
+        case WType::Q4_0: return Q4_0_BYTES;
+        case WType::Q4_1: return Q4_1_BYTES;
+        case WType::Q8_0: return Q8_0_BYTES;
+        case WType::Q4_K: return Q4_K_BYTES;
+    }
+    return 0;
+}
+
+// ---- launchers (return hipSuccess or the launch error) --------------------
+
+// x [m, k] f32 -> FloatRec [m, k/32]
+hipError_t launch_prep_float(const float* x, size_t m, size_t k, FloatRec* rec, hipStream_t s);
+// x [m, k] f32 -> NativeRec [m, k/32]; optionally also the Q8_0 bytes
+// [m, k/32 * 34] and the f32 scales [m, k/32] of quantize_row_q8_0.
+hipError_t launch_prep_native(const float* x, size_t m, size_t k, NativeRec* rec,
+                              uint8_t* q8_bytes, float* scales, hipStream_t s);
+
+// y[m, n] = x . W^T from prepared activations, one GEMV per activation row.
+hipError_t launch_gemv(WType t, bool native, const uint8_t* w, size_t n, size_t k,
+                       const void* xrec, size_t m, float* y, hipStream_t s);
+
+// int32 block partials of the Q4_0 x Q8_0 path for one activation row.
+hipError_t launch_q4_0_block_dots(const uint8_t* w, size_t n, size_t k, const NativeRec* rec,
+                                  int32_t* partials, hipStream_t s);
+
+// Dequantize selected rows of a Q4_0 / Q4_1 / Q8_0 matrix to f32.
+hipError_t launch_dequant_rows(WType t, const uint8_t* w, size_t n, size_t k,
+                               const int32_t* rows, size_t n_rows, float* out, hipStream_t s);
+
+}  // namespace rdl

@@ -1,0 +1,148 @@
+"""Pins the oracle's matmuls and dequantizers (rustml/quant/main/src/core/quantize.rs,
+rustml/core/main/src/core/tensor/tensor.rs:535-639, rustml/gguf/main/src/core/parser.rs:549-593)."""
+import numpy as np
+import pytest
+
+from rdlquant import synth
+
+
+def f64_gemm(x, wdeq, m, k, n):
+    return x.reshape(m, k).astype(np.float64) @ wdeq.reshape(n, k).astype(np.float64).T
+
+
+def test_to_f32_q4_0_gguf_order(orc):
+    # tensor.rs:553-563: byte j -> element j (lo) and j+16 (hi), value d*(q-8)
+    blk = np.zeros(18, np.uint8)
+    blk[0:2] = np.array([1.0], np.float16).view(np.uint8)  # d = 1
+    blk[2:] = np.array([(((j + 1) & 15) << 4) | j for j in range(16)], np.uint8)
+    out = orc.to_f32("q4_0", blk, 32)
+    want = np.array([j - 8 for j in range(16)] + [((j + 1) & 15) - 8 for j in range(16)], np.float32)
+    assert np.array_equal(out, want)
+
+
+def test_to_f32_q8_0_and_q4_1(orc):
+    rng = np.random.default_rng(5)
+    w8 = synth.q8_0_weights(3, 64, 1)
+    out = orc.to_f32("q8_0", w8, 3 * 64).reshape(-1, 32)
+    b = w8.reshape(-1, 34)
+    d = b[:, 0:2].copy().view(np.float16).astype(np.float32)
+    assert np.array_equal(out, d * b[:, 2:].view(np.int8).astype(np.float32))
+    w41 = synth.q4_1_weights(2, 64, 2)
+    out = orc.to_f32("q4_1", w41, 128).reshape(-1, 32)
+    b = w41.reshape(-1, 20)
+    d = b[:, 0:2].copy().view(np.float16).astype(np.float32)
+    mv = b[:, 2:4].copy().view(np.float16).astype(np.float32)
+    nib = np.concatenate([b[:, 4:] & 0xF, b[:, 4:] >> 4], axis=1).astype(np.float32)
+    assert np.array_equal(out, d * nib + mv)
+
+
+@pytest.mark.parametrize("kind,gen,deq", [
+    ("q8", synth.q8_0_weights, "q8_0"),
+    ("q4", synth.q4_0_weights, "q4_0"),
+    ("q4_1", synth.q4_1_weights, "q4_1"),
+])
+def test_float_matmul_vs_f64(orc, kind, gen, deq):
+    m, k, n = 3, 512, 40
+    x = synth.activations(m, k, 3)
+    w = gen(n, k, 4)
+    y = orc.matmul(kind, x, w, m, k, n, threads=2).reshape(m, n)
+    wd = orc.to_f32(deq, w, n * k)
+    want = f64_gemm(x, wd, m, k, n)
+    bound = 2.0 ** -20 * (np.abs(x.reshape(m, k)) @ np.abs(wd.reshape(n, k)).T) + 1e-12
+    assert np.all(np.abs(y - want) <= bound)
+
+
+def test_native_vs_float_agreement(orc):
+    # llmforge simd_test.rs:245-276 style: native and float paths agree within 2%
+    x = ((np.arange(128, dtype=np.float32) - 64) * np.float32(0.02)).reshape(1, 128)
+    w = synth.q4_0_weights(4, 128, 9)
+    a = orc.matmul("q4", x, w, 1, 128, 4)
+    b = orc.matmul("q4_native", x, w, 1, 128, 4)
+    assert np.all(np.abs(a - b) <= 0.02 * np.abs(a) + 1e-3)
+
+
+def test_native_equals_partials_composition(orc):
+    # y = sum_b (float(int_dot_b) * sx_b) * sw_b in block order (quantize.rs:383-384)
+    m, k, n = 2, 256, 5
+    x = synth.activations(m, k, 21)
+    w = synth.q4_0_weights(n, k, 22)
+    part = orc.block_dots(x, w, m, k, n)
+    y = orc.matmul("q4_native", x, w, m, k, n).reshape(m, n)
+    wb = w.reshape(n, k // 32, 18)
+    ws = wb[:, :, 0:2].copy().view(np.float16).astype(np.float32)[..., 0]
+    for r in range(m):
+        _, sx = orc.quantize_row_q8_0(x[r])
+        for c in range(n):
+            acc = np.float32(0)
+            for b in range(k // 32):
+                acc = np.float32(acc + np.float32(np.float32(np.float32(part[r, c, b]) * sx[b]) * ws[c, b]))
+            assert acc == y[r, c]
+    # and the partials are the integer dots against the Q8_0 codes
+    q8, _ = orc.quantize_row_q8_0(x[0])
+    codes = q8.reshape(-1, 34)[:, 2:].view(np.int8).astype(np.int64)
+    nib = np.concatenate([wb[..., 2:] & 0xF, wb[..., 2:] >> 4], axis=2).astype(np.int64) - 8
+    assert np.array_equal(part[0], (nib * codes[None]).sum(axis=2))
+
+
+def test_q4k_exact_small_integers(orc):
+    # d, dmin powers of two, small integer q/sc/mn: every product is exact, so
+    # the dequantization has a closed form to compare bit for bit.
+    rng = np.random.default_rng(8)
+    n, k = 2, 512
+    ns = k // 256
+    q = rng.integers(0, 16, size=(n, ns, 4, 2, 32), dtype=np.uint8)
+    sc = rng.integers(0, 64, size=(n, ns, 8), dtype=np.uint8)
+    mn = rng.integers(0, 64, size=(n, ns, 8), dtype=np.uint8)
+    blob = np.zeros((n, ns, 144), np.uint8)
+    blob[..., 0:2] = np.array([0.25], np.float16).view(np.uint8)
+    blob[..., 2:4] = np.array([0.5], np.float16).view(np.uint8)
+    blob[..., 4:16] = synth.pack_q4k_scales(sc, mn)
+    blob[..., 16:] = (q[..., 0, :] | (q[..., 1, :] << 4)).reshape(n, ns, 128)
+    out = orc.to_f32("q4k", blob.reshape(-1), n * k).reshape(n, ns, 4, 2, 32)
+    # sub-block j = 2*chunk + (0 lo | 1 hi)
+    scj = sc.reshape(n, ns, 4, 2, 1).astype(np.float32)
+    mnj = mn.reshape(n, ns, 4, 2, 1).astype(np.float32)
+    want = 0.25 * scj * q.astype(np.float32) - 0.5 * mnj
+    assert np.array_equal(out, want.astype(np.float32))
+
+
+def test_q4k_scale_pack_roundtrip():
+    # synth.pack_q4k_scales must invert parser.rs:562-569 exactly
+    rng = np.random.default_rng(9)
+    sc = rng.integers(0, 64, size=(100, 8), dtype=np.uint8)
+    mn = rng.integers(0, 64, size=(100, 8), dtype=np.uint8)
+    s = synth.pack_q4k_scales(sc, mn).astype(np.int64)
+    usc = np.concatenate([s[:, 0:4] & 63, ((s[:, 0:4] >> 6) & 3) | ((s[:, 8:12] & 0xF) << 2)], axis=1)
+    umn = np.concatenate([s[:, 4:8] & 63, ((s[:, 4:8] >> 6) & 3) | ((s[:, 8:12] >> 4) << 2)], axis=1)
+    assert np.array_equal(usc, sc) and np.array_equal(umn, mn)
+
+
+def test_q4k_matmul_vs_f64(orc):
+    m, k, n = 2, 1024, 24
+    x = synth.activations(m, k, 31)
+    w = synth.q4_k_weights(n, k, 32)
+    y = orc.matmul("q4k", x, w, m, k, n, threads=2).reshape(m, n)
+    wd = orc.to_f32("q4k", w, n * k)
+    want = f64_gemm(x, wd, m, k, n)
+    bound = 2.0 ** -13 * (np.abs(x.reshape(m, k)) @ np.abs(wd.reshape(n, k)).T) + 1e-9
+    assert np.all(np.abs(y - want) <= bound)
+
+
+@pytest.mark.parametrize("kind", ["q8", "q4", "q4_native", "q4_1", "q4_1_native"])
+def test_block_alignment_error(orc, kind):
+    with pytest.raises(orc.OracleError) as e:
+        orc.matmul(kind, np.zeros(33, np.float32), np.zeros(100, np.uint8), 1, 33, 1)
+    assert e.value.code == 3
+
+
+def test_short_weight_is_shape_mismatch(orc):
+    with pytest.raises(orc.OracleError) as e:
+        orc.matmul("q4", np.zeros(64, np.float32), np.zeros(35, np.uint8), 1, 64, 1)
+    assert e.value.code == 2
+
+
+def test_cols_split_equals_row_split(orc):
+    m, k, n = 1, 1024, 33
+    x = synth.activations(m, k, 41)
+    w = synth.q4_0_weights(n, k, 42)
+    assert np.array_equal(orc.matmul("q4", x, w, m, k, n, 1), orc.matmul("q4_cols", x, w, m, k, n, 4))
