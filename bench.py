@@ -1,10 +1,16 @@
 """Benchmark of the Q4_0 decode GEMV on one MI355X.
 
 A step is one batch-1 Linear forward of the Llama-7B FFN up/gate shape
-(W 11008x4096 GGUF Q4_0, x f32 [4096]) through the C ABI: activation prep +
-GEMV, i.e. rustml_quant::matmul_f32_q4 (quantize.rs:265-320) with the weight
-resident in HBM.  Consecutive steps use different weight copies (more than
-the 256 MB Infinity Cache in total) so each step streams its weight from HBM.
+(W 11008x4096 GGUF Q4_0, x f32 [4096]) through the C ABI
+(rdl_linear_forward_dev: one kernel, activation prep fused), i.e.
+rustml_quant::matmul_f32_q4 (quantize.rs:265-320) with the weight resident in
+HBM.  Consecutive steps use different weight copies (more than the 256 MB
+Infinity Cache in total) so each step streams its weight from HBM.
+
+Timed region: the K steps are captured once in a HIP graph (so host launch
+overhead is not measured) and replayed once between two events.  The
+roofline figure times each GEMV kernel at its boundaries (hipExtLaunchKernel
+events) over K separate launches.
 
 Prints one JSON line (see the keys below).
 """
@@ -98,35 +104,44 @@ def main():
         weights.append((t, rq.Weight.wrap_device(t.data_ptr(), wbytes, rq.DTYPE_Q4_0, N_OUT, K_IN, t)))
     del w0
     x = torch.from_numpy(synth.activations(1, K_IN, SEED + 100).reshape(-1)).to(dev)
-    rec = torch.empty(rq.activation_record_bytes(1, K_IN, rq.MODE_FLOAT), dtype=torch.uint8, device=dev)
     y = torch.empty(N_OUT, dtype=torch.float32, device=dev)
 
-    def step(i, ev=None):
-        rq.prepare_activations_dev(x.data_ptr(), 1, K_IN, rq.MODE_FLOAT, rec.data_ptr(), sh)
-        if ev is not None:
-            ev[0].record(stream)
-        weights[i % len(weights)][1].forward_prepared_dev(rec.data_ptr(), 1, y.data_ptr(), rq.MODE_FLOAT, sh)
-        if ev is not None:
-            ev[1].record(stream)
+    def step(i, s_handle):
+        weights[i % len(weights)][1].forward_dev(x.data_ptr(), 1, y.data_ptr(), rq.MODE_FLOAT, s_handle)
 
     for i in range(args.warmup):
-        step(i)
+        step(i, sh)
     torch.cuda.synchronize()
 
-    # timed region: K whole steps; per-launch events bracket the GEMV kernel
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(args.steps)]
+    # capture the K steps in one graph; one untimed replay, then the timed one
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        cap = torch.cuda.current_stream().cuda_stream
+        for i in range(args.steps):
+            step(i, cap)
+    graph.replay()
+    torch.cuda.synchronize()
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
     t0.record(stream)
-    for i in range(args.steps):
-        step(i, evs[i])
+    graph.replay()
     t1.record(stream)
     torch.cuda.synchronize()
     total_ms = t0.elapsed_time(t1)
     ms_per_step = total_ms / args.steps
-    kern_ms = [a.elapsed_time(b) for a, b in evs]
+
+    # kernel-boundary timing of the GEMV kernel over K separate launches
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.steps)]
+    for a, b in evs:  # materialize the events
+        a.record(stream)
+        b.record(stream)
+    torch.cuda.synchronize()
+    for i, (a, b) in enumerate(evs):
+        rq.time_next_launch(a.cuda_event, b.cuda_event)
+        step(i, sh)
+    torch.cuda.synchronize()
+    kern_ms = sorted(a.elapsed_time(b) for a, b in evs)
     kern_avg_ms = sum(kern_ms) / len(kern_ms)
 
     abytes = algorithmic_bytes(N_OUT, K_IN)
@@ -155,7 +170,7 @@ def main():
         "data": "synthetic (seeded BASELINE config 2 bytes)",
         "config": {
             "workload": "config2: Q4_0 GEMV y=Wx, W 11008x4096 GGUF Q4_0, x f32[4096], batch 1, "
-                        "float path (matmul_f32_q4); step = activation prep + GEMV",
+                        "float path (matmul_f32_q4); step = one fused prep+GEMV kernel",
             "weight_copies": args.copies,
             "weight_bytes_total": wbytes * args.copies,
             "algorithmic_bytes_per_step": abytes,
@@ -164,12 +179,13 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "gemv_float_kernel<Q4_0>",
+            "kernel": "gemv_fused_kernel<Q4_0, float>",
             "achieved": round(achieved, 2),
             "peak": PEAK_HBM_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBPS, 4),
             "kernel_avg_us": round(kern_avg_ms * 1e3, 3),
+            "kernel_median_us": round(kern_ms[len(kern_ms) // 2] * 1e3, 3),
             "traffic": None,
         },
     }

@@ -81,6 +81,12 @@ const char* rdl_version(void);
 /* Number of visible gfx950 devices (0 when there is no GPU; never an error). */
 int32_t rdl_device_count(void);
 
+/* Instrumentation (no reference counterpart): the next GEMV/GEMM kernel the
+ * calling thread launches records its start and end into these hipEvent_t
+ * (created with timing enabled) at the kernel boundaries, through
+ * hipExtLaunchKernel -- the same interval a kernel trace reports. */
+rdl_status rdl_time_next_launch(void* start_event, void* stop_event);
+
 /* ---- host-pointer drop-ins for rustml_quant ------------------------------
  * input_data: f32 [m, in_features]; weight_bytes: blocks of [out_features,
  * in_features]; output: f32 [m, out_features] (output_len >= m*out_features). */

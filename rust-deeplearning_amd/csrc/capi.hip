@@ -14,6 +14,10 @@
 #include "../../include/rdl_quant.h"
 #include "rdl_internal.hpp"
 
+namespace rdl {
+thread_local LaunchEvents g_launch_events;
+}
+
 using rdl::FloatRec;
 using rdl::NativeRec;
 using rdl::WType;
@@ -119,13 +123,25 @@ size_t rec_bytes(bool native, size_t m, size_t k) {
     return m * (k / rdl::QK) * (native ? sizeof(NativeRec) : sizeof(FloatRec));
 }
 
-// Prepare activations and run the product on `s`; xrec must hold rec_bytes().
+// Activation rows up to which one fused launch (prep in LDS + GEMV) is used.
+constexpr size_t FUSED_MAX_M = 4;
+
+bool use_fused(WType t, size_t m, size_t k, const float* x_dev) {
+    return m <= FUSED_MAX_M && k > 0 && k <= rdl::fused_max_k(t) && ((uintptr_t)x_dev & 15) == 0;
+}
+
+// Prepare activations and run the product on `s`; xrec must hold rec_bytes()
+// unless use_fused() holds.
 rdl_status run_linear(WType t, bool native, const uint8_t* w_dev, size_t n, size_t k,
                       const float* x_dev, size_t m, float* y_dev, void* xrec, hipStream_t s) {
     if (m == 0 || n == 0) return RDL_OK;
     // k == 0: no blocks; the GEMV then writes zeros (empty dot, as in the reference).
     if (k == 0) {
         HIP_TRY(rdl::launch_gemv(t, native, w_dev, n, k, xrec, m, y_dev, s));
+        return RDL_OK;
+    }
+    if (use_fused(t, m, k, x_dev)) {
+        HIP_TRY(rdl::launch_gemv_fused(t, native, w_dev, n, k, x_dev, m, y_dev, s));
         return RDL_OK;
     }
     if (native)
@@ -156,7 +172,7 @@ rdl_status host_matmul(WType t, bool native, const float* x, size_t x_len, const
     HIP_TRY(dx.alloc(m * k * sizeof(float)));
     HIP_TRY(dw.alloc(wb + 64));
     HIP_TRY(dy.alloc(m * n * sizeof(float)));
-    HIP_TRY(dr.alloc(rec_bytes(native, m, k)));
+    if (!use_fused(t, m, k, (const float*)dx.p)) HIP_TRY(dr.alloc(rec_bytes(native, m, k)));
     HIP_TRY(hipMemcpy(dx.p, x, m * k * sizeof(float), hipMemcpyHostToDevice));
     HIP_TRY(hipMemcpy(dw.p, w, wb, hipMemcpyHostToDevice));
     st = run_linear(t, native, (const uint8_t*)dw.p, n, k, (const float*)dx.p, m, (float*)dy.p,
@@ -190,6 +206,12 @@ const char* rdl_last_error(void) { return g_err.c_str(); }
 const char* rdl_version(void) { return "rdlquant 0.1.0 (gfx950)"; }
 
 int32_t rdl_device_count(void) { return count_devices(); }
+
+rdl_status rdl_time_next_launch(void* start_event, void* stop_event) {
+    rdl::g_launch_events.start = (hipEvent_t)start_event;
+    rdl::g_launch_events.stop = (hipEvent_t)stop_event;
+    return ok();
+}
 
 rdl_status rdl_matmul_f32_q8(const float* x, size_t x_len, const uint8_t* w, size_t w_len,
                              size_t m, size_t k, size_t n, float* y, size_t y_len) {
@@ -341,7 +363,7 @@ rdl_status rdl_linear_forward_dev(const rdl_weight* w, const float* x_dev, size_
     const bool native = mode == RDL_MODE_NATIVE && (w->type == WType::Q4_0 || w->type == WType::Q4_1);
     hipStream_t s = (hipStream_t)stream;
     void* rec = nullptr;
-    const size_t rb = rec_bytes(native, m, w->k);
+    const size_t rb = use_fused(w->type, m, w->k, x_dev) ? 0 : rec_bytes(native, m, w->k);
     if (rb) HIP_TRY(hipMallocAsync(&rec, rb, s));
     rdl_status st = run_linear(w->type, native, (const uint8_t*)w->dev, w->n, w->k, x_dev, m, y_dev,
                                rec, s);

@@ -51,11 +51,11 @@ __device__ __forceinline__ XF load_xf(const FloatRec* r) {
     x.c0 = p[4];
     x.c1 = p[5];
     i32x4 m = p[6];
-    x.S = __builtin_bit_cast(float, m.x);
+    x.S = as_f32(m.x);
     x.sa = m.y;
     x.sb = m.z;
     x.sc = m.w;
-    x.xsum = __builtin_bit_cast(float, p[7].x);
+    x.xsum = as_f32(p[7].x);
     return x;
 }
 struct XN {  // native mode: Q8_0 codes of the column
@@ -69,7 +69,7 @@ __device__ __forceinline__ XN load_xn(const NativeRec* r) {
     x.q0 = p[0];
     x.q1 = p[1];
     i32x4 m = p[2];
-    x.scale = __builtin_bit_cast(float, m.x);
+    x.scale = as_f32(m.x);
     x.qsum = m.y;
     return x;
 }
@@ -477,25 +477,25 @@ hipError_t launch_r(WType t, bool native, const uint8_t* w, size_t n, size_t k, 
     const dim3 block(GEMV_THREADS);
     const int ni = (int)n;
     if (t == WType::Q4_K) {
-        hipLaunchKernelGGL((gemv_q4k_kernel<R>), grid, block, 0, s, w, ni, (int)(k / QK_K),
+        launch_kernel((gemv_q4k_kernel<R>), grid, block, 0, s, w, ni, (int)(k / QK_K),
                            (const FloatRec*)xrec, y);
         return hipGetLastError();
     }
     const int nb = (int)(k / QK);
     if (native && t == WType::Q4_0) {
-        hipLaunchKernelGGL((gemv_native_kernel<R, (int)WType::Q4_0>), grid, block, 0, s, w, ni, nb,
+        launch_kernel((gemv_native_kernel<R, (int)WType::Q4_0>), grid, block, 0, s, w, ni, nb,
                            (const NativeRec*)xrec, y);
     } else if (native && t == WType::Q4_1) {
-        hipLaunchKernelGGL((gemv_native_kernel<R, (int)WType::Q4_1>), grid, block, 0, s, w, ni, nb,
+        launch_kernel((gemv_native_kernel<R, (int)WType::Q4_1>), grid, block, 0, s, w, ni, nb,
                            (const NativeRec*)xrec, y);
     } else if (t == WType::Q4_0) {
-        hipLaunchKernelGGL((gemv_float_kernel<R, (int)WType::Q4_0>), grid, block, 0, s, w, ni, nb,
+        launch_kernel((gemv_float_kernel<R, (int)WType::Q4_0>), grid, block, 0, s, w, ni, nb,
                            (const FloatRec*)xrec, y);
     } else if (t == WType::Q4_1) {
-        hipLaunchKernelGGL((gemv_float_kernel<R, (int)WType::Q4_1>), grid, block, 0, s, w, ni, nb,
+        launch_kernel((gemv_float_kernel<R, (int)WType::Q4_1>), grid, block, 0, s, w, ni, nb,
                            (const FloatRec*)xrec, y);
     } else {
-        hipLaunchKernelGGL((gemv_float_kernel<R, (int)WType::Q8_0>), grid, block, 0, s, w, ni, nb,
+        launch_kernel((gemv_float_kernel<R, (int)WType::Q8_0>), grid, block, 0, s, w, ni, nb,
                            (const FloatRec*)xrec, y);
     }
     return hipGetLastError();

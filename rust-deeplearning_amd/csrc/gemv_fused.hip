@@ -1,0 +1,876 @@
+// gemv_fused.hip -- single-launch decode GEMV: activation preparation fused
+// into the GEMV, y = W x for one activation row per blockIdx.y.
+//
+// Reference semantics are those of gemv.hip (matmul_f32_q8 / _q4 / _q4_native /
+// _q4_1 / _q4_1_native, quantize.rs:201-572; Q4_K parser.rs:549-593).
+//
+// Shape of a launch (MI355X: 256 CUs):
+//   * about one workgroup of NW = 16 waves per CU; workgroup g owns rows
+//     [g*rpw, (g+1)*rpw) and hands them to its waves round-robin, so wave w
+//     owns at most R rows;
+//   * phase 0: every wave issues the loads of all its weight blocks (R rows x
+//     up to CPL columns per lane) before anything else -- the weight stream
+//     does not depend on x;
+//   * phase 1: while those loads are in flight the workgroup converts x into
+//     per-column records in LDS (same encodings as FloatRec / NativeRec,
+//     stored as eight 16-byte groups per column, group-major, so that 64 lanes
+//     reading 64 consecutive columns hit 64 consecutive 16-byte slots);
+//   * phase 2: each lane dots its blocks against its columns' records on
+//     v_dot4_i32_i8; the R row sums are reduced across the wave.
+#include <type_traits>
+
+#include "rdl_device.hpp"
+#include "rdl_internal.hpp"
+
+namespace rdl {
+
+namespace {
+
+// waves per workgroup (template parameter NW of the kernels); NT = NW * 64
+constexpr uint32_t NIB = 0x0F0F0F0Fu;
+constexpr uint32_t ONES = 0x01010101u;
+
+// ---- phase 1: records in LDS ---------------------------------------------------
+// Group layout per column c (i32x4 slots at lds[g * nb + c]):
+//   float:  g0,g1 = a digits (dwords 0-3, 4-7), g2,g3 = b, g4,g5 = c,
+//           g6 = {S, sum a, sum b, sum c}, g7 = {sum x, 0, 0, 0}
+//   native: g0,g1 = q8 codes, g2 = {scale, sum q8, 0, 0}
+// Eight threads share a column; thread k of the eight handles elements 4k..4k+3,
+// which form digit dword k.
+
+__device__ __forceinline__ int lds_word(int g, int k4, int nb, int c) {  // dword index
+    return (g * nb + c) * 4 + k4;
+}
+
+__device__ __forceinline__ float max8(float v) {
+    v = fmaxf(v, __shfl_xor(v, 1, 8));
+    v = fmaxf(v, __shfl_xor(v, 2, 8));
+    return fmaxf(v, __shfl_xor(v, 4, 8));
+}
+__device__ __forceinline__ int sum8(int v) {
+    v += __shfl_xor(v, 1, 8);
+    v += __shfl_xor(v, 2, 8);
+    return v + __shfl_xor(v, 4, 8);
+}
+__device__ __forceinline__ float sumf8(float v) {
+    v += __shfl_xor(v, 1, 8);
+    v += __shfl_xor(v, 2, 8);
+    return v + __shfl_xor(v, 4, 8);
+}
+
+// 24-bit fixed-point digits of x_j * (127*65536 / amax):  t + 0x808080 is in
+// [0, 2^24), its bytes u are the digits biased by 128, and u ^ 0x80 is the
+// int8 pattern of the signed digit, so e = (t + 0x808080) ^ 0x808080 holds
+// the digits c (byte 0), b (byte 1), a (byte 2).
+// x loads for the prep, issued before the weight stream so they return first.
+// The prep's x loads are issued first, by inline asm, so that they precede
+// every weight load in the wave's in-order load queue; wait_prep_x<N>() then
+// waits for them alone ("vmcnt <= N" with N = the number of weight loads the
+// wave issued after them) while the weight stream stays in flight.  The
+// compiler does not track these asm loads, so the explicit wait is the only
+// guard: N must not exceed the number of load instructions actually issued
+// between the two points (the "memory" clobbers keep every load in between).
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <int NW, int PI>
+__device__ __forceinline__ void load_prep_x(const float* __restrict__ x, int nb, f32x4 (&xv)[PI]) {
+    constexpr int NT = NW * 64;
+#pragma unroll
+    for (int j = 0; j < PI; j++) {
+        const int p = min((int)threadIdx.x + j * NT, nb * 8 - 1);
+        const float* ptr = x + (p >> 3) * 32 + (p & 7) * 4;
+        asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(xv[j]) : "v"(ptr) : "memory");
+    }
+}
+
+template <int N>
+__device__ __forceinline__ void wait_prep_x() {
+    static_assert(N >= 0 && N <= 63, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <int NW, int PI>
+__device__ void prep_float_lds(const f32x4 (&xv)[PI], int nb, int* __restrict__ lds) {
+    constexpr int NT = NW * 64;
+#pragma unroll
+    for (int j = 0; j < PI; j++) {
+        const int p = threadIdx.x + j * NT;
+        if (j * NT >= nb * 8) break;  // uniform
+        const int c = p >> 3, k = p & 7;
+        const f32x4 v = xv[j];
+        const bool bad = !(isfinite(v.x) && isfinite(v.y) && isfinite(v.z) && isfinite(v.w));
+        float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+        amax = max8(amax);
+        const int anybad = sum8(bad ? 1 : 0);
+        // scale tiny blocks by 2^64 so that 8323072/amax stays finite (exact)
+        const float pw = (amax < 0x1p-60f) ? 0x1p64f : 1.0f;
+        const float inv = (amax > 0.0f && !anybad) ? 8323072.0f / (amax * pw) : 0.0f;
+        const float f = anybad ? 0.0f : pw * inv;
+        uint32_t e0 = (uint32_t)(rintf(v.x * f) + 8421504.0f) ^ 0x808080u;
+        uint32_t e1 = (uint32_t)(rintf(v.y * f) + 8421504.0f) ^ 0x808080u;
+        uint32_t e2 = (uint32_t)(rintf(v.z * f) + 8421504.0f) ^ 0x808080u;
+        uint32_t e3 = (uint32_t)(rintf(v.w * f) + 8421504.0f) ^ 0x808080u;
+        if (anybad) e0 = e1 = e2 = e3 = 0u;  // S is NaN for this block anyway
+        // gather byte k of e0..e3 into one dword per digit
+        const uint32_t p01 = perm(e1, e0, 0x05010400u);   // c0 c1 b0 b1
+        const uint32_t p23 = perm(e3, e2, 0x05010400u);   // c2 c3 b2 b3
+        const uint32_t q01 = perm(e1, e0, 0x0c0c0602u);   // a0 a1 0 0
+        const uint32_t q23 = perm(e3, e2, 0x0c0c0602u);   // a2 a3 0 0
+        const uint32_t dc = perm(p23, p01, 0x05040100u);
+        const uint32_t db = perm(p23, p01, 0x07060302u);
+        const uint32_t da = perm(q23, q01, 0x05040100u);
+        const int g = k >> 2, k4 = k & 3;
+        if (p < nb * 8) {
+            lds[lds_word(0 + g, k4, nb, c)] = (int)da;
+            lds[lds_word(2 + g, k4, nb, c)] = (int)db;
+            lds[lds_word(4 + g, k4, nb, c)] = (int)dc;
+        }
+        const int sa = sum8(__builtin_amdgcn_sdot4((int)da, (int)ONES, 0, false));
+        const int sb = sum8(__builtin_amdgcn_sdot4((int)db, (int)ONES, 0, false));
+        const int sc = sum8(__builtin_amdgcn_sdot4((int)dc, (int)ONES, 0, false));
+        const float xs = sumf8((v.x + v.y) + (v.z + v.w));
+        if (k == 0 && p < nb * 8) {
+            const float nan = __builtin_nanf("");
+            lds[lds_word(6, 0, nb, c)] = __builtin_bit_cast(int, anybad ? nan : amax / 127.0f);
+            lds[lds_word(6, 1, nb, c)] = sa;
+            lds[lds_word(6, 2, nb, c)] = sb;
+            lds[lds_word(6, 3, nb, c)] = sc;
+            lds[lds_word(7, 0, nb, c)] = __builtin_bit_cast(int, anybad ? nan : xs);
+        }
+    }
+}
+
+// quantize_row_q8_0 (quantize.rs:164-193), byte-exact, into LDS records.
+template <int NW, int PI>
+__device__ void prep_native_lds(const f32x4 (&xv)[PI], int nb, int* __restrict__ lds) {
+    constexpr int NT = NW * 64;
+#pragma unroll
+    for (int j = 0; j < PI; j++) {
+        const int p = threadIdx.x + j * NT;
+        if (j * NT >= nb * 8) break;  // uniform
+        const int c = p >> 3, k = p & 7;
+        const f32x4 v = xv[j];
+        // fmaxf(0, |x|) drops NaN as the fold from 0.0 with f32::max does
+        float amax = fmaxf(fmaxf(fmaxf(0.0f, fabsf(v.x)), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+        amax = max8(amax);
+        const float scale = (amax == 0.0f) ? 0.0f : amax / 127.0f;
+        const float rt = h2f(f2h_rne(scale));
+        const float inv = (rt == 0.0f) ? 0.0f : 1.0f / rt;
+        const float vv[4] = {v.x, v.y, v.z, v.w};
+        uint32_t d = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float r = roundf(vv[j] * inv);
+            const int q = (r != r) ? 0 : (int)fminf(fmaxf(r, -128.0f), 127.0f);
+            d |= ((uint32_t)q & 0xFFu) << (8 * j);
+        }
+        if (p < nb * 8) lds[lds_word(k >> 2, k & 3, nb, c)] = (int)d;
+        const int qs = sum8(__builtin_amdgcn_sdot4((int)d, (int)ONES, 0, false));
+        if (k == 0 && p < nb * 8) {
+            lds[lds_word(2, 0, nb, c)] = __builtin_bit_cast(int, rt);
+            lds[lds_word(2, 1, nb, c)] = qs;
+        }
+    }
+}
+
+// ---- int4-digit records for Q4_0 / Q4_1 (float mode) --------------------------------
+// x_j ~= S4 * t_j with t_j = rint(x_j * 7829365 / amax), a signed 24-bit code
+// (|t| <= 0x777777 = 7829367, the largest code the digits hold; the scale
+// leaves two units for the rounding of amax * (7829365 / amax))
+// held as six signed base-16 digits: t + 0x888888 is in [0, 2^24), so the
+// nibbles of e = (t + 0x888888) ^ 0x888888 are the digits as int4 (nibble L
+// weighs 16^L).  The digit dwords follow the Q4 nibble order (byte j of a
+// block holds element j low and j+16 high), so that v_dot8_i32_i4 multiplies
+// the weight nibbles in place: dword k of level L holds the digits of elements
+// 4k, 4k+16, 4k+1, 4k+17, 4k+2, 4k+18, 4k+3, 4k+19.
+// Group layout per column (i32x4 at lds[g * nb + c]): g0..g5 = level 0..5
+// (dwords k = 0..3), g6 = {S4, sum x, 0, 0}.  Four threads share a column;
+// thread k handles elements 4k..4k+3 and 4k+16..4k+19.
+
+__device__ __forceinline__ float max4(float v) {
+    v = fmaxf(v, __shfl_xor(v, 1, 4));
+    return fmaxf(v, __shfl_xor(v, 2, 4));
+}
+__device__ __forceinline__ int sum4(int v) {
+    v += __shfl_xor(v, 1, 4);
+    return v + __shfl_xor(v, 2, 4);
+}
+__device__ __forceinline__ float sumf4(float v) {
+    v += __shfl_xor(v, 1, 4);
+    return v + __shfl_xor(v, 2, 4);
+}
+
+// Nibble levels 2b and 2b+1 of the eight codes: P holds byte b of elements
+// 4k..4k+3, Q byte b of elements 4k+16..4k+19.
+__device__ __forceinline__ void nib_levels(uint32_t P, uint32_t Q, uint32_t& lo, uint32_t& hi) {
+    lo = (P & 0x0F0F0F0Fu) | ((Q & 0x0F0F0F0Fu) << 4);
+    hi = ((P >> 4) & 0x0F0F0F0Fu) | (Q & 0xF0F0F0F0u);
+}
+
+template <int NW, int PI>
+__device__ __forceinline__ void load_prep_x4(const float* __restrict__ x, int nb, f32x4 (&xv)[PI][2]) {
+    constexpr int NT = NW * 64;
+#pragma unroll
+    for (int j = 0; j < PI; j++) {
+        const int p = min((int)threadIdx.x + j * NT, nb * 4 - 1);
+        const float* ptr = x + (p >> 2) * 32 + (p & 3) * 4;
+        asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(xv[j][0]) : "v"(ptr) : "memory");
+        asm volatile("global_load_dwordx4 %0, %1, off offset:64" : "=v"(xv[j][1]) : "v"(ptr) : "memory");
+    }
+}
+
+template <int NW, int PI>
+__device__ void prep_float4_lds(const f32x4 (&xv)[PI][2], int nb, int* __restrict__ lds) {
+    constexpr int NT = NW * 64;
+#pragma unroll
+    for (int j = 0; j < PI; j++) {
+        const int p = threadIdx.x + j * NT;
+        if (j * NT >= nb * 4) break;  // uniform
+        const int c = p >> 2, k = p & 3;
+        const f32x4 va = xv[j][0], vb = xv[j][1];
+        const float v[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};
+        bool bad = false;
+        float amax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            bad |= !isfinite(v[i]);
+            amax = fmaxf(amax, fabsf(v[i]));
+        }
+        amax = max4(amax);
+        const int anybad = sum4(bad ? 1 : 0);
+        const float pw = (amax < 0x1p-60f) ? 0x1p64f : 1.0f;
+        const float f = (amax > 0.0f && !anybad) ? pw * (7829365.0f / (amax * pw)) : 0.0f;
+        uint32_t e[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            e[i] = anybad ? 0u : ((uint32_t)(rintf(v[i] * f) + 8947848.0f) ^ 0x888888u);
+        // byte b of e[0..3] -> P_b, of e[4..7] -> Q_b
+        const uint32_t a01 = perm(e[1], e[0], 0x05010400u), a23 = perm(e[3], e[2], 0x05010400u);
+        const uint32_t b01 = perm(e[5], e[4], 0x05010400u), b23 = perm(e[7], e[6], 0x05010400u);
+        const uint32_t P0 = perm(a23, a01, 0x05040100u), P1 = perm(a23, a01, 0x07060302u);
+        const uint32_t Q0 = perm(b23, b01, 0x05040100u), Q1 = perm(b23, b01, 0x07060302u);
+        const uint32_t c01 = perm(e[1], e[0], 0x0c0c0602u), c23 = perm(e[3], e[2], 0x0c0c0602u);
+        const uint32_t d01 = perm(e[5], e[4], 0x0c0c0602u), d23 = perm(e[7], e[6], 0x0c0c0602u);
+        const uint32_t P2 = perm(c23, c01, 0x05040100u), Q2 = perm(d23, d01, 0x05040100u);
+        uint32_t L[6];
+        nib_levels(P0, Q0, L[0], L[1]);
+        nib_levels(P1, Q1, L[2], L[3]);
+        nib_levels(P2, Q2, L[4], L[5]);
+        float xs = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) xs += v[i];
+        xs = sumf4(xs);
+        if (p < nb * 4) {
+#pragma unroll
+            for (int lv = 0; lv < 6; lv++) lds[lds_word(lv, k, nb, c)] = (int)L[lv];
+            if (k == 0) {
+                const float nan = __builtin_nanf("");
+                lds[lds_word(6, 0, nb, c)] = __builtin_bit_cast(int, anybad ? nan : amax / 7829365.0f);
+                lds[lds_word(6, 1, nb, c)] = __builtin_bit_cast(int, anybad ? nan : xs);
+            }
+        }
+    }
+}
+
+// Only vector members: S and sum(x) stay packed in `meta` (as loaded) and are
+// bit-cast where they are used.
+struct RF4 {
+    i32x4 lv[6];
+    i32x4 meta;  // {S4, sum x, 0, 0}
+    __device__ float S() const { return as_f32(meta.x); }
+    __device__ float xsum() const { return as_f32(meta.y); }
+};
+__device__ __forceinline__ RF4 read_rf4(const i32x4* __restrict__ l4, int nb, int c) {
+    RF4 r;
+#pragma unroll
+    for (int lv = 0; lv < 6; lv++) r.lv[lv] = l4[lv * nb + c];
+    r.meta = l4[6 * nb + c];
+    return r;
+}
+
+// sum_j w_j * t_j for signed int4 weight nibbles w (four dwords), as a float.
+__device__ __forceinline__ float dot_i4(const uint32_t (&w)[4], const RF4& x) {
+    int D[6];
+#pragma unroll
+    for (int lv = 0; lv < 6; lv++) {
+        int a = __builtin_amdgcn_sdot8((int)w[0], x.lv[lv].x, 0, false);
+        a = __builtin_amdgcn_sdot8((int)w[1], x.lv[lv].y, a, false);
+        a = __builtin_amdgcn_sdot8((int)w[2], x.lv[lv].z, a, false);
+        D[lv] = __builtin_amdgcn_sdot8((int)w[3], x.lv[lv].w, a, false);
+    }
+    // |D| <= 32 * 8 * 8, so each three-level Horner sum stays far inside int32
+    const int hi = (((D[5] << 4) + D[4]) << 4) + D[3];
+    const int lo = (((D[2] << 4) + D[1]) << 4) + D[0];
+    return fmaf((float)hi, 4096.0f, (float)lo);
+}
+
+// ---- records from LDS -------------------------------------------------------------
+struct RF {
+    i32x4 a0, a1, b0, b1, c0, c1;
+    float S;
+    int sa, sb, sc;
+    float xsum;
+};
+__device__ __forceinline__ RF read_rf(const i32x4* __restrict__ l4, int nb, int c) {
+    RF r;
+    r.a0 = l4[0 * nb + c];
+    r.a1 = l4[1 * nb + c];
+    r.b0 = l4[2 * nb + c];
+    r.b1 = l4[3 * nb + c];
+    r.c0 = l4[4 * nb + c];
+    r.c1 = l4[5 * nb + c];
+    const i32x4 m = l4[6 * nb + c];
+    r.S = as_f32(m.x);
+    r.sa = m.y;
+    r.sb = m.z;
+    r.sc = m.w;
+    r.xsum = as_f32(l4[7 * nb + c].x);
+    return r;
+}
+struct RN {
+    i32x4 q0, q1;
+    float scale;
+    int qsum;
+};
+__device__ __forceinline__ RN read_rn(const i32x4* __restrict__ l4, int nb, int c) {
+    RN r;
+    r.q0 = l4[0 * nb + c];
+    r.q1 = l4[1 * nb + c];
+    const i32x4 m = l4[2 * nb + c];
+    r.scale = as_f32(m.x);
+    r.qsum = m.y;
+    return r;
+}
+
+__device__ __forceinline__ float dot3(const uint32_t (&w)[8], const RF& x, int ia, int ib, int ic) {
+    int A = ia, B = ib, C = ic;
+    A = dot4(w[0], x.a0.x, A); A = dot4(w[1], x.a0.y, A); A = dot4(w[2], x.a0.z, A); A = dot4(w[3], x.a0.w, A);
+    A = dot4(w[4], x.a1.x, A); A = dot4(w[5], x.a1.y, A); A = dot4(w[6], x.a1.z, A); A = dot4(w[7], x.a1.w, A);
+    B = dot4(w[0], x.b0.x, B); B = dot4(w[1], x.b0.y, B); B = dot4(w[2], x.b0.z, B); B = dot4(w[3], x.b0.w, B);
+    B = dot4(w[4], x.b1.x, B); B = dot4(w[5], x.b1.y, B); B = dot4(w[6], x.b1.z, B); B = dot4(w[7], x.b1.w, B);
+    C = dot4(w[0], x.c0.x, C); C = dot4(w[1], x.c0.y, C); C = dot4(w[2], x.c0.z, C); C = dot4(w[3], x.c0.w, C);
+    C = dot4(w[4], x.c1.x, C); C = dot4(w[5], x.c1.y, C); C = dot4(w[6], x.c1.z, C); C = dot4(w[7], x.c1.w, C);
+    const float t = fmaf((float)C, 1.0f / 256.0f, (float)B);
+    return fmaf(t, 1.0f / 256.0f, (float)A);
+}
+__device__ __forceinline__ int dot1(const uint32_t (&w)[8], const RN& x, int acc) {
+    acc = dot4(w[0], x.q0.x, acc); acc = dot4(w[1], x.q0.y, acc);
+    acc = dot4(w[2], x.q0.z, acc); acc = dot4(w[3], x.q0.w, acc);
+    acc = dot4(w[4], x.q1.x, acc); acc = dot4(w[5], x.q1.y, acc);
+    acc = dot4(w[6], x.q1.z, acc); acc = dot4(w[7], x.q1.w, acc);
+    return acc;
+}
+
+// ---- weight windows ------------------------------------------------------------------
+template <int WT> struct Geo;
+template <> struct Geo<(int)WType::Q4_0> { static constexpr int BYTES = 18, WORDS = 5; };
+template <> struct Geo<(int)WType::Q4_1> { static constexpr int BYTES = 20, WORDS = 5; };
+template <> struct Geo<(int)WType::Q8_0> { static constexpr int BYTES = 34, WORDS = 9; };
+
+// Window of WORDS dwords from the dword-aligned base at or below byte `off`.
+// GUARD: the last dword may end 2 bytes past the matrix; read it as 16 bits then.
+template <int WORDS, bool GUARD>
+__device__ __forceinline__ void load_window(const uint8_t* __restrict__ W, uint32_t off,
+                                            uint32_t wbytes, uint32_t (&w)[WORDS]) {
+    const uint32_t base = off & ~3u;
+    const uint8_t* p = W + base;
+    const u32x4a4 v0 = *reinterpret_cast<const u32x4a4*>(p);
+    w[0] = v0.x; w[1] = v0.y; w[2] = v0.z; w[3] = v0.w;
+    if (WORDS == 9) {
+        const u32x4a4 v1 = *reinterpret_cast<const u32x4a4*>(p + 16);
+        w[4] = v1.x; w[5] = v1.y; w[6] = v1.z; w[7] = v1.w;
+    }
+    const uint32_t* tail = reinterpret_cast<const uint32_t*>(p + 4 * (WORDS - 1));
+    if (GUARD && base + 4 * WORDS > wbytes)
+        w[WORDS - 1] = *reinterpret_cast<const uint16_t*>(tail);
+    else
+        w[WORDS - 1] = *tail;
+}
+
+// Per-block decode + dot; returns the block's contribution to y.
+template <int WT, bool NATIVE>
+struct BlockDot;
+
+template <>
+struct BlockDot<(int)WType::Q4_0, false> {
+    __device__ static float run(const uint32_t (&w)[5], uint32_t sel, uint32_t dsh, const RF& x,
+                                int ia, int ib, int ic) {
+        uint32_t q[8];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint32_t nbl = perm(w[k + 1], w[k], sel);
+            q[k] = nbl & NIB;
+            q[k + 4] = (nbl >> 4) & NIB;
+        }
+        const float d = h2f((w[0] >> dsh) & 0xFFFFu);
+        return (x.S * d) * dot3(q, x, ia, ib, ic);
+    }
+};
+template <>
+struct BlockDot<(int)WType::Q8_0, false> {
+    __device__ static float run(const uint32_t (&w)[9], uint32_t sel, uint32_t dsh, const RF& x,
+                                int, int, int) {
+        uint32_t q[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) q[k] = perm(w[k + 1], w[k], sel);
+        const float d = h2f((w[0] >> dsh) & 0xFFFFu);
+        return (x.S * d) * dot3(q, x, 0, 0, 0);
+    }
+};
+template <>
+struct BlockDot<(int)WType::Q4_1, false> {
+    __device__ static float run(const uint32_t (&w)[5], uint32_t, uint32_t, const RF& x, int, int,
+                                int) {
+        uint32_t q[8];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            q[k] = w[k + 1] & NIB;
+            q[k + 4] = (w[k + 1] >> 4) & NIB;
+        }
+        const float d = h2f(w[0] & 0xFFFFu), m = h2f(w[0] >> 16);
+        return fmaf(x.S * d, dot3(q, x, 0, 0, 0), m * x.xsum);
+    }
+};
+template <>
+struct BlockDot<(int)WType::Q4_0, true> {
+    __device__ static float run(const uint32_t (&w)[5], uint32_t sel, uint32_t dsh, const RN& x) {
+        uint32_t q[8];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint32_t nbl = perm(w[k + 1], w[k], sel);
+            q[k] = nbl & NIB;
+            q[k + 4] = (nbl >> 4) & NIB;
+        }
+        const float d = h2f((w[0] >> dsh) & 0xFFFFu);
+        // dot_q4q8_block = sum q*q8 - 8 sum q8 (exact); (int as f32) * sx * sw
+        return ((float)dot1(q, x, -8 * x.qsum) * x.scale) * d;
+    }
+};
+template <>
+struct BlockDot<(int)WType::Q4_1, true> {
+    __device__ static float run(const uint32_t (&w)[5], uint32_t, uint32_t, const RN& x) {
+        uint32_t q[8];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            q[k] = w[k + 1] & NIB;
+            q[k + 4] = (w[k + 1] >> 4) & NIB;
+        }
+        const float d = h2f(w[0] & 0xFFFFu), m = h2f(w[0] >> 16);
+        // q8_scale * (d * unsigned_dot + m * q8_sum)   (quantize.rs:562)
+        return x.scale * (d * (float)dot1(q, x, 0) + m * (float)x.qsum);
+    }
+};
+
+// Q4_0 / Q4_1 float mode on int4 digits.
+template <int WT>
+__device__ __forceinline__ float block_dot_i4(const uint32_t (&w)[5], uint32_t sel, uint32_t dsh,
+                                              const RF4& x) {
+    uint32_t q[4];
+    if (WT == (int)WType::Q4_0) {
+#pragma unroll
+        for (int k = 0; k < 4; k++) q[k] = perm(w[k + 1], w[k], sel) ^ 0x88888888u;  // q - 8
+        const float d = h2f((w[0] >> dsh) & 0xFFFFu);
+        return (x.S() * d) * dot_i4(q, x);
+    } else {
+#pragma unroll
+        for (int k = 0; k < 4; k++) q[k] = w[k + 1] ^ 0x88888888u;  // q - 8
+        const float d = h2f(w[0] & 0xFFFFu), m = h2f(w[0] >> 16);
+        // sum q x = sum (q-8) x + 8 sum x
+        return fmaf(x.S() * d, dot_i4(q, x), fmaf(8.0f, d, m) * x.xsum());
+    }
+}
+
+template <int R>
+__device__ __forceinline__ float wave_reduce_rows(float (&v)[R], int lane) {
+    int count = R;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        if (count > 1) {
+            const int half = count / 2;
+            const bool upper = (lane & o) != 0;
+#pragma unroll
+            for (int i = 0; i < R / 2; i++) {
+                if (i < half) {
+                    const float keep = upper ? v[half + i] : v[i];
+                    const float send = upper ? v[i] : v[half + i];
+                    v[i] = keep + __shfl_xor(send, o);
+                }
+            }
+            count = half;
+        } else {
+            v[0] += __shfl_xor(v[0], o);
+        }
+    }
+    return v[0];
+}
+
+// ---- the fused kernel (Q4_0 / Q4_1 / Q8_0) ----------------------------------------------
+// Block g of the matrix starts at byte g*BYTES; with BYTES = 18 or 34 its
+// dword alignment alternates with g.  When nb is even the parity of g is the
+// parity of the column, so the realignment selectors are per column.
+//
+// A wave owns R rows x CPL columns = NB blocks per lane, visited row-major.
+// The loads run PF blocks ahead of the compute in program order: a wave issues
+// its instructions in order and the memory pipeline accepts only so many
+// loads per CU, so interleaving load issue with compute is what lets the dot
+// products overlap the weight stream.
+template <int WT, bool NATIVE, int R, int CPL, bool NB_EVEN, int NW>
+__global__ __launch_bounds__(NW * 64) void gemv_fused_kernel(const uint8_t* __restrict__ W, int n,
+                                                        int nb, int rpw,
+                                                        const float* __restrict__ X,
+                                                        float* __restrict__ Y) {
+    extern __shared__ i32x4 lds4[];
+    constexpr int BYTES = Geo<WT>::BYTES, WORDS = Geo<WT>::WORDS;
+    constexpr int LPB = (WORDS == 9) ? 3 : 2;    // load instructions per block
+    constexpr int NB = R * CPL;                   // blocks per lane
+    constexpr int PF = (NB < 4) ? NB : 4;         // blocks in flight ahead of the compute
+    // Q4_0 / Q4_1 float mode use int4-digit records (four threads per column),
+    // everything else int8 records (eight threads per column)
+    constexpr bool I4 = !NATIVE && (WT == (int)WType::Q4_0 || WT == (int)WType::Q4_1);
+    constexpr int PI = I4 ? (CPL * 4 + NW - 1) / NW : (CPL * 8 + NW - 1) / NW;
+    const int lane = threadIdx.x & 63;
+    const int wv = threadIdx.x >> 6;
+    const int r0 = blockIdx.x * rpw;
+    const int rend = min(n, r0 + rpw);
+    const float* x = X + (size_t)blockIdx.y * nb * 32;
+    float* y = Y + (size_t)blockIdx.y * n;
+    const uint32_t row_bytes = (uint32_t)nb * BYTES;
+    const uint32_t wbytes = (uint32_t)n * row_bytes;
+
+    // Branch-free load issue (rows past the workgroup's range are clamped and
+    // re-read a valid row), so the compiler's wait counts are exact.  With nb
+    // even the last block of the matrix has an odd index and its window ends
+    // exactly at the end of the matrix; only odd nb needs the guarded tail load.
+    uint32_t win[NB][WORDS];
+    auto issue = [&](int b) {
+        const int r = b / CPL, i = b % CPL;
+        const int row = min(r0 + wv + r * NW, rend - 1);
+        const uint32_t off = (uint32_t)row * row_bytes + (uint32_t)min(lane + 64 * i, nb - 1) * BYTES;
+        if (NB_EVEN)
+            load_window<WORDS, false>(W, off, wbytes, win[b]);
+        else
+            load_window<WORDS, true>(W, off, wbytes, win[b]);
+    };
+
+    // ---- x for the prep first, then the first PF blocks ----
+    if constexpr (I4) {
+        f32x4 xv[PI][2];
+        load_prep_x4<NW, PI>(x, nb, xv);
+#pragma unroll
+        for (int b = 0; b < PF; b++) issue(b);
+        wait_prep_x<PF * LPB>();
+        prep_float4_lds<NW, PI>(xv, nb, reinterpret_cast<int*>(lds4));
+    } else {
+        f32x4 xv[PI];
+        load_prep_x<NW, PI>(x, nb, xv);
+#pragma unroll
+        for (int b = 0; b < PF; b++) issue(b);
+        wait_prep_x<PF * LPB>();
+        if constexpr (NATIVE)
+            prep_native_lds<NW, PI>(xv, nb, reinterpret_cast<int*>(lds4));
+        else
+            prep_float_lds<NW, PI>(xv, nb, reinterpret_cast<int*>(lds4));
+    }
+    __syncthreads();
+
+    // column records: kept in registers when a lane has at most two columns
+    constexpr bool KEEP = (CPL <= 2);
+    using Rec = typename std::conditional<NATIVE, RN, typename std::conditional<I4, RF4, RF>::type>::type;
+    Rec keep[KEEP ? CPL : 1];
+    auto read_rec = [&](int col) -> Rec {
+        if constexpr (NATIVE) return read_rn(lds4, nb, col);
+        else if constexpr (I4) return read_rf4(lds4, nb, col);
+        else return read_rf(lds4, nb, col);
+    };
+    if constexpr (KEEP) {
+#pragma unroll
+        for (int i = 0; i < CPL; i++) keep[i] = read_rec(min(lane + 64 * i, nb - 1));
+    }
+
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        if (b + PF < NB) issue(b + PF);
+        const int r = b / CPL, i = b % CPL;
+        const int row = r0 + wv + r * NW;
+        const int col = lane + 64 * i;
+        if (row < rend && col < nb) {
+            const bool odd = NB_EVEN ? (col & 1) : (((row * nb + col) & 1) != 0);
+            const uint32_t sel = odd ? 0x07060504u : 0x05040302u;
+            const uint32_t dsh = odd ? 16u : 0u;
+            if constexpr (NATIVE) {
+                const RN xr = KEEP ? keep[KEEP ? i : 0] : read_rec(col);
+                acc[r] += BlockDot<WT, true>::run(win[b], sel, dsh, xr);
+            } else if constexpr (I4) {
+                const RF4 xr = KEEP ? keep[KEEP ? i : 0] : read_rec(col);
+                acc[r] += block_dot_i4<WT>(win[b], sel, dsh, xr);
+            } else {
+                const RF xr = KEEP ? keep[KEEP ? i : 0] : read_rec(col);
+                const int ia = (WT == (int)WType::Q4_0) ? -8 * xr.sa : 0;
+                const int ib = (WT == (int)WType::Q4_0) ? -8 * xr.sb : 0;
+                const int ic = (WT == (int)WType::Q4_0) ? -8 * xr.sc : 0;
+                acc[r] += BlockDot<WT, false>::run(win[b], sel, dsh, xr, ia, ib, ic);
+            }
+        }
+    }
+    if (r0 + wv >= rend) return;  // wave-uniform; the wave had nothing to store
+
+    // ---- reduce and store ----
+    constexpr int RP = (R > 2) ? 4 : R;  // reduction width: power of two >= R
+    float red[RP];
+#pragma unroll
+    for (int r = 0; r < RP; r++) red[r] = (r < R) ? acc[r] : 0.0f;
+    const float s = wave_reduce_rows<RP>(red, lane);
+    constexpr int LOG2R = (RP >= 4) ? 2 : (RP >= 2) ? 1 : 0;
+    constexpr int SPAN = 64 >> LOG2R;
+    if ((lane & (SPAN - 1)) == 0) {
+        const int row = r0 + wv + (lane >> (6 - LOG2R)) * NW;
+        if (row < rend) y[row] = s;
+    }
+}
+
+// ---- Q4_K (float mode) ------------------------------------------------------------------
+// A unit is one 32-byte chunk of a super-block's nibbles: sub-block 2c (lo
+// nibbles) and 2c+1 (hi nibbles) of super-block sb (parser.rs:574-589).
+__device__ __forceinline__ void q4k_scale_min(const u32x4& h, int c, int& sc1, int& mn1, int& sc2,
+                                              int& mn2) {
+    const uint32_t j1 = 2 * c;
+    if (c < 2) {
+        // j < 4: sc = s[j] & 63, mn = s[j+4] & 63                  (parser.rs:565-566)
+        sc1 = (int)((h.y >> (8 * j1)) & 63);
+        sc2 = (int)((h.y >> (8 * (j1 + 1))) & 63);
+        mn1 = (int)((h.z >> (8 * j1)) & 63);
+        mn2 = (int)((h.z >> (8 * (j1 + 1))) & 63);
+    } else {
+        // j >= 4, i = j-4: sc = ((s[i]>>6)&3) | ((s[i+8]&0xF)<<2),
+        //                  mn = ((s[i+4]>>6)&3) | ((s[i+8]>>4)<<2) (parser.rs:567-568)
+        const uint32_t i1 = j1 - 4;
+        const uint32_t si1 = h.y >> (8 * i1), si2 = h.y >> (8 * (i1 + 1));
+        const uint32_t ti1 = h.z >> (8 * i1), ti2 = h.z >> (8 * (i1 + 1));
+        const uint32_t ui1 = h.w >> (8 * i1), ui2 = h.w >> (8 * (i1 + 1));
+        sc1 = (int)(((si1 >> 6) & 3) | ((ui1 & 0xF) << 2));
+        sc2 = (int)(((si2 >> 6) & 3) | ((ui2 & 0xF) << 2));
+        mn1 = (int)(((ti1 >> 6) & 3) | (((ui1 >> 4) & 0xF) << 2));
+        mn2 = (int)(((ti2 >> 6) & 3) | (((ui2 >> 4) & 0xF) << 2));
+    }
+}
+
+template <int R, int UPL, int NW>
+__global__ __launch_bounds__(NW * 64) void gemv_q4k_fused_kernel(const uint8_t* __restrict__ W, int n,
+                                                            int nsb, int rpw,
+                                                            const float* __restrict__ X,
+                                                            float* __restrict__ Y) {
+    extern __shared__ i32x4 lds4[];
+    const int lane = threadIdx.x & 63;
+    const int wv = threadIdx.x >> 6;
+    const int r0 = blockIdx.x * rpw;
+    const int rend = min(n, r0 + rpw);
+    const int nb = nsb * 8, nunits = nsb * 4;
+    const float* x = X + (size_t)blockIdx.y * nb * 32;
+    float* y = Y + (size_t)blockIdx.y * n;
+    const uint32_t row_bytes = (uint32_t)nsb * Q4_K_BYTES;
+    constexpr int PI = (UPL * 16 + NW - 1) / NW;  // nb * 8 = 16 * units <= 1024 * UPL
+    f32x4 xv[PI];
+    load_prep_x<NW, PI>(x, nb, xv);
+
+    u32x4 hdr[R][UPL], qa[R][UPL], qb[R][UPL];
+    // no control flow here (rows clamped): exactly 3 loads per (row, unit)
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const int row = min(r0 + wv + r * NW, rend - 1);
+#pragma unroll
+        for (int i = 0; i < UPL; i++) {
+            const int u = min(lane + 64 * i, nunits - 1);
+            const uint8_t* p = W + (uint32_t)row * row_bytes + (uint32_t)(u >> 2) * Q4_K_BYTES;
+            hdr[r][i] = *reinterpret_cast<const u32x4*>(p);
+            qa[r][i] = *reinterpret_cast<const u32x4*>(p + 16 + 32 * (u & 3));
+            qb[r][i] = *reinterpret_cast<const u32x4*>(p + 32 + 32 * (u & 3));
+        }
+    }
+    wait_prep_x<R * UPL * 3>();  // header + two 16-byte nibble loads per unit
+    prep_float_lds<NW, PI>(xv, nb, reinterpret_cast<int*>(lds4));
+    __syncthreads();
+    if (r0 + wv >= rend) return;
+
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < UPL; i++) {
+        const int u = lane + 64 * i;
+        if (u < nunits) {
+            const int sb = u >> 2, c = u & 3;
+            const RF x1 = read_rf(lds4, nb, sb * 8 + 2 * c);
+            const RF x2 = read_rf(lds4, nb, sb * 8 + 2 * c + 1);
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                if (r0 + wv + r * NW < rend) {
+                    const uint32_t raw[8] = {qa[r][i].x, qa[r][i].y, qa[r][i].z, qa[r][i].w,
+                                             qb[r][i].x, qb[r][i].y, qb[r][i].z, qb[r][i].w};
+                    uint32_t lo[8], hi[8];
+#pragma unroll
+                    for (int k = 0; k < 8; k++) {
+                        lo[k] = raw[k] & NIB;
+                        hi[k] = (raw[k] >> 4) & NIB;
+                    }
+                    const float d = h2f(hdr[r][i].x & 0xFFFFu);
+                    const float dmin = h2f(hdr[r][i].x >> 16);
+                    int sc1, mn1, sc2, mn2;
+                    q4k_scale_min(hdr[r][i], c, sc1, mn1, sc2, mn2);
+                    // element value (d*sc)*q - (dmin*mn)   (parser.rs:577-587)
+                    const float d1 = d * (float)sc1, m1 = dmin * (float)mn1;
+                    const float d2 = d * (float)sc2, m2 = dmin * (float)mn2;
+                    float a = acc[r];
+                    a = fmaf(d1 * x1.S, dot3(lo, x1, 0, 0, 0), a);
+                    a = fmaf(-m1, x1.xsum, a);
+                    a = fmaf(d2 * x2.S, dot3(hi, x2, 0, 0, 0), a);
+                    a = fmaf(-m2, x2.xsum, a);
+                    acc[r] = a;
+                }
+            }
+        }
+    }
+    const float s = wave_reduce_rows<R>(acc, lane);
+    constexpr int LOG2R = (R >= 4) ? 2 : (R >= 2) ? 1 : 0;
+    constexpr int SPAN = 64 >> LOG2R;
+    if ((lane & (SPAN - 1)) == 0) {
+        const int row = r0 + wv + (lane >> (6 - LOG2R)) * NW;
+        if (row < rend) y[row] = s;
+    }
+}
+
+int g_num_cus = 0;
+
+int num_cus() {
+    if (g_num_cus == 0) {
+        int dev = 0, cus = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+            cus > 0)
+            g_num_cus = cus;
+        else
+            g_num_cus = 256;
+    }
+    return g_num_cus;
+}
+
+// Columns per lane (CPL) x rows per wave (R) <= 8 keeps the block windows
+// within the VGPR budget.
+int cpl_for(int nb) { return nb <= 128 ? 2 : nb <= 256 ? 4 : 8; }
+
+struct Cfg {
+    int nw;   // waves per workgroup
+    int rpw;  // rows per workgroup
+    int r;    // rows per wave (template R)
+};
+
+// Spread the rows over about `wg_per_cu` workgroups per CU with at most rmax
+// rows per wave.
+Cfg pick_cfg(int n, int nw, int rmax, int wg_per_cu) {
+    const int target = num_cus() * wg_per_cu;
+    int rpw = (n + target - 1) / target;
+    if (rpw > rmax * nw) rpw = rmax * nw;
+    if (rpw < 1) rpw = 1;
+    int r = (rpw + nw - 1) / nw;
+    r = r <= 1 ? 1 : r <= 2 ? 2 : r <= 3 ? 3 : 4;
+    return Cfg{nw, rpw, r};
+}
+
+template <int WT, bool NATIVE, int CPL, bool EVEN, int NW>
+void launch_nw(const uint8_t* w, int n, int nb, const float* x, size_t m, float* y, hipStream_t s,
+               const Cfg& c, size_t lds) {
+    const dim3 grid((unsigned)((n + c.rpw - 1) / c.rpw), (unsigned)m), block(NW * 64);
+    constexpr int RMAX = 8 / CPL;
+    const int rpw = c.rpw;
+    if (c.r <= 1 || RMAX == 1)
+        launch_kernel((gemv_fused_kernel<WT, NATIVE, 1, CPL, EVEN, NW>), grid, block, lds, s, w, n, nb, rpw, x, y);
+    else if (c.r <= 2 || RMAX == 2)
+        launch_kernel((gemv_fused_kernel<WT, NATIVE, (RMAX >= 2 ? 2 : 1), CPL, EVEN, NW>), grid, block, lds, s, w, n, nb, rpw, x, y);
+    else if (c.r <= 3)
+        launch_kernel((gemv_fused_kernel<WT, NATIVE, (RMAX >= 4 ? 3 : 1), CPL, EVEN, NW>), grid, block, lds, s, w, n, nb, rpw, x, y);
+    else
+        launch_kernel((gemv_fused_kernel<WT, NATIVE, (RMAX >= 4 ? 4 : 1), CPL, EVEN, NW>), grid, block, lds, s, w, n, nb, rpw, x, y);
+}
+
+template <int WT, bool NATIVE, int CPL, bool EVEN>
+void launch_even(const uint8_t* w, int n, int nb, const float* x, size_t m, float* y,
+                 hipStream_t s, const Cfg& c, size_t lds) {
+    if (c.nw == 4) launch_nw<WT, NATIVE, CPL, EVEN, 4>(w, n, nb, x, m, y, s, c, lds);
+    else if (c.nw == 8) launch_nw<WT, NATIVE, CPL, EVEN, 8>(w, n, nb, x, m, y, s, c, lds);
+    else launch_nw<WT, NATIVE, CPL, EVEN, 16>(w, n, nb, x, m, y, s, c, lds);
+}
+
+template <int WT, bool NATIVE, int CPL>
+void launch_wt(const uint8_t* w, int n, int nb, const float* x, size_t m, float* y,
+               hipStream_t s, const Cfg& c, size_t lds) {
+    if ((nb & 1) == 0 || WT == (int)WType::Q4_1)
+        launch_even<WT, NATIVE, CPL, true>(w, n, nb, x, m, y, s, c, lds);
+    else
+        launch_even<WT, NATIVE, CPL, false>(w, n, nb, x, m, y, s, c, lds);
+}
+
+template <int WT, bool NATIVE>
+void launch_cpl(const uint8_t* w, int n, int nb, const float* x, size_t m, float* y,
+                hipStream_t s, size_t lds, int nw, int wg_per_cu) {
+    const int cpl = cpl_for(nb);
+    const Cfg c = pick_cfg(n, nw, 8 / cpl, wg_per_cu);
+    switch (cpl) {
+        case 2: launch_wt<WT, NATIVE, 2>(w, n, nb, x, m, y, s, c, lds); break;
+        case 4: launch_wt<WT, NATIVE, 4>(w, n, nb, x, m, y, s, c, lds); break;
+        default: launch_wt<WT, NATIVE, 8>(w, n, nb, x, m, y, s, c, lds); break;
+    }
+}
+
+template <int NW>
+void launch_q4k_nw(const uint8_t* w, int n, int nsb, const float* x, size_t m, float* y,
+                   hipStream_t s, size_t lds, int wg_per_cu) {
+    const int units = nsb * 4;
+    if (units > 64) {
+        const Cfg c = pick_cfg(n, NW, 1, wg_per_cu);
+        const dim3 grid((unsigned)((n + c.rpw - 1) / c.rpw), (unsigned)m), block(NW * 64);
+        launch_kernel((gemv_q4k_fused_kernel<1, 4, NW>), grid, block, lds, s, w, n, nsb, c.rpw, x, y);
+        return;
+    }
+    const Cfg c = pick_cfg(n, NW, 4, wg_per_cu);
+    const dim3 grid((unsigned)((n + c.rpw - 1) / c.rpw), (unsigned)m), block(NW * 64);
+    switch (c.r) {
+        case 1: launch_kernel((gemv_q4k_fused_kernel<1, 1, NW>), grid, block, lds, s, w, n, nsb, c.rpw, x, y); break;
+        case 2: launch_kernel((gemv_q4k_fused_kernel<2, 1, NW>), grid, block, lds, s, w, n, nsb, c.rpw, x, y); break;
+        case 3: launch_kernel((gemv_q4k_fused_kernel<3, 1, NW>), grid, block, lds, s, w, n, nsb, c.rpw, x, y); break;
+        default: launch_kernel((gemv_q4k_fused_kernel<4, 1, NW>), grid, block, lds, s, w, n, nsb, c.rpw, x, y); break;
+    }
+}
+
+}  // namespace
+
+// Largest K the fused kernels take (records for all of K live in LDS and a
+// lane holds at most 8 columns of blocks in registers).
+size_t fused_max_k(WType t) { return t == WType::Q4_K ? 16384 : 16384; }
+
+hipError_t launch_gemv_fused(WType t, bool native, const uint8_t* w, size_t n, size_t k,
+                             const float* x, size_t m, float* y, hipStream_t s) {
+    if (n == 0 || m == 0) return hipSuccess;
+    const int nb = (int)(k / QK);
+    const size_t lds = (size_t)(native ? 3 : 8) * 16 * (nb > 0 ? nb : 1);
+    const int ni = (int)n;
+    const int nw = 16, wg_per_cu = 1;
+    if (t == WType::Q4_K) {
+        launch_q4k_nw<16>(w, ni, (int)(k / QK_K), x, m, y, s, lds, wg_per_cu);
+        return hipGetLastError();
+    }
+    if (native) {
+        if (t == WType::Q4_1) launch_cpl<(int)WType::Q4_1, true>(w, ni, nb, x, m, y, s, lds, nw, wg_per_cu);
+        else launch_cpl<(int)WType::Q4_0, true>(w, ni, nb, x, m, y, s, lds, nw, wg_per_cu);
+    } else if (t == WType::Q4_1) {
+        launch_cpl<(int)WType::Q4_1, false>(w, ni, nb, x, m, y, s, lds, nw, wg_per_cu);
+    } else if (t == WType::Q8_0) {
+        launch_cpl<(int)WType::Q8_0, false>(w, ni, nb, x, m, y, s, lds, nw, wg_per_cu);
+    } else {
+        launch_cpl<(int)WType::Q4_0, false>(w, ni, nb, x, m, y, s, lds, nw, wg_per_cu);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace rdl

@@ -10,6 +10,12 @@ typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 
+// Reinterpret an int32 as f32.  Takes the value (not an lvalue): clang lowers
+// __builtin_bit_cast of an ext_vector_type component such as v.y as a load
+// from the start of the vector, i.e. it returns v.x.  Use this helper for
+// vector components.
+__device__ __forceinline__ float as_f32(int32_t v) { return __builtin_bit_cast(float, v); }
+
 // IEEE binary16 -> binary32 through the hardware converter (exact, keeps
 // subnormals: kernels run with f16 denormals enabled, the HSA default).
 __device__ __forceinline__ float h2f(uint32_t bits16) {

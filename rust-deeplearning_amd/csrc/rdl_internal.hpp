@@ -2,6 +2,7 @@
 // librdlquant.so (kernels, launchers and the C ABI).  Not part of the ABI.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
@@ -69,6 +70,26 @@ inline size_t block_bytes(WType t) {
     return 0;
 }
 
+// ---- kernel-boundary timing -----------------------------------------------
+// When set (rdl_time_next_launch), the next product-kernel launch of this
+// thread records its start/end into these events via hipExtLaunchKernel.
+struct LaunchEvents {
+    hipEvent_t start = nullptr, stop = nullptr;
+};
+extern thread_local LaunchEvents g_launch_events;
+
+template <typename F, typename... Args>
+inline void launch_kernel(F kernel, dim3 grid, dim3 block, size_t lds, hipStream_t s,
+                          Args... args) {
+    LaunchEvents& ev = g_launch_events;
+    if (ev.start || ev.stop) {
+        hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t)lds, s, ev.start, ev.stop, 0, args...);
+        ev = LaunchEvents{};
+    } else {
+        hipLaunchKernelGGL(kernel, grid, block, lds, s, args...);
+    }
+}
+
 // ---- launchers (return hipSuccess or the launch error) --------------------
 
 // x [m, k] f32 -> FloatRec [m, k/32]
@@ -81,6 +102,12 @@ hipError_t launch_prep_native(const float* x, size_t m, size_t k, NativeRec* rec
 // y[m, n] = x . W^T from prepared activations, one GEMV per activation row.
 hipError_t launch_gemv(WType t, bool native, const uint8_t* w, size_t n, size_t k,
                        const void* xrec, size_t m, float* y, hipStream_t s);
+
+// Single-launch GEMV with the activation preparation fused in (x f32 [m, k],
+// 16-byte aligned); valid for k <= fused_max_k(t).
+size_t fused_max_k(WType t);
+hipError_t launch_gemv_fused(WType t, bool native, const uint8_t* w, size_t n, size_t k,
+                             const float* x, size_t m, float* y, hipStream_t s);
 
 // int32 block partials of the Q4_0 x Q8_0 path for one activation row.
 hipError_t launch_q4_0_block_dots(const uint8_t* w, size_t n, size_t k, const NativeRec* rec,

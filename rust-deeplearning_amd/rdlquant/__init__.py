@@ -89,6 +89,7 @@ _decl("rdl_status_string", C.c_char_p, _i32)
 _decl("rdl_last_error", C.c_char_p)
 _decl("rdl_version", C.c_char_p)
 _decl("rdl_device_count", _i32)
+_decl("rdl_time_next_launch", _i32, _p, _p)
 for _n in ("q8", "q4", "q4_native", "q4_1", "q4_1_native", "q4_k"):
     _decl(f"rdl_matmul_f32_{_n}", _i32, _fp, _sz, _u8p, _sz, _sz, _sz, _sz, _fp, _sz)
 _decl("rdl_quantize_row_q8_0", _i32, _fp, _sz, _u8p, _sz, _fp, _sz)
@@ -152,6 +153,12 @@ def device_count() -> int:
 
 def version() -> str:
     return lib.rdl_version().decode()
+
+
+def time_next_launch(start_event, stop_event):
+    """Kernel-boundary timing of this thread's next product-kernel launch
+    (hipEvent_t handles, e.g. torch.cuda.Event(enable_timing=True).cuda_event)."""
+    check(lib.rdl_time_next_launch(start_event, stop_event))
 
 
 # ---- host drop-ins (rustml_quant) -----------------------------------------

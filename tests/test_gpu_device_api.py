@@ -1,0 +1,148 @@
+"""GPU tests of the device-resident entry points (weights in HBM, torch streams)."""
+import numpy as np
+import pytest
+
+from rdlquant import synth
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-3, 1e-4
+KIND = {2: "q4", 3: "q4_1", 8: "q8", 12: "q4k"}
+DEQ = {2: "q4_0", 3: "q4_1", 8: "q8_0", 12: "q4k"}
+
+
+def close(got, want, exact):
+    got, want = np.asarray(got, np.float64).ravel(), np.asarray(want, np.float64).ravel()
+    assert np.all(np.abs(got - exact) <= ATOL + RTOL * np.abs(exact))
+    assert np.all(np.abs(got - want) <= ATOL + RTOL * np.abs(want) + np.abs(want - exact))
+
+
+def dev_weight(rq, torch, w, dtype, n, k):
+    t = torch.from_numpy(w).cuda()
+    return t, rq.Weight.wrap_device(t.data_ptr(), t.numel(), dtype, n, k, keepalive=t)
+
+
+@pytest.mark.parametrize("dtype,n,k", [(2, 11008, 4096), (8, 4096, 4096), (12, 4096, 14336),
+                                       (2, 4096, 14336), (3, 100, 512), (2, 7, 20480)])
+@pytest.mark.parametrize("m", [1, 2])
+def test_prepared_records_path(rq, orc, gpu, dtype, n, k, m):
+    import torch
+
+    x = synth.activations(m, k, 50 + n)
+    w = synth.weights(dtype, n, k, 51 + k)
+    _, h = dev_weight(rq, torch, w, dtype, n, k)
+    xt = torch.from_numpy(x.reshape(-1)).cuda()
+    rec = torch.empty(rq.activation_record_bytes(m, k, rq.MODE_FLOAT), dtype=torch.uint8, device="cuda")
+    yt = torch.empty(m * n, dtype=torch.float32, device="cuda")
+    s = torch.cuda.current_stream().cuda_stream
+    rq.prepare_activations_dev(xt.data_ptr(), m, k, rq.MODE_FLOAT, rec.data_ptr(), s)
+    h.forward_prepared_dev(rec.data_ptr(), m, yt.data_ptr(), rq.MODE_FLOAT, s)
+    torch.cuda.synchronize()
+    want = orc.matmul(KIND[dtype], x, w, m, k, n, threads=8)
+    wd = orc.to_f32(DEQ[dtype], w, n * k).reshape(n, k).astype(np.float64)
+    close(yt.cpu().numpy(), want, (x.astype(np.float64) @ wd.T).ravel())
+    # the fused single-launch path on the same data
+    yf = torch.empty_like(yt)
+    h.forward_dev(xt.data_ptr(), m, yf.data_ptr(), rq.MODE_FLOAT, s)
+    torch.cuda.synchronize()
+    close(yf.cpu().numpy(), want, (x.astype(np.float64) @ wd.T).ravel())
+
+
+def test_prepared_native_bit_equal_to_fused(rq, gpu):
+    import torch
+
+    n, k = 3000, 4096
+    x = synth.activations(1, k, 61)
+    w = synth.q4_0_weights(n, k, 62)
+    _, h = dev_weight(rq, torch, w, 2, n, k)
+    xt = torch.from_numpy(x.reshape(-1)).cuda()
+    s = torch.cuda.current_stream().cuda_stream
+    rec = torch.empty(rq.activation_record_bytes(1, k, rq.MODE_NATIVE), dtype=torch.uint8, device="cuda")
+    y1 = torch.empty(n, dtype=torch.float32, device="cuda")
+    y2 = torch.empty(n, dtype=torch.float32, device="cuda")
+    rq.prepare_activations_dev(xt.data_ptr(), 1, k, rq.MODE_NATIVE, rec.data_ptr(), s)
+    h.forward_prepared_dev(rec.data_ptr(), 1, y1.data_ptr(), rq.MODE_NATIVE, s)
+    h.forward_dev(xt.data_ptr(), 1, y2.data_ptr(), rq.MODE_NATIVE, s)
+    torch.cuda.synchronize()
+    # both reduce exact int32 block dots; only the f32 summation order may differ
+    a, b = y1.cpu().numpy().astype(np.float64), y2.cpu().numpy().astype(np.float64)
+    assert np.all(np.abs(a - b) <= 1e-5 + 1e-5 * np.abs(a))
+
+
+@pytest.mark.parametrize("dtype,kind", [(2, "q4_0"), (8, "q8_0"), (3, "q4_1")])
+def test_dequantize_rows_exact(rq, orc, gpu, dtype, kind):
+    import torch
+
+    n, k = 300, 4096
+    w = synth.weights(dtype, n, k, 70 + dtype)
+    _, h = dev_weight(rq, torch, w, dtype, n, k)
+    rows = np.array([0, 299, 17, 17, 150], dtype=np.int32)
+    rt = torch.from_numpy(rows).cuda()
+    out = torch.empty(len(rows) * k, dtype=torch.float32, device="cuda")
+    h.dequantize_rows_dev(rt.data_ptr(), len(rows), out.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    full = orc.to_f32(kind, w, n * k).reshape(n, k)
+    assert np.array_equal(out.cpu().numpy().reshape(len(rows), k), full[rows])
+
+
+def test_block_dots_dev_exact(rq, orc, gpu):
+    import torch
+
+    n, k = 1000, 4096
+    x = synth.activations(1, k, 81)
+    w = synth.q4_0_weights(n, k, 82)
+    _, h = dev_weight(rq, torch, w, 2, n, k)
+    xt = torch.from_numpy(x.reshape(-1)).cuda()
+    part = torch.empty(n * (k // 32), dtype=torch.int32, device="cuda")
+    h.block_dots_dev(xt.data_ptr(), part.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert np.array_equal(part.cpu().numpy().reshape(1, n, k // 32), orc.block_dots(x, w, 1, k, n))
+
+
+def test_graph_replays_match_eager(rq, gpu):
+    """Captured launches replayed several times, with eager work in between,
+    reproduce the eager result bit for bit (the kernels are deterministic)."""
+    import torch
+
+    n, k = 4096, 4096
+    hs = []
+    for i in range(3):
+        hs.append(dev_weight(rq, torch, synth.q4_0_weights(n, k, 90 + i), 2, n, k))
+    xt = torch.from_numpy(synth.activations(1, k, 93).reshape(-1)).cuda()
+    ys = [torch.empty(n, dtype=torch.float32, device="cuda") for _ in range(3)]
+    s = torch.cuda.current_stream().cuda_stream
+    for (_, h), y in zip(hs, ys):
+        h.forward_dev(xt.data_ptr(), 1, y.data_ptr(), rq.MODE_FLOAT, s)
+    torch.cuda.synchronize()
+    eager = [y.cpu().numpy().copy() for y in ys]
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        cs = torch.cuda.current_stream().cuda_stream
+        for (_, h), y in zip(hs, ys):
+            h.forward_dev(xt.data_ptr(), 1, y.data_ptr(), rq.MODE_FLOAT, cs)
+    for rep in range(4):
+        for y in ys:
+            y.fill_(-1.0)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for y, e in zip(ys, eager):
+            assert np.array_equal(y.cpu().numpy(), e), f"replay {rep}"
+        _ = (xt * 2).sum().item()  # unrelated eager work between replays
+
+
+def test_time_next_launch(rq, gpu):
+    import torch
+
+    n, k = 11008, 4096
+    _, h = dev_weight(rq, torch, synth.q4_0_weights(n, k, 95), 2, n, k)
+    xt = torch.from_numpy(synth.activations(1, k, 96).reshape(-1)).cuda()
+    y = torch.empty(n, dtype=torch.float32, device="cuda")
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(); b.record()
+    torch.cuda.synchronize()
+    rq.time_next_launch(a.cuda_event, b.cuda_event)
+    h.forward_dev(xt.data_ptr(), 1, y.data_ptr(), rq.MODE_FLOAT, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b)
+    assert 0.0005 < ms < 5.0, ms
