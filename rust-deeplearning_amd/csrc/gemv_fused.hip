@@ -42,21 +42,6 @@ __device__ __forceinline__ int lds_word(int g, int k4, int nb, int c) {  // dwor
     return (g * nb + c) * 4 + k4;
 }
 
-__device__ __forceinline__ float max8(float v) {
-    v = fmaxf(v, __shfl_xor(v, 1, 8));
-    v = fmaxf(v, __shfl_xor(v, 2, 8));
-    return fmaxf(v, __shfl_xor(v, 4, 8));
-}
-__device__ __forceinline__ int sum8(int v) {
-    v += __shfl_xor(v, 1, 8);
-    v += __shfl_xor(v, 2, 8);
-    return v + __shfl_xor(v, 4, 8);
-}
-__device__ __forceinline__ float sumf8(float v) {
-    v += __shfl_xor(v, 1, 8);
-    v += __shfl_xor(v, 2, 8);
-    return v + __shfl_xor(v, 4, 8);
-}
 
 // 24-bit fixed-point digits of x_j * (127*65536 / amax):  t + 0x808080 is in
 // [0, 2^24), its bytes u are the digits biased by 128, and u ^ 0x80 is the
@@ -100,8 +85,8 @@ __device__ void prep_float_lds(const f32x4 (&xv)[PI], int nb, int* __restrict__ 
         const f32x4 v = xv[j];
         const bool bad = !(isfinite(v.x) && isfinite(v.y) && isfinite(v.z) && isfinite(v.w));
         float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-        amax = max8(amax);
-        const int anybad = sum8(bad ? 1 : 0);
+        amax = max8_f32(amax);
+        const int anybad = sum8_i32(bad ? 1 : 0);
         // scale tiny blocks by 2^64 so that 8323072/amax stays finite (exact)
         const float pw = (amax < 0x1p-60f) ? 0x1p64f : 1.0f;
         const float inv = (amax > 0.0f && !anybad) ? 8323072.0f / (amax * pw) : 0.0f;
@@ -125,10 +110,10 @@ __device__ void prep_float_lds(const f32x4 (&xv)[PI], int nb, int* __restrict__ 
             lds[lds_word(2 + g, k4, nb, c)] = (int)db;
             lds[lds_word(4 + g, k4, nb, c)] = (int)dc;
         }
-        const int sa = sum8(__builtin_amdgcn_sdot4((int)da, (int)ONES, 0, false));
-        const int sb = sum8(__builtin_amdgcn_sdot4((int)db, (int)ONES, 0, false));
-        const int sc = sum8(__builtin_amdgcn_sdot4((int)dc, (int)ONES, 0, false));
-        const float xs = sumf8((v.x + v.y) + (v.z + v.w));
+        const int sa = sum8_i32(__builtin_amdgcn_sdot4((int)da, (int)ONES, 0, false));
+        const int sb = sum8_i32(__builtin_amdgcn_sdot4((int)db, (int)ONES, 0, false));
+        const int sc = sum8_i32(__builtin_amdgcn_sdot4((int)dc, (int)ONES, 0, false));
+        const float xs = sum8_f32((v.x + v.y) + (v.z + v.w));
         if (k == 0 && p < nb * 8) {
             const float nan = __builtin_nanf("");
             lds[lds_word(6, 0, nb, c)] = __builtin_bit_cast(int, anybad ? nan : amax / 127.0f);
@@ -152,7 +137,7 @@ __device__ void prep_native_lds(const f32x4 (&xv)[PI], int nb, int* __restrict__
         const f32x4 v = xv[j];
         // fmaxf(0, |x|) drops NaN as the fold from 0.0 with f32::max does
         float amax = fmaxf(fmaxf(fmaxf(0.0f, fabsf(v.x)), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-        amax = max8(amax);
+        amax = max8_f32(amax);
         const float scale = (amax == 0.0f) ? 0.0f : amax / 127.0f;
         const float rt = h2f(f2h_rne(scale));
         const float inv = (rt == 0.0f) ? 0.0f : 1.0f / rt;
@@ -165,7 +150,7 @@ __device__ void prep_native_lds(const f32x4 (&xv)[PI], int nb, int* __restrict__
             d |= ((uint32_t)q & 0xFFu) << (8 * j);
         }
         if (p < nb * 8) lds[lds_word(k >> 2, k & 3, nb, c)] = (int)d;
-        const int qs = sum8(__builtin_amdgcn_sdot4((int)d, (int)ONES, 0, false));
+        const int qs = sum8_i32(__builtin_amdgcn_sdot4((int)d, (int)ONES, 0, false));
         if (k == 0 && p < nb * 8) {
             lds[lds_word(2, 0, nb, c)] = __builtin_bit_cast(int, rt);
             lds[lds_word(2, 1, nb, c)] = qs;
@@ -187,18 +172,6 @@ __device__ void prep_native_lds(const f32x4 (&xv)[PI], int nb, int* __restrict__
 // (dwords k = 0..3), g6 = {S4, sum x, 0, 0}.  Four threads share a column;
 // thread k handles elements 4k..4k+3 and 4k+16..4k+19.
 
-__device__ __forceinline__ float max4(float v) {
-    v = fmaxf(v, __shfl_xor(v, 1, 4));
-    return fmaxf(v, __shfl_xor(v, 2, 4));
-}
-__device__ __forceinline__ int sum4(int v) {
-    v += __shfl_xor(v, 1, 4);
-    return v + __shfl_xor(v, 2, 4);
-}
-__device__ __forceinline__ float sumf4(float v) {
-    v += __shfl_xor(v, 1, 4);
-    return v + __shfl_xor(v, 2, 4);
-}
 
 // Nibble levels 2b and 2b+1 of the eight codes: P holds byte b of elements
 // 4k..4k+3, Q byte b of elements 4k+16..4k+19.
@@ -236,8 +209,8 @@ __device__ void prep_float4_lds(const f32x4 (&xv)[PI][2], int nb, int* __restric
             bad |= !isfinite(v[i]);
             amax = fmaxf(amax, fabsf(v[i]));
         }
-        amax = max4(amax);
-        const int anybad = sum4(bad ? 1 : 0);
+        amax = max4_f32(amax);
+        const int anybad = sum4_i32(bad ? 1 : 0);
         const float pw = (amax < 0x1p-60f) ? 0x1p64f : 1.0f;
         const float f = (amax > 0.0f && !anybad) ? pw * (7829365.0f / (amax * pw)) : 0.0f;
         uint32_t e[8];
@@ -259,7 +232,7 @@ __device__ void prep_float4_lds(const f32x4 (&xv)[PI][2], int nb, int* __restric
         float xs = 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; i++) xs += v[i];
-        xs = sumf4(xs);
+        xs = sum4_f32(xs);
         if (p < nb * 4) {
 #pragma unroll
             for (int lv = 0; lv < 6; lv++) lds[lds_word(lv, k, nb, c)] = (int)L[lv];
@@ -367,24 +340,27 @@ template <> struct Geo<(int)WType::Q4_0> { static constexpr int BYTES = 18, WORD
 template <> struct Geo<(int)WType::Q4_1> { static constexpr int BYTES = 20, WORDS = 5; };
 template <> struct Geo<(int)WType::Q8_0> { static constexpr int BYTES = 34, WORDS = 9; };
 
-// Window of WORDS dwords from the dword-aligned base at or below byte `off`.
-// GUARD: the last dword may end 2 bytes past the matrix; read it as 16 bits then.
+// Window of WORDS dwords from the dword-aligned base at or below byte `off`
+// (off = RSRC_OOB: no load, zeros).  Branch-free.
+// GUARD: the last dword may end 2 bytes past the matrix (an aligned block at
+// the very end); it is then read as the matrix's last dword shifted down 16.
 template <int WORDS, bool GUARD>
-__device__ __forceinline__ void load_window(const uint8_t* __restrict__ W, uint32_t off,
+__device__ __forceinline__ void load_window(__amdgpu_buffer_rsrc_t rs, uint32_t off,
                                             uint32_t wbytes, uint32_t (&w)[WORDS]) {
     const uint32_t base = off & ~3u;
-    const uint8_t* p = W + base;
-    const u32x4a4 v0 = *reinterpret_cast<const u32x4a4*>(p);
+    const u32x4 v0 = buf_load_b128(rs, base);
     w[0] = v0.x; w[1] = v0.y; w[2] = v0.z; w[3] = v0.w;
-    if (WORDS == 9) {
-        const u32x4a4 v1 = *reinterpret_cast<const u32x4a4*>(p + 16);
+    if constexpr (WORDS == 9) {
+        const u32x4 v1 = buf_load_b128(rs, base + 16);
         w[4] = v1.x; w[5] = v1.y; w[6] = v1.z; w[7] = v1.w;
     }
-    const uint32_t* tail = reinterpret_cast<const uint32_t*>(p + 4 * (WORDS - 1));
-    if (GUARD && base + 4 * WORDS > wbytes)
-        w[WORDS - 1] = *reinterpret_cast<const uint16_t*>(tail);
-    else
-        w[WORDS - 1] = *tail;
+    const uint32_t toff = base + 4 * (WORDS - 1);
+    if constexpr (GUARD) {
+        const bool over = base < wbytes && base + 4 * WORDS > wbytes;
+        w[WORDS - 1] = buf_load_b32(rs, over ? wbytes - 4 : toff) >> (over ? 16 : 0);
+    } else {
+        w[WORDS - 1] = buf_load_b32(rs, toff);
+    }
 }
 
 // Per-block decode + dot; returns the block's contribution to y.
@@ -480,29 +456,6 @@ __device__ __forceinline__ float block_dot_i4(const uint32_t (&w)[5], uint32_t s
     }
 }
 
-template <int R>
-__device__ __forceinline__ float wave_reduce_rows(float (&v)[R], int lane) {
-    int count = R;
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        if (count > 1) {
-            const int half = count / 2;
-            const bool upper = (lane & o) != 0;
-#pragma unroll
-            for (int i = 0; i < R / 2; i++) {
-                if (i < half) {
-                    const float keep = upper ? v[half + i] : v[i];
-                    const float send = upper ? v[i] : v[half + i];
-                    v[i] = keep + __shfl_xor(send, o);
-                }
-            }
-            count = half;
-        } else {
-            v[0] += __shfl_xor(v[0], o);
-        }
-    }
-    return v[0];
-}
 
 // ---- the fused kernel (Q4_0 / Q4_1 / Q8_0) ----------------------------------------------
 // Block g of the matrix starts at byte g*BYTES; with BYTES = 18 or 34 its
@@ -537,19 +490,20 @@ __global__ __launch_bounds__(NW * 64) void gemv_fused_kernel(const uint8_t* __re
     const uint32_t row_bytes = (uint32_t)nb * BYTES;
     const uint32_t wbytes = (uint32_t)n * row_bytes;
 
-    // Branch-free load issue (rows past the workgroup's range are clamped and
-    // re-read a valid row), so the compiler's wait counts are exact.  With nb
-    // even the last block of the matrix has an odd index and its window ends
-    // exactly at the end of the matrix; only odd nb needs the guarded tail load.
+    // Branch-free load issue (a slot past the workgroup's rows or the row's
+    // blocks loads nothing: out-of-range buffer offset), so the compiler's
+    // wait counts are exact.  With nb even the last block of the matrix has an
+    // odd index and its window ends exactly at the end of the matrix; only odd
+    // nb needs the guarded tail load.
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(W, wbytes);
     uint32_t win[NB][WORDS];
     auto issue = [&](int b) {
         const int r = b / CPL, i = b % CPL;
-        const int row = min(r0 + wv + r * NW, rend - 1);
-        const uint32_t off = (uint32_t)row * row_bytes + (uint32_t)min(lane + 64 * i, nb - 1) * BYTES;
-        if (NB_EVEN)
-            load_window<WORDS, false>(W, off, wbytes, win[b]);
-        else
-            load_window<WORDS, true>(W, off, wbytes, win[b]);
+        const int row = r0 + wv + r * NW, col = lane + 64 * i;
+        const uint32_t off = (row < rend && col < nb)
+                                 ? (uint32_t)row * row_bytes + (uint32_t)col * BYTES
+                                 : RSRC_OOB;
+        load_window<WORDS, !NB_EVEN>(rs, off, wbytes, win[b]);
     };
 
     // ---- x for the prep first, then the first PF blocks ----
@@ -618,15 +572,10 @@ __global__ __launch_bounds__(NW * 64) void gemv_fused_kernel(const uint8_t* __re
     if (r0 + wv >= rend) return;  // wave-uniform; the wave had nothing to store
 
     // ---- reduce and store ----
-    constexpr int RP = (R > 2) ? 4 : R;  // reduction width: power of two >= R
-    float red[RP];
-#pragma unroll
-    for (int r = 0; r < RP; r++) red[r] = (r < R) ? acc[r] : 0.0f;
-    const float s = wave_reduce_rows<RP>(red, lane);
-    constexpr int LOG2R = (RP >= 4) ? 2 : (RP >= 2) ? 1 : 0;
-    constexpr int SPAN = 64 >> LOG2R;
-    if ((lane & (SPAN - 1)) == 0) {
-        const int row = r0 + wv + (lane >> (6 - LOG2R)) * NW;
+    const float s = wave_reduce_rows<R>(acc);
+    constexpr int SH = reduce_span_log2<R>();
+    if ((lane & ((1 << SH) - 1)) == 0) {
+        const int row = r0 + wv + (lane >> SH) * NW;
         if (row < rend) y[row] = s;
     }
 }
@@ -676,17 +625,22 @@ __global__ __launch_bounds__(NW * 64) void gemv_q4k_fused_kernel(const uint8_t* 
     load_prep_x<NW, PI>(x, nb, xv);
 
     u32x4 hdr[R][UPL], qa[R][UPL], qb[R][UPL];
-    // no control flow here (rows clamped): exactly 3 loads per (row, unit)
+    // no control flow here (empty slots load nothing through an out-of-range
+    // buffer offset): exactly 3 loads per (row, unit)
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(W, (uint32_t)n * row_bytes);
 #pragma unroll
     for (int r = 0; r < R; r++) {
-        const int row = min(r0 + wv + r * NW, rend - 1);
+        const int row = r0 + wv + r * NW;
 #pragma unroll
         for (int i = 0; i < UPL; i++) {
-            const int u = min(lane + 64 * i, nunits - 1);
-            const uint8_t* p = W + (uint32_t)row * row_bytes + (uint32_t)(u >> 2) * Q4_K_BYTES;
-            hdr[r][i] = *reinterpret_cast<const u32x4*>(p);
-            qa[r][i] = *reinterpret_cast<const u32x4*>(p + 16 + 32 * (u & 3));
-            qb[r][i] = *reinterpret_cast<const u32x4*>(p + 32 + 32 * (u & 3));
+            const int u = lane + 64 * i;
+            const uint32_t off = (row < rend && u < nunits)
+                                     ? (uint32_t)row * row_bytes + (uint32_t)(u >> 2) * Q4_K_BYTES
+                                     : RSRC_OOB;
+            const uint32_t q = off + 16 + 32 * (u & 3);
+            hdr[r][i] = buf_load_b128(rs, off);
+            qa[r][i] = buf_load_b128(rs, q);
+            qb[r][i] = buf_load_b128(rs, q + 16);
         }
     }
     wait_prep_x<R * UPL * 3>();  // header + two 16-byte nibble loads per unit
@@ -732,11 +686,10 @@ __global__ __launch_bounds__(NW * 64) void gemv_q4k_fused_kernel(const uint8_t* 
             }
         }
     }
-    const float s = wave_reduce_rows<R>(acc, lane);
-    constexpr int LOG2R = (R >= 4) ? 2 : (R >= 2) ? 1 : 0;
-    constexpr int SPAN = 64 >> LOG2R;
-    if ((lane & (SPAN - 1)) == 0) {
-        const int row = r0 + wv + (lane >> (6 - LOG2R)) * NW;
+    const float s = wave_reduce_rows<R>(acc);
+    constexpr int SH = reduce_span_log2<R>();
+    if ((lane & ((1 << SH) - 1)) == 0) {
+        const int row = r0 + wv + (lane >> SH) * NW;
         if (row < rend) y[row] = s;
     }
 }

@@ -61,4 +61,111 @@ __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel)
     return __builtin_amdgcn_perm(hi, lo, sel);
 }
 
+// ---- cross-lane reductions without an LDS round trip ----------------------
+// DPP lane patterns (a DPP row is 16 lanes).
+constexpr int DPP_QUAD_XOR1 = 0xB1;        // quad_perm [1,0,3,2]: lane i <- i^1
+constexpr int DPP_QUAD_XOR2 = 0x4E;        // quad_perm [2,3,0,1]: lane i <- i^2
+constexpr int DPP_ROW_HALF_MIRROR = 0x141; // lane i <- 7-i within each 8 lanes
+constexpr int DPP_ROW_MIRROR = 0x140;      // lane i <- 15-i within each 16 lanes
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i32(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return as_f32(dpp_i32<CTRL>(__builtin_bit_cast(int32_t, v)));
+}
+
+// Sum / max over each aligned group of 4 or 8 lanes, returned in every lane
+// of the group.  Each step pairs a lane with one in the other half of its
+// group, and both lanes of a pair compute the same (commutative) result, so
+// every lane of a group ends up with identical bits.
+__device__ __forceinline__ int sum4_i32(int v) {
+    v += dpp_i32<DPP_QUAD_XOR1>(v);
+    return v + dpp_i32<DPP_QUAD_XOR2>(v);
+}
+__device__ __forceinline__ float sum4_f32(float v) {
+    v += dpp_f32<DPP_QUAD_XOR1>(v);
+    return v + dpp_f32<DPP_QUAD_XOR2>(v);
+}
+__device__ __forceinline__ float max4_f32(float v) {
+    v = fmaxf(v, dpp_f32<DPP_QUAD_XOR1>(v));
+    return fmaxf(v, dpp_f32<DPP_QUAD_XOR2>(v));
+}
+__device__ __forceinline__ int sum8_i32(int v) {
+    v = sum4_i32(v);
+    return v + dpp_i32<DPP_ROW_HALF_MIRROR>(v);
+}
+__device__ __forceinline__ float sum8_f32(float v) {
+    v = sum4_f32(v);
+    return v + dpp_f32<DPP_ROW_HALF_MIRROR>(v);
+}
+__device__ __forceinline__ float max8_f32(float v) {
+    v = max4_f32(v);
+    return fmaxf(v, dpp_f32<DPP_ROW_HALF_MIRROR>(v));
+}
+
+// gfx950 v_permlane32_swap / v_permlane16_swap folds.
+// fold32(x, y): lanes 0-31 get x[l] + x[l+32], lanes 32-63 get y[l-32] + y[l].
+// fold16(x, y): lanes of the even 16-lane rows get x[l] + x[l+16], lanes of
+// the odd rows get y[l-16] + y[l].
+__device__ __forceinline__ float fold32(float x, float y) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x),
+                                                    __builtin_bit_cast(uint32_t, y), false, false);
+    const uint32_t lo = r[0], hi = r[1];  // by value: see as_f32
+    return __builtin_bit_cast(float, lo) + __builtin_bit_cast(float, hi);
+}
+__device__ __forceinline__ float fold16(float x, float y) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, x),
+                                                    __builtin_bit_cast(uint32_t, y), false, false);
+    const uint32_t lo = r[0], hi = r[1];  // by value: see as_f32
+    return __builtin_bit_cast(float, lo) + __builtin_bit_cast(float, hi);
+}
+
+// Row sums of a wave: v[r] holds lane partials of row r (R <= 4).  Returns,
+// in every lane, the 64-lane total of row (lane >> 4) for R = 3, 4, of row
+// (lane >> 5) for R = 2 and of row 0 for R = 1 (rows >= R read as zero).
+template <int R>
+__device__ __forceinline__ float wave_reduce_rows(const float (&v)[R]) {
+    static_assert(R >= 1 && R <= 4, "rows per wave");
+    float s;
+    if constexpr (R >= 3) {
+        const float a = fold32(v[0], v[2]);
+        const float b = fold32(v[1], R == 4 ? v[R == 4 ? 3 : 0] : 0.0f);
+        s = fold16(a, b);
+    } else if constexpr (R == 2) {
+        s = fold32(v[0], v[1]);
+        s = fold16(s, s);
+    } else {
+        s = fold32(v[0], v[0]);
+        s = fold16(s, s);
+    }
+    s += dpp_f32<DPP_QUAD_XOR1>(s);
+    s += dpp_f32<DPP_QUAD_XOR2>(s);
+    s += dpp_f32<DPP_ROW_HALF_MIRROR>(s);
+    return s + dpp_f32<DPP_ROW_MIRROR>(s);
+}
+// log2 of the lanes that share one row total after wave_reduce_rows<R>.
+template <int R>
+constexpr int reduce_span_log2() { return R >= 3 ? 4 : R == 2 ? 5 : 6; }
+
+// ---- buffer loads ---------------------------------------------------------
+// Raw buffer loads over [base, base + bytes): an offset at or beyond `bytes`
+// returns zero without touching memory, which gives branch-free loads for
+// lanes that have nothing to load (offset RSRC_OOB).  bytes < 2^31.
+constexpr uint32_t RSRC_OOB = 0x80000000u;
+constexpr uint32_t RSRC_MAX_BYTES = 0x7FFFFF00u;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    // 0x00020000: the gfx9-family descriptor word 3 (32-bit data format).
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                             0x00020000);
+}
+__device__ __forceinline__ u32x4 buf_load_b128(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(rs, (int)off, 0, 0);
+}
+__device__ __forceinline__ uint32_t buf_load_b32(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(rs, (int)off, 0, 0);
+}
+
 }  // namespace rdl

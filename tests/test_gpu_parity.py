@@ -82,8 +82,11 @@ def test_gemv_float_baseline_shapes(rq, orc, gpu, name, dtype, n, k, kind, seed)
     check_parity(y, want, exact_f64(orc, kind, x, w, 1, k, n))
 
 
+# (1, 6000, 256) and (2, 14336, 512) take the fused kernel's 2- and 4-row-per-wave
+# reductions on a 256-CU device (the baseline shapes take 1 and 3).
 @pytest.mark.parametrize("m,n,k", [(1, 1, 32), (1, 3, 64), (2, 17, 96), (3, 65, 4096 + 32),
-                                   (1, 129, 2048), (4, 7, 8192), (5, 300, 320)])
+                                   (1, 129, 2048), (4, 7, 8192), (5, 300, 320),
+                                   (1, 6000, 256), (2, 14336, 512)])
 @pytest.mark.parametrize("dtype,kind", [(2, "q4"), (8, "q8"), (3, "q4_1")])
 def test_gemv_float_ragged(rq, orc, gpu, m, n, k, dtype, kind):
     x = synth.activations(m, k, 7 + n)
@@ -92,7 +95,10 @@ def test_gemv_float_ragged(rq, orc, gpu, m, n, k, dtype, kind):
     check_parity(fn(x, w, m, k, n), orc.matmul(kind, x, w, m, k, n), exact_f64(orc, kind, x, w, m, k, n))
 
 
-@pytest.mark.parametrize("m,n,k", [(1, 1, 256), (2, 5, 512), (1, 33, 1280), (3, 8, 14336)])
+# (1, 10000, 1024) and (2, 9000, 4096) take the 3-rows-per-wave Q4_K kernel on a
+# 256-CU device; (1, 6000, 2048) the 2-row one.
+@pytest.mark.parametrize("m,n,k", [(1, 1, 256), (2, 5, 512), (1, 33, 1280), (3, 8, 14336),
+                                   (1, 10000, 1024), (2, 9000, 4096), (1, 6000, 2048)])
 def test_gemv_q4k_ragged(rq, orc, gpu, m, n, k):
     x = synth.activations(m, k, 3 + n)
     w = synth.q4_k_weights(n, k, 5 + k)
