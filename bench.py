@@ -166,11 +166,11 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4_0 weights, int8 dot4 -> i32, f32 accumulate",
+        "dtype": "q4_0 weights x int4-digit x (v_dot8_i32_i4 -> i32), f32 combine",
         "data": "synthetic (seeded BASELINE config 2 bytes)",
         "config": {
             "workload": "config2: Q4_0 GEMV y=Wx, W 11008x4096 GGUF Q4_0, x f32[4096], batch 1, "
-                        "float path (matmul_f32_q4); step = one fused prep+GEMV kernel",
+                        "float path (matmul_f32_q4, the Linear default); step = one fused prep+GEMV kernel",
             "weight_copies": args.copies,
             "weight_bytes_total": wbytes * args.copies,
             "algorithmic_bytes_per_step": abytes,

@@ -126,8 +126,9 @@ size_t rec_bytes(bool native, size_t m, size_t k) {
 // Activation rows up to which one fused launch (prep in LDS + GEMV) is used.
 constexpr size_t FUSED_MAX_M = 4;
 
-bool use_fused(WType t, size_t m, size_t k, const float* x_dev) {
-    return m <= FUSED_MAX_M && k > 0 && k <= rdl::fused_max_k(t) && ((uintptr_t)x_dev & 15) == 0;
+bool use_fused(WType t, size_t m, size_t n, size_t k, const float* x_dev) {
+    return m <= FUSED_MAX_M && k > 0 && k <= rdl::fused_max_k(t) && ((uintptr_t)x_dev & 15) == 0 &&
+           (uint64_t)n * (k / rdl::block_elems(t)) * rdl::block_bytes(t) <= rdl::FUSED_MAX_WEIGHT_BYTES;
 }
 
 // Prepare activations and run the product on `s`; xrec must hold rec_bytes()
@@ -140,7 +141,7 @@ rdl_status run_linear(WType t, bool native, const uint8_t* w_dev, size_t n, size
         HIP_TRY(rdl::launch_gemv(t, native, w_dev, n, k, xrec, m, y_dev, s));
         return RDL_OK;
     }
-    if (use_fused(t, m, k, x_dev)) {
+    if (use_fused(t, m, n, k, x_dev)) {
         HIP_TRY(rdl::launch_gemv_fused(t, native, w_dev, n, k, x_dev, m, y_dev, s));
         return RDL_OK;
     }
@@ -172,7 +173,7 @@ rdl_status host_matmul(WType t, bool native, const float* x, size_t x_len, const
     HIP_TRY(dx.alloc(m * k * sizeof(float)));
     HIP_TRY(dw.alloc(wb + 64));
     HIP_TRY(dy.alloc(m * n * sizeof(float)));
-    if (!use_fused(t, m, k, (const float*)dx.p)) HIP_TRY(dr.alloc(rec_bytes(native, m, k)));
+    if (!use_fused(t, m, n, k, (const float*)dx.p)) HIP_TRY(dr.alloc(rec_bytes(native, m, k)));
     HIP_TRY(hipMemcpy(dx.p, x, m * k * sizeof(float), hipMemcpyHostToDevice));
     HIP_TRY(hipMemcpy(dw.p, w, wb, hipMemcpyHostToDevice));
     st = run_linear(t, native, (const uint8_t*)dw.p, n, k, (const float*)dx.p, m, (float*)dy.p,
@@ -363,7 +364,7 @@ rdl_status rdl_linear_forward_dev(const rdl_weight* w, const float* x_dev, size_
     const bool native = mode == RDL_MODE_NATIVE && (w->type == WType::Q4_0 || w->type == WType::Q4_1);
     hipStream_t s = (hipStream_t)stream;
     void* rec = nullptr;
-    const size_t rb = use_fused(w->type, m, w->k, x_dev) ? 0 : rec_bytes(native, m, w->k);
+    const size_t rb = use_fused(w->type, m, w->n, w->k, x_dev) ? 0 : rec_bytes(native, m, w->k);
     if (rb) HIP_TRY(hipMallocAsync(&rec, rb, s));
     rdl_status st = run_linear(w->type, native, (const uint8_t*)w->dev, w->n, w->k, x_dev, m, y_dev,
                                rec, s);

@@ -476,10 +476,16 @@ __global__ __launch_bounds__(NW * 64) void gemv_fused_kernel(const uint8_t* __re
     constexpr int BYTES = Geo<WT>::BYTES, WORDS = Geo<WT>::WORDS;
     constexpr int LPB = (WORDS == 9) ? 3 : 2;    // load instructions per block
     constexpr int NB = R * CPL;                   // blocks per lane
-    constexpr int PF = (NB < 4) ? NB : 4;         // blocks in flight ahead of the compute
     // Q4_0 / Q4_1 float mode use int4-digit records (four threads per column),
     // everything else int8 records (eight threads per column)
     constexpr bool I4 = !NATIVE && (WT == (int)WType::Q4_0 || WT == (int)WType::Q4_1);
+    // PF blocks in flight ahead of the compute; only P0 <= PF of them are
+    // issued before the prep.  The prep waits for its x loads, which queue in
+    // the CU behind every weight load issued before them, so the longer prep
+    // of the int4 records wants fewer weight loads in front of it (measured on
+    // MI355X: P0 = 2, PF = 3 for int4 records, 4 / 4 otherwise).
+    constexpr int PF = (NB < (I4 ? 3 : 4)) ? NB : (I4 ? 3 : 4);
+    constexpr int P0 = (PF < (I4 ? 2 : 4)) ? PF : (I4 ? 2 : 4);
     constexpr int PI = I4 ? (CPL * 4 + NW - 1) / NW : (CPL * 8 + NW - 1) / NW;
     const int lane = threadIdx.x & 63;
     const int wv = threadIdx.x >> 6;
@@ -511,21 +517,23 @@ __global__ __launch_bounds__(NW * 64) void gemv_fused_kernel(const uint8_t* __re
         f32x4 xv[PI][2];
         load_prep_x4<NW, PI>(x, nb, xv);
 #pragma unroll
-        for (int b = 0; b < PF; b++) issue(b);
-        wait_prep_x<PF * LPB>();
+        for (int b = 0; b < P0; b++) issue(b);
+        wait_prep_x<P0 * LPB>();
         prep_float4_lds<NW, PI>(xv, nb, reinterpret_cast<int*>(lds4));
     } else {
         f32x4 xv[PI];
         load_prep_x<NW, PI>(x, nb, xv);
 #pragma unroll
-        for (int b = 0; b < PF; b++) issue(b);
-        wait_prep_x<PF * LPB>();
+        for (int b = 0; b < P0; b++) issue(b);
+        wait_prep_x<P0 * LPB>();
         if constexpr (NATIVE)
             prep_native_lds<NW, PI>(xv, nb, reinterpret_cast<int*>(lds4));
         else
             prep_float_lds<NW, PI>(xv, nb, reinterpret_cast<int*>(lds4));
     }
     __syncthreads();
+#pragma unroll
+    for (int b = P0; b < PF; b++) issue(b);
 
     // column records: kept in registers when a lane has at most two columns
     constexpr bool KEEP = (CPL <= 2);
@@ -808,9 +816,21 @@ hipError_t launch_gemv_fused(WType t, bool native, const uint8_t* w, size_t n, s
     const int nb = (int)(k / QK);
     const size_t lds = (size_t)(native ? 3 : 8) * 16 * (nb > 0 ? nb : 1);
     const int ni = (int)n;
-    const int nw = 16, wg_per_cu = 1;
+    if ((uint64_t)n * (k / block_elems(t)) * block_bytes(t) > FUSED_MAX_WEIGHT_BYTES)
+        return hipErrorInvalidValue;  // weight windows use 32-bit buffer offsets
+    // int4-record float GEMVs: 8-wave workgroups, two per CU (the prep runs on
+    // half as many lanes per workgroup but overlaps the other workgroup's
+    // stream); everything else one 16-wave workgroup per CU.
+    const bool i4 = !native && (t == WType::Q4_0 || t == WType::Q4_1);
+    const int nw = i4 ? 8 : 16, wg_per_cu = i4 ? 2 : 1;
     if (t == WType::Q4_K) {
-        launch_q4k_nw<16>(w, ni, (int)(k / QK_K), x, m, y, s, lds, wg_per_cu);
+        // up to 64 units per row (K <= 4096): rows spread over 8-wave
+        // workgroups, two per CU; longer rows: one 16-wave workgroup per CU
+        const int nsb = (int)(k / QK_K);
+        if (nsb * 4 <= 64)
+            launch_q4k_nw<8>(w, ni, nsb, x, m, y, s, lds, 2);
+        else
+            launch_q4k_nw<16>(w, ni, nsb, x, m, y, s, lds, 1);
         return hipGetLastError();
     }
     if (native) {

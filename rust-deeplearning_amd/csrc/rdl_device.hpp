@@ -155,7 +155,6 @@ constexpr int reduce_span_log2() { return R >= 3 ? 4 : R == 2 ? 5 : 6; }
 // returns zero without touching memory, which gives branch-free loads for
 // lanes that have nothing to load (offset RSRC_OOB).  bytes < 2^31.
 constexpr uint32_t RSRC_OOB = 0x80000000u;
-constexpr uint32_t RSRC_MAX_BYTES = 0x7FFFFF00u;
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
     // 0x00020000: the gfx9-family descriptor word 3 (32-bit data format).
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,

@@ -104,7 +104,9 @@ hipError_t launch_gemv(WType t, bool native, const uint8_t* w, size_t n, size_t 
                        const void* xrec, size_t m, float* y, hipStream_t s);
 
 // Single-launch GEMV with the activation preparation fused in (x f32 [m, k],
-// 16-byte aligned); valid for k <= fused_max_k(t).
+// 16-byte aligned); valid for k <= fused_max_k(t) and weights of at most
+// FUSED_MAX_WEIGHT_BYTES (its loads use 32-bit buffer offsets).
+constexpr uint64_t FUSED_MAX_WEIGHT_BYTES = 0x7FFFFF00u;
 size_t fused_max_k(WType t);
 hipError_t launch_gemv_fused(WType t, bool native, const uint8_t* w, size_t n, size_t k,
                              const float* x, size_t m, float* y, hipStream_t s);
