@@ -29,11 +29,26 @@ METRIC = "Q4_0/Q4_K GEMV achieved HBM GB/s (% peak); 7B Q4_0 decode tokens/s"
 PEAK_HBM_GBPS = 8000.0
 N_OUT, K_IN = 11008, 4096
 SEED = 0x5EED0002
+# the kernel the library launches for this workload (8-wave workgroups, 3 rows per wave)
+KERNEL_KEY = "gemv_fused_kernel<2, false, 3, 2, true, 8>|config2"
 
 
 def algorithmic_bytes(n, k):
-    """Weight blocks + x (f32) + y (f32), read/written once."""
+    """Weight blocks + x (f32) + y (f32), each read or written once."""
     return n * (k // 32) * 18 + 4 * k + 4 * n
+
+
+def measured_traffic(kernel_key):
+    """HBM bytes per launch of the timed kernel, from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE passes (scaled by a known-size copy); None when no
+    measurement for this kernel and workload is on file."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f).get(kernel_key)
+    except (OSError, ValueError):
+        return None
+    return None if rec is None else int(rec["traffic_bytes_per_launch"])
 
 
 def cpu_baseline(budget_s=10.0):
@@ -77,10 +92,14 @@ def main():
     ap.add_argument("--copies", type=int, default=24)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="first run 3 plain device copies of this many MiB (a known-size "
+                         "reference for HBM traffic counters)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py measures one GPU: every box in this build has a single MI355X; "
-              "multi-GPU runs are not part of this path (see DESIGN.md, sharding).", file=sys.stderr)
+        print("bench.py measures one GPU: the GEMV runs on a single MI355X and multi-GPU "
+              "runs are not part of this path (rows would shard across GPUs with an "
+              "all-gather of y).", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np
@@ -93,6 +112,14 @@ def main():
     torch.cuda.set_device(dev)
     stream = torch.cuda.current_stream()
     sh = stream.cuda_stream
+
+    if args.calib_copy_mib > 0:
+        src = torch.ones(args.calib_copy_mib << 18, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     wbytes = N_OUT * (K_IN // 32) * 18
     w_host = synth.q4_0_weights(N_OUT, K_IN, SEED)
@@ -179,14 +206,16 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "gemv_fused_kernel<Q4_0, float>",
+            "kernel": KERNEL_KEY.split("|")[0],
             "achieved": round(achieved, 2),
             "peak": PEAK_HBM_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBPS, 4),
             "kernel_avg_us": round(kern_avg_ms * 1e3, 3),
             "kernel_median_us": round(kern_ms[len(kern_ms) // 2] * 1e3, 3),
-            "traffic": None,
+            "traffic": measured_traffic(KERNEL_KEY),
+            "traffic_source": "profiles/gemv_q4_0_config2_pmc.md (FETCH_SIZE x2.0 + WRITE_SIZE, "
+                              "scaled by a 256 MiB copy)",
         },
     }
     if not args.no_cpu:
