@@ -28,6 +28,7 @@ struct rdl_weight {
     WType type;
     size_t n, k;
     bool owned;
+    bool gemm_ok;  // block scales fit the prefill GEMM's f16 operands
 };
 
 namespace {
@@ -131,20 +132,47 @@ bool use_fused(WType t, size_t m, size_t n, size_t k, const float* x_dev) {
            (uint64_t)n * (k / rdl::block_elems(t)) * rdl::block_bytes(t) <= rdl::FUSED_MAX_WEIGHT_BYTES;
 }
 
-// Prepare activations and run the product on `s`; xrec must hold rec_bytes()
-// unless use_fused() holds.
+// How a product runs: one fused GEMV launch (m <= 4), the matrix-core GEMM
+// (Q4_0 float mode, more rows), or activation records + the records GEMV.
+enum class Path { Fused, Gemm, Records };
+
+Path pick_path(WType t, bool native, size_t m, size_t n, size_t k, const float* x_dev, bool gemm_ok) {
+    if (use_fused(t, m, n, k, x_dev)) return Path::Fused;
+    if (!native && t == WType::Q4_0 && gemm_ok && k > 0 &&
+        (uint64_t)m * k * 2 <= rdl::FUSED_MAX_WEIGHT_BYTES &&
+        (uint64_t)n * (k / rdl::QK) * rdl::Q4_0_BYTES <= rdl::FUSED_MAX_WEIGHT_BYTES)
+        return Path::Gemm;
+    return Path::Records;
+}
+
+size_t scratch_bytes(Path p, bool native, size_t m, size_t k) {
+    switch (p) {
+        case Path::Fused: return 0;
+        case Path::Gemm: return rdl::gemm_scratch_bytes(m, k);
+        case Path::Records: return rec_bytes(native, m, k);
+    }
+    return 0;
+}
+
+// Run the product on `s`; `scratch` holds scratch_bytes(path) bytes.
 rdl_status run_linear(WType t, bool native, const uint8_t* w_dev, size_t n, size_t k,
-                      const float* x_dev, size_t m, float* y_dev, void* xrec, hipStream_t s) {
+                      const float* x_dev, size_t m, float* y_dev, void* scratch, hipStream_t s,
+                      Path path) {
     if (m == 0 || n == 0) return RDL_OK;
     // k == 0: no blocks; the GEMV then writes zeros (empty dot, as in the reference).
     if (k == 0) {
-        HIP_TRY(rdl::launch_gemv(t, native, w_dev, n, k, xrec, m, y_dev, s));
+        HIP_TRY(rdl::launch_gemv(t, native, w_dev, n, k, scratch, m, y_dev, s));
         return RDL_OK;
     }
-    if (use_fused(t, m, n, k, x_dev)) {
+    if (path == Path::Fused) {
         HIP_TRY(rdl::launch_gemv_fused(t, native, w_dev, n, k, x_dev, m, y_dev, s));
         return RDL_OK;
     }
+    if (path == Path::Gemm) {
+        HIP_TRY(rdl::launch_gemm_q4_0(w_dev, n, k, x_dev, m, y_dev, scratch, s));
+        return RDL_OK;
+    }
+    void* xrec = scratch;
     if (native)
         HIP_TRY(rdl::launch_prep_native(x_dev, m, k, (NativeRec*)xrec, nullptr, nullptr, s));
     else
@@ -173,11 +201,16 @@ rdl_status host_matmul(WType t, bool native, const float* x, size_t x_len, const
     HIP_TRY(dx.alloc(m * k * sizeof(float)));
     HIP_TRY(dw.alloc(wb + 64));
     HIP_TRY(dy.alloc(m * n * sizeof(float)));
-    if (!use_fused(t, m, n, k, (const float*)dx.p)) HIP_TRY(dr.alloc(rec_bytes(native, m, k)));
     HIP_TRY(hipMemcpy(dx.p, x, m * k * sizeof(float), hipMemcpyHostToDevice));
     HIP_TRY(hipMemcpy(dw.p, w, wb, hipMemcpyHostToDevice));
+    bool gemm_ok = false;
+    if (!native && t == WType::Q4_0 && m > FUSED_MAX_M)
+        HIP_TRY(rdl::gemm_scales_ok(t, (const uint8_t*)dw.p, n, k, &gemm_ok));
+    const Path path = pick_path(t, native, m, n, k, (const float*)dx.p, gemm_ok);
+    const size_t sb = scratch_bytes(path, native, m, k);
+    if (sb) HIP_TRY(dr.alloc(sb));
     st = run_linear(t, native, (const uint8_t*)dw.p, n, k, (const float*)dx.p, m, (float*)dy.p,
-                    dr.p, nullptr);
+                    dr.p, nullptr, path);
     if (st != RDL_OK) return st;
     HIP_TRY(hipMemcpy(y, dy.p, m * n * sizeof(float), hipMemcpyDeviceToHost));
     return ok();
@@ -321,7 +354,15 @@ rdl_status rdl_weight_upload(const uint8_t* bytes, size_t len, int32_t dtype,
             return fail(RDL_ERR_HIP, "hipMemcpy failed: %s", hipGetErrorString(e));
         }
     }
-    *out = new rdl_weight{d, need, t, out_features, in_features, true};
+    bool gemm_ok = false;
+    {
+        const hipError_t e = rdl::gemm_scales_ok(t, (const uint8_t*)d, out_features, in_features, &gemm_ok);
+        if (e != hipSuccess) {
+            (void)hipFree(d);
+            return fail(RDL_ERR_HIP, "weight scale scan failed: %s", hipGetErrorString(e));
+        }
+    }
+    *out = new rdl_weight{d, need, t, out_features, in_features, true, gemm_ok};
     return ok();
 }
 
@@ -342,7 +383,12 @@ rdl_status rdl_weight_wrap_device(const void* dev_bytes, size_t len, int32_t dty
         return fail(RDL_ERR_INVALID_DATA, "Q4_K device bytes must be 16-byte aligned");
     if ((uintptr_t)dev_bytes & 3)
         return fail(RDL_ERR_INVALID_DATA, "device bytes must be 4-byte aligned");
-    *out = new rdl_weight{const_cast<void*>(dev_bytes), need, t, out_features, in_features, false};
+    rdl_status st = require_device();
+    if (st != RDL_OK) return st;
+    bool gemm_ok = false;
+    HIP_TRY(rdl::gemm_scales_ok(t, (const uint8_t*)dev_bytes, out_features, in_features, &gemm_ok));
+    *out = new rdl_weight{const_cast<void*>(dev_bytes), need, t, out_features, in_features, false,
+                          gemm_ok};
     return ok();
 }
 
@@ -364,10 +410,11 @@ rdl_status rdl_linear_forward_dev(const rdl_weight* w, const float* x_dev, size_
     const bool native = mode == RDL_MODE_NATIVE && (w->type == WType::Q4_0 || w->type == WType::Q4_1);
     hipStream_t s = (hipStream_t)stream;
     void* rec = nullptr;
-    const size_t rb = use_fused(w->type, m, w->n, w->k, x_dev) ? 0 : rec_bytes(native, m, w->k);
+    const Path path = pick_path(w->type, native, m, w->n, w->k, x_dev, w->gemm_ok);
+    const size_t rb = scratch_bytes(path, native, m, w->k);
     if (rb) HIP_TRY(hipMallocAsync(&rec, rb, s));
     rdl_status st = run_linear(w->type, native, (const uint8_t*)w->dev, w->n, w->k, x_dev, m, y_dev,
-                               rec, s);
+                               rec, s, path);
     if (rec) {
         hipError_t e = hipFreeAsync(rec, s);
         if (st == RDL_OK && e != hipSuccess)

@@ -704,7 +704,9 @@ __global__ __launch_bounds__(NW * 64) void gemv_q4k_fused_kernel(const uint8_t* 
 
 int g_num_cus = 0;
 
-int num_cus() {
+}  // namespace
+
+int device_cu_count() {
     if (g_num_cus == 0) {
         int dev = 0, cus = 0;
         if (hipGetDevice(&dev) == hipSuccess &&
@@ -716,6 +718,10 @@ int num_cus() {
     }
     return g_num_cus;
 }
+
+namespace {
+
+int num_cus() { return device_cu_count(); }
 
 // Columns per lane (CPL) x rows per wave (R) <= 8 keeps the block windows
 // within the VGPR budget.

@@ -111,6 +111,19 @@ size_t fused_max_k(WType t);
 hipError_t launch_gemv_fused(WType t, bool native, const uint8_t* w, size_t n, size_t k,
                              const float* x, size_t m, float* y, hipStream_t s);
 
+// Compute units of the current device (queried once; 256 on MI355X).
+int device_cu_count();
+
+// Prefill GEMM for Q4_0 weights in float mode (matrix cores): y[m, n] =
+// x[m, k] . W^T.  `scratch` holds gemm_scratch_bytes(m, k) bytes (the f16
+// x split); W must have |d| <= 4096 in every block scale.
+size_t gemm_scratch_bytes(size_t m, size_t k);
+// Whether every block scale of W fits the GEMM's f16 operands (synchronous
+// scan on the null stream; false for types without a GEMM kernel).
+hipError_t gemm_scales_ok(WType t, const uint8_t* w, size_t n, size_t k, bool* ok);
+hipError_t launch_gemm_q4_0(const uint8_t* w, size_t n, size_t k, const float* x, size_t m, float* y,
+                            void* scratch, hipStream_t s);
+
 // int32 block partials of the Q4_0 x Q8_0 path for one activation row.
 hipError_t launch_q4_0_block_dots(const uint8_t* w, size_t n, size_t k, const NativeRec* rec,
                                   int32_t* partials, hipStream_t s);

@@ -1,0 +1,89 @@
+"""GPU parity of the Q4_0 prefill GEMM (matrix cores): the many-row case of
+matmul_f32_q4 (quantize.rs:265-320) through the C ABI, against the CPU
+restatement and the exact (f64) value of the reference computation."""
+import numpy as np
+import pytest
+
+from parity import assert_close, check_parity, exact_f64
+from rdlquant import synth
+
+pytestmark = pytest.mark.gpu
+
+THREADS = 16
+
+
+def run(rq, orc, m, n, k, seed, rows=None):
+    x = synth.activations(m, k, seed)
+    w = synth.q4_0_weights(n, k, seed + 1)
+    got = rq.matmul_f32_q4(x, w, m, k, n).reshape(m, n)
+    if rows is not None:
+        x, got, m = x[rows], got[rows], len(rows)
+    want = orc.matmul("q4", x, w, m, k, n, threads=THREADS)
+    check_parity(got.reshape(-1), want, exact_f64(orc, "q4", x, w, m, k, n))
+
+
+# W 4096x4096 Q4_0, M in {16, 64, 512, 2048}
+@pytest.mark.parametrize("m", [16, 64, 512])
+def test_config4_prefill(rq, orc, gpu, m):
+    run(rq, orc, m, 4096, 4096, 0x5EED0004 + m)
+
+
+def test_config4_prefill_2048_sampled_rows(rq, orc, gpu):
+    # each output row depends only on its x row: check 48 spread rows, all tiles
+    rows = np.unique(np.linspace(0, 2047, 48).astype(int))
+    run(rq, orc, 2048, 4096, 4096, 0x5EED0804, rows=rows)
+
+
+# ragged: partial tiles in both dimensions, odd block counts (block windows
+# straddling the matrix end), chunk counts not dividing the blocks
+@pytest.mark.parametrize("m,n,k", [(5, 1, 32), (5, 17, 96), (17, 100, 4128), (33, 130, 1056),
+                                   (100, 64, 2080), (300, 257, 544), (1030, 33, 160)])
+def test_gemm_ragged(rq, orc, gpu, m, n, k):
+    run(rq, orc, m, n, k, 31 + m + n + k)
+
+
+def test_gemm_matches_gemv_rows(rq, gpu):
+    # the same rows through the one-row GEMV and the GEMM agree within the bar
+    m, n, k = 24, 320, 2048
+    x = synth.activations(m, k, 41)
+    w = synth.q4_0_weights(n, k, 42)
+    gemm = rq.matmul_f32_q4(x, w, m, k, n).reshape(m, n)
+    for r in (0, 7, 23):
+        gemv = rq.matmul_f32_q4(x[r:r + 1], w, 1, k, n)
+        assert_close(gemm[r], gemv, rtol=2e-3, atol=2e-4)
+
+
+def test_large_scales_take_the_exact_path(rq, orc, gpu):
+    # |d| > 4096 does not fit the GEMM's f16 operands; the library must route
+    # such a weight elsewhere and stay within the bar
+    m, n, k = 8, 40, 256
+    w = synth.q4_0_weights(n, k, 51)
+    blocks = w.reshape(n, -1, 18)
+    blocks[3, 2, 0:2] = np.frombuffer(np.float16(20000.0).tobytes(), np.uint8)
+    x = synth.activations(m, k, 52)
+    check_parity(rq.matmul_f32_q4(x, w, m, k, n), orc.matmul("q4", x, w, m, k, n),
+                 exact_f64(orc, "q4", x, w, m, k, n))
+
+
+def test_wide_dynamic_range_rows(rq, orc, gpu):
+    # rows scaled by 2^-40 .. 2^+40: the per-row power-of-two scaling keeps each
+    # row's relative accuracy
+    m, n, k = 12, 48, 512
+    x = synth.activations(m, k, 61)
+    x *= (2.0 ** np.linspace(-40, 40, m)).astype(np.float32)[:, None]
+    w = synth.q4_0_weights(n, k, 62)
+    got = rq.matmul_f32_q4(x, w, m, k, n).reshape(m, n)
+    exact = exact_f64(orc, "q4", x, w, m, k, n).reshape(m, n)
+    for r in range(m):
+        scale = np.abs(exact[r]).max()
+        assert_close(got[r] / scale, exact[r] / scale)
+
+
+def test_nan_row_stays_in_its_row(rq, gpu):
+    m, n, k = 20, 64, 256
+    x = synth.activations(m, k, 71)
+    w = synth.q4_0_weights(n, k, 72)
+    x[6, 100] = np.nan
+    y = rq.matmul_f32_q4(x, w, m, k, n).reshape(m, n)
+    assert np.all(np.isnan(y[6]))
+    assert np.all(np.isfinite(np.delete(y, 6, axis=0)))

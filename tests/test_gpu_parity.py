@@ -10,38 +10,7 @@ from rdlquant import synth
 
 pytestmark = pytest.mark.gpu
 
-RTOL, ATOL = 1e-3, 1e-4
-
-
-def assert_close(got, want, rtol=RTOL, atol=ATOL, slack=0.0):
-    got = np.asarray(got, np.float64).reshape(-1)
-    want = np.asarray(want, np.float64).reshape(-1)
-    err = np.abs(got - want)
-    tol = atol + rtol * np.abs(want) + slack
-    bad = np.nonzero(~(err <= tol))[0]
-    assert bad.size == 0, (
-        f"{bad.size}/{want.size} outside tol; worst idx {bad[np.argmax(err[bad])]} "
-        f"got {got[bad[0]]} want {want[bad[0]]}")
-
-
-DEQ = {"q8": "q8_0", "q4": "q4_0", "q4_1": "q4_1", "q4k": "q4k"}
-
-
-def exact_f64(orc, kind, x, w, m, k, n):
-    """The reference's float-path product evaluated exactly (f64) over its own
-    f32 dequantized weights (Tensor::to_f32 / dequantize_q4k)."""
-    wd = orc.to_f32(DEQ[kind], w, n * k).reshape(n, k).astype(np.float64)
-    return (np.asarray(x, np.float64).reshape(m, k) @ wd.T).reshape(-1)
-
-
-def check_parity(got, want, exact, rtol=RTOL, atol=ATOL):
-    """got: GPU; want: the reference CPU path (oracle, f32); exact: f64 value of
-    the same computation.  (1) the GPU result is within the bar of the exact
-    value; (2) it agrees with the CPU path within the bar plus the CPU path's
-    own f32 rounding error |want - exact| (the reference's summation order --
-    faer for Q4_K -- is not pinned, so only that much of its noise is defined)."""
-    assert_close(got, exact, rtol, atol)
-    assert_close(got, want, rtol, atol, slack=np.abs(np.asarray(want, np.float64) - exact))
+from parity import ATOL, RTOL, assert_close, check_parity, exact_f64  # noqa: E402,F401
 
 
 # ---- quantize_row_q8_0: byte-exact --------------------------------------------------
