@@ -108,13 +108,13 @@ __device__ __forceinline__ void a_fragment(uint32_t n0, uint32_t n1, uint32_t db
     al = half8_t{l0[0], l0[1], l1[0], l1[1], l2[0], l2[1], l3[0], l3[1]};
 }
 
-template <int FJ, int FI, int WJ, int WI, int KS>
+template <int FJ, int FI, int WJ, int WI, int KS, int KB>
 struct GemmCfg {
     static constexpr int NW = WJ * WI * KS;
     static constexpr int NT = NW * 64;
     static constexpr int TJ = WJ * FJ * 16;
     static constexpr int TI = WI * FI * 16;
-    static constexpr int CB = 2 * KS;                       // blocks per chunk
+    static constexpr int CB = KB * KS;                      // blocks per chunk
     static constexpr int WN_BYTES = TJ * Lds<CB>::WN_STRIDE;
     static constexpr int WD_BYTES = TJ * CB * 2;
     static constexpr int X_BYTES = TI * Lds<CB>::X_STRIDE;  // one of hi / lo
@@ -123,22 +123,43 @@ struct GemmCfg {
     static constexpr int LDS = 2 * STAGE_AL;
     static constexpr int WBLK = (TJ * CB + NT - 1) / NT;          // weight blocks per thread
     static constexpr int XU = (TI * CB * 4 + NT - 1) / NT;         // 16-byte x units per thread (each of hi, lo)
+    static constexpr int RED = (KS > 1) ? (KS - 1) * WJ * WI * FJ * FI * 64 * 16 : 0;
 };
 
-template <int FJ, int FI, int WJ, int WI, int KS>
+// One chunk's global loads, held in registers until they are written to LDS.
+template <int WBLK, int XU>
+struct Staged {
+    uint32_t w[WBLK][5];
+    u32x4 xh[XU], xl[XU];
+};
+
+// Tile order: workgroups are dealt to the 8 XCDs round-robin (linear id % 8);
+// give each XCD a contiguous run of tiles in row-major tile order, so the
+// workgroups that share x rows share one L2.
+__device__ __forceinline__ void tile_of(int nj, int ni, int& bx, int& by) {
+    const int total = nj * ni, L = blockIdx.x;
+    const int t = (total % 8 == 0) ? (L % 8) * (total / 8) + L / 8 : L;
+    bx = t % nj;
+    by = t / nj;
+}
+
+template <int FJ, int FI, int WJ, int WI, int KS, int KB>
 __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_f16_kernel(
     const uint8_t* __restrict__ W, int n, int nb, const _Float16* __restrict__ XH,
     const _Float16* __restrict__ XL, const int* __restrict__ XE, int m, float* __restrict__ Y) {
-    using C = GemmCfg<FJ, FI, WJ, WI, KS>;
+    using C = GemmCfg<FJ, FI, WJ, WI, KS, KB>;
     constexpr int CB = C::CB;
+    using S = Staged<C::WBLK, C::XU>;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int ks = wave % KS;
     const int wi = (wave / KS) % WI;
     const int wj = wave / (KS * WI);
-    const int j0 = blockIdx.x * C::TJ;
-    const int i0 = blockIdx.y * C::TI;
+    int bx, by;
+    tile_of((n + C::TJ - 1) / C::TJ, (m + C::TI - 1) / C::TI, bx, by);
+    const int j0 = bx * C::TJ;
+    const int i0 = by * C::TI;
     const int k = nb * 32;
     const uint32_t row_bytes = (uint32_t)nb * 18u;
     const uint32_t wbytes = (uint32_t)n * row_bytes;
@@ -147,10 +168,7 @@ __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_f16_kernel(
     const __amdgpu_buffer_rsrc_t xlrs = make_rsrc(XL, (uint32_t)m * (uint32_t)k * 2u);
     const int nchunks = (nb + CB - 1) / CB;
 
-    // ---- staging registers ----
-    uint32_t wwin[C::WBLK][5];
-    u32x4 xh[C::XU], xl[C::XU];
-    auto load_chunk = [&](int c) {
+    auto load_chunk = [&](int c, S& r) {
 #pragma unroll
         for (int u = 0; u < C::WBLK; u++) {
             const int idx = threadIdx.x + u * C::NT;
@@ -161,10 +179,10 @@ __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_f16_kernel(
                                      : RSRC_OOB;
             const uint32_t base = off & ~3u;
             const u32x4 v = buf_load_b128(wrs, base);
-            wwin[u][0] = v.x; wwin[u][1] = v.y; wwin[u][2] = v.z; wwin[u][3] = v.w;
+            r.w[u][0] = v.x; r.w[u][1] = v.y; r.w[u][2] = v.z; r.w[u][3] = v.w;
             // the last block of an odd-sized matrix ends 2 bytes before its window
             const bool over = base < wbytes && base + 20u > wbytes;
-            wwin[u][4] = buf_load_b32(wrs, over ? wbytes - 4u : base + 16u) >> (over ? 16 : 0);
+            r.w[u][4] = buf_load_b32(wrs, over ? wbytes - 4u : base + 16u) >> (over ? 16 : 0);
         }
 #pragma unroll
         for (int u = 0; u < C::XU; u++) {
@@ -174,11 +192,11 @@ __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_f16_kernel(
             const uint32_t off = (idx < C::TI * CB * 4 && i < m && kk < k)
                                      ? ((uint32_t)i * (uint32_t)k + (uint32_t)kk) * 2u
                                      : RSRC_OOB;
-            xh[u] = buf_load_b128(xhrs, off);
-            xl[u] = buf_load_b128(xlrs, off);
+            r.xh[u] = buf_load_b128(xhrs, off);
+            r.xl[u] = buf_load_b128(xlrs, off);
         }
     };
-    auto store_chunk = [&](int c, int buf) {
+    auto store_chunk = [&](int c, int buf, const S& r) {
         uint8_t* st = lds + buf * C::STAGE_AL;
         uint8_t* wn = st;
         uint16_t* wd = reinterpret_cast<uint16_t*>(st + C::WN_BYTES);
@@ -193,13 +211,13 @@ __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_f16_kernel(
                 // block g = j * nb + b starts at 18 g: 2 bytes past a dword when g is odd
                 const bool odd = (((uint32_t)j * (uint32_t)nb + (uint32_t)b) & 1u) != 0;
                 const uint32_t sel = odd ? 0x07060504u : 0x05040302u;
-                const uint32_t dbits = odd ? (wwin[u][0] >> 16) : (wwin[u][0] & 0xFFFFu);
+                const uint32_t dbits = odd ? (r.w[u][0] >> 16) : (r.w[u][0] & 0xFFFFu);
                 // rows are 8-byte aligned (padded stride): two 8-byte stores
                 uint2 lo, hi;
-                lo.x = perm(wwin[u][1], wwin[u][0], sel);
-                lo.y = perm(wwin[u][2], wwin[u][1], sel);
-                hi.x = perm(wwin[u][3], wwin[u][2], sel);
-                hi.y = perm(wwin[u][4], wwin[u][3], sel);
+                lo.x = perm(r.w[u][1], r.w[u][0], sel);
+                lo.y = perm(r.w[u][2], r.w[u][1], sel);
+                hi.x = perm(r.w[u][3], r.w[u][2], sel);
+                hi.y = perm(r.w[u][4], r.w[u][3], sel);
                 uint2* dst = reinterpret_cast<uint2*>(wn + jl * Lds<CB>::WN_STRIDE + bl * 16);
                 dst[0] = lo;
                 dst[1] = hi;
@@ -211,8 +229,8 @@ __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_f16_kernel(
             const int idx = threadIdx.x + u * C::NT;
             if (idx < C::TI * CB * 4) {
                 const int il = idx / (CB * 4), q = idx % (CB * 4);
-                *reinterpret_cast<u32x4*>(xhs + il * Lds<CB>::X_STRIDE + q * 16) = xh[u];
-                *reinterpret_cast<u32x4*>(xls + il * Lds<CB>::X_STRIDE + q * 16) = xl[u];
+                *reinterpret_cast<u32x4*>(xhs + il * Lds<CB>::X_STRIDE + q * 16) = r.xh[u];
+                *reinterpret_cast<u32x4*>(xls + il * Lds<CB>::X_STRIDE + q * 16) = r.xl[u];
             }
         }
     };
@@ -223,22 +241,16 @@ __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_f16_kernel(
 #pragma unroll
         for (int b = 0; b < FI; b++) acc[a][b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    load_chunk(0);
-    store_chunk(0, 0);
-    __syncthreads();
-
     const int g = lane >> 4, r16 = lane & 15;
-    for (int c = 0; c < nchunks; c++) {
-        const int buf = c & 1;
-        if (c + 1 < nchunks) load_chunk(c + 1);
+    auto compute_chunk = [&](int buf) {
         const uint8_t* st = lds + buf * C::STAGE_AL;
         const uint8_t* wn = st;
         const uint16_t* wd = reinterpret_cast<const uint16_t*>(st + C::WN_BYTES);
         const uint8_t* xhs = st + C::WN_BYTES + C::WD_BYTES;
         const uint8_t* xls = xhs + C::X_BYTES;
 #pragma unroll
-        for (int kb = 0; kb < 2; kb++) {
-            const int bl = ks * 2 + kb;  // this wave's block within the chunk
+        for (int kb = 0; kb < KB; kb++) {
+            const int bl = ks * KB + kb;  // this wave's block within the chunk
             half8_t ah[FJ], al[FJ];
 #pragma unroll
             for (int a = 0; a < FJ; a++) {
@@ -263,7 +275,24 @@ __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_f16_kernel(
                 }
             }
         }
-        if (c + 1 < nchunks) store_chunk(c + 1, buf ^ 1);
+    };
+
+    // Loads run two chunks ahead of the compute: register set P holds chunk
+    // c + 2 while LDS buffer 1 - P receives chunk c + 1.
+    S r0, r1;
+    load_chunk(0, r0);
+    if (nchunks > 1) load_chunk(1, r1);
+    store_chunk(0, 0, r0);
+    __syncthreads();
+    for (int c = 0; c < nchunks; c += 2) {
+        if (c + 2 < nchunks) load_chunk(c + 2, r0);
+        compute_chunk(0);
+        if (c + 1 < nchunks) store_chunk(c + 1, 1, r1);
+        __syncthreads();
+        if (c + 1 >= nchunks) break;
+        if (c + 3 < nchunks) load_chunk(c + 3, r1);
+        compute_chunk(1);
+        if (c + 2 < nchunks) store_chunk(c + 2, 0, r0);
         __syncthreads();
     }
 
@@ -314,19 +343,20 @@ __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_f16_kernel(
     }
 }
 
-template <int FJ, int FI, int WJ, int WI, int KS>
+template <int FJ, int FI, int WJ, int WI, int KS, int KB>
 hipError_t launch_cfg(const uint8_t* w, int n, int nb, const _Float16* xh, const _Float16* xl,
                       const int* xe, int m, float* y, hipStream_t s) {
-    using C = GemmCfg<FJ, FI, WJ, WI, KS>;
-    auto kern = gemm_q4_0_f16_kernel<FJ, FI, WJ, WI, KS>;
-    static_assert(C::LDS >= (KS > 1 ? (KS - 1) * WJ * WI * FJ * FI * 64 * 16 : 0), "K-split LDS");
+    using C = GemmCfg<FJ, FI, WJ, WI, KS, KB>;
+    auto kern = gemm_q4_0_f16_kernel<FJ, FI, WJ, WI, KS, KB>;
+    static_assert(C::LDS >= C::RED, "K-split sums fit the staging LDS");
+    static_assert(C::LDS <= 160 * 1024, "LDS per workgroup");
     if (C::LDS > 65536) {
         const hipError_t e = hipFuncSetAttribute((const void*)kern,
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
         if (e != hipSuccess) return e;
     }
-    const dim3 grid((unsigned)((n + C::TJ - 1) / C::TJ), (unsigned)((m + C::TI - 1) / C::TI));
-    launch_kernel(kern, grid, dim3(C::NT), (size_t)C::LDS, s, w, n, nb, xh, xl, xe, m, y);
+    const unsigned tiles = (unsigned)((n + C::TJ - 1) / C::TJ) * (unsigned)((m + C::TI - 1) / C::TI);
+    launch_kernel(kern, dim3(tiles), dim3(C::NT), (size_t)C::LDS, s, w, n, nb, xh, xl, xe, m, y);
     return hipGetLastError();
 }
 
@@ -386,12 +416,12 @@ hipError_t launch_gemm_q4_0(const uint8_t* w, size_t n, size_t k, const float* x
     const int cus = device_cu_count();
     // Tile choice: enough workgroups for the CUs, then the largest tile
     // (fewest re-reads of x and W from L2).
-    if (m >= 1024) return launch_cfg<4, 4, 2, 2, 1>(w, ni, nb, xh, xl, xe, mi, y, s);
-    if (m >= 256) return launch_cfg<4, 2, 2, 2, 1>(w, ni, nb, xh, xl, xe, mi, y, s);
+    if (m >= 1024) return launch_cfg<4, 4, 2, 2, 1, 2>(w, ni, nb, xh, xl, xe, mi, y, s);
+    if (m >= 256) return launch_cfg<4, 2, 2, 2, 1, 4>(w, ni, nb, xh, xl, xe, mi, y, s);
     if (m >= 48 && (size_t)((n + 31) / 32) * ((m + 63) / 64) >= (size_t)cus)
-        return launch_cfg<2, 4, 1, 1, 4>(w, ni, nb, xh, xl, xe, mi, y, s);
-    if (m > 16) return launch_cfg<1, 2, 1, 1, 4>(w, ni, nb, xh, xl, xe, mi, y, s);
-    return launch_cfg<1, 1, 1, 1, 4>(w, ni, nb, xh, xl, xe, mi, y, s);
+        return launch_cfg<2, 4, 1, 1, 4, 2>(w, ni, nb, xh, xl, xe, mi, y, s);
+    if (m > 16) return launch_cfg<1, 2, 1, 1, 4, 2>(w, ni, nb, xh, xl, xe, mi, y, s);
+    return launch_cfg<1, 1, 1, 1, 4, 8>(w, ni, nb, xh, xl, xe, mi, y, s);
 }
 
 }  // namespace rdl
