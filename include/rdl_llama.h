@@ -1,0 +1,112 @@
+/* rdl_llama.h -- batch-1 Llama-style decoder on one MI355X, built on the
+ * quantized Linear path of rdl_quant.h (librdlquant.so).
+ *
+ * It replaces, for Q4_0 GGUF models with RMSNorm, RoPE, grouped-query
+ * attention and SwiGLU, the rustml decode loop:
+ *   LlmModel::forward_with_cache_pass   rustml/nlp/main/src/core/model.rs:890-937
+ *   TransformerBlock::forward_with_cache rustml/nn/main/src/core/transformer_block.rs:297-356
+ *   MultiHeadAttention::forward_with_cache rustml/nn/main/src/core/attention.rs:353-449
+ *   FeedForward::forward (SwiGLU)       rustml/nn/main/src/core/feed_forward.rs:138-150
+ *   RoPEFreqs::new / apply              rustml/nn/main/src/core/rope.rs:93-200
+ *   KVCache                             rustml/nn/main/src/core/kv_cache.rs:10-114
+ *   Generator::prefill / decode_step    rustml/nlp/main/src/core/generator.rs:212-240
+ *   sampling::argmax                    rustml/nlp/main/src/core/sampling.rs:8-18
+ * Activations, the KV cache and the sampled tokens stay on the device; a
+ * greedy decode step is one replay of a captured HIP graph.
+ *
+ * Divergences from the reference, by design: the KV cache may be held in
+ * f16 (kv_f16 = 1; the reference keeps f32), and the last row's logits are
+ * the only ones computed (the reference computes every row and keeps the
+ * last). */
+#ifndef RDL_LLAMA_H
+#define RDL_LLAMA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "rdl_quant.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ModelConfig fields used by the Llama path (rustml/nlp/main/src/api/types.rs:186). */
+typedef struct rdl_llama_config {
+    int32_t dim;         /* hidden size */
+    int32_t n_layers;
+    int32_t n_heads;     /* query heads */
+    int32_t n_kv_heads;  /* key/value heads (n_heads % n_kv_heads == 0) */
+    int32_t head_dim;    /* dim == n_heads * head_dim; even */
+    int32_t ffn_dim;     /* SwiGLU hidden size */
+    int32_t vocab;
+    int32_t max_seq;     /* KV cache capacity (max_seq_len) */
+    float norm_eps;
+    float rope_theta;
+    int32_t kv_f16;      /* 1: f16 KV cache, 0: f32 (the reference's) */
+    int32_t max_batch;   /* most rows one forward call takes (prefill chunk) */
+} rdl_llama_config;
+
+typedef struct rdl_llama rdl_llama;
+
+/* Weight slots.  Q4_0 GGUF bytes for the matrices (row-major [out, in]
+ * blocks, as Linear::from_weights receives them) and the embedding; f32 for
+ * the norm weights.  `layer` is ignored for the model-level slots. */
+enum {
+    RDL_LLAMA_TOKEN_EMBEDDING = 0, /* [vocab, dim] Q4_0 (dequantized per row like Tensor::to_f32) */
+    RDL_LLAMA_ATTN_NORM = 1,       /* [dim] f32 */
+    RDL_LLAMA_WQ = 2,              /* [n_heads*head_dim, dim] Q4_0 */
+    RDL_LLAMA_WK = 3,              /* [n_kv_heads*head_dim, dim] Q4_0 */
+    RDL_LLAMA_WV = 4,              /* [n_kv_heads*head_dim, dim] Q4_0 */
+    RDL_LLAMA_WO = 5,              /* [dim, n_heads*head_dim] Q4_0 */
+    RDL_LLAMA_FFN_NORM = 6,        /* [dim] f32 */
+    RDL_LLAMA_W_GATE = 7,          /* [ffn_dim, dim] Q4_0 */
+    RDL_LLAMA_W_UP = 8,            /* [ffn_dim, dim] Q4_0 */
+    RDL_LLAMA_W_DOWN = 9,          /* [dim, ffn_dim] Q4_0 */
+    RDL_LLAMA_FINAL_NORM = 10,     /* [dim] f32 */
+    RDL_LLAMA_OUTPUT = 11          /* [vocab, dim] Q4_0 */
+};
+
+/* Allocates weights, KV cache and activations on the current device. */
+rdl_status rdl_llama_create(const rdl_llama_config* cfg, rdl_llama** out);
+rdl_status rdl_llama_free(rdl_llama* model);
+
+/* Copies one weight from host memory (len must equal the slot's size). */
+rdl_status rdl_llama_set_weight(rdl_llama* model, int32_t slot, int32_t layer, const void* bytes,
+                                size_t len);
+
+/* Seeded synthetic weights on the device, all slots: Q4_0 blocks with
+ * nibbles uniform in [0, 15] and d = f16(|N(0, 0.02)| / 8), norm weights 1.0. */
+rdl_status rdl_llama_init_random(rdl_llama* model, uint64_t seed);
+
+/* Empties the KV cache (KVCache::new state, current_len = 0). */
+rdl_status rdl_llama_reset(rdl_llama* model);
+
+/* Number of cached positions (KVCache::current_len). */
+rdl_status rdl_llama_position(const rdl_llama* model, size_t* out);
+
+/* forward_with_cache_pass over n tokens followed by cache.advance(n): the
+ * logits of the last row, copied to host memory (vocab floats).  Token ids
+ * must be < vocab; n <= max_batch; position + n <= max_seq.  Synchronous. */
+rdl_status rdl_llama_forward(rdl_llama* model, const int32_t* tokens, size_t n, float* logits,
+                             size_t logits_len);
+
+/* Greedy generation (Generator::generate with argmax sampling): prefill of
+ * the prompt (in chunks of max_batch), then n_gen - 1 decode steps, each one
+ * replay of a captured graph; out_tokens receives the n_gen sampled ids.
+ * Continues from the current cache position.  Synchronous. */
+rdl_status rdl_llama_generate_greedy(rdl_llama* model, const int32_t* prompt, size_t n_prompt,
+                                     size_t n_gen, int32_t* out_tokens);
+
+/* Device time, in milliseconds, of the last rdl_llama_generate_greedy call:
+ * its prefill and its decode steps (HIP events on the model's stream). */
+rdl_status rdl_llama_last_timing(const rdl_llama* model, float* prefill_ms, float* decode_ms);
+
+/* The model's RoPE tables (RoPEFreqs::new: [max_seq, head_dim/2] f32 each),
+ * copied to host memory. */
+rdl_status rdl_llama_rope_tables(const rdl_llama* model, float* cos_out, float* sin_out, size_t len);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,113 @@
+"""CPU restatement of the rustml Q4_0 Llama decode path, for the GPU decoder's
+parity tests.
+
+TEST INFRASTRUCTURE ONLY (imported by tests/): it checks librdlquant's
+rdl_llama_* path and is never called by the product.
+
+Follows, in f32:
+  LlmModel::forward_with_cache_pass      rustml/nlp/main/src/core/model.rs:890-937
+  TransformerBlock::forward_with_cache   rustml/nn/main/src/core/transformer_block.rs:321-355
+  MultiHeadAttention::forward_with_cache rustml/nn/main/src/core/attention.rs:353-449
+  FeedForward::forward (SwiGLU)          rustml/nn/main/src/core/feed_forward.rs:138-150
+  RoPEFreqs::apply (scalar form)         rustml/nn/main/src/core/rope.rs:134-200
+  Tensor::softmax (last dim)             rustml/core/main/src/core/tensor/ops.rs:582-628
+  Tensor::silu                           rustml/core/main/src/core/tensor/ops.rs:441-446
+  Embedding::forward over to_f32 rows    rustml/nn/main/src/core/embedding.rs:50-76
+  sampling::argmax                       rustml/nlp/main/src/core/sampling.rs:8-18
+The Q4_0 Linears and the embedding dequantization call the C restatement
+(oracle/rdl_oracle.c: matmul_f32_q4, to_f32), RMSNorm its AVX2-order row
+(orc_rms_norm_row) and the RoPE tables orc_rope_tables.  The f32 matmuls of
+attention (faer in the reference) and the softmax sum use numpy's order: their
+summation order is not pinned, only f32 accuracy.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from . import oracle as orc
+
+
+class LlamaRef:
+    def __init__(self, cfg, weights, threads=8):
+        """cfg: rdlquant.llama.LlamaConfig; weights: dict slot -> array (model
+        slots) or (slot, layer) -> array, as given to LlamaModel.set_weight."""
+        self.c = cfg
+        self.w = weights
+        self.threads = threads
+        c = cfg
+        self.cos, self.sin = orc.rope_tables(c.head_dim, c.max_seq, c.rope_theta)
+        self.kv = [[np.zeros((c.n_kv_heads, c.max_seq, c.head_dim), np.float32) for _ in range(2)]
+                   for _ in range(c.n_layers)]
+        self.pos = 0
+
+    def _linear(self, key, x, n, k):
+        m = x.shape[0]
+        return orc.matmul("q4", x, self.w[key], m, k, n, threads=self.threads).reshape(m, n)
+
+    def _rope(self, t, start):
+        # t [heads, S, D]: out1 = x1 cos - x2 sin, out2 = x1 sin + x2 cos
+        half = self.c.head_dim // 2
+        s = t.shape[1]
+        cs = self.cos[start:start + s][None]
+        sn = self.sin[start:start + s][None]
+        x1, x2 = t[..., :half], t[..., half:]
+        return np.concatenate([x1 * cs - x2 * sn, x1 * sn + x2 * cs], axis=-1).astype(np.float32)
+
+    def forward_with_cache(self, tokens):
+        """Last row's logits; the cache advances by len(tokens)."""
+        c = self.c
+        tokens = np.asarray(tokens, np.int64).reshape(-1)
+        s = tokens.size
+        emb = self.w["emb_f32"]
+        x = emb[tokens].astype(np.float32)  # [S, dim]
+        start = self.pos
+        hd, nh, nkv = c.head_dim, c.n_heads, c.n_kv_heads
+        scale = np.float32(np.sqrt(np.float32(hd)))
+        for layer in range(c.n_layers):
+            xn = orc.rms_norm(x, self.w[("attn_norm", layer)], c.norm_eps)
+            q = self._linear(("wq", layer), xn, nh * hd, c.dim)
+            k = self._linear(("wk", layer), xn, nkv * hd, c.dim)
+            v = self._linear(("wv", layer), xn, nkv * hd, c.dim)
+            q = q.reshape(s, nh, hd).transpose(1, 0, 2)
+            k = k.reshape(s, nkv, hd).transpose(1, 0, 2)
+            v = v.reshape(s, nkv, hd).transpose(1, 0, 2)
+            q, k = self._rope(q, start), self._rope(k, start)
+            kc, vc = self.kv[layer]
+            kc[:, start:start + s] = k
+            vc[:, start:start + s] = v
+            total = start + s
+            n_rep = nh // nkv
+            ctx = np.zeros((nh, s, hd), np.float32)
+            for h in range(nh):
+                kh, vh = kc[h // n_rep, :total], vc[h // n_rep, :total]
+                sc = (q[h] @ kh.T).astype(np.float32) / scale
+                if s > 1:  # causal mask (Tensor::causal_mask(seq_len, total_len))
+                    for i in range(s):
+                        sc[i, start + i + 1:] = -np.inf
+                mx = sc.max(axis=1, keepdims=True)
+                e = np.exp(sc - mx).astype(np.float32)
+                p = (e / e.sum(axis=1, keepdims=True, dtype=np.float32)).astype(np.float32)
+                ctx[h] = (p @ vh).astype(np.float32)
+            ctx = ctx.transpose(1, 0, 2).reshape(s, nh * hd)
+            attn = self._linear(("wo", layer), ctx, c.dim, nh * hd)
+            x = (attn + x).astype(np.float32)
+            xn = orc.rms_norm(x, self.w[("ffn_norm", layer)], c.norm_eps)
+            gate = self._linear(("w_gate", layer), xn, c.ffn_dim, c.dim)
+            up = self._linear(("w_up", layer), xn, c.ffn_dim, c.dim)
+            sig = (np.float32(1.0) / (np.float32(1.0) + np.exp(-gate))).astype(np.float32)
+            h = ((gate * sig) * up).astype(np.float32)
+            down = self._linear(("w_down", layer), h, c.dim, c.ffn_dim)
+            x = (x + down).astype(np.float32)
+        xl = orc.rms_norm(x[-1:], self.w["final_norm"], c.norm_eps)
+        logits = self._linear("output", xl, c.vocab, c.dim).reshape(-1)
+        self.pos += s
+        return logits
+
+
+def argmax(logits):
+    """sampling::argmax: first maximum wins; NaN never wins; 0 for an all-NaN row."""
+    best, val = 0, -np.inf
+    for i, v in enumerate(np.asarray(logits, np.float32)):
+        if v > val:
+            val, best = v, i
+    return best

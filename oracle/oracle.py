@@ -55,6 +55,8 @@ _decl("orc_q4_0_q8_0_block_dots", _i, _fp, _u8p, _sz, _sz, _sz, _sz, _i32p)
 for _n in ("q4_0", "q4_1", "q8_0"):
     _decl(f"orc_to_f32_{_n}", _i, _u8p, _sz, _sz, _fp)
 _decl("orc_dequantize_q4k", _i, _u8p, _sz, _sz, _fp)
+_decl("orc_rope_tables", None, _i, _i, _f, _fp, _fp)
+_decl("orc_rms_norm_row", None, _fp, _fp, _sz, _f, _fp)
 
 
 class OracleError(Exception):
@@ -159,3 +161,25 @@ def to_f32(kind, w, n_elements):
     if rc:
         raise OracleError(rc)
     return out
+
+
+def rope_tables(head_dim, max_seq, theta):
+    half = head_dim // 2
+    c = np.zeros(max_seq * half, np.float32)
+    s = np.zeros(max_seq * half, np.float32)
+    lib.orc_rope_tables(head_dim, max_seq, theta, c.ctypes.data_as(_fp), s.ctypes.data_as(_fp))
+    return c.reshape(max_seq, half), s.reshape(max_seq, half)
+
+
+def rms_norm(x, gamma, eps):
+    """Tensor::rms_norm over the last axis of x (rows restated one at a time)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    g, gp = _f32(gamma)
+    rows = x.reshape(-1, x.shape[-1])
+    out = np.zeros_like(rows)
+    for r in range(rows.shape[0]):
+        row = np.ascontiguousarray(rows[r])
+        o = np.zeros(row.size, np.float32)
+        lib.orc_rms_norm_row(row.ctypes.data_as(_fp), gp, row.size, eps, o.ctypes.data_as(_fp))
+        out[r] = o
+    return out.reshape(x.shape)

@@ -600,3 +600,48 @@ int orc_matmul_f32_f32(const float* x, const float* w, size_t m, size_t k, size_
     free(jobs);
     return ORC_OK;
 }
+
+/* ---- decoder pieces ---- */
+
+void orc_rope_tables(int head_dim, int max_seq, float theta, float* cos_out, float* sin_out) {
+    /* rope.rs:97-105 */
+    const int half = head_dim / 2;
+    for (int pos = 0; pos < max_seq; pos++)
+        for (int i = 0; i < half; i++) {
+            const float freq = 1.0f / powf(theta, 2.0f * (float)i / (float)head_dim);
+            const float angle = (float)pos * freq;
+            cos_out[(size_t)pos * half + i] = cosf(angle);
+            sin_out[(size_t)pos * half + i] = sinf(angle);
+        }
+}
+
+void orc_rms_norm_row(const float* row, const float* gamma, size_t dim, float eps, float* out) {
+    if (dim < 8) { /* scalar fallback, ops.rs:735-744 */
+        float sum_sq = 0.0f;
+        for (size_t i = 0; i < dim; i++) sum_sq += row[i] * row[i];
+        const float rms = sqrtf(sum_sq / (float)dim + eps);
+        for (size_t j = 0; j < dim; j++) out[j] = row[j] / rms * gamma[j];
+        return;
+    }
+    float acc0[8] = {0}, acc1[8] = {0};
+    size_t i = 0;
+    for (; i + 16 <= dim; i += 16) /* ops.rs:23-29 */
+        for (int l = 0; l < 8; l++) {
+            const float v0 = row[i + l], v1 = row[i + 8 + l];
+            acc0[l] = acc0[l] + v0 * v0;
+            acc1[l] = acc1[l] + v1 * v1;
+        }
+    for (; i + 8 <= dim; i += 8) /* ops.rs:30-34 */
+        for (int l = 0; l < 8; l++) acc0[l] = acc0[l] + row[i + l] * row[i + l];
+    float sv[8];
+    for (int l = 0; l < 8; l++) sv[l] = acc0[l] + acc1[l];
+    /* ops.rs:35-43: lo + hi, movehdup, movehl, add_ss */
+    float s128[4];
+    for (int l = 0; l < 4; l++) s128[l] = sv[l] + sv[4 + l];
+    const float sums0 = s128[0] + s128[1], sums2 = s128[2] + s128[3];
+    float sum_sq = sums0 + sums2;
+    for (; i < dim; i++) sum_sq += row[i] * row[i]; /* ops.rs:44-48 */
+    const float rms = sqrtf(sum_sq / (float)dim + eps); /* ops.rs:51-53 */
+    const float inv_rms = 1.0f / rms;
+    for (size_t j = 0; j < dim; j++) out[j] = (row[j] * inv_rms) * gamma[j];
+}

@@ -107,6 +107,21 @@ int orc_matmul_f32_q4k(const float* x, const uint8_t* w, size_t w_len, size_t m,
 int orc_matmul_f32_f32(const float* x, const float* w, size_t m, size_t k, size_t n, float* y,
                        int threads);
 
+/* ---- decoder pieces (config 5) ---- */
+
+/* RoPEFreqs::new (rustml/nn/main/src/core/rope.rs:93-108): cos/sin tables
+ * [max_seq][head_dim/2] in f32: freq = 1 / powf(theta, 2i/hd), angle =
+ * pos * freq, with the C library's powf / cosf / sinf (the calls Rust's f32
+ * powf / cos / sin make). */
+void orc_rope_tables(int head_dim, int max_seq, float theta, float* cos_out, float* sin_out);
+
+/* Tensor::rms_norm for one row (rustml/core/main/src/core/tensor/ops.rs:688-751)
+ * on its AVX2 path (rms_norm_row_avx2, ops.rs:14-69, taken for dim >= 8):
+ * two 8-lane sum-of-squares accumulators over 16-element steps, the 8-lane
+ * tail, the hi/lo + movehdup + movehl horizontal sum, the scalar remainder;
+ * out = (x * (1 / sqrt(sum / dim + eps))) * g. */
+void orc_rms_norm_row(const float* row, const float* gamma, size_t dim, float eps, float* out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -31,11 +31,11 @@ struct rdl_weight {
     bool gemm_ok;  // block scales fit the prefill GEMM's f16 operands
 };
 
-namespace {
+namespace rdl {
 
 thread_local std::string g_err;
 
-rdl_status fail(rdl_status st, const char* fmt, ...) {
+rdl_status api_fail(rdl_status st, const char* fmt, ...) {
     char buf[512];
     va_list ap;
     va_start(ap, fmt);
@@ -45,17 +45,18 @@ rdl_status fail(rdl_status st, const char* fmt, ...) {
     return st;
 }
 
-rdl_status ok() {
+rdl_status api_ok() {
     g_err.clear();
     return RDL_OK;
 }
 
-#define HIP_TRY(expr)                                                                     \
-    do {                                                                                  \
-        hipError_t e_ = (expr);                                                           \
-        if (e_ != hipSuccess)                                                             \
-            return fail(RDL_ERR_HIP, "%s failed: %s", #expr, hipGetErrorString(e_));      \
-    } while (0)
+}  // namespace rdl
+
+namespace {
+
+using rdl::g_err;
+constexpr auto fail = rdl::api_fail;
+constexpr auto ok = rdl::api_ok;
 
 const char* type_name(WType t) {
     switch (t) {
@@ -84,7 +85,9 @@ int count_devices() {
     return good;
 }
 
-rdl_status require_device() {
+}  // namespace
+
+rdl_status rdl::api_require_device() {
     int n = 0;
     if (hipGetDeviceCount(&n) != hipSuccess || n == 0)
         return fail(RDL_ERR_NO_DEVICE, "no HIP device is visible");
@@ -98,6 +101,10 @@ rdl_status require_device() {
                     p.gcnArchName);
     return RDL_OK;
 }
+
+namespace {
+
+constexpr auto require_device = rdl::api_require_device;
 
 // Shape checks shared by every matmul entry point.
 rdl_status check_matmul(WType t, const float* x, size_t x_len, const uint8_t* w, size_t w_len,

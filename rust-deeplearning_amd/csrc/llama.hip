@@ -1,0 +1,684 @@
+// llama.hip -- batch-1 Llama-style decoder (include/rdl_llama.h): the rustml
+// decode loop with every activation on the device and the Q4_0 Linears on
+// this library's fused GEMV (one or a few rows) and matrix-core GEMM (prompt
+// chunks).
+//
+// Per layer (TransformerBlock::forward_with_cache, transformer_block.rs:297-356,
+// standard pre-norm branch):
+//   xn  = rms_norm(x, attn_norm)                    ops.rs:688-751
+//   qkv = xn . [Wq; Wk; Wv]^T                       one launch over the
+//                                                    row-concatenated weights
+//   rope(q), rope(k) at start_pos; k, v -> cache    attention.rs:393-399, rope.rs:134-200
+//   att = softmax(q k^T / sqrt(hd) + causal) v      attention.rs:401-446, head h reads
+//                                                    KV head h / (n_heads / n_kv)
+//   x  += att . Wo^T
+//   xn  = rms_norm(x, ffn_norm)
+//   gu  = xn . [Wgate; Wup]^T
+//   h   = silu(gate) * up                           feed_forward.rs:138-150, ops.rs:441-446
+//   x  += h . Wdown^T
+// then rms_norm(x, norm) . Wout^T on the last row, argmax (sampling.rs:8-18).
+// The cache position lives in device memory, so a decode step has no host
+// dependency and is captured once as a HIP graph and replayed.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+#include "../../include/rdl_llama.h"
+#include "rdl_device.hpp"
+#include "rdl_internal.hpp"
+
+namespace rdl {
+namespace {
+
+constexpr int NT = 256;  // threads of the element-wise / reduction kernels
+
+__device__ __forceinline__ float wave_sum(float v) {
+    v = sum8_f32(v);
+    v += dpp_f32<DPP_ROW_MIRROR>(v);
+    v += __shfl_xor(v, 16);
+    return v + __shfl_xor(v, 32);
+}
+__device__ __forceinline__ float wave_max(float v) {
+    v = max8_f32(v);
+    v = fmaxf(v, dpp_f32<DPP_ROW_MIRROR>(v));
+    v = fmaxf(v, __shfl_xor(v, 16));
+    return fmaxf(v, __shfl_xor(v, 32));
+}
+// Sum / max over a 256-thread block, returned to every thread.
+__device__ __forceinline__ float block_sum(float v, float* red) {
+    v = wave_sum(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return (red[0] + red[1]) + (red[2] + red[3]);
+}
+__device__ __forceinline__ float block_max(float v, float* red) {
+    v = wave_max(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// rms = sqrt(sum(x^2) / d + eps); out = x * (1 / rms) * g   (ops.rs:688-751)
+__global__ __launch_bounds__(NT) void rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ g,
+                                                     int d, float eps, float* __restrict__ out) {
+    __shared__ float red[NT / 64];
+    const float* xr = x + (size_t)blockIdx.x * d;
+    float* o = out + (size_t)blockIdx.x * d;
+    float ss = 0.0f;
+    for (int c = threadIdx.x; c < d; c += NT) ss += xr[c] * xr[c];
+    ss = block_sum(ss, red);
+    const float rms = sqrtf(ss / (float)d + eps);
+    const float inv = 1.0f / rms;
+    for (int c = threadIdx.x; c < d; c += NT) o[c] = (xr[c] * inv) * g[c];
+}
+
+// RoPE (half-split pairs (i, i + hd/2), rope.rs:134-200) of q and k at
+// positions pos..pos+m-1, then k and v into the cache (KVCache::update,
+// kv_cache.rs:94-106; cache layout [kv_head][max_seq][hd]).
+template <typename KV>
+__global__ void rope_kv_kernel(float* __restrict__ qkv, int qkv_dim, const int* __restrict__ pos_dev,
+                               const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+                               int n_heads, int n_kv, int hd, KV* __restrict__ kc, KV* __restrict__ vc,
+                               int max_seq) {
+    const int s = blockIdx.y, head = blockIdx.x, i = threadIdx.x, half = hd >> 1;
+    const int pos = *pos_dev + s;
+    float* row = qkv + (size_t)s * qkv_dim;
+    const float c = cos_t[(size_t)pos * half + i], sn = sin_t[(size_t)pos * half + i];
+    if (head < n_heads) {
+        float* q = row + head * hd;
+        const float x1 = q[i], x2 = q[half + i];
+        q[i] = x1 * c - x2 * sn;
+        q[half + i] = x1 * sn + x2 * c;
+    } else {
+        const int kvh = head - n_heads;
+        const float* k = row + n_heads * hd + kvh * hd;
+        const float* v = row + (n_heads + n_kv) * hd + kvh * hd;
+        const float x1 = k[i], x2 = k[half + i];
+        KV* kd = kc + ((size_t)kvh * max_seq + pos) * hd;
+        KV* vd = vc + ((size_t)kvh * max_seq + pos) * hd;
+        kd[i] = (KV)(x1 * c - x2 * sn);
+        kd[half + i] = (KV)(x1 * sn + x2 * c);
+        vd[i] = (KV)v[i];
+        vd[half + i] = (KV)v[half + i];
+    }
+}
+
+// Attention of query row s (position pos + s) and head h over the cached keys
+// 0 .. pos + s (the causal mask of attention.rs:424-433 keeps exactly these):
+// scores q.k / sqrt(hd), softmax (max-subtracted, ops.rs:582-628), then the
+// probability-weighted sum of the values.  One workgroup per (head, row).
+template <typename KV>
+__global__ __launch_bounds__(NT) void attention_kernel(const float* __restrict__ qkv, int qkv_dim,
+                                                       const int* __restrict__ pos_dev,
+                                                       const KV* __restrict__ kc,
+                                                       const KV* __restrict__ vc, int max_seq,
+                                                       int n_heads, int n_kv, int hd, float scale,
+                                                       float* __restrict__ out) {
+    extern __shared__ float sm[];  // q[hd] | part[4][hd] | scores[t]
+    __shared__ float red[NT / 64];
+    const int h = blockIdx.x, s = blockIdx.y;
+    const int kvh = h / (n_heads / n_kv);
+    const int t = *pos_dev + s + 1;
+    float* qs = sm;
+    float* part = sm + hd;
+    float* sc = part + 4 * hd;
+    const float* q = qkv + (size_t)s * qkv_dim + h * hd;
+    for (int d = threadIdx.x; d < hd; d += NT) qs[d] = q[d];
+    __syncthreads();
+    const KV* kbase = kc + (size_t)kvh * max_seq * hd;
+    for (int p = threadIdx.x; p < t; p += NT) {
+        const KV* kr = kbase + (size_t)p * hd;
+        float acc = 0.0f;
+        for (int d = 0; d < hd; d++) acc += qs[d] * (float)kr[d];
+        sc[p] = acc / scale;
+    }
+    __syncthreads();
+    float mx = -__builtin_inff();
+    for (int p = threadIdx.x; p < t; p += NT) mx = fmaxf(mx, sc[p]);
+    mx = block_max(mx, red);
+    float sum = 0.0f;
+    for (int p = threadIdx.x; p < t; p += NT) {
+        const float e = expf(sc[p] - mx);
+        sc[p] = e;
+        sum += e;
+    }
+    sum = block_sum(sum, red);
+    for (int p = threadIdx.x; p < t; p += NT) sc[p] = sc[p] / sum;
+    __syncthreads();
+    // context: wave w takes positions w, w + 4, ...; lane l dims l, l + 64, ...
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const KV* vbase = vc + (size_t)kvh * max_seq * hd;
+    for (int d0 = 0; d0 < hd; d0 += 64) {
+        const int d = d0 + lane;
+        float acc = 0.0f;
+        if (d < hd)
+            for (int p = w; p < t; p += 4) acc += sc[p] * (float)vbase[(size_t)p * hd + d];
+        if (d < hd) part[w * hd + d] = acc;
+    }
+    __syncthreads();
+    float* o = out + (size_t)s * n_heads * hd + h * hd;
+    for (int d = threadIdx.x; d < hd; d += NT) o[d] = (part[d] + part[hd + d]) + (part[2 * hd + d] + part[3 * hd + d]);
+}
+
+// x += y (Tensor::add_inplace, ops.rs:276-289)
+__global__ void add_kernel(float* __restrict__ x, const float* __restrict__ y, size_t n) {
+    const size_t i = (size_t)blockIdx.x * NT + threadIdx.x;
+    if (i < n) x[i] = x[i] + y[i];
+}
+
+// h = silu(gate) * up, silu(g) = g * (1 / (1 + exp(-g)))   (ops.rs:441-446)
+__global__ void swiglu_kernel(const float* __restrict__ gu, int ffn, size_t n, float* __restrict__ h) {
+    const size_t i = (size_t)blockIdx.x * NT + threadIdx.x;
+    if (i >= n) return;
+    const size_t s = i / ffn, j = i % ffn;
+    const float g = gu[s * 2 * ffn + j], u = gu[s * 2 * ffn + ffn + j];
+    const float sig = 1.0f / (1.0f + expf(-g));
+    h[i] = (g * sig) * u;
+}
+
+// argmax with the first maximum winning (strict >, NaN never wins; an
+// all-NaN / -inf row gives 0, sampling.rs:8-18).  Writes the token for the
+// next step and out_tokens[*step], then advances *step.
+constexpr int ARGMAX_NT = 1024;
+__global__ __launch_bounds__(ARGMAX_NT) void argmax_kernel(const float* __restrict__ logits, int vocab,
+                                                           int* __restrict__ token, int* __restrict__ out_tokens,
+                                                           int* __restrict__ step) {
+    __shared__ float bv[ARGMAX_NT / 64];
+    __shared__ int bi[ARGMAX_NT / 64];
+    float best = -__builtin_inff();
+    int idx = 0x7FFFFFFF;
+    for (int i = threadIdx.x; i < vocab; i += ARGMAX_NT) {
+        const float v = logits[i];
+        if (v > best) {
+            best = v;
+            idx = i;
+        }
+    }
+    // (value, index) reduction: larger value, then smaller index
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float ov = __shfl_xor(best, o);
+        const int oi = __shfl_xor(idx, o);
+        if (ov > best || (ov == best && oi < idx)) {
+            best = ov;
+            idx = oi;
+        }
+    }
+    if ((threadIdx.x & 63) == 0) {
+        bv[threadIdx.x >> 6] = best;
+        bi[threadIdx.x >> 6] = idx;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < ARGMAX_NT / 64; w++)
+            if (bv[w] > best || (bv[w] == best && bi[w] < idx)) {
+                best = bv[w];
+                idx = bi[w];
+            }
+        if (idx == 0x7FFFFFFF) idx = 0;
+        const int st = *step;
+        token[0] = idx;
+        out_tokens[st] = idx;
+        *step = st + 1;
+    }
+}
+
+// KVCache::advance (kv_cache.rs:112-114)
+__global__ void advance_kernel(int* pos, int by) {
+    if (threadIdx.x == 0) *pos += by;
+}
+__global__ void set_int_kernel(int* p, int v) {
+    if (threadIdx.x == 0) *p = v;
+}
+
+// ---- synthetic weights --------------------------------------------------------------
+__device__ __forceinline__ uint64_t splitmix64(uint64_t& s) {
+    uint64_t z = (s += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+// Q4_0 blocks: 16 random nibble bytes, d = f16(|N(0, sigma)| / 8) (Box-Muller).
+__global__ void fill_q4_0_kernel(uint8_t* __restrict__ w, size_t nblocks, uint64_t seed, float sigma) {
+    const size_t g = (size_t)blockIdx.x * NT + threadIdx.x;
+    if (g >= nblocks) return;
+    uint64_t st = seed ^ (g * 0xD1B54A32D192ED03ull);
+    const uint64_t a = splitmix64(st), b = splitmix64(st), c = splitmix64(st);
+    const float u1 = ((float)(c >> 40) + 1.0f) * 0x1p-24f;  // (0, 1]
+    const float u2 = (float)((c >> 16) & 0xFFFFFFu) * 0x1p-24f;
+    const float z = sqrtf(-2.0f * logf(u1)) * cosf(6.2831853f * u2);
+    const uint32_t d = f2h_rne(fabsf(z) * sigma / 8.0f);
+    uint16_t* p = reinterpret_cast<uint16_t*>(w + g * Q4_0_BYTES);  // blocks are 2-byte aligned
+    p[0] = (uint16_t)d;
+    for (int i = 0; i < 4; i++) p[1 + i] = (uint16_t)(a >> (16 * i));
+    for (int i = 0; i < 4; i++) p[5 + i] = (uint16_t)(b >> (16 * i));
+}
+__global__ void fill_f32_kernel(float* __restrict__ p, size_t n, float v) {
+    const size_t i = (size_t)blockIdx.x * NT + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+unsigned blocks_for(size_t n) { return (unsigned)((n + NT - 1) / NT); }
+
+}  // namespace
+
+// ---- the model -------------------------------------------------------------------------
+struct LlamaModel {
+    rdl_llama_config cfg{};
+    int q_dim = 0, kv_dim = 0, qkv_dim = 0;
+    size_t row_q4(int k) const { return (size_t)(k / QK) * Q4_0_BYTES; }
+
+    struct Mat {
+        uint8_t* dev = nullptr;
+        int n = 0, k = 0;
+        bool gemm_ok = true;
+        size_t bytes() const { return (size_t)n * (k / QK) * Q4_0_BYTES; }
+    };
+    struct Layer {
+        Mat qkv, o, gu, down;
+        float* attn_norm = nullptr;
+        float* ffn_norm = nullptr;
+    };
+    std::vector<Layer> layers;
+    Mat emb, out;
+    float* final_norm = nullptr;
+    void* kc = nullptr;  // [layer][kv_head][max_seq][hd]
+    void* vc = nullptr;
+    float *cos_t = nullptr, *sin_t = nullptr;
+    std::vector<float> cos_h, sin_h;
+    // activations for up to max_batch rows
+    float *x = nullptr, *xn = nullptr, *qkv = nullptr, *att = nullptr, *gu = nullptr, *hb = nullptr,
+          *logits = nullptr;
+    int *tokens = nullptr, *pos = nullptr, *step = nullptr, *out_tokens = nullptr;
+    size_t out_cap = 0;
+    void* gemm_scratch = nullptr;
+    hipStream_t stream = nullptr;
+    hipGraphExec_t decode_exec = nullptr;
+    hipGraph_t decode_graph = nullptr;
+    hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
+    float prefill_ms = 0.0f, decode_ms = 0.0f;
+    size_t host_pos = 0;  // mirror of *pos
+    std::vector<void*> allocs;
+
+    ~LlamaModel() {
+        if (decode_exec) (void)hipGraphExecDestroy(decode_exec);
+        if (decode_graph) (void)hipGraphDestroy(decode_graph);
+        for (hipEvent_t e : ev)
+            if (e) (void)hipEventDestroy(e);
+        if (stream) (void)hipStreamDestroy(stream);
+        for (void* p : allocs) (void)hipFree(p);
+    }
+
+    hipError_t alloc(void** p, size_t bytes) {
+        hipError_t e = hipMalloc(p, bytes ? bytes : 16);
+        if (e == hipSuccess) allocs.push_back(*p);
+        return e;
+    }
+    template <typename T>
+    hipError_t alloc_t(T** p, size_t count) {
+        return alloc(reinterpret_cast<void**>(p), count * sizeof(T));
+    }
+    size_t kv_elem() const { return cfg.kv_f16 ? 2 : 4; }
+    size_t kv_layer_elems() const { return (size_t)cfg.n_kv_heads * cfg.max_seq * cfg.head_dim; }
+
+    // y[m, mat.n] = x[m, mat.k] . W^T on the model's stream
+    hipError_t linear(const Mat& w, const float* xin, size_t m, float* y) {
+        if (m <= 4) return launch_gemv_fused(WType::Q4_0, false, w.dev, w.n, w.k, xin, m, y, stream);
+        if (w.gemm_ok) return launch_gemm_q4_0(w.dev, w.n, w.k, xin, m, y, gemm_scratch, stream);
+        // rows one launch at a time through the fused GEMV (scales beyond the GEMM's range)
+        for (size_t r = 0; r < m; r += 4) {
+            const size_t mr = (m - r < 4) ? m - r : 4;
+            hipError_t e = launch_gemv_fused(WType::Q4_0, false, w.dev, w.n, w.k, xin + r * w.k, mr,
+                                             y + r * w.n, stream);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
+
+    template <typename KV>
+    hipError_t layer_attention(int l, size_t m) {
+        KV* kcl = reinterpret_cast<KV*>(kc) + (size_t)l * kv_layer_elems();
+        KV* vcl = reinterpret_cast<KV*>(vc) + (size_t)l * kv_layer_elems();
+        const int hd = cfg.head_dim;
+        hipLaunchKernelGGL(rope_kv_kernel<KV>, dim3(cfg.n_heads + cfg.n_kv_heads, (unsigned)m), dim3(hd / 2), 0,
+                           stream, qkv, qkv_dim, pos, cos_t, sin_t, cfg.n_heads, cfg.n_kv_heads, hd, kcl, vcl,
+                           cfg.max_seq);
+        const size_t lds = (size_t)(5 * hd + cfg.max_seq) * sizeof(float);
+        const float scale = sqrtf((float)hd);
+        hipLaunchKernelGGL(attention_kernel<KV>, dim3(cfg.n_heads, (unsigned)m), dim3(NT), lds, stream, qkv,
+                           qkv_dim, pos, kcl, vcl, cfg.max_seq, cfg.n_heads, cfg.n_kv_heads, hd, scale, att);
+        return hipGetLastError();
+    }
+
+    // forward_with_cache_pass over m rows whose token ids are in `tokens`,
+    // the last row's logits into `logits`, then the position advances by m.
+    hipError_t forward(size_t m) {
+        const int d = cfg.dim;
+        hipError_t e = launch_dequant_rows(WType::Q4_0, emb.dev, emb.n, emb.k, tokens, m, x, stream);
+        if (e != hipSuccess) return e;
+        for (int l = 0; l < cfg.n_layers; l++) {
+            Layer& L = layers[l];
+            hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)m), dim3(NT), 0, stream, x, L.attn_norm, d,
+                               cfg.norm_eps, xn);
+            if ((e = linear(L.qkv, xn, m, qkv)) != hipSuccess) return e;
+            e = cfg.kv_f16 ? layer_attention<_Float16>(l, m) : layer_attention<float>(l, m);
+            if (e != hipSuccess) return e;
+            if ((e = linear(L.o, att, m, xn)) != hipSuccess) return e;
+            hipLaunchKernelGGL(add_kernel, dim3(blocks_for(m * d)), dim3(NT), 0, stream, x, xn, m * d);
+            hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)m), dim3(NT), 0, stream, x, L.ffn_norm, d,
+                               cfg.norm_eps, xn);
+            if ((e = linear(L.gu, xn, m, gu)) != hipSuccess) return e;
+            hipLaunchKernelGGL(swiglu_kernel, dim3(blocks_for(m * cfg.ffn_dim)), dim3(NT), 0, stream, gu,
+                               cfg.ffn_dim, m * cfg.ffn_dim, hb);
+            if ((e = linear(L.down, hb, m, xn)) != hipSuccess) return e;
+            hipLaunchKernelGGL(add_kernel, dim3(blocks_for(m * d)), dim3(NT), 0, stream, x, xn, m * d);
+        }
+        const float* last = x + (m - 1) * d;
+        hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(NT), 0, stream, last, final_norm, d, cfg.norm_eps, xn);
+        if ((e = linear(out, xn, 1, logits)) != hipSuccess) return e;
+        hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(64), 0, stream, pos, (int)m);
+        return hipGetLastError();
+    }
+
+    // One greedy decode step: token (device) -> logits -> argmax -> token.
+    hipError_t decode_step() {
+        hipError_t e = forward(1);
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(ARGMAX_NT), 0, stream, logits, cfg.vocab, tokens,
+                           out_tokens, step);
+        return hipGetLastError();
+    }
+};
+
+}  // namespace rdl
+
+struct rdl_llama {
+    rdl::LlamaModel m;
+};
+
+using rdl::api_fail;
+using rdl::api_ok;
+
+namespace {
+
+bool valid_config(const rdl_llama_config& c) {
+    return c.dim > 0 && c.n_layers > 0 && c.n_heads > 0 && c.n_kv_heads > 0 && c.head_dim > 0 &&
+           c.head_dim % 2 == 0 && c.head_dim <= 256 && c.n_heads % c.n_kv_heads == 0 && c.ffn_dim > 0 &&
+           c.vocab > 0 && c.max_seq > 0 && c.max_batch > 0 && c.dim % 32 == 0 && c.ffn_dim % 32 == 0 &&
+           (c.n_heads * c.head_dim) % 32 == 0 && c.dim <= 16384 && c.ffn_dim <= 16384 &&
+           c.n_heads * c.head_dim <= 16384;
+}
+
+}  // namespace
+
+extern "C" {
+
+rdl_status rdl_llama_create(const rdl_llama_config* cfg, rdl_llama** out) {
+    if (!cfg || !out) return api_fail(RDL_ERR_NULL_POINTER, "NULL argument");
+    *out = nullptr;
+    if (!valid_config(*cfg))
+        return api_fail(RDL_ERR_INVALID_DATA,
+                        "unsupported config (dim, ffn_dim, heads*head_dim multiples of 32 and <= 16384; "
+                        "head_dim even <= 256; n_heads %% n_kv_heads == 0)");
+    rdl_status st = rdl::api_require_device();
+    if (st != RDL_OK) return st;
+    rdl_llama* h = new rdl_llama();
+    rdl::LlamaModel& M = h->m;
+    M.cfg = *cfg;
+    const rdl_llama_config& c = M.cfg;
+    M.q_dim = c.n_heads * c.head_dim;
+    M.kv_dim = c.n_kv_heads * c.head_dim;
+    M.qkv_dim = M.q_dim + 2 * M.kv_dim;
+    auto mat = [&](rdl::LlamaModel::Mat& w, int n, int k) -> hipError_t {
+        w.n = n;
+        w.k = k;
+        return M.alloc(reinterpret_cast<void**>(&w.dev), w.bytes() + 64);
+    };
+    auto fail_free = [&](hipError_t e) {
+        delete h;
+        return api_fail(RDL_ERR_HIP, "allocation failed: %s", hipGetErrorString(e));
+    };
+    hipError_t e = hipStreamCreateWithFlags(&M.stream, hipStreamNonBlocking);
+    if (e != hipSuccess) return fail_free(e);
+    for (auto& ev : M.ev)
+        if ((e = hipEventCreate(&ev)) != hipSuccess) return fail_free(e);
+    M.layers.resize(c.n_layers);
+    for (auto& L : M.layers) {
+        if ((e = mat(L.qkv, M.qkv_dim, c.dim)) != hipSuccess) return fail_free(e);
+        if ((e = mat(L.o, c.dim, M.q_dim)) != hipSuccess) return fail_free(e);
+        if ((e = mat(L.gu, 2 * c.ffn_dim, c.dim)) != hipSuccess) return fail_free(e);
+        if ((e = mat(L.down, c.dim, c.ffn_dim)) != hipSuccess) return fail_free(e);
+        if ((e = M.alloc_t(&L.attn_norm, c.dim)) != hipSuccess) return fail_free(e);
+        if ((e = M.alloc_t(&L.ffn_norm, c.dim)) != hipSuccess) return fail_free(e);
+    }
+    if ((e = mat(M.emb, c.vocab, c.dim)) != hipSuccess) return fail_free(e);
+    if ((e = mat(M.out, c.vocab, c.dim)) != hipSuccess) return fail_free(e);
+    if ((e = M.alloc_t(&M.final_norm, c.dim)) != hipSuccess) return fail_free(e);
+    const size_t kv_bytes = (size_t)c.n_layers * M.kv_layer_elems() * M.kv_elem();
+    if ((e = M.alloc(&M.kc, kv_bytes)) != hipSuccess) return fail_free(e);
+    if ((e = M.alloc(&M.vc, kv_bytes)) != hipSuccess) return fail_free(e);
+    const size_t mb = c.max_batch;
+    if ((e = M.alloc_t(&M.x, mb * c.dim)) != hipSuccess) return fail_free(e);
+    if ((e = M.alloc_t(&M.xn, mb * c.dim)) != hipSuccess) return fail_free(e);
+    if ((e = M.alloc_t(&M.qkv, mb * M.qkv_dim)) != hipSuccess) return fail_free(e);
+    if ((e = M.alloc_t(&M.att, mb * M.q_dim)) != hipSuccess) return fail_free(e);
+    if ((e = M.alloc_t(&M.gu, mb * 2 * c.ffn_dim)) != hipSuccess) return fail_free(e);
+    if ((e = M.alloc_t(&M.hb, mb * c.ffn_dim)) != hipSuccess) return fail_free(e);
+    if ((e = M.alloc_t(&M.logits, c.vocab)) != hipSuccess) return fail_free(e);
+    if ((e = M.alloc_t(&M.tokens, mb)) != hipSuccess) return fail_free(e);
+    if ((e = M.alloc_t(&M.pos, 1)) != hipSuccess) return fail_free(e);
+    if ((e = M.alloc_t(&M.step, 1)) != hipSuccess) return fail_free(e);
+    M.out_cap = (size_t)c.max_seq + 1;
+    if ((e = M.alloc_t(&M.out_tokens, M.out_cap)) != hipSuccess) return fail_free(e);
+    const size_t kmax = (size_t)std::max(std::max(c.dim, c.ffn_dim), M.q_dim);
+    if ((e = M.alloc(&M.gemm_scratch, rdl::gemm_scratch_bytes(mb, kmax))) != hipSuccess) return fail_free(e);
+    // RoPEFreqs::new (rope.rs:93-108) in f32 with the C library's powf / cosf / sinf
+    const int half = c.head_dim / 2;
+    M.cos_h.resize((size_t)c.max_seq * half);
+    M.sin_h.resize((size_t)c.max_seq * half);
+    for (int p = 0; p < c.max_seq; p++)
+        for (int i = 0; i < half; i++) {
+            const float freq = 1.0f / powf(c.rope_theta, (2.0f * (float)i) / (float)c.head_dim);
+            const float angle = (float)p * freq;
+            M.cos_h[(size_t)p * half + i] = cosf(angle);
+            M.sin_h[(size_t)p * half + i] = sinf(angle);
+        }
+    if ((e = M.alloc_t(&M.cos_t, M.cos_h.size())) != hipSuccess) return fail_free(e);
+    if ((e = M.alloc_t(&M.sin_t, M.sin_h.size())) != hipSuccess) return fail_free(e);
+    if ((e = hipMemcpy(M.cos_t, M.cos_h.data(), M.cos_h.size() * 4, hipMemcpyHostToDevice)) != hipSuccess ||
+        (e = hipMemcpy(M.sin_t, M.sin_h.data(), M.sin_h.size() * 4, hipMemcpyHostToDevice)) != hipSuccess)
+        return fail_free(e);
+    hipLaunchKernelGGL(rdl::set_int_kernel, dim3(1), dim3(64), 0, M.stream, M.pos, 0);
+    if ((e = hipStreamSynchronize(M.stream)) != hipSuccess) return fail_free(e);
+    *out = h;
+    return api_ok();
+}
+
+rdl_status rdl_llama_free(rdl_llama* model) {
+    delete model;
+    return api_ok();
+}
+
+rdl_status rdl_llama_set_weight(rdl_llama* model, int32_t slot, int32_t layer, const void* bytes, size_t len) {
+    if (!model || !bytes) return api_fail(RDL_ERR_NULL_POINTER, "NULL argument");
+    rdl::LlamaModel& M = model->m;
+    const rdl_llama_config& c = M.cfg;
+    const bool per_layer = slot >= RDL_LLAMA_ATTN_NORM && slot <= RDL_LLAMA_W_DOWN;
+    if (per_layer && (layer < 0 || layer >= c.n_layers))
+        return api_fail(RDL_ERR_INVALID_DATA, "layer %d out of range", layer);
+    void* dst = nullptr;
+    size_t need = 0;
+    rdl::LlamaModel::Mat* mat = nullptr;
+    auto q4 = [&](rdl::LlamaModel::Mat& w, int row0, int rows) {
+        mat = &w;
+        dst = w.dev + (size_t)row0 * M.row_q4(w.k);
+        need = (size_t)rows * M.row_q4(w.k);
+    };
+    switch (slot) {
+        case RDL_LLAMA_TOKEN_EMBEDDING: q4(M.emb, 0, c.vocab); break;
+        case RDL_LLAMA_OUTPUT: q4(M.out, 0, c.vocab); break;
+        case RDL_LLAMA_FINAL_NORM: dst = M.final_norm; need = (size_t)c.dim * 4; break;
+        case RDL_LLAMA_ATTN_NORM: dst = M.layers[layer].attn_norm; need = (size_t)c.dim * 4; break;
+        case RDL_LLAMA_FFN_NORM: dst = M.layers[layer].ffn_norm; need = (size_t)c.dim * 4; break;
+        case RDL_LLAMA_WQ: q4(M.layers[layer].qkv, 0, M.q_dim); break;
+        case RDL_LLAMA_WK: q4(M.layers[layer].qkv, M.q_dim, M.kv_dim); break;
+        case RDL_LLAMA_WV: q4(M.layers[layer].qkv, M.q_dim + M.kv_dim, M.kv_dim); break;
+        case RDL_LLAMA_WO: q4(M.layers[layer].o, 0, c.dim); break;
+        case RDL_LLAMA_W_GATE: q4(M.layers[layer].gu, 0, c.ffn_dim); break;
+        case RDL_LLAMA_W_UP: q4(M.layers[layer].gu, c.ffn_dim, c.ffn_dim); break;
+        case RDL_LLAMA_W_DOWN: q4(M.layers[layer].down, 0, c.dim); break;
+        default: return api_fail(RDL_ERR_INVALID_DATA, "unknown weight slot %d", slot);
+    }
+    if (len != need) return api_fail(RDL_ERR_SHAPE_MISMATCH, "slot %d: expected %zu bytes, got %zu", slot, need, len);
+    HIP_TRY(hipMemcpy(dst, bytes, len, hipMemcpyHostToDevice));
+    if (mat && mat != &M.emb) {
+        bool ok = false;
+        HIP_TRY(rdl::gemm_scales_ok(rdl::WType::Q4_0, mat->dev, mat->n, mat->k, &ok));
+        mat->gemm_ok = ok;
+    }
+    return api_ok();
+}
+
+rdl_status rdl_llama_init_random(rdl_llama* model, uint64_t seed) {
+    if (!model) return api_fail(RDL_ERR_NULL_POINTER, "NULL model");
+    rdl::LlamaModel& M = model->m;
+    const rdl_llama_config& c = M.cfg;
+    uint64_t tag = 0;
+    auto fill_mat = [&](rdl::LlamaModel::Mat& w) {
+        const size_t nblocks = (size_t)w.n * (w.k / rdl::QK);
+        hipLaunchKernelGGL(rdl::fill_q4_0_kernel, dim3(rdl::blocks_for(nblocks)), dim3(rdl::NT), 0, M.stream,
+                           w.dev, nblocks, seed * 0x100000001B3ull + (++tag) * 0x9E3779B97F4A7C15ull, 0.02f);
+        w.gemm_ok = true;  // |d| = |N(0, 0.02)| / 8 is far below the GEMM's f16 limit
+    };
+    auto fill_ones = [&](float* p) {
+        hipLaunchKernelGGL(rdl::fill_f32_kernel, dim3(rdl::blocks_for(c.dim)), dim3(rdl::NT), 0, M.stream, p,
+                           (size_t)c.dim, 1.0f);
+    };
+    fill_mat(M.emb);
+    for (auto& L : M.layers) {
+        fill_mat(L.qkv);
+        fill_mat(L.o);
+        fill_mat(L.gu);
+        fill_mat(L.down);
+        fill_ones(L.attn_norm);
+        fill_ones(L.ffn_norm);
+    }
+    fill_mat(M.out);
+    fill_ones(M.final_norm);
+    HIP_TRY(hipGetLastError());
+    HIP_TRY(hipStreamSynchronize(M.stream));
+    return api_ok();
+}
+
+rdl_status rdl_llama_reset(rdl_llama* model) {
+    if (!model) return api_fail(RDL_ERR_NULL_POINTER, "NULL model");
+    rdl::LlamaModel& M = model->m;
+    hipLaunchKernelGGL(rdl::set_int_kernel, dim3(1), dim3(64), 0, M.stream, M.pos, 0);
+    HIP_TRY(hipGetLastError());
+    HIP_TRY(hipStreamSynchronize(M.stream));
+    M.host_pos = 0;
+    return api_ok();
+}
+
+rdl_status rdl_llama_position(const rdl_llama* model, size_t* out) {
+    if (!model || !out) return api_fail(RDL_ERR_NULL_POINTER, "NULL argument");
+    *out = model->m.host_pos;
+    return api_ok();
+}
+
+rdl_status rdl_llama_forward(rdl_llama* model, const int32_t* tokens, size_t n, float* logits, size_t logits_len) {
+    if (!model || !tokens || !logits) return api_fail(RDL_ERR_NULL_POINTER, "NULL argument");
+    rdl::LlamaModel& M = model->m;
+    const rdl_llama_config& c = M.cfg;
+    if (n == 0 || n > (size_t)c.max_batch)
+        return api_fail(RDL_ERR_SHAPE_MISMATCH, "%zu tokens: 1 .. max_batch (%d) per call", n, c.max_batch);
+    if (logits_len < (size_t)c.vocab)
+        return api_fail(RDL_ERR_SHAPE_MISMATCH, "logits length %zu < vocab %d", logits_len, c.vocab);
+    if (M.host_pos + n > (size_t)c.max_seq)
+        return api_fail(RDL_ERR_INVALID_DATA, "sequence length %zu exceeds maximum %d (start_pos=%zu)",
+                        M.host_pos + n, c.max_seq, M.host_pos);
+    for (size_t i = 0; i < n; i++)
+        if (tokens[i] < 0 || tokens[i] >= c.vocab)
+            return api_fail(RDL_ERR_INVALID_DATA, "token %d out of bounds for embedding with %d entries",
+                            tokens[i], c.vocab);
+    HIP_TRY(hipMemcpyAsync(M.tokens, tokens, n * 4, hipMemcpyHostToDevice, M.stream));
+    HIP_TRY(M.forward(n));
+    HIP_TRY(hipMemcpyAsync(logits, M.logits, (size_t)c.vocab * 4, hipMemcpyDeviceToHost, M.stream));
+    HIP_TRY(hipStreamSynchronize(M.stream));
+    M.host_pos += n;
+    return api_ok();
+}
+
+rdl_status rdl_llama_generate_greedy(rdl_llama* model, const int32_t* prompt, size_t n_prompt, size_t n_gen,
+                                     int32_t* out_tokens) {
+    if (!model || (!prompt && n_prompt) || (!out_tokens && n_gen))
+        return api_fail(RDL_ERR_NULL_POINTER, "NULL argument");
+    rdl::LlamaModel& M = model->m;
+    const rdl_llama_config& c = M.cfg;
+    if (n_prompt == 0) return api_fail(RDL_ERR_INVALID_DATA, "empty prompt");
+    if (n_gen == 0) return api_ok();
+    // the last sampled token is not fed back: positions used = prompt + n_gen - 1
+    if (M.host_pos + n_prompt + n_gen - 1 > (size_t)c.max_seq)
+        return api_fail(RDL_ERR_INVALID_DATA, "sequence length %zu exceeds maximum %d",
+                        M.host_pos + n_prompt + n_gen - 1, c.max_seq);
+    for (size_t i = 0; i < n_prompt; i++)
+        if (prompt[i] < 0 || prompt[i] >= c.vocab)
+            return api_fail(RDL_ERR_INVALID_DATA, "token %d out of bounds for embedding with %d entries",
+                            prompt[i], c.vocab);
+    hipLaunchKernelGGL(rdl::set_int_kernel, dim3(1), dim3(64), 0, M.stream, M.step, 0);
+    HIP_TRY(hipEventRecord(M.ev[0], M.stream));
+    // prefill in chunks; the last chunk's logits give the first token
+    for (size_t r = 0; r < n_prompt; r += (size_t)c.max_batch) {
+        const size_t mr = std::min(n_prompt - r, (size_t)c.max_batch);
+        HIP_TRY(hipMemcpyAsync(M.tokens, prompt + r, mr * 4, hipMemcpyHostToDevice, M.stream));
+        HIP_TRY(M.forward(mr));
+    }
+    hipLaunchKernelGGL(rdl::argmax_kernel, dim3(1), dim3(rdl::ARGMAX_NT), 0, M.stream, M.logits, c.vocab,
+                       M.tokens, M.out_tokens, M.step);
+    HIP_TRY(hipGetLastError());
+    HIP_TRY(hipEventRecord(M.ev[1], M.stream));
+    if (n_gen > 1) {
+        if (!M.decode_exec) {
+            HIP_TRY(hipStreamBeginCapture(M.stream, hipStreamCaptureModeThreadLocal));
+            const hipError_t ce = M.decode_step();
+            hipGraph_t g = nullptr;
+            const hipError_t ee = hipStreamEndCapture(M.stream, &g);
+            HIP_TRY(ce);
+            HIP_TRY(ee);
+            M.decode_graph = g;
+            HIP_TRY(hipGraphInstantiate(&M.decode_exec, g, nullptr, nullptr, 0));
+        }
+        for (size_t i = 1; i < n_gen; i++) HIP_TRY(hipGraphLaunch(M.decode_exec, M.stream));
+    }
+    HIP_TRY(hipEventRecord(M.ev[2], M.stream));
+    HIP_TRY(hipMemcpyAsync(out_tokens, M.out_tokens, n_gen * 4, hipMemcpyDeviceToHost, M.stream));
+    HIP_TRY(hipStreamSynchronize(M.stream));
+    HIP_TRY(hipEventElapsedTime(&M.prefill_ms, M.ev[0], M.ev[1]));
+    HIP_TRY(hipEventElapsedTime(&M.decode_ms, M.ev[1], M.ev[2]));
+    M.host_pos += n_prompt + n_gen - 1;
+    return api_ok();
+}
+
+rdl_status rdl_llama_last_timing(const rdl_llama* model, float* prefill_ms, float* decode_ms) {
+    if (!model || !prefill_ms || !decode_ms) return api_fail(RDL_ERR_NULL_POINTER, "NULL argument");
+    *prefill_ms = model->m.prefill_ms;
+    *decode_ms = model->m.decode_ms;
+    return api_ok();
+}
+
+rdl_status rdl_llama_rope_tables(const rdl_llama* model, float* cos_out, float* sin_out, size_t len) {
+    if (!model || !cos_out || !sin_out) return api_fail(RDL_ERR_NULL_POINTER, "NULL argument");
+    const rdl::LlamaModel& M = model->m;
+    if (len != M.cos_h.size())
+        return api_fail(RDL_ERR_SHAPE_MISMATCH, "tables hold %zu floats, got %zu", M.cos_h.size(), len);
+    memcpy(cos_out, M.cos_h.data(), len * 4);
+    memcpy(sin_out, M.sin_h.data(), len * 4);
+    return api_ok();
+}
+
+}  // extern "C"

@@ -7,7 +7,23 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "../../include/rdl_quant.h"
+
+// HIP_TRY for functions returning rdl_status: a failing HIP call sets the
+// thread's last-error text and returns RDL_ERR_HIP.
+#define HIP_TRY(expr)                                                                          \
+    do {                                                                                       \
+        hipError_t e_ = (expr);                                                                \
+        if (e_ != hipSuccess)                                                                  \
+            return ::rdl::api_fail(RDL_ERR_HIP, "%s failed: %s", #expr, hipGetErrorString(e_)); \
+    } while (0)
+
 namespace rdl {
+
+// Error reporting shared by the C ABI translation units (capi.hip).
+rdl_status api_fail(rdl_status st, const char* fmt, ...);
+rdl_status api_ok();
+rdl_status api_require_device();
 
 // GGUF block geometry (rustml/quant/main/src/api/types.rs:1-17,
 // rustml/gguf/main/src/api/types.rs:54-76).

@@ -301,7 +301,11 @@ def quantize_row_q8_0_dev(x_ptr, n, out_ptr, scales_ptr, stream=0):
 
 
 def declared_symbols():
-    """Every function name include/rdl_quant.h declares."""
-    text = open(HEADER_PATH).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(rdl_[a-z0-9_]+)\s*\(", text)))
+    """Every function name the headers in include/ declare."""
+    import glob
+
+    names = set()
+    for path in sorted(glob.glob(os.path.join(os.path.dirname(HEADER_PATH), "*.h"))):
+        text = re.sub(r"/\*.*?\*/", "", open(path).read(), flags=re.S)
+        names.update(re.findall(r"\b(rdl_[a-z0-9_]+)\s*\(", text))
+    return sorted(names)

@@ -1,0 +1,136 @@
+"""ctypes binding of the device decoder in librdlquant.so (include/rdl_llama.h).
+
+LlamaModel mirrors the rustml decode path for Q4_0 Llama-style models:
+forward_with_cache (LlmModel::forward_with_cache_pass + KVCache::advance,
+rustml/nlp/main/src/core/model.rs:890-937), prefill / decode_step
+(Generator, rustml/nlp/main/src/core/generator.rs:212-240) and greedy
+generation with sampling::argmax (rustml/nlp/main/src/core/sampling.rs:8-18).
+Everything runs on the GPU; there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import _decl, _i32, _p, _sz, check, lib
+
+TOKEN_EMBEDDING, ATTN_NORM, WQ, WK, WV, WO, FFN_NORM, W_GATE, W_UP, W_DOWN, FINAL_NORM, OUTPUT = range(12)
+
+
+class _Config(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in ("dim", "n_layers", "n_heads", "n_kv_heads", "head_dim", "ffn_dim",
+                                           "vocab", "max_seq")] + \
+               [("norm_eps", C.c_float), ("rope_theta", C.c_float), ("kv_f16", C.c_int32),
+                ("max_batch", C.c_int32)]
+
+
+_decl("rdl_llama_create", _i32, C.POINTER(_Config), C.POINTER(_p))
+_decl("rdl_llama_free", _i32, _p)
+_decl("rdl_llama_set_weight", _i32, _p, _i32, _i32, _p, _sz)
+_decl("rdl_llama_init_random", _i32, _p, C.c_uint64)
+_decl("rdl_llama_reset", _i32, _p)
+_decl("rdl_llama_position", _i32, _p, C.POINTER(_sz))
+_decl("rdl_llama_forward", _i32, _p, C.POINTER(C.c_int32), _sz, C.POINTER(C.c_float), _sz)
+_decl("rdl_llama_generate_greedy", _i32, _p, C.POINTER(C.c_int32), _sz, _sz, C.POINTER(C.c_int32))
+_decl("rdl_llama_last_timing", _i32, _p, C.POINTER(C.c_float), C.POINTER(C.c_float))
+_decl("rdl_llama_rope_tables", _i32, _p, C.POINTER(C.c_float), C.POINTER(C.c_float), _sz)
+
+
+@dataclass
+class LlamaConfig:
+    """The ModelConfig fields of the Llama path (rustml/nlp/main/src/api/types.rs:186)."""
+    dim: int = 4096
+    n_layers: int = 32
+    n_heads: int = 32
+    n_kv_heads: int = 8
+    head_dim: int = 128
+    ffn_dim: int = 14336
+    vocab: int = 32000
+    max_seq: int = 2048
+    norm_eps: float = 1e-5
+    rope_theta: float = 10000.0
+    kv_f16: bool = True
+    max_batch: int = 128
+
+    def _c(self):
+        return _Config(self.dim, self.n_layers, self.n_heads, self.n_kv_heads, self.head_dim, self.ffn_dim,
+                       self.vocab, self.max_seq, self.norm_eps, self.rope_theta, int(self.kv_f16),
+                       self.max_batch)
+
+
+def _i32_array(tokens):
+    return np.ascontiguousarray(np.asarray(tokens, dtype=np.int32).reshape(-1))
+
+
+class LlamaModel:
+    """Q4_0 Llama-style decoder resident on the current GPU."""
+
+    def __init__(self, config: LlamaConfig):
+        self.config = config
+        h = _p()
+        cfg = config._c()
+        check(lib.rdl_llama_create(C.byref(cfg), C.byref(h)))
+        self._h = h
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib.rdl_llama_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+    def set_weight(self, slot: int, layer: int, data: np.ndarray) -> None:
+        """Q4_0 GGUF bytes (uint8) for matrices and the embedding, f32 for norms."""
+        a = np.ascontiguousarray(data)
+        check(lib.rdl_llama_set_weight(self._h, slot, layer, a.ctypes.data, a.nbytes))
+
+    def init_random(self, seed: int) -> None:
+        check(lib.rdl_llama_init_random(self._h, C.c_uint64(seed & (2**64 - 1))))
+
+    def reset(self) -> None:
+        check(lib.rdl_llama_reset(self._h))
+
+    @property
+    def position(self) -> int:
+        out = _sz()
+        check(lib.rdl_llama_position(self._h, C.byref(out)))
+        return int(out.value)
+
+    def forward_with_cache(self, tokens) -> np.ndarray:
+        """Logits of the last of `tokens` (vocab floats); the cache advances by len(tokens)."""
+        t = _i32_array(tokens)
+        logits = np.empty(self.config.vocab, dtype=np.float32)
+        check(lib.rdl_llama_forward(self._h, t.ctypes.data_as(C.POINTER(C.c_int32)), t.size,
+                                    logits.ctypes.data_as(C.POINTER(C.c_float)), logits.size))
+        return logits
+
+    def prefill(self, tokens) -> np.ndarray:
+        return self.forward_with_cache(tokens)
+
+    def decode_step(self, token: int) -> np.ndarray:
+        return self.forward_with_cache([token])
+
+    def generate_greedy(self, prompt, n_gen: int) -> np.ndarray:
+        """n_gen argmax tokens after the prompt (prefill + n_gen - 1 graph-replayed steps)."""
+        p = _i32_array(prompt)
+        out = np.empty(n_gen, dtype=np.int32)
+        check(lib.rdl_llama_generate_greedy(self._h, p.ctypes.data_as(C.POINTER(C.c_int32)), p.size, n_gen,
+                                            out.ctypes.data_as(C.POINTER(C.c_int32))))
+        return out
+
+    def last_timing(self):
+        """(prefill_ms, decode_ms) of the last generate_greedy call, device time."""
+        a, b = C.c_float(), C.c_float()
+        check(lib.rdl_llama_last_timing(self._h, C.byref(a), C.byref(b)))
+        return float(a.value), float(b.value)
+
+    def rope_tables(self):
+        n = self.config.max_seq * (self.config.head_dim // 2)
+        c = np.empty(n, np.float32)
+        s = np.empty(n, np.float32)
+        check(lib.rdl_llama_rope_tables(self._h, c.ctypes.data_as(C.POINTER(C.c_float)),
+                                        s.ctypes.data_as(C.POINTER(C.c_float)), n))
+        return c.reshape(self.config.max_seq, -1), s.reshape(self.config.max_seq, -1)

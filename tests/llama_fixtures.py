@@ -1,0 +1,47 @@
+"""Seeded tiny Llama-style models for the decoder tests (CPU oracle and GPU)."""
+import numpy as np
+
+from rdlquant import synth
+
+
+def tiny_config(**kw):
+    from rdlquant.llama import LlamaConfig
+    base = dict(dim=256, n_layers=2, n_heads=4, n_kv_heads=2, head_dim=64, ffn_dim=512, vocab=320,
+                max_seq=64, norm_eps=1e-5, rope_theta=10000.0, kv_f16=False, max_batch=16)
+    base.update(kw)
+    return LlamaConfig(**base)
+
+
+def tiny_weights(cfg, seed=1234):
+    """(gpu_slots, oracle_weights): the same seeded bytes for both sides."""
+    from rdlquant import llama as L
+    from oracle import oracle as orc
+    rng = np.random.default_rng(seed)
+    q, kv = cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim
+    slots, ref = [], {}
+    s = seed
+
+    def q4(n, k):
+        nonlocal s
+        s += 1
+        return synth.q4_0_weights(n, k, s)
+
+    def norm():
+        return (1.0 + 0.1 * rng.standard_normal(cfg.dim)).astype(np.float32)
+
+    emb = q4(cfg.vocab, cfg.dim)
+    slots.append((L.TOKEN_EMBEDDING, 0, emb))
+    ref["emb_f32"] = orc.to_f32("q4_0", emb, cfg.vocab * cfg.dim).reshape(cfg.vocab, cfg.dim)
+    for layer in range(cfg.n_layers):
+        for slot, name, arr in ((L.ATTN_NORM, "attn_norm", norm()), (L.WQ, "wq", q4(q, cfg.dim)),
+                                (L.WK, "wk", q4(kv, cfg.dim)), (L.WV, "wv", q4(kv, cfg.dim)),
+                                (L.WO, "wo", q4(cfg.dim, q)), (L.FFN_NORM, "ffn_norm", norm()),
+                                (L.W_GATE, "w_gate", q4(cfg.ffn_dim, cfg.dim)),
+                                (L.W_UP, "w_up", q4(cfg.ffn_dim, cfg.dim)),
+                                (L.W_DOWN, "w_down", q4(cfg.dim, cfg.ffn_dim))):
+            slots.append((slot, layer, arr))
+            ref[(name, layer)] = arr
+    fin, out = norm(), q4(cfg.vocab, cfg.dim)
+    slots += [(L.FINAL_NORM, 0, fin), (L.OUTPUT, 0, out)]
+    ref["final_norm"], ref["output"] = fin, out
+    return slots, ref
