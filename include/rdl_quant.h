@@ -177,6 +177,23 @@ rdl_status rdl_prepare_activations_dev(const float* x_dev, size_t m, size_t k, i
 rdl_status rdl_linear_prepared_dev(const rdl_weight* w, const void* rec_dev, size_t m,
                                    float* y_dev, int32_t mode, void* stream);
 
+/* Fused decode-loop Linear, Q4_0 weights, float mode (the GEMV of
+ * matmul_f32_q4, quantize.rs:265-320), m <= 4 rows, in_features / 32 even:
+ *   prologue RDL_PROLOGUE_NONE:    x as given;
+ *   prologue RDL_PROLOGUE_RMSNORM: rms_norm(x, gamma, eps) per row first
+ *     (Tensor::rms_norm, rustml/core/main/src/core/tensor/ops.rs:688-751);
+ *   prologue RDL_PROLOGUE_SWIGLU:  silu(x[:, :k]) * x[:, k:2k] first, each x
+ *     row holding [gate | up] (FeedForward::forward, feed_forward.rs:138-150);
+ *   residual != 0: y += result (Tensor::add_inplace, transformer_block.rs:333,352),
+ *     y read before it is written; otherwise y = result.
+ * x_stride = floats between x rows (>= k, >= 2k for SWIGLU; multiple of 4;
+ * x 16-byte aligned).  No counterpart in the reference: there these are
+ * separate tensor operations; one launch, no scratch memory. */
+enum { RDL_PROLOGUE_NONE = 0, RDL_PROLOGUE_RMSNORM = 1, RDL_PROLOGUE_SWIGLU = 2 };
+rdl_status rdl_linear_fused_dev(const rdl_weight* w, const float* x_dev, size_t x_stride, size_t m,
+                                float* y_dev, int32_t prologue, const float* gamma_dev, float eps,
+                                int32_t residual, void* stream);
+
 /* quantize_row_q8_0 on device: x_dev f32 [n] -> out_dev (n/32)*34 bytes and
  * scales_dev f32 [n/32] (scales_dev may be NULL). */
 rdl_status rdl_quantize_row_q8_0_dev(const float* x_dev, size_t n, uint8_t* out_dev,

@@ -74,6 +74,21 @@ __device__ __forceinline__ void wait_prep_x() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// The compiler takes an asm load's result as ready right after the load and
+// may move arithmetic on it above the explicit wait.  Passing each result
+// through an empty volatile asm placed after the wait makes every use depend
+// on a value defined after it.
+template <int PI>
+__device__ __forceinline__ void after_wait(f32x4 (&v)[PI]) {
+#pragma unroll
+    for (int j = 0; j < PI; j++) asm volatile("" : "+v"(v[j]));
+}
+template <int PI>
+__device__ __forceinline__ void after_wait(f32x4 (&v)[PI][2]) {
+#pragma unroll
+    for (int j = 0; j < PI; j++) asm volatile("" : "+v"(v[j][0]), "+v"(v[j][1]));
+}
+
 template <int NW, int PI>
 __device__ void prep_float_lds(const f32x4 (&xv)[PI], int nb, int* __restrict__ lds) {
     constexpr int NT = NW * 64;
@@ -180,28 +195,88 @@ __device__ __forceinline__ void nib_levels(uint32_t P, uint32_t Q, uint32_t& lo,
     hi = ((P >> 4) & 0x0F0F0F0Fu) | (Q & 0xF0F0F0F0u);
 }
 
-template <int NW, int PI>
-__device__ __forceinline__ void load_prep_x4(const float* __restrict__ x, int nb, f32x4 (&xv)[PI][2]) {
+// Prologues applied to x as the prep reads it (decoder fusion):
+//   PRO_RMSNORM: x_j * (1 / sqrt(sum(x^2) / K + eps)) * g_j (ops.rs:688-751),
+//                aux = g, the sum formed by the workgroup;
+//   PRO_SWIGLU:  silu(x_j) * x_{K + j}, silu(v) = v * (1 / (1 + exp(-v)))
+//                (feed_forward.rs:138-150, ops.rs:441-446), aux = x + K.
+constexpr int PRO_NONE = 0, PRO_RMSNORM = 1, PRO_SWIGLU = 2;
+
+// Fusion arguments of one launch (unused fields are ignored).
+struct Fuse {
+    const float* g;  // RMSNorm weights
+    float eps;
+    int xstride;     // floats between activation rows
+};
+
+template <int NW, int PI, int PRO = PRO_NONE>
+__device__ __forceinline__ void load_prep_x4(const float* __restrict__ x, const float* __restrict__ aux, int nb,
+                                             f32x4 (&xv)[PI][2], f32x4 (&av)[PI][2]) {
     constexpr int NT = NW * 64;
 #pragma unroll
     for (int j = 0; j < PI; j++) {
         const int p = min((int)threadIdx.x + j * NT, nb * 4 - 1);
-        const float* ptr = x + (p >> 2) * 32 + (p & 3) * 4;
+        const int o = (p >> 2) * 32 + (p & 3) * 4;
+        const float* ptr = x + o;
         asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(xv[j][0]) : "v"(ptr) : "memory");
         asm volatile("global_load_dwordx4 %0, %1, off offset:64" : "=v"(xv[j][1]) : "v"(ptr) : "memory");
+        if constexpr (PRO != PRO_NONE) {
+            const float* aptr = aux + o;
+            asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(av[j][0]) : "v"(aptr) : "memory");
+            asm volatile("global_load_dwordx4 %0, %1, off offset:64" : "=v"(av[j][1]) : "v"(aptr) : "memory");
+        }
     }
 }
 
-template <int NW, int PI>
-__device__ void prep_float4_lds(const f32x4 (&xv)[PI][2], int nb, int* __restrict__ lds) {
+template <int NW, int PI, int PRO = PRO_NONE>
+__device__ void prep_float4_lds(const f32x4 (&xv)[PI][2], const f32x4 (&av)[PI][2], float eps, int nb,
+                                int* __restrict__ lds) {
     constexpr int NT = NW * 64;
+    float inv = 1.0f;
+    if constexpr (PRO == PRO_RMSNORM) {
+        // sum of squares over the row: this thread's elements, then the
+        // workgroup (fixed reduction tree: every workgroup gets the same bits)
+        float ss = 0.0f;
+#pragma unroll
+        for (int j = 0; j < PI; j++) {
+            if ((int)threadIdx.x + j * NT < nb * 4) {
+                const f32x4 a = xv[j][0], b = xv[j][1];
+                ss += ((a.x * a.x + a.y * a.y) + (a.z * a.z + a.w * a.w)) +
+                      ((b.x * b.x + b.y * b.y) + (b.z * b.z + b.w * b.w));
+            }
+        }
+        ss = sum8_f32(ss);
+        ss += dpp_f32<DPP_ROW_MIRROR>(ss);
+        ss += __shfl_xor(ss, 16);
+        ss += __shfl_xor(ss, 32);
+        float* red = reinterpret_cast<float*>(lds + 7 * 4 * nb);  // group 7 is free in int4 records
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+        __syncthreads();
+        float tot = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) tot += red[w];
+        inv = 1.0f / sqrtf(tot / (float)(nb * 32) + eps);
+    }
 #pragma unroll
     for (int j = 0; j < PI; j++) {
         const int p = threadIdx.x + j * NT;
         if (j * NT >= nb * 4) break;  // uniform
         const int c = p >> 2, k = p & 3;
         const f32x4 va = xv[j][0], vb = xv[j][1];
-        const float v[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};
+        float v[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};
+        if constexpr (PRO != PRO_NONE) {
+            const f32x4 ga = av[j][0], gb = av[j][1];
+            const float a[8] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w};
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                if constexpr (PRO == PRO_RMSNORM) {
+                    v[i] = (v[i] * inv) * a[i];
+                } else {
+                    const float sig = 1.0f / (1.0f + expf(-v[i]));
+                    v[i] = (v[i] * sig) * a[i];
+                }
+            }
+        }
         bool bad = false;
         float amax = 0.0f;
 #pragma unroll
@@ -467,11 +542,13 @@ __device__ __forceinline__ float block_dot_i4(const uint32_t (&w)[5], uint32_t s
 // its instructions in order and the memory pipeline accepts only so many
 // loads per CU, so interleaving load issue with compute is what lets the dot
 // products overlap the weight stream.
-template <int WT, bool NATIVE, int R, int CPL, bool NB_EVEN, int NW>
+// PRO: prologue on x (PRO_NONE / PRO_RMSNORM / PRO_SWIGLU, int4 records
+// only); RES: y += W x in place (the residual add of transformer_block.rs:333,352).
+template <int WT, bool NATIVE, int R, int CPL, bool NB_EVEN, int NW, int PRO = PRO_NONE, bool RES = false>
 __global__ __launch_bounds__(NW * 64) void gemv_fused_kernel(const uint8_t* __restrict__ W, int n,
                                                         int nb, int rpw,
                                                         const float* __restrict__ X,
-                                                        float* __restrict__ Y) {
+                                                        float* __restrict__ Y, Fuse fz) {
     extern __shared__ i32x4 lds4[];
     constexpr int BYTES = Geo<WT>::BYTES, WORDS = Geo<WT>::WORDS;
     constexpr int LPB = (WORDS == 9) ? 3 : 2;    // load instructions per block
@@ -491,7 +568,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_fused_kernel(const uint8_t* __re
     const int wv = threadIdx.x >> 6;
     const int r0 = blockIdx.x * rpw;
     const int rend = min(n, r0 + rpw);
-    const float* x = X + (size_t)blockIdx.y * nb * 32;
+    static_assert(PRO == PRO_NONE || I4, "prologues run on the int4-record prep");
+    const float* x = X + (size_t)blockIdx.y * fz.xstride;
     float* y = Y + (size_t)blockIdx.y * n;
     const uint32_t row_bytes = (uint32_t)nb * BYTES;
     const uint32_t wbytes = (uint32_t)n * row_bytes;
@@ -514,18 +592,22 @@ __global__ __launch_bounds__(NW * 64) void gemv_fused_kernel(const uint8_t* __re
 
     // ---- x for the prep first, then the first PF blocks ----
     if constexpr (I4) {
-        f32x4 xv[PI][2];
-        load_prep_x4<NW, PI>(x, nb, xv);
+        f32x4 xv[PI][2], av[PI][2];
+        const float* aux = (PRO == PRO_RMSNORM) ? fz.g : x + nb * 32;
+        load_prep_x4<NW, PI, PRO>(x, aux, nb, xv, av);
 #pragma unroll
         for (int b = 0; b < P0; b++) issue(b);
         wait_prep_x<P0 * LPB>();
-        prep_float4_lds<NW, PI>(xv, nb, reinterpret_cast<int*>(lds4));
+        after_wait<PI>(xv);
+        if constexpr (PRO != PRO_NONE) after_wait<PI>(av);
+        prep_float4_lds<NW, PI, PRO>(xv, av, fz.eps, nb, reinterpret_cast<int*>(lds4));
     } else {
         f32x4 xv[PI];
         load_prep_x<NW, PI>(x, nb, xv);
 #pragma unroll
         for (int b = 0; b < P0; b++) issue(b);
         wait_prep_x<P0 * LPB>();
+        after_wait<PI>(xv);
         if constexpr (NATIVE)
             prep_native_lds<NW, PI>(xv, nb, reinterpret_cast<int*>(lds4));
         else
@@ -584,7 +666,12 @@ __global__ __launch_bounds__(NW * 64) void gemv_fused_kernel(const uint8_t* __re
     constexpr int SH = reduce_span_log2<R>();
     if ((lane & ((1 << SH) - 1)) == 0) {
         const int row = r0 + wv + (lane >> SH) * NW;
-        if (row < rend) y[row] = s;
+        if (row < rend) {
+            if constexpr (RES)
+                y[row] = s + y[row];
+            else
+                y[row] = s;
+        }
     }
 }
 
@@ -652,6 +739,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_q4k_fused_kernel(const uint8_t* 
         }
     }
     wait_prep_x<R * UPL * 3>();  // header + two 16-byte nibble loads per unit
+    after_wait<PI>(xv);
     prep_float_lds<NW, PI>(xv, nb, reinterpret_cast<int*>(lds4));
     __syncthreads();
     if (r0 + wv >= rend) return;
@@ -745,28 +833,29 @@ Cfg pick_cfg(int n, int nw, int rmax, int wg_per_cu) {
     return Cfg{nw, rpw, r};
 }
 
-template <int WT, bool NATIVE, int CPL, bool EVEN, int NW>
+template <int WT, bool NATIVE, int CPL, bool EVEN, int NW, int PRO = PRO_NONE, bool RES = false>
 void launch_nw(const uint8_t* w, int n, int nb, const float* x, size_t m, float* y, hipStream_t s,
-               const Cfg& c, size_t lds) {
+               const Cfg& c, size_t lds, const Fuse& fz) {
     const dim3 grid((unsigned)((n + c.rpw - 1) / c.rpw), (unsigned)m), block(NW * 64);
     constexpr int RMAX = 8 / CPL;
     const int rpw = c.rpw;
     if (c.r <= 1 || RMAX == 1)
-        launch_kernel((gemv_fused_kernel<WT, NATIVE, 1, CPL, EVEN, NW>), grid, block, lds, s, w, n, nb, rpw, x, y);
+        launch_kernel((gemv_fused_kernel<WT, NATIVE, 1, CPL, EVEN, NW, PRO, RES>), grid, block, lds, s, w, n, nb, rpw, x, y, fz);
     else if (c.r <= 2 || RMAX == 2)
-        launch_kernel((gemv_fused_kernel<WT, NATIVE, (RMAX >= 2 ? 2 : 1), CPL, EVEN, NW>), grid, block, lds, s, w, n, nb, rpw, x, y);
+        launch_kernel((gemv_fused_kernel<WT, NATIVE, (RMAX >= 2 ? 2 : 1), CPL, EVEN, NW, PRO, RES>), grid, block, lds, s, w, n, nb, rpw, x, y, fz);
     else if (c.r <= 3)
-        launch_kernel((gemv_fused_kernel<WT, NATIVE, (RMAX >= 4 ? 3 : 1), CPL, EVEN, NW>), grid, block, lds, s, w, n, nb, rpw, x, y);
+        launch_kernel((gemv_fused_kernel<WT, NATIVE, (RMAX >= 4 ? 3 : 1), CPL, EVEN, NW, PRO, RES>), grid, block, lds, s, w, n, nb, rpw, x, y, fz);
     else
-        launch_kernel((gemv_fused_kernel<WT, NATIVE, (RMAX >= 4 ? 4 : 1), CPL, EVEN, NW>), grid, block, lds, s, w, n, nb, rpw, x, y);
+        launch_kernel((gemv_fused_kernel<WT, NATIVE, (RMAX >= 4 ? 4 : 1), CPL, EVEN, NW, PRO, RES>), grid, block, lds, s, w, n, nb, rpw, x, y, fz);
 }
 
 template <int WT, bool NATIVE, int CPL, bool EVEN>
 void launch_even(const uint8_t* w, int n, int nb, const float* x, size_t m, float* y,
                  hipStream_t s, const Cfg& c, size_t lds) {
-    if (c.nw == 4) launch_nw<WT, NATIVE, CPL, EVEN, 4>(w, n, nb, x, m, y, s, c, lds);
-    else if (c.nw == 8) launch_nw<WT, NATIVE, CPL, EVEN, 8>(w, n, nb, x, m, y, s, c, lds);
-    else launch_nw<WT, NATIVE, CPL, EVEN, 16>(w, n, nb, x, m, y, s, c, lds);
+    const Fuse fz{nullptr, 0.0f, nb * 32};
+    if (c.nw == 4) launch_nw<WT, NATIVE, CPL, EVEN, 4>(w, n, nb, x, m, y, s, c, lds, fz);
+    else if (c.nw == 8) launch_nw<WT, NATIVE, CPL, EVEN, 8>(w, n, nb, x, m, y, s, c, lds, fz);
+    else launch_nw<WT, NATIVE, CPL, EVEN, 16>(w, n, nb, x, m, y, s, c, lds, fz);
 }
 
 template <int WT, bool NATIVE, int CPL>
@@ -810,7 +899,45 @@ void launch_q4k_nw(const uint8_t* w, int n, int nsb, const float* x, size_t m, f
     }
 }
 
+// Decoder fusion: Q4_0 float mode, 8-wave workgroups (two per CU), nb even.
+template <int PRO, bool RES>
+void launch_q4_0_fused_ex(const uint8_t* w, int n, int nb, const float* x, size_t m, float* y,
+                          hipStream_t s, size_t lds, const Fuse& fz) {
+    const int cpl = cpl_for(nb);
+    const Cfg c = pick_cfg(n, 8, 8 / cpl, 2);
+    constexpr int Q = (int)WType::Q4_0;
+    switch (cpl) {
+        case 2: launch_nw<Q, false, 2, true, 8, PRO, RES>(w, n, nb, x, m, y, s, c, lds, fz); break;
+        case 4: launch_nw<Q, false, 4, true, 8, PRO, RES>(w, n, nb, x, m, y, s, c, lds, fz); break;
+        default: launch_nw<Q, false, 8, true, 8, PRO, RES>(w, n, nb, x, m, y, s, c, lds, fz); break;
+    }
+}
+
 }  // namespace
+
+hipError_t launch_gemv_q4_0_fused_ex(const uint8_t* w, size_t n, size_t k, const float* x, size_t xstride,
+                                     size_t m, float* y, int prologue, const float* g, float eps,
+                                     bool residual, hipStream_t s) {
+    if (n == 0 || m == 0) return hipSuccess;
+    const int nb = (int)(k / QK);
+    if (nb == 0 || (nb & 1) || k > fused_max_k(WType::Q4_0) || ((uintptr_t)x & 15) || (xstride & 3) ||
+        (uint64_t)n * nb * Q4_0_BYTES > FUSED_MAX_WEIGHT_BYTES || m > 4)
+        return hipErrorInvalidValue;
+    const Fuse fz{g, eps, (int)xstride};
+    const size_t lds = (size_t)8 * 16 * nb;
+    const int ni = (int)n;
+    if (prologue == PRO_RMSNORM && !residual)
+        launch_q4_0_fused_ex<PRO_RMSNORM, false>(w, ni, nb, x, m, y, s, lds, fz);
+    else if (prologue == PRO_NONE && residual)
+        launch_q4_0_fused_ex<PRO_NONE, true>(w, ni, nb, x, m, y, s, lds, fz);
+    else if (prologue == PRO_SWIGLU && residual)
+        launch_q4_0_fused_ex<PRO_SWIGLU, true>(w, ni, nb, x, m, y, s, lds, fz);
+    else if (prologue == PRO_NONE && !residual)
+        launch_q4_0_fused_ex<PRO_NONE, false>(w, ni, nb, x, m, y, s, lds, fz);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
 
 // Largest K the fused kernels take (records for all of K live in LDS and a
 // lane holds at most 8 columns of blocks in registers).

@@ -67,14 +67,41 @@ __device__ __forceinline__ float block_max(float v, float* red) {
 __global__ __launch_bounds__(NT) void rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ g,
                                                      int d, float eps, float* __restrict__ out) {
     __shared__ float red[NT / 64];
-    const float* xr = x + (size_t)blockIdx.x * d;
-    float* o = out + (size_t)blockIdx.x * d;
+    // d % 4 == 0: float4 per thread, RN of them issued before any use
+    constexpr int RN = 8;
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    const f4* xr = reinterpret_cast<const f4*>(x + (size_t)blockIdx.x * d);
+    const f4* g4 = reinterpret_cast<const f4*>(g);
+    f4* o = reinterpret_cast<f4*>(out + (size_t)blockIdx.x * d);
+    const int d4 = d / 4;
     float ss = 0.0f;
-    for (int c = threadIdx.x; c < d; c += NT) ss += xr[c] * xr[c];
+    for (int c0 = 0; c0 < d4; c0 += RN * NT) {
+        f4 v[RN];
+#pragma unroll
+        for (int r = 0; r < RN; r++) {
+            const int c = c0 + r * NT + threadIdx.x;
+            v[r] = (c < d4) ? xr[c] : f4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+#pragma unroll
+        for (int r = 0; r < RN; r++) ss += (v[r].x * v[r].x + v[r].y * v[r].y) + (v[r].z * v[r].z + v[r].w * v[r].w);
+    }
     ss = block_sum(ss, red);
     const float rms = sqrtf(ss / (float)d + eps);
     const float inv = 1.0f / rms;
-    for (int c = threadIdx.x; c < d; c += NT) o[c] = (xr[c] * inv) * g[c];
+    for (int c0 = 0; c0 < d4; c0 += RN * NT) {
+        f4 v[RN], gv[RN];
+#pragma unroll
+        for (int r = 0; r < RN; r++) {
+            const int c = c0 + r * NT + threadIdx.x;
+            v[r] = (c < d4) ? xr[c] : f4{0.0f, 0.0f, 0.0f, 0.0f};
+            gv[r] = (c < d4) ? g4[c] : f4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+#pragma unroll
+        for (int r = 0; r < RN; r++) {
+            const int c = c0 + r * NT + threadIdx.x;
+            if (c < d4) o[c] = (v[r] * inv) * gv[r];
+        }
+    }
 }
 
 // RoPE (half-split pairs (i, i + hd/2), rope.rs:134-200) of q and k at
@@ -110,59 +137,97 @@ __global__ void rope_kv_kernel(float* __restrict__ qkv, int qkv_dim, const int* 
 
 // Attention of query row s (position pos + s) and head h over the cached keys
 // 0 .. pos + s (the causal mask of attention.rs:424-433 keeps exactly these):
-// scores q.k / sqrt(hd), softmax (max-subtracted, ops.rs:582-628), then the
-// probability-weighted sum of the values.  One workgroup per (head, row).
+// scores q.k / sqrt(hd), max-subtracted softmax (ops.rs:582-628), then the
+// probability-weighted sum of the values.  Split over the keys in chunks of
+// ATT_CHUNK: one wave per (head, row, chunk) forms the chunk's scores (one
+// key per lane), its max m_c, sum l_c = sum exp(score - m_c) and the
+// unnormalised context o_c = sum exp(score - m_c) v; attention_combine_kernel
+// then forms (sum_c exp(m_c - M) o_c) / (sum_c exp(m_c - M) l_c), M = max m_c.
+// Chunks past the row's length exit at once, so a launch sized for the cache
+// capacity serves every position (the captured decode graph).
+constexpr int ATT_CHUNK = 64;
+
 template <typename KV>
-__global__ __launch_bounds__(NT) void attention_kernel(const float* __restrict__ qkv, int qkv_dim,
-                                                       const int* __restrict__ pos_dev,
-                                                       const KV* __restrict__ kc,
-                                                       const KV* __restrict__ vc, int max_seq,
-                                                       int n_heads, int n_kv, int hd, float scale,
-                                                       float* __restrict__ out) {
-    extern __shared__ float sm[];  // q[hd] | part[4][hd] | scores[t]
-    __shared__ float red[NT / 64];
-    const int h = blockIdx.x, s = blockIdx.y;
-    const int kvh = h / (n_heads / n_kv);
+__global__ __launch_bounds__(64) void attention_chunk_kernel(const float* __restrict__ qkv, int qkv_dim,
+                                                             const int* __restrict__ pos_dev,
+                                                             const KV* __restrict__ kc,
+                                                             const KV* __restrict__ vc, int max_seq,
+                                                             int n_heads, int n_kv, int hd, float scale,
+                                                             float* __restrict__ part, int nchunk) {
+    extern __shared__ float qs[];
+    const int h = blockIdx.x, s = blockIdx.y, c = blockIdx.z, lane = threadIdx.x;
     const int t = *pos_dev + s + 1;
-    float* qs = sm;
-    float* part = sm + hd;
-    float* sc = part + 4 * hd;
+    const int p0 = c * ATT_CHUNK;
+    if (p0 >= t) return;  // whole wave
+    const int kvh = h / (n_heads / n_kv);
     const float* q = qkv + (size_t)s * qkv_dim + h * hd;
-    for (int d = threadIdx.x; d < hd; d += NT) qs[d] = q[d];
+    for (int d = lane; d < hd; d += 64) qs[d] = q[d];
     __syncthreads();
-    const KV* kbase = kc + (size_t)kvh * max_seq * hd;
-    for (int p = threadIdx.x; p < t; p += NT) {
-        const KV* kr = kbase + (size_t)p * hd;
-        float acc = 0.0f;
-        for (int d = 0; d < hd; d++) acc += qs[d] * (float)kr[d];
-        sc[p] = acc / scale;
+    const int p = p0 + lane;
+    const bool valid = p < t;
+    // score of key p: 16-byte loads of the key row
+    const KV* kr = kc + ((size_t)kvh * max_seq + (valid ? p : p0)) * hd;
+    float acc = 0.0f;
+    constexpr int V = 16 / sizeof(KV);
+    for (int d = 0; d < hd; d += V) {
+        typedef KV kvv __attribute__((ext_vector_type(V)));
+        const kvv kv = *reinterpret_cast<const kvv*>(kr + d);
+#pragma unroll
+        for (int i = 0; i < V; i++) acc += qs[d + i] * (float)kv[i];
     }
-    __syncthreads();
-    float mx = -__builtin_inff();
-    for (int p = threadIdx.x; p < t; p += NT) mx = fmaxf(mx, sc[p]);
-    mx = block_max(mx, red);
-    float sum = 0.0f;
-    for (int p = threadIdx.x; p < t; p += NT) {
-        const float e = expf(sc[p] - mx);
-        sc[p] = e;
-        sum += e;
+    const float sc = valid ? acc / scale : -__builtin_inff();
+    const float mx = wave_max(sc);
+    const float e = valid ? expf(sc - mx) : 0.0f;
+    const float l = wave_sum(e);
+    // context: lane owns dims 2 lane, 2 lane + 1 of each 128-dim slice
+    const KV* vb = vc + (size_t)kvh * max_seq * hd;
+    const int nvalid = min(ATT_CHUNK, t - p0);
+    float* po = part + (((size_t)s * n_heads + h) * nchunk + c) * (hd + 2);
+    for (int d0 = 0; d0 < hd; d0 += 128) {
+        const int d = d0 + 2 * lane;
+        float o0 = 0.0f, o1 = 0.0f;
+        if (d < hd) {
+            // branch-free so that all 64 row loads are in flight together: a
+            // key past the row's length re-reads the last valid row with weight 0
+#pragma unroll
+            for (int j = 0; j < ATT_CHUNK; j++) {
+                const float ej = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e), j));
+                typedef KV kv2 __attribute__((ext_vector_type(2)));
+                const int pj = p0 + min(j, nvalid - 1);
+                const kv2 v2 = *reinterpret_cast<const kv2*>(vb + (size_t)pj * hd + d);
+                o0 += ej * (float)v2[0];
+                o1 += ej * (float)v2[1];
+            }
+            po[2 + d] = o0;
+            po[2 + d + 1] = o1;
+        }
     }
-    sum = block_sum(sum, red);
-    for (int p = threadIdx.x; p < t; p += NT) sc[p] = sc[p] / sum;
-    __syncthreads();
-    // context: wave w takes positions w, w + 4, ...; lane l dims l, l + 64, ...
-    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const KV* vbase = vc + (size_t)kvh * max_seq * hd;
-    for (int d0 = 0; d0 < hd; d0 += 64) {
-        const int d = d0 + lane;
-        float acc = 0.0f;
-        if (d < hd)
-            for (int p = w; p < t; p += 4) acc += sc[p] * (float)vbase[(size_t)p * hd + d];
-        if (d < hd) part[w * hd + d] = acc;
+    if (lane == 0) {
+        po[0] = mx;
+        po[1] = l;
     }
-    __syncthreads();
+}
+
+__global__ __launch_bounds__(128) void attention_combine_kernel(const float* __restrict__ part,
+                                                                const int* __restrict__ pos_dev, int n_heads,
+                                                                int hd, int nchunk, float* __restrict__ out) {
+    const int h = blockIdx.x, s = blockIdx.y;
+    const int t = *pos_dev + s + 1;
+    const int nc = (t + ATT_CHUNK - 1) / ATT_CHUNK;
+    const float* pb = part + ((size_t)s * n_heads + h) * nchunk * (hd + 2);
+    float M = -__builtin_inff();
+    for (int c = 0; c < nc; c++) M = fmaxf(M, pb[(size_t)c * (hd + 2)]);
+    float L = 0.0f;
+    for (int c = 0; c < nc; c++) L += pb[(size_t)c * (hd + 2) + 1] * expf(pb[(size_t)c * (hd + 2)] - M);
     float* o = out + (size_t)s * n_heads * hd + h * hd;
-    for (int d = threadIdx.x; d < hd; d += NT) o[d] = (part[d] + part[hd + d]) + (part[2 * hd + d] + part[3 * hd + d]);
+    for (int d = threadIdx.x; d < hd; d += 128) {
+        float O = 0.0f;
+        for (int c = 0; c < nc; c++) {
+            const float* pc = pb + (size_t)c * (hd + 2);
+            O += pc[2 + d] * expf(pc[0] - M);
+        }
+        o[d] = O / L;
+    }
 }
 
 // x += y (Tensor::add_inplace, ops.rs:276-289)
@@ -297,6 +362,8 @@ struct LlamaModel {
     int *tokens = nullptr, *pos = nullptr, *step = nullptr, *out_tokens = nullptr;
     size_t out_cap = 0;
     void* gemm_scratch = nullptr;
+    float* att_part = nullptr;  // [max_batch][n_heads][chunks of max_seq][hd + 2]
+    int att_nchunk = 0;
     hipStream_t stream = nullptr;
     hipGraphExec_t decode_exec = nullptr;
     hipGraph_t decode_graph = nullptr;
@@ -340,6 +407,14 @@ struct LlamaModel {
         return hipSuccess;
     }
 
+    // Attention chunks to launch for m rows starting at the current position
+    // (capture_any_pos: the launch is recorded once for every position).
+    bool capture_any_pos = false;
+    int chunks_needed(size_t m) const {
+        const size_t upto = capture_any_pos ? (size_t)cfg.max_seq : host_pos + m;
+        return (int)((upto + ATT_CHUNK - 1) / ATT_CHUNK);
+    }
+
     template <typename KV>
     hipError_t layer_attention(int l, size_t m) {
         KV* kcl = reinterpret_cast<KV*>(kc) + (size_t)l * kv_layer_elems();
@@ -348,16 +423,56 @@ struct LlamaModel {
         hipLaunchKernelGGL(rope_kv_kernel<KV>, dim3(cfg.n_heads + cfg.n_kv_heads, (unsigned)m), dim3(hd / 2), 0,
                            stream, qkv, qkv_dim, pos, cos_t, sin_t, cfg.n_heads, cfg.n_kv_heads, hd, kcl, vcl,
                            cfg.max_seq);
-        const size_t lds = (size_t)(5 * hd + cfg.max_seq) * sizeof(float);
         const float scale = sqrtf((float)hd);
-        hipLaunchKernelGGL(attention_kernel<KV>, dim3(cfg.n_heads, (unsigned)m), dim3(NT), lds, stream, qkv,
-                           qkv_dim, pos, kcl, vcl, cfg.max_seq, cfg.n_heads, cfg.n_kv_heads, hd, scale, att);
+        // chunks that can hold keys for these rows (every chunk of the cache
+        // when the launch is captured for replay at any position)
+        const int nz = chunks_needed(m);
+        hipLaunchKernelGGL(attention_chunk_kernel<KV>, dim3(cfg.n_heads, (unsigned)m, (unsigned)nz), dim3(64),
+                           (size_t)hd * sizeof(float), stream, qkv, qkv_dim, pos, kcl, vcl, cfg.max_seq,
+                           cfg.n_heads, cfg.n_kv_heads, hd, scale, att_part, att_nchunk);
+        hipLaunchKernelGGL(attention_combine_kernel, dim3(cfg.n_heads, (unsigned)m), dim3(128), 0, stream,
+                           att_part, pos, cfg.n_heads, hd, att_nchunk, att);
         return hipGetLastError();
     }
 
     // forward_with_cache_pass over m rows whose token ids are in `tokens`,
     // the last row's logits into `logits`, then the position advances by m.
+    // Up to 4 rows: RMSNorm, SwiGLU and the residual adds ride in the GEMV
+    // launches (prologue / epilogue of the fused GEMV): 7 launches a layer.
+    hipError_t forward_fused(size_t m) {
+        const int d = cfg.dim;
+        const float eps = cfg.norm_eps;
+        hipError_t e = launch_dequant_rows(WType::Q4_0, emb.dev, emb.n, emb.k, tokens, m, x, stream);
+        if (e != hipSuccess) return e;
+        for (int l = 0; l < cfg.n_layers; l++) {
+            Layer& L = layers[l];
+            // qkv = rms_norm(x) . [Wq; Wk; Wv]^T
+            e = launch_gemv_q4_0_fused_ex(L.qkv.dev, L.qkv.n, d, x, d, m, qkv, 1, L.attn_norm, eps, false, stream);
+            if (e != hipSuccess) return e;
+            e = cfg.kv_f16 ? layer_attention<_Float16>(l, m) : layer_attention<float>(l, m);
+            if (e != hipSuccess) return e;
+            // x += att . Wo^T
+            e = launch_gemv_q4_0_fused_ex(L.o.dev, L.o.n, q_dim, att, q_dim, m, x, 0, nullptr, 0.0f, true, stream);
+            if (e != hipSuccess) return e;
+            // gu = rms_norm(x) . [Wgate; Wup]^T
+            e = launch_gemv_q4_0_fused_ex(L.gu.dev, L.gu.n, d, x, d, m, gu, 1, L.ffn_norm, eps, false, stream);
+            if (e != hipSuccess) return e;
+            // x += (silu(gate) * up) . Wdown^T
+            e = launch_gemv_q4_0_fused_ex(L.down.dev, L.down.n, cfg.ffn_dim, gu, 2 * (size_t)cfg.ffn_dim, m, x, 2,
+                                          nullptr, 0.0f, true, stream);
+            if (e != hipSuccess) return e;
+        }
+        // logits = rms_norm(x_last, norm) . Wout^T
+        e = launch_gemv_q4_0_fused_ex(out.dev, out.n, d, x + (m - 1) * d, d, 1, logits, 1, final_norm, eps, false,
+                                      stream);
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(64), 0, stream, pos, (int)m);
+        return hipGetLastError();
+    }
+    bool fusable = false;  // every GEMV of the model meets the fused-launch shape rules
+
     hipError_t forward(size_t m) {
+        if (m <= 4 && fusable) return forward_fused(m);
         const int d = cfg.dim;
         hipError_t e = launch_dequant_rows(WType::Q4_0, emb.dev, emb.n, emb.k, tokens, m, x, stream);
         if (e != hipSuccess) return e;
@@ -477,6 +592,12 @@ rdl_status rdl_llama_create(const rdl_llama_config* cfg, rdl_llama** out) {
     if ((e = M.alloc_t(&M.out_tokens, M.out_cap)) != hipSuccess) return fail_free(e);
     const size_t kmax = (size_t)std::max(std::max(c.dim, c.ffn_dim), M.q_dim);
     if ((e = M.alloc(&M.gemm_scratch, rdl::gemm_scratch_bytes(mb, kmax))) != hipSuccess) return fail_free(e);
+    M.fusable = (c.dim / 32) % 2 == 0 && (M.q_dim / 32) % 2 == 0 && (c.ffn_dim / 32) % 2 == 0 &&
+                (uint64_t)2 * c.ffn_dim * (c.dim / 32) * rdl::Q4_0_BYTES <= rdl::FUSED_MAX_WEIGHT_BYTES &&
+                (uint64_t)c.vocab * (c.dim / 32) * rdl::Q4_0_BYTES <= rdl::FUSED_MAX_WEIGHT_BYTES;
+    M.att_nchunk = (c.max_seq + rdl::ATT_CHUNK - 1) / rdl::ATT_CHUNK;
+    if ((e = M.alloc_t(&M.att_part, mb * c.n_heads * (size_t)M.att_nchunk * (c.head_dim + 2))) != hipSuccess)
+        return fail_free(e);
     // RoPEFreqs::new (rope.rs:93-108) in f32 with the C library's powf / cosf / sinf
     const int half = c.head_dim / 2;
     M.cos_h.resize((size_t)c.max_seq * half);
@@ -633,10 +754,16 @@ rdl_status rdl_llama_generate_greedy(rdl_llama* model, const int32_t* prompt, si
     hipLaunchKernelGGL(rdl::set_int_kernel, dim3(1), dim3(64), 0, M.stream, M.step, 0);
     HIP_TRY(hipEventRecord(M.ev[0], M.stream));
     // prefill in chunks; the last chunk's logits give the first token
+    const size_t start = M.host_pos;
     for (size_t r = 0; r < n_prompt; r += (size_t)c.max_batch) {
         const size_t mr = std::min(n_prompt - r, (size_t)c.max_batch);
         HIP_TRY(hipMemcpyAsync(M.tokens, prompt + r, mr * 4, hipMemcpyHostToDevice, M.stream));
-        HIP_TRY(M.forward(mr));
+        const hipError_t fe = M.forward(mr);
+        M.host_pos += mr;  // the device position advanced with the forward
+        if (fe != hipSuccess) {
+            M.host_pos = start;
+            return api_fail(RDL_ERR_HIP, "prefill failed: %s", hipGetErrorString(fe));
+        }
     }
     hipLaunchKernelGGL(rdl::argmax_kernel, dim3(1), dim3(rdl::ARGMAX_NT), 0, M.stream, M.logits, c.vocab,
                        M.tokens, M.out_tokens, M.step);
@@ -645,7 +772,9 @@ rdl_status rdl_llama_generate_greedy(rdl_llama* model, const int32_t* prompt, si
     if (n_gen > 1) {
         if (!M.decode_exec) {
             HIP_TRY(hipStreamBeginCapture(M.stream, hipStreamCaptureModeThreadLocal));
+            M.capture_any_pos = true;
             const hipError_t ce = M.decode_step();
+            M.capture_any_pos = false;
             hipGraph_t g = nullptr;
             const hipError_t ee = hipStreamEndCapture(M.stream, &g);
             HIP_TRY(ce);
@@ -660,7 +789,7 @@ rdl_status rdl_llama_generate_greedy(rdl_llama* model, const int32_t* prompt, si
     HIP_TRY(hipStreamSynchronize(M.stream));
     HIP_TRY(hipEventElapsedTime(&M.prefill_ms, M.ev[0], M.ev[1]));
     HIP_TRY(hipEventElapsedTime(&M.decode_ms, M.ev[1], M.ev[2]));
-    M.host_pos += n_prompt + n_gen - 1;
+    M.host_pos += n_gen - 1;
     return api_ok();
 }
 

@@ -104,6 +104,9 @@ _decl("rdl_linear_prepared_dev", _i32, _p, _p, _sz, _p, _i32, _p)
 _decl("rdl_quantize_row_q8_0_dev", _i32, _p, _sz, _p, _p, _p)
 _decl("rdl_dequantize_rows_dev", _i32, _p, _p, _sz, _p, _p)
 _decl("rdl_q4_0_q8_0_block_dots_dev", _i32, _p, _p, _p, _p)
+_decl("rdl_linear_fused_dev", _i32, _p, _p, _sz, _sz, _p, _i32, _p, C.c_float, _i32, _p)
+
+PROLOGUE_NONE, PROLOGUE_RMSNORM, PROLOGUE_SWIGLU = 0, 1, 2
 
 
 # ---- errors (QuantError, rustml/quant/main/src/api/error.rs:1-18) ---------
@@ -274,6 +277,12 @@ class Weight:
             self.free()
         except Exception:
             pass
+
+    def forward_fused_dev(self, x_ptr, x_stride, m, y_ptr, prologue=0, gamma_ptr=0, eps=0.0, residual=False,
+                          stream=0):
+        """rdl_linear_fused_dev: Q4_0, m <= 4; RMSNorm / SwiGLU prologue, residual epilogue."""
+        check(lib.rdl_linear_fused_dev(self.handle, x_ptr, x_stride, m, y_ptr, prologue, gamma_ptr or None, eps,
+                                       int(bool(residual)), stream))
 
     def forward_dev(self, x_ptr, m, y_ptr, mode=MODE_FLOAT, stream=0):
         check(lib.rdl_linear_forward_dev(self.handle, x_ptr, m, y_ptr, mode, stream))
