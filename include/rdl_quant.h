@@ -184,15 +184,20 @@ rdl_status rdl_linear_prepared_dev(const rdl_weight* w, const void* rec_dev, siz
  *     (Tensor::rms_norm, rustml/core/main/src/core/tensor/ops.rs:688-751);
  *   prologue RDL_PROLOGUE_SWIGLU:  silu(x[:, :k]) * x[:, k:2k] first, each x
  *     row holding [gate | up] (FeedForward::forward, feed_forward.rs:138-150);
- *   residual != 0: y += result (Tensor::add_inplace, transformer_block.rs:333,352),
- *     y read before it is written; otherwise y = result.
- * x_stride = floats between x rows (>= k, >= 2k for SWIGLU; multiple of 4;
- * x 16-byte aligned).  No counterpart in the reference: there these are
- * separate tensor operations; one launch, no scratch memory. */
+ *   epilogue RDL_EPILOGUE_STORE:    y = result;
+ *   epilogue RDL_EPILOGUE_RESIDUAL: y += result (Tensor::add_inplace,
+ *     transformer_block.rs:333,352), y read before it is written;
+ *   epilogue RDL_EPILOGUE_SWIGLU:   the weight rows 2j, 2j+1 are gate_j, up_j
+ *     and y[j] = silu(result[2j]) * result[2j+1] (y rows out_features/2 long;
+ *     out_features even, in_features <= 8192).
+ * x_stride = floats between x rows (>= k, >= 2k for the SWIGLU prologue;
+ * multiple of 4; x 16-byte aligned).  No counterpart in the reference: there
+ * these are separate tensor operations; here one launch, no scratch memory. */
 enum { RDL_PROLOGUE_NONE = 0, RDL_PROLOGUE_RMSNORM = 1, RDL_PROLOGUE_SWIGLU = 2 };
+enum { RDL_EPILOGUE_STORE = 0, RDL_EPILOGUE_RESIDUAL = 1, RDL_EPILOGUE_SWIGLU = 2 };
 rdl_status rdl_linear_fused_dev(const rdl_weight* w, const float* x_dev, size_t x_stride, size_t m,
                                 float* y_dev, int32_t prologue, const float* gamma_dev, float eps,
-                                int32_t residual, void* stream);
+                                int32_t epilogue, void* stream);
 
 /* quantize_row_q8_0 on device: x_dev f32 [n] -> out_dev (n/32)*34 bytes and
  * scales_dev f32 [n/32] (scales_dev may be NULL). */

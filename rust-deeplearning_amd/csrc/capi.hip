@@ -468,23 +468,26 @@ rdl_status rdl_linear_prepared_dev(const rdl_weight* w, const void* rec_dev, siz
 
 rdl_status rdl_linear_fused_dev(const rdl_weight* w, const float* x_dev, size_t x_stride, size_t m,
                                 float* y_dev, int32_t prologue, const float* gamma_dev, float eps,
-                                int32_t residual, void* stream) {
+                                int32_t epilogue, void* stream) {
     if (!w) return fail(RDL_ERR_NULL_POINTER, "weight handle is NULL");
     if (w->type != WType::Q4_0) return fail(RDL_ERR_DTYPE_MISMATCH, "fused Linear takes Q4_0 weights");
     if (prologue < RDL_PROLOGUE_NONE || prologue > RDL_PROLOGUE_SWIGLU)
         return fail(RDL_ERR_INVALID_DATA, "unknown prologue %d", prologue);
+    if (epilogue < RDL_EPILOGUE_STORE || epilogue > RDL_EPILOGUE_SWIGLU)
+        return fail(RDL_ERR_INVALID_DATA, "unknown epilogue %d", epilogue);
     if (m == 0 || w->n == 0) return ok();
     if (!x_dev || !y_dev || (prologue == RDL_PROLOGUE_RMSNORM && !gamma_dev))
         return fail(RDL_ERR_NULL_POINTER, "NULL device pointer");
     const size_t k = w->k, nb = k / rdl::QK;
     if (m > 4 || nb == 0 || (nb & 1) || k > rdl::fused_max_k(WType::Q4_0) || (x_stride & 3) ||
         ((uintptr_t)x_dev & 15) || x_stride < (prologue == RDL_PROLOGUE_SWIGLU ? 2 * k : k) ||
-        w->len > rdl::FUSED_MAX_WEIGHT_BYTES)
+        w->len > rdl::FUSED_MAX_WEIGHT_BYTES ||
+        (epilogue == RDL_EPILOGUE_SWIGLU && ((w->n & 1) || nb > 256)))
         return fail(RDL_ERR_UNSUPPORTED,
                     "fused Linear: m <= 4, in_features/32 even and <= 16384, x 16-byte aligned, "
                     "x_stride a multiple of 4 covering the row (m=%zu k=%zu stride=%zu)", m, k, x_stride);
     HIP_TRY(rdl::launch_gemv_q4_0_fused_ex((const uint8_t*)w->dev, w->n, k, x_dev, x_stride, m, y_dev, prologue,
-                                           gamma_dev, eps, residual != 0, (hipStream_t)stream));
+                                           gamma_dev, eps, epilogue, (hipStream_t)stream));
     return ok();
 }
 

@@ -542,9 +542,14 @@ __device__ __forceinline__ float block_dot_i4(const uint32_t (&w)[5], uint32_t s
 // its instructions in order and the memory pipeline accepts only so many
 // loads per CU, so interleaving load issue with compute is what lets the dot
 // products overlap the weight stream.
-// PRO: prologue on x (PRO_NONE / PRO_RMSNORM / PRO_SWIGLU, int4 records
-// only); RES: y += W x in place (the residual add of transformer_block.rs:333,352).
-template <int WT, bool NATIVE, int R, int CPL, bool NB_EVEN, int NW, int PRO = PRO_NONE, bool RES = false>
+// Epilogues: EPI_STORE y = W x; EPI_RESIDUAL y += W x in place (the residual
+// add of transformer_block.rs:333,352); EPI_SWIGLU: W holds [gate_j; up_j]
+// as rows 2j, 2j+1 and y[j] = silu(gate_j) * up_j (feed_forward.rs:138-150) --
+// a wave then owns row pairs, so both halves of a pair meet in one wave.
+constexpr int EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_SWIGLU = 2;
+
+// PRO: prologue on x (PRO_NONE / PRO_RMSNORM / PRO_SWIGLU, int4 records only).
+template <int WT, bool NATIVE, int R, int CPL, bool NB_EVEN, int NW, int PRO = PRO_NONE, int EPI = EPI_STORE>
 __global__ __launch_bounds__(NW * 64) void gemv_fused_kernel(const uint8_t* __restrict__ W, int n,
                                                         int nb, int rpw,
                                                         const float* __restrict__ X,
@@ -569,8 +574,13 @@ __global__ __launch_bounds__(NW * 64) void gemv_fused_kernel(const uint8_t* __re
     const int r0 = blockIdx.x * rpw;
     const int rend = min(n, r0 + rpw);
     static_assert(PRO == PRO_NONE || I4, "prologues run on the int4-record prep");
+    static_assert(EPI != EPI_SWIGLU || R % 2 == 0, "SwiGLU pairs need an even row count per wave");
     const float* x = X + (size_t)blockIdx.y * fz.xstride;
-    float* y = Y + (size_t)blockIdx.y * n;
+    float* y = Y + (size_t)blockIdx.y * (EPI == EPI_SWIGLU ? n / 2 : n);
+    // matrix row of the wave's r-th row
+    auto row_of = [&](int r) {
+        return (EPI == EPI_SWIGLU) ? r0 + 2 * (wv + (r >> 1) * NW) + (r & 1) : r0 + wv + r * NW;
+    };
     const uint32_t row_bytes = (uint32_t)nb * BYTES;
     const uint32_t wbytes = (uint32_t)n * row_bytes;
 
@@ -583,7 +593,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_fused_kernel(const uint8_t* __re
     uint32_t win[NB][WORDS];
     auto issue = [&](int b) {
         const int r = b / CPL, i = b % CPL;
-        const int row = r0 + wv + r * NW, col = lane + 64 * i;
+        const int row = row_of(r), col = lane + 64 * i;
         const uint32_t off = (row < rend && col < nb)
                                  ? (uint32_t)row * row_bytes + (uint32_t)col * BYTES
                                  : RSRC_OOB;
@@ -638,7 +648,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_fused_kernel(const uint8_t* __re
     for (int b = 0; b < NB; b++) {
         if (b + PF < NB) issue(b + PF);
         const int r = b / CPL, i = b % CPL;
-        const int row = r0 + wv + r * NW;
+        const int row = row_of(r);
         const int col = lane + 64 * i;
         if (row < rend && col < nb) {
             const bool odd = NB_EVEN ? (col & 1) : (((row * nb + col) & 1) != 0);
@@ -659,15 +669,22 @@ __global__ __launch_bounds__(NW * 64) void gemv_fused_kernel(const uint8_t* __re
             }
         }
     }
-    if (r0 + wv >= rend) return;  // wave-uniform; the wave had nothing to store
+    if (row_of(0) >= rend) return;  // wave-uniform; the wave had nothing to store
 
     // ---- reduce and store ----
     const float s = wave_reduce_rows<R>(acc);
     constexpr int SH = reduce_span_log2<R>();
-    if ((lane & ((1 << SH) - 1)) == 0) {
-        const int row = r0 + wv + (lane >> SH) * NW;
+    if constexpr (EPI == EPI_SWIGLU) {
+        // rows r (gate, even) and r + 1 (up) sit in adjacent lane groups
+        const float up = __shfl_down(s, 1 << SH);
+        if ((lane & ((2 << SH) - 1)) == 0) {
+            const int g = row_of(lane >> SH);
+            if (g + 1 < rend) y[g >> 1] = (s * (1.0f / (1.0f + expf(-s)))) * up;
+        }
+    } else if ((lane & ((1 << SH) - 1)) == 0) {
+        const int row = row_of(lane >> SH);
         if (row < rend) {
-            if constexpr (RES)
+            if constexpr (EPI == EPI_RESIDUAL)
                 y[row] = s + y[row];
             else
                 y[row] = s;
@@ -833,13 +850,24 @@ Cfg pick_cfg(int n, int nw, int rmax, int wg_per_cu) {
     return Cfg{nw, rpw, r};
 }
 
-template <int WT, bool NATIVE, int CPL, bool EVEN, int NW, int PRO = PRO_NONE, bool RES = false>
+template <int WT, bool NATIVE, int CPL, bool EVEN, int NW, int PRO = PRO_NONE, int RES = EPI_STORE>
 void launch_nw(const uint8_t* w, int n, int nb, const float* x, size_t m, float* y, hipStream_t s,
                const Cfg& c, size_t lds, const Fuse& fz) {
     const dim3 grid((unsigned)((n + c.rpw - 1) / c.rpw), (unsigned)m), block(NW * 64);
     constexpr int RMAX = 8 / CPL;
     const int rpw = c.rpw;
-    if (c.r <= 1 || RMAX == 1)
+    if constexpr (RES == EPI_SWIGLU) {
+        // even row counts only (row pairs); RMAX 1 is rejected by the caller
+        if constexpr (RMAX >= 4) {
+            if (c.r >= 4)
+                launch_kernel((gemv_fused_kernel<WT, NATIVE, 4, CPL, EVEN, NW, PRO, RES>), grid, block, lds, s, w, n, nb, rpw, x, y, fz);
+            else
+                launch_kernel((gemv_fused_kernel<WT, NATIVE, 2, CPL, EVEN, NW, PRO, RES>), grid, block, lds, s, w, n, nb, rpw, x, y, fz);
+        } else if constexpr (RMAX >= 2) {
+            launch_kernel((gemv_fused_kernel<WT, NATIVE, 2, CPL, EVEN, NW, PRO, RES>), grid, block, lds, s, w, n, nb, rpw, x, y, fz);
+        }
+        return;
+    } else if (c.r <= 1 || RMAX == 1)
         launch_kernel((gemv_fused_kernel<WT, NATIVE, 1, CPL, EVEN, NW, PRO, RES>), grid, block, lds, s, w, n, nb, rpw, x, y, fz);
     else if (c.r <= 2 || RMAX == 2)
         launch_kernel((gemv_fused_kernel<WT, NATIVE, (RMAX >= 2 ? 2 : 1), CPL, EVEN, NW, PRO, RES>), grid, block, lds, s, w, n, nb, rpw, x, y, fz);
@@ -900,11 +928,16 @@ void launch_q4k_nw(const uint8_t* w, int n, int nsb, const float* x, size_t m, f
 }
 
 // Decoder fusion: Q4_0 float mode, 8-wave workgroups (two per CU), nb even.
-template <int PRO, bool RES>
+template <int PRO, int RES>
 void launch_q4_0_fused_ex(const uint8_t* w, int n, int nb, const float* x, size_t m, float* y,
                           hipStream_t s, size_t lds, const Fuse& fz) {
     const int cpl = cpl_for(nb);
-    const Cfg c = pick_cfg(n, 8, 8 / cpl, 2);
+    Cfg c = pick_cfg(n, 8, 8 / cpl, 2);
+    if (RES == EPI_SWIGLU) {
+        // whole row pairs per wave: R even, a workgroup takes NW * R rows
+        c.r = (8 / cpl >= 4 && n >= 2 * 8 * 4 * 256) ? 4 : 2;
+        c.rpw = 8 * c.r;
+    }
     constexpr int Q = (int)WType::Q4_0;
     switch (cpl) {
         case 2: launch_nw<Q, false, 2, true, 8, PRO, RES>(w, n, nb, x, m, y, s, c, lds, fz); break;
@@ -917,7 +950,7 @@ void launch_q4_0_fused_ex(const uint8_t* w, int n, int nb, const float* x, size_
 
 hipError_t launch_gemv_q4_0_fused_ex(const uint8_t* w, size_t n, size_t k, const float* x, size_t xstride,
                                      size_t m, float* y, int prologue, const float* g, float eps,
-                                     bool residual, hipStream_t s) {
+                                     int epilogue, hipStream_t s) {
     if (n == 0 || m == 0) return hipSuccess;
     const int nb = (int)(k / QK);
     if (nb == 0 || (nb & 1) || k > fused_max_k(WType::Q4_0) || ((uintptr_t)x & 15) || (xstride & 3) ||
@@ -926,14 +959,19 @@ hipError_t launch_gemv_q4_0_fused_ex(const uint8_t* w, size_t n, size_t k, const
     const Fuse fz{g, eps, (int)xstride};
     const size_t lds = (size_t)8 * 16 * nb;
     const int ni = (int)n;
-    if (prologue == PRO_RMSNORM && !residual)
-        launch_q4_0_fused_ex<PRO_RMSNORM, false>(w, ni, nb, x, m, y, s, lds, fz);
-    else if (prologue == PRO_NONE && residual)
-        launch_q4_0_fused_ex<PRO_NONE, true>(w, ni, nb, x, m, y, s, lds, fz);
-    else if (prologue == PRO_SWIGLU && residual)
-        launch_q4_0_fused_ex<PRO_SWIGLU, true>(w, ni, nb, x, m, y, s, lds, fz);
-    else if (prologue == PRO_NONE && !residual)
-        launch_q4_0_fused_ex<PRO_NONE, false>(w, ni, nb, x, m, y, s, lds, fz);
+    if (epilogue == EPI_SWIGLU && ((n & 1) || cpl_for(nb) > 4)) return hipErrorInvalidValue;
+    if (prologue == PRO_RMSNORM && epilogue == EPI_STORE)
+        launch_q4_0_fused_ex<PRO_RMSNORM, EPI_STORE>(w, ni, nb, x, m, y, s, lds, fz);
+    else if (prologue == PRO_RMSNORM && epilogue == EPI_SWIGLU)
+        launch_q4_0_fused_ex<PRO_RMSNORM, EPI_SWIGLU>(w, ni, nb, x, m, y, s, lds, fz);
+    else if (prologue == PRO_NONE && epilogue == EPI_RESIDUAL)
+        launch_q4_0_fused_ex<PRO_NONE, EPI_RESIDUAL>(w, ni, nb, x, m, y, s, lds, fz);
+    else if (prologue == PRO_SWIGLU && epilogue == EPI_RESIDUAL)
+        launch_q4_0_fused_ex<PRO_SWIGLU, EPI_RESIDUAL>(w, ni, nb, x, m, y, s, lds, fz);
+    else if (prologue == PRO_NONE && epilogue == EPI_STORE)
+        launch_q4_0_fused_ex<PRO_NONE, EPI_STORE>(w, ni, nb, x, m, y, s, lds, fz);
+    else if (prologue == PRO_NONE && epilogue == EPI_SWIGLU)
+        launch_q4_0_fused_ex<PRO_NONE, EPI_SWIGLU>(w, ni, nb, x, m, y, s, lds, fz);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();

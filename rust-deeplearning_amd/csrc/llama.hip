@@ -147,14 +147,17 @@ __global__ void rope_kv_kernel(float* __restrict__ qkv, int qkv_dim, const int* 
 // capacity serves every position (the captured decode graph).
 constexpr int ATT_CHUNK = 64;
 
-template <typename KV>
+// HD: head dim as a compile-time constant (64, 128, 256), so that all of a
+// key row's loads are issued before its dot product; 0: runtime hd.
+template <typename KV, int HD>
 __global__ __launch_bounds__(64) void attention_chunk_kernel(const float* __restrict__ qkv, int qkv_dim,
                                                              const int* __restrict__ pos_dev,
                                                              const KV* __restrict__ kc,
                                                              const KV* __restrict__ vc, int max_seq,
-                                                             int n_heads, int n_kv, int hd, float scale,
+                                                             int n_heads, int n_kv, int hd_rt, float scale,
                                                              float* __restrict__ part, int nchunk) {
     extern __shared__ float qs[];
+    const int hd = HD ? HD : hd_rt;
     const int h = blockIdx.x, s = blockIdx.y, c = blockIdx.z, lane = threadIdx.x;
     const int t = *pos_dev + s + 1;
     const int p0 = c * ATT_CHUNK;
@@ -165,15 +168,25 @@ __global__ __launch_bounds__(64) void attention_chunk_kernel(const float* __rest
     __syncthreads();
     const int p = p0 + lane;
     const bool valid = p < t;
-    // score of key p: 16-byte loads of the key row
+    // score of key p = lane's key
     const KV* kr = kc + ((size_t)kvh * max_seq + (valid ? p : p0)) * hd;
-    float acc = 0.0f;
     constexpr int V = 16 / sizeof(KV);
-    for (int d = 0; d < hd; d += V) {
-        typedef KV kvv __attribute__((ext_vector_type(V)));
-        const kvv kv = *reinterpret_cast<const kvv*>(kr + d);
+    typedef KV kvv __attribute__((ext_vector_type(V)));
+    float acc = 0.0f;
+    if constexpr (HD > 0) {
+        kvv kreg[HD / V];
 #pragma unroll
-        for (int i = 0; i < V; i++) acc += qs[d + i] * (float)kv[i];
+        for (int i = 0; i < HD / V; i++) kreg[i] = *reinterpret_cast<const kvv*>(kr + i * V);
+#pragma unroll
+        for (int i = 0; i < HD / V; i++)
+#pragma unroll
+            for (int e = 0; e < V; e++) acc += qs[i * V + e] * (float)kreg[i][e];
+    } else {
+        for (int d = 0; d < hd; d += V) {
+            const kvv kv = *reinterpret_cast<const kvv*>(kr + d);
+#pragma unroll
+            for (int e = 0; e < V; e++) acc += qs[d + e] * (float)kv[e];
+        }
     }
     const float sc = valid ? acc / scale : -__builtin_inff();
     const float mx = wave_max(sc);
@@ -208,25 +221,43 @@ __global__ __launch_bounds__(64) void attention_chunk_kernel(const float* __rest
     }
 }
 
+// One thread per chunk reads (m_c, l_c); the weights exp(m_c - M) / L go to
+// LDS; each output dim then sums its chunks in batches of 8 branch-free loads.
 __global__ __launch_bounds__(128) void attention_combine_kernel(const float* __restrict__ part,
                                                                 const int* __restrict__ pos_dev, int n_heads,
                                                                 int hd, int nchunk, float* __restrict__ out) {
+    __shared__ float wc[1024];
+    __shared__ float red[2];
     const int h = blockIdx.x, s = blockIdx.y;
     const int t = *pos_dev + s + 1;
-    const int nc = (t + ATT_CHUNK - 1) / ATT_CHUNK;
+    const int nc = (t + ATT_CHUNK - 1) / ATT_CHUNK;  // <= nchunk <= 1024
     const float* pb = part + ((size_t)s * n_heads + h) * nchunk * (hd + 2);
-    float M = -__builtin_inff();
-    for (int c = 0; c < nc; c++) M = fmaxf(M, pb[(size_t)c * (hd + 2)]);
-    float L = 0.0f;
-    for (int c = 0; c < nc; c++) L += pb[(size_t)c * (hd + 2) + 1] * expf(pb[(size_t)c * (hd + 2)] - M);
+    if (threadIdx.x < 64) {
+        float M = -__builtin_inff();
+        for (int c = threadIdx.x; c < nc; c += 64) M = fmaxf(M, pb[(size_t)c * (hd + 2)]);
+        M = wave_max(M);
+        float L = 0.0f;
+        for (int c = threadIdx.x; c < nc; c += 64) {
+            const float w = expf(pb[(size_t)c * (hd + 2)] - M);
+            wc[c] = w;
+            L += pb[(size_t)c * (hd + 2) + 1] * w;
+        }
+        L = wave_sum(L);
+        if (threadIdx.x == 0) red[0] = L;
+    }
+    __syncthreads();
+    const float invL = 1.0f / red[0];
     float* o = out + (size_t)s * n_heads * hd + h * hd;
     for (int d = threadIdx.x; d < hd; d += 128) {
         float O = 0.0f;
-        for (int c = 0; c < nc; c++) {
-            const float* pc = pb + (size_t)c * (hd + 2);
-            O += pc[2 + d] * expf(pc[0] - M);
+        for (int c0 = 0; c0 < nc; c0 += 8) {
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) v[i] = pb[(size_t)min(c0 + i, nc - 1) * (hd + 2) + 2 + d];
+#pragma unroll
+            for (int i = 0; i < 8; i++) O += (c0 + i < nc) ? v[i] * wc[c0 + i] : 0.0f;
         }
-        o[d] = O / L;
+        o[d] = O * invL;
     }
 }
 
@@ -236,12 +267,13 @@ __global__ void add_kernel(float* __restrict__ x, const float* __restrict__ y, s
     if (i < n) x[i] = x[i] + y[i];
 }
 
-// h = silu(gate) * up, silu(g) = g * (1 / (1 + exp(-g)))   (ops.rs:441-446)
+// h = silu(gate) * up, silu(g) = g * (1 / (1 + exp(-g)))   (ops.rs:441-446);
+// gu rows hold (gate_j, up_j) at 2j, 2j + 1 (the interleaved Wgu rows)
 __global__ void swiglu_kernel(const float* __restrict__ gu, int ffn, size_t n, float* __restrict__ h) {
     const size_t i = (size_t)blockIdx.x * NT + threadIdx.x;
     if (i >= n) return;
     const size_t s = i / ffn, j = i % ffn;
-    const float g = gu[s * 2 * ffn + j], u = gu[s * 2 * ffn + ffn + j];
+    const float g = gu[s * 2 * ffn + 2 * j], u = gu[s * 2 * ffn + 2 * j + 1];
     const float sig = 1.0f / (1.0f + expf(-g));
     h[i] = (g * sig) * u;
 }
@@ -427,8 +459,13 @@ struct LlamaModel {
         // chunks that can hold keys for these rows (every chunk of the cache
         // when the launch is captured for replay at any position)
         const int nz = chunks_needed(m);
-        hipLaunchKernelGGL(attention_chunk_kernel<KV>, dim3(cfg.n_heads, (unsigned)m, (unsigned)nz), dim3(64),
-                           (size_t)hd * sizeof(float), stream, qkv, qkv_dim, pos, kcl, vcl, cfg.max_seq,
+        const dim3 grid(cfg.n_heads, (unsigned)m, (unsigned)nz);
+        const size_t lds = (size_t)hd * sizeof(float);
+        auto kern = (hd == 128) ? attention_chunk_kernel<KV, 128>
+                  : (hd == 64)  ? attention_chunk_kernel<KV, 64>
+                  : (hd == 256) ? attention_chunk_kernel<KV, 256>
+                                : attention_chunk_kernel<KV, 0>;
+        hipLaunchKernelGGL(kern, grid, dim3(64), lds, stream, qkv, qkv_dim, pos, kcl, vcl, cfg.max_seq,
                            cfg.n_heads, cfg.n_kv_heads, hd, scale, att_part, att_nchunk);
         hipLaunchKernelGGL(attention_combine_kernel, dim3(cfg.n_heads, (unsigned)m), dim3(128), 0, stream,
                            att_part, pos, cfg.n_heads, hd, att_nchunk, att);
@@ -447,23 +484,23 @@ struct LlamaModel {
         for (int l = 0; l < cfg.n_layers; l++) {
             Layer& L = layers[l];
             // qkv = rms_norm(x) . [Wq; Wk; Wv]^T
-            e = launch_gemv_q4_0_fused_ex(L.qkv.dev, L.qkv.n, d, x, d, m, qkv, 1, L.attn_norm, eps, false, stream);
+            e = launch_gemv_q4_0_fused_ex(L.qkv.dev, L.qkv.n, d, x, d, m, qkv, 1, L.attn_norm, eps, 0, stream);
             if (e != hipSuccess) return e;
             e = cfg.kv_f16 ? layer_attention<_Float16>(l, m) : layer_attention<float>(l, m);
             if (e != hipSuccess) return e;
             // x += att . Wo^T
-            e = launch_gemv_q4_0_fused_ex(L.o.dev, L.o.n, q_dim, att, q_dim, m, x, 0, nullptr, 0.0f, true, stream);
+            e = launch_gemv_q4_0_fused_ex(L.o.dev, L.o.n, q_dim, att, q_dim, m, x, 0, nullptr, 0.0f, 1, stream);
             if (e != hipSuccess) return e;
-            // gu = rms_norm(x) . [Wgate; Wup]^T
-            e = launch_gemv_q4_0_fused_ex(L.gu.dev, L.gu.n, d, x, d, m, gu, 1, L.ffn_norm, eps, false, stream);
+            // h = silu(gate) * up with [gate; up] = rms_norm(x) . Wgu^T (rows interleaved)
+            e = launch_gemv_q4_0_fused_ex(L.gu.dev, L.gu.n, d, x, d, m, hb, 1, L.ffn_norm, eps, 2, stream);
             if (e != hipSuccess) return e;
-            // x += (silu(gate) * up) . Wdown^T
-            e = launch_gemv_q4_0_fused_ex(L.down.dev, L.down.n, cfg.ffn_dim, gu, 2 * (size_t)cfg.ffn_dim, m, x, 2,
-                                          nullptr, 0.0f, true, stream);
+            // x += h . Wdown^T
+            e = launch_gemv_q4_0_fused_ex(L.down.dev, L.down.n, cfg.ffn_dim, hb, cfg.ffn_dim, m, x, 0, nullptr, 0.0f,
+                                          1, stream);
             if (e != hipSuccess) return e;
         }
         // logits = rms_norm(x_last, norm) . Wout^T
-        e = launch_gemv_q4_0_fused_ex(out.dev, out.n, d, x + (m - 1) * d, d, 1, logits, 1, final_norm, eps, false,
+        e = launch_gemv_q4_0_fused_ex(out.dev, out.n, d, x + (m - 1) * d, d, 1, logits, 1, final_norm, eps, 0,
                                       stream);
         if (e != hipSuccess) return e;
         hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(64), 0, stream, pos, (int)m);
@@ -524,7 +561,7 @@ namespace {
 bool valid_config(const rdl_llama_config& c) {
     return c.dim > 0 && c.n_layers > 0 && c.n_heads > 0 && c.n_kv_heads > 0 && c.head_dim > 0 &&
            c.head_dim % 2 == 0 && c.head_dim <= 256 && c.n_heads % c.n_kv_heads == 0 && c.ffn_dim > 0 &&
-           c.vocab > 0 && c.max_seq > 0 && c.max_batch > 0 && c.dim % 32 == 0 && c.ffn_dim % 32 == 0 &&
+           c.vocab > 0 && c.max_seq > 0 && c.max_seq <= 65536 && c.max_batch > 0 && c.dim % 32 == 0 && c.ffn_dim % 32 == 0 &&
            (c.n_heads * c.head_dim) % 32 == 0 && c.dim <= 16384 && c.ffn_dim <= 16384 &&
            c.n_heads * c.head_dim <= 16384;
 }
@@ -650,8 +687,20 @@ rdl_status rdl_llama_set_weight(rdl_llama* model, int32_t slot, int32_t layer, c
         case RDL_LLAMA_WK: q4(M.layers[layer].qkv, M.q_dim, M.kv_dim); break;
         case RDL_LLAMA_WV: q4(M.layers[layer].qkv, M.q_dim + M.kv_dim, M.kv_dim); break;
         case RDL_LLAMA_WO: q4(M.layers[layer].o, 0, c.dim); break;
-        case RDL_LLAMA_W_GATE: q4(M.layers[layer].gu, 0, c.ffn_dim); break;
-        case RDL_LLAMA_W_UP: q4(M.layers[layer].gu, c.ffn_dim, c.ffn_dim); break;
+        case RDL_LLAMA_W_GATE:  // even rows of the interleaved [gate; up] matrix
+        case RDL_LLAMA_W_UP: {   // odd rows
+            rdl::LlamaModel::Mat& w = M.layers[layer].gu;
+            const size_t rb = M.row_q4(w.k);
+            if (len != (size_t)c.ffn_dim * rb)
+                return api_fail(RDL_ERR_SHAPE_MISMATCH, "slot %d: expected %zu bytes, got %zu", slot,
+                                (size_t)c.ffn_dim * rb, len);
+            HIP_TRY(hipMemcpy2D(w.dev + (slot == RDL_LLAMA_W_UP ? rb : 0), 2 * rb, bytes, rb, rb, c.ffn_dim,
+                                hipMemcpyHostToDevice));
+            bool ok = false;
+            HIP_TRY(rdl::gemm_scales_ok(rdl::WType::Q4_0, w.dev, w.n, w.k, &ok));
+            w.gemm_ok = ok;
+            return api_ok();
+        }
         case RDL_LLAMA_W_DOWN: q4(M.layers[layer].down, 0, c.dim); break;
         default: return api_fail(RDL_ERR_INVALID_DATA, "unknown weight slot %d", slot);
     }

@@ -142,10 +142,11 @@ hipError_t launch_gemm_q4_0(const uint8_t* w, size_t n, size_t k, const float* x
 
 // Decoder fusion of the Q4_0 float-mode fused GEMV (m <= 4, k / 32 even,
 // x 16-byte aligned): prologue 0 none, 1 RMSNorm with weights g and eps,
-// 2 SwiGLU of [gate | up] rows (x row stride xstride >= 2k); residual: y += W x.
+// 2 SwiGLU of [gate | up] x rows (row stride xstride >= 2k); epilogue 0 y = W x,
+// 1 y += W x, 2 y[j] = silu(W x)[2j] * (W x)[2j+1] (n even, y rows n/2 long).
 hipError_t launch_gemv_q4_0_fused_ex(const uint8_t* w, size_t n, size_t k, const float* x, size_t xstride,
                                      size_t m, float* y, int prologue, const float* g, float eps,
-                                     bool residual, hipStream_t s);
+                                     int epilogue, hipStream_t s);
 
 // int32 block partials of the Q4_0 x Q8_0 path for one activation row.
 hipError_t launch_q4_0_block_dots(const uint8_t* w, size_t n, size_t k, const NativeRec* rec,

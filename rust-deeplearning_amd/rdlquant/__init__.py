@@ -107,6 +107,7 @@ _decl("rdl_q4_0_q8_0_block_dots_dev", _i32, _p, _p, _p, _p)
 _decl("rdl_linear_fused_dev", _i32, _p, _p, _sz, _sz, _p, _i32, _p, C.c_float, _i32, _p)
 
 PROLOGUE_NONE, PROLOGUE_RMSNORM, PROLOGUE_SWIGLU = 0, 1, 2
+EPILOGUE_STORE, EPILOGUE_RESIDUAL, EPILOGUE_SWIGLU = 0, 1, 2
 
 
 # ---- errors (QuantError, rustml/quant/main/src/api/error.rs:1-18) ---------
@@ -278,11 +279,12 @@ class Weight:
         except Exception:
             pass
 
-    def forward_fused_dev(self, x_ptr, x_stride, m, y_ptr, prologue=0, gamma_ptr=0, eps=0.0, residual=False,
+    def forward_fused_dev(self, x_ptr, x_stride, m, y_ptr, prologue=0, gamma_ptr=0, eps=0.0, epilogue=0,
                           stream=0):
-        """rdl_linear_fused_dev: Q4_0, m <= 4; RMSNorm / SwiGLU prologue, residual epilogue."""
+        """rdl_linear_fused_dev: Q4_0, m <= 4; RMSNorm / SwiGLU prologue; store / residual /
+        SwiGLU-pair epilogue."""
         check(lib.rdl_linear_fused_dev(self.handle, x_ptr, x_stride, m, y_ptr, prologue, gamma_ptr or None, eps,
-                                       int(bool(residual)), stream))
+                                       int(epilogue), stream))
 
     def forward_dev(self, x_ptr, m, y_ptr, mode=MODE_FLOAT, stream=0):
         check(lib.rdl_linear_forward_dev(self.handle, x_ptr, m, y_ptr, mode, stream))

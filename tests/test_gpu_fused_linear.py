@@ -23,7 +23,7 @@ def run(rq, torch, w, x, xs, m, n, prologue, g=None, eps=0.0, y0=None):
     yd = dev(torch, y0) if y0 is not None else torch.empty(m * n, dtype=torch.float32, device="cuda:0")
     gd = dev(torch, g) if g is not None else None
     W.forward_fused_dev(xd.data_ptr(), xs, m, yd.data_ptr(), prologue, gd.data_ptr() if gd is not None else 0,
-                        eps, y0 is not None)
+                        eps, rq.EPILOGUE_RESIDUAL if y0 is not None else rq.EPILOGUE_STORE)
     torch.cuda.synchronize()
     return yd.cpu().numpy().reshape(-1)
 
@@ -85,3 +85,27 @@ def test_rejects_unsupported_shapes(rq, gpu):
     y = torch.zeros(8, device="cuda:0")
     with pytest.raises(rq.QuantError):
         W.forward_fused_dev(x.data_ptr(), 96, 1, y.data_ptr())
+
+
+@pytest.mark.parametrize("m,ffn,k", [(1, 160, 256), (3, 1000, 4096), (4, 14336, 4096), (1, 32, 8192)])
+def test_swiglu_pair_epilogue(rq, orc, gpu, m, ffn, k):
+    import torch
+    gate = synth.q4_0_weights(ffn, k, 21).reshape(ffn, -1)
+    up = synth.q4_0_weights(ffn, k, 22).reshape(ffn, -1)
+    inter = np.empty((2 * ffn, gate.shape[1]), np.uint8)
+    inter[0::2], inter[1::2] = gate, up  # rows 2j, 2j+1 = gate_j, up_j
+    x = synth.activations(m, k, 23)
+    g = (1.0 + 0.1 * np.random.default_rng(24).standard_normal(k)).astype(np.float32)
+    W = rq.Weight.upload(inter.reshape(-1), rq.DTYPE_Q4_0, 2 * ffn, k)
+    xd, gd = dev(torch, x), dev(torch, g)
+    yd = torch.empty(m * ffn, dtype=torch.float32, device="cuda:0")
+    W.forward_fused_dev(xd.data_ptr(), k, m, yd.data_ptr(), rq.PROLOGUE_RMSNORM, gd.data_ptr(), 1e-5,
+                        rq.EPILOGUE_SWIGLU)
+    torch.cuda.synchronize()
+    got = yd.cpu().numpy().reshape(m, ffn)
+    xn = orc.rms_norm(x, g, 1e-5)
+    a = orc.matmul("q4", xn, gate.reshape(-1), m, k, ffn, threads=8).reshape(m, ffn)
+    b = orc.matmul("q4", xn, up.reshape(-1), m, k, ffn, threads=8).reshape(m, ffn)
+    want = (a * (np.float32(1.0) / (np.float32(1.0) + np.exp(-a)))) * b
+    # the product of two in-tolerance factors: bar on each scaled by the other
+    assert np.all(np.abs(got - want) <= 2e-3 * np.abs(want) + 2e-4 * (np.abs(b) + np.abs(a) + 1.0))
