@@ -207,6 +207,13 @@ struct Fuse {
     const float* g;  // RMSNorm weights
     float eps;
     int xstride;     // floats between activation rows
+    // EPI_ROPE_KV (rope.rs:134-200, kv_cache.rs:94-106)
+    const int* pos;             // cache position of activation row 0
+    const float* cos_t;         // [max_seq][hd / 2]
+    const float* sin_t;
+    void* kc;                   // [n_kv][max_seq][hd], f16 or f32
+    void* vc;
+    int n_heads, n_kv, hd, max_seq, kv_f16;
 };
 
 template <int NW, int PI, int PRO = PRO_NONE>
@@ -546,7 +553,10 @@ __device__ __forceinline__ float block_dot_i4(const uint32_t (&w)[5], uint32_t s
 // add of transformer_block.rs:333,352); EPI_SWIGLU: W holds [gate_j; up_j]
 // as rows 2j, 2j+1 and y[j] = silu(gate_j) * up_j (feed_forward.rs:138-150) --
 // a wave then owns row pairs, so both halves of a pair meet in one wave.
-constexpr int EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_SWIGLU = 2;
+// EPI_ROPE_KV: W holds [Wq; Wk; Wv] and a wave owns the RoPE pairs (i, i + hd/2)
+// of a head: q rows are rotated in place in y, k rows rotated and v rows
+// copied into the KV cache at the row's position (y's k / v rows unwritten).
+constexpr int EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_SWIGLU = 2, EPI_ROPE_KV = 3;
 
 // PRO: prologue on x (PRO_NONE / PRO_RMSNORM / PRO_SWIGLU, int4 records only).
 template <int WT, bool NATIVE, int R, int CPL, bool NB_EVEN, int NW, int PRO = PRO_NONE, int EPI = EPI_STORE>
@@ -574,12 +584,25 @@ __global__ __launch_bounds__(NW * 64) void gemv_fused_kernel(const uint8_t* __re
     const int r0 = blockIdx.x * rpw;
     const int rend = min(n, r0 + rpw);
     static_assert(PRO == PRO_NONE || I4, "prologues run on the int4-record prep");
-    static_assert(EPI != EPI_SWIGLU || R % 2 == 0, "SwiGLU pairs need an even row count per wave");
+    constexpr bool PAIRS = (EPI == EPI_SWIGLU || EPI == EPI_ROPE_KV);
+    static_assert(!PAIRS || R % 2 == 0, "row pairs need an even row count per wave");
     const float* x = X + (size_t)blockIdx.y * fz.xstride;
     float* y = Y + (size_t)blockIdx.y * (EPI == EPI_SWIGLU ? n / 2 : n);
-    // matrix row of the wave's r-th row
-    auto row_of = [&](int r) {
-        return (EPI == EPI_SWIGLU) ? r0 + 2 * (wv + (r >> 1) * NW) + (r & 1) : r0 + wv + r * NW;
+    const int half = fz.hd >> 1;
+    // The wave's r-th row as a linear row in [r0, r0 + rpw) (validity against
+    // rend) and as a matrix row (addressing).  Pairs (r, r + 1 even/odd):
+    // SwiGLU rows 2j, 2j + 1; RoPE: linear pair p is the partners (i, i + hd/2)
+    // of head p / (hd/2), i = p % (hd/2).
+    auto row_of = [&](int r) {  // linear
+        if constexpr (PAIRS) return r0 + 2 * (wv + (r >> 1) * NW) + (r & 1);
+        return r0 + wv + r * NW;
+    };
+    auto mat_row = [&](int lin) {
+        if constexpr (EPI == EPI_ROPE_KV) {
+            const int pp = lin >> 1;
+            return (pp / half) * fz.hd + pp % half + (lin & 1) * half;
+        }
+        return lin;
     };
     const uint32_t row_bytes = (uint32_t)nb * BYTES;
     const uint32_t wbytes = (uint32_t)n * row_bytes;
@@ -595,7 +618,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_fused_kernel(const uint8_t* __re
         const int r = b / CPL, i = b % CPL;
         const int row = row_of(r), col = lane + 64 * i;
         const uint32_t off = (row < rend && col < nb)
-                                 ? (uint32_t)row * row_bytes + (uint32_t)col * BYTES
+                                 ? (uint32_t)mat_row(row) * row_bytes + (uint32_t)col * BYTES
                                  : RSRC_OOB;
         load_window<WORDS, !NB_EVEN>(rs, off, wbytes, win[b]);
     };
@@ -680,6 +703,43 @@ __global__ __launch_bounds__(NW * 64) void gemv_fused_kernel(const uint8_t* __re
         if ((lane & ((2 << SH) - 1)) == 0) {
             const int g = row_of(lane >> SH);
             if (g + 1 < rend) y[g >> 1] = (s * (1.0f / (1.0f + expf(-s)))) * up;
+        }
+    } else if constexpr (EPI == EPI_ROPE_KV) {
+        const float x2 = __shfl_down(s, 1 << SH);
+        if ((lane & ((2 << SH) - 1)) == 0) {
+            const int l1 = row_of(lane >> SH);
+            if (l1 < rend) {
+                const int r1 = mat_row(l1);  // row of x1; x2's row is r1 + half
+                const int head = r1 / fz.hd, i = r1 % fz.hd;
+                const int pos = *fz.pos + blockIdx.y;
+                const float x1 = s;
+                if (head < fz.n_heads + fz.n_kv) {
+                    const float c = fz.cos_t[(size_t)pos * half + i], sn = fz.sin_t[(size_t)pos * half + i];
+                    const float o1 = x1 * c - x2 * sn, o2 = x1 * sn + x2 * c;
+                    if (head < fz.n_heads) {
+                        y[r1] = o1;
+                        y[r1 + half] = o2;
+                    } else {
+                        const size_t ko = ((size_t)(head - fz.n_heads) * fz.max_seq + pos) * fz.hd + i;
+                        if (fz.kv_f16) {
+                            reinterpret_cast<_Float16*>(fz.kc)[ko] = (_Float16)o1;
+                            reinterpret_cast<_Float16*>(fz.kc)[ko + half] = (_Float16)o2;
+                        } else {
+                            reinterpret_cast<float*>(fz.kc)[ko] = o1;
+                            reinterpret_cast<float*>(fz.kc)[ko + half] = o2;
+                        }
+                    }
+                } else {
+                    const size_t vo = ((size_t)(head - fz.n_heads - fz.n_kv) * fz.max_seq + pos) * fz.hd + i;
+                    if (fz.kv_f16) {
+                        reinterpret_cast<_Float16*>(fz.vc)[vo] = (_Float16)x1;
+                        reinterpret_cast<_Float16*>(fz.vc)[vo + half] = (_Float16)x2;
+                    } else {
+                        reinterpret_cast<float*>(fz.vc)[vo] = x1;
+                        reinterpret_cast<float*>(fz.vc)[vo + half] = x2;
+                    }
+                }
+            }
         }
     } else if ((lane & ((1 << SH) - 1)) == 0) {
         const int row = row_of(lane >> SH);
@@ -856,7 +916,7 @@ void launch_nw(const uint8_t* w, int n, int nb, const float* x, size_t m, float*
     const dim3 grid((unsigned)((n + c.rpw - 1) / c.rpw), (unsigned)m), block(NW * 64);
     constexpr int RMAX = 8 / CPL;
     const int rpw = c.rpw;
-    if constexpr (RES == EPI_SWIGLU) {
+    if constexpr (RES == EPI_SWIGLU || RES == EPI_ROPE_KV) {
         // even row counts only (row pairs); RMAX 1 is rejected by the caller
         if constexpr (RMAX >= 4) {
             if (c.r >= 4)
@@ -880,7 +940,8 @@ void launch_nw(const uint8_t* w, int n, int nb, const float* x, size_t m, float*
 template <int WT, bool NATIVE, int CPL, bool EVEN>
 void launch_even(const uint8_t* w, int n, int nb, const float* x, size_t m, float* y,
                  hipStream_t s, const Cfg& c, size_t lds) {
-    const Fuse fz{nullptr, 0.0f, nb * 32};
+    Fuse fz{};
+    fz.xstride = nb * 32;
     if (c.nw == 4) launch_nw<WT, NATIVE, CPL, EVEN, 4>(w, n, nb, x, m, y, s, c, lds, fz);
     else if (c.nw == 8) launch_nw<WT, NATIVE, CPL, EVEN, 8>(w, n, nb, x, m, y, s, c, lds, fz);
     else launch_nw<WT, NATIVE, CPL, EVEN, 16>(w, n, nb, x, m, y, s, c, lds, fz);
@@ -927,18 +988,25 @@ void launch_q4k_nw(const uint8_t* w, int n, int nsb, const float* x, size_t m, f
     }
 }
 
-// Decoder fusion: Q4_0 float mode, 8-wave workgroups (two per CU), nb even.
+// Decoder fusion: Q4_0 float mode, nb even.  8-wave workgroups, two per CU;
+// rows longer than 4096 (their x, re-read by every workgroup, is long): one
+// 16-wave workgroup per CU.
 template <int PRO, int RES>
 void launch_q4_0_fused_ex(const uint8_t* w, int n, int nb, const float* x, size_t m, float* y,
                           hipStream_t s, size_t lds, const Fuse& fz) {
     const int cpl = cpl_for(nb);
+    constexpr int Q = (int)WType::Q4_0;
+    if (RES != EPI_SWIGLU && RES != EPI_ROPE_KV && cpl == 8) {
+        const Cfg c16 = pick_cfg(n, 16, 1, 1);
+        launch_nw<Q, false, 8, true, 16, PRO, RES>(w, n, nb, x, m, y, s, c16, lds, fz);
+        return;
+    }
     Cfg c = pick_cfg(n, 8, 8 / cpl, 2);
-    if (RES == EPI_SWIGLU) {
+    if (RES == EPI_SWIGLU || RES == EPI_ROPE_KV) {
         // whole row pairs per wave: R even, a workgroup takes NW * R rows
         c.r = (8 / cpl >= 4 && n >= 2 * 8 * 4 * 256) ? 4 : 2;
         c.rpw = 8 * c.r;
     }
-    constexpr int Q = (int)WType::Q4_0;
     switch (cpl) {
         case 2: launch_nw<Q, false, 2, true, 8, PRO, RES>(w, n, nb, x, m, y, s, c, lds, fz); break;
         case 4: launch_nw<Q, false, 4, true, 8, PRO, RES>(w, n, nb, x, m, y, s, c, lds, fz); break;
@@ -956,10 +1024,14 @@ hipError_t launch_gemv_q4_0_fused_ex(const uint8_t* w, size_t n, size_t k, const
     if (nb == 0 || (nb & 1) || k > fused_max_k(WType::Q4_0) || ((uintptr_t)x & 15) || (xstride & 3) ||
         (uint64_t)n * nb * Q4_0_BYTES > FUSED_MAX_WEIGHT_BYTES || m > 4)
         return hipErrorInvalidValue;
-    const Fuse fz{g, eps, (int)xstride};
+    Fuse fz{};
+    fz.g = g;
+    fz.eps = eps;
+    fz.xstride = (int)xstride;
     const size_t lds = (size_t)8 * 16 * nb;
     const int ni = (int)n;
     if (epilogue == EPI_SWIGLU && ((n & 1) || cpl_for(nb) > 4)) return hipErrorInvalidValue;
+    if (epilogue == EPI_ROPE_KV) return hipErrorInvalidValue;  // launch_gemv_q4_0_rope_kv
     if (prologue == PRO_RMSNORM && epilogue == EPI_STORE)
         launch_q4_0_fused_ex<PRO_RMSNORM, EPI_STORE>(w, ni, nb, x, m, y, s, lds, fz);
     else if (prologue == PRO_RMSNORM && epilogue == EPI_SWIGLU)
@@ -974,6 +1046,33 @@ hipError_t launch_gemv_q4_0_fused_ex(const uint8_t* w, size_t n, size_t k, const
         launch_q4_0_fused_ex<PRO_NONE, EPI_SWIGLU>(w, ni, nb, x, m, y, s, lds, fz);
     else
         return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv_q4_0_rope_kv(const uint8_t* w, size_t n, size_t k, const float* x, size_t m, float* y,
+                                    const float* g, float eps, const int* pos, const float* cos_t,
+                                    const float* sin_t, void* kc, void* vc, int n_heads, int n_kv, int hd,
+                                    int max_seq, bool kv_f16, hipStream_t s) {
+    if (n == 0 || m == 0) return hipSuccess;
+    const int nb = (int)(k / QK);
+    if (nb == 0 || (nb & 1) || cpl_for(nb) > 4 || ((uintptr_t)x & 15) || m > 4 || (hd & 1) ||
+        n != (size_t)(n_heads + 2 * n_kv) * hd || (uint64_t)n * nb * Q4_0_BYTES > FUSED_MAX_WEIGHT_BYTES)
+        return hipErrorInvalidValue;
+    Fuse fz{};
+    fz.g = g;
+    fz.eps = eps;
+    fz.xstride = (int)k;
+    fz.pos = pos;
+    fz.cos_t = cos_t;
+    fz.sin_t = sin_t;
+    fz.kc = kc;
+    fz.vc = vc;
+    fz.n_heads = n_heads;
+    fz.n_kv = n_kv;
+    fz.hd = hd;
+    fz.max_seq = max_seq;
+    fz.kv_f16 = kv_f16 ? 1 : 0;
+    launch_q4_0_fused_ex<PRO_RMSNORM, EPI_ROPE_KV>(w, (int)n, nb, x, m, y, s, (size_t)8 * 16 * nb, fz);
     return hipGetLastError();
 }
 

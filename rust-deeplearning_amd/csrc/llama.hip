@@ -149,114 +149,146 @@ constexpr int ATT_CHUNK = 64;
 
 // HD: head dim as a compile-time constant (64, 128, 256), so that all of a
 // key row's loads are issued before its dot product; 0: runtime hd.
+// A workgroup of ATT_WAVES waves covers ATT_WAVES chunks (ATT_SPAN keys):
+// wave w forms chunk w's max m_w, sum l_w and unnormalised context o_w; the
+// workgroup combines its chunks in LDS.  A row with more than ATT_SPAN keys
+// uses several workgroups, and the last of them to finish combines their
+// partials (device-scope counter, chunk order fixed: deterministic).
+constexpr int ATT_WAVES = 8;
+constexpr int ATT_SPAN = ATT_CHUNK * ATT_WAVES;
+
 template <typename KV, int HD>
-__global__ __launch_bounds__(64) void attention_chunk_kernel(const float* __restrict__ qkv, int qkv_dim,
-                                                             const int* __restrict__ pos_dev,
-                                                             const KV* __restrict__ kc,
-                                                             const KV* __restrict__ vc, int max_seq,
-                                                             int n_heads, int n_kv, int hd_rt, float scale,
-                                                             float* __restrict__ part, int nchunk) {
-    extern __shared__ float qs[];
+__global__ __launch_bounds__(64 * ATT_WAVES) void attention_kernel(
+    const float* __restrict__ qkv, int qkv_dim, const int* __restrict__ pos_dev, const KV* __restrict__ kc,
+    const KV* __restrict__ vc, int max_seq, int n_heads, int n_kv, int hd_rt, float scale,
+    float* __restrict__ part, int nspan, int* __restrict__ counters, float* __restrict__ out) {
+    extern __shared__ float sm[];  // q[hd] | o[ATT_WAVES][hd]
+    __shared__ float ml[ATT_WAVES][2];
+    __shared__ float wsc[1024];
+    __shared__ int last;
     const int hd = HD ? HD : hd_rt;
-    const int h = blockIdx.x, s = blockIdx.y, c = blockIdx.z, lane = threadIdx.x;
+    const int h = blockIdx.x, s = blockIdx.y, z = blockIdx.z;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int t = *pos_dev + s + 1;
-    const int p0 = c * ATT_CHUNK;
-    if (p0 >= t) return;  // whole wave
+    if (z * ATT_SPAN >= t) return;  // whole workgroup
+    float* qs = sm;
+    float* os = sm + hd;
     const int kvh = h / (n_heads / n_kv);
     const float* q = qkv + (size_t)s * qkv_dim + h * hd;
-    for (int d = lane; d < hd; d += 64) qs[d] = q[d];
+    for (int d = threadIdx.x; d < hd; d += 64 * ATT_WAVES) qs[d] = q[d];
     __syncthreads();
-    const int p = p0 + lane;
-    const bool valid = p < t;
-    // score of key p = lane's key
-    const KV* kr = kc + ((size_t)kvh * max_seq + (valid ? p : p0)) * hd;
-    constexpr int V = 16 / sizeof(KV);
-    typedef KV kvv __attribute__((ext_vector_type(V)));
-    float acc = 0.0f;
-    if constexpr (HD > 0) {
-        kvv kreg[HD / V];
+    const int p0 = z * ATT_SPAN + w * ATT_CHUNK;
+    float mx = -__builtin_inff(), l = 0.0f;
+    if (p0 < t) {  // wave-uniform
+        const int p = p0 + lane;
+        const bool valid = p < t;
+        const KV* kr = kc + ((size_t)kvh * max_seq + (valid ? p : p0)) * hd;
+        constexpr int V = 16 / sizeof(KV);
+        typedef KV kvv __attribute__((ext_vector_type(V)));
+        float acc = 0.0f;
+        if constexpr (HD > 0) {
+            kvv kreg[HD / V];
 #pragma unroll
-        for (int i = 0; i < HD / V; i++) kreg[i] = *reinterpret_cast<const kvv*>(kr + i * V);
+            for (int i = 0; i < HD / V; i++) kreg[i] = *reinterpret_cast<const kvv*>(kr + i * V);
 #pragma unroll
-        for (int i = 0; i < HD / V; i++)
+            for (int i = 0; i < HD / V; i++)
 #pragma unroll
-            for (int e = 0; e < V; e++) acc += qs[i * V + e] * (float)kreg[i][e];
-    } else {
-        for (int d = 0; d < hd; d += V) {
-            const kvv kv = *reinterpret_cast<const kvv*>(kr + d);
+                for (int e = 0; e < V; e++) acc += qs[i * V + e] * (float)kreg[i][e];
+        } else {
+            for (int d = 0; d < hd; d += V) {
+                const kvv kv = *reinterpret_cast<const kvv*>(kr + d);
 #pragma unroll
-            for (int e = 0; e < V; e++) acc += qs[d + e] * (float)kv[e];
-        }
-    }
-    const float sc = valid ? acc / scale : -__builtin_inff();
-    const float mx = wave_max(sc);
-    const float e = valid ? expf(sc - mx) : 0.0f;
-    const float l = wave_sum(e);
-    // context: lane owns dims 2 lane, 2 lane + 1 of each 128-dim slice
-    const KV* vb = vc + (size_t)kvh * max_seq * hd;
-    const int nvalid = min(ATT_CHUNK, t - p0);
-    float* po = part + (((size_t)s * n_heads + h) * nchunk + c) * (hd + 2);
-    for (int d0 = 0; d0 < hd; d0 += 128) {
-        const int d = d0 + 2 * lane;
-        float o0 = 0.0f, o1 = 0.0f;
-        if (d < hd) {
-            // branch-free so that all 64 row loads are in flight together: a
-            // key past the row's length re-reads the last valid row with weight 0
-#pragma unroll
-            for (int j = 0; j < ATT_CHUNK; j++) {
-                const float ej = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e), j));
-                typedef KV kv2 __attribute__((ext_vector_type(2)));
-                const int pj = p0 + min(j, nvalid - 1);
-                const kv2 v2 = *reinterpret_cast<const kv2*>(vb + (size_t)pj * hd + d);
-                o0 += ej * (float)v2[0];
-                o1 += ej * (float)v2[1];
+                for (int e = 0; e < V; e++) acc += qs[d + e] * (float)kv[e];
             }
-            po[2 + d] = o0;
-            po[2 + d + 1] = o1;
+        }
+        const float sc = valid ? acc / scale : -__builtin_inff();
+        mx = wave_max(sc);
+        const float e = valid ? expf(sc - mx) : 0.0f;
+        l = wave_sum(e);
+        const KV* vb = vc + (size_t)kvh * max_seq * hd;
+        const int nvalid = min(ATT_CHUNK, t - p0);
+        for (int d0 = 0; d0 < hd; d0 += 128) {
+            const int d = d0 + 2 * lane;
+            if (d < hd) {
+                float o0 = 0.0f, o1 = 0.0f;
+                // branch-free: a key past the row's length re-reads the last
+                // valid row with weight 0, so all row loads are in flight together
+#pragma unroll
+                for (int j = 0; j < ATT_CHUNK; j++) {
+                    const float ej =
+                        __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e), j));
+                    typedef KV kv2 __attribute__((ext_vector_type(2)));
+                    const int pj = p0 + min(j, nvalid - 1);
+                    const kv2 v2 = *reinterpret_cast<const kv2*>(vb + (size_t)pj * hd + d);
+                    o0 += ej * (float)v2[0];
+                    o1 += ej * (float)v2[1];
+                }
+                os[w * hd + d] = o0;
+                os[w * hd + d + 1] = o1;
+            }
         }
     }
     if (lane == 0) {
-        po[0] = mx;
-        po[1] = l;
-    }
-}
-
-// One thread per chunk reads (m_c, l_c); the weights exp(m_c - M) / L go to
-// LDS; each output dim then sums its chunks in batches of 8 branch-free loads.
-__global__ __launch_bounds__(128) void attention_combine_kernel(const float* __restrict__ part,
-                                                                const int* __restrict__ pos_dev, int n_heads,
-                                                                int hd, int nchunk, float* __restrict__ out) {
-    __shared__ float wc[1024];
-    __shared__ float red[2];
-    const int h = blockIdx.x, s = blockIdx.y;
-    const int t = *pos_dev + s + 1;
-    const int nc = (t + ATT_CHUNK - 1) / ATT_CHUNK;  // <= nchunk <= 1024
-    const float* pb = part + ((size_t)s * n_heads + h) * nchunk * (hd + 2);
-    if (threadIdx.x < 64) {
-        float M = -__builtin_inff();
-        for (int c = threadIdx.x; c < nc; c += 64) M = fmaxf(M, pb[(size_t)c * (hd + 2)]);
-        M = wave_max(M);
-        float L = 0.0f;
-        for (int c = threadIdx.x; c < nc; c += 64) {
-            const float w = expf(pb[(size_t)c * (hd + 2)] - M);
-            wc[c] = w;
-            L += pb[(size_t)c * (hd + 2) + 1] * w;
-        }
-        L = wave_sum(L);
-        if (threadIdx.x == 0) red[0] = L;
+        ml[w][0] = mx;
+        ml[w][1] = l;
     }
     __syncthreads();
-    const float invL = 1.0f / red[0];
+    // combine this workgroup's chunks (inactive waves carry m = -inf, l = 0)
+    const int nw = min(ATT_WAVES, (t - z * ATT_SPAN + ATT_CHUNK - 1) / ATT_CHUNK);
+    float M = -__builtin_inff();
+    for (int c = 0; c < nw; c++) M = fmaxf(M, ml[c][0]);
+    float L = 0.0f;
+    for (int c = 0; c < nw; c++) L += ml[c][1] * expf(ml[c][0] - M);
+    const int nz = (t + ATT_SPAN - 1) / ATT_SPAN;
     float* o = out + (size_t)s * n_heads * hd + h * hd;
-    for (int d = threadIdx.x; d < hd; d += 128) {
-        float O = 0.0f;
-        for (int c0 = 0; c0 < nc; c0 += 8) {
-            float v[8];
-#pragma unroll
-            for (int i = 0; i < 8; i++) v[i] = pb[(size_t)min(c0 + i, nc - 1) * (hd + 2) + 2 + d];
-#pragma unroll
-            for (int i = 0; i < 8; i++) O += (c0 + i < nc) ? v[i] * wc[c0 + i] : 0.0f;
+    if (nz == 1) {
+        const float invL = 1.0f / L;
+        for (int d = threadIdx.x; d < hd; d += 64 * ATT_WAVES) {
+            float O = 0.0f;
+            for (int c = 0; c < nw; c++) O += os[c * hd + d] * expf(ml[c][0] - M);
+            o[d] = O * invL;
         }
+        return;
+    }
+    // several workgroups: partial (M, L, O) to global, the last one combines
+    float* po = part + (((size_t)s * n_heads + h) * nspan + z) * (hd + 2);
+    for (int d = threadIdx.x; d < hd; d += 64 * ATT_WAVES) {
+        float O = 0.0f;
+        for (int c = 0; c < nw; c++) O += os[c * hd + d] * expf(ml[c][0] - M);
+        po[2 + d] = O;
+    }
+    if (threadIdx.x == 0) {
+        po[0] = M;
+        po[1] = L;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int* cnt = counters + (size_t)s * n_heads + h;
+        const int old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        last = (old == nz - 1);
+        if (last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!last) return;
+    const float* pb = part + ((size_t)s * n_heads + h) * nspan * (hd + 2);
+    if (w == 0) {
+        float MM = -__builtin_inff();
+        for (int c = lane; c < nz; c += 64) MM = fmaxf(MM, pb[(size_t)c * (hd + 2)]);
+        MM = wave_max(MM);
+        float LL = 0.0f;
+        for (int c = lane; c < nz; c += 64) {
+            const float wgt = expf(pb[(size_t)c * (hd + 2)] - MM);
+            wsc[c] = wgt;
+            LL += pb[(size_t)c * (hd + 2) + 1] * wgt;
+        }
+        LL = wave_sum(LL);
+        if (lane == 0) ml[0][1] = LL;
+    }
+    __syncthreads();
+    const float invL = 1.0f / ml[0][1];
+    for (int d = threadIdx.x; d < hd; d += 64 * ATT_WAVES) {
+        float O = 0.0f;
+        for (int c = 0; c < nz; c++) O += pb[(size_t)c * (hd + 2) + 2 + d] * wsc[c];
         o[d] = O * invL;
     }
 }
@@ -394,8 +426,9 @@ struct LlamaModel {
     int *tokens = nullptr, *pos = nullptr, *step = nullptr, *out_tokens = nullptr;
     size_t out_cap = 0;
     void* gemm_scratch = nullptr;
-    float* att_part = nullptr;  // [max_batch][n_heads][chunks of max_seq][hd + 2]
-    int att_nchunk = 0;
+    float* att_part = nullptr;  // [max_batch][n_heads][spans of max_seq][hd + 2]
+    int* att_cnt = nullptr;     // [max_batch][n_heads] finished-chunk counters (zero between launches)
+    int att_nspan = 0;
     hipStream_t stream = nullptr;
     hipGraphExec_t decode_exec = nullptr;
     hipGraph_t decode_graph = nullptr;
@@ -442,33 +475,37 @@ struct LlamaModel {
     // Attention chunks to launch for m rows starting at the current position
     // (capture_any_pos: the launch is recorded once for every position).
     bool capture_any_pos = false;
-    int chunks_needed(size_t m) const {
+    int chunks_needed(size_t m) const {  // workgroups of ATT_SPAN keys
         const size_t upto = capture_any_pos ? (size_t)cfg.max_seq : host_pos + m;
-        return (int)((upto + ATT_CHUNK - 1) / ATT_CHUNK);
+        return (int)((upto + ATT_SPAN - 1) / ATT_SPAN);
     }
 
+    void* kv_layer(void* base, int l) const {
+        return reinterpret_cast<uint8_t*>(base) + (size_t)l * kv_layer_elems() * kv_elem();
+    }
+
+    // RoPE + cache write (unless the qkv launch did it), then attention.
     template <typename KV>
-    hipError_t layer_attention(int l, size_t m) {
-        KV* kcl = reinterpret_cast<KV*>(kc) + (size_t)l * kv_layer_elems();
-        KV* vcl = reinterpret_cast<KV*>(vc) + (size_t)l * kv_layer_elems();
+    hipError_t layer_attention(int l, size_t m, bool rope = true) {
+        KV* kcl = reinterpret_cast<KV*>(kv_layer(kc, l));
+        KV* vcl = reinterpret_cast<KV*>(kv_layer(vc, l));
         const int hd = cfg.head_dim;
-        hipLaunchKernelGGL(rope_kv_kernel<KV>, dim3(cfg.n_heads + cfg.n_kv_heads, (unsigned)m), dim3(hd / 2), 0,
-                           stream, qkv, qkv_dim, pos, cos_t, sin_t, cfg.n_heads, cfg.n_kv_heads, hd, kcl, vcl,
-                           cfg.max_seq);
+        if (rope)
+            hipLaunchKernelGGL(rope_kv_kernel<KV>, dim3(cfg.n_heads + cfg.n_kv_heads, (unsigned)m), dim3(hd / 2), 0,
+                               stream, qkv, qkv_dim, pos, cos_t, sin_t, cfg.n_heads, cfg.n_kv_heads, hd, kcl, vcl,
+                               cfg.max_seq);
         const float scale = sqrtf((float)hd);
         // chunks that can hold keys for these rows (every chunk of the cache
         // when the launch is captured for replay at any position)
         const int nz = chunks_needed(m);
         const dim3 grid(cfg.n_heads, (unsigned)m, (unsigned)nz);
-        const size_t lds = (size_t)hd * sizeof(float);
-        auto kern = (hd == 128) ? attention_chunk_kernel<KV, 128>
-                  : (hd == 64)  ? attention_chunk_kernel<KV, 64>
-                  : (hd == 256) ? attention_chunk_kernel<KV, 256>
-                                : attention_chunk_kernel<KV, 0>;
-        hipLaunchKernelGGL(kern, grid, dim3(64), lds, stream, qkv, qkv_dim, pos, kcl, vcl, cfg.max_seq,
-                           cfg.n_heads, cfg.n_kv_heads, hd, scale, att_part, att_nchunk);
-        hipLaunchKernelGGL(attention_combine_kernel, dim3(cfg.n_heads, (unsigned)m), dim3(128), 0, stream,
-                           att_part, pos, cfg.n_heads, hd, att_nchunk, att);
+        const size_t lds = (size_t)(1 + ATT_WAVES) * hd * sizeof(float);
+        auto kern = (hd == 128) ? attention_kernel<KV, 128>
+                  : (hd == 64)  ? attention_kernel<KV, 64>
+                  : (hd == 256) ? attention_kernel<KV, 256>
+                                : attention_kernel<KV, 0>;
+        hipLaunchKernelGGL(kern, grid, dim3(64 * ATT_WAVES), lds, stream, qkv, qkv_dim, pos, kcl, vcl, cfg.max_seq,
+                           cfg.n_heads, cfg.n_kv_heads, hd, scale, att_part, att_nspan, att_cnt, att);
         return hipGetLastError();
     }
 
@@ -483,10 +520,12 @@ struct LlamaModel {
         if (e != hipSuccess) return e;
         for (int l = 0; l < cfg.n_layers; l++) {
             Layer& L = layers[l];
-            // qkv = rms_norm(x) . [Wq; Wk; Wv]^T
-            e = launch_gemv_q4_0_fused_ex(L.qkv.dev, L.qkv.n, d, x, d, m, qkv, 1, L.attn_norm, eps, 0, stream);
+            // q = rope(rms_norm(x) . Wq^T); k, v -> cache (RoPE on k) in the same launch
+            e = launch_gemv_q4_0_rope_kv(L.qkv.dev, L.qkv.n, d, x, m, qkv, L.attn_norm, eps, pos, cos_t, sin_t,
+                                         kv_layer(kc, l), kv_layer(vc, l), cfg.n_heads, cfg.n_kv_heads,
+                                         cfg.head_dim, cfg.max_seq, cfg.kv_f16 != 0, stream);
             if (e != hipSuccess) return e;
-            e = cfg.kv_f16 ? layer_attention<_Float16>(l, m) : layer_attention<float>(l, m);
+            e = cfg.kv_f16 ? layer_attention<_Float16>(l, m, false) : layer_attention<float>(l, m, false);
             if (e != hipSuccess) return e;
             // x += att . Wo^T
             e = launch_gemv_q4_0_fused_ex(L.o.dev, L.o.n, q_dim, att, q_dim, m, x, 0, nullptr, 0.0f, 1, stream);
@@ -629,12 +668,16 @@ rdl_status rdl_llama_create(const rdl_llama_config* cfg, rdl_llama** out) {
     if ((e = M.alloc_t(&M.out_tokens, M.out_cap)) != hipSuccess) return fail_free(e);
     const size_t kmax = (size_t)std::max(std::max(c.dim, c.ffn_dim), M.q_dim);
     if ((e = M.alloc(&M.gemm_scratch, rdl::gemm_scratch_bytes(mb, kmax))) != hipSuccess) return fail_free(e);
+    // (row-pair epilogues need at most 4 columns per lane: dim <= 8192)
     M.fusable = (c.dim / 32) % 2 == 0 && (M.q_dim / 32) % 2 == 0 && (c.ffn_dim / 32) % 2 == 0 &&
+                c.dim / 32 <= 256 &&
                 (uint64_t)2 * c.ffn_dim * (c.dim / 32) * rdl::Q4_0_BYTES <= rdl::FUSED_MAX_WEIGHT_BYTES &&
                 (uint64_t)c.vocab * (c.dim / 32) * rdl::Q4_0_BYTES <= rdl::FUSED_MAX_WEIGHT_BYTES;
-    M.att_nchunk = (c.max_seq + rdl::ATT_CHUNK - 1) / rdl::ATT_CHUNK;
-    if ((e = M.alloc_t(&M.att_part, mb * c.n_heads * (size_t)M.att_nchunk * (c.head_dim + 2))) != hipSuccess)
+    M.att_nspan = (c.max_seq + rdl::ATT_SPAN - 1) / rdl::ATT_SPAN;
+    if ((e = M.alloc_t(&M.att_part, mb * c.n_heads * (size_t)M.att_nspan * (c.head_dim + 2))) != hipSuccess)
         return fail_free(e);
+    if ((e = M.alloc_t(&M.att_cnt, mb * c.n_heads)) != hipSuccess) return fail_free(e);
+    if ((e = hipMemset(M.att_cnt, 0, mb * c.n_heads * sizeof(int))) != hipSuccess) return fail_free(e);
     // RoPEFreqs::new (rope.rs:93-108) in f32 with the C library's powf / cosf / sinf
     const int half = c.head_dim / 2;
     M.cos_h.resize((size_t)c.max_seq * half);

@@ -148,6 +148,14 @@ hipError_t launch_gemv_q4_0_fused_ex(const uint8_t* w, size_t n, size_t k, const
                                      size_t m, float* y, int prologue, const float* g, float eps,
                                      int epilogue, hipStream_t s);
 
+// The decoder's q/k/v projection in one launch: y = rms_norm(x, g) . [Wq; Wk; Wv]^T
+// with RoPE at positions *pos + row applied to q (in y) and k, and k, v
+// written into the cache ([n_kv][max_seq][hd], f16 or f32); m <= 4.
+hipError_t launch_gemv_q4_0_rope_kv(const uint8_t* w, size_t n, size_t k, const float* x, size_t m, float* y,
+                                    const float* g, float eps, const int* pos, const float* cos_t,
+                                    const float* sin_t, void* kc, void* vc, int n_heads, int n_kv, int hd,
+                                    int max_seq, bool kv_f16, hipStream_t s);
+
 // int32 block partials of the Q4_0 x Q8_0 path for one activation row.
 hipError_t launch_q4_0_block_dots(const uint8_t* w, size_t n, size_t k, const NativeRec* rec,
                                   int32_t* partials, hipStream_t s);
