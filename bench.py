@@ -1,18 +1,24 @@
-"""Benchmark of the Q4_0 decode GEMV on one MI355X.
+"""Benchmark of the quantized Linear hot path on one MI355X.
 
-A step is one batch-1 Linear forward of the Llama-7B FFN up/gate shape
-(W 11008x4096 GGUF Q4_0, x f32 [4096]) through the C ABI
-(rdl_linear_forward_dev: one kernel, activation prep fused), i.e.
-rustml_quant::matmul_f32_q4 (quantize.rs:265-320) with the weight resident in
-HBM.  Consecutive steps use different weight copies (more than the 256 MB
-Infinity Cache in total) so each step streams its weight from HBM.
+Headline (`value`): the Q4_0 decode GEMV of configs[1].  A step is one
+batch-1 Linear forward of the Llama-7B FFN up/gate shape (W 11008x4096 GGUF
+Q4_0, x f32 [4096]) through the C ABI (rdl_linear_forward_dev: one kernel,
+activation prep fused), i.e. rustml_quant::matmul_f32_q4 (quantize.rs:265-320)
+with the weight resident in HBM.  Consecutive steps use different weight
+copies (more than the 256 MB Infinity Cache in total) so each step streams
+its weight from HBM.
 
 Timed region: the K steps are captured once in a HIP graph (so host launch
 overhead is not measured) and replayed once between two events.  The
 roofline figure times each GEMV kernel at its boundaries (hipExtLaunchKernel
 events) over K separate launches.
 
-Prints one JSON line (see the keys below).
+The same JSON line carries, under "workloads", the other configurations of
+the metric: configs[0] (Q8_0 GEMV) and configs[2] (Q4_K GEMV pair) timed the
+same way, configs[3] (Q4_0 prefill GEMM, M in {16, 64, 512, 2048}) as
+TFLOP/s, and configs[4] (random-init 7B Q4_0 Llama, 128-token prompt, 256
+greedy tokens) as decode tokens/s with its HBM roofline per token.
+`--workload` restricts the run to one of them (for profiling).
 """
 import argparse
 import json
@@ -27,15 +33,23 @@ sys.path.insert(0, os.path.join(ROOT, "rust-deeplearning_amd"))
 
 METRIC = "Q4_0/Q4_K GEMV achieved HBM GB/s (% peak); 7B Q4_0 decode tokens/s"
 PEAK_HBM_GBPS = 8000.0
+PEAK_F16_TFLOPS = 2500.0  # dense f16/bf16 MFMA, MI355X
 N_OUT, K_IN = 11008, 4096
 SEED = 0x5EED0002
 # the kernel the library launches for this workload (8-wave workgroups, 3 rows per wave)
 KERNEL_KEY = "gemv_fused_kernel<2, false, 3, 2, true, 8>|config2"
+# configs[4]
+LLAMA_SEED = 0x5EED0005
+PROMPT_LEN, GEN_TOKENS = 128, 256
+
+# GGML type id -> (elements per block, bytes per block)
+BLOCK = {2: (32, 18), 8: (32, 34), 12: (256, 144)}
 
 
-def algorithmic_bytes(n, k):
+def algorithmic_bytes(n, k, dtype=2):
     """Weight blocks + x (f32) + y (f32), each read or written once."""
-    return n * (k // 32) * 18 + 4 * k + 4 * n
+    qk, bb = BLOCK[dtype]
+    return n * (k // qk) * bb + 4 * k + 4 * n
 
 
 def measured_traffic(kernel_key):
@@ -54,8 +68,6 @@ def measured_traffic(kernel_key):
 def cpu_baseline(budget_s=10.0):
     """The reference decomposition of an M=1 matmul_f32_q4 (one rayon task -> one core),
     restated in C (oracle/), timed on this host over a bounded sample."""
-    import numpy as np
-
     from oracle import oracle as orc
     from rdlquant import synth
 
@@ -84,6 +96,237 @@ def cpu_baseline(budget_s=10.0):
     }
 
 
+class Rig:
+    """Device, stream and rotating weight copies for the GEMV/GEMM timings."""
+
+    def __init__(self):
+        import torch
+
+        import rdlquant as rq
+        from rdlquant import synth
+
+        self.torch, self.rq, self.synth = torch, rq, synth
+        self.dev = torch.device("cuda:0")
+        torch.cuda.set_device(self.dev)
+        self.stream = torch.cuda.current_stream()
+
+    def weight_copies(self, dtype, n, k, seed, min_total=600 << 20, min_copies=8):
+        torch, rq = self.torch, self.rq
+        w_host = self.synth.weights(dtype, n, k, seed)
+        nbytes = w_host.size
+        copies = max(min_copies, -(-min_total // nbytes))
+        w0 = torch.from_numpy(w_host).to(self.dev)
+        out = []
+        for _ in range(copies):
+            t = torch.empty(nbytes + 256, dtype=torch.uint8, device=self.dev)
+            t[:nbytes].copy_(w0)
+            out.append((t, rq.Weight.wrap_device(t.data_ptr(), nbytes, dtype, n, k, t)))
+        return w_host, out
+
+    def time_gemv(self, weights, x, y, steps, warmup):
+        """(graph-replay ms per step, sorted per-launch kernel ms) for y = W_i x."""
+        torch, rq = self.torch, self.rq
+        sh = self.stream.cuda_stream
+
+        def step(i, s_handle):
+            weights[i % len(weights)][1].forward_dev(x.data_ptr(), 1, y.data_ptr(), rq.MODE_FLOAT, s_handle)
+
+        for i in range(warmup):
+            step(i, sh)
+        torch.cuda.synchronize()
+        # capture the K steps in one graph; one untimed replay, then the timed one
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            cap = torch.cuda.current_stream().cuda_stream
+            for i in range(steps):
+                step(i, cap)
+        graph.replay()
+        torch.cuda.synchronize()
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record(self.stream)
+        graph.replay()
+        t1.record(self.stream)
+        torch.cuda.synchronize()
+        ms_per_step = t0.elapsed_time(t1) / steps
+        del graph
+
+        # kernel-boundary timing over K separate launches
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in range(steps)]
+        for a, b in evs:  # materialize the events
+            a.record(self.stream)
+            b.record(self.stream)
+        torch.cuda.synchronize()
+        for i, (a, b) in enumerate(evs):
+            rq.time_next_launch(a.cuda_event, b.cuda_event)
+            step(i, sh)
+        torch.cuda.synchronize()
+        kern_ms = sorted(a.elapsed_time(b) for a, b in evs)
+        return ms_per_step, kern_ms
+
+
+def exact_check(rig, weight, x, y, m, n, k):
+    """y within 1e-3 rel + 1e-4 abs of the exact (f64) product over the weight's
+    f32 values (Tensor::to_f32 / dequantize_q4k, expanded by the library's
+    bit-exact row dequantization); torch does the f64 product on the device."""
+    torch = rig.torch
+    rows = torch.arange(n, dtype=torch.int32, device=rig.dev)
+    wf = torch.empty(n, k, dtype=torch.float32, device=rig.dev)
+    weight.dequantize_rows_dev(rows.data_ptr(), n, wf.data_ptr(), rig.stream.cuda_stream)
+    want = x.reshape(m, k).double() @ wf.double().T
+    got = y.reshape(m, n).double()
+    ok = bool(((got - want).abs() <= 1e-4 + 1e-3 * want.abs()).all().item())
+    del wf
+    return ok
+
+
+def gemv_line(rig, name, dtype, n, k, seed, steps, warmup):
+    """One GEMV configuration: throughput, kernel roofline and a parity spot check."""
+    torch = rig.torch
+    w_host, weights = rig.weight_copies(dtype, n, k, seed)
+    x_host = rig.synth.activations(1, k, seed + 100)
+    x = torch.from_numpy(x_host.reshape(-1)).to(rig.dev)
+    y = torch.empty(n, dtype=torch.float32, device=rig.dev)
+    ms, kern_ms = rig.time_gemv(weights, x, y, steps, warmup)
+    kavg = sum(kern_ms) / len(kern_ms)
+    abytes = algorithmic_bytes(n, k, dtype)
+    ok = exact_check(rig, weights[0][1], x, y, 1, n, k)
+    copies = len(weights)
+    del weights
+    torch.cuda.empty_cache()
+    return {
+        "workload": name,
+        "value": round(abytes / (ms * 1e-3) / 1e9, 2),
+        "unit": "GB/s",
+        "ms_per_step": round(ms, 6),
+        "algorithmic_bytes_per_step": abytes,
+        "weight_copies_rotated": copies,
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(abytes / (kavg * 1e-3) / 1e9, 2),
+            "peak": PEAK_HBM_GBPS,
+            "unit": "GB/s",
+            "frac": round(abytes / (kavg * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
+            "kernel_avg_us": round(kavg * 1e3, 3),
+            "kernel_median_us": round(kern_ms[len(kern_ms) // 2] * 1e3, 3),
+        },
+        "parity_vs_exact": ok,
+    }
+
+
+def gemm_lines(rig, ms_list, seed=0x5EED0004):
+    """Y = X W^T, W 4096x4096 Q4_0, X f32 [M, 4096]; the whole call
+    (activation split + MFMA GEMM) timed over a loop of launches."""
+    torch, rq = rig.torch, rig.rq
+    n = k = 4096
+    w_host, weights = rig.weight_copies(2, n, k, seed, min_copies=16)
+    s = rig.stream
+    out = []
+    for m in ms_list:
+        x_host = rig.synth.activations(m, k, seed + 100 + m)
+        x = torch.from_numpy(x_host).to(rig.dev)
+        y = torch.empty(m, n, dtype=torch.float32, device=rig.dev)
+        for i in range(10):
+            weights[i % len(weights)][1].forward_dev(x.data_ptr(), m, y.data_ptr(), rq.MODE_FLOAT, s.cuda_stream)
+        torch.cuda.synchronize()
+        it = 200 if m <= 512 else 60
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(s)
+        for i in range(it):
+            weights[i % len(weights)][1].forward_dev(x.data_ptr(), m, y.data_ptr(), rq.MODE_FLOAT, s.cuda_stream)
+        b.record(s)
+        torch.cuda.synchronize()
+        ms = a.elapsed_time(b) / it
+        flops = 2.0 * m * n * k
+        abytes = n * (k // 32) * 18 + 4 * m * k + 4 * m * n
+        ok = exact_check(rig, weights[0][1], x, y, m, n, k)
+        tflops = flops / (ms * 1e-3) / 1e12
+        gbps = abytes / (ms * 1e-3) / 1e9
+        bound = "mfma" if flops / abytes > PEAK_F16_TFLOPS * 1e12 / (PEAK_HBM_GBPS * 1e9) else "hbm"
+        out.append({
+            "workload": f"config4 M={m}",
+            "value": round(tflops, 2),
+            "unit": "TFLOP/s",
+            "ms_per_call": round(ms, 5),
+            "hbm_GBs": round(gbps, 1),
+            "roofline": {
+                "bound": bound,
+                "achieved": round(tflops, 2) if bound == "mfma" else round(gbps, 1),
+                "peak": PEAK_F16_TFLOPS if bound == "mfma" else PEAK_HBM_GBPS,
+                "unit": "TFLOP/s" if bound == "mfma" else "GB/s",
+                "frac": round(tflops / PEAK_F16_TFLOPS if bound == "mfma" else gbps / PEAK_HBM_GBPS, 4),
+            },
+            "parity_vs_exact": ok,
+        })
+        del x, y
+    del weights
+    torch.cuda.empty_cache()
+    return out
+
+
+def decode_bytes_per_token(cfg, ctx_mean):
+    """Q4_0 Linear + lm_head weight bytes, one embedding row, and f16 K/V reads
+    over ctx_mean cached positions, per decode token."""
+    d, f, hd = cfg.dim, cfg.ffn_dim, cfg.head_dim
+    per_layer = (d * cfg.n_heads * hd + 2 * d * cfg.n_kv_heads * hd + cfg.n_heads * hd * d + 3 * d * f)
+    params = cfg.n_layers * per_layer + cfg.vocab * d
+    kv = cfg.n_layers * 2 * cfg.n_kv_heads * hd * (2 if cfg.kv_f16 else 4)
+    return params // 32 * 18 + (d // 32) * 18 + int(kv * ctx_mean)
+
+
+def decode_line(rig, reps=2):
+    """random-init 7B Q4_0 Llama, greedy decode of 256 tokens after a
+    128-token prompt, each step one replay of the captured decode graph."""
+    import numpy as np
+
+    from rdlquant.llama import LlamaConfig, LlamaModel
+
+    cfg = LlamaConfig()
+    model = LlamaModel(cfg)
+    model.init_random(LLAMA_SEED)
+    prompt = np.random.default_rng(LLAMA_SEED).integers(0, cfg.vocab, PROMPT_LEN)
+    runs = []
+    toks0 = None
+    for _ in range(reps + 1):  # the first run captures the graph; not timed
+        model.reset()
+        toks = model.generate_greedy(prompt, GEN_TOKENS + 1)
+        runs.append(model.last_timing())
+        if toks0 is None:
+            toks0 = toks
+        elif not np.array_equal(toks, toks0):
+            raise RuntimeError("greedy decode is not deterministic across runs")
+    model.close()
+    rig.torch.cuda.empty_cache()
+    decode_ms = min(r[1] for r in runs[1:])
+    prefill_ms = min(r[0] for r in runs[1:])
+    ms_tok = decode_ms / GEN_TOKENS
+    # positions attended by the 256 steps: PROMPT_LEN+1 .. PROMPT_LEN+GEN_TOKENS
+    ctx_mean = PROMPT_LEN + (GEN_TOKENS + 1) / 2
+    bpt = decode_bytes_per_token(cfg, ctx_mean)
+    gbps = bpt / (ms_tok * 1e-3) / 1e9
+    return {
+        "workload": "config5: random-init Llama-7B-shape Q4_0 (32 layers, 4096, 32/8 heads x 128, "
+                    "FFN 14336, vocab 32000), f16 KV, 128-token prompt, 256 greedy tokens",
+        "value": round(GEN_TOKENS / (decode_ms * 1e-3), 1),
+        "unit": "tokens/s",
+        "ms_per_token": round(ms_tok, 4),
+        "prefill_ms_128_tokens": round(prefill_ms, 3),
+        "prefill_tokens_s": round(PROMPT_LEN / (prefill_ms * 1e-3), 1),
+        "bytes_per_token": bpt,
+        "tokens_s_at_100pct_hbm": round(PEAK_HBM_GBPS * 1e9 / bpt, 1),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(gbps, 1),
+            "peak": PEAK_HBM_GBPS,
+            "unit": "GB/s",
+            "frac": round(gbps / PEAK_HBM_GBPS, 4),
+        },
+        "first_tokens": [int(t) for t in toks0[:8]],
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -92,6 +335,8 @@ def main():
     ap.add_argument("--copies", type=int, default=24)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--workload", default="all", choices=["all", "gemv", "q8_0", "q4_k", "gemm", "decode"],
+                    help="all: the headline line plus every other configuration; otherwise only one")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="first run 3 plain device copies of this many MiB (a known-size "
                          "reference for HBM traffic counters)")
@@ -102,16 +347,11 @@ def main():
               "all-gather of y).", file=sys.stderr)
         sys.exit(2)
 
-    import numpy as np
     import torch
 
-    import rdlquant as rq
-    from rdlquant import synth
-
-    dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
-    stream = torch.cuda.current_stream()
-    sh = stream.cuda_stream
+    rig = Rig()
+    rq, synth = rig.rq, rig.synth
+    dev = rig.dev
 
     if args.calib_copy_mib > 0:
         src = torch.ones(args.calib_copy_mib << 18, dtype=torch.float32, device=dev)
@@ -120,6 +360,23 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+
+    wl = args.workload
+    if wl in ("q8_0", "q4_k", "gemm", "decode"):
+        if wl == "q8_0":
+            line = gemv_line(rig, "config1: Q8_0 GEMV 4096x4096", 8, 4096, 4096, 0x5EED0001,
+                             args.steps, args.warmup)
+        elif wl == "q4_k":
+            line = [gemv_line(rig, "config3 up: Q4_K GEMV 14336x4096", 12, 14336, 4096, 0x5EED0003,
+                              args.steps, args.warmup),
+                    gemv_line(rig, "config3 down: Q4_K GEMV 4096x14336", 12, 4096, 14336, 0x5EED0013,
+                              args.steps, args.warmup)]
+        elif wl == "gemm":
+            line = gemm_lines(rig, [16, 64, 512, 2048])
+        else:
+            line = decode_line(rig)
+        print(json.dumps(line), flush=True)
+        return
 
     wbytes = N_OUT * (K_IN // 32) * 18
     w_host = synth.q4_0_weights(N_OUT, K_IN, SEED)
@@ -132,55 +389,16 @@ def main():
     del w0
     x = torch.from_numpy(synth.activations(1, K_IN, SEED + 100).reshape(-1)).to(dev)
     y = torch.empty(N_OUT, dtype=torch.float32, device=dev)
-
-    def step(i, s_handle):
-        weights[i % len(weights)][1].forward_dev(x.data_ptr(), 1, y.data_ptr(), rq.MODE_FLOAT, s_handle)
-
-    for i in range(args.warmup):
-        step(i, sh)
-    torch.cuda.synchronize()
-
-    # capture the K steps in one graph; one untimed replay, then the timed one
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        cap = torch.cuda.current_stream().cuda_stream
-        for i in range(args.steps):
-            step(i, cap)
-    graph.replay()
-    torch.cuda.synchronize()
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
-    t0.record(stream)
-    graph.replay()
-    t1.record(stream)
-    torch.cuda.synchronize()
-    total_ms = t0.elapsed_time(t1)
-    ms_per_step = total_ms / args.steps
-
-    # kernel-boundary timing of the GEMV kernel over K separate launches
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(args.steps)]
-    for a, b in evs:  # materialize the events
-        a.record(stream)
-        b.record(stream)
-    torch.cuda.synchronize()
-    for i, (a, b) in enumerate(evs):
-        rq.time_next_launch(a.cuda_event, b.cuda_event)
-        step(i, sh)
-    torch.cuda.synchronize()
-    kern_ms = sorted(a.elapsed_time(b) for a, b in evs)
+    ms_per_step, kern_ms = rig.time_gemv(weights, x, y, args.steps, args.warmup)
     kern_avg_ms = sum(kern_ms) / len(kern_ms)
 
     abytes = algorithmic_bytes(N_OUT, K_IN)
     value = abytes / (ms_per_step * 1e-3) / 1e9
     achieved = abytes / (kern_avg_ms * 1e-3) / 1e9
 
-    # correctness spot check of the last step against the oracle
-    from oracle import oracle as orc
-
-    want = orc.matmul("q4", synth.activations(1, K_IN, SEED + 100), w_host, 1, K_IN, N_OUT, threads=8)
-    got = y.cpu().numpy()
-    parity_ok = bool(np.all(np.abs(got - want) <= 1e-4 + 1e-3 * np.abs(want)))
+    parity_ok = exact_check(rig, weights[0][1], x, y, 1, N_OUT, K_IN)
+    del weights
+    torch.cuda.empty_cache()
 
     out = {
         "metric": METRIC,
@@ -202,7 +420,7 @@ def main():
             "weight_bytes_total": wbytes * args.copies,
             "algorithmic_bytes_per_step": abytes,
             "pct_of_hbm_peak": round(100 * value / PEAK_HBM_GBPS, 2),
-            "parity_vs_oracle": parity_ok,
+            "parity_vs_exact": parity_ok,
         },
         "roofline": {
             "bound": "hbm",
@@ -218,6 +436,19 @@ def main():
                               "scaled by a 256 MiB copy)",
         },
     }
+    if wl == "all":
+        sub_steps = min(args.steps, 500)
+        sub_warm = min(args.warmup, 50)
+        out["workloads"] = {
+            "config1_q8_0": gemv_line(rig, "config1: Q8_0 GEMV 4096x4096", 8, 4096, 4096, 0x5EED0001,
+                                      sub_steps, sub_warm),
+            "config3_q4_k_up": gemv_line(rig, "config3 up: Q4_K GEMV 14336x4096", 12, 14336, 4096,
+                                         0x5EED0003, sub_steps, sub_warm),
+            "config3_q4_k_down": gemv_line(rig, "config3 down: Q4_K GEMV 4096x14336", 12, 4096, 14336,
+                                           0x5EED0013, sub_steps, sub_warm),
+            "config4_gemm": gemm_lines(rig, [16, 64, 512, 2048]),
+            "config5_decode": decode_line(rig),
+        }
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(out), flush=True)

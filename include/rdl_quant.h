@@ -204,10 +204,13 @@ rdl_status rdl_linear_fused_dev(const rdl_weight* w, const float* x_dev, size_t 
 rdl_status rdl_quantize_row_q8_0_dev(const float* x_dev, size_t n, uint8_t* out_dev,
                                      float* scales_dev, void* stream);
 
-/* Tensor::to_f32 for Q4_0 / Q4_1 / Q8_0 rows (tensor.rs:535-639): dequantize the
- * rows `row_ids[0..n_rows)` (int32, device) of a weight into out_dev f32
- * [n_rows, K].  This is the embedding gather of the decode loop
- * (rustml/nn/main/src/core/embedding.rs:50-76) on a matrix kept quantized. */
+/* Tensor::to_f32 for Q4_0 / Q4_1 / Q8_0 rows (tensor.rs:535-639) and
+ * dequantize_q4k for Q4_K rows (rustml/gguf/main/src/core/parser.rs:549-593):
+ * dequantize the rows `row_ids[0..n_rows)` (int32, device, each < N) of a
+ * weight into out_dev f32 [n_rows, K], bit-exact.  This is the embedding
+ * gather of the decode loop (rustml/nn/main/src/core/embedding.rs:50-76) on a
+ * matrix kept quantized, and the load-time F32 expansion of Q4_K tensors
+ * (parser.rs:321-325) when a caller wants it. */
 rdl_status rdl_dequantize_rows_dev(const rdl_weight* w, const int32_t* row_ids_dev,
                                    size_t n_rows, float* out_dev, void* stream);
 

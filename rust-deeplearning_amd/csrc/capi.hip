@@ -510,8 +510,6 @@ rdl_status rdl_quantize_row_q8_0_dev(const float* x_dev, size_t n, uint8_t* out_
 rdl_status rdl_dequantize_rows_dev(const rdl_weight* w, const int32_t* row_ids_dev, size_t n_rows,
                                    float* out_dev, void* stream) {
     if (!w) return fail(RDL_ERR_NULL_POINTER, "weight handle is NULL");
-    if (w->type == WType::Q4_K)
-        return fail(RDL_ERR_DTYPE_MISMATCH, "row dequantization supports Q4_0, Q4_1, Q8_0");
     if (n_rows == 0) return ok();
     if (!row_ids_dev || !out_dev) return fail(RDL_ERR_NULL_POINTER, "NULL device pointer");
     HIP_TRY(rdl::launch_dequant_rows(w->type, (const uint8_t*)w->dev, w->n, w->k, row_ids_dev,

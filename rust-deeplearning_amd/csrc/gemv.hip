@@ -426,7 +426,10 @@ __global__ __launch_bounds__(256) void q4_0_block_dots_kernel(const uint8_t* __r
     P[gid] = dot1(q, x, -8 * x.qsum);
 }
 
-// Tensor::to_f32 rows (tensor.rs:535-639): one thread per 32-element block.
+// Tensor::to_f32 rows (tensor.rs:535-639) and dequantize_q4k (parser.rs:549-593):
+// one thread per 32 elements (for Q4_K, one of the eight sub-blocks of a
+// super-block).  Every product below is exact in f32 (f16 scale x 4- or
+// 6-bit integer), so each output has the reference's single rounding.
 template <int WT>
 __global__ __launch_bounds__(256) void dequant_rows_kernel(const uint8_t* __restrict__ W,
                                                            int nb, const int32_t* __restrict__ rows,
@@ -436,7 +439,26 @@ __global__ __launch_bounds__(256) void dequant_rows_kernel(const uint8_t* __rest
     const int r = (int)(gid / nb), b = (int)(gid % nb);
     const size_t g = (size_t)rows[r] * nb + b;
     float* o = out + gid * QK;
-    if (WT == (int)WType::Q8_0) {
+    if (WT == (int)WType::Q4_K) {
+        // sub-block j of super-block g / 8: chunk c = j / 2 of the nibble bytes,
+        // low nibbles for even j, high for odd (parser.rs:571-590)
+        const uint8_t* p = W + (g / 8) * Q4_K_BYTES;
+        const int j = (int)(g % 8);
+        const float d = h2f(p[0] | (p[1] << 8)), dmin = h2f(p[2] | (p[3] << 8));
+        const uint8_t* sb = p + 4;
+        int sc, mn;  // parser.rs:562-569
+        if (j < 4) {
+            sc = sb[j] & 63;
+            mn = sb[j + 4] & 63;
+        } else {
+            sc = (sb[j - 4] >> 6) | ((sb[j + 4] & 0xF) << 2);
+            mn = (sb[j] >> 6) | ((sb[j + 4] >> 4) << 2);
+        }
+        const float d1 = d * (float)sc, m1 = dmin * (float)mn;
+        const uint8_t* q = p + 16 + 32 * (j >> 1);
+        const int sh = (j & 1) * 4;
+        for (int l = 0; l < 32; l++) o[l] = d1 * (float)((q[l] >> sh) & 0xF) - m1;
+    } else if (WT == (int)WType::Q8_0) {
         const uint8_t* p = W + g * Q8_0_BYTES;
         const float s = h2f(p[0] | (p[1] << 8));
         for (int j = 0; j < 32; j++) o[j] = s * (float)(int8_t)p[2 + j];
@@ -530,7 +552,10 @@ hipError_t launch_dequant_rows(WType t, const uint8_t* w, size_t n, size_t k, co
     if (total == 0) return hipSuccess;
     const dim3 grid((unsigned)((total + 255) / 256));
     const int nb = (int)(k / QK);
-    if (t == WType::Q8_0)
+    if (t == WType::Q4_K)
+        hipLaunchKernelGGL((dequant_rows_kernel<(int)WType::Q4_K>), grid, dim3(256), 0, s, w, nb,
+                           rows, (int)n_rows, out);
+    else if (t == WType::Q8_0)
         hipLaunchKernelGGL((dequant_rows_kernel<(int)WType::Q8_0>), grid, dim3(256), 0, s, w, nb,
                            rows, (int)n_rows, out);
     else if (t == WType::Q4_1)

@@ -69,7 +69,7 @@ def test_prepared_native_bit_equal_to_fused(rq, gpu):
     assert np.all(np.abs(a - b) <= 1e-5 + 1e-5 * np.abs(a))
 
 
-@pytest.mark.parametrize("dtype,kind", [(2, "q4_0"), (8, "q8_0"), (3, "q4_1")])
+@pytest.mark.parametrize("dtype,kind", [(2, "q4_0"), (8, "q8_0"), (3, "q4_1"), (12, "q4k")])
 def test_dequantize_rows_exact(rq, orc, gpu, dtype, kind):
     import torch
 
