@@ -24,6 +24,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <type_traits>
 #include <vector>
 
 #include "../../include/rdl_llama.h"
@@ -185,46 +186,89 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attention_kernel(
         const KV* kr = kc + ((size_t)kvh * max_seq + (valid ? p : p0)) * hd;
         constexpr int V = 16 / sizeof(KV);
         typedef KV kvv __attribute__((ext_vector_type(V)));
+        const KV* vb = vc + (size_t)kvh * max_seq * hd;
+        const int nvalid = min(ATT_CHUNK, t - p0);
+        // V rows in pieces of 16 bytes: CPR lanes cover a row, one load covers
+        // KG rows; load i of lane l is row KG i + l / CPR (when CPR <= 16)
+        constexpr int CPR = HD * (int)sizeof(KV) / 16;
+        constexpr bool VPRE = HD > 0 && CPR <= 16 && 64 % (CPR > 0 ? CPR : 1) == 0;
+        constexpr int KG = VPRE ? 64 / CPR : 1;
         float acc = 0.0f;
-        if constexpr (HD > 0) {
-            kvv kreg[HD / V];
+        if constexpr (VPRE) {
+            // K and V loads all in flight before the first use: one round trip
+            kvv kreg[HD / V], vreg[CPR];
+            const int vk = lane / CPR, ve = (lane % CPR) * V;
 #pragma unroll
             for (int i = 0; i < HD / V; i++) kreg[i] = *reinterpret_cast<const kvv*>(kr + i * V);
+#pragma unroll
+            for (int i = 0; i < CPR; i++) {  // rows past the length re-read the last valid row
+                const int j = min(KG * i + vk, nvalid - 1);
+                vreg[i] = *reinterpret_cast<const kvv*>(vb + (size_t)(p0 + j) * hd + ve);
+            }
+            __builtin_amdgcn_sched_barrier(0);  // keep every load ahead of the arithmetic
 #pragma unroll
             for (int i = 0; i < HD / V; i++)
 #pragma unroll
                 for (int e = 0; e < V; e++) acc += qs[i * V + e] * (float)kreg[i][e];
-        } else {
-            for (int d = 0; d < hd; d += V) {
-                const kvv kv = *reinterpret_cast<const kvv*>(kr + d);
+            const float sc = valid ? acc / scale : -__builtin_inff();
+            mx = wave_max(sc);
+            const float e = valid ? expf(sc - mx) : 0.0f;
+            l = wave_sum(e);
+            float o[V];
 #pragma unroll
-                for (int e = 0; e < V; e++) acc += qs[d + e] * (float)kv[e];
+            for (int c = 0; c < V; c++) o[c] = 0.0f;
+#pragma unroll
+            for (int i = 0; i < CPR; i++) {
+                const float pj = __shfl(e, KG * i + vk);  // rows past the length carry 0
+#pragma unroll
+                for (int c = 0; c < V; c++) o[c] += pj * (float)vreg[i][c];
             }
-        }
-        const float sc = valid ? acc / scale : -__builtin_inff();
-        mx = wave_max(sc);
-        const float e = valid ? expf(sc - mx) : 0.0f;
-        l = wave_sum(e);
-        const KV* vb = vc + (size_t)kvh * max_seq * hd;
-        const int nvalid = min(ATT_CHUNK, t - p0);
-        for (int d0 = 0; d0 < hd; d0 += 128) {
-            const int d = d0 + 2 * lane;
-            if (d < hd) {
-                float o0 = 0.0f, o1 = 0.0f;
-                // branch-free: a key past the row's length re-reads the last
-                // valid row with weight 0, so all row loads are in flight together
 #pragma unroll
-                for (int j = 0; j < ATT_CHUNK; j++) {
-                    const float ej =
-                        __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e), j));
-                    typedef KV kv2 __attribute__((ext_vector_type(2)));
-                    const int pj = p0 + min(j, nvalid - 1);
-                    const kv2 v2 = *reinterpret_cast<const kv2*>(vb + (size_t)pj * hd + d);
-                    o0 += ej * (float)v2[0];
-                    o1 += ej * (float)v2[1];
+            for (int off = CPR; off < 64; off <<= 1)
+#pragma unroll
+                for (int c = 0; c < V; c++) o[c] += __shfl_xor(o[c], off);
+            if (lane < CPR)
+#pragma unroll
+                for (int c = 0; c < V; c++) os[w * hd + ve + c] = o[c];
+        } else {
+            if constexpr (HD > 0) {
+                kvv kreg[HD / V];
+#pragma unroll
+                for (int i = 0; i < HD / V; i++) kreg[i] = *reinterpret_cast<const kvv*>(kr + i * V);
+#pragma unroll
+                for (int i = 0; i < HD / V; i++)
+#pragma unroll
+                    for (int e = 0; e < V; e++) acc += qs[i * V + e] * (float)kreg[i][e];
+            } else {
+                for (int d = 0; d < hd; d += V) {
+                    const kvv kv = *reinterpret_cast<const kvv*>(kr + d);
+#pragma unroll
+                    for (int e = 0; e < V; e++) acc += qs[d + e] * (float)kv[e];
                 }
-                os[w * hd + d] = o0;
-                os[w * hd + d + 1] = o1;
+            }
+            const float sc = valid ? acc / scale : -__builtin_inff();
+            mx = wave_max(sc);
+            const float e = valid ? expf(sc - mx) : 0.0f;
+            l = wave_sum(e);
+            for (int d0 = 0; d0 < hd; d0 += 128) {
+                const int d = d0 + 2 * lane;
+                if (d < hd) {
+                    float o0 = 0.0f, o1 = 0.0f;
+                    // branch-free: a key past the row's length re-reads the last
+                    // valid row with weight 0, so all row loads are in flight together
+#pragma unroll
+                    for (int j = 0; j < ATT_CHUNK; j++) {
+                        const float ej =
+                            __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e), j));
+                        typedef KV kv2 __attribute__((ext_vector_type(2)));
+                        const int pj = p0 + min(j, nvalid - 1);
+                        const kv2 v2 = *reinterpret_cast<const kv2*>(vb + (size_t)pj * hd + d);
+                        o0 += ej * (float)v2[0];
+                        o1 += ej * (float)v2[1];
+                    }
+                    os[w * hd + d] = o0;
+                    os[w * hd + d + 1] = o1;
+                }
             }
         }
     }
