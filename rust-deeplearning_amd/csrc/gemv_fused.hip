@@ -757,28 +757,35 @@ __global__ __launch_bounds__(NW * 64) void gemv_fused_kernel(const uint8_t* __re
 // nibbles) and 2c+1 (hi nibbles) of super-block sb (parser.rs:574-589).
 __device__ __forceinline__ void q4k_scale_min(const u32x4& h, int c, int& sc1, int& mn1, int& sc2,
                                               int& mn2) {
-    const uint32_t j1 = 2 * c;
-    if (c < 2) {
-        // j < 4: sc = s[j] & 63, mn = s[j+4] & 63                  (parser.rs:565-566)
-        sc1 = (int)((h.y >> (8 * j1)) & 63);
-        sc2 = (int)((h.y >> (8 * (j1 + 1))) & 63);
-        mn1 = (int)((h.z >> (8 * j1)) & 63);
-        mn2 = (int)((h.z >> (8 * (j1 + 1))) & 63);
-    } else {
-        // j >= 4, i = j-4: sc = ((s[i]>>6)&3) | ((s[i+8]&0xF)<<2),
-        //                  mn = ((s[i+4]>>6)&3) | ((s[i+8]>>4)<<2) (parser.rs:567-568)
-        const uint32_t i1 = j1 - 4;
-        const uint32_t si1 = h.y >> (8 * i1), si2 = h.y >> (8 * (i1 + 1));
-        const uint32_t ti1 = h.z >> (8 * i1), ti2 = h.z >> (8 * (i1 + 1));
-        const uint32_t ui1 = h.w >> (8 * i1), ui2 = h.w >> (8 * (i1 + 1));
-        sc1 = (int)(((si1 >> 6) & 3) | ((ui1 & 0xF) << 2));
-        sc2 = (int)(((si2 >> 6) & 3) | ((ui2 & 0xF) << 2));
-        mn1 = (int)(((ti1 >> 6) & 3) | (((ui1 >> 4) & 0xF) << 2));
-        mn2 = (int)(((ti2 >> 6) & 3) | (((ui2 >> 4) & 0xF) << 2));
-    }
+    // both forms, then a select: no branch on the lane's chunk index, so the
+    // rows of a wave stay one straight-line block each
+    const uint32_t j1 = 2 * (c & 1);  // byte of sub-block 2c within its group of four
+    // j < 4: sc = s[j] & 63, mn = s[j+4] & 63                        (parser.rs:565-566)
+    const uint32_t a_sc1 = (h.y >> (8 * j1)) & 63, a_sc2 = (h.y >> (8 * (j1 + 1))) & 63;
+    const uint32_t a_mn1 = (h.z >> (8 * j1)) & 63, a_mn2 = (h.z >> (8 * (j1 + 1))) & 63;
+    // j >= 4, i = j-4: sc = ((s[i]>>6)&3) | ((s[i+8]&0xF)<<2),
+    //                  mn = ((s[i+4]>>6)&3) | ((s[i+8]>>4)<<2)       (parser.rs:567-568)
+    const uint32_t si1 = h.y >> (8 * j1), si2 = h.y >> (8 * (j1 + 1));
+    const uint32_t ti1 = h.z >> (8 * j1), ti2 = h.z >> (8 * (j1 + 1));
+    const uint32_t ui1 = h.w >> (8 * j1), ui2 = h.w >> (8 * (j1 + 1));
+    const uint32_t b_sc1 = ((si1 >> 6) & 3) | ((ui1 & 0xF) << 2);
+    const uint32_t b_sc2 = ((si2 >> 6) & 3) | ((ui2 & 0xF) << 2);
+    const uint32_t b_mn1 = ((ti1 >> 6) & 3) | (((ui1 >> 4) & 0xF) << 2);
+    const uint32_t b_mn2 = ((ti2 >> 6) & 3) | (((ui2 >> 4) & 0xF) << 2);
+    const bool lo = c < 2;
+    sc1 = (int)(lo ? a_sc1 : b_sc1);
+    sc2 = (int)(lo ? a_sc2 : b_sc2);
+    mn1 = (int)(lo ? a_mn1 : b_mn1);
+    mn2 = (int)(lo ? a_mn2 : b_mn2);
 }
 
-template <int R, int UPL, int NW>
+// Loads of Q4_K rows in flight ahead of the arithmetic (both Q4_K kernels).
+constexpr int Q4K_AHEAD = 2;
+
+// Q4_K rows of at most 64 units (K <= 4096): lane u takes unit u of R rows
+// per wave (rows r0 + wv + r * NW); each activation record is read from LDS
+// once for the R rows.
+template <int R, int NW>
 __global__ __launch_bounds__(NW * 64) void gemv_q4k_fused_kernel(const uint8_t* __restrict__ W, int n,
                                                             int nsb, int rpw,
                                                             const float* __restrict__ X,
@@ -792,30 +799,28 @@ __global__ __launch_bounds__(NW * 64) void gemv_q4k_fused_kernel(const uint8_t* 
     const float* x = X + (size_t)blockIdx.y * nb * 32;
     float* y = Y + (size_t)blockIdx.y * n;
     const uint32_t row_bytes = (uint32_t)nsb * Q4_K_BYTES;
-    constexpr int PI = (UPL * 16 + NW - 1) / NW;  // nb * 8 = 16 * units <= 1024 * UPL
+    constexpr int PI = (16 + NW - 1) / NW;  // nb * 8 = 16 * units <= 1024 float4 pieces
     f32x4 xv[PI];
     load_prep_x<NW, PI>(x, nb, xv);
 
-    u32x4 hdr[R][UPL], qa[R][UPL], qb[R][UPL];
-    // no control flow here (empty slots load nothing through an out-of-range
-    // buffer offset): exactly 3 loads per (row, unit)
+    // rows issued Q4K_AHEAD at a time, as in gemv_q4k_splitk_kernel
+    const int u = lane;
+    const bool uok = u < nunits;
+    u32x4 hdr[R], qa[R], qb[R];
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(W, (uint32_t)n * row_bytes);
-#pragma unroll
-    for (int r = 0; r < R; r++) {
+    auto issue = [&](int r) {
         const int row = r0 + wv + r * NW;
+        const uint32_t off =
+            (row < rend && uok) ? (uint32_t)row * row_bytes + (uint32_t)(u >> 2) * Q4_K_BYTES : RSRC_OOB;
+        const uint32_t q = off + 16 + 32 * (u & 3);
+        hdr[r] = buf_load_b128(rs, off);
+        qa[r] = buf_load_b128(rs, q);
+        qb[r] = buf_load_b128(rs, q + 16);
+    };
+    constexpr int P0 = R < Q4K_AHEAD ? R : Q4K_AHEAD;
 #pragma unroll
-        for (int i = 0; i < UPL; i++) {
-            const int u = lane + 64 * i;
-            const uint32_t off = (row < rend && u < nunits)
-                                     ? (uint32_t)row * row_bytes + (uint32_t)(u >> 2) * Q4_K_BYTES
-                                     : RSRC_OOB;
-            const uint32_t q = off + 16 + 32 * (u & 3);
-            hdr[r][i] = buf_load_b128(rs, off);
-            qa[r][i] = buf_load_b128(rs, q);
-            qb[r][i] = buf_load_b128(rs, q + 16);
-        }
-    }
-    wait_prep_x<R * UPL * 3>();  // header + two 16-byte nibble loads per unit
+    for (int r = 0; r < P0; r++) issue(r);
+    wait_prep_x<P0 * 3>();  // header + two 16-byte nibble loads per row
     after_wait<PI>(xv);
     prep_float_lds<NW, PI>(xv, nb, reinterpret_cast<int*>(lds4));
     __syncthreads();
@@ -824,46 +829,153 @@ __global__ __launch_bounds__(NW * 64) void gemv_q4k_fused_kernel(const uint8_t* 
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; r++) acc[r] = 0.0f;
+    if (uok) {
+        const int sb = u >> 2, c = u & 3;
+        const RF x1 = read_rf(lds4, nb, sb * 8 + 2 * c);
+        const RF x2 = read_rf(lds4, nb, sb * 8 + 2 * c + 1);
 #pragma unroll
-    for (int i = 0; i < UPL; i++) {
-        const int u = lane + 64 * i;
-        if (u < nunits) {
-            const int sb = u >> 2, c = u & 3;
-            const RF x1 = read_rf(lds4, nb, sb * 8 + 2 * c);
-            const RF x2 = read_rf(lds4, nb, sb * 8 + 2 * c + 1);
+        for (int r = 0; r < R; r++) {
+            if (r + P0 < R) issue(r + P0);
+            __builtin_amdgcn_sched_barrier(0);
+            // row r's data enter the arithmetic here and not earlier (keeps the
+            // compiler from hoisting every row's scale work above the first dot)
+            asm volatile("" : "+v"(hdr[r]), "+v"(qa[r]), "+v"(qb[r]));
+            const uint32_t raw[8] = {qa[r].x, qa[r].y, qa[r].z, qa[r].w, qb[r].x, qb[r].y, qb[r].z, qb[r].w};
+            uint32_t lo[8], hi[8];
 #pragma unroll
-            for (int r = 0; r < R; r++) {
-                if (r0 + wv + r * NW < rend) {
-                    const uint32_t raw[8] = {qa[r][i].x, qa[r][i].y, qa[r][i].z, qa[r][i].w,
-                                             qb[r][i].x, qb[r][i].y, qb[r][i].z, qb[r][i].w};
-                    uint32_t lo[8], hi[8];
-#pragma unroll
-                    for (int k = 0; k < 8; k++) {
-                        lo[k] = raw[k] & NIB;
-                        hi[k] = (raw[k] >> 4) & NIB;
-                    }
-                    const float d = h2f(hdr[r][i].x & 0xFFFFu);
-                    const float dmin = h2f(hdr[r][i].x >> 16);
-                    int sc1, mn1, sc2, mn2;
-                    q4k_scale_min(hdr[r][i], c, sc1, mn1, sc2, mn2);
-                    // element value (d*sc)*q - (dmin*mn)   (parser.rs:577-587)
-                    const float d1 = d * (float)sc1, m1 = dmin * (float)mn1;
-                    const float d2 = d * (float)sc2, m2 = dmin * (float)mn2;
-                    float a = acc[r];
-                    a = fmaf(d1 * x1.S, dot3(lo, x1, 0, 0, 0), a);
-                    a = fmaf(-m1, x1.xsum, a);
-                    a = fmaf(d2 * x2.S, dot3(hi, x2, 0, 0, 0), a);
-                    a = fmaf(-m2, x2.xsum, a);
-                    acc[r] = a;
-                }
+            for (int k = 0; k < 8; k++) {
+                lo[k] = raw[k] & NIB;
+                hi[k] = (raw[k] >> 4) & NIB;
             }
+            const float d = h2f(hdr[r].x & 0xFFFFu);
+            const float dmin = h2f(hdr[r].x >> 16);
+            int sc1, mn1, sc2, mn2;
+            q4k_scale_min(hdr[r], c, sc1, mn1, sc2, mn2);
+            // element value (d*sc)*q - (dmin*mn)   (parser.rs:577-587)
+            const float d1 = d * (float)sc1, m1 = dmin * (float)mn1;
+            const float d2 = d * (float)sc2, m2 = dmin * (float)mn2;
+            float a = acc[r];
+            a = fmaf(d1 * x1.S, dot3(lo, x1, 0, 0, 0), a);
+            a = fmaf(-m1, x1.xsum, a);
+            a = fmaf(d2 * x2.S, dot3(hi, x2, 0, 0, 0), a);
+            a = fmaf(-m2, x2.xsum, a);
+            acc[r] = a;
+            __builtin_amdgcn_sched_barrier(0);  // one row at a time, in load order
         }
     }
+    // rows past rend hold 0 (their loads read zeros); they are not stored
     const float s = wave_reduce_rows<R>(acc);
     constexpr int SH = reduce_span_log2<R>();
     if ((lane & ((1 << SH) - 1)) == 0) {
         const int row = r0 + wv + (lane >> SH) * NW;
         if (row < rend) y[row] = s;
+    }
+}
+
+// Q4_K rows longer than 64 units: K is split over the waves of a workgroup so
+// that every wave can keep R rows in registers and read each activation
+// record from LDS once for all of them.  Wave w takes K slice ks = w % KS
+// (units ks * ups .. + ups - 1, one per lane, ups <= 64) of rows
+// r0 + rg + r * RG, rg = w / KS, r < R; the KS slice sums of a row are added
+// in a fixed order at the end, through LDS.
+template <int R, int KS, int NW>
+__global__ __launch_bounds__(NW * 64) void gemv_q4k_splitk_kernel(const uint8_t* __restrict__ W, int n, int nsb,
+                                                                  int ups, const float* __restrict__ X,
+                                                                  float* __restrict__ Y) {
+    static_assert(NW % KS == 0, "slices per workgroup");
+    constexpr int RG = NW / KS;  // row groups
+    constexpr int RPW = RG * R;  // rows per workgroup
+    extern __shared__ i32x4 lds4[];
+    const int lane = threadIdx.x & 63;
+    const int wv = threadIdx.x >> 6;
+    const int ks = wv % KS, rg = wv / KS;
+    const int r0 = blockIdx.x * RPW;
+    const int rend = min(n, r0 + RPW);
+    const int nb = nsb * 8, nunits = nsb * 4;
+    const float* x = X + (size_t)blockIdx.y * nb * 32;
+    float* y = Y + (size_t)blockIdx.y * n;
+    const uint32_t row_bytes = (uint32_t)nsb * Q4_K_BYTES;
+    constexpr int PI = (KS * 16 + NW - 1) / NW;  // nb * 8 = 16 * units <= 1024 * KS float4 pieces
+    f32x4 xv[PI];
+    load_prep_x<NW, PI>(x, nb, xv);
+
+    const int u = ks * ups + lane;
+    const bool uok = lane < ups && u < nunits;
+    // Rows are loaded Q4K_AHEAD at a time: row r + Q4K_AHEAD is issued when
+    // row r's arithmetic starts, so each wave's loads arrive in the order they
+    // are used and the arithmetic overlaps the stream.  No control flow around
+    // the loads (empty slots load nothing through an out-of-range offset).
+    u32x4 hdr[R], qa[R], qb[R];
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(W, (uint32_t)n * row_bytes);
+    auto issue = [&](int r) {
+        const int row = r0 + rg + r * RG;
+        const uint32_t off =
+            (row < rend && uok) ? (uint32_t)row * row_bytes + (uint32_t)(u >> 2) * Q4_K_BYTES : RSRC_OOB;
+        const uint32_t q = off + 16 + 32 * (u & 3);
+        hdr[r] = buf_load_b128(rs, off);
+        qa[r] = buf_load_b128(rs, q);
+        qb[r] = buf_load_b128(rs, q + 16);
+    };
+    constexpr int P0 = R < Q4K_AHEAD ? R : Q4K_AHEAD;
+#pragma unroll
+    for (int r = 0; r < P0; r++) issue(r);
+    wait_prep_x<P0 * 3>();  // header + two 16-byte nibble loads per row
+    after_wait<PI>(xv);
+    prep_float_lds<NW, PI>(xv, nb, reinterpret_cast<int*>(lds4));
+    __syncthreads();
+
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
+    if (uok) {
+        const int sb = u >> 2, c = u & 3;
+        const RF x1 = read_rf(lds4, nb, sb * 8 + 2 * c);
+        const RF x2 = read_rf(lds4, nb, sb * 8 + 2 * c + 1);
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            if (r + P0 < R) issue(r + P0);
+            __builtin_amdgcn_sched_barrier(0);
+            // row r's data enter the arithmetic here and not earlier (keeps the
+            // compiler from hoisting every row's scale work above the first dot)
+            asm volatile("" : "+v"(hdr[r]), "+v"(qa[r]), "+v"(qb[r]));
+            const uint32_t raw[8] = {qa[r].x, qa[r].y, qa[r].z, qa[r].w, qb[r].x, qb[r].y, qb[r].z, qb[r].w};
+            uint32_t lo[8], hi[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                lo[k] = raw[k] & NIB;
+                hi[k] = (raw[k] >> 4) & NIB;
+            }
+            const float d = h2f(hdr[r].x & 0xFFFFu);
+            const float dmin = h2f(hdr[r].x >> 16);
+            int sc1, mn1, sc2, mn2;
+            q4k_scale_min(hdr[r], c, sc1, mn1, sc2, mn2);
+            // element value (d*sc)*q - (dmin*mn)   (parser.rs:577-587)
+            const float d1 = d * (float)sc1, m1 = dmin * (float)mn1;
+            const float d2 = d * (float)sc2, m2 = dmin * (float)mn2;
+            float a = acc[r];
+            a = fmaf(d1 * x1.S, dot3(lo, x1, 0, 0, 0), a);
+            a = fmaf(-m1, x1.xsum, a);
+            a = fmaf(d2 * x2.S, dot3(hi, x2, 0, 0, 0), a);
+            a = fmaf(-m2, x2.xsum, a);
+            acc[r] = a;
+            // one row at a time, in load order: row r's arithmetic runs while
+            // the loads of rows r + 1 .. are still arriving
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    // rows of empty slots hold 0 (their loads read zeros): no masking needed
+    const float s = wave_reduce_rows<R>(acc);
+    constexpr int SH = reduce_span_log2<R>();
+    // [KS][RPW] slice sums over the start of the records, once every wave has read them
+    float* red = reinterpret_cast<float*>(lds4);
+    __syncthreads();
+    if ((lane & ((1 << SH) - 1)) == 0) red[ks * RPW + rg + (lane >> SH) * RG] = s;
+    __syncthreads();
+    for (int i = threadIdx.x; i < RPW; i += NW * 64) {
+        float t = red[i];
+#pragma unroll
+        for (int k = 1; k < KS; k++) t += red[k * RPW + i];
+        if (r0 + i < rend) y[r0 + i] = t;
     }
 }
 
@@ -968,23 +1080,33 @@ void launch_cpl(const uint8_t* w, int n, int nb, const float* x, size_t m, float
     }
 }
 
+// Rows of more than 64 units (K > 4096): K split over 2 or 4 waves of a
+// 16-wave workgroup, 4 rows per wave (gemv_q4k_splitk_kernel).
+template <int KS>
+void launch_q4k_splitk(const uint8_t* w, int n, int nsb, const float* x, size_t m, float* y, hipStream_t s,
+                       size_t lds) {
+    constexpr int NW = 16, R = 4, RPW = NW / KS * R;
+    const int units = nsb * 4, ups = (units + KS - 1) / KS;
+    const dim3 grid((unsigned)((n + RPW - 1) / RPW), (unsigned)m), block(NW * 64);
+    launch_kernel((gemv_q4k_splitk_kernel<R, KS, NW>), grid, block, lds, s, w, n, nsb, ups, x, y);
+}
+
 template <int NW>
 void launch_q4k_nw(const uint8_t* w, int n, int nsb, const float* x, size_t m, float* y,
                    hipStream_t s, size_t lds, int wg_per_cu) {
     const int units = nsb * 4;
-    if (units > 64) {
-        const Cfg c = pick_cfg(n, NW, 1, wg_per_cu);
-        const dim3 grid((unsigned)((n + c.rpw - 1) / c.rpw), (unsigned)m), block(NW * 64);
-        launch_kernel((gemv_q4k_fused_kernel<1, 4, NW>), grid, block, lds, s, w, n, nsb, c.rpw, x, y);
+    if (units > 64) {  // units <= 256 (K <= 16384)
+        if (units <= 128) launch_q4k_splitk<2>(w, n, nsb, x, m, y, s, lds);
+        else launch_q4k_splitk<4>(w, n, nsb, x, m, y, s, lds);
         return;
     }
     const Cfg c = pick_cfg(n, NW, 4, wg_per_cu);
     const dim3 grid((unsigned)((n + c.rpw - 1) / c.rpw), (unsigned)m), block(NW * 64);
     switch (c.r) {
-        case 1: launch_kernel((gemv_q4k_fused_kernel<1, 1, NW>), grid, block, lds, s, w, n, nsb, c.rpw, x, y); break;
-        case 2: launch_kernel((gemv_q4k_fused_kernel<2, 1, NW>), grid, block, lds, s, w, n, nsb, c.rpw, x, y); break;
-        case 3: launch_kernel((gemv_q4k_fused_kernel<3, 1, NW>), grid, block, lds, s, w, n, nsb, c.rpw, x, y); break;
-        default: launch_kernel((gemv_q4k_fused_kernel<4, 1, NW>), grid, block, lds, s, w, n, nsb, c.rpw, x, y); break;
+        case 1: launch_kernel((gemv_q4k_fused_kernel<1, NW>), grid, block, lds, s, w, n, nsb, c.rpw, x, y); break;
+        case 2: launch_kernel((gemv_q4k_fused_kernel<2, NW>), grid, block, lds, s, w, n, nsb, c.rpw, x, y); break;
+        case 3: launch_kernel((gemv_q4k_fused_kernel<3, NW>), grid, block, lds, s, w, n, nsb, c.rpw, x, y); break;
+        default: launch_kernel((gemv_q4k_fused_kernel<4, NW>), grid, block, lds, s, w, n, nsb, c.rpw, x, y); break;
     }
 }
 
