@@ -79,6 +79,65 @@ __global__ __launch_bounds__(XPREP_THREADS) void gemm_xprep_kernel(const float* 
     }
 }
 
+// The same split with each row's values held in registers between the max
+// and the conversion (k <= 4 * 4 * XPREP_FAST_THREADS): one global read.
+constexpr int XPREP_FAST_THREADS = 1024;
+__global__ __launch_bounds__(XPREP_FAST_THREADS) void gemm_xprep_fast_kernel(const float* __restrict__ X, int k,
+                                                                             _Float16* __restrict__ XH,
+                                                                             _Float16* __restrict__ XL,
+                                                                             int* __restrict__ XE) {
+    constexpr int NT = XPREP_FAST_THREADS, NV = 4;
+    __shared__ float red[NT / 64];
+    const int row = blockIdx.x;
+    const float* x = X + (size_t)row * k;
+    f32x4 v[NV];
+    const int k4 = k >> 2;  // k % 32 == 0
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        const int p = threadIdx.x + j * NT;
+        v[j] = p < k4 ? reinterpret_cast<const f32x4*>(x)[p] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    float amax = 0.0f;
+    bool bad = false;
+#pragma unroll
+    for (int j = 0; j < NV; j++)
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            bad |= !isfinite(v[j][t]);
+            amax = fmaxf(amax, fabsf(v[j][t]));
+        }
+    if (bad) amax = __builtin_inff();
+    amax = max8_f32(amax);
+    amax = fmaxf(amax, dpp_f32<DPP_ROW_MIRROR>(amax));
+    amax = fmaxf(amax, __shfl_xor(amax, 16));
+    amax = fmaxf(amax, __shfl_xor(amax, 32));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+    __syncthreads();
+    amax = red[0];
+#pragma unroll
+    for (int w = 1; w < NT / 64; w++) amax = fmaxf(amax, red[w]);
+    // e: amax * 2^-e in [2^14, 2^15); non-finite or zero rows keep e = 0
+    int e = 0;
+    if (amax > 0.0f && isfinite(amax)) e = ilogbf(amax) - 14;
+    if (threadIdx.x == 0) XE[row] = e;
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        const int p = threadIdx.x + j * NT;
+        if (p < k4) {
+            h4 hv, lv;
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const float s = ldexpf(v[j][t], -e);
+                hv[t] = (_Float16)s;
+                lv[t] = (_Float16)(s - (float)hv[t]);
+            }
+            reinterpret_cast<h4*>(XH + (size_t)row * k)[p] = hv;
+            reinterpret_cast<h4*>(XL + (size_t)row * k)[p] = lv;
+        }
+    }
+}
+
 // ---- GEMM ------------------------------------------------------------------------
 // LDS row strides, padded so that the 16 rows a fragment read touches fall in
 // distinct banks: nibble rows CB*16 + 8 bytes, x rows CB*64 + 16 bytes.
@@ -409,7 +468,11 @@ hipError_t launch_gemm_q4_0(const uint8_t* w, size_t n, size_t k, const float* x
     _Float16* xh = reinterpret_cast<_Float16*>(scratch);
     _Float16* xl = reinterpret_cast<_Float16*>(reinterpret_cast<uint8_t*>(scratch) + xb);
     int* xe = reinterpret_cast<int*>(reinterpret_cast<uint8_t*>(scratch) + 2 * xb);
-    launch_kernel(gemm_xprep_kernel, dim3((unsigned)m), dim3(XPREP_THREADS), 0, s, x, (int)k, xh, xl, xe);
+    if (k <= (size_t)16 * XPREP_FAST_THREADS)
+        launch_kernel(gemm_xprep_fast_kernel, dim3((unsigned)m), dim3(XPREP_FAST_THREADS), 0, s, x, (int)k, xh, xl,
+                      xe);
+    else
+        launch_kernel(gemm_xprep_kernel, dim3((unsigned)m), dim3(XPREP_THREADS), 0, s, x, (int)k, xh, xl, xe);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int ni = (int)n, nb = (int)(k / QK), mi = (int)m;

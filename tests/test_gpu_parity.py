@@ -52,10 +52,12 @@ def test_gemv_float_baseline_shapes(rq, orc, gpu, name, dtype, n, k, kind, seed)
 
 
 # (1, 6000, 256) and (2, 14336, 512) take the fused kernel's 2- and 4-row-per-wave
-# reductions on a 256-CU device (the baseline shapes take 1 and 3).
+# reductions on a 256-CU device (the baseline shapes take 1 and 3).  K > 8192
+# splits K over 4 waves: an odd block count (8224), ragged rows, the largest K.
 @pytest.mark.parametrize("m,n,k", [(1, 1, 32), (1, 3, 64), (2, 17, 96), (3, 65, 4096 + 32),
                                    (1, 129, 2048), (4, 7, 8192), (5, 300, 320),
-                                   (1, 6000, 256), (2, 14336, 512)])
+                                   (1, 6000, 256), (2, 14336, 512),
+                                   (3, 37, 8224), (1, 1000, 12288), (2, 21, 16384)])
 @pytest.mark.parametrize("dtype,kind", [(2, "q4"), (8, "q8"), (3, "q4_1")])
 def test_gemv_float_ragged(rq, orc, gpu, m, n, k, dtype, kind):
     x = synth.activations(m, k, 7 + n)
@@ -94,7 +96,7 @@ def test_native_block_dots_config2(rq, orc, gpu):
     assert np.array_equal(rq.q4_0_q8_0_block_dots(x, w, 1, k, n), orc.block_dots(x, w, 1, k, n))
 
 
-@pytest.mark.parametrize("m,n,k", [(1, 11008, 4096), (1, 4096, 14336), (3, 33, 96), (1, 1, 32)])
+@pytest.mark.parametrize("m,n,k", [(1, 11008, 4096), (1, 4096, 14336), (3, 33, 96), (1, 1, 32), (2, 45, 8224)])
 def test_native_gemv(rq, orc, gpu, m, n, k):
     x = synth.activations(m, k, 300 + n)
     w = synth.q4_0_weights(n, k, 301 + k)
