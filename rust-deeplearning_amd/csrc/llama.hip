@@ -48,20 +48,13 @@ __device__ __forceinline__ float wave_max(float v) {
     v = fmaxf(v, __shfl_xor(v, 16));
     return fmaxf(v, __shfl_xor(v, 32));
 }
-// Sum / max over a 256-thread block, returned to every thread.
+// Sum over a 256-thread block, returned to every thread.
 __device__ __forceinline__ float block_sum(float v, float* red) {
     v = wave_sum(v);
     __syncthreads();
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();
     return (red[0] + red[1]) + (red[2] + red[3]);
-}
-__device__ __forceinline__ float block_max(float v, float* red) {
-    v = wave_max(v);
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 }
 
 // rms = sqrt(sum(x^2) / d + eps); out = x * (1 / rms) * g   (ops.rs:688-751)
@@ -354,18 +347,49 @@ __global__ void swiglu_kernel(const float* __restrict__ gu, int ffn, size_t n, f
     h[i] = (g * sig) * u;
 }
 
-// argmax with the first maximum winning (strict >, NaN never wins; an
-// all-NaN / -inf row gives 0, sampling.rs:8-18).  Writes the token for the
-// next step and out_tokens[*step], then advances *step.
-constexpr int ARGMAX_NT = 1024;
-__global__ __launch_bounds__(ARGMAX_NT) void argmax_kernel(const float* __restrict__ logits, int vocab,
+// One greedy sampling step in one launch: argmax of the logits with the first
+// maximum winning (strict >, NaN never wins; an all-NaN / -inf row gives 0,
+// sampling.rs:8-18), the token written for the next step and to
+// out_tokens[*step] (then *step + 1), the position advanced by `advance`
+// (KVCache::advance, kv_cache.rs:112-114), and the sampled token's embedding
+// row dequantized into x (Embedding::forward, embedding.rs:50-76, on the Q4_0
+// table as Tensor::to_f32 computes it: d * (q - 8)) for the next step.
+constexpr int SAMPLE_NT = 1024;
+__global__ __launch_bounds__(SAMPLE_NT) void sample_kernel(const float* __restrict__ logits, int vocab,
                                                            int* __restrict__ token, int* __restrict__ out_tokens,
-                                                           int* __restrict__ step) {
-    __shared__ float bv[ARGMAX_NT / 64];
-    __shared__ int bi[ARGMAX_NT / 64];
+                                                           int* __restrict__ step, int* __restrict__ pos,
+                                                           int advance, const uint8_t* __restrict__ emb, int dim,
+                                                           float* __restrict__ x) {
+    __shared__ float bv[SAMPLE_NT / 64];
+    __shared__ int bi[SAMPLE_NT / 64];
+    __shared__ int win;
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    constexpr int VU = 8;  // float4 loads in flight per thread
     float best = -__builtin_inff();
     int idx = 0x7FFFFFFF;
-    for (int i = threadIdx.x; i < vocab; i += ARGMAX_NT) {
+    const int n4 = vocab >> 2;
+    const f4* l4 = reinterpret_cast<const f4*>(logits);
+    // each thread visits its indices in increasing order
+    for (int base = 0; base < n4; base += SAMPLE_NT * VU) {
+        f4 v[VU];
+#pragma unroll
+        for (int j = 0; j < VU; j++) {
+            const int p = base + (int)threadIdx.x + j * SAMPLE_NT;
+            v[j] = p < n4 ? l4[p] : f4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+#pragma unroll
+        for (int j = 0; j < VU; j++) {
+            const int p = base + (int)threadIdx.x + j * SAMPLE_NT;
+            if (p < n4)
+#pragma unroll
+                for (int t = 0; t < 4; t++)
+                    if (v[j][t] > best) {
+                        best = v[j][t];
+                        idx = 4 * p + t;
+                    }
+        }
+    }
+    for (int i = 4 * n4 + (int)threadIdx.x; i < vocab; i += SAMPLE_NT) {
         const float v = logits[i];
         if (v > best) {
             best = v;
@@ -387,7 +411,7 @@ __global__ __launch_bounds__(ARGMAX_NT) void argmax_kernel(const float* __restri
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        for (int w = 1; w < ARGMAX_NT / 64; w++)
+        for (int w = 1; w < SAMPLE_NT / 64; w++)
             if (bv[w] > best || (bv[w] == best && bi[w] < idx)) {
                 best = bv[w];
                 idx = bi[w];
@@ -397,6 +421,17 @@ __global__ __launch_bounds__(ARGMAX_NT) void argmax_kernel(const float* __restri
         token[0] = idx;
         out_tokens[st] = idx;
         *step = st + 1;
+        if (advance) *pos += advance;
+        win = idx;
+    }
+    __syncthreads();
+    const uint8_t* row = emb + (size_t)win * (dim / 32) * Q4_0_BYTES;
+    for (int e = threadIdx.x; e < dim; e += SAMPLE_NT) {
+        const uint8_t* blk = row + (e >> 5) * Q4_0_BYTES;
+        const int j = e & 31;
+        const float d = h2f(blk[0] | (blk[1] << 8));
+        const uint8_t v = blk[2 + (j & 15)];
+        x[e] = d * (float)((int)(j < 16 ? (v & 0x0F) : (v >> 4)) - 8);
     }
 }
 
@@ -557,11 +592,14 @@ struct LlamaModel {
     // the last row's logits into `logits`, then the position advances by m.
     // Up to 4 rows: RMSNorm, SwiGLU and the residual adds ride in the GEMV
     // launches (prologue / epilogue of the fused GEMV): 7 launches a layer.
-    hipError_t forward_fused(size_t m) {
+    // embed: x from the token ids (otherwise x already holds the rows, as
+    // sample_kernel leaves them); advance: the position moves on by m here.
+    hipError_t forward_fused(size_t m, bool embed = true, bool advance = true) {
         const int d = cfg.dim;
         const float eps = cfg.norm_eps;
-        hipError_t e = launch_dequant_rows(WType::Q4_0, emb.dev, emb.n, emb.k, tokens, m, x, stream);
-        if (e != hipSuccess) return e;
+        hipError_t e = hipSuccess;
+        if (embed && (e = launch_dequant_rows(WType::Q4_0, emb.dev, emb.n, emb.k, tokens, m, x, stream)) != hipSuccess)
+            return e;
         for (int l = 0; l < cfg.n_layers; l++) {
             Layer& L = layers[l];
             // q = rope(rms_norm(x) . Wq^T); k, v -> cache (RoPE on k) in the same launch
@@ -586,7 +624,7 @@ struct LlamaModel {
         e = launch_gemv_q4_0_fused_ex(out.dev, out.n, d, x + (m - 1) * d, d, 1, logits, 1, final_norm, eps, 0,
                                       stream);
         if (e != hipSuccess) return e;
-        hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(64), 0, stream, pos, (int)m);
+        if (advance) hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(64), 0, stream, pos, (int)m);
         return hipGetLastError();
     }
     bool fusable = false;  // every GEMV of the model meets the fused-launch shape rules
@@ -620,12 +658,19 @@ struct LlamaModel {
         return hipGetLastError();
     }
 
-    // One greedy decode step: token (device) -> logits -> argmax -> token.
+    // argmax of `logits` -> token, out_tokens, step; position += advance; the
+    // token's embedding row -> x (the input of the next decode step)
+    void sample(int advance) {
+        hipLaunchKernelGGL(sample_kernel, dim3(1), dim3(SAMPLE_NT), 0, stream, logits, cfg.vocab, tokens, out_tokens,
+                           step, pos, advance, emb.dev, cfg.dim, x);
+    }
+
+    // One greedy decode step: x (the last token's embedding, left by sample)
+    // -> logits -> sample: the next token and its embedding.
     hipError_t decode_step() {
-        hipError_t e = forward(1);
+        hipError_t e = fusable ? forward_fused(1, false, false) : forward(1);
         if (e != hipSuccess) return e;
-        hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(ARGMAX_NT), 0, stream, logits, cfg.vocab, tokens,
-                           out_tokens, step);
+        sample(fusable ? 1 : 0);
         return hipGetLastError();
     }
 };
@@ -901,8 +946,7 @@ rdl_status rdl_llama_generate_greedy(rdl_llama* model, const int32_t* prompt, si
             return api_fail(RDL_ERR_HIP, "prefill failed: %s", hipGetErrorString(fe));
         }
     }
-    hipLaunchKernelGGL(rdl::argmax_kernel, dim3(1), dim3(rdl::ARGMAX_NT), 0, M.stream, M.logits, c.vocab,
-                       M.tokens, M.out_tokens, M.step);
+    M.sample(0);  // the prefill advanced the position
     HIP_TRY(hipGetLastError());
     HIP_TRY(hipEventRecord(M.ev[1], M.stream));
     if (n_gen > 1) {
