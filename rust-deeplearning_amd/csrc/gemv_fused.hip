@@ -1126,7 +1126,9 @@ void launch_q4_0_fused_ex(const uint8_t* w, int n, int nb, const float* x, size_
     Cfg c = pick_cfg(n, 8, 8 / cpl, 2);
     if (RES == EPI_SWIGLU || RES == EPI_ROPE_KV) {
         // whole row pairs per wave: R even, a workgroup takes NW * R rows
-        c.r = (8 / cpl >= 4 && n >= 2 * 8 * 4 * 256) ? 4 : 2;
+        // (two pairs a wave where the columns allow; measured on MI355X in the
+        // 7B decode step, also for the 6144-row q/k/v launch)
+        c.r = (8 / cpl >= 4) ? 4 : 2;
         c.rpw = 8 * c.r;
     }
     switch (cpl) {
