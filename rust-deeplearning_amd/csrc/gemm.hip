@@ -479,8 +479,10 @@ hipError_t launch_gemm_q4_0(const uint8_t* w, size_t n, size_t k, const float* x
     const int cus = device_cu_count();
     // Tile choice: enough workgroups for the CUs, then the largest tile
     // (fewest re-reads of x and W from L2).
-    if (m >= 1024) return launch_cfg<4, 4, 2, 2, 1, 2>(w, ni, nb, xh, xl, xe, mi, y, s);
-    if (m >= 256) return launch_cfg<4, 2, 2, 2, 1, 4>(w, ni, nb, xh, xl, xe, mi, y, s);
+    // (M >= 256: swept on MI355X at M = 512, 2048 over tile shape, waves and
+    // chunk size; two-way K splits keep 8 waves a workgroup within the LDS)
+    if (m >= 1024) return launch_cfg<4, 4, 2, 2, 2, 1>(w, ni, nb, xh, xl, xe, mi, y, s);
+    if (m >= 256) return launch_cfg<2, 4, 2, 2, 2, 2>(w, ni, nb, xh, xl, xe, mi, y, s);
     if (m >= 48 && (size_t)((n + 31) / 32) * ((m + 63) / 64) >= (size_t)cus)
         return launch_cfg<2, 4, 1, 1, 4, 2>(w, ni, nb, xh, xl, xe, mi, y, s);
     if (m > 16) return launch_cfg<1, 2, 1, 1, 4, 2>(w, ni, nb, xh, xl, xe, mi, y, s);
