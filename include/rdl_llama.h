@@ -24,6 +24,7 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "rdl_gguf.h"
 #include "rdl_quant.h"
 
 #ifdef __cplusplus
@@ -104,6 +105,35 @@ rdl_status rdl_llama_last_timing(const rdl_llama* model, float* prefill_ms, floa
 /* The model's RoPE tables (RoPEFreqs::new: [max_seq, head_dim/2] f32 each),
  * copied to host memory. */
 rdl_status rdl_llama_rope_tables(const rdl_llama* model, float* cos_out, float* sin_out, size_t len);
+
+/* The config a model was created with (for a GGUF load: as resolved from
+ * the file's metadata and tensor shapes). */
+rdl_status rdl_llama_get_config(const rdl_llama* model, rdl_llama_config* out);
+
+/* Options of rdl_llama_load_gguf. */
+typedef struct rdl_llama_gguf_options {
+    int32_t max_seq;   /* KV cache capacity; 0: the file's context_length (2048 if absent) */
+    int32_t max_batch; /* rows per forward call; 0: 32 */
+    int32_t kv_f16;    /* 1: f16 KV cache, 0: f32 */
+} rdl_llama_gguf_options;
+
+/* LlmModel::from_pretrained over GGUFFile::load_and_remap, the Llama branch
+ * of rustml/nlp/main/src/bin/infer.rs:80-120:
+ *   config   to_model_config (parser.rs:214-289) -> gguf_config_to_model_config
+ *            (gguf_bridge.rs:46-84) -> ModelConfig::validate (types.rs:794-826)
+ *   names    gguf_llama_weight_map (weight_map.rs:26-73)
+ *   weights  from_pretrained (nlp/main/src/core/model.rs:81-232)
+ * head_dim = dim / n_heads, the FFN width and the vocabulary come from the
+ * ffn_up and output matrices.  Every mapped tensor's type, shape and file
+ * bounds are checked before anything is allocated; the bytes then go from the
+ * file mapping to HBM through pinned staging buffers, without a host copy of
+ * the file.  Tensors the map does not name are ignored.  Errors: a missing
+ * weight gives RDL_ERR_NOT_FOUND "Missing weight: <internal name>" (the
+ * reference's ModelError text); a matrix that is not Q4_0, norm weights that
+ * are not F32/F16, a model without ffn_gate or a gemma3 file give
+ * RDL_ERR_UNSUPPORTED; dims that differ from the config give
+ * RDL_ERR_SHAPE_MISMATCH.  opt may be NULL (all defaults). */
+rdl_status rdl_llama_load_gguf(const rdl_gguf* gguf, const rdl_llama_gguf_options* opt, rdl_llama** out);
 
 #ifdef __cplusplus
 }

@@ -12,6 +12,7 @@
 #include <string>
 
 #include "../../include/rdl_quant.h"
+#include "../../include/rdl_gguf.h"
 #include "rdl_internal.hpp"
 
 namespace rdl {
@@ -238,6 +239,11 @@ const char* rdl_status_string(rdl_status s) {
         case RDL_ERR_HIP: return "HIP runtime error";
         case RDL_ERR_NO_DEVICE: return "no gfx950 device";
         case RDL_ERR_UNSUPPORTED: return "unsupported shape";
+        case RDL_ERR_GGUF_IO: return "IO error";
+        case RDL_ERR_GGUF_INVALID_FORMAT: return "Invalid GGUF format";
+        case RDL_ERR_GGUF_UNSUPPORTED_TYPE: return "Unsupported GGML type";
+        case RDL_ERR_GGUF_MISSING_METADATA: return "Missing metadata";
+        case RDL_ERR_NOT_FOUND: return "not found";
     }
     return "unknown status";
 }

@@ -22,11 +22,14 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstdio>
+#include <string>
 #include <cmath>
 #include <cstring>
 #include <type_traits>
 #include <vector>
 
+#include "../../include/rdl_gguf.h"
 #include "../../include/rdl_llama.h"
 #include "rdl_device.hpp"
 #include "rdl_internal.hpp"
@@ -694,6 +697,63 @@ bool valid_config(const rdl_llama_config& c) {
            c.n_heads * c.head_dim <= 16384;
 }
 
+// Where a weight slot's bytes go: `rows` rows of row_bytes, at dst with row
+// pitch dpitch (the gate and up rows interleave in one matrix).
+struct SlotTarget {
+    uint8_t* dst = nullptr;
+    size_t row_bytes = 0, rows = 0, dpitch = 0;
+    rdl::LlamaModel::Mat* mat = nullptr;  // quantized matrix to rescan after the copy
+    bool q4 = false;                      // Q4_0 rows (else f32 norm weights)
+    size_t bytes() const { return row_bytes * rows; }
+};
+
+rdl_status slot_target(rdl::LlamaModel& M, int32_t slot, int32_t layer, SlotTarget* t) {
+    const rdl_llama_config& c = M.cfg;
+    const bool per_layer = slot >= RDL_LLAMA_ATTN_NORM && slot <= RDL_LLAMA_W_DOWN;
+    if (per_layer && (layer < 0 || layer >= c.n_layers))
+        return api_fail(RDL_ERR_INVALID_DATA, "layer %d out of range", layer);
+    auto q4 = [&](rdl::LlamaModel::Mat& w, int row0, int rows, int interleave = 1) {
+        const size_t rb = M.row_q4(w.k);
+        t->mat = &w;
+        t->q4 = true;
+        t->row_bytes = rb;
+        t->rows = (size_t)rows;
+        t->dpitch = rb * interleave;
+        t->dst = w.dev + (size_t)row0 * rb;
+    };
+    auto f32 = [&](float* p) {
+        t->dst = reinterpret_cast<uint8_t*>(p);
+        t->row_bytes = t->dpitch = (size_t)c.dim * 4;
+        t->rows = 1;
+    };
+    switch (slot) {
+        case RDL_LLAMA_TOKEN_EMBEDDING: q4(M.emb, 0, c.vocab); t->mat = nullptr; break;  // no GEMM over it
+        case RDL_LLAMA_OUTPUT: q4(M.out, 0, c.vocab); break;
+        case RDL_LLAMA_FINAL_NORM: f32(M.final_norm); break;
+        case RDL_LLAMA_ATTN_NORM: f32(M.layers[layer].attn_norm); break;
+        case RDL_LLAMA_FFN_NORM: f32(M.layers[layer].ffn_norm); break;
+        case RDL_LLAMA_WQ: q4(M.layers[layer].qkv, 0, M.q_dim); break;
+        case RDL_LLAMA_WK: q4(M.layers[layer].qkv, M.q_dim, M.kv_dim); break;
+        case RDL_LLAMA_WV: q4(M.layers[layer].qkv, M.q_dim + M.kv_dim, M.kv_dim); break;
+        case RDL_LLAMA_WO: q4(M.layers[layer].o, 0, c.dim); break;
+        case RDL_LLAMA_W_GATE: q4(M.layers[layer].gu, 0, c.ffn_dim, 2); break;  // even rows of [gate; up]
+        case RDL_LLAMA_W_UP: q4(M.layers[layer].gu, 1, c.ffn_dim, 2); break;    // odd rows
+        case RDL_LLAMA_W_DOWN: q4(M.layers[layer].down, 0, c.dim); break;
+        default: return api_fail(RDL_ERR_INVALID_DATA, "unknown weight slot %d", slot);
+    }
+    return api_ok();
+}
+
+// After a matrix's bytes changed: whether its block scales suit the GEMM.
+rdl_status finish_slot(const SlotTarget& t) {
+    if (t.mat) {
+        bool ok = false;
+        HIP_TRY(rdl::gemm_scales_ok(rdl::WType::Q4_0, t.mat->dev, t.mat->n, t.mat->k, &ok));
+        t.mat->gemm_ok = ok;
+    }
+    return api_ok();
+}
+
 }  // namespace
 
 extern "C" {
@@ -797,53 +857,13 @@ rdl_status rdl_llama_free(rdl_llama* model) {
 rdl_status rdl_llama_set_weight(rdl_llama* model, int32_t slot, int32_t layer, const void* bytes, size_t len) {
     if (!model || !bytes) return api_fail(RDL_ERR_NULL_POINTER, "NULL argument");
     rdl::LlamaModel& M = model->m;
-    const rdl_llama_config& c = M.cfg;
-    const bool per_layer = slot >= RDL_LLAMA_ATTN_NORM && slot <= RDL_LLAMA_W_DOWN;
-    if (per_layer && (layer < 0 || layer >= c.n_layers))
-        return api_fail(RDL_ERR_INVALID_DATA, "layer %d out of range", layer);
-    void* dst = nullptr;
-    size_t need = 0;
-    rdl::LlamaModel::Mat* mat = nullptr;
-    auto q4 = [&](rdl::LlamaModel::Mat& w, int row0, int rows) {
-        mat = &w;
-        dst = w.dev + (size_t)row0 * M.row_q4(w.k);
-        need = (size_t)rows * M.row_q4(w.k);
-    };
-    switch (slot) {
-        case RDL_LLAMA_TOKEN_EMBEDDING: q4(M.emb, 0, c.vocab); break;
-        case RDL_LLAMA_OUTPUT: q4(M.out, 0, c.vocab); break;
-        case RDL_LLAMA_FINAL_NORM: dst = M.final_norm; need = (size_t)c.dim * 4; break;
-        case RDL_LLAMA_ATTN_NORM: dst = M.layers[layer].attn_norm; need = (size_t)c.dim * 4; break;
-        case RDL_LLAMA_FFN_NORM: dst = M.layers[layer].ffn_norm; need = (size_t)c.dim * 4; break;
-        case RDL_LLAMA_WQ: q4(M.layers[layer].qkv, 0, M.q_dim); break;
-        case RDL_LLAMA_WK: q4(M.layers[layer].qkv, M.q_dim, M.kv_dim); break;
-        case RDL_LLAMA_WV: q4(M.layers[layer].qkv, M.q_dim + M.kv_dim, M.kv_dim); break;
-        case RDL_LLAMA_WO: q4(M.layers[layer].o, 0, c.dim); break;
-        case RDL_LLAMA_W_GATE:  // even rows of the interleaved [gate; up] matrix
-        case RDL_LLAMA_W_UP: {   // odd rows
-            rdl::LlamaModel::Mat& w = M.layers[layer].gu;
-            const size_t rb = M.row_q4(w.k);
-            if (len != (size_t)c.ffn_dim * rb)
-                return api_fail(RDL_ERR_SHAPE_MISMATCH, "slot %d: expected %zu bytes, got %zu", slot,
-                                (size_t)c.ffn_dim * rb, len);
-            HIP_TRY(hipMemcpy2D(w.dev + (slot == RDL_LLAMA_W_UP ? rb : 0), 2 * rb, bytes, rb, rb, c.ffn_dim,
-                                hipMemcpyHostToDevice));
-            bool ok = false;
-            HIP_TRY(rdl::gemm_scales_ok(rdl::WType::Q4_0, w.dev, w.n, w.k, &ok));
-            w.gemm_ok = ok;
-            return api_ok();
-        }
-        case RDL_LLAMA_W_DOWN: q4(M.layers[layer].down, 0, c.dim); break;
-        default: return api_fail(RDL_ERR_INVALID_DATA, "unknown weight slot %d", slot);
-    }
-    if (len != need) return api_fail(RDL_ERR_SHAPE_MISMATCH, "slot %d: expected %zu bytes, got %zu", slot, need, len);
-    HIP_TRY(hipMemcpy(dst, bytes, len, hipMemcpyHostToDevice));
-    if (mat && mat != &M.emb) {
-        bool ok = false;
-        HIP_TRY(rdl::gemm_scales_ok(rdl::WType::Q4_0, mat->dev, mat->n, mat->k, &ok));
-        mat->gemm_ok = ok;
-    }
-    return api_ok();
+    SlotTarget t;
+    rdl_status st = slot_target(M, slot, layer, &t);
+    if (st != RDL_OK) return st;
+    if (len != t.bytes())
+        return api_fail(RDL_ERR_SHAPE_MISMATCH, "slot %d: expected %zu bytes, got %zu", slot, t.bytes(), len);
+    HIP_TRY(hipMemcpy2D(t.dst, t.dpitch, bytes, t.row_bytes, t.row_bytes, t.rows, hipMemcpyHostToDevice));
+    return finish_slot(t);
 }
 
 rdl_status rdl_llama_init_random(rdl_llama* model, uint64_t seed) {
@@ -987,6 +1007,253 @@ rdl_status rdl_llama_rope_tables(const rdl_llama* model, float* cos_out, float* 
         return api_fail(RDL_ERR_SHAPE_MISMATCH, "tables hold %zu floats, got %zu", M.cos_h.size(), len);
     memcpy(cos_out, M.cos_h.data(), len * 4);
     memcpy(sin_out, M.sin_h.data(), len * 4);
+    return api_ok();
+}
+
+}  // extern "C"
+
+// ---- loading from a GGUF file ------------------------------------------------
+namespace {
+
+// Tensor names of the Llama weight map (weight_map.rs:26-73) and the internal
+// names from_pretrained asks for (model.rs:95-223), per slot.
+struct SlotName {
+    int slot;
+    const char* gguf;      // model-level name, or the suffix after "blk.<i>."
+    const char* internal;  // printf format with the layer index where per-layer
+};
+constexpr SlotName MODEL_NAMES[] = {
+    {RDL_LLAMA_TOKEN_EMBEDDING, "token_embd.weight", "token_embedding.weight"},
+    {RDL_LLAMA_FINAL_NORM, "output_norm.weight", "norm.weight"},
+    {RDL_LLAMA_OUTPUT, "output.weight", "output.weight"},
+};
+// in the order from_pretrained loads a layer (model.rs:146-211)
+constexpr SlotName LAYER_NAMES[] = {
+    {RDL_LLAMA_WQ, "attn_q.weight", "layers.%d.attention.q_proj.weight"},
+    {RDL_LLAMA_WK, "attn_k.weight", "layers.%d.attention.k_proj.weight"},
+    {RDL_LLAMA_WV, "attn_v.weight", "layers.%d.attention.v_proj.weight"},
+    {RDL_LLAMA_WO, "attn_output.weight", "layers.%d.attention.out_proj.weight"},
+    {RDL_LLAMA_W_UP, "ffn_up.weight", "layers.%d.feed_forward.up_proj.weight"},
+    {RDL_LLAMA_W_DOWN, "ffn_down.weight", "layers.%d.feed_forward.down_proj.weight"},
+    {RDL_LLAMA_W_GATE, "ffn_gate.weight", "layers.%d.feed_forward.gate_proj.weight"},
+    {RDL_LLAMA_ATTN_NORM, "attn_norm.weight", "layers.%d.attention_norm.weight"},
+    {RDL_LLAMA_FFN_NORM, "ffn_norm.weight", "layers.%d.ffn_norm.weight"},
+};
+
+const char* ggml_name(int32_t t) {
+    switch (t) {
+        case 0: return "F32"; case 1: return "F16"; case 2: return "Q4_0"; case 3: return "Q4_1";
+        case 6: return "Q5_0"; case 7: return "Q5_1"; case 8: return "Q8_0"; case 9: return "Q8_1";
+        case 10: return "Q2K"; case 11: return "Q3K"; case 12: return "Q4K"; case 13: return "Q5K";
+        case 14: return "Q6K"; case 15: return "Q8K";
+    }
+    return "?";
+}
+
+// The slot and layer a GGUF tensor name maps to (false: not a weight of the
+// Llama map for n_layers layers; such tensors are ignored, as remap passes
+// them through and from_pretrained never asks for them).
+bool gguf_slot(const char* name, int n_layers, int* slot, int* layer) {
+    for (const SlotName& m : MODEL_NAMES)
+        if (strcmp(name, m.gguf) == 0) return *slot = m.slot, *layer = 0, true;
+    if (strncmp(name, "blk.", 4) != 0) return false;
+    const char* p = name + 4;
+    // the decimal form format!("blk.{}", i) writes: no sign, no leading zero
+    if (!(*p >= '0' && *p <= '9') || (p[0] == '0' && p[1] >= '0' && p[1] <= '9')) return false;
+    long i = 0;
+    while (*p >= '0' && *p <= '9') {
+        i = i * 10 + (*p++ - '0');
+        if (i >= n_layers) return false;
+    }
+    if (*p++ != '.') return false;
+    for (const SlotName& l : LAYER_NAMES)
+        if (strcmp(p, l.gguf) == 0) return *slot = l.slot, *layer = (int)i, true;
+    return false;
+}
+
+std::string internal_name(const SlotName& s, int layer) {
+    char buf[128];
+    snprintf(buf, sizeof buf, s.internal, layer);
+    return buf;
+}
+
+std::string dims_str(const rdl_gguf_tensor_info& ti) {
+    std::string r = "[";
+    for (uint32_t d = 0; d < ti.n_dims; d++) r += (d ? ", " : "") + std::to_string(ti.dims[d]);
+    return r + "]";
+}
+
+// Expected GGUF dims (innermost first) of a slot's tensor: {k, n} or {dim}.
+void slot_dims(const rdl_llama_config& c, int slot, uint64_t d[2], uint32_t* nd) {
+    const uint64_t q = (uint64_t)c.n_heads * c.head_dim, kv = (uint64_t)c.n_kv_heads * c.head_dim;
+    *nd = 2;
+    switch (slot) {
+        case RDL_LLAMA_TOKEN_EMBEDDING:
+        case RDL_LLAMA_OUTPUT: d[0] = c.dim, d[1] = c.vocab; return;
+        case RDL_LLAMA_WQ: d[0] = c.dim, d[1] = q; return;
+        case RDL_LLAMA_WK:
+        case RDL_LLAMA_WV: d[0] = c.dim, d[1] = kv; return;
+        case RDL_LLAMA_WO: d[0] = q, d[1] = c.dim; return;
+        case RDL_LLAMA_W_GATE:
+        case RDL_LLAMA_W_UP: d[0] = c.dim, d[1] = c.ffn_dim; return;
+        case RDL_LLAMA_W_DOWN: d[0] = c.ffn_dim, d[1] = c.dim; return;
+    }
+    *nd = 1;
+    d[0] = c.dim;
+}
+
+// Type and shape of one tensor against its slot.
+rdl_status check_tensor(const rdl_llama_config& c, int slot, const rdl_gguf_tensor_info& ti) {
+    const bool norm = slot == RDL_LLAMA_ATTN_NORM || slot == RDL_LLAMA_FFN_NORM || slot == RDL_LLAMA_FINAL_NORM;
+    if (norm ? (ti.ggml_type != 0 && ti.ggml_type != 1) : ti.ggml_type != 2)
+        return api_fail(RDL_ERR_UNSUPPORTED, "tensor '%s' is %s; the decoder takes %s", ti.name,
+                        ggml_name(ti.ggml_type), norm ? "F32 or F16 norm weights" : "Q4_0 matrices");
+    uint64_t d[2];
+    uint32_t nd = 0;
+    slot_dims(c, slot, d, &nd);
+    bool same = ti.n_dims == nd;
+    for (uint32_t i = 0; same && i < nd; i++) same = ti.dims[i] == d[i];
+    if (!same) {
+        const std::string want = nd == 2 ? "[" + std::to_string(d[0]) + ", " + std::to_string(d[1]) + "]"
+                                         : "[" + std::to_string(d[0]) + "]";
+        return api_fail(RDL_ERR_SHAPE_MISMATCH, "tensor '%s': expected dims %s, got %s", ti.name, want.c_str(),
+                        dims_str(ti).c_str());
+    }
+    return api_ok();
+}
+
+// A present tensor's info by GGUF name (the last one of that name).
+bool find_info(const rdl_gguf* g, const char* name, rdl_gguf_tensor_info* ti) {
+    size_t i = 0;
+    return rdl_gguf_find_tensor(g, name, &i) == RDL_OK && rdl_gguf_tensor_info_at(g, i, ti) == RDL_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+rdl_status rdl_llama_load_gguf(const rdl_gguf* g, const rdl_llama_gguf_options* opt, rdl_llama** out) {
+    if (!g || !out) return api_fail(RDL_ERR_NULL_POINTER, "NULL argument");
+    *out = nullptr;
+    rdl_gguf_model_config gc;
+    rdl_status st = rdl_gguf_model_config_get(g, &gc);
+    if (st != RDL_OK) return st;
+    if (strcmp(gc.architecture, "gemma3") == 0)
+        return api_fail(RDL_ERR_UNSUPPORTED, "architecture gemma3 (from_pretrained_gemma3) is not built");
+    // gguf_config_to_model_config + ModelConfig::validate (gguf_bridge.rs:46-84, types.rs:794-826)
+    const uint32_t n_kv = gc.has_n_kv_heads ? gc.n_kv_heads : gc.n_heads;
+    const uint32_t max_seq = (opt && opt->max_seq > 0) ? (uint32_t)opt->max_seq : gc.max_seq_len;
+    if (gc.dim == 0) return api_fail(RDL_ERR_INVALID_DATA, "dim must be > 0");
+    if (gc.n_heads == 0) return api_fail(RDL_ERR_INVALID_DATA, "n_heads must be > 0");
+    if (gc.dim % gc.n_heads != 0)
+        return api_fail(RDL_ERR_INVALID_DATA, "dim (%u) must be divisible by n_heads (%u)", gc.dim, gc.n_heads);
+    if (gc.vocab_size == 0) return api_fail(RDL_ERR_INVALID_DATA, "vocab_size must be > 0");
+    if (gc.n_layers == 0) return api_fail(RDL_ERR_INVALID_DATA, "n_layers must be > 0");
+    if (max_seq == 0) return api_fail(RDL_ERR_INVALID_DATA, "max_seq_len must be > 0");
+    if (gc.has_n_kv_heads && gc.n_kv_heads == 0) return api_fail(RDL_ERR_INVALID_DATA, "n_kv_heads must be > 0");
+    if (gc.n_heads % n_kv != 0)
+        return api_fail(RDL_ERR_INVALID_DATA, "n_heads (%u) must be divisible by n_kv_heads (%u)", gc.n_heads, n_kv);
+    if (gc.n_layers > 4096 || gc.n_heads > 4096 || gc.dim > (1u << 20) || max_seq > (1u << 20))
+        return api_fail(RDL_ERR_UNSUPPORTED, "config beyond the decoder's limits");
+
+    // Presence, in from_pretrained's order: the first missing weight is named.
+    auto missing = [&](const SlotName& s, int layer) {
+        return api_fail(RDL_ERR_NOT_FOUND, "Missing weight: %s", internal_name(s, layer).c_str());
+    };
+    rdl_gguf_tensor_info emb{}, outw{}, up0{};
+    if (!find_info(g, MODEL_NAMES[0].gguf, &emb)) return missing(MODEL_NAMES[0], 0);
+    for (uint32_t l = 0; l < gc.n_layers; l++)
+        for (const SlotName& s : LAYER_NAMES) {
+            char nm[96];
+            snprintf(nm, sizeof nm, "blk.%u.%s", l, s.gguf);
+            rdl_gguf_tensor_info ti;
+            if (!find_info(g, nm, &ti)) {
+                if (s.slot == RDL_LLAMA_W_GATE)  // FeedForward without gate: Activation::Silu MLP
+                    return api_fail(RDL_ERR_UNSUPPORTED, "%s: the decoder is SwiGLU only (no gate weight)", nm);
+                return missing(s, (int)l);
+            }
+        }
+    rdl_gguf_tensor_info norm{};
+    if (!find_info(g, MODEL_NAMES[1].gguf, &norm)) return missing(MODEL_NAMES[1], 0);
+    if (!find_info(g, MODEL_NAMES[2].gguf, &outw)) return missing(MODEL_NAMES[2], 0);
+    if (!find_info(g, "blk.0.ffn_up.weight", &up0)) return missing(LAYER_NAMES[4], 0);
+
+    rdl_llama_config c{};
+    c.dim = (int32_t)gc.dim;
+    c.n_layers = (int32_t)gc.n_layers;
+    c.n_heads = (int32_t)gc.n_heads;
+    c.n_kv_heads = (int32_t)n_kv;
+    c.head_dim = (int32_t)(gc.dim / gc.n_heads);  // MultiHeadAttention::from_weights: d_model / num_heads
+    // the matrices fix the FFN width and vocabulary (Linear::from_weights takes their shapes)
+    c.ffn_dim = up0.n_dims == 2 ? (int32_t)std::min<uint64_t>(up0.dims[1], INT32_MAX) : 0;
+    c.vocab = outw.n_dims == 2 ? (int32_t)std::min<uint64_t>(outw.dims[1], INT32_MAX) : 0;
+    c.max_seq = (int32_t)max_seq;
+    c.norm_eps = gc.norm_eps;
+    c.rope_theta = gc.rope_theta;
+    c.kv_f16 = opt ? opt->kv_f16 : 1;
+    c.max_batch = (opt && opt->max_batch > 0) ? opt->max_batch : 32;
+
+    // Type, shape and file bounds of every mapped tensor before allocating.
+    const size_t nt = [&] { size_t n = 0; rdl_gguf_tensor_count(g, &n); return n; }();
+    std::vector<std::pair<size_t, std::pair<int, int>>> plan;  // tensor index, (slot, layer)
+    for (size_t i = 0; i < nt; i++) {
+        rdl_gguf_tensor_info ti;
+        if ((st = rdl_gguf_tensor_info_at(g, i, &ti)) != RDL_OK) return st;
+        int slot = 0, layer = 0;
+        if (strlen(ti.name) != ti.name_len || !gguf_slot(ti.name, c.n_layers, &slot, &layer)) continue;
+        if ((st = check_tensor(c, slot, ti)) != RDL_OK) return st;
+        const void* src = nullptr;
+        uint64_t len = 0;
+        if ((st = rdl_gguf_tensor_data(g, i, &src, &len)) != RDL_OK) return st;
+        plan.push_back({i, {slot, layer}});
+    }
+
+    rdl_llama* h = nullptr;
+    if ((st = rdl_llama_create(&c, &h)) != RDL_OK) return st;
+    rdl::LlamaModel& M = h->m;
+    auto fail = [&](rdl_status s) {
+        rdl_llama_free(h);
+        return s;
+    };
+    rdl::Stager stage;
+    std::vector<float> f32;
+    for (const auto& p : plan) {
+        const void* src = nullptr;
+        uint64_t len = 0;
+        rdl_gguf_tensor_info ti;
+        rdl_gguf_tensor_info_at(g, p.first, &ti);
+        rdl_gguf_tensor_data(g, p.first, &src, &len);
+        SlotTarget t;
+        if ((st = slot_target(M, p.second.first, p.second.second, &t)) != RDL_OK) return fail(st);
+        if (ti.ggml_type == 1) {  // F16 norm weights: to f32 as Tensor::to_f32 does
+            f32.resize((size_t)c.dim);
+            const auto* hp = static_cast<const uint8_t*>(src);
+            for (int j = 0; j < c.dim; j++) {
+                _Float16 v;
+                memcpy(&v, hp + 2 * j, 2);
+                f32[j] = (float)v;
+            }
+            src = f32.data();
+        }
+        const hipError_t e = stage.copy2d(src, t.row_bytes, t.rows, t.dst, t.dpitch, M.stream);
+        if (e != hipSuccess)
+            return fail(api_fail(RDL_ERR_HIP, "upload of '%s' failed: %s", ti.name, hipGetErrorString(e)));
+    }
+    // block-scale scan of each matrix once (the GEMM's f16 range)
+    std::vector<rdl::LlamaModel::Mat*> mats = {&M.out};
+    for (auto& L : M.layers) mats.insert(mats.end(), {&L.qkv, &L.o, &L.gu, &L.down});
+    for (rdl::LlamaModel::Mat* m : mats) {
+        SlotTarget t;
+        t.mat = m;
+        if ((st = finish_slot(t)) != RDL_OK) return fail(st);
+    }
+    *out = h;
+    return api_ok();
+}
+
+rdl_status rdl_llama_get_config(const rdl_llama* model, rdl_llama_config* out) {
+    if (!model || !out) return api_fail(RDL_ERR_NULL_POINTER, "NULL argument");
+    *out = model->m.cfg;
     return api_ok();
 }
 

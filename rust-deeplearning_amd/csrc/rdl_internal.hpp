@@ -86,6 +86,23 @@ inline size_t block_bytes(WType t) {
     return 0;
 }
 
+// ---- host -> device staging ------------------------------------------------
+// Two pinned buffers of CHUNK bytes: the host copy of one chunk into a buffer
+// overlaps the DMA of the other buffer's chunk.  Used to move GGUF tensor
+// bytes from a file mapping into HBM.  Not thread-safe; synchronous (returns
+// once every byte has reached the device).
+struct Stager {
+    static constexpr size_t CHUNK = (size_t)32 << 20;
+    uint8_t* buf[2] = {nullptr, nullptr};
+    hipEvent_t ev[2] = {nullptr, nullptr};
+    ~Stager();
+    hipError_t init();
+    // `rows` rows of row_bytes each, packed in src, to dst with row pitch
+    // dpitch (dpitch == row_bytes: one packed copy of any length; otherwise
+    // row_bytes <= CHUNK).
+    hipError_t copy2d(const void* src, size_t row_bytes, size_t rows, void* dst, size_t dpitch, hipStream_t s);
+};
+
 // ---- kernel-boundary timing -----------------------------------------------
 // When set (rdl_time_next_launch), the next product-kernel launch of this
 // thread records its start/end into these events via hipExtLaunchKernel.

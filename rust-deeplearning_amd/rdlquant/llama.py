@@ -36,6 +36,14 @@ _decl("rdl_llama_forward", _i32, _p, C.POINTER(C.c_int32), _sz, C.POINTER(C.c_fl
 _decl("rdl_llama_generate_greedy", _i32, _p, C.POINTER(C.c_int32), _sz, _sz, C.POINTER(C.c_int32))
 _decl("rdl_llama_last_timing", _i32, _p, C.POINTER(C.c_float), C.POINTER(C.c_float))
 _decl("rdl_llama_rope_tables", _i32, _p, C.POINTER(C.c_float), C.POINTER(C.c_float), _sz)
+_decl("rdl_llama_get_config", _i32, _p, C.POINTER(_Config))
+
+
+class _GgufOptions(C.Structure):
+    _fields_ = [("max_seq", C.c_int32), ("max_batch", C.c_int32), ("kv_f16", C.c_int32)]
+
+
+_decl("rdl_llama_load_gguf", _i32, _p, C.POINTER(_GgufOptions), C.POINTER(_p))
 
 
 @dataclass
@@ -73,6 +81,31 @@ class LlamaModel:
         cfg = config._c()
         check(lib.rdl_llama_create(C.byref(cfg), C.byref(h)))
         self._h = h
+
+    @classmethod
+    def from_gguf(cls, gguf, max_seq: int = 0, max_batch: int = 32, kv_f16: bool = True) -> "LlamaModel":
+        """LlmModel::from_pretrained over a GGUF file (a path or an open
+        rdlquant.gguf.GGUFFile): config from the metadata, tensors through the
+        Llama weight map, bytes from the file mapping straight to HBM
+        (include/rdl_llama.h: rdl_llama_load_gguf).  max_seq 0: the file's
+        context_length."""
+        from .gguf import GGUFFile
+
+        f = gguf if isinstance(gguf, GGUFFile) else GGUFFile.parse_header(gguf)
+        opt = _GgufOptions(max_seq, max_batch, int(kv_f16))
+        h = _p()
+        check(lib.rdl_llama_load_gguf(f.handle, C.byref(opt), C.byref(h)))
+        c = _Config()
+        status = lib.rdl_llama_get_config(h, C.byref(c))
+        if status != 0:
+            lib.rdl_llama_free(h)
+            check(status)
+        self = cls.__new__(cls)
+        self._h = h
+        self.config = LlamaConfig(c.dim, c.n_layers, c.n_heads, c.n_kv_heads, c.head_dim, c.ffn_dim, c.vocab,
+                                  c.max_seq, float(c.norm_eps), float(c.rope_theta), bool(c.kv_f16),
+                                  c.max_batch)
+        return self
 
     def close(self):
         if getattr(self, "_h", None):

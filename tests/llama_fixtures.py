@@ -45,3 +45,24 @@ def tiny_weights(cfg, seed=1234):
     slots += [(L.FINAL_NORM, 0, fin), (L.OUTPUT, 0, out)]
     ref["final_norm"], ref["output"] = fin, out
     return slots, ref
+
+
+def gguf_name(slot, layer):
+    """The GGUF tensor name of a decoder slot (gguf_llama_weight_map,
+    rustml/gguf/main/src/core/weight_map.rs:26-73)."""
+    from rdlquant import llama as L
+    model = {L.TOKEN_EMBEDDING: "token_embd.weight", L.FINAL_NORM: "output_norm.weight",
+             L.OUTPUT: "output.weight"}
+    per_layer = {L.ATTN_NORM: "attn_norm", L.WQ: "attn_q", L.WK: "attn_k", L.WV: "attn_v", L.WO: "attn_output",
+                 L.FFN_NORM: "ffn_norm", L.W_GATE: "ffn_gate", L.W_UP: "ffn_up", L.W_DOWN: "ffn_down"}
+    return model[slot] if slot in model else f"blk.{layer}.{per_layer[slot]}.weight"
+
+
+def write_gguf(path, cfg, slots, **kw):
+    """A Llama GGUF file holding the bytes of `slots` (as tiny_weights returns
+    them); keyword arguments go to gguf_writer.llama_builder."""
+    from rdlquant import gguf_writer
+    by_name = {gguf_name(s, l): a for s, l, a in slots}
+    b = gguf_writer.llama_builder(cfg, lambda name: by_name[name], **kw)
+    b.write(path)
+    return b

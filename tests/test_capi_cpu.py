@@ -16,7 +16,7 @@ def test_exports_every_declared_symbol(rq):
 
 
 def test_status_strings(rq):
-    for code in range(9):
+    for code in range(14):
         assert rq.lib.rdl_status_string(code)
     assert rq.version().startswith("rdlquant")
 
