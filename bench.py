@@ -41,9 +41,11 @@ KERNEL_KEY = "gemv_fused_kernel<2, false, 3, 2, true, 8>|config2"
 # configs[4]
 LLAMA_SEED = 0x5EED0005
 PROMPT_LEN, GEN_TOKENS = 128, 256
+# not a BASELINE config: the lm_head of a llama.cpp Q4_0 7B file is Q6_K
+Q6K_LM_HEAD = "Q6_K GEMV 32000x4096 (the output matrix of llama.cpp Q4_0 7B files)"
 
 # GGML type id -> (elements per block, bytes per block)
-BLOCK = {2: (32, 18), 8: (32, 34), 12: (256, 144)}
+BLOCK = {2: (32, 18), 8: (32, 34), 12: (256, 144), 14: (256, 210)}
 
 
 def algorithmic_bytes(n, k, dtype=2):
@@ -327,6 +329,87 @@ def decode_line(rig, reps=2):
     }
 
 
+def load_line(rig):
+    """A synthetic config-5 (Llama-7B-shape Q4_0) GGUF file written to TMPDIR,
+    then loaded into a device-resident decoder (rdl_llama_load_gguf): parse of
+    the mapped file, type/shape checks and the pinned-staged upload of every
+    tensor.  The file was just written, so its pages are in the page cache:
+    this is the load rate from memory, not from a cold disk."""
+    import os
+    import shutil
+    import tempfile
+
+    import numpy as np
+
+    from rdlquant import gguf_writer
+    from rdlquant.gguf import GGUFFile
+    from rdlquant.llama import LlamaConfig, LlamaModel
+
+    cfg = LlamaConfig()
+    shapes = gguf_writer.llama_tensor_shapes(cfg)
+    cache = {}
+
+    def data(name):  # one seeded tensor per distinct shape (load time does not depend on values)
+        dims, t = shapes[name]
+        key = (tuple(dims), t)
+        if key not in cache:
+            if t == gguf_writer.GGML_F32:
+                cache[key] = np.ones(dims[0], np.float32)
+            else:
+                cache[key] = rig.synth.q4_0_weights(dims[1], dims[0], LLAMA_SEED + len(cache))
+        return cache[key]
+
+    tmp = tempfile.mkdtemp(prefix="rdl_load_", dir=os.environ.get("TMPDIR", "/tmp"))
+    try:
+        path = os.path.join(tmp, "llama7b_q4_0.gguf")
+        t0 = time.perf_counter()
+        size = gguf_writer.llama_builder(cfg, data).write(path)
+        write_s = time.perf_counter() - t0
+        cache.clear()
+        loads = []
+        for _ in range(2):
+            t0 = time.perf_counter()
+            f = GGUFFile.parse_header(path)
+            t1 = time.perf_counter()
+            m = LlamaModel.from_gguf(f, max_seq=2048, max_batch=128)
+            rig.torch.cuda.synchronize()
+            t2 = time.perf_counter()
+            toks = m.generate_greedy([1, 2, 3, 4], 4)
+            m.close()
+            f.close()
+            rig.torch.cuda.empty_cache()
+            loads.append((t1 - t0, t2 - t0, [int(t) for t in toks]))
+        # the reference's I/O pattern (parser.rs:143-148, 292-296, 346): the
+        # file read into memory twice and every tensor copied out of it
+        t0 = time.perf_counter()
+        with open(path, "rb") as fh:
+            head = fh.read()
+        with open(path, "rb") as fh:
+            whole = fh.read()
+        ref_f = GGUFFile.parse_bytes(head)
+        del head
+        copies = [bytes(whole[ref_f.data_offset + ti.offset:ref_f.data_offset + ti.offset + ti.n_bytes])
+                  for ti in ref_f.tensor_infos]
+        ref_s = time.perf_counter() - t0
+        del copies, whole, ref_f
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    parse_s, load_s, toks = min(loads, key=lambda r: r[1])
+    return {
+        "workload": "GGUF load: config5 Llama-7B-shape Q4_0 file (291 tensors) -> device decoder "
+                    "(parse + checks + upload of every tensor), file in the page cache",
+        "file_bytes": size,
+        "write_s": round(write_s, 2),
+        "parse_ms": round(parse_s * 1e3, 3),
+        "load_s": round(load_s, 3),
+        "value": round(size / load_s / 1e9, 2),
+        "unit": "GB/s (file bytes / load time)",
+        "reference_io_pattern_s": round(ref_s, 3),
+        "reference_io_pattern_note": "host only: read_to_end twice + one Vec per tensor, no device upload",
+        "first_tokens": toks,
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -335,8 +418,9 @@ def main():
     ap.add_argument("--copies", type=int, default=24)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--workload", default="all", choices=["all", "gemv", "q8_0", "q4_k", "gemm", "decode"],
-                    help="all: the headline line plus every other configuration; otherwise only one")
+    ap.add_argument("--workload", default="all", choices=["all", "gemv", "q8_0", "q4_k", "q6_k", "gemm", "decode", "load"],
+                    help="all: the headline line plus configs 1, 3, 4, 5 and the Q6_K lm_head; otherwise only one "
+                         "(load: the GGUF file load, run only when asked)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="first run 3 plain device copies of this many MiB (a known-size "
                          "reference for HBM traffic counters)")
@@ -362,7 +446,7 @@ def main():
         del src, dst
 
     wl = args.workload
-    if wl in ("q8_0", "q4_k", "gemm", "decode"):
+    if wl in ("q8_0", "q4_k", "q6_k", "gemm", "decode", "load"):
         if wl == "q8_0":
             line = gemv_line(rig, "config1: Q8_0 GEMV 4096x4096", 8, 4096, 4096, 0x5EED0001,
                              args.steps, args.warmup)
@@ -371,8 +455,12 @@ def main():
                               args.steps, args.warmup),
                     gemv_line(rig, "config3 down: Q4_K GEMV 4096x14336", 12, 4096, 14336, 0x5EED0013,
                               args.steps, args.warmup)]
+        elif wl == "q6_k":
+            line = gemv_line(rig, Q6K_LM_HEAD, 14, 32000, 4096, 0x5EED0006, args.steps, args.warmup)
         elif wl == "gemm":
             line = gemm_lines(rig, [16, 64, 512, 2048])
+        elif wl == "load":
+            line = load_line(rig)
         else:
             line = decode_line(rig)
         print(json.dumps(line), flush=True)
@@ -446,6 +534,7 @@ def main():
                                          0x5EED0003, sub_steps, sub_warm),
             "config3_q4_k_down": gemv_line(rig, "config3 down: Q4_K GEMV 4096x14336", 12, 4096, 14336,
                                            0x5EED0013, sub_steps, sub_warm),
+            "q6_k_lm_head": gemv_line(rig, Q6K_LM_HEAD, 14, 32000, 4096, 0x5EED0006, sub_steps, sub_warm),
             "config4_gemm": gemm_lines(rig, [16, 64, 512, 2048]),
             "config5_decode": decode_line(rig),
         }

@@ -45,6 +45,9 @@ typedef struct rdl_llama_config {
     float rope_theta;
     int32_t kv_f16;      /* 1: f16 KV cache, 0: f32 (the reference's) */
     int32_t max_batch;   /* most rows one forward call takes (prefill chunk) */
+    int32_t output_dtype; /* GGML type of the output matrix: RDL_DTYPE_Q4_0 (also
+                             when 0), _Q8_0, _Q4_1, _Q4_K or _Q6_K (K-quants:
+                             dim % 256 == 0) */
 } rdl_llama_config;
 
 typedef struct rdl_llama rdl_llama;
@@ -64,7 +67,7 @@ enum {
     RDL_LLAMA_W_UP = 8,            /* [ffn_dim, dim] Q4_0 */
     RDL_LLAMA_W_DOWN = 9,          /* [dim, ffn_dim] Q4_0 */
     RDL_LLAMA_FINAL_NORM = 10,     /* [dim] f32 */
-    RDL_LLAMA_OUTPUT = 11          /* [vocab, dim] Q4_0 */
+    RDL_LLAMA_OUTPUT = 11          /* [vocab, dim] in output_dtype's GGUF blocks */
 };
 
 /* Allocates weights, KV cache and activations on the current device. */
@@ -76,7 +79,8 @@ rdl_status rdl_llama_set_weight(rdl_llama* model, int32_t slot, int32_t layer, c
                                 size_t len);
 
 /* Seeded synthetic weights on the device, all slots: Q4_0 blocks with
- * nibbles uniform in [0, 15] and d = f16(|N(0, 0.02)| / 8), norm weights 1.0. */
+ * nibbles uniform in [0, 15] and d = f16(|N(0, 0.02)| / 8), norm weights 1.0.
+ * Q4_0 output matrices only (RDL_ERR_UNSUPPORTED otherwise). */
 rdl_status rdl_llama_init_random(rdl_llama* model, uint64_t seed);
 
 /* Empties the KV cache (KVCache::new state, current_len = 0). */

@@ -1,6 +1,6 @@
 /*
  * rdl_quant.h -- C ABI of librdlquant.so, the MI355X (gfx950) implementation
- * of rustml's GGUF block-quantized matmul path (Q8_0, Q4_0, Q4_1, Q4_K).
+ * of rustml's GGUF block-quantized matmul path (Q8_0, Q4_0, Q4_1, Q4_K, Q6_K).
  *
  * Reference interface replaced (paths relative to the rust-deeplearning
  * repository root):
@@ -21,7 +21,7 @@
  *   - Rust slices become (pointer, length) pairs.  The reference does not check
  *     slice lengths (an out-of-range slice panics); this ABI checks them and
  *     returns RDL_ERR_SHAPE_MISMATCH instead.
- *   - K % 32 != 0 (K % 256 for Q4_K) returns RDL_ERR_BLOCK_ALIGNMENT, checked
+ *   - K % 32 != 0 (K % 256 for Q4_K / Q6_K) returns RDL_ERR_BLOCK_ALIGNMENT, checked
  *     before any length check, as in quantize.rs:208-213 / 272-277 / 333-338.
  *   - Host-pointer entry points (rdl_matmul_*, rdl_quantize_row_q8_0) are
  *     synchronous, like the reference's Vec-returning functions: inputs are
@@ -62,7 +62,8 @@ enum {
     RDL_DTYPE_Q4_0 = 2,
     RDL_DTYPE_Q4_1 = 3,
     RDL_DTYPE_Q8_0 = 8,
-    RDL_DTYPE_Q4_K = 12 /* additive extension: rustml_core::DType has no Q4_K */
+    RDL_DTYPE_Q4_K = 12, /* additive extension: rustml_core::DType has no Q4_K */
+    RDL_DTYPE_Q6_K = 14  /* additive extension: rustml_core::DType has no Q6_K */
 };
 
 /* ---- arithmetic modes (Linear::use_native_q4, linear.rs:23-24, 96-98) ---- */
@@ -121,6 +122,14 @@ rdl_status rdl_matmul_f32_q4_1_native(const float* input_data, size_t input_len,
  * dequantize_q4k :549-593) and runs the F32 Linear path (linear.rs:167-170); this
  * computes the same product straight from the 144-byte super-blocks. */
 rdl_status rdl_matmul_f32_q4_k(const float* input_data, size_t input_len,
+                               const uint8_t* weight_bytes, size_t weight_len, size_t m,
+                               size_t in_features, size_t out_features, float* output,
+                               size_t output_len);
+/* Additive extension (no reference counterpart): Q6_K weights kept resident.
+ * The reference dequantizes Q6_K at load (parser.rs:321-325, dequantize_q6k
+ * :510-547) and runs the F32 Linear path; this computes the same product
+ * straight from the 210-byte super-blocks.  in_features % 256 == 0. */
+rdl_status rdl_matmul_f32_q6_k(const float* input_data, size_t input_len,
                                const uint8_t* weight_bytes, size_t weight_len, size_t m,
                                size_t in_features, size_t out_features, float* output,
                                size_t output_len);
@@ -204,13 +213,14 @@ rdl_status rdl_linear_fused_dev(const rdl_weight* w, const float* x_dev, size_t 
 rdl_status rdl_quantize_row_q8_0_dev(const float* x_dev, size_t n, uint8_t* out_dev,
                                      float* scales_dev, void* stream);
 
-/* Tensor::to_f32 for Q4_0 / Q4_1 / Q8_0 rows (tensor.rs:535-639) and
- * dequantize_q4k for Q4_K rows (rustml/gguf/main/src/core/parser.rs:549-593):
- * dequantize the rows `row_ids[0..n_rows)` (int32, device, each < N) of a
- * weight into out_dev f32 [n_rows, K], bit-exact.  This is the embedding
- * gather of the decode loop (rustml/nn/main/src/core/embedding.rs:50-76) on a
- * matrix kept quantized, and the load-time F32 expansion of Q4_K tensors
- * (parser.rs:321-325) when a caller wants it. */
+/* Tensor::to_f32 for Q4_0 / Q4_1 / Q8_0 rows (tensor.rs:535-639),
+ * dequantize_q4k for Q4_K rows (rustml/gguf/main/src/core/parser.rs:549-593)
+ * and dequantize_q6k for Q6_K rows (parser.rs:510-547): dequantize the rows
+ * `row_ids[0..n_rows)` (int32, device, each < N) of a weight into out_dev f32
+ * [n_rows, K], bit-exact.  This is the embedding gather of the decode loop
+ * (rustml/nn/main/src/core/embedding.rs:50-76) on a matrix kept quantized,
+ * and the load-time F32 expansion of K-quant tensors (parser.rs:321-325) when
+ * a caller wants it. */
 rdl_status rdl_dequantize_rows_dev(const rdl_weight* w, const int32_t* row_ids_dev,
                                    size_t n_rows, float* out_dev, void* stream);
 

@@ -42,7 +42,11 @@ class LlamaRef:
 
     def _linear(self, key, x, n, k):
         m = x.shape[0]
-        return orc.matmul("q4", x, self.w[key], m, k, n, threads=self.threads).reshape(m, n)
+        # the output matrix may be another GGUF type ("output_kind": an oracle
+        # matmul kind); the reference runs K-quants as F32 after load-time
+        # dequantization, which the oracle's q4k / q6k kinds restate
+        kind = self.w.get("output_kind", "q4") if key == "output" else "q4"
+        return orc.matmul(kind, x, self.w[key], m, k, n, threads=self.threads).reshape(m, n)
 
     def _rope(self, t, start):
         # t [heads, S, D]: out1 = x1 cos - x2 sin, out2 = x1 sin + x2 cos

@@ -48,13 +48,14 @@ _decl("orc_dot_q4_block_lanes", _f, _fp, _u8p, _f)
 _decl("orc_dot_q4q8_block", C.c_int32, _u8p, _i8p)
 _decl("orc_dot_q4_1_q8_block", None, _u8p, _i8p, _i32p, _i32p)
 _decl("orc_quantize_row_q8_0", None, _fp, _sz, _u8p, _fp)
-for _n in ("q8", "q4", "q4_native", "q4_1", "q4_1_native", "q4_cols", "q4k"):
+for _n in ("q8", "q4", "q4_native", "q4_1", "q4_1_native", "q4_cols", "q4k", "q6k"):
     _decl(f"orc_matmul_f32_{_n}", _i, _fp, _u8p, _sz, _sz, _sz, _sz, _fp, _i)
 _decl("orc_matmul_f32_f32", _i, _fp, _fp, _sz, _sz, _sz, _fp, _i)
 _decl("orc_q4_0_q8_0_block_dots", _i, _fp, _u8p, _sz, _sz, _sz, _sz, _i32p)
 for _n in ("q4_0", "q4_1", "q8_0"):
     _decl(f"orc_to_f32_{_n}", _i, _u8p, _sz, _sz, _fp)
 _decl("orc_dequantize_q4k", _i, _u8p, _sz, _sz, _fp)
+_decl("orc_dequantize_q6k", _i, _u8p, _sz, _sz, _fp)
 _decl("orc_rope_tables", None, _i, _i, _f, _fp, _fp)
 _decl("orc_rms_norm_row", None, _fp, _fp, _sz, _f, _fp)
 
@@ -124,7 +125,7 @@ def quantize_row_q8_0(x):
 
 
 def matmul(kind, x, w, m, k, n, threads=1):
-    """kind in q8, q4, q4_native, q4_1, q4_1_native, q4_cols, q4k."""
+    """kind in q8, q4, q4_native, q4_1, q4_1_native, q4_cols, q4k, q6k."""
     x, xp = _f32(x)
     w, wp = _u8(w)
     y = np.zeros(m * n, dtype=np.float32)
@@ -156,7 +157,7 @@ def to_f32(kind, w, n_elements):
     w, wp = _u8(w)
     out = np.zeros(n_elements, dtype=np.float32)
     fn = {"q4_0": lib.orc_to_f32_q4_0, "q4_1": lib.orc_to_f32_q4_1, "q8_0": lib.orc_to_f32_q8_0,
-          "q4k": lib.orc_dequantize_q4k}[kind]
+          "q4k": lib.orc_dequantize_q4k, "q6k": lib.orc_dequantize_q6k}[kind]
     rc = fn(wp, w.size, n_elements, out.ctypes.data_as(_fp))
     if rc:
         raise OracleError(rc)

@@ -26,6 +26,7 @@ enum {
     Q4_1_BYTES = 20,
     QK_K = 256,
     Q4_K_BYTES = 144,
+    Q6_K_BYTES = 210,
 };
 
 /* ------------------------------------------------------------------------ */
@@ -268,7 +269,7 @@ void orc_quantize_row_q8_0(const float* input, size_t n, uint8_t* output, float*
 /* matmuls                                                                   */
 /* ------------------------------------------------------------------------ */
 
-typedef enum { K_Q8, K_Q4, K_Q4_NATIVE, K_Q4_1, K_Q4_1_NATIVE, K_Q4K } kind_t;
+typedef enum { K_Q8, K_Q4, K_Q4_NATIVE, K_Q4_1, K_Q4_1_NATIVE, K_Q4K, K_Q6K } kind_t;
 
 typedef struct {
     kind_t kind;
@@ -288,6 +289,7 @@ static size_t block_bytes_of(kind_t kd) {
         case K_Q4_1:
         case K_Q4_1_NATIVE: return Q4_1_BYTES;
         case K_Q4K: return Q4_K_BYTES;
+        case K_Q6K: return Q6_K_BYTES;
     }
     return 0;
 }
@@ -296,11 +298,14 @@ static void run_row(const job_t* j, size_t r, uint8_t* q8buf, float* q8s, float*
     const size_t k = j->k;
     const float* xr = j->x + r * k;
     float* yr = j->y + r * j->n;
-    if (j->kind == K_Q4K) {
+    if (j->kind == K_Q4K || j->kind == K_Q6K) {
         const size_t nsb = k / QK_K;
-        const size_t row_bytes = nsb * Q4_K_BYTES;
+        const size_t row_bytes = nsb * block_bytes_of(j->kind);
         for (size_t c = j->col_begin; c < j->col_end; c++) {
-            orc_dequantize_q4k(j->w + c * row_bytes, row_bytes, k, wrow);
+            if (j->kind == K_Q4K)
+                orc_dequantize_q4k(j->w + c * row_bytes, row_bytes, k, wrow);
+            else
+                orc_dequantize_q6k(j->w + c * row_bytes, row_bytes, k, wrow);
             float dot = 0.0f;
             for (size_t l = 0; l < k; l++) dot += xr[l] * wrow[l];
             yr[c] = dot;
@@ -363,7 +368,7 @@ static void* job_thread(void* arg) {
     size_t nb = j->k / QK + 1;
     uint8_t* q8buf = (uint8_t*)malloc(nb * Q8_0_BYTES);
     float* q8s = (float*)malloc(nb * sizeof(float));
-    float* wrow = (j->kind == K_Q4K) ? (float*)malloc(j->k * sizeof(float)) : NULL;
+    float* wrow = (j->kind == K_Q4K || j->kind == K_Q6K) ? (float*)malloc(j->k * sizeof(float)) : NULL;
     for (size_t r = j->row_begin; r < j->row_end; r++) run_row(j, r, q8buf, q8s, wrow);
     free(q8buf);
     free(q8s);
@@ -401,7 +406,7 @@ static void run_split(job_t proto, int by_rows, int threads) {
 
 static int matmul_common(kind_t kd, const float* x, const uint8_t* w, size_t w_len, size_t m,
                          size_t k, size_t n, float* y, int threads, int by_rows) {
-    size_t unit = (kd == K_Q4K) ? QK_K : QK;
+    size_t unit = (kd == K_Q4K || kd == K_Q6K) ? QK_K : QK;
     if (k % unit != 0) return ORC_ERR_BLOCK_ALIGNMENT;
     if (w_len < n * (k / unit) * block_bytes_of(kd)) return ORC_ERR_SHAPE_MISMATCH;
     job_t j = {kd, x, w, m, k, n, y, 0, m, 0, n};
@@ -436,6 +441,11 @@ int orc_matmul_f32_q4_cols(const float* x, const uint8_t* w, size_t w_len, size_
 int orc_matmul_f32_q4k(const float* x, const uint8_t* w, size_t w_len, size_t m, size_t k, size_t n,
                        float* y, int threads) {
     return matmul_common(K_Q4K, x, w, w_len, m, k, n, y, threads, 0);
+}
+
+int orc_matmul_f32_q6k(const float* x, const uint8_t* w, size_t w_len, size_t m, size_t k, size_t n,
+                       float* y, int threads) {
+    return matmul_common(K_Q6K, x, w, w_len, m, k, n, y, threads, 0);
 }
 
 int orc_q4_0_q8_0_block_dots(const float* x, const uint8_t* w, size_t w_len, size_t m, size_t k,
@@ -528,6 +538,40 @@ int orc_dequantize_q4k(const uint8_t* data, size_t data_len, size_t n_elements, 
             float d2 = d * (float)sc[2 * c + 1], m2 = dmin * (float)mn[2 * c + 1];
             for (int l = 0; l < 32; l++) o[64 * c + l] = d1 * (float)(q[l] & 0xF) - m1;
             for (int l = 0; l < 32; l++) o[64 * c + 32 + l] = d2 * (float)(q[l] >> 4) - m2;
+        }
+    }
+    return ORC_OK;
+}
+
+/* parser.rs:510-547: two halves of 128 elements; element half*128 + 32*t + l
+ * takes its low four bits from ql (byte half*64 + l for t = 0, 2 and
+ * half*64 + 32 + l for t = 1, 3; low nibble for t < 2, high for t >= 2), its
+ * high two bits from bits 2t, 2t+1 of qh[half*32 + l], and the signed scale
+ * scales[half*8 + l/16 + 2t]; value (d * scale) * (q - 32). */
+int orc_dequantize_q6k(const uint8_t* data, size_t data_len, size_t n_elements, float* out) {
+    if (n_elements % QK_K) return ORC_ERR_BLOCK_ALIGNMENT;
+    size_t nb = n_elements / QK_K;
+    if (data_len < nb * Q6_K_BYTES) return ORC_ERR_SHAPE_MISMATCH;
+    for (size_t b = 0; b < nb; b++) {
+        const uint8_t* blk = data + b * Q6_K_BYTES;
+        const uint8_t* ql = blk;
+        const uint8_t* qh = blk + 128;
+        const int8_t* sc = (const int8_t*)(blk + 192);
+        const float d = rd_f16(blk + 208);
+        float* o = out + b * QK_K;
+        for (int half = 0; half < 2; half++) {
+            for (int l = 0; l < 32; l++) {
+                const int is = l / 16;
+                const uint8_t lo = ql[half * 64 + l], hi = ql[half * 64 + 32 + l], h = qh[half * 32 + l];
+                const int q1 = (int)((lo & 0xF) | (((h >> 0) & 3) << 4)) - 32;
+                const int q2 = (int)((hi & 0xF) | (((h >> 2) & 3) << 4)) - 32;
+                const int q3 = (int)((lo >> 4) | (((h >> 4) & 3) << 4)) - 32;
+                const int q4 = (int)((hi >> 4) | (((h >> 6) & 3) << 4)) - 32;
+                o[half * 128 + l] = d * (float)sc[half * 8 + is] * (float)q1;
+                o[half * 128 + l + 32] = d * (float)sc[half * 8 + is + 2] * (float)q2;
+                o[half * 128 + l + 64] = d * (float)sc[half * 8 + is + 4] * (float)q3;
+                o[half * 128 + l + 96] = d * (float)sc[half * 8 + is + 6] * (float)q4;
+            }
         }
     }
     return ORC_OK;

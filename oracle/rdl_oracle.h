@@ -102,6 +102,14 @@ int orc_dequantize_q4k(const uint8_t* data, size_t data_len, size_t n_elements, 
  * sequentially in f32 -- parity unpinned beyond the f64 tolerance check. */
 int orc_matmul_f32_q4k(const float* x, const uint8_t* w, size_t w_len, size_t m, size_t k,
                        size_t n, float* y, int threads);
+/* dequantize_q6k: rustml/gguf/main/src/core/parser.rs:510-547 (ql low nibbles,
+ * qh high bit pairs, int8 scales per 16 elements, f16 d at byte 208). */
+int orc_dequantize_q6k(const uint8_t* data, size_t data_len, size_t n_elements, float* out);
+/* Q6_K "GEMV" as the reference runs it: dequantized at load (parser.rs:321-325),
+ * then the F32 Linear; each dot summed sequentially in f32 (parity unpinned
+ * beyond the f64 tolerance check, as for Q4_K). */
+int orc_matmul_f32_q6k(const float* x, const uint8_t* w, size_t w_len, size_t m, size_t k,
+                       size_t n, float* y, int threads);
 /* The timed part of the reference Q4_K path: an F32 GEMV over an already
  * dequantized [N,K] matrix, split over output rows on `threads`. */
 int orc_matmul_f32_f32(const float* x, const float* w, size_t m, size_t k, size_t n, float* y,

@@ -65,12 +65,14 @@ const char* type_name(WType t) {
         case WType::Q4_1: return "Q4_1";
         case WType::Q8_0: return "Q8_0";
         case WType::Q4_K: return "Q4_K";
+        case WType::Q6_K: return "Q6_K";
     }
     return "?";
 }
 
 bool valid_type(int32_t d) {
-    return d == RDL_DTYPE_Q4_0 || d == RDL_DTYPE_Q4_1 || d == RDL_DTYPE_Q8_0 || d == RDL_DTYPE_Q4_K;
+    return d == RDL_DTYPE_Q4_0 || d == RDL_DTYPE_Q4_1 || d == RDL_DTYPE_Q8_0 || d == RDL_DTYPE_Q4_K ||
+           d == RDL_DTYPE_Q6_K;
 }
 
 // Visible gfx950 devices; 0 without a GPU.
@@ -284,6 +286,11 @@ rdl_status rdl_matmul_f32_q4_1_native(const float* x, size_t x_len, const uint8_
 rdl_status rdl_matmul_f32_q4_k(const float* x, size_t x_len, const uint8_t* w, size_t w_len,
                                size_t m, size_t k, size_t n, float* y, size_t y_len) {
     return host_matmul(WType::Q4_K, false, x, x_len, w, w_len, m, k, n, y, y_len);
+}
+
+rdl_status rdl_matmul_f32_q6_k(const float* x, size_t x_len, const uint8_t* w, size_t w_len,
+                               size_t m, size_t k, size_t n, float* y, size_t y_len) {
+    return host_matmul(WType::Q6_K, false, x, x_len, w, w_len, m, k, n, y, y_len);
 }
 
 rdl_status rdl_quantize_row_q8_0(const float* input, size_t input_len, uint8_t* output,

@@ -7,6 +7,7 @@
 //   Q4_1 float   matmul_f32_q4_1       quantize.rs:429-495
 //   Q4_1 native  matmul_f32_q4_1_native quantize.rs:501-572
 //   Q4_K float   dequantize_q4k (rustml/gguf/main/src/core/parser.rs:549-593) + F32 GEMV
+//   Q6_K float   dequantize_q6k (parser.rs:510-547) + F32 GEMV
 //
 // Mapping (wave-level, no LDS):
 //   * one wave owns R consecutive weight rows for one activation row;
@@ -409,6 +410,55 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_q4k_kernel(const uint8_t* _
     store_rows<R>(acc, lane, row0, n, yr);
 }
 
+// Q6_K float mode.  A unit is one 32-element column of a super-block (the
+// Q6KUnit layout); lane l owns units l, l+64, ...
+template <int R>
+__global__ __launch_bounds__(GEMV_THREADS) void gemv_q6k_kernel(const uint8_t* __restrict__ W,
+                                                                int n, int nsb,
+                                                                const FloatRec* __restrict__ X,
+                                                                float* __restrict__ Y) {
+    const int lane = threadIdx.x & 63;
+    const int wave = blockIdx.x * WAVES + (threadIdx.x >> 6);
+    const int row0 = wave * R;
+    if (row0 >= n) return;
+    const int nunits = nsb * 8;
+    const FloatRec* xr = X + (size_t)blockIdx.y * nunits;
+    float* yr = Y + (size_t)blockIdx.y * n;
+    const size_t row_bytes = (size_t)nsb * Q6_K_BYTES;
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
+    for (int u = lane; u < nunits; u += 64) {
+        const XF x = load_xf(xr + u);
+        int off[6];
+        q6k_offsets(x, off);
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const int row = min(row0 + r, n - 1);
+            // block offsets fit 32 bits: the launcher bounds the matrix below 2 GiB
+            const Q6KUnit g = q6k_unit((uint32_t)(row * row_bytes + (size_t)(u >> 3) * Q6_K_BYTES), u & 7);
+            uint32_t wl[9], wh[9];
+            const u32x4a4* pl = reinterpret_cast<const u32x4a4*>(W + (g.ql & ~3u));
+            const u32x4a4* ph = reinterpret_cast<const u32x4a4*>(W + (g.qh & ~3u));
+            const u32x4a4 l0 = pl[0], l1 = pl[1], h0 = ph[0], h1 = ph[1];
+            wl[0] = l0.x; wl[1] = l0.y; wl[2] = l0.z; wl[3] = l0.w;
+            wl[4] = l1.x; wl[5] = l1.y; wl[6] = l1.z; wl[7] = l1.w;
+            wh[0] = h0.x; wh[1] = h0.y; wh[2] = h0.z; wh[3] = h0.w;
+            wh[4] = h1.x; wh[5] = h1.y; wh[6] = h1.z; wh[7] = h1.w;
+            // the ninth dword stays inside the block (the runs end at or before byte 192)
+            wl[8] = *reinterpret_cast<const uint32_t*>(W + (g.ql & ~3u) + 32);
+            wh[8] = *reinterpret_cast<const uint32_t*>(W + (g.qh & ~3u) + 32);
+            uint32_t q[8];
+            q6k_codes(wl, wh, q6k_sel(g.ql), g.t, q);
+            const uint32_t scw = *reinterpret_cast<const uint16_t*>(W + g.sc);
+            const float d = h2f(*reinterpret_cast<const uint16_t*>(W + g.d));
+            const float f = q6k_dot(q, x, off, (int)(int8_t)(scw & 0xFF), (int)(int8_t)(scw >> 8));
+            acc[r] = fmaf(d * x.S, f, acc[r]);
+        }
+    }
+    store_rows<R>(acc, lane, row0, n, yr);
+}
+
 // int32 block partials of the native Q4_0 path, one thread per (row, block).
 __global__ __launch_bounds__(256) void q4_0_block_dots_kernel(const uint8_t* __restrict__ W,
                                                               int n, int nb,
@@ -426,10 +476,12 @@ __global__ __launch_bounds__(256) void q4_0_block_dots_kernel(const uint8_t* __r
     P[gid] = dot1(q, x, -8 * x.qsum);
 }
 
-// Tensor::to_f32 rows (tensor.rs:535-639) and dequantize_q4k (parser.rs:549-593):
-// one thread per 32 elements (for Q4_K, one of the eight sub-blocks of a
-// super-block).  Every product below is exact in f32 (f16 scale x 4- or
-// 6-bit integer), so each output has the reference's single rounding.
+// Tensor::to_f32 rows (tensor.rs:535-639), dequantize_q4k (parser.rs:549-593) and
+// dequantize_q6k (parser.rs:510-547): one thread per 32 elements (for Q4_K one
+// of the eight sub-blocks of a super-block, for Q6_K one of its eight columns).
+// Every product below is exact in f32 (f16 scale x 4- or 6-bit integer; for
+// Q6_K f16 x int8 x 6-bit code, at most 24 significant bits), so each output
+// has the reference's single rounding.
 template <int WT>
 __global__ __launch_bounds__(256) void dequant_rows_kernel(const uint8_t* __restrict__ W,
                                                            int nb, const int32_t* __restrict__ rows,
@@ -439,7 +491,19 @@ __global__ __launch_bounds__(256) void dequant_rows_kernel(const uint8_t* __rest
     const int r = (int)(gid / nb), b = (int)(gid % nb);
     const size_t g = (size_t)rows[r] * nb + b;
     float* o = out + gid * QK;
-    if (WT == (int)WType::Q4_K) {
+    if (WT == (int)WType::Q6_K) {
+        // column j of super-block g / 8 (parser.rs:525-541): (d * scale) * (code - 32)
+        const uint8_t* p = W + (g / 8) * Q6_K_BYTES;
+        const int j = (int)(g % 8), half = j >> 2, t = j & 3;
+        const float d = h2f(p[208] | (p[209] << 8));
+        const uint8_t* ql = p + 64 * half + 32 * (t & 1);
+        const uint8_t* qh = p + 128 + 32 * half;
+        const int8_t* sc = reinterpret_cast<const int8_t*>(p + 192 + 8 * half + 2 * t);
+        for (int l = 0; l < 32; l++) {
+            const int code = ((ql[l] >> (4 * (t >> 1))) & 0xF) | (((qh[l] >> (2 * t)) & 3) << 4);
+            o[l] = d * (float)sc[l >> 4] * (float)(code - 32);
+        }
+    } else if (WT == (int)WType::Q4_K) {
         // sub-block j of super-block g / 8: chunk c = j / 2 of the nibble bytes,
         // low nibbles for even j, high for odd (parser.rs:571-590)
         const uint8_t* p = W + (g / 8) * Q4_K_BYTES;
@@ -503,6 +567,12 @@ hipError_t launch_r(WType t, bool native, const uint8_t* w, size_t n, size_t k, 
                            (const FloatRec*)xrec, y);
         return hipGetLastError();
     }
+    if (t == WType::Q6_K) {
+        if ((uint64_t)n * (k / QK_K) * Q6_K_BYTES >= ((uint64_t)1 << 32)) return hipErrorInvalidValue;
+        launch_kernel((gemv_q6k_kernel<R>), grid, block, 0, s, w, ni, (int)(k / QK_K),
+                           (const FloatRec*)xrec, y);
+        return hipGetLastError();
+    }
     const int nb = (int)(k / QK);
     if (native && t == WType::Q4_0) {
         launch_kernel((gemv_native_kernel<R, (int)WType::Q4_0>), grid, block, 0, s, w, ni, nb,
@@ -554,6 +624,9 @@ hipError_t launch_dequant_rows(WType t, const uint8_t* w, size_t n, size_t k, co
     const int nb = (int)(k / QK);
     if (t == WType::Q4_K)
         hipLaunchKernelGGL((dequant_rows_kernel<(int)WType::Q4_K>), grid, dim3(256), 0, s, w, nb,
+                           rows, (int)n_rows, out);
+    else if (t == WType::Q6_K)
+        hipLaunchKernelGGL((dequant_rows_kernel<(int)WType::Q6_K>), grid, dim3(256), 0, s, w, nb,
                            rows, (int)n_rows, out);
     else if (t == WType::Q8_0)
         hipLaunchKernelGGL((dequant_rows_kernel<(int)WType::Q8_0>), grid, dim3(256), 0, s, w, nb,

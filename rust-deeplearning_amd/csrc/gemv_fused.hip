@@ -2,7 +2,8 @@
 // into the GEMV, y = W x for one activation row per blockIdx.y.
 //
 // Reference semantics are those of gemv.hip (matmul_f32_q8 / _q4 / _q4_native /
-// _q4_1 / _q4_1_native, quantize.rs:201-572; Q4_K parser.rs:549-593).
+// _q4_1 / _q4_1_native, quantize.rs:201-572; Q4_K parser.rs:549-593; Q6_K
+// parser.rs:510-547).
 //
 // Shape of a launch (MI355X: 256 CUs):
 //   * about one workgroup of NW = 16 waves per CU; workgroup g owns rows
@@ -979,6 +980,124 @@ __global__ __launch_bounds__(NW * 64) void gemv_q4k_splitk_kernel(const uint8_t*
     }
 }
 
+// ---- Q6_K (float mode) ------------------------------------------------------------------
+// A unit is one 32-element column of a super-block (Q6KUnit): K / 32 units a
+// row.  K is split over KS waves of the workgroup as in gemv_q4k_splitk_kernel:
+// wave w takes units ks * ups .. + ups - 1 (one per lane, ups <= 64) of R rows
+// of each row group (RG = NW / KS waves share a slice; a group is RG * R rows).
+// A workgroup converts x once and then walks the row groups blockIdx.x,
+// blockIdx.x + gridDim.x, ...: the loads of the next group's first rows are
+// issued while the current group's last rows are computed.  The KS slice sums
+// of a row are added in a fixed order through LDS (two buffers, one barrier a
+// group).
+constexpr int Q6K_AHEAD = 2;  // rows whose loads are in flight ahead of the arithmetic
+
+template <int R, int KS, int NW>
+__global__ __launch_bounds__(NW * 64) void gemv_q6k_splitk_kernel(const uint8_t* __restrict__ W, int n, int nsb,
+                                                                  int ups, const float* __restrict__ X,
+                                                                  float* __restrict__ Y) {
+    static_assert(NW % KS == 0, "slices per workgroup");
+    constexpr int RG = NW / KS;  // waves per slice
+    constexpr int RPW = RG * R;  // rows per group
+    extern __shared__ i32x4 lds4[];
+    const int lane = threadIdx.x & 63;
+    const int wv = threadIdx.x >> 6;
+    const int ks = wv % KS, rg = wv / KS;
+    const int ngroups = (n + RPW - 1) / RPW;
+    const int nb = nsb * 8;  // units = 32-element columns
+    const float* x = X + (size_t)blockIdx.y * nb * 32;
+    float* y = Y + (size_t)blockIdx.y * n;
+    const uint32_t row_bytes = (uint32_t)nsb * Q6_K_BYTES;
+    constexpr int PI = (KS * 8 + NW - 1) / NW;  // nb * 8 <= 512 * KS float4 pieces
+    f32x4 xv[PI];
+    load_prep_x<NW, PI>(x, nb, xv);
+
+    const int u = ks * ups + lane;
+    const bool uok = lane < ups && u < nb;
+    // eight loads a row: two nine-dword windows (ql, qh), the scale pair, d;
+    // empty slots read zeros through out-of-range offsets
+    u32x4 l0[R], l1[R], h0[R], h1[R];
+    uint32_t l2[R], h2[R], scw[R], dw[R];
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(W, (uint32_t)n * row_bytes);
+    auto block_of = [&](int grp, int r) {  // byte offset of the unit's super-block in row r of group grp
+        return (uint32_t)(grp * RPW + rg + r * RG) * row_bytes + (uint32_t)(u >> 3) * Q6_K_BYTES;
+    };
+    // slot r <- row r of group grp
+    auto issue = [&](int grp, int r) {
+        const int row = grp * RPW + rg + r * RG;
+        const bool live = row < n && grp < ngroups && uok;
+        const Q6KUnit g = q6k_unit(block_of(grp, r), u & 7);
+        const uint32_t bl = live ? (g.ql & ~3u) : RSRC_OOB, bh = live ? (g.qh & ~3u) : RSRC_OOB;
+        l0[r] = buf_load_b128(rs, bl);
+        l1[r] = buf_load_b128(rs, bl + 16);
+        l2[r] = buf_load_b32(rs, bl + 32);
+        h0[r] = buf_load_b128(rs, bh);
+        h1[r] = buf_load_b128(rs, bh + 16);
+        h2[r] = buf_load_b32(rs, bh + 32);
+        scw[r] = buf_load_b16(rs, live ? g.sc : RSRC_OOB);
+        dw[r] = buf_load_b16(rs, live ? g.d : RSRC_OOB);
+    };
+    constexpr int P0 = R < Q6K_AHEAD ? R : Q6K_AHEAD;
+    const int tcol = u & 3;  // column within the half
+    int grp = blockIdx.x;
+#pragma unroll
+    for (int r = 0; r < P0; r++) issue(grp, r);
+    wait_prep_x<P0 * 8>();  // eight weight loads per row
+    after_wait<PI>(xv);
+    prep_float_lds<NW, PI>(xv, nb, reinterpret_cast<int*>(lds4));
+    __syncthreads();
+
+    // the records are read once; the slice sums then go to LDS past them
+    RF xr{};
+    int off[6] = {0, 0, 0, 0, 0, 0};
+    if (uok) {
+        xr = read_rf(lds4, nb, u);
+        q6k_offsets(xr, off);
+    }
+    float* red = reinterpret_cast<float*>(lds4) + (size_t)nb * 32;  // [2][KS][RPW]
+    constexpr int SH = reduce_span_log2<R>();
+    for (int it = 0; grp < ngroups; grp += gridDim.x, it ^= 1) {
+        float acc[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) acc[r] = 0.0f;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            // keep P0 rows in flight, running into the next group (into slots
+            // already consumed: the next group's rows are issued after row r's
+            // arithmetic, since with P0 == R the slot is r's own)
+            if (r + P0 < R) issue(grp, r + P0);
+            __builtin_amdgcn_sched_barrier(0);
+            // row r's data enter the arithmetic here and not earlier
+            asm volatile("" : "+v"(l0[r]), "+v"(l1[r]), "+v"(l2[r]), "+v"(h0[r]), "+v"(h1[r]), "+v"(h2[r]),
+                         "+v"(scw[r]), "+v"(dw[r]));
+            if (uok) {
+                const uint32_t wl[9] = {l0[r].x, l0[r].y, l0[r].z, l0[r].w, l1[r].x, l1[r].y, l1[r].z, l1[r].w, l2[r]};
+                const uint32_t wh[9] = {h0[r].x, h0[r].y, h0[r].z, h0[r].w, h1[r].x, h1[r].y, h1[r].z, h1[r].w, h2[r]};
+                uint32_t q[8];
+                // the ql / qh runs share the block's dword alignment
+                q6k_codes(wl, wh, q6k_sel(block_of(grp, r)), tcol, q);
+                const int sc0 = (int)(int8_t)(scw[r] & 0xFFu), sc1 = (int)(int8_t)((scw[r] >> 8) & 0xFFu);
+                const float f = q6k_dot(q, xr, off, sc0, sc1);
+                acc[r] = fmaf(h2f(dw[r]) * xr.S, f, acc[r]);
+            }
+            if (r + P0 >= R) issue(grp + gridDim.x, r + P0 - R);
+            __builtin_amdgcn_sched_barrier(0);  // one row at a time, in load order
+        }
+        // rows of empty slots hold 0 (d reads as zero): no masking needed
+        const float sum = wave_reduce_rows<R>(acc);
+        float* rb = red + it * (KS * RPW);
+        if ((lane & ((1 << SH) - 1)) == 0) rb[ks * RPW + rg + (lane >> SH) * RG] = sum;
+        __syncthreads();  // (the other buffer was last read before this barrier)
+        const int r0 = grp * RPW;
+        for (int i = threadIdx.x; i < RPW; i += NW * 64) {
+            float t = rb[i];
+#pragma unroll
+            for (int k = 1; k < KS; k++) t += rb[k * RPW + i];
+            if (r0 + i < n) y[r0 + i] = t;
+        }
+    }
+}
+
 int g_num_cus = 0;
 
 }  // namespace
@@ -1110,6 +1229,37 @@ void launch_q4k_nw(const uint8_t* w, int n, int nsb, const float* x, size_t m, f
     }
 }
 
+// Q6_K: 16-wave workgroups, K split over KS = 1, 2, 4 or 8 waves (at most 64
+// units a wave), one workgroup per CU walking the row groups.
+template <int KS, int R>
+void launch_q6k_ks_r(const uint8_t* w, int n, int nsb, const float* x, size_t m, float* y, hipStream_t s,
+                     size_t lds) {
+    constexpr int NW = 16, RPW = NW / KS * R;
+    const int units = nsb * 8, ups = (units + KS - 1) / KS;
+    // one workgroup per CU, each walking its share of the row groups
+    const int groups = (n + RPW - 1) / RPW;
+    const int wgs = groups < num_cus() ? groups : num_cus();
+    const dim3 grid((unsigned)wgs, (unsigned)m), block(NW * 64);
+    lds += (size_t)2 * KS * RPW * sizeof(float);  // slice sums after the records
+    launch_kernel((gemv_q6k_splitk_kernel<R, KS, 16>), grid, block, lds, s, w, n, nsb, ups, x, y);
+}
+template <int KS>
+void launch_q6k_ks(const uint8_t* w, int n, int nsb, const float* x, size_t m, float* y, hipStream_t s,
+                   size_t lds) {
+    // R rows a wave a group: 4 when every CU gets at least one group of them
+    const long rg = 16 / KS;
+    if ((n + rg * 4 - 1) / (rg * 4) >= num_cus()) launch_q6k_ks_r<KS, 4>(w, n, nsb, x, m, y, s, lds);
+    else if ((n + rg * 2 - 1) / (rg * 2) >= num_cus()) launch_q6k_ks_r<KS, 2>(w, n, nsb, x, m, y, s, lds);
+    else launch_q6k_ks_r<KS, 1>(w, n, nsb, x, m, y, s, lds);
+}
+void launch_q6k(const uint8_t* w, int n, int nsb, const float* x, size_t m, float* y, hipStream_t s, size_t lds) {
+    const int units = nsb * 8;  // <= 512 (K <= 16384)
+    if (units <= 64) launch_q6k_ks<1>(w, n, nsb, x, m, y, s, lds);
+    else if (units <= 128) launch_q6k_ks<2>(w, n, nsb, x, m, y, s, lds);
+    else if (units <= 256) launch_q6k_ks<4>(w, n, nsb, x, m, y, s, lds);
+    else launch_q6k_ks<8>(w, n, nsb, x, m, y, s, lds);
+}
+
 // Decoder fusion: Q4_0 float mode, nb even.  8-wave workgroups, two per CU;
 // rows longer than 4096 (their x, re-read by every workgroup, is long): one
 // 16-wave workgroup per CU.
@@ -1219,6 +1369,11 @@ hipError_t launch_gemv_fused(WType t, bool native, const uint8_t* w, size_t n, s
     // one 16-wave workgroup per CU (Q4_0 4096 x 14336: 11.1 -> 9.6 us).
     const bool i4 = !native && (t == WType::Q4_0 || t == WType::Q4_1) && cpl_for(nb) < 8;
     const int nw = i4 ? 8 : 16, wg_per_cu = i4 ? 2 : 1;
+    if (t == WType::Q6_K) {
+        if (native) return hipErrorInvalidValue;
+        launch_q6k(w, ni, (int)(k / QK_K), x, m, y, s, lds);
+        return hipGetLastError();
+    }
     if (t == WType::Q4_K) {
         // up to 64 units per row (K <= 4096): rows spread over 8-wave
         // workgroups, two per CU; longer rows: one 16-wave workgroup per CU

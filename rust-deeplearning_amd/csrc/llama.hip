@@ -488,7 +488,9 @@ struct LlamaModel {
         uint8_t* dev = nullptr;
         int n = 0, k = 0;
         bool gemm_ok = true;
-        size_t bytes() const { return (size_t)n * (k / QK) * Q4_0_BYTES; }
+        WType type = WType::Q4_0;  // the output matrix may be another GGUF type
+        size_t row_bytes() const { return (size_t)(k / block_elems(type)) * block_bytes(type); }
+        size_t bytes() const { return (size_t)n * row_bytes(); }
     };
     struct Layer {
         Mat qkv, o, gu, down;
@@ -542,7 +544,7 @@ struct LlamaModel {
 
     // y[m, mat.n] = x[m, mat.k] . W^T on the model's stream
     hipError_t linear(const Mat& w, const float* xin, size_t m, float* y) {
-        if (m <= 4) return launch_gemv_fused(WType::Q4_0, false, w.dev, w.n, w.k, xin, m, y, stream);
+        if (m <= 4) return launch_gemv_fused(w.type, false, w.dev, w.n, w.k, xin, m, y, stream);
         if (w.gemm_ok) return launch_gemm_q4_0(w.dev, w.n, w.k, xin, m, y, gemm_scratch, stream);
         // rows one launch at a time through the fused GEMV (scales beyond the GEMM's range)
         for (size_t r = 0; r < m; r += 4) {
@@ -623,9 +625,14 @@ struct LlamaModel {
                                           1, stream);
             if (e != hipSuccess) return e;
         }
-        // logits = rms_norm(x_last, norm) . Wout^T
-        e = launch_gemv_q4_0_fused_ex(out.dev, out.n, d, x + (m - 1) * d, d, 1, logits, 1, final_norm, eps, 0,
-                                      stream);
+        // logits = rms_norm(x_last, norm) . Wout^T (the norm fused into the GEMV for Q4_0)
+        if (out.type == WType::Q4_0) {
+            e = launch_gemv_q4_0_fused_ex(out.dev, out.n, d, x + (m - 1) * d, d, 1, logits, 1, final_norm, eps, 0,
+                                          stream);
+        } else {
+            hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(NT), 0, stream, x + (m - 1) * d, final_norm, d, eps, xn);
+            e = launch_gemv_fused(out.type, false, out.dev, out.n, out.k, xn, 1, logits, stream);
+        }
         if (e != hipSuccess) return e;
         if (advance) hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(64), 0, stream, pos, (int)m);
         return hipGetLastError();
@@ -713,7 +720,7 @@ rdl_status slot_target(rdl::LlamaModel& M, int32_t slot, int32_t layer, SlotTarg
     if (per_layer && (layer < 0 || layer >= c.n_layers))
         return api_fail(RDL_ERR_INVALID_DATA, "layer %d out of range", layer);
     auto q4 = [&](rdl::LlamaModel::Mat& w, int row0, int rows, int interleave = 1) {
-        const size_t rb = M.row_q4(w.k);
+        const size_t rb = w.row_bytes();
         t->mat = &w;
         t->q4 = true;
         t->row_bytes = rb;
@@ -748,7 +755,7 @@ rdl_status slot_target(rdl::LlamaModel& M, int32_t slot, int32_t layer, SlotTarg
 rdl_status finish_slot(const SlotTarget& t) {
     if (t.mat) {
         bool ok = false;
-        HIP_TRY(rdl::gemm_scales_ok(rdl::WType::Q4_0, t.mat->dev, t.mat->n, t.mat->k, &ok));
+        HIP_TRY(rdl::gemm_scales_ok(t.mat->type, t.mat->dev, t.mat->n, t.mat->k, &ok));
         t.mat->gemm_ok = ok;
     }
     return api_ok();
@@ -767,9 +774,17 @@ rdl_status rdl_llama_create(const rdl_llama_config* cfg, rdl_llama** out) {
                         "head_dim even <= 256; n_heads %% n_kv_heads == 0)");
     rdl_status st = rdl::api_require_device();
     if (st != RDL_OK) return st;
+    const int32_t od = cfg->output_dtype == 0 ? RDL_DTYPE_Q4_0 : cfg->output_dtype;
+    if (od != RDL_DTYPE_Q4_0 && od != RDL_DTYPE_Q8_0 && od != RDL_DTYPE_Q4_1 && od != RDL_DTYPE_Q4_K &&
+        od != RDL_DTYPE_Q6_K)
+        return api_fail(RDL_ERR_UNSUPPORTED, "output matrix type %d (Q4_0, Q8_0, Q4_1, Q4_K or Q6_K)", od);
+    if ((od == RDL_DTYPE_Q4_K || od == RDL_DTYPE_Q6_K) && cfg->dim % rdl::QK_K != 0)
+        return api_fail(RDL_ERR_UNSUPPORTED, "K-quant output matrix needs dim %% 256 == 0 (dim %d)", cfg->dim);
     rdl_llama* h = new rdl_llama();
     rdl::LlamaModel& M = h->m;
     M.cfg = *cfg;
+    M.cfg.output_dtype = od;
+    M.out.type = (rdl::WType)od;
     const rdl_llama_config& c = M.cfg;
     M.q_dim = c.n_heads * c.head_dim;
     M.kv_dim = c.n_kv_heads * c.head_dim;
@@ -821,7 +836,7 @@ rdl_status rdl_llama_create(const rdl_llama_config* cfg, rdl_llama** out) {
     M.fusable = (c.dim / 32) % 2 == 0 && (M.q_dim / 32) % 2 == 0 && (c.ffn_dim / 32) % 2 == 0 &&
                 c.dim / 32 <= 256 &&
                 (uint64_t)2 * c.ffn_dim * (c.dim / 32) * rdl::Q4_0_BYTES <= rdl::FUSED_MAX_WEIGHT_BYTES &&
-                (uint64_t)c.vocab * (c.dim / 32) * rdl::Q4_0_BYTES <= rdl::FUSED_MAX_WEIGHT_BYTES;
+                (uint64_t)M.out.bytes() <= rdl::FUSED_MAX_WEIGHT_BYTES;
     M.att_nspan = (c.max_seq + rdl::ATT_SPAN - 1) / rdl::ATT_SPAN;
     if ((e = M.alloc_t(&M.att_part, mb * c.n_heads * (size_t)M.att_nspan * (c.head_dim + 2))) != hipSuccess)
         return fail_free(e);
@@ -870,6 +885,8 @@ rdl_status rdl_llama_init_random(rdl_llama* model, uint64_t seed) {
     if (!model) return api_fail(RDL_ERR_NULL_POINTER, "NULL model");
     rdl::LlamaModel& M = model->m;
     const rdl_llama_config& c = M.cfg;
+    if (M.out.type != rdl::WType::Q4_0)
+        return api_fail(RDL_ERR_UNSUPPORTED, "synthetic weights are Q4_0: output_dtype must be Q4_0");
     uint64_t tag = 0;
     auto fill_mat = [&](rdl::LlamaModel::Mat& w) {
         const size_t nblocks = (size_t)w.n * (w.k / rdl::QK);
@@ -1105,9 +1122,16 @@ void slot_dims(const rdl_llama_config& c, int slot, uint64_t d[2], uint32_t* nd)
 // Type and shape of one tensor against its slot.
 rdl_status check_tensor(const rdl_llama_config& c, int slot, const rdl_gguf_tensor_info& ti) {
     const bool norm = slot == RDL_LLAMA_ATTN_NORM || slot == RDL_LLAMA_FFN_NORM || slot == RDL_LLAMA_FINAL_NORM;
-    if (norm ? (ti.ggml_type != 0 && ti.ggml_type != 1) : ti.ggml_type != 2)
+    if (slot == RDL_LLAMA_OUTPUT) {
+        const int32_t t = ti.ggml_type;
+        if (t != RDL_DTYPE_Q4_0 && t != RDL_DTYPE_Q8_0 && t != RDL_DTYPE_Q4_1 && t != RDL_DTYPE_Q4_K &&
+            t != RDL_DTYPE_Q6_K)
+            return api_fail(RDL_ERR_UNSUPPORTED, "tensor '%s' is %s; the output matrix may be Q4_0, Q8_0, "
+                            "Q4_1, Q4_K or Q6_K", ti.name, ggml_name(t));
+    } else if (norm ? (ti.ggml_type != 0 && ti.ggml_type != 1) : ti.ggml_type != 2) {
         return api_fail(RDL_ERR_UNSUPPORTED, "tensor '%s' is %s; the decoder takes %s", ti.name,
                         ggml_name(ti.ggml_type), norm ? "F32 or F16 norm weights" : "Q4_0 matrices");
+    }
     uint64_t d[2];
     uint32_t nd = 0;
     slot_dims(c, slot, d, &nd);
@@ -1192,6 +1216,7 @@ rdl_status rdl_llama_load_gguf(const rdl_gguf* g, const rdl_llama_gguf_options* 
     c.rope_theta = gc.rope_theta;
     c.kv_f16 = opt ? opt->kv_f16 : 1;
     c.max_batch = (opt && opt->max_batch > 0) ? opt->max_batch : 32;
+    c.output_dtype = outw.ggml_type;
 
     // Type, shape and file bounds of every mapped tensor before allocating.
     const size_t nt = [&] { size_t n = 0; rdl_gguf_tensor_count(g, &n); return n; }();

@@ -166,5 +166,81 @@ __device__ __forceinline__ u32x4 buf_load_b128(__amdgpu_buffer_rsrc_t rs, uint32
 __device__ __forceinline__ uint32_t buf_load_b32(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
     return __builtin_amdgcn_raw_buffer_load_b32(rs, (int)off, 0, 0);
 }
+__device__ __forceinline__ uint32_t buf_load_b16(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, (int)off, 0, 0);
+}
+
+// ---- Q6_K units ---------------------------------------------------------------
+// A unit is one 32-element column of a 256-element Q6_K super-block: column
+// j = 4 * half + t holds elements 128 * half + 32 * t + l, l < 32.  Its codes
+// (dequantize_q6k, rustml/gguf/main/src/core/parser.rs:510-547): low four bits
+// from ql[64 * half + 32 * (t & 1) + l] (low nibble for t < 2, high for t >= 2),
+// high two bits from bits 2t, 2t + 1 of qh[32 * half + l]; element value
+// (d * scales[8 * half + 2t + l / 16]) * (code - 32), scales int8, d f16 at
+// byte 208.  Blocks are 210 bytes, so a block starts on a 2- or 4-byte
+// boundary; the 32-byte ql and qh runs are read as nine-dword windows from
+// the dword below them and realigned with v_perm_b32.
+struct Q6KUnit {
+    uint32_t ql, qh;  // first byte of the unit's ql / qh run
+    uint32_t sc;      // its two scales (l < 16, l >= 16)
+    uint32_t d;       // the block's f16 scale
+    int t;            // column within the half
+};
+__device__ __forceinline__ Q6KUnit q6k_unit(uint32_t block, int j) {
+    const uint32_t half = (uint32_t)j >> 2, t = (uint32_t)j & 3;
+    return {block + 64 * half + 32 * (t & 1), block + 128 + 32 * half, block + 192 + 8 * half + 2 * t,
+            block + 208, (int)t};
+}
+// v_perm selector taking the 4 bytes that start at run & 3 (0 or 2) in {w[k+1]:w[k]}
+__device__ __forceinline__ uint32_t q6k_sel(uint32_t run) { return (run & 2) ? 0x05040302u : 0x03020100u; }
+
+// The 32 codes (0..63) of a unit as 8 dwords of bytes (dword k: elements 4k..4k+3).
+__device__ __forceinline__ void q6k_codes(const uint32_t (&wl)[9], const uint32_t (&wh)[9], uint32_t sel, int t,
+                                          uint32_t (&q)[8]) {
+    const uint32_t nsh = 4 * (uint32_t)(t >> 1), hsh = 2 * (uint32_t)t;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const uint32_t lo = perm(wl[k + 1], wl[k], sel), hi = perm(wh[k + 1], wh[k], sel);
+        q[k] = ((lo >> nsh) & 0x0F0F0F0Fu) | (((hi >> hsh) & 0x03030303u) << 4);
+    }
+}
+
+// Starting values of the unit's six digit sums: -32 * (sum of the a / b / c
+// digits over elements 0..15 and 16..31), so that the dots below give
+// sum (code - 32) * digit exactly.  X: a float-mode record view (a0, a1 =
+// a digits of elements 0..15 / 16..31, likewise b, c; sa, sb, sc = sums over
+// all 32).
+template <class X>
+__device__ __forceinline__ void q6k_offsets(const X& x, int (&off)[6]) {
+    constexpr int ONE4 = 0x01010101;
+    auto half_sum = [](const i32x4& v) {
+        return dot4(ONE4, v.x, dot4(ONE4, v.y, dot4(ONE4, v.z, dot4(ONE4, v.w, 0))));
+    };
+    const int a = half_sum(x.a0), b = half_sum(x.b0), c = half_sum(x.c0);
+    off[0] = -32 * a;
+    off[1] = -32 * (x.sa - a);
+    off[2] = -32 * b;
+    off[3] = -32 * (x.sb - b);
+    off[4] = -32 * c;
+    off[5] = -32 * (x.sc - c);
+}
+
+// sum over the unit of scale * (code - 32) * x_digits, combined as
+// A + (B + C / 256) / 256 (exact in int32 up to the final conversion);
+// sc0 / sc1: the scales of elements 0..15 / 16..31.
+template <class X>
+__device__ __forceinline__ float q6k_dot(const uint32_t (&q)[8], const X& x, const int (&off)[6], int sc0,
+                                         int sc1) {
+    int A0 = off[0], A1 = off[1], B0 = off[2], B1 = off[3], C0 = off[4], C1 = off[5];
+    A0 = dot4(q[0], x.a0.x, A0); A0 = dot4(q[1], x.a0.y, A0); A0 = dot4(q[2], x.a0.z, A0); A0 = dot4(q[3], x.a0.w, A0);
+    A1 = dot4(q[4], x.a1.x, A1); A1 = dot4(q[5], x.a1.y, A1); A1 = dot4(q[6], x.a1.z, A1); A1 = dot4(q[7], x.a1.w, A1);
+    B0 = dot4(q[0], x.b0.x, B0); B0 = dot4(q[1], x.b0.y, B0); B0 = dot4(q[2], x.b0.z, B0); B0 = dot4(q[3], x.b0.w, B0);
+    B1 = dot4(q[4], x.b1.x, B1); B1 = dot4(q[5], x.b1.y, B1); B1 = dot4(q[6], x.b1.z, B1); B1 = dot4(q[7], x.b1.w, B1);
+    C0 = dot4(q[0], x.c0.x, C0); C0 = dot4(q[1], x.c0.y, C0); C0 = dot4(q[2], x.c0.z, C0); C0 = dot4(q[3], x.c0.w, C0);
+    C1 = dot4(q[4], x.c1.x, C1); C1 = dot4(q[5], x.c1.y, C1); C1 = dot4(q[6], x.c1.z, C1); C1 = dot4(q[7], x.c1.w, C1);
+    // |A0|, |A1| <= 16 * 63 * 128 + 32 * 16 * 128 < 2^18, |scale| <= 128: no int32 overflow
+    const int IA = sc0 * A0 + sc1 * A1, IB = sc0 * B0 + sc1 * B1, IC = sc0 * C0 + sc1 * C1;
+    return fmaf(fmaf((float)IC, 1.0f / 256.0f, (float)IB), 1.0f / 256.0f, (float)IA);
+}
 
 }  // namespace rdl

@@ -31,8 +31,9 @@ constexpr int QK = 32;          // elements per Q4_0 / Q4_1 / Q8_0 block
 constexpr int Q4_0_BYTES = 18;  // [f16 d][16 B nibbles]
 constexpr int Q4_1_BYTES = 20;  // [f16 d][f16 m][16 B nibbles]
 constexpr int Q8_0_BYTES = 34;  // [f16 d][32 x i8]
-constexpr int QK_K = 256;       // elements per Q4_K super-block
+constexpr int QK_K = 256;       // elements per Q4_K / Q6_K super-block
 constexpr int Q4_K_BYTES = 144; // [f16 d][f16 dmin][12 B scales][128 B nibbles]
+constexpr int Q6_K_BYTES = 210; // [128 B ql][64 B qh][16 x i8 scales][f16 d]
 
 // ---------------------------------------------------------------------------
 // Prepared activations.
@@ -73,15 +74,16 @@ struct alignas(16) NativeRec {
 };
 static_assert(sizeof(NativeRec) == 48, "NativeRec layout");
 
-enum class WType : int { Q4_0 = 2, Q4_1 = 3, Q8_0 = 8, Q4_K = 12 };
+enum class WType : int { Q4_0 = 2, Q4_1 = 3, Q8_0 = 8, Q4_K = 12, Q6_K = 14 };
 
-inline size_t block_elems(WType t) { return t == WType::Q4_K ? QK_K : QK; }
+inline size_t block_elems(WType t) { return (t == WType::Q4_K || t == WType::Q6_K) ? QK_K : QK; }
 inline size_t block_bytes(WType t) {
     switch (t) {
         case WType::Q4_0: return Q4_0_BYTES;
         case WType::Q4_1: return Q4_1_BYTES;
         case WType::Q8_0: return Q8_0_BYTES;
         case WType::Q4_K: return Q4_K_BYTES;
+        case WType::Q6_K: return Q6_K_BYTES;
     }
     return 0;
 }

@@ -64,11 +64,13 @@ DTYPE_Q4_0 = 2
 DTYPE_Q4_1 = 3
 DTYPE_Q8_0 = 8
 DTYPE_Q4_K = 12
+DTYPE_Q6_K = 14
 
 MODE_FLOAT = 0
 MODE_NATIVE = 1
 
-BLOCK = {DTYPE_Q4_0: (32, 18), DTYPE_Q4_1: (32, 20), DTYPE_Q8_0: (32, 34), DTYPE_Q4_K: (256, 144)}
+BLOCK = {DTYPE_Q4_0: (32, 18), DTYPE_Q4_1: (32, 20), DTYPE_Q8_0: (32, 34), DTYPE_Q4_K: (256, 144),
+         DTYPE_Q6_K: (256, 210)}
 
 _sz = C.c_size_t
 _p = C.c_void_p
@@ -90,7 +92,7 @@ _decl("rdl_last_error", C.c_char_p)
 _decl("rdl_version", C.c_char_p)
 _decl("rdl_device_count", _i32)
 _decl("rdl_time_next_launch", _i32, _p, _p)
-for _n in ("q8", "q4", "q4_native", "q4_1", "q4_1_native", "q4_k"):
+for _n in ("q8", "q4", "q4_native", "q4_1", "q4_1_native", "q4_k", "q6_k"):
     _decl(f"rdl_matmul_f32_{_n}", _i32, _fp, _sz, _u8p, _sz, _sz, _sz, _sz, _fp, _sz)
 _decl("rdl_quantize_row_q8_0", _i32, _fp, _sz, _u8p, _sz, _fp, _sz)
 _decl("rdl_q4_0_q8_0_block_dots", _i32, _fp, _sz, _u8p, _sz, _sz, _sz, _sz, _i32p, _sz)
@@ -216,6 +218,13 @@ def matmul_f32_q4_1_native(input_data, weight_bytes, m, in_features, out_feature
 def matmul_f32_q4_k(input_data, weight_bytes, m, in_features, out_features):
     """Extension: the reference's dequantize_q4k + F32 Linear, from resident super-blocks."""
     return _matmul(lib.rdl_matmul_f32_q4_k, input_data, weight_bytes, m, in_features, out_features)
+
+
+def matmul_f32_q6_k(input_data, weight_bytes, m, in_features, out_features):
+    """Q6_K product straight from the 210-byte super-blocks (the reference
+    dequantizes them at load, rustml/gguf/main/src/core/parser.rs:510-547,
+    and runs the F32 Linear)."""
+    return _matmul(lib.rdl_matmul_f32_q6_k, input_data, weight_bytes, m, in_features, out_features)
 
 
 def quantize_row_q8_0(input_data):

@@ -9,7 +9,7 @@ of 32 after the tensor infos (the alignment GGUFFile::parse_bytes assumes,
 rustml/gguf/main/src/core/parser.rs:202), and `write` streams the file
 tensor by tensor, so a multi-GB model never sits in memory whole.
 
-write_llama_gguf lays out a Llama-architecture file with the tensor names of
+llama_builder lays out a Llama-architecture file with the tensor names of
 gguf_llama_weight_map (rustml/gguf/main/src/core/weight_map.rs:26-73) and the
 metadata keys GGUFFile::to_model_config reads (parser.rs:214-289).
 
@@ -185,7 +185,8 @@ LLAMA_LAYER_TENSORS = ("attn_norm", "attn_q", "attn_k", "attn_v", "attn_output",
 
 def llama_tensor_shapes(cfg):
     """GGUF name -> (dims innermost first, ggml type) for a Q4_0 Llama model of
-    `cfg` (rdlquant.llama.LlamaConfig fields), in llama.cpp's file order."""
+    `cfg` (rdlquant.llama.LlamaConfig fields; the output matrix in
+    cfg.output_dtype), in llama.cpp's file order."""
     d, q, kv, f, v = cfg.dim, cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim, cfg.ffn_dim, cfg.vocab
     out = {"token_embd.weight": ([d, v], GGML_Q4_0)}
     for i in range(cfg.n_layers):
@@ -200,7 +201,7 @@ def llama_tensor_shapes(cfg):
         out[p + "ffn_up.weight"] = ([d, f], GGML_Q4_0)
         out[p + "ffn_down.weight"] = ([f, d], GGML_Q4_0)
     out["output_norm.weight"] = ([d], GGML_F32)
-    out["output.weight"] = ([d, v], GGML_Q4_0)
+    out["output.weight"] = ([d, v], getattr(cfg, "output_dtype", GGML_Q4_0) or GGML_Q4_0)
     return out
 
 

@@ -23,7 +23,7 @@ class _Config(C.Structure):
     _fields_ = [(n, C.c_int32) for n in ("dim", "n_layers", "n_heads", "n_kv_heads", "head_dim", "ffn_dim",
                                            "vocab", "max_seq")] + \
                [("norm_eps", C.c_float), ("rope_theta", C.c_float), ("kv_f16", C.c_int32),
-                ("max_batch", C.c_int32)]
+                ("max_batch", C.c_int32), ("output_dtype", C.c_int32)]
 
 
 _decl("rdl_llama_create", _i32, C.POINTER(_Config), C.POINTER(_p))
@@ -61,11 +61,12 @@ class LlamaConfig:
     rope_theta: float = 10000.0
     kv_f16: bool = True
     max_batch: int = 128
+    output_dtype: int = 2  # GGML type of the output matrix (Q4_0; also Q8_0, Q4_1, Q4_K, Q6_K)
 
     def _c(self):
         return _Config(self.dim, self.n_layers, self.n_heads, self.n_kv_heads, self.head_dim, self.ffn_dim,
                        self.vocab, self.max_seq, self.norm_eps, self.rope_theta, int(self.kv_f16),
-                       self.max_batch)
+                       self.max_batch, self.output_dtype)
 
 
 def _i32_array(tokens):
@@ -104,7 +105,7 @@ class LlamaModel:
         self._h = h
         self.config = LlamaConfig(c.dim, c.n_layers, c.n_heads, c.n_kv_heads, c.head_dim, c.ffn_dim, c.vocab,
                                   c.max_seq, float(c.norm_eps), float(c.rope_theta), bool(c.kv_f16),
-                                  c.max_batch)
+                                  c.max_batch, c.output_dtype)
         return self
 
     def close(self):
@@ -116,7 +117,8 @@ class LlamaModel:
         self.close()
 
     def set_weight(self, slot: int, layer: int, data: np.ndarray) -> None:
-        """Q4_0 GGUF bytes (uint8) for matrices and the embedding, f32 for norms."""
+        """GGUF block bytes (uint8) for matrices and the embedding (Q4_0; the
+        output matrix in config.output_dtype), f32 for norms."""
         a = np.ascontiguousarray(data)
         check(lib.rdl_llama_set_weight(self._h, slot, layer, a.ctypes.data, a.nbytes))
 

@@ -102,6 +102,41 @@ def q4_k_weights(n, k, seed, d_sigma=0.01):
     return out.reshape(-1)
 
 
+def pack_q6_k(codes, scales, d_bits) -> np.ndarray:
+    """Q6_K super-blocks from codes [..., 256] in 0..63 (value = code - 32),
+    int8 scales [..., 16] and f16 bit patterns d [...]: the inverse of the
+    unpack in dequantize_q6k (rustml/gguf/main/src/core/parser.rs:510-547).
+    Element 128*h + 32*t + l: low nibble in ql[64*h + 32*(t&1) + l] (low
+    half for t < 2, high half for t >= 2), high bit pair at bits 2t, 2t+1 of
+    qh[32*h + l]."""
+    c = np.asarray(codes, dtype=np.uint8)
+    lead = c.shape[:-1]
+    c = c.reshape(lead + (2, 4, 32))  # [half][t][l]
+    lo = c & 0x0F
+    ql = np.empty(lead + (2, 2, 32), dtype=np.uint8)  # [half][t & 1][l]
+    ql[..., 0, :] = lo[..., 0, :] | (lo[..., 2, :] << 4)
+    ql[..., 1, :] = lo[..., 1, :] | (lo[..., 3, :] << 4)
+    hb = (c >> 4) & 3
+    qh = hb[..., 0, :] | (hb[..., 1, :] << 2) | (hb[..., 2, :] << 4) | (hb[..., 3, :] << 6)  # [half][l]
+    out = np.empty(lead + (210,), dtype=np.uint8)
+    out[..., 0:128] = ql.reshape(lead + (128,))
+    out[..., 128:192] = qh.reshape(lead + (64,))
+    out[..., 192:208] = np.asarray(scales, dtype=np.int8).view(np.uint8)
+    out[..., 208:210] = np.asarray(d_bits, dtype=np.uint16)[..., None].view(np.uint8).reshape(lead + (2,))
+    return out
+
+
+def q6_k_weights(n, k, seed, d_sigma=0.002):
+    """Q6_K: codes ~ U{0..63}, scales ~ U{-128..127}, d = f16(|N(0, d_sigma)|); 210 B super-blocks."""
+    r = _rng(seed)
+    ns = k // 256
+    codes = r.integers(0, 64, size=(n, ns, 256), dtype=np.uint8)
+    scales = r.integers(-128, 128, size=(n, ns, 16), dtype=np.int16).astype(np.int8)
+    d = f16_bits(np.abs(r.normal(0.0, d_sigma, size=(n, ns))))
+    return pack_q6_k(codes, scales, d).reshape(-1)
+
+
 def weights(dtype, n, k, seed):
-    """Weights of GGML type id `dtype` (2 = Q4_0, 3 = Q4_1, 8 = Q8_0, 12 = Q4_K)."""
-    return {2: q4_0_weights, 3: q4_1_weights, 8: q8_0_weights, 12: q4_k_weights}[dtype](n, k, seed)
+    """Weights of GGML type id `dtype` (2 = Q4_0, 3 = Q4_1, 8 = Q8_0, 12 = Q4_K, 14 = Q6_K)."""
+    return {2: q4_0_weights, 3: q4_1_weights, 8: q8_0_weights, 12: q4_k_weights,
+            14: q6_k_weights}[dtype](n, k, seed)

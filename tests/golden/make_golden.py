@@ -6,7 +6,7 @@ cannot be built or run here, so the expected outputs come from the oracle,
 which tests/test_golden.py pins independently (f64 brute force over the
 dequantized weights, exact integer dots, closed forms of quantize_row_q8_0).
 
-Run from the repository root:  python tests/golden/make_golden.py
+Run from the repository root:  python tests/golden/make_golden.py [linear case ...]
 """
 import os
 import sys
@@ -30,6 +30,7 @@ LINEAR_CASES = {
     "q4_0": (2, 4, 256, 2, "q4", "q4_native"),
     "q4_1": (3, 4, 256, 2, "q4_1", "q4_1_native"),
     "q4_k": (12, 2, 512, 2, "q4k", None),
+    "q6_k": (14, 3, 768, 2, "q6k", None),
 }
 
 
@@ -44,7 +45,7 @@ def linear_fixture(name):
         out["y_native"] = orc.matmul(nk, x, w, m, k, n).reshape(m, n)
     if dtype == 2:
         out["partials"] = orc.block_dots(x, w, m, k, n)
-    kind = {8: "q8_0", 2: "q4_0", 3: "q4_1", 12: "q4k"}[dtype]
+    kind = {8: "q8_0", 2: "q4_0", 3: "q4_1", 12: "q4k", 14: "q6k"}[dtype]
     out["w_f32"] = orc.to_f32(kind, w, n * k).reshape(n, k)
     return out
 
@@ -67,9 +68,11 @@ def quantize_row_input():
     return b.reshape(-1)
 
 
-def main():
-    for name in LINEAR_CASES:
+def main(names=None):
+    for name in names or LINEAR_CASES:
         np.savez_compressed(os.path.join(HERE, f"linear_{name}.npz"), **linear_fixture(name))
+    if names:
+        return
     x = quantize_row_input()
     q, s = orc.quantize_row_q8_0(x)
     np.savez_compressed(os.path.join(HERE, "quantize_row_q8_0.npz"), x=x, q=q, scales=s)
@@ -82,4 +85,4 @@ def main():
 
 
 if __name__ == "__main__":
-    main()
+    main(sys.argv[1:] or None)

@@ -41,9 +41,12 @@ def tiny_weights(cfg, seed=1234):
                                 (L.W_DOWN, "w_down", q4(cfg.dim, cfg.ffn_dim))):
             slots.append((slot, layer, arr))
             ref[(name, layer)] = arr
-    fin, out = norm(), q4(cfg.vocab, cfg.dim)
+    s += 1
+    out = synth.weights(cfg.output_dtype, cfg.vocab, cfg.dim, s)
+    fin = norm()
     slots += [(L.FINAL_NORM, 0, fin), (L.OUTPUT, 0, out)]
     ref["final_norm"], ref["output"] = fin, out
+    ref["output_kind"] = {2: "q4", 3: "q4_1", 8: "q8", 12: "q4k", 14: "q6k"}[cfg.output_dtype]
     return slots, ref
 
 

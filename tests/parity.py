@@ -19,12 +19,12 @@ def assert_close(got, want, rtol=RTOL, atol=ATOL, slack=0.0):
         f"got {got[bad[0]]} want {want[bad[0]]}")
 
 
-DEQ = {"q8": "q8_0", "q4": "q4_0", "q4_1": "q4_1", "q4k": "q4k"}
+DEQ = {"q8": "q8_0", "q4": "q4_0", "q4_1": "q4_1", "q4k": "q4k", "q6k": "q6k"}
 
 
 def exact_f64(orc, kind, x, w, m, k, n):
     """The reference's float-path product evaluated exactly (f64) over its own
-    f32 dequantized weights (Tensor::to_f32 / dequantize_q4k)."""
+    f32 dequantized weights (Tensor::to_f32 / dequantize_q4k / dequantize_q6k)."""
     wd = orc.to_f32(DEQ[kind], w, n * k).reshape(n, k).astype(np.float64)
     return (np.asarray(x, np.float64).reshape(m, k) @ wd.T).reshape(-1)
 

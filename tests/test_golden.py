@@ -11,7 +11,7 @@ from parity import ATOL, RTOL
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 LINEAR = {"q8_0": ("q8", None), "q4_0": ("q4", "q4_native"), "q4_1": ("q4_1", "q4_1_native"),
-          "q4_k": ("q4k", None)}
+          "q4_k": ("q4k", None), "q6_k": ("q6k", None)}
 
 
 def load(name):
@@ -26,7 +26,7 @@ def test_oracle_reproduces_linear_fixture(orc, name):
     assert np.array_equal(orc.matmul(fk, d["x"], d["w"], m, k, n).reshape(m, n), d["y_float"])
     if nk:
         assert np.array_equal(orc.matmul(nk, d["x"], d["w"], m, k, n).reshape(m, n), d["y_native"])
-    kind = {"q4_k": "q4k"}.get(name, name)
+    kind = {"q4_k": "q4k", "q6_k": "q6k"}.get(name, name)
     assert np.array_equal(orc.to_f32(kind, d["w"], n * k).reshape(n, k), d["w_f32"])
 
 

@@ -7,8 +7,8 @@ from rdlquant import synth
 pytestmark = pytest.mark.gpu
 
 RTOL, ATOL = 1e-3, 1e-4
-KIND = {2: "q4", 3: "q4_1", 8: "q8", 12: "q4k"}
-DEQ = {2: "q4_0", 3: "q4_1", 8: "q8_0", 12: "q4k"}
+KIND = {2: "q4", 3: "q4_1", 8: "q8", 12: "q4k", 14: "q6k"}
+DEQ = {2: "q4_0", 3: "q4_1", 8: "q8_0", 12: "q4k", 14: "q6k"}
 
 
 def close(got, want, exact):
@@ -23,7 +23,8 @@ def dev_weight(rq, torch, w, dtype, n, k):
 
 
 @pytest.mark.parametrize("dtype,n,k", [(2, 11008, 4096), (8, 4096, 4096), (12, 4096, 14336),
-                                       (2, 4096, 14336), (3, 100, 512), (2, 7, 20480)])
+                                       (2, 4096, 14336), (3, 100, 512), (2, 7, 20480),
+                                       (14, 32000, 4096), (14, 4096, 14336), (14, 9, 1280)])
 @pytest.mark.parametrize("m", [1, 2])
 def test_prepared_records_path(rq, orc, gpu, dtype, n, k, m):
     import torch
@@ -69,7 +70,7 @@ def test_prepared_native_bit_equal_to_fused(rq, gpu):
     assert np.all(np.abs(a - b) <= 1e-5 + 1e-5 * np.abs(a))
 
 
-@pytest.mark.parametrize("dtype,kind", [(2, "q4_0"), (8, "q8_0"), (3, "q4_1"), (12, "q4k")])
+@pytest.mark.parametrize("dtype,kind", [(2, "q4_0"), (8, "q8_0"), (3, "q4_1"), (12, "q4k"), (14, "q6k")])
 def test_dequantize_rows_exact(rq, orc, gpu, dtype, kind):
     import torch
 

@@ -162,3 +162,17 @@ def test_7b_layer_shapes_staged_in_chunks(rq, gpu, tmp_path):
     want = run(from_slots(cfg, slots), prompt, 8)
     assert np.array_equal(got[0], want[0])
     assert np.array_equal(got[1], want[1])
+
+
+def test_q6_k_output_from_gguf(rq, gpu, tmp_path):
+    """A file with a Q6_K output.weight (as llama.cpp writes Q4_0 models)."""
+    from rdlquant.llama import LlamaModel
+    cfg = tiny_config(output_dtype=14)
+    slots, _ = tiny_weights(cfg, seed=81)
+    p = tmp_path / "q6k_out.gguf"
+    write_gguf(p, cfg, slots)
+    m = LlamaModel.from_gguf(str(p), max_batch=cfg.max_batch, kv_f16=False)
+    assert m.config.output_dtype == 14
+    prompt = [4, 40, 44, 144]
+    got, want = run(m, prompt, 7), run(from_slots(cfg, slots), prompt, 7)
+    assert np.array_equal(got[0], want[0]) and np.array_equal(got[1], want[1])

@@ -22,6 +22,7 @@ def load(name):
     ("q4_0", "matmul_f32_q4", "matmul_f32_q4_native"),
     ("q4_1", "matmul_f32_q4_1", "matmul_f32_q4_1_native"),
     ("q4_k", "matmul_f32_q4_k", None),
+    ("q6_k", "matmul_f32_q6_k", None),
 ])
 def test_linear_fixture(rq, gpu, name, fn, native_fn):
     d = load(f"linear_{name}.npz")
@@ -46,7 +47,7 @@ def test_quantize_row_fixture(rq, gpu):
     assert np.array_equal(s, d["scales"])
 
 
-@pytest.mark.parametrize("name,dtype", [("q8_0", 8), ("q4_0", 2), ("q4_1", 3), ("q4_k", 12)])
+@pytest.mark.parametrize("name,dtype", [("q8_0", 8), ("q4_0", 2), ("q4_1", 3), ("q4_k", 12), ("q6_k", 14)])
 def test_dequantized_rows_fixture(rq, gpu, name, dtype):
     import torch
     d = load(f"linear_{name}.npz")

@@ -173,3 +173,30 @@ def test_long_context_spans(rq, gpu, kw):
         logits = ref.forward_with_cache([want_toks[-1]])
     if not f16:
         assert gen.tolist() == want_toks
+
+
+@pytest.mark.parametrize("out_dtype", [14, 8, 12])
+def test_output_matrix_types(rq, gpu, out_dtype):
+    """An output matrix in Q6_K / Q8_0 / Q4_K (llama.cpp files keep lm_head in
+    Q6_K): prefill, fused decode steps and greedy generation against the
+    oracle's forward (the reference dequantizes K-quants at load and runs the
+    F32 Linear)."""
+    cfg = tiny_config(output_dtype=out_dtype)
+    m, ref = build(cfg, seed=4321)
+    prompt = [9, 8, 7, 6, 5, 4, 3, 2, 1]
+    assert_close(m.forward_with_cache(prompt), ref.forward_with_cache(prompt))
+    tok = 12
+    for _ in range(4):
+        got = m.decode_step(tok)
+        want = ref.forward_with_cache([tok])
+        assert_close(got, want)
+        tok = argmax(want)
+    m.reset()
+    toks = m.generate_greedy(prompt, 6)
+    m.reset()
+    eager = [argmax(m.forward_with_cache(prompt))]
+    for _ in range(5):
+        eager.append(argmax(m.forward_with_cache([eager[-1]])))
+    assert list(toks) == eager
+    with pytest.raises(rq.DeviceError):
+        m.init_random(1)

@@ -81,6 +81,21 @@ def test_gemv_q4k_ragged(rq, orc, gpu, m, n, k):
                  exact_f64(orc, "q4k", x, w, m, k, n))
 
 
+# Q6_K (dequantize_q6k + F32 Linear in the reference): K split over 1 (K <= 2048),
+# 2, 4 or 8 waves of 64 columns; odd super-block counts (K = 768, 1280, 4352,
+# 8448) put every other row on a 2-byte boundary; ragged last slices; the
+# lm_head shape; m > 4 takes the records kernel.
+@pytest.mark.parametrize("m,n,k", [(1, 1, 256), (2, 5, 768), (1, 33, 1280), (3, 8, 14336),
+                                   (1, 1000, 2048), (4, 300, 4096), (1, 32000, 4096), (1, 37, 4352),
+                                   (2, 100, 8192), (1, 77, 8448), (1, 130, 16384), (5, 40, 4096),
+                                   (9, 70, 768), (6, 3, 16640)])
+def test_gemv_q6k_ragged(rq, orc, gpu, m, n, k):
+    x = synth.activations(m, k, 13 + n)
+    w = synth.q6_k_weights(n, k, 17 + k)
+    check_parity(rq.matmul_f32_q6_k(x, w, m, k, n), orc.matmul("q6k", x, w, m, k, n, threads=8),
+                 exact_f64(orc, "q6k", x, w, m, k, n))
+
+
 # ---- native mode: int32 partials bit-exact, outputs within tolerance --------------------
 def test_native_block_dots_bit_exact(rq, orc, gpu):
     m, n, k = 2, 64, 512

@@ -1,5 +1,5 @@
 """Pins the oracle's matmuls and dequantizers (rustml/quant/main/src/core/quantize.rs,
-rustml/core/main/src/core/tensor/tensor.rs:535-639, rustml/gguf/main/src/core/parser.rs:549-593)."""
+rustml/core/main/src/core/tensor/tensor.rs:535-639, rustml/gguf/main/src/core/parser.rs:510-593)."""
 import numpy as np
 import pytest
 
@@ -123,6 +123,55 @@ def test_q4k_matmul_vs_f64(orc):
     w = synth.q4_k_weights(n, k, 32)
     y = orc.matmul("q4k", x, w, m, k, n, threads=2).reshape(m, n)
     wd = orc.to_f32("q4k", w, n * k)
+    want = f64_gemm(x, wd, m, k, n)
+    bound = 2.0 ** -13 * (np.abs(x.reshape(m, k)) @ np.abs(wd.reshape(n, k)).T) + 1e-9
+    assert np.all(np.abs(y - want) <= bound)
+
+
+def test_q6k_known_block(orc):
+    """A block worked by hand from parser.rs:525-541: ql bytes 0x21 (low nibble
+    1, high 2), qh bytes 0xE4 (bit pairs 0, 1, 2, 3 for t = 0..3), scales
+    1..16, d = 0.5.  Element 128h + 32t + l has code (1 or 2) + 16t and scale
+    index 8h + 2t + l // 16."""
+    blk = np.zeros(210, np.uint8)
+    blk[0:128] = 0x21
+    blk[128:192] = 0xE4
+    blk[192:208] = np.arange(1, 17, dtype=np.int8).view(np.uint8)
+    blk[208:210] = np.array([0.5], np.float16).view(np.uint8)
+    out = orc.to_f32("q6k", blk, 256)
+    want = np.empty(256, np.float32)
+    for h in range(2):
+        for t in range(4):
+            code = (1 if t < 2 else 2) + 16 * t
+            for l in range(32):
+                want[128 * h + 32 * t + l] = 0.5 * (8 * h + 2 * t + l // 16 + 1) * (code - 32)
+    assert np.array_equal(out, want)
+
+
+def test_q6k_pack_roundtrip_and_signed_scales(orc):
+    """synth.pack_q6_k inverts the unpack: every code, negative scales, and
+    (d * scale) * (code - 32) exact in f32."""
+    rng = np.random.default_rng(10)
+    n, k = 3, 768
+    ns = k // 256
+    codes = rng.integers(0, 64, size=(n, ns, 256), dtype=np.uint8)
+    codes[0, 0] = np.arange(256) % 64  # every code in every position class
+    scales = rng.integers(-128, 128, size=(n, ns, 16), dtype=np.int16).astype(np.int8)
+    d = synth.f16_bits(np.abs(rng.normal(0, 0.01, size=(n, ns))))
+    blob = synth.pack_q6_k(codes, scales, d)
+    out = orc.to_f32("q6k", blob.reshape(-1), n * k).reshape(n, ns, 256)
+    df = d.view(np.float16).astype(np.float32)[..., None]
+    sc = np.repeat(scales.astype(np.float32), 16, axis=-1)  # element e -> scale e // 16
+    want = (df * sc) * (codes.astype(np.float32) - 32)
+    assert np.array_equal(out, want.astype(np.float32))
+
+
+def test_q6k_matmul_vs_f64(orc):
+    m, k, n = 2, 1024, 24
+    x = synth.activations(m, k, 33)
+    w = synth.q6_k_weights(n, k, 34)
+    y = orc.matmul("q6k", x, w, m, k, n, threads=2).reshape(m, n)
+    wd = orc.to_f32("q6k", w, n * k)
     want = f64_gemm(x, wd, m, k, n)
     bound = 2.0 ** -13 * (np.abs(x.reshape(m, k)) @ np.abs(wd.reshape(n, k)).T) + 1e-9
     assert np.all(np.abs(y - want) <= bound)
