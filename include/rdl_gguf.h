@@ -126,6 +126,22 @@ rdl_status rdl_gguf_tensor_data(const rdl_gguf* g, size_t i, const void** data, 
  * `stream` is a hipStream_t (NULL: the null stream). */
 rdl_status rdl_gguf_upload_tensor(const rdl_gguf* g, size_t i, void* dst_dev, uint64_t dst_len, void* stream);
 
+/* load_tensors' F32 expansion for one tensor, on the device: tensor i's
+ * blocks are uploaded to device scratch and expanded into dst_dev (f32,
+ * 16-byte aligned, dst_len >= the tensor's element count) exactly as the
+ * reference dequantizes at load (parser.rs:321-346, 371-776: K-quants,
+ * Q4_1, Q5_0, Q5_1, Q8_1) or Tensor::to_f32 expands it at model build
+ * (tensor.rs:535-639: F16, Q4_0, Q8_0); F32 is copied.  Only whole blocks
+ * are expanded, the elements after them are zero (the reference's
+ * n_elements / block_size).  Synchronous. */
+rdl_status rdl_gguf_upload_tensor_f32(const rdl_gguf* g, size_t i, float* dst_dev, uint64_t dst_len, void* stream);
+
+/* The same expansion of n_elements of GGML type ggml_type already in device
+ * memory (src_dev: GGUF blocks, src_len bytes) into dst_dev; stream-ordered.
+ * Unknown type ids give RDL_ERR_GGUF_UNSUPPORTED_TYPE. */
+rdl_status rdl_dequantize_gguf_dev(int32_t ggml_type, const void* src_dev, size_t src_len, size_t n_elements,
+                                   float* dst_dev, void* stream);
+
 /* GgufModelConfig (types.rs:165-186) as filled by to_model_config
  * (parser.rs:214-289).  Optional fields the file lacks are 0, or -1 for the
  * token ids; has_* flags say which were present. */

@@ -56,6 +56,8 @@ for _n in ("q4_0", "q4_1", "q8_0"):
     _decl(f"orc_to_f32_{_n}", _i, _u8p, _sz, _sz, _fp)
 _decl("orc_dequantize_q4k", _i, _u8p, _sz, _sz, _fp)
 _decl("orc_dequantize_q6k", _i, _u8p, _sz, _sz, _fp)
+for _n in ("q4_1_legacy", "q5_0", "q5_1", "q8_1", "q5k", "q8k", "q3k", "q2k"):
+    _decl(f"orc_dequantize_{_n}", _i, _u8p, _sz, _sz, _fp)
 _decl("orc_rope_tables", None, _i, _i, _f, _fp, _fp)
 _decl("orc_rms_norm_row", None, _fp, _fp, _sz, _f, _fp)
 
@@ -157,7 +159,10 @@ def to_f32(kind, w, n_elements):
     w, wp = _u8(w)
     out = np.zeros(n_elements, dtype=np.float32)
     fn = {"q4_0": lib.orc_to_f32_q4_0, "q4_1": lib.orc_to_f32_q4_1, "q8_0": lib.orc_to_f32_q8_0,
-          "q4k": lib.orc_dequantize_q4k, "q6k": lib.orc_dequantize_q6k}[kind]
+          "q4k": lib.orc_dequantize_q4k, "q6k": lib.orc_dequantize_q6k,
+          "q4_1_legacy": lib.orc_dequantize_q4_1_legacy, "q5_0": lib.orc_dequantize_q5_0,
+          "q5_1": lib.orc_dequantize_q5_1, "q8_1": lib.orc_dequantize_q8_1, "q5k": lib.orc_dequantize_q5k,
+          "q8k": lib.orc_dequantize_q8k, "q3k": lib.orc_dequantize_q3k, "q2k": lib.orc_dequantize_q2k}[kind]
     rc = fn(wp, w.size, n_elements, out.ctypes.data_as(_fp))
     if rc:
         raise OracleError(rc)

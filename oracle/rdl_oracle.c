@@ -577,6 +577,225 @@ int orc_dequantize_q6k(const uint8_t* data, size_t data_len, size_t n_elements, 
     return ORC_OK;
 }
 
+/* ---- the other load-time dequantizers (parser.rs:371-760) ----------------
+ * Each writes n_elements / block_size whole blocks (the reference's block
+ * count); elements past them keep the zero the reference's output Vec holds. */
+
+static float rd_f32le(const uint8_t* p) {
+    float f;
+    memcpy(&f, p, 4);  /* the host is little-endian, as the file */
+    return f;
+}
+static uint32_t rd_u32le(const uint8_t* p) {
+    return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+
+/* parser.rs:386-408: [f16 d][f16 m][16 B]; d * nibble + m */
+int orc_dequantize_q4_1_legacy(const uint8_t* data, size_t data_len, size_t n_elements, float* out) {
+    size_t nb = n_elements / 32;
+    if (data_len < nb * 20) return ORC_ERR_SHAPE_MISMATCH;
+    memset(out, 0, n_elements * sizeof(float));
+    for (size_t b = 0; b < nb; b++) {
+        const uint8_t* blk = data + b * 20;
+        float d = rd_f16(blk), m = rd_f16(blk + 2);
+        for (int j = 0; j < 16; j++) {
+            out[b * 32 + j] = d * (float)(blk[4 + j] & 0xF) + m;
+            out[b * 32 + j + 16] = d * (float)(blk[4 + j] >> 4) + m;
+        }
+    }
+    return ORC_OK;
+}
+
+/* parser.rs:411-437: [f16 d][u32 qh][16 B]; d * ((nibble | bit << 4) - 16) */
+int orc_dequantize_q5_0(const uint8_t* data, size_t data_len, size_t n_elements, float* out) {
+    size_t nb = n_elements / 32;
+    if (data_len < nb * 22) return ORC_ERR_SHAPE_MISMATCH;
+    memset(out, 0, n_elements * sizeof(float));
+    for (size_t b = 0; b < nb; b++) {
+        const uint8_t* blk = data + b * 22;
+        float d = rd_f16(blk);
+        uint32_t qh = rd_u32le(blk + 2);
+        for (int j = 0; j < 16; j++) {
+            int lo = (blk[6 + j] & 0xF) | (int)(((qh >> j) & 1) << 4);
+            int hi = (blk[6 + j] >> 4) | (int)(((qh >> (j + 16)) & 1) << 4);
+            out[b * 32 + j] = d * ((float)lo - 16.0f);
+            out[b * 32 + j + 16] = d * ((float)hi - 16.0f);
+        }
+    }
+    return ORC_OK;
+}
+
+/* parser.rs:440-467: [f16 d][f16 m][u32 qh][16 B]; d * (nibble | bit << 4) + m */
+int orc_dequantize_q5_1(const uint8_t* data, size_t data_len, size_t n_elements, float* out) {
+    size_t nb = n_elements / 32;
+    if (data_len < nb * 24) return ORC_ERR_SHAPE_MISMATCH;
+    memset(out, 0, n_elements * sizeof(float));
+    for (size_t b = 0; b < nb; b++) {
+        const uint8_t* blk = data + b * 24;
+        float d = rd_f16(blk), m = rd_f16(blk + 2);
+        uint32_t qh = rd_u32le(blk + 4);
+        for (int j = 0; j < 16; j++) {
+            uint32_t lo = (uint32_t)(blk[8 + j] & 0xF) | (((qh >> j) & 1) << 4);
+            uint32_t hi = (uint32_t)(blk[8 + j] >> 4) | (((qh >> (j + 16)) & 1) << 4);
+            out[b * 32 + j] = d * (float)lo + m;
+            out[b * 32 + j + 16] = d * (float)hi + m;
+        }
+    }
+    return ORC_OK;
+}
+
+/* parser.rs:470-489: [f32 d][f32 s][32 x i8]; d * q (s unused) */
+int orc_dequantize_q8_1(const uint8_t* data, size_t data_len, size_t n_elements, float* out) {
+    size_t nb = n_elements / 32;
+    if (data_len < nb * 40) return ORC_ERR_SHAPE_MISMATCH;
+    memset(out, 0, n_elements * sizeof(float));
+    for (size_t b = 0; b < nb; b++) {
+        const uint8_t* blk = data + b * 40;
+        float d = rd_f32le(blk);
+        for (int j = 0; j < 32; j++) out[b * 32 + j] = d * (float)(int8_t)blk[8 + j];
+    }
+    return ORC_OK;
+}
+
+/* parser.rs:595-646: [f16 d][f16 dmin][12 B scales][32 B qh][128 B qs]; the
+ * Q4_K scale/min unpack; element 64c + l (+32): d*sc * (nibble + 16 * bit) - dmin*mn,
+ * the bit of qh[l] at 2c (lo nibbles) or 2c + 1 (hi nibbles). */
+int orc_dequantize_q5k(const uint8_t* data, size_t data_len, size_t n_elements, float* out) {
+    size_t nb = n_elements / QK_K;
+    if (data_len < nb * 176) return ORC_ERR_SHAPE_MISMATCH;
+    memset(out, 0, n_elements * sizeof(float));
+    for (size_t b = 0; b < nb; b++) {
+        const uint8_t* blk = data + b * 176;
+        float d = rd_f16(blk), dmin = rd_f16(blk + 2);
+        const uint8_t* s = blk + 4;
+        const uint8_t* qh = blk + 16;
+        const uint8_t* qs = blk + 48;
+        uint8_t sc[8], mn[8];
+        for (int i = 0; i < 4; i++) {
+            sc[i] = s[i] & 63;
+            mn[i] = s[i + 4] & 63;
+            sc[i + 4] = (uint8_t)(((s[i] >> 6) & 3) | ((s[i + 8] & 0xF) << 2));
+            mn[i + 4] = (uint8_t)(((s[i + 4] >> 6) & 3) | ((s[i + 8] >> 4) << 2));
+        }
+        float* o = out + b * QK_K;
+        uint8_t u1 = 1, u2 = 2;
+        for (int c = 0; c < 4; c++) {
+            float d1 = d * (float)sc[2 * c], m1 = dmin * (float)mn[2 * c];
+            float d2 = d * (float)sc[2 * c + 1], m2 = dmin * (float)mn[2 * c + 1];
+            for (int l = 0; l < 32; l++) {
+                int hb = (qh[l] & u1) ? 16 : 0;
+                o[64 * c + l] = d1 * (float)((qs[32 * c + l] & 0xF) + hb) - m1;
+            }
+            for (int l = 0; l < 32; l++) {
+                int hb = (qh[l] & u2) ? 16 : 0;
+                o[64 * c + 32 + l] = d2 * (float)((qs[32 * c + l] >> 4) + hb) - m2;
+            }
+            u1 = (uint8_t)(u1 << 2);
+            u2 = (uint8_t)(u2 << 2);
+        }
+    }
+    return ORC_OK;
+}
+
+/* parser.rs:649-667: [f32 d][256 x i8][32 B bsums]; d * q */
+int orc_dequantize_q8k(const uint8_t* data, size_t data_len, size_t n_elements, float* out) {
+    size_t nb = n_elements / QK_K;
+    if (data_len < nb * 292) return ORC_ERR_SHAPE_MISMATCH;
+    memset(out, 0, n_elements * sizeof(float));
+    for (size_t b = 0; b < nb; b++) {
+        const uint8_t* blk = data + b * 292;
+        float d = rd_f32le(blk);
+        for (int j = 0; j < 256; j++) out[b * QK_K + j] = d * (float)(int8_t)blk[4 + j];
+    }
+    return ORC_OK;
+}
+
+/* parser.rs:669-735: [32 B hmask][64 B qs][12 B scales][f16 d].  The sixteen
+ * 6-bit scales: low nibbles from bytes 0..7 (scale i < 8: low nibble of byte
+ * i; 8 <= i < 16: high nibble of byte i - 8), high bit pairs from bytes 8..11
+ * (scale i: bits 2(i / 4) .. +1 of byte 8 + i % 4), each minus 32.  Element
+ * order: two halves of 128, four shift steps of 32 (16 + 16 with scales is,
+ * is + 1), value d*(scale - 32) * (2-bit q + (hmask bit set ? 0 : -4)). */
+int orc_dequantize_q3k(const uint8_t* data, size_t data_len, size_t n_elements, float* out) {
+    size_t nb = n_elements / QK_K;
+    if (data_len < nb * 110) return ORC_ERR_SHAPE_MISMATCH;
+    memset(out, 0, n_elements * sizeof(float));
+    for (size_t b = 0; b < nb; b++) {
+        const uint8_t* blk = data + b * 110;
+        const uint8_t* hm = blk;
+        const uint8_t* qs = blk + 32;
+        const uint8_t* sr = blk + 96;
+        const float d_all = rd_f16(blk + 108);
+        /* the aux-word unpack of :682-698 */
+        const uint32_t km1 = 0x03030303u, km2 = 0x0f0f0f0fu;
+        uint32_t a0 = rd_u32le(sr), a1 = rd_u32le(sr + 4), tmp = rd_u32le(sr + 8);
+        uint32_t aux[4];
+        aux[2] = ((a0 >> 4) & km2) | (((tmp >> 4) & km1) << 4);
+        aux[3] = ((a1 >> 4) & km2) | (((tmp >> 6) & km1) << 4);
+        aux[0] = (a0 & km2) | (((tmp >> 0) & km1) << 4);
+        aux[1] = (a1 & km2) | (((tmp >> 2) & km1) << 4);
+        int8_t scb[16];
+        for (int i = 0; i < 16; i++) scb[i] = (int8_t)((aux[i / 4] >> (8 * (i % 4))) & 0xFF);
+        float* o = out + b * QK_K;
+        int y = 0, is = 0;
+        uint8_t m = 1;
+        for (int half = 0; half < 2; half++) {
+            const uint8_t* q = qs + 32 * half;
+            int shift = 0;
+            for (int j = 0; j < 4; j++) {
+                float dl = d_all * ((float)scb[is] - 32.0f);
+                for (int l = 0; l < 16; l++) {
+                    int q2 = (q[l] >> shift) & 3;
+                    int hb = (hm[l] & m) ? 0 : -4;
+                    o[y++] = dl * (float)(q2 + hb);
+                }
+                dl = d_all * ((float)scb[is + 1] - 32.0f);
+                for (int l = 0; l < 16; l++) {
+                    int q2 = (q[l + 16] >> shift) & 3;
+                    int hb = (hm[l + 16] & m) ? 0 : -4;
+                    o[y++] = dl * (float)(q2 + hb);
+                }
+                is += 2;
+                shift += 2;
+                m = (uint8_t)(m << 1);
+            }
+        }
+    }
+    return ORC_OK;
+}
+
+/* parser.rs:737-776: [16 B scales][64 B qs][f16 d][f16 dmin]; scale byte:
+ * low nibble scale, high nibble min; value d*sc * q2 - dmin*mn, same element
+ * order as Q3_K. */
+int orc_dequantize_q2k(const uint8_t* data, size_t data_len, size_t n_elements, float* out) {
+    size_t nb = n_elements / QK_K;
+    if (data_len < nb * 84) return ORC_ERR_SHAPE_MISMATCH;
+    memset(out, 0, n_elements * sizeof(float));
+    for (size_t b = 0; b < nb; b++) {
+        const uint8_t* blk = data + b * 84;
+        const uint8_t* sc = blk;
+        const uint8_t* qs = blk + 16;
+        const float d = rd_f16(blk + 80), dmin = rd_f16(blk + 82);
+        float* o = out + b * QK_K;
+        int y = 0, is = 0;
+        for (int half = 0; half < 2; half++) {
+            const uint8_t* q = qs + 32 * half;
+            int shift = 0;
+            for (int j = 0; j < 4; j++) {
+                uint8_t s = sc[is++];
+                float dl = d * (float)(s & 0xF), ml = dmin * (float)(s >> 4);
+                for (int l = 0; l < 16; l++) o[y++] = dl * (float)((q[l] >> shift) & 3) - ml;
+                s = sc[is++];
+                dl = d * (float)(s & 0xF);
+                ml = dmin * (float)(s >> 4);
+                for (int l = 0; l < 16; l++) o[y++] = dl * (float)((q[l + 16] >> shift) & 3) - ml;
+                shift += 2;
+            }
+        }
+    }
+    return ORC_OK;
+}
+
 /* ------------------------------------------------------------------------ */
 /* F32 GEMV used as the timed part of the reference Q4_K path                */
 /* ------------------------------------------------------------------------ */

@@ -105,6 +105,18 @@ int orc_matmul_f32_q4k(const float* x, const uint8_t* w, size_t w_len, size_t m,
 /* dequantize_q6k: rustml/gguf/main/src/core/parser.rs:510-547 (ql low nibbles,
  * qh high bit pairs, int8 scales per 16 elements, f16 d at byte 208). */
 int orc_dequantize_q6k(const uint8_t* data, size_t data_len, size_t n_elements, float* out);
+/* The remaining load-time dequantizers of load_tensors (parser.rs:371-760):
+ * Q4_1 (:386-408), Q5_0 (:411-437), Q5_1 (:440-467), Q8_1 (:470-489), Q5_K
+ * (:595-646), Q8_K (:649-667), Q3_K (:669-735), Q2_K (:737-776).  Whole
+ * blocks of n_elements only; the rest of out is zero, as in the reference. */
+int orc_dequantize_q4_1_legacy(const uint8_t* data, size_t data_len, size_t n_elements, float* out);
+int orc_dequantize_q5_0(const uint8_t* data, size_t data_len, size_t n_elements, float* out);
+int orc_dequantize_q5_1(const uint8_t* data, size_t data_len, size_t n_elements, float* out);
+int orc_dequantize_q8_1(const uint8_t* data, size_t data_len, size_t n_elements, float* out);
+int orc_dequantize_q5k(const uint8_t* data, size_t data_len, size_t n_elements, float* out);
+int orc_dequantize_q8k(const uint8_t* data, size_t data_len, size_t n_elements, float* out);
+int orc_dequantize_q3k(const uint8_t* data, size_t data_len, size_t n_elements, float* out);
+int orc_dequantize_q2k(const uint8_t* data, size_t data_len, size_t n_elements, float* out);
 /* Q6_K "GEMV" as the reference runs it: dequantized at load (parser.rs:321-325),
  * then the F32 Linear; each dot summed sequentially in f32 (parity unpinned
  * beyond the f64 tolerance check, as for Q4_K). */

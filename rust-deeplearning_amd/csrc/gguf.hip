@@ -129,6 +129,7 @@ struct rdl_gguf {
         int32_t type = 0;
         uint64_t offset = 0;
         uint64_t n_bytes = 0;
+        uint64_t n_elements = 0;  // product(dims), when it fits (size_overflow otherwise)
         bool size_overflow = false;
     };
     std::vector<Tensor> tensors;
@@ -317,6 +318,8 @@ rdl_status parse(rdl_gguf* g) {
         const u128 bytes = nb * (u128)geo.block_bytes;
         t.size_overflow = !zero && (wide || nb > ~(u128)0 / (u128)geo.block_bytes || bytes > (u128)UINT64_MAX);
         t.n_bytes = t.size_overflow ? UINT64_MAX : (uint64_t)bytes;
+        // (a tensor whose bytes lie inside the file has fewer than 2^64 elements)
+        t.n_elements = zero ? 0 : (wide || ne > (u128)UINT64_MAX) ? UINT64_MAX : (uint64_t)ne;
         g->tensor_index[t.name] = g->tensors.size();
         g->tensors.push_back(std::move(t));
     }
@@ -582,6 +585,38 @@ rdl_status rdl_gguf_upload_tensor(const rdl_gguf* g, size_t i, void* dst_dev, ui
     std::lock_guard<std::mutex> lk(gm->stage_mu);
     if (!gm->stager) gm->stager = new rdl::Stager();
     HIP_TRY(gm->stager->copy2d(src, (size_t)len, 1, dst_dev, (size_t)len, (hipStream_t)stream));
+    return api_ok();
+}
+
+rdl_status rdl_gguf_upload_tensor_f32(const rdl_gguf* g, size_t i, float* dst_dev, uint64_t dst_len, void* stream) {
+    if (!g || !dst_dev) return api_fail(RDL_ERR_NULL_POINTER, "NULL argument");
+    const void* src = nullptr;
+    uint64_t len = 0;
+    rdl_status st = rdl_gguf_tensor_data(g, i, &src, &len);
+    if (st != RDL_OK) return st;
+    const rdl_gguf::Tensor& t = g->tensors[i];
+    if (dst_len < t.n_elements)
+        return api_fail(RDL_ERR_SHAPE_MISMATCH, "tensor '%s' has %llu elements, destination %llu",
+                        t.name.c_str(), (unsigned long long)t.n_elements, (unsigned long long)dst_len);
+    if ((uintptr_t)dst_dev & 15) return api_fail(RDL_ERR_INVALID_DATA, "destination must be 16-byte aligned");
+    if ((st = rdl::api_require_device()) != RDL_OK) return st;
+    if (t.n_elements == 0) return api_ok();
+    hipStream_t s = (hipStream_t)stream;
+    auto* gm = const_cast<rdl_gguf*>(g);
+    std::lock_guard<std::mutex> lk(gm->stage_mu);
+    if (!gm->stager) gm->stager = new rdl::Stager();
+    if (t.type == 0) {  // F32: the file bytes are the values
+        HIP_TRY(gm->stager->copy2d(src, (size_t)len, 1, dst_dev, (size_t)len, s));
+        return api_ok();
+    }
+    // the raw blocks into device scratch, expanded from there
+    void* raw = nullptr;
+    HIP_TRY(hipMalloc(&raw, (size_t)len + 16));
+    hipError_t e = gm->stager->copy2d(src, (size_t)len, 1, raw, (size_t)len, s);
+    if (e == hipSuccess) e = rdl::launch_dequant_gguf(t.type, static_cast<const uint8_t*>(raw), t.n_elements, dst_dev, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    (void)hipFree(raw);
+    if (e != hipSuccess) return api_fail(RDL_ERR_HIP, "f32 upload of '%s' failed: %s", t.name.c_str(), hipGetErrorString(e));
     return api_ok();
 }
 

@@ -179,6 +179,13 @@ hipError_t launch_gemv_q4_0_rope_kv(const uint8_t* w, size_t n, size_t k, const 
 hipError_t launch_q4_0_block_dots(const uint8_t* w, size_t n, size_t k, const NativeRec* rec,
                                   int32_t* partials, hipStream_t s);
 
+// GGMLType block geometry (elements, bytes per block); false for unknown ids.
+bool ggml_geometry(int32_t ggml_type, int* block_size, int* block_bytes);
+// Any GGML tensor type to f32 (load_tensors + Tensor::to_f32): the whole
+// blocks of n_elements, zeros after them; dst 16-byte aligned.
+hipError_t launch_dequant_gguf(int32_t ggml_type, const uint8_t* src, size_t n_elements, float* dst,
+                               hipStream_t s);
+
 // Dequantize selected rows of a Q4_0 / Q4_1 / Q8_0 matrix to f32.
 hipError_t launch_dequant_rows(WType t, const uint8_t* w, size_t n, size_t k,
                                const int32_t* rows, size_t n_rows, float* out, hipStream_t s);

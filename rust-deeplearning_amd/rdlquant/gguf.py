@@ -102,6 +102,8 @@ _decl("rdl_gguf_find_tensor", _i32, _p, C.c_char_p, C.POINTER(_sz))
 _decl("rdl_gguf_tensor_data", _i32, _p, _sz, C.POINTER(C.c_void_p), C.POINTER(C.c_uint64))
 _decl("rdl_gguf_upload_tensor", _i32, _p, _sz, _p, C.c_uint64, _p)
 _decl("rdl_gguf_model_config_get", _i32, _p, C.POINTER(_ModelConfig))
+_decl("rdl_gguf_upload_tensor_f32", _i32, _p, _sz, _p, C.c_uint64, _p)
+_decl("rdl_dequantize_gguf_dev", _i32, _i32, _p, _sz, _sz, _p, _p)
 
 _FMT = {U8: "<B", I8: "<b", U16: "<H", I16: "<h", U32: "<I", I32: "<i", F32: "<f", U64: "<Q", I64: "<q",
         F64: "<d"}
@@ -316,6 +318,12 @@ class GGUFFile:
         """A tensor's raw bytes into device memory at dst_ptr (synchronous)."""
         check(lib.rdl_gguf_upload_tensor(self._h, self._index(tensor), dst_ptr, dst_len, stream))
 
+    def upload_tensor_f32(self, tensor, dst_ptr: int, dst_len: int, stream: int = 0) -> None:
+        """load_tensors' F32 expansion of one tensor on the device (K-quants,
+        Q4_1, Q5_*, Q8_1 as parser.rs:371-776; F16, Q4_0, Q8_0 as Tensor::to_f32)
+        into dst_ptr (dst_len floats, 16-byte aligned); synchronous."""
+        check(lib.rdl_gguf_upload_tensor_f32(self._h, self._index(tensor), dst_ptr, dst_len, stream))
+
     def load_tensors(self) -> dict:
         """name -> LoadedTensor over views of the mapping (raw GGUF bytes for
         every type; the reference's load-time dequantization of K-quants and
@@ -346,3 +354,10 @@ class GGUFFile:
 def ggml_block(ggml_type: int):
     """(block_size, block_bytes) of a GGML type (types.rs:49-77)."""
     return GGML_BLOCK[ggml_type]
+
+
+def dequantize_gguf_dev(ggml_type: int, src_ptr: int, src_len: int, n_elements: int, dst_ptr: int,
+                        stream: int = 0) -> None:
+    """n_elements of GGML type ggml_type (GGUF blocks at src_ptr, device) to f32
+    at dst_ptr, bit-exact with the reference's load-time dequantization."""
+    check(lib.rdl_dequantize_gguf_dev(ggml_type, src_ptr, src_len, n_elements, dst_ptr, stream))

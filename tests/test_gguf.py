@@ -497,3 +497,14 @@ def test_open_missing_file(G, tmp_path):
     with pytest.raises(G.GgufIoError) as e:
         G.GGUFFile.parse_header(tmp_path / "absent.gguf")
     assert "os error 2" in str(e.value)
+
+
+def test_dequantize_rejects_unknown_types_and_short_sources(G):
+    with pytest.raises(G.UnsupportedType) as e:
+        G.dequantize_gguf_dev(4, 0, 0, 32, 0)
+    assert "GGML type: 4" in str(e.value)
+    with pytest.raises(G.UnsupportedType):
+        G.dequantize_gguf_dev(16, 0, 0, 32, 0)
+    import rdlquant as rq
+    with pytest.raises(rq.ShapeMismatch):
+        G.dequantize_gguf_dev(14, 0, 209, 256, 0)  # one Q6_K block is 210 bytes
