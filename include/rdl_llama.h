@@ -1,8 +1,8 @@
 /* rdl_llama.h -- batch-1 Llama-style decoder on one MI355X, built on the
  * quantized Linear path of rdl_quant.h (librdlquant.so).
  *
- * It replaces, for Q4_0 GGUF models with RMSNorm, RoPE, grouped-query
- * attention and SwiGLU, the rustml decode loop:
+ * It replaces, for GGUF models (Q4_0, Q8_0, Q4_1, Q4_K, Q6_K matrices) with
+ * RMSNorm, RoPE, grouped-query attention and SwiGLU, the rustml decode loop:
  *   LlmModel::forward_with_cache_pass   rustml/nlp/main/src/core/model.rs:890-937
  *   TransformerBlock::forward_with_cache rustml/nn/main/src/core/transformer_block.rs:297-356
  *   MultiHeadAttention::forward_with_cache rustml/nn/main/src/core/attention.rs:353-449
@@ -52,26 +52,40 @@ typedef struct rdl_llama_config {
 
 typedef struct rdl_llama rdl_llama;
 
-/* Weight slots.  Q4_0 GGUF bytes for the matrices (row-major [out, in]
- * blocks, as Linear::from_weights receives them) and the embedding; f32 for
+/* Weight slots.  GGUF block bytes for the matrices (row-major [out, in]
+ * blocks, as Linear::from_weights receives them) and the embedding, in the
+ * slot's type (Q4_0 unless rdl_llama_create_typed says otherwise); f32 for
  * the norm weights.  `layer` is ignored for the model-level slots. */
 enum {
-    RDL_LLAMA_TOKEN_EMBEDDING = 0, /* [vocab, dim] Q4_0 (dequantized per row like Tensor::to_f32) */
+    RDL_LLAMA_TOKEN_EMBEDDING = 0, /* [vocab, dim] (dequantized per row like Tensor::to_f32) */
     RDL_LLAMA_ATTN_NORM = 1,       /* [dim] f32 */
-    RDL_LLAMA_WQ = 2,              /* [n_heads*head_dim, dim] Q4_0 */
-    RDL_LLAMA_WK = 3,              /* [n_kv_heads*head_dim, dim] Q4_0 */
-    RDL_LLAMA_WV = 4,              /* [n_kv_heads*head_dim, dim] Q4_0 */
-    RDL_LLAMA_WO = 5,              /* [dim, n_heads*head_dim] Q4_0 */
+    RDL_LLAMA_WQ = 2,              /* [n_heads*head_dim, dim] */
+    RDL_LLAMA_WK = 3,              /* [n_kv_heads*head_dim, dim] */
+    RDL_LLAMA_WV = 4,              /* [n_kv_heads*head_dim, dim] */
+    RDL_LLAMA_WO = 5,              /* [dim, n_heads*head_dim] */
     RDL_LLAMA_FFN_NORM = 6,        /* [dim] f32 */
-    RDL_LLAMA_W_GATE = 7,          /* [ffn_dim, dim] Q4_0 */
-    RDL_LLAMA_W_UP = 8,            /* [ffn_dim, dim] Q4_0 */
-    RDL_LLAMA_W_DOWN = 9,          /* [dim, ffn_dim] Q4_0 */
+    RDL_LLAMA_W_GATE = 7,          /* [ffn_dim, dim] */
+    RDL_LLAMA_W_UP = 8,            /* [ffn_dim, dim] */
+    RDL_LLAMA_W_DOWN = 9,          /* [dim, ffn_dim] */
     RDL_LLAMA_FINAL_NORM = 10,     /* [dim] f32 */
-    RDL_LLAMA_OUTPUT = 11          /* [vocab, dim] in output_dtype's GGUF blocks */
+    RDL_LLAMA_OUTPUT = 11,         /* [vocab, dim] in output_dtype's GGUF blocks */
+    RDL_LLAMA_SLOTS = 12
 };
 
-/* Allocates weights, KV cache and activations on the current device. */
+/* Allocates weights, KV cache and activations on the current device; every
+ * matrix and the embedding Q4_0, the output matrix in cfg->output_dtype. */
 rdl_status rdl_llama_create(const rdl_llama_config* cfg, rdl_llama** out);
+
+/* The same with a GGUF type per matrix (as llama.cpp's mixed files hold
+ * them, e.g. Q4_K with Q6_K attn_v / ffn_down layers): types[layer *
+ * RDL_LLAMA_SLOTS + slot] for the per-layer matrix slots, layer 0's row for
+ * the embedding and output slots; norm slots are ignored; 0 means Q4_0 (the
+ * output: cfg->output_dtype).  Types: Q4_0, Q8_0, Q4_1, Q4_K, Q6_K (K-quants
+ * need in_features % 256 == 0).  A layer whose matrices are all Q4_0 runs
+ * the fused launches; other layers run their GEMVs by type with separate
+ * norm / RoPE / SwiGLU / add launches (q, k, v and gate, up as separate
+ * matrices when their types differ).  types may be NULL (rdl_llama_create). */
+rdl_status rdl_llama_create_typed(const rdl_llama_config* cfg, const int32_t* types, rdl_llama** out);
 rdl_status rdl_llama_free(rdl_llama* model);
 
 /* Copies one weight from host memory (len must equal the slot's size). */
@@ -80,7 +94,7 @@ rdl_status rdl_llama_set_weight(rdl_llama* model, int32_t slot, int32_t layer, c
 
 /* Seeded synthetic weights on the device, all slots: Q4_0 blocks with
  * nibbles uniform in [0, 15] and d = f16(|N(0, 0.02)| / 8), norm weights 1.0.
- * Q4_0 output matrices only (RDL_ERR_UNSUPPORTED otherwise). */
+ * All-Q4_0 models only (RDL_ERR_UNSUPPORTED otherwise). */
 rdl_status rdl_llama_init_random(rdl_llama* model, uint64_t seed);
 
 /* Empties the KV cache (KVCache::new state, current_len = 0). */
@@ -133,8 +147,10 @@ typedef struct rdl_llama_gguf_options {
  * file mapping to HBM through pinned staging buffers, without a host copy of
  * the file.  Tensors the map does not name are ignored.  Errors: a missing
  * weight gives RDL_ERR_NOT_FOUND "Missing weight: <internal name>" (the
- * reference's ModelError text); a matrix that is not Q4_0, norm weights that
- * are not F32/F16, a model without ffn_gate or a gemma3 file give
+ * reference's ModelError text); a matrix or embedding that is not Q4_0 /
+ * Q8_0 / Q4_1 / Q4_K / Q6_K (each keeps its own type, as in
+ * rdl_llama_create_typed), norm weights that are not F32/F16, a model
+ * without ffn_gate or a gemma3 file give
  * RDL_ERR_UNSUPPORTED; dims that differ from the config give
  * RDL_ERR_SHAPE_MISMATCH.  opt may be NULL (all defaults). */
 rdl_status rdl_llama_load_gguf(const rdl_gguf* gguf, const rdl_llama_gguf_options* opt, rdl_llama** out);

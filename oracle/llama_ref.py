@@ -42,10 +42,12 @@ class LlamaRef:
 
     def _linear(self, key, x, n, k):
         m = x.shape[0]
-        # the output matrix may be another GGUF type ("output_kind": an oracle
-        # matmul kind); the reference runs K-quants as F32 after load-time
-        # dequantization, which the oracle's q4k / q6k kinds restate
-        kind = self.w.get("output_kind", "q4") if key == "output" else "q4"
+        # a matrix may be another GGUF type (weights["kinds"][key]: an oracle
+        # matmul kind; "output_kind" for the output matrix); the reference
+        # runs K-quants as F32 after load-time dequantization, which the
+        # oracle's q4k / q6k kinds restate
+        kinds = self.w.get("kinds", {})
+        kind = kinds.get(key, self.w.get("output_kind", "q4") if key == "output" else "q4")
         return orc.matmul(kind, x, self.w[key], m, k, n, threads=self.threads).reshape(m, n)
 
     def _rope(self, t, start):

@@ -188,7 +188,7 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attention_kernel(
         // KG rows; load i of lane l is row KG i + l / CPR (when CPR <= 16)
         constexpr int CPR = HD * (int)sizeof(KV) / 16;
         constexpr bool VPRE = HD > 0 && CPR <= 16 && 64 % (CPR > 0 ? CPR : 1) == 0;
-        constexpr int KG = VPRE ? 64 / CPR : 1;
+        constexpr int KG = VPRE ? 64 / (CPR > 0 ? CPR : 1) : 1;
         float acc = 0.0f;
         if constexpr (VPRE) {
             // K and V loads all in flight before the first use: one round trip
@@ -350,13 +350,24 @@ __global__ void swiglu_kernel(const float* __restrict__ gu, int ffn, size_t n, f
     h[i] = (g * sig) * u;
 }
 
+// The same over separate [rows, ffn] gate and up buffers.
+__global__ void swiglu2_kernel(const float* __restrict__ g, const float* __restrict__ u, size_t n,
+                               float* __restrict__ h) {
+    const size_t i = (size_t)blockIdx.x * NT + threadIdx.x;
+    if (i >= n) return;
+    const float gv = g[i];
+    const float sig = 1.0f / (1.0f + expf(-gv));
+    h[i] = (gv * sig) * u[i];
+}
+
 // One greedy sampling step in one launch: argmax of the logits with the first
 // maximum winning (strict >, NaN never wins; an all-NaN / -inf row gives 0,
 // sampling.rs:8-18), the token written for the next step and to
 // out_tokens[*step] (then *step + 1), the position advanced by `advance`
 // (KVCache::advance, kv_cache.rs:112-114), and the sampled token's embedding
 // row dequantized into x (Embedding::forward, embedding.rs:50-76, on the Q4_0
-// table as Tensor::to_f32 computes it: d * (q - 8)) for the next step.
+// table as Tensor::to_f32 computes it: d * (q - 8)) for the next step (emb
+// NULL: no embedding, the next forward reads the token id).
 constexpr int SAMPLE_NT = 1024;
 __global__ __launch_bounds__(SAMPLE_NT) void sample_kernel(const float* __restrict__ logits, int vocab,
                                                            int* __restrict__ token, int* __restrict__ out_tokens,
@@ -428,6 +439,7 @@ __global__ __launch_bounds__(SAMPLE_NT) void sample_kernel(const float* __restri
         win = idx;
     }
     __syncthreads();
+    if (!emb) return;
     const uint8_t* row = emb + (size_t)win * (dim / 32) * Q4_0_BYTES;
     for (int e = threadIdx.x; e < dim; e += SAMPLE_NT) {
         const uint8_t* blk = row + (e >> 5) * Q4_0_BYTES;
@@ -488,12 +500,17 @@ struct LlamaModel {
         uint8_t* dev = nullptr;
         int n = 0, k = 0;
         bool gemm_ok = true;
-        WType type = WType::Q4_0;  // the output matrix may be another GGUF type
+        WType type = WType::Q4_0;
         size_t row_bytes() const { return (size_t)(k / block_elems(type)) * block_bytes(type); }
         size_t bytes() const { return (size_t)n * row_bytes(); }
     };
     struct Layer {
+        // q/k/v rows concatenated and gate/up rows interleaved when the parts
+        // share a GGUF type; otherwise the parts stand alone (split_*)
         Mat qkv, o, gu, down;
+        Mat q, k, v, gate, up;
+        bool split_qkv = false, split_gu = false;
+        bool fused = false;  // Q4_0 throughout: the fused launches serve m <= 4 rows
         float* attn_norm = nullptr;
         float* ffn_norm = nullptr;
     };
@@ -507,6 +524,7 @@ struct LlamaModel {
     // activations for up to max_batch rows
     float *x = nullptr, *xn = nullptr, *qkv = nullptr, *att = nullptr, *gu = nullptr, *hb = nullptr,
           *logits = nullptr;
+    float* part_tmp = nullptr;  // [max_batch][qkv_dim]: split q/k/v rows before they join qkv
     int *tokens = nullptr, *pos = nullptr, *step = nullptr, *out_tokens = nullptr;
     size_t out_cap = 0;
     void* gemm_scratch = nullptr;
@@ -545,11 +563,12 @@ struct LlamaModel {
     // y[m, mat.n] = x[m, mat.k] . W^T on the model's stream
     hipError_t linear(const Mat& w, const float* xin, size_t m, float* y) {
         if (m <= 4) return launch_gemv_fused(w.type, false, w.dev, w.n, w.k, xin, m, y, stream);
-        if (w.gemm_ok) return launch_gemm_q4_0(w.dev, w.n, w.k, xin, m, y, gemm_scratch, stream);
-        // rows one launch at a time through the fused GEMV (scales beyond the GEMM's range)
+        if (w.type == WType::Q4_0 && w.gemm_ok) return launch_gemm_q4_0(w.dev, w.n, w.k, xin, m, y, gemm_scratch, stream);
+        // rows four at a time through the fused GEMV (other types, or scales
+        // beyond the GEMM's range)
         for (size_t r = 0; r < m; r += 4) {
             const size_t mr = (m - r < 4) ? m - r : 4;
-            hipError_t e = launch_gemv_fused(WType::Q4_0, false, w.dev, w.n, w.k, xin + r * w.k, mr,
+            hipError_t e = launch_gemv_fused(w.type, false, w.dev, w.n, w.k, xin + r * w.k, mr,
                                              y + r * w.n, stream);
             if (e != hipSuccess) return e;
         }
@@ -593,78 +612,103 @@ struct LlamaModel {
         return hipGetLastError();
     }
 
-    // forward_with_cache_pass over m rows whose token ids are in `tokens`,
-    // the last row's logits into `logits`, then the position advances by m.
-    // Up to 4 rows: RMSNorm, SwiGLU and the residual adds ride in the GEMV
-    // launches (prologue / epilogue of the fused GEMV): 7 launches a layer.
-    // embed: x from the token ids (otherwise x already holds the rows, as
-    // sample_kernel leaves them); advance: the position moves on by m here.
-    hipError_t forward_fused(size_t m, bool embed = true, bool advance = true) {
+    // One layer through the fused Q4_0 launches (m <= 4): RMSNorm, RoPE + KV,
+    // SwiGLU and the residual adds ride in the GEMV launches (prologue /
+    // epilogue of the fused GEMV): five launches.
+    hipError_t layer_fused(int l, size_t m) {
+        const int d = cfg.dim;
+        const float eps = cfg.norm_eps;
+        Layer& L = layers[l];
+        // q = rope(rms_norm(x) . Wq^T); k, v -> cache (RoPE on k) in the same launch
+        hipError_t e = launch_gemv_q4_0_rope_kv(L.qkv.dev, L.qkv.n, d, x, m, qkv, L.attn_norm, eps, pos, cos_t,
+                                                sin_t, kv_layer(kc, l), kv_layer(vc, l), cfg.n_heads, cfg.n_kv_heads,
+                                                cfg.head_dim, cfg.max_seq, cfg.kv_f16 != 0, stream);
+        if (e != hipSuccess) return e;
+        e = cfg.kv_f16 ? layer_attention<_Float16>(l, m, false) : layer_attention<float>(l, m, false);
+        if (e != hipSuccess) return e;
+        // x += att . Wo^T
+        e = launch_gemv_q4_0_fused_ex(L.o.dev, L.o.n, q_dim, att, q_dim, m, x, 0, nullptr, 0.0f, 1, stream);
+        if (e != hipSuccess) return e;
+        // h = silu(gate) * up with [gate; up] = rms_norm(x) . Wgu^T (rows interleaved)
+        e = launch_gemv_q4_0_fused_ex(L.gu.dev, L.gu.n, d, x, d, m, hb, 1, L.ffn_norm, eps, 2, stream);
+        if (e != hipSuccess) return e;
+        // x += h . Wdown^T
+        return launch_gemv_q4_0_fused_ex(L.down.dev, L.down.n, cfg.ffn_dim, hb, cfg.ffn_dim, m, x, 0, nullptr,
+                                         0.0f, 1, stream);
+    }
+
+    // One layer with separate norm / add / SwiGLU / RoPE launches around the
+    // GEMVs (any resident type, any row count; m > 4 Q4_0 rows take the GEMM).
+    hipError_t layer_plain(int l, size_t m) {
+        const int d = cfg.dim;
+        Layer& L = layers[l];
+        hipError_t e;
+        hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)m), dim3(NT), 0, stream, x, L.attn_norm, d, cfg.norm_eps,
+                           xn);
+        if (!L.split_qkv) {
+            if ((e = linear(L.qkv, xn, m, qkv)) != hipSuccess) return e;
+        } else if (m == 1) {  // one row: the parts land in place
+            if ((e = linear(L.q, xn, 1, qkv)) != hipSuccess) return e;
+            if ((e = linear(L.k, xn, 1, qkv + q_dim)) != hipSuccess) return e;
+            if ((e = linear(L.v, xn, 1, qkv + q_dim + kv_dim)) != hipSuccess) return e;
+        } else {  // [m, part] rows, then strided into the [m, qkv_dim] rows
+            const Mat* parts[3] = {&L.q, &L.k, &L.v};
+            const int cols[3] = {0, q_dim, q_dim + kv_dim};
+            for (int i = 0; i < 3; i++) {
+                if ((e = linear(*parts[i], xn, m, part_tmp)) != hipSuccess) return e;
+                const size_t w = (size_t)parts[i]->n * sizeof(float);
+                if ((e = hipMemcpy2DAsync(qkv + cols[i], (size_t)qkv_dim * sizeof(float), part_tmp, w, w, m,
+                                          hipMemcpyDeviceToDevice, stream)) != hipSuccess)
+                    return e;
+            }
+        }
+        e = cfg.kv_f16 ? layer_attention<_Float16>(l, m) : layer_attention<float>(l, m);
+        if (e != hipSuccess) return e;
+        if ((e = linear(L.o, att, m, xn)) != hipSuccess) return e;
+        hipLaunchKernelGGL(add_kernel, dim3(blocks_for(m * d)), dim3(NT), 0, stream, x, xn, m * d);
+        hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)m), dim3(NT), 0, stream, x, L.ffn_norm, d, cfg.norm_eps,
+                           xn);
+        const size_t nf = m * (size_t)cfg.ffn_dim;
+        if (!L.split_gu) {
+            if ((e = linear(L.gu, xn, m, gu)) != hipSuccess) return e;
+            hipLaunchKernelGGL(swiglu_kernel, dim3(blocks_for(nf)), dim3(NT), 0, stream, gu, cfg.ffn_dim, nf, hb);
+        } else {
+            if ((e = linear(L.gate, xn, m, gu)) != hipSuccess) return e;
+            if ((e = linear(L.up, xn, m, gu + nf)) != hipSuccess) return e;
+            hipLaunchKernelGGL(swiglu2_kernel, dim3(blocks_for(nf)), dim3(NT), 0, stream, gu, gu + nf, nf, hb);
+        }
+        if ((e = linear(L.down, hb, m, xn)) != hipSuccess) return e;
+        hipLaunchKernelGGL(add_kernel, dim3(blocks_for(m * d)), dim3(NT), 0, stream, x, xn, m * d);
+        return hipGetLastError();
+    }
+
+    bool fused_shapes = false;  // the model's shapes meet the fused launches' rules
+    bool sample_embeds = false; // Q4_0 embedding table: sample_kernel writes the next x
+
+    // forward_with_cache_pass over m rows whose token ids are in `tokens`, the
+    // last row's logits into `logits`.  embed: x from the token ids (otherwise
+    // x already holds the rows, as sample_kernel leaves them); advance: the
+    // position moves on by m here.
+    hipError_t forward(size_t m, bool embed = true, bool advance = true) {
         const int d = cfg.dim;
         const float eps = cfg.norm_eps;
         hipError_t e = hipSuccess;
-        if (embed && (e = launch_dequant_rows(WType::Q4_0, emb.dev, emb.n, emb.k, tokens, m, x, stream)) != hipSuccess)
+        if (embed && (e = launch_dequant_rows(emb.type, emb.dev, emb.n, emb.k, tokens, m, x, stream)) != hipSuccess)
             return e;
         for (int l = 0; l < cfg.n_layers; l++) {
-            Layer& L = layers[l];
-            // q = rope(rms_norm(x) . Wq^T); k, v -> cache (RoPE on k) in the same launch
-            e = launch_gemv_q4_0_rope_kv(L.qkv.dev, L.qkv.n, d, x, m, qkv, L.attn_norm, eps, pos, cos_t, sin_t,
-                                         kv_layer(kc, l), kv_layer(vc, l), cfg.n_heads, cfg.n_kv_heads,
-                                         cfg.head_dim, cfg.max_seq, cfg.kv_f16 != 0, stream);
-            if (e != hipSuccess) return e;
-            e = cfg.kv_f16 ? layer_attention<_Float16>(l, m, false) : layer_attention<float>(l, m, false);
-            if (e != hipSuccess) return e;
-            // x += att . Wo^T
-            e = launch_gemv_q4_0_fused_ex(L.o.dev, L.o.n, q_dim, att, q_dim, m, x, 0, nullptr, 0.0f, 1, stream);
-            if (e != hipSuccess) return e;
-            // h = silu(gate) * up with [gate; up] = rms_norm(x) . Wgu^T (rows interleaved)
-            e = launch_gemv_q4_0_fused_ex(L.gu.dev, L.gu.n, d, x, d, m, hb, 1, L.ffn_norm, eps, 2, stream);
-            if (e != hipSuccess) return e;
-            // x += h . Wdown^T
-            e = launch_gemv_q4_0_fused_ex(L.down.dev, L.down.n, cfg.ffn_dim, hb, cfg.ffn_dim, m, x, 0, nullptr, 0.0f,
-                                          1, stream);
+            e = (m <= 4 && layers[l].fused) ? layer_fused(l, m) : layer_plain(l, m);
             if (e != hipSuccess) return e;
         }
         // logits = rms_norm(x_last, norm) . Wout^T (the norm fused into the GEMV for Q4_0)
-        if (out.type == WType::Q4_0) {
+        if (fused_shapes && out.type == WType::Q4_0) {
             e = launch_gemv_q4_0_fused_ex(out.dev, out.n, d, x + (m - 1) * d, d, 1, logits, 1, final_norm, eps, 0,
                                           stream);
         } else {
             hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(NT), 0, stream, x + (m - 1) * d, final_norm, d, eps, xn);
-            e = launch_gemv_fused(out.type, false, out.dev, out.n, out.k, xn, 1, logits, stream);
+            e = linear(out, xn, 1, logits);
         }
         if (e != hipSuccess) return e;
         if (advance) hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(64), 0, stream, pos, (int)m);
-        return hipGetLastError();
-    }
-    bool fusable = false;  // every GEMV of the model meets the fused-launch shape rules
-
-    hipError_t forward(size_t m) {
-        if (m <= 4 && fusable) return forward_fused(m);
-        const int d = cfg.dim;
-        hipError_t e = launch_dequant_rows(WType::Q4_0, emb.dev, emb.n, emb.k, tokens, m, x, stream);
-        if (e != hipSuccess) return e;
-        for (int l = 0; l < cfg.n_layers; l++) {
-            Layer& L = layers[l];
-            hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)m), dim3(NT), 0, stream, x, L.attn_norm, d,
-                               cfg.norm_eps, xn);
-            if ((e = linear(L.qkv, xn, m, qkv)) != hipSuccess) return e;
-            e = cfg.kv_f16 ? layer_attention<_Float16>(l, m) : layer_attention<float>(l, m);
-            if (e != hipSuccess) return e;
-            if ((e = linear(L.o, att, m, xn)) != hipSuccess) return e;
-            hipLaunchKernelGGL(add_kernel, dim3(blocks_for(m * d)), dim3(NT), 0, stream, x, xn, m * d);
-            hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)m), dim3(NT), 0, stream, x, L.ffn_norm, d,
-                               cfg.norm_eps, xn);
-            if ((e = linear(L.gu, xn, m, gu)) != hipSuccess) return e;
-            hipLaunchKernelGGL(swiglu_kernel, dim3(blocks_for(m * cfg.ffn_dim)), dim3(NT), 0, stream, gu,
-                               cfg.ffn_dim, m * cfg.ffn_dim, hb);
-            if ((e = linear(L.down, hb, m, xn)) != hipSuccess) return e;
-            hipLaunchKernelGGL(add_kernel, dim3(blocks_for(m * d)), dim3(NT), 0, stream, x, xn, m * d);
-        }
-        const float* last = x + (m - 1) * d;
-        hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(NT), 0, stream, last, final_norm, d, cfg.norm_eps, xn);
-        if ((e = linear(out, xn, 1, logits)) != hipSuccess) return e;
-        hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(64), 0, stream, pos, (int)m);
         return hipGetLastError();
     }
 
@@ -672,15 +716,16 @@ struct LlamaModel {
     // token's embedding row -> x (the input of the next decode step)
     void sample(int advance) {
         hipLaunchKernelGGL(sample_kernel, dim3(1), dim3(SAMPLE_NT), 0, stream, logits, cfg.vocab, tokens, out_tokens,
-                           step, pos, advance, emb.dev, cfg.dim, x);
+                           step, pos, advance, sample_embeds ? emb.dev : nullptr, cfg.dim, x);
     }
 
-    // One greedy decode step: x (the last token's embedding, left by sample)
-    // -> logits -> sample: the next token and its embedding.
+    // One greedy decode step: the last token (its embedding in x when the
+    // sampling launch wrote it) -> logits -> sample: the next token (and its
+    // embedding, and the position advance, when the table is Q4_0).
     hipError_t decode_step() {
-        hipError_t e = fusable ? forward_fused(1, false, false) : forward(1);
+        hipError_t e = forward(1, !sample_embeds, !sample_embeds);
         if (e != hipSuccess) return e;
-        sample(fusable ? 1 : 0);
+        sample(sample_embeds ? 1 : 0);
         return hipGetLastError();
     }
 };
@@ -739,12 +784,32 @@ rdl_status slot_target(rdl::LlamaModel& M, int32_t slot, int32_t layer, SlotTarg
         case RDL_LLAMA_FINAL_NORM: f32(M.final_norm); break;
         case RDL_LLAMA_ATTN_NORM: f32(M.layers[layer].attn_norm); break;
         case RDL_LLAMA_FFN_NORM: f32(M.layers[layer].ffn_norm); break;
-        case RDL_LLAMA_WQ: q4(M.layers[layer].qkv, 0, M.q_dim); break;
-        case RDL_LLAMA_WK: q4(M.layers[layer].qkv, M.q_dim, M.kv_dim); break;
-        case RDL_LLAMA_WV: q4(M.layers[layer].qkv, M.q_dim + M.kv_dim, M.kv_dim); break;
+        case RDL_LLAMA_WQ: {
+            auto& L = M.layers[layer];
+            L.split_qkv ? q4(L.q, 0, M.q_dim) : q4(L.qkv, 0, M.q_dim);
+            break;
+        }
+        case RDL_LLAMA_WK: {
+            auto& L = M.layers[layer];
+            L.split_qkv ? q4(L.k, 0, M.kv_dim) : q4(L.qkv, M.q_dim, M.kv_dim);
+            break;
+        }
+        case RDL_LLAMA_WV: {
+            auto& L = M.layers[layer];
+            L.split_qkv ? q4(L.v, 0, M.kv_dim) : q4(L.qkv, M.q_dim + M.kv_dim, M.kv_dim);
+            break;
+        }
         case RDL_LLAMA_WO: q4(M.layers[layer].o, 0, c.dim); break;
-        case RDL_LLAMA_W_GATE: q4(M.layers[layer].gu, 0, c.ffn_dim, 2); break;  // even rows of [gate; up]
-        case RDL_LLAMA_W_UP: q4(M.layers[layer].gu, 1, c.ffn_dim, 2); break;    // odd rows
+        case RDL_LLAMA_W_GATE: {  // even rows of the interleaved [gate; up]
+            auto& L = M.layers[layer];
+            L.split_gu ? q4(L.gate, 0, c.ffn_dim) : q4(L.gu, 0, c.ffn_dim, 2);
+            break;
+        }
+        case RDL_LLAMA_W_UP: {  // odd rows
+            auto& L = M.layers[layer];
+            L.split_gu ? q4(L.up, 0, c.ffn_dim) : q4(L.gu, 1, c.ffn_dim, 2);
+            break;
+        }
         case RDL_LLAMA_W_DOWN: q4(M.layers[layer].down, 0, c.dim); break;
         default: return api_fail(RDL_ERR_INVALID_DATA, "unknown weight slot %d", slot);
     }
@@ -766,32 +831,61 @@ rdl_status finish_slot(const SlotTarget& t) {
 extern "C" {
 
 rdl_status rdl_llama_create(const rdl_llama_config* cfg, rdl_llama** out) {
+    return rdl_llama_create_typed(cfg, nullptr, out);
+}
+
+rdl_status rdl_llama_create_typed(const rdl_llama_config* cfg, const int32_t* types, rdl_llama** out) {
     if (!cfg || !out) return api_fail(RDL_ERR_NULL_POINTER, "NULL argument");
     *out = nullptr;
     if (!valid_config(*cfg))
         return api_fail(RDL_ERR_INVALID_DATA,
                         "unsupported config (dim, ffn_dim, heads*head_dim multiples of 32 and <= 16384; "
                         "head_dim even <= 256; n_heads %% n_kv_heads == 0)");
+    const int32_t od = cfg->output_dtype == 0 ? RDL_DTYPE_Q4_0 : cfg->output_dtype;
+    const int q_dim = cfg->n_heads * cfg->head_dim;
+    // the GGUF type of every matrix: types[layer * RDL_LLAMA_SLOTS + slot],
+    // model-level slots in layer 0's row; 0 = Q4_0 (the output: output_dtype)
+    auto type_of = [&](int slot, int layer) -> int32_t {
+        const int32_t t = types ? types[(size_t)layer * RDL_LLAMA_SLOTS + slot] : 0;
+        if (t != 0) return t;
+        return slot == RDL_LLAMA_OUTPUT ? od : RDL_DTYPE_Q4_0;
+    };
+    auto in_features = [&](int slot) {
+        return slot == RDL_LLAMA_WO ? q_dim : slot == RDL_LLAMA_W_DOWN ? cfg->ffn_dim : cfg->dim;
+    };
+    for (int l = 0; l < cfg->n_layers; l++)
+        for (int slot = 0; slot < RDL_LLAMA_SLOTS; slot++) {
+            const bool model_slot =
+                slot == RDL_LLAMA_TOKEN_EMBEDDING || slot == RDL_LLAMA_FINAL_NORM || slot == RDL_LLAMA_OUTPUT;
+            if (slot == RDL_LLAMA_ATTN_NORM || slot == RDL_LLAMA_FFN_NORM || slot == RDL_LLAMA_FINAL_NORM ||
+                (model_slot && l > 0))
+                continue;
+            const int32_t t = type_of(slot, l);
+            if (t != RDL_DTYPE_Q4_0 && t != RDL_DTYPE_Q8_0 && t != RDL_DTYPE_Q4_1 && t != RDL_DTYPE_Q4_K &&
+                t != RDL_DTYPE_Q6_K)
+                return api_fail(RDL_ERR_UNSUPPORTED, "slot %d layer %d: type %d (Q4_0, Q8_0, Q4_1, Q4_K or Q6_K)",
+                                slot, l, t);
+            if ((t == RDL_DTYPE_Q4_K || t == RDL_DTYPE_Q6_K) && in_features(slot) % rdl::QK_K != 0)
+                return api_fail(RDL_ERR_UNSUPPORTED, "slot %d layer %d: a K-quant matrix needs in_features %% 256 "
+                                "== 0 (%d)", slot, l, in_features(slot));
+        }
     rdl_status st = rdl::api_require_device();
     if (st != RDL_OK) return st;
-    const int32_t od = cfg->output_dtype == 0 ? RDL_DTYPE_Q4_0 : cfg->output_dtype;
-    if (od != RDL_DTYPE_Q4_0 && od != RDL_DTYPE_Q8_0 && od != RDL_DTYPE_Q4_1 && od != RDL_DTYPE_Q4_K &&
-        od != RDL_DTYPE_Q6_K)
-        return api_fail(RDL_ERR_UNSUPPORTED, "output matrix type %d (Q4_0, Q8_0, Q4_1, Q4_K or Q6_K)", od);
-    if ((od == RDL_DTYPE_Q4_K || od == RDL_DTYPE_Q6_K) && cfg->dim % rdl::QK_K != 0)
-        return api_fail(RDL_ERR_UNSUPPORTED, "K-quant output matrix needs dim %% 256 == 0 (dim %d)", cfg->dim);
     rdl_llama* h = new rdl_llama();
     rdl::LlamaModel& M = h->m;
     M.cfg = *cfg;
-    M.cfg.output_dtype = od;
-    M.out.type = (rdl::WType)od;
+    M.cfg.output_dtype = type_of(RDL_LLAMA_OUTPUT, 0);
+    M.out.type = (rdl::WType)M.cfg.output_dtype;
+    M.emb.type = (rdl::WType)type_of(RDL_LLAMA_TOKEN_EMBEDDING, 0);
+    M.sample_embeds = M.emb.type == rdl::WType::Q4_0;
     const rdl_llama_config& c = M.cfg;
     M.q_dim = c.n_heads * c.head_dim;
     M.kv_dim = c.n_kv_heads * c.head_dim;
     M.qkv_dim = M.q_dim + 2 * M.kv_dim;
-    auto mat = [&](rdl::LlamaModel::Mat& w, int n, int k) -> hipError_t {
+    auto mat = [&](rdl::LlamaModel::Mat& w, int n, int k, int32_t t = RDL_DTYPE_Q4_0) -> hipError_t {
         w.n = n;
         w.k = k;
+        w.type = (rdl::WType)t;
         return M.alloc(reinterpret_cast<void**>(&w.dev), w.bytes() + 64);
     };
     auto fail_free = [&](hipError_t e) {
@@ -803,16 +897,34 @@ rdl_status rdl_llama_create(const rdl_llama_config* cfg, rdl_llama** out) {
     for (auto& ev : M.ev)
         if ((e = hipEventCreate(&ev)) != hipSuccess) return fail_free(e);
     M.layers.resize(c.n_layers);
-    for (auto& L : M.layers) {
-        if ((e = mat(L.qkv, M.qkv_dim, c.dim)) != hipSuccess) return fail_free(e);
-        if ((e = mat(L.o, c.dim, M.q_dim)) != hipSuccess) return fail_free(e);
-        if ((e = mat(L.gu, 2 * c.ffn_dim, c.dim)) != hipSuccess) return fail_free(e);
-        if ((e = mat(L.down, c.dim, c.ffn_dim)) != hipSuccess) return fail_free(e);
+    bool any_split_qkv = false;
+    for (int l = 0; l < c.n_layers; l++) {
+        rdl::LlamaModel::Layer& L = M.layers[l];
+        const int32_t tq = type_of(RDL_LLAMA_WQ, l), tk = type_of(RDL_LLAMA_WK, l), tv = type_of(RDL_LLAMA_WV, l);
+        const int32_t tg = type_of(RDL_LLAMA_W_GATE, l), tu = type_of(RDL_LLAMA_W_UP, l);
+        L.split_qkv = tq != tk || tq != tv;
+        L.split_gu = tg != tu;
+        any_split_qkv |= L.split_qkv;
+        if (L.split_qkv) {
+            if ((e = mat(L.q, M.q_dim, c.dim, tq)) != hipSuccess) return fail_free(e);
+            if ((e = mat(L.k, M.kv_dim, c.dim, tk)) != hipSuccess) return fail_free(e);
+            if ((e = mat(L.v, M.kv_dim, c.dim, tv)) != hipSuccess) return fail_free(e);
+        } else if ((e = mat(L.qkv, M.qkv_dim, c.dim, tq)) != hipSuccess) {
+            return fail_free(e);
+        }
+        if ((e = mat(L.o, c.dim, M.q_dim, type_of(RDL_LLAMA_WO, l))) != hipSuccess) return fail_free(e);
+        if (L.split_gu) {
+            if ((e = mat(L.gate, c.ffn_dim, c.dim, tg)) != hipSuccess) return fail_free(e);
+            if ((e = mat(L.up, c.ffn_dim, c.dim, tu)) != hipSuccess) return fail_free(e);
+        } else if ((e = mat(L.gu, 2 * c.ffn_dim, c.dim, tg)) != hipSuccess) {
+            return fail_free(e);
+        }
+        if ((e = mat(L.down, c.dim, c.ffn_dim, type_of(RDL_LLAMA_W_DOWN, l))) != hipSuccess) return fail_free(e);
         if ((e = M.alloc_t(&L.attn_norm, c.dim)) != hipSuccess) return fail_free(e);
         if ((e = M.alloc_t(&L.ffn_norm, c.dim)) != hipSuccess) return fail_free(e);
     }
-    if ((e = mat(M.emb, c.vocab, c.dim)) != hipSuccess) return fail_free(e);
-    if ((e = mat(M.out, c.vocab, c.dim)) != hipSuccess) return fail_free(e);
+    if ((e = mat(M.emb, c.vocab, c.dim, (int32_t)M.emb.type)) != hipSuccess) return fail_free(e);
+    if ((e = mat(M.out, c.vocab, c.dim, (int32_t)M.out.type)) != hipSuccess) return fail_free(e);
     if ((e = M.alloc_t(&M.final_norm, c.dim)) != hipSuccess) return fail_free(e);
     const size_t kv_bytes = (size_t)c.n_layers * M.kv_layer_elems() * M.kv_elem();
     if ((e = M.alloc(&M.kc, kv_bytes)) != hipSuccess) return fail_free(e);
@@ -832,11 +944,15 @@ rdl_status rdl_llama_create(const rdl_llama_config* cfg, rdl_llama** out) {
     if ((e = M.alloc_t(&M.out_tokens, M.out_cap)) != hipSuccess) return fail_free(e);
     const size_t kmax = (size_t)std::max(std::max(c.dim, c.ffn_dim), M.q_dim);
     if ((e = M.alloc(&M.gemm_scratch, rdl::gemm_scratch_bytes(mb, kmax))) != hipSuccess) return fail_free(e);
+    if (any_split_qkv && (e = M.alloc_t(&M.part_tmp, mb * M.qkv_dim)) != hipSuccess) return fail_free(e);
     // (row-pair epilogues need at most 4 columns per lane: dim <= 8192)
-    M.fusable = (c.dim / 32) % 2 == 0 && (M.q_dim / 32) % 2 == 0 && (c.ffn_dim / 32) % 2 == 0 &&
-                c.dim / 32 <= 256 &&
-                (uint64_t)2 * c.ffn_dim * (c.dim / 32) * rdl::Q4_0_BYTES <= rdl::FUSED_MAX_WEIGHT_BYTES &&
-                (uint64_t)M.out.bytes() <= rdl::FUSED_MAX_WEIGHT_BYTES;
+    M.fused_shapes = (c.dim / 32) % 2 == 0 && (M.q_dim / 32) % 2 == 0 && (c.ffn_dim / 32) % 2 == 0 &&
+                     c.dim / 32 <= 256 &&
+                     (uint64_t)2 * c.ffn_dim * (c.dim / 32) * rdl::Q4_0_BYTES <= rdl::FUSED_MAX_WEIGHT_BYTES &&
+                     (uint64_t)c.vocab * (c.dim / 32) * rdl::Q4_0_BYTES <= rdl::FUSED_MAX_WEIGHT_BYTES;
+    for (auto& L : M.layers)
+        L.fused = M.fused_shapes && !L.split_qkv && !L.split_gu && L.qkv.type == rdl::WType::Q4_0 &&
+                  L.o.type == rdl::WType::Q4_0 && L.gu.type == rdl::WType::Q4_0 && L.down.type == rdl::WType::Q4_0;
     M.att_nspan = (c.max_seq + rdl::ATT_SPAN - 1) / rdl::ATT_SPAN;
     if ((e = M.alloc_t(&M.att_part, mb * c.n_heads * (size_t)M.att_nspan * (c.head_dim + 2))) != hipSuccess)
         return fail_free(e);
@@ -885,8 +1001,11 @@ rdl_status rdl_llama_init_random(rdl_llama* model, uint64_t seed) {
     if (!model) return api_fail(RDL_ERR_NULL_POINTER, "NULL model");
     rdl::LlamaModel& M = model->m;
     const rdl_llama_config& c = M.cfg;
-    if (M.out.type != rdl::WType::Q4_0)
-        return api_fail(RDL_ERR_UNSUPPORTED, "synthetic weights are Q4_0: output_dtype must be Q4_0");
+    bool all_q4 = M.out.type == rdl::WType::Q4_0 && M.emb.type == rdl::WType::Q4_0;
+    for (auto& L : M.layers) all_q4 &= L.fused || (!L.split_qkv && !L.split_gu && L.qkv.type == rdl::WType::Q4_0 &&
+                                                  L.o.type == rdl::WType::Q4_0 && L.gu.type == rdl::WType::Q4_0 &&
+                                                  L.down.type == rdl::WType::Q4_0);
+    if (!all_q4) return api_fail(RDL_ERR_UNSUPPORTED, "synthetic weights are Q4_0: every matrix must be Q4_0");
     uint64_t tag = 0;
     auto fill_mat = [&](rdl::LlamaModel::Mat& w) {
         const size_t nblocks = (size_t)w.n * (w.k / rdl::QK);
@@ -1122,16 +1241,12 @@ void slot_dims(const rdl_llama_config& c, int slot, uint64_t d[2], uint32_t* nd)
 // Type and shape of one tensor against its slot.
 rdl_status check_tensor(const rdl_llama_config& c, int slot, const rdl_gguf_tensor_info& ti) {
     const bool norm = slot == RDL_LLAMA_ATTN_NORM || slot == RDL_LLAMA_FFN_NORM || slot == RDL_LLAMA_FINAL_NORM;
-    if (slot == RDL_LLAMA_OUTPUT) {
-        const int32_t t = ti.ggml_type;
-        if (t != RDL_DTYPE_Q4_0 && t != RDL_DTYPE_Q8_0 && t != RDL_DTYPE_Q4_1 && t != RDL_DTYPE_Q4_K &&
-            t != RDL_DTYPE_Q6_K)
-            return api_fail(RDL_ERR_UNSUPPORTED, "tensor '%s' is %s; the output matrix may be Q4_0, Q8_0, "
-                            "Q4_1, Q4_K or Q6_K", ti.name, ggml_name(t));
-    } else if (norm ? (ti.ggml_type != 0 && ti.ggml_type != 1) : ti.ggml_type != 2) {
-        return api_fail(RDL_ERR_UNSUPPORTED, "tensor '%s' is %s; the decoder takes %s", ti.name,
-                        ggml_name(ti.ggml_type), norm ? "F32 or F16 norm weights" : "Q4_0 matrices");
-    }
+    const int32_t t = ti.ggml_type;
+    if (norm ? (t != 0 && t != 1)
+             : (t != RDL_DTYPE_Q4_0 && t != RDL_DTYPE_Q8_0 && t != RDL_DTYPE_Q4_1 && t != RDL_DTYPE_Q4_K &&
+                t != RDL_DTYPE_Q6_K))
+        return api_fail(RDL_ERR_UNSUPPORTED, "tensor '%s' is %s; the decoder takes %s", ti.name, ggml_name(t),
+                        norm ? "F32 or F16 norm weights" : "Q4_0, Q8_0, Q4_1, Q4_K or Q6_K matrices");
     uint64_t d[2];
     uint32_t nd = 0;
     slot_dims(c, slot, d, &nd);
@@ -1233,8 +1348,17 @@ rdl_status rdl_llama_load_gguf(const rdl_gguf* g, const rdl_llama_gguf_options* 
         plan.push_back({i, {slot, layer}});
     }
 
+    // the file's type for every matrix slot (the later of two same-named tensors)
+    std::vector<int32_t> types((size_t)c.n_layers * RDL_LLAMA_SLOTS, 0);
+    for (const auto& p : plan) {
+        rdl_gguf_tensor_info ti;
+        rdl_gguf_tensor_info_at(g, p.first, &ti);
+        const int slot = p.second.first, layer = p.second.second;
+        if (slot != RDL_LLAMA_ATTN_NORM && slot != RDL_LLAMA_FFN_NORM && slot != RDL_LLAMA_FINAL_NORM)
+            types[(size_t)layer * RDL_LLAMA_SLOTS + slot] = ti.ggml_type;
+    }
     rdl_llama* h = nullptr;
-    if ((st = rdl_llama_create(&c, &h)) != RDL_OK) return st;
+    if ((st = rdl_llama_create_typed(&c, types.data(), &h)) != RDL_OK) return st;
     rdl::LlamaModel& M = h->m;
     auto fail = [&](rdl_status s) {
         rdl_llama_free(h);
@@ -1266,8 +1390,9 @@ rdl_status rdl_llama_load_gguf(const rdl_gguf* g, const rdl_llama_gguf_options* 
     }
     // block-scale scan of each matrix once (the GEMM's f16 range)
     std::vector<rdl::LlamaModel::Mat*> mats = {&M.out};
-    for (auto& L : M.layers) mats.insert(mats.end(), {&L.qkv, &L.o, &L.gu, &L.down});
+    for (auto& L : M.layers) mats.insert(mats.end(), {&L.qkv, &L.o, &L.gu, &L.down, &L.q, &L.k, &L.v, &L.gate, &L.up});
     for (rdl::LlamaModel::Mat* m : mats) {
+        if (!m->dev) continue;  // the combined or the split form of a layer's q/k/v, gate/up
         SlotTarget t;
         t.mat = m;
         if ((st = finish_slot(t)) != RDL_OK) return fail(st);

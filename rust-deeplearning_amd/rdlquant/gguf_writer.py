@@ -183,10 +183,11 @@ LLAMA_LAYER_TENSORS = ("attn_norm", "attn_q", "attn_k", "attn_v", "attn_output",
                        "ffn_up", "ffn_down")
 
 
-def llama_tensor_shapes(cfg):
-    """GGUF name -> (dims innermost first, ggml type) for a Q4_0 Llama model of
-    `cfg` (rdlquant.llama.LlamaConfig fields; the output matrix in
-    cfg.output_dtype), in llama.cpp's file order."""
+def llama_tensor_shapes(cfg, types=None):
+    """GGUF name -> (dims innermost first, ggml type) for a Llama model of
+    `cfg` (rdlquant.llama.LlamaConfig fields), in llama.cpp's file order:
+    matrices Q4_0 unless `types` ({GGUF name: GGML type}) says otherwise,
+    the output matrix in cfg.output_dtype."""
     d, q, kv, f, v = cfg.dim, cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim, cfg.ffn_dim, cfg.vocab
     out = {"token_embd.weight": ([d, v], GGML_Q4_0)}
     for i in range(cfg.n_layers):
@@ -202,14 +203,17 @@ def llama_tensor_shapes(cfg):
         out[p + "ffn_down.weight"] = ([f, d], GGML_Q4_0)
     out["output_norm.weight"] = ([d], GGML_F32)
     out["output.weight"] = ([d, v], getattr(cfg, "output_dtype", GGML_Q4_0) or GGML_Q4_0)
+    for name, t in (types or {}).items():
+        out[name] = (out[name][0], t)
     return out
 
 
 def llama_builder(cfg, tensor_data, arch="llama", context_length=None, extra_metadata=None,
-                  skip=()):
+                  skip=(), types=None):
     """A GgufBuilder of a Llama model: metadata from `cfg`, tensors in
-    llama_tensor_shapes order with bytes from tensor_data(name) (bytes-like or
-    a callable); names in `skip` are left out."""
+    llama_tensor_shapes order (types: {GGUF name: GGML type}) with bytes from
+    tensor_data(name) (bytes-like or a callable); names in `skip` are left
+    out."""
     b = GgufBuilder()
     b.add_string("general.architecture", arch)
     b.add_string("general.name", "synthetic")
@@ -226,7 +230,7 @@ def llama_builder(cfg, tensor_data, arch="llama", context_length=None, extra_met
     b.add_u32("tokenizer.ggml.eos_token_id", 2)
     for k, (t, v) in (extra_metadata or {}).items():
         b.add_value(k, t, v)
-    for name, (dims, t) in llama_tensor_shapes(cfg).items():
+    for name, (dims, t) in llama_tensor_shapes(cfg, types).items():
         if name not in skip:
             b.add_tensor_data(name, dims, t, tensor_data(name))
     return b

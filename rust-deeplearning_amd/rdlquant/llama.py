@@ -17,6 +17,7 @@ import numpy as np
 from . import _decl, _i32, _p, _sz, check, lib
 
 TOKEN_EMBEDDING, ATTN_NORM, WQ, WK, WV, WO, FFN_NORM, W_GATE, W_UP, W_DOWN, FINAL_NORM, OUTPUT = range(12)
+SLOTS = 12
 
 
 class _Config(C.Structure):
@@ -27,6 +28,7 @@ class _Config(C.Structure):
 
 
 _decl("rdl_llama_create", _i32, C.POINTER(_Config), C.POINTER(_p))
+_decl("rdl_llama_create_typed", _i32, C.POINTER(_Config), C.POINTER(C.c_int32), C.POINTER(_p))
 _decl("rdl_llama_free", _i32, _p)
 _decl("rdl_llama_set_weight", _i32, _p, _i32, _i32, _p, _sz)
 _decl("rdl_llama_init_random", _i32, _p, C.c_uint64)
@@ -76,11 +78,20 @@ def _i32_array(tokens):
 class LlamaModel:
     """Q4_0 Llama-style decoder resident on the current GPU."""
 
-    def __init__(self, config: LlamaConfig):
+    def __init__(self, config: LlamaConfig, types=None):
+        """types: None (every matrix Q4_0, the output in config.output_dtype) or
+        {(slot, layer): GGML type id} for the matrices that are not Q4_0
+        (rdl_llama_create_typed; model-level slots use layer 0)."""
         self.config = config
         h = _p()
         cfg = config._c()
-        check(lib.rdl_llama_create(C.byref(cfg), C.byref(h)))
+        if types:
+            t = np.zeros(config.n_layers * SLOTS, dtype=np.int32)
+            for (slot, layer), v in types.items():
+                t[layer * SLOTS + slot] = v
+            check(lib.rdl_llama_create_typed(C.byref(cfg), t.ctypes.data_as(C.POINTER(C.c_int32)), C.byref(h)))
+        else:
+            check(lib.rdl_llama_create(C.byref(cfg), C.byref(h)))
         self._h = h
 
     @classmethod

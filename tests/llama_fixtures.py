@@ -12,42 +12,58 @@ def tiny_config(**kw):
     return LlamaConfig(**base)
 
 
-def tiny_weights(cfg, seed=1234):
-    """(gpu_slots, oracle_weights): the same seeded bytes for both sides."""
+KIND = {2: "q4", 3: "q4_1", 8: "q8", 12: "q4k", 14: "q6k"}  # GGML type -> oracle matmul kind
+DEQ = {2: "q4_0", 3: "q4_1", 8: "q8_0", 12: "q4k", 14: "q6k"}  # GGML type -> oracle to_f32 kind
+
+
+def tiny_weights(cfg, seed=1234, types=None):
+    """(gpu_slots, oracle_weights): the same seeded bytes for both sides.
+    types: {(slot, layer): GGML type} for matrices that are not Q4_0."""
     from rdlquant import llama as L
     from oracle import oracle as orc
     rng = np.random.default_rng(seed)
     q, kv = cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim
-    slots, ref = [], {}
+    types = types or {}
+    slots, ref = [], {"kinds": {}}
     s = seed
 
-    def q4(n, k):
+    def mat(slot, layer, n, k):
         nonlocal s
         s += 1
-        return synth.q4_0_weights(n, k, s)
+        return synth.weights(types.get((slot, layer), 2), n, k, s)
 
     def norm():
         return (1.0 + 0.1 * rng.standard_normal(cfg.dim)).astype(np.float32)
 
-    emb = q4(cfg.vocab, cfg.dim)
+    emb = mat(L.TOKEN_EMBEDDING, 0, cfg.vocab, cfg.dim)
     slots.append((L.TOKEN_EMBEDDING, 0, emb))
-    ref["emb_f32"] = orc.to_f32("q4_0", emb, cfg.vocab * cfg.dim).reshape(cfg.vocab, cfg.dim)
+    et = types.get((L.TOKEN_EMBEDDING, 0), 2)
+    ref["emb_f32"] = orc.to_f32(DEQ[et], emb, cfg.vocab * cfg.dim).reshape(cfg.vocab, cfg.dim)
     for layer in range(cfg.n_layers):
-        for slot, name, arr in ((L.ATTN_NORM, "attn_norm", norm()), (L.WQ, "wq", q4(q, cfg.dim)),
-                                (L.WK, "wk", q4(kv, cfg.dim)), (L.WV, "wv", q4(kv, cfg.dim)),
-                                (L.WO, "wo", q4(cfg.dim, q)), (L.FFN_NORM, "ffn_norm", norm()),
-                                (L.W_GATE, "w_gate", q4(cfg.ffn_dim, cfg.dim)),
-                                (L.W_UP, "w_up", q4(cfg.ffn_dim, cfg.dim)),
-                                (L.W_DOWN, "w_down", q4(cfg.dim, cfg.ffn_dim))):
+        for slot, name, arr in ((L.ATTN_NORM, "attn_norm", norm()), (L.WQ, "wq", mat(L.WQ, layer, q, cfg.dim)),
+                                (L.WK, "wk", mat(L.WK, layer, kv, cfg.dim)),
+                                (L.WV, "wv", mat(L.WV, layer, kv, cfg.dim)),
+                                (L.WO, "wo", mat(L.WO, layer, cfg.dim, q)), (L.FFN_NORM, "ffn_norm", norm()),
+                                (L.W_GATE, "w_gate", mat(L.W_GATE, layer, cfg.ffn_dim, cfg.dim)),
+                                (L.W_UP, "w_up", mat(L.W_UP, layer, cfg.ffn_dim, cfg.dim)),
+                                (L.W_DOWN, "w_down", mat(L.W_DOWN, layer, cfg.dim, cfg.ffn_dim))):
             slots.append((slot, layer, arr))
             ref[(name, layer)] = arr
+            if (slot, layer) in types:
+                ref["kinds"][(name, layer)] = KIND[types[(slot, layer)]]
     s += 1
-    out = synth.weights(cfg.output_dtype, cfg.vocab, cfg.dim, s)
+    ot = types.get((L.OUTPUT, 0), cfg.output_dtype)
+    out = synth.weights(ot, cfg.vocab, cfg.dim, s)
     fin = norm()
     slots += [(L.FINAL_NORM, 0, fin), (L.OUTPUT, 0, out)]
     ref["final_norm"], ref["output"] = fin, out
-    ref["output_kind"] = {2: "q4", 3: "q4_1", 8: "q8", 12: "q4k", 14: "q6k"}[cfg.output_dtype]
+    ref["output_kind"] = KIND[ot]
     return slots, ref
+
+
+def gguf_types(types):
+    """{(slot, layer): GGML type} -> {GGUF tensor name: GGML type}."""
+    return {gguf_name(sl, la): t for (sl, la), t in (types or {}).items()}
 
 
 def gguf_name(slot, layer):

@@ -451,8 +451,9 @@ def test_loader_rejects_types_shapes_arch(G, W, tmp_path, rq):
             b.add_tensor_data(n, dims, tt, np.zeros(W.tensor_nbytes(dims, tt), np.uint8))
         return b
 
-    e = _load_error(G, W, tmp_path, with_type("blk.0.ffn_down.weight", W.GGML_Q8_0))
-    assert isinstance(e, rq.DeviceError) and "blk.0.ffn_down.weight" in str(e) and "Q8_0" in str(e)
+    # matrices may be Q4_0, Q8_0, Q4_1, Q4_K or Q6_K; Q5_K is not resident
+    e = _load_error(G, W, tmp_path, with_type("blk.0.ffn_down.weight", W.GGML_Q5_K))
+    assert isinstance(e, rq.DeviceError) and "blk.0.ffn_down.weight" in str(e) and "Q5K" in str(e)
     e = _load_error(G, W, tmp_path, with_type("output_norm.weight", W.GGML_Q4_0))
     assert "output_norm.weight" in str(e)
     # dims that disagree with the config

@@ -176,3 +176,22 @@ def test_q6_k_output_from_gguf(rq, gpu, tmp_path):
     prompt = [4, 40, 44, 144]
     got, want = run(m, prompt, 7), run(from_slots(cfg, slots), prompt, 7)
     assert np.array_equal(got[0], want[0]) and np.array_equal(got[1], want[1])
+
+
+def test_mixed_type_file(rq, gpu, tmp_path):
+    """A file mixing GGUF types per tensor (as llama.cpp's Q4_K_M files do)."""
+    from llama_fixtures import gguf_types
+    from rdlquant.llama import LlamaModel
+    from test_gpu_llama import mixed_types
+    cfg = tiny_config(n_layers=3, output_dtype=8)
+    types = mixed_types()
+    slots, _ = tiny_weights(cfg, seed=82, types=types)
+    p = tmp_path / "mixed.gguf"
+    write_gguf(p, cfg, slots, types=gguf_types(types))
+    m = LlamaModel.from_gguf(str(p), max_batch=cfg.max_batch, kv_f16=False)
+    ref = LlamaModel(cfg, types=types)
+    for slot, layer, arr in slots:
+        ref.set_weight(slot, layer, arr)
+    prompt = [7, 77, 177, 277, 17]
+    got, want = run(m, prompt, 7), run(ref, prompt, 7)
+    assert np.array_equal(got[0], want[0]) and np.array_equal(got[1], want[1])

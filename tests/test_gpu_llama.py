@@ -200,3 +200,66 @@ def test_output_matrix_types(rq, gpu, out_dtype):
     assert list(toks) == eager
     with pytest.raises(rq.DeviceError):
         m.init_random(1)
+
+
+def mixed_types():
+    """Layer 0 all Q4_0 (fused launches); layer 1 as llama.cpp's Q4_K_M mixes
+    (q, k Q4_K, v Q6_K: split q/k/v; gate Q4_K, up Q6_K: split gate/up; o
+    Q8_0; down Q6_K); layer 2 non-Q4_0 but combined (q/k/v Q8_0, gate/up
+    Q4_1, down Q4_K); a Q6_K embedding table and a Q8_0 output matrix."""
+    import rdlquant.llama as L
+    t = {(L.TOKEN_EMBEDDING, 0): 14, (L.OUTPUT, 0): 8}
+    t.update({(L.WQ, 1): 12, (L.WK, 1): 12, (L.WV, 1): 14, (L.WO, 1): 8, (L.W_GATE, 1): 12, (L.W_UP, 1): 14,
+              (L.W_DOWN, 1): 14})
+    t.update({(L.WQ, 2): 8, (L.WK, 2): 8, (L.WV, 2): 8, (L.W_GATE, 2): 3, (L.W_UP, 2): 3, (L.W_DOWN, 2): 12})
+    return t
+
+
+def build_typed(cfg, types, seed):
+    from rdlquant.llama import LlamaModel
+    slots, ref_w = tiny_weights(cfg, seed, types=types)
+    m = LlamaModel(cfg, types=types)
+    for slot, layer, arr in slots:
+        m.set_weight(slot, layer, arr)
+    return m, LlamaRef(cfg, ref_w), slots
+
+
+@pytest.mark.parametrize("kv_f16", [False, True])
+def test_mixed_type_layers(rq, gpu, kv_f16):
+    """Fused and per-type layers in one model: prefill (the GEMM and the
+    records paths), decode steps and greedy generation against the oracle."""
+    cfg = tiny_config(n_layers=3, kv_f16=kv_f16, output_dtype=8)
+    m, ref, _ = build_typed(cfg, mixed_types(), 99)
+    prompt = [3, 141, 59, 26, 53, 58, 97, 93, 23]
+    if kv_f16:  # f16 cache: within 1e-2 of the largest logit
+        got, want = m.forward_with_cache(prompt), ref.forward_with_cache(prompt)
+        assert np.max(np.abs(got - want)) <= 1e-2 * np.max(np.abs(want))
+        return
+    assert_close(m.forward_with_cache(prompt), ref.forward_with_cache(prompt))
+    tok = 11
+    for _ in range(4):
+        got = m.decode_step(tok)
+        want = ref.forward_with_cache([tok])
+        assert_close(got, want)
+        tok = argmax(want)
+    m.reset()
+    toks = m.generate_greedy(prompt, 6)
+    m.reset()
+    eager = [argmax(m.forward_with_cache(prompt))]
+    for _ in range(5):
+        eager.append(argmax(m.forward_with_cache([eager[-1]])))
+    assert list(toks) == eager
+
+
+def test_typed_create_rejects(rq, gpu):
+    import rdlquant.llama as L
+    from rdlquant.llama import LlamaModel
+    cfg = tiny_config(ffn_dim=288)
+    with pytest.raises(rq.DeviceError) as e:  # K-quant down over ffn 288
+        LlamaModel(cfg, types={(L.W_DOWN, 0): 12})
+    assert "256" in str(e.value)
+    with pytest.raises(rq.DeviceError):
+        LlamaModel(tiny_config(), types={(L.WQ, 1): 13})  # Q5_K is not resident
+    m = LlamaModel(tiny_config(), types={(L.WO, 0): 8})
+    with pytest.raises(rq.DeviceError):
+        m.init_random(1)
