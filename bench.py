@@ -375,6 +375,81 @@ def decode_line(rig, reps=2):
     }
 
 
+def q4_k_m_types(n_layers):
+    """{(slot, layer): GGML type} of llama.cpp's Q4_K_M recipe for a Llama
+    model: Q4_K everywhere except Q6_K for the output matrix and for attn_v /
+    ffn_down in the first and last eighth of the layers and every third one
+    between them."""
+    import rdlquant.llama as L
+    t = {(L.TOKEN_EMBEDDING, 0): 12, (L.OUTPUT, 0): 14}
+    for i in range(n_layers):
+        more = i < n_layers // 8 or i >= 7 * n_layers // 8 or (i - n_layers // 8) % 3 == 2
+        for slot in (L.WQ, L.WK, L.WO, L.W_GATE, L.W_UP):
+            t[(slot, i)] = 12
+        t[(L.WV, i)] = 14 if more else 12
+        t[(L.W_DOWN, i)] = 14 if more else 12
+    return t
+
+
+def decode_q4_k_m_line(rig, reps=2):
+    """Not a BASELINE config: the config-5 model shape with llama.cpp's Q4_K_M
+    type mix (Q4_K layers, Q6_K attn_v / ffn_down in 18 of 32 layers, Q4_K
+    embedding, Q6_K output), synthetic weights (one seeded matrix per shape
+    and type, repeated over the layers), greedy decode as config 5."""
+    import numpy as np
+
+    import rdlquant.llama as L
+    from rdlquant.llama import LlamaConfig, LlamaModel
+
+    cfg = LlamaConfig()
+    types = q4_k_m_types(cfg.n_layers)
+    model = LlamaModel(cfg, types=types)
+    q, kv = cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim
+    shape = {L.TOKEN_EMBEDDING: (cfg.vocab, cfg.dim), L.OUTPUT: (cfg.vocab, cfg.dim), L.WQ: (q, cfg.dim),
+             L.WK: (kv, cfg.dim), L.WV: (kv, cfg.dim), L.WO: (cfg.dim, q), L.W_GATE: (cfg.ffn_dim, cfg.dim),
+             L.W_UP: (cfg.ffn_dim, cfg.dim), L.W_DOWN: (cfg.dim, cfg.ffn_dim)}
+    cache = {}
+    nbytes = 0
+    for (slot, layer), t in sorted(types.items(), key=lambda kv_: (kv_[0][1], kv_[0][0])):
+        n, k = shape[slot]
+        key = (n, k, t)
+        if key not in cache:
+            cache[key] = rig.synth.weights(t, n, k, LLAMA_SEED + 0x100 + len(cache))
+        model.set_weight(slot, layer, cache[key])
+        if slot != L.TOKEN_EMBEDDING:
+            nbytes += cache[key].size
+    ones = np.ones(cfg.dim, np.float32)
+    for layer in range(cfg.n_layers):
+        model.set_weight(L.ATTN_NORM, layer, ones)
+        model.set_weight(L.FFN_NORM, layer, ones)
+    model.set_weight(L.FINAL_NORM, 0, ones)
+    cache.clear()
+    prompt = np.random.default_rng(LLAMA_SEED).integers(0, cfg.vocab, PROMPT_LEN)
+    runs = []
+    for _ in range(reps + 1):
+        model.reset()
+        model.generate_greedy(prompt, GEN_TOKENS + 1)
+        runs.append(model.last_timing())
+    model.close()
+    rig.torch.cuda.empty_cache()
+    decode_ms = min(r[1] for r in runs[1:])
+    ms_tok = decode_ms / GEN_TOKENS
+    ctx_mean = PROMPT_LEN + (GEN_TOKENS + 1) / 2
+    kvb = cfg.n_layers * 2 * cfg.n_kv_heads * cfg.head_dim * 2
+    bpt = nbytes + cfg.dim * 144 // 256 + int(kvb * ctx_mean)
+    gbps = bpt / (ms_tok * 1e-3) / 1e9
+    return {
+        "workload": "7B Llama shape, llama.cpp Q4_K_M type mix (synthetic weights), f16 KV, 128-token prompt, "
+                    "256 greedy tokens",
+        "value": round(GEN_TOKENS / (decode_ms * 1e-3), 1),
+        "unit": "tokens/s",
+        "ms_per_token": round(ms_tok, 4),
+        "bytes_per_token": bpt,
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                     "frac": round(gbps / PEAK_HBM_GBPS, 4)},
+    }
+
+
 def load_line(rig):
     """A synthetic config-5 (Llama-7B-shape Q4_0) GGUF file written to TMPDIR,
     then loaded into a device-resident decoder (rdl_llama_load_gguf): parse of
@@ -464,9 +539,10 @@ def main():
     ap.add_argument("--copies", type=int, default=24)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--workload", default="all", choices=["all", "gemv", "q8_0", "q4_k", "q6_k", "gemm", "decode", "load"],
+    ap.add_argument("--workload", default="all", choices=["all", "gemv", "q8_0", "q4_k", "q6_k", "gemm", "decode", "decode_q4_k_m", "load"],
                     help="all: the headline line plus configs 1, 3, 4, 5 and the Q6_K lm_head; otherwise only one "
-                         "(load: the GGUF file load, run only when asked)")
+                         "(load: the GGUF file load, decode_q4_k_m: a Q4_K_M-mixed 7B decode; run only "
+                         "when asked)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="first run 3 plain device copies of this many MiB (a known-size "
                          "reference for HBM traffic counters)")
@@ -492,7 +568,7 @@ def main():
         del src, dst
 
     wl = args.workload
-    if wl in ("q8_0", "q4_k", "q6_k", "gemm", "decode", "load"):
+    if wl in ("q8_0", "q4_k", "q6_k", "gemm", "decode", "decode_q4_k_m", "load"):
         if wl == "q8_0":
             line = gemv_line(rig, "config1: Q8_0 GEMV 4096x4096", 8, 4096, 4096, 0x5EED0001,
                              args.steps, args.warmup)
@@ -507,6 +583,8 @@ def main():
             line = gemm_lines(rig, [16, 64, 512, 2048])
         elif wl == "load":
             line = load_line(rig)
+        elif wl == "decode_q4_k_m":
+            line = decode_q4_k_m_line(rig)
         else:
             line = decode_line(rig)
         print(json.dumps(line), flush=True)
