@@ -753,6 +753,92 @@ __global__ __launch_bounds__(NW * 64) void gemv_fused_kernel(const uint8_t* __re
     }
 }
 
+// ---- K-quant decoder fusion -------------------------------------------------------------
+// The Q4_K / Q6_K kernels below take the decoder's RMSNorm as a prologue on
+// x (PRO_RMSNORM) and one of three epilogues: EPI_STORE, EPI_RESIDUAL
+// (y += W x) or EPI_SWIGLU (rows 2j, 2j + 1 are gate j, up j; y_j =
+// silu(gate_j) * up_j).
+struct KqFuse {
+    const float* g;  // RMSNorm weights (PRO_RMSNORM)
+    float eps;
+    int xstride;     // floats between activation rows
+    int ystride;     // floats between output rows
+};
+
+// x pieces as load_prep_x, then (PRO_RMSNORM) the matching pieces of g: both
+// ahead of the weight stream, both covered by wait_prep_x.
+template <int NW, int PI, int PRO>
+__device__ __forceinline__ void load_prep_xg(const float* __restrict__ x, const float* __restrict__ g, int nb,
+                                             f32x4 (&xv)[PI], f32x4 (&gv)[PI]) {
+    load_prep_x<NW, PI>(x, nb, xv);
+    if constexpr (PRO == PRO_RMSNORM) load_prep_x<NW, PI>(g, nb, gv);
+}
+
+// x_j <- (x_j * (1 / sqrt(sum(x^2) / K + eps))) * g_j (ops.rs:688-751) on the
+// pieces of load_prep_x, the sum formed by the workgroup in a fixed order.
+// `red` holds NW floats of LDS that nothing else uses until the next barrier.
+template <int NW, int PI>
+__device__ void rmsnorm_pieces(f32x4 (&xv)[PI], const f32x4 (&gv)[PI], float eps, int nb, float* red) {
+    constexpr int NT = NW * 64;
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < PI; j++) {
+        if ((int)threadIdx.x + j * NT < nb * 8) {  // clamped duplicates past the row count once
+            const f32x4 a = xv[j];
+            ss += (a.x * a.x + a.y * a.y) + (a.z * a.z + a.w * a.w);
+        }
+    }
+    ss = sum8_f32(ss);
+    ss += dpp_f32<DPP_ROW_MIRROR>(ss);
+    ss += __shfl_xor(ss, 16);
+    ss += __shfl_xor(ss, 32);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; w++) tot += red[w];
+    const float inv = 1.0f / sqrtf(tot / (float)(nb * 32) + eps);
+#pragma unroll
+    for (int j = 0; j < PI; j++) {
+        xv[j].x = (xv[j].x * inv) * gv[j].x;
+        xv[j].y = (xv[j].y * inv) * gv[j].y;
+        xv[j].z = (xv[j].z * inv) * gv[j].z;
+        xv[j].w = (xv[j].w * inv) * gv[j].w;
+    }
+}
+
+// silu(gate) * up as the fused Q4_0 epilogue forms it (feed_forward.rs:138-150)
+__device__ __forceinline__ float swiglu1(float gate, float up) {
+    return (gate * (1.0f / (1.0f + expf(-gate)))) * up;
+}
+
+// Final store of the split-K kernels: rb[k * RPW + i] holds slice k's sum of
+// local row i of the rows from r0.
+template <int KS, int RPW, int NW, int EPI>
+__device__ __forceinline__ void store_slices(const float* rb, int r0, int n, float* __restrict__ y) {
+    if constexpr (EPI == EPI_SWIGLU) {
+        for (int i = threadIdx.x; i < RPW / 2; i += NW * 64) {
+            float t0 = rb[2 * i], t1 = rb[2 * i + 1];
+#pragma unroll
+            for (int k = 1; k < KS; k++) {
+                t0 += rb[k * RPW + 2 * i];
+                t1 += rb[k * RPW + 2 * i + 1];
+            }
+            if (r0 + 2 * i + 1 < n) y[(r0 >> 1) + i] = swiglu1(t0, t1);
+        }
+    } else {
+        for (int i = threadIdx.x; i < RPW; i += NW * 64) {
+            float t = rb[i];
+#pragma unroll
+            for (int k = 1; k < KS; k++) t += rb[k * RPW + i];
+            if (r0 + i < n) {
+                if constexpr (EPI == EPI_RESIDUAL) y[r0 + i] = t + y[r0 + i];
+                else y[r0 + i] = t;
+            }
+        }
+    }
+}
+
 // ---- Q4_K (float mode) ------------------------------------------------------------------
 // A unit is one 32-byte chunk of a super-block's nibbles: sub-block 2c (lo
 // nibbles) and 2c+1 (hi nibbles) of super-block sb (parser.rs:574-589).
@@ -784,25 +870,32 @@ __device__ __forceinline__ void q4k_scale_min(const u32x4& h, int c, int& sc1, i
 constexpr int Q4K_AHEAD = 2;
 
 // Q4_K rows of at most 64 units (K <= 4096): lane u takes unit u of R rows
-// per wave (rows r0 + wv + r * NW); each activation record is read from LDS
-// once for the R rows.
-template <int R, int NW>
+// per wave (rows r0 + wv + r * NW; EPI_SWIGLU: row pairs 2j, 2j + 1 in one
+// wave, pair j = wv + (r / 2) * NW of the workgroup's); each activation record
+// is read from LDS once for the R rows.
+template <int R, int NW, int PRO = PRO_NONE, int EPI = EPI_STORE>
 __global__ __launch_bounds__(NW * 64) void gemv_q4k_fused_kernel(const uint8_t* __restrict__ W, int n,
                                                             int nsb, int rpw,
                                                             const float* __restrict__ X,
-                                                            float* __restrict__ Y) {
+                                                            float* __restrict__ Y, KqFuse fz) {
     extern __shared__ i32x4 lds4[];
+    constexpr bool PAIRS = (EPI == EPI_SWIGLU);
+    static_assert(!PAIRS || R % 2 == 0, "row pairs need an even row count per wave");
     const int lane = threadIdx.x & 63;
     const int wv = threadIdx.x >> 6;
     const int r0 = blockIdx.x * rpw;
     const int rend = min(n, r0 + rpw);
     const int nb = nsb * 8, nunits = nsb * 4;
-    const float* x = X + (size_t)blockIdx.y * nb * 32;
-    float* y = Y + (size_t)blockIdx.y * n;
+    const float* x = X + (size_t)blockIdx.y * fz.xstride;
+    float* y = Y + (size_t)blockIdx.y * fz.ystride;
     const uint32_t row_bytes = (uint32_t)nsb * Q4_K_BYTES;
     constexpr int PI = (16 + NW - 1) / NW;  // nb * 8 = 16 * units <= 1024 float4 pieces
-    f32x4 xv[PI];
-    load_prep_x<NW, PI>(x, nb, xv);
+    f32x4 xv[PI], gv[PI];
+    load_prep_xg<NW, PI, PRO>(x, fz.g, nb, xv, gv);
+    auto row_of = [&](int r) {
+        if constexpr (PAIRS) return r0 + 2 * (wv + (r >> 1) * NW) + (r & 1);
+        return r0 + wv + r * NW;
+    };
 
     // rows issued Q4K_AHEAD at a time, as in gemv_q4k_splitk_kernel
     const int u = lane;
@@ -810,7 +903,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_q4k_fused_kernel(const uint8_t* 
     u32x4 hdr[R], qa[R], qb[R];
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(W, (uint32_t)n * row_bytes);
     auto issue = [&](int r) {
-        const int row = r0 + wv + r * NW;
+        const int row = row_of(r);
         const uint32_t off =
             (row < rend && uok) ? (uint32_t)row * row_bytes + (uint32_t)(u >> 2) * Q4_K_BYTES : RSRC_OOB;
         const uint32_t q = off + 16 + 32 * (u & 3);
@@ -823,9 +916,13 @@ __global__ __launch_bounds__(NW * 64) void gemv_q4k_fused_kernel(const uint8_t* 
     for (int r = 0; r < P0; r++) issue(r);
     wait_prep_x<P0 * 3>();  // header + two 16-byte nibble loads per row
     after_wait<PI>(xv);
+    if constexpr (PRO == PRO_RMSNORM) {
+        after_wait<PI>(gv);
+        rmsnorm_pieces<NW, PI>(xv, gv, fz.eps, nb, reinterpret_cast<float*>(lds4) + nb * 32);
+    }
     prep_float_lds<NW, PI>(xv, nb, reinterpret_cast<int*>(lds4));
     __syncthreads();
-    if (r0 + wv >= rend) return;
+    if (row_of(0) >= rend) return;  // wave-uniform; the wave has no rows
 
     float acc[R];
 #pragma unroll
@@ -867,9 +964,19 @@ __global__ __launch_bounds__(NW * 64) void gemv_q4k_fused_kernel(const uint8_t* 
     // rows past rend hold 0 (their loads read zeros); they are not stored
     const float s = wave_reduce_rows<R>(acc);
     constexpr int SH = reduce_span_log2<R>();
-    if ((lane & ((1 << SH) - 1)) == 0) {
-        const int row = r0 + wv + (lane >> SH) * NW;
-        if (row < rend) y[row] = s;
+    if constexpr (PAIRS) {
+        // gate (row r, even) and up (row r + 1) sit in adjacent lane groups
+        const float up = __shfl_down(s, 1 << SH);
+        if ((lane & ((2 << SH) - 1)) == 0) {
+            const int g = row_of(lane >> SH);
+            if (g + 1 < rend) y[g >> 1] = swiglu1(s, up);
+        }
+    } else if ((lane & ((1 << SH) - 1)) == 0) {
+        const int row = row_of(lane >> SH);
+        if (row < rend) {
+            if constexpr (EPI == EPI_RESIDUAL) y[row] = s + y[row];
+            else y[row] = s;
+        }
     }
 }
 
@@ -879,10 +986,10 @@ __global__ __launch_bounds__(NW * 64) void gemv_q4k_fused_kernel(const uint8_t* 
 // (units ks * ups .. + ups - 1, one per lane, ups <= 64) of rows
 // r0 + rg + r * RG, rg = w / KS, r < R; the KS slice sums of a row are added
 // in a fixed order at the end, through LDS.
-template <int R, int KS, int NW>
+template <int R, int KS, int NW, int PRO = PRO_NONE, int EPI = EPI_STORE>
 __global__ __launch_bounds__(NW * 64) void gemv_q4k_splitk_kernel(const uint8_t* __restrict__ W, int n, int nsb,
                                                                   int ups, const float* __restrict__ X,
-                                                                  float* __restrict__ Y) {
+                                                                  float* __restrict__ Y, KqFuse fz) {
     static_assert(NW % KS == 0, "slices per workgroup");
     constexpr int RG = NW / KS;  // row groups
     constexpr int RPW = RG * R;  // rows per workgroup
@@ -893,12 +1000,12 @@ __global__ __launch_bounds__(NW * 64) void gemv_q4k_splitk_kernel(const uint8_t*
     const int r0 = blockIdx.x * RPW;
     const int rend = min(n, r0 + RPW);
     const int nb = nsb * 8, nunits = nsb * 4;
-    const float* x = X + (size_t)blockIdx.y * nb * 32;
-    float* y = Y + (size_t)blockIdx.y * n;
+    const float* x = X + (size_t)blockIdx.y * fz.xstride;
+    float* y = Y + (size_t)blockIdx.y * fz.ystride;
     const uint32_t row_bytes = (uint32_t)nsb * Q4_K_BYTES;
     constexpr int PI = (KS * 16 + NW - 1) / NW;  // nb * 8 = 16 * units <= 1024 * KS float4 pieces
-    f32x4 xv[PI];
-    load_prep_x<NW, PI>(x, nb, xv);
+    f32x4 xv[PI], gv[PI];
+    load_prep_xg<NW, PI, PRO>(x, fz.g, nb, xv, gv);
 
     const int u = ks * ups + lane;
     const bool uok = lane < ups && u < nunits;
@@ -922,6 +1029,10 @@ __global__ __launch_bounds__(NW * 64) void gemv_q4k_splitk_kernel(const uint8_t*
     for (int r = 0; r < P0; r++) issue(r);
     wait_prep_x<P0 * 3>();  // header + two 16-byte nibble loads per row
     after_wait<PI>(xv);
+    if constexpr (PRO == PRO_RMSNORM) {
+        after_wait<PI>(gv);
+        rmsnorm_pieces<NW, PI>(xv, gv, fz.eps, nb, reinterpret_cast<float*>(lds4) + nb * 32);
+    }
     prep_float_lds<NW, PI>(xv, nb, reinterpret_cast<int*>(lds4));
     __syncthreads();
 
@@ -972,12 +1083,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_q4k_splitk_kernel(const uint8_t*
     __syncthreads();
     if ((lane & ((1 << SH) - 1)) == 0) red[ks * RPW + rg + (lane >> SH) * RG] = s;
     __syncthreads();
-    for (int i = threadIdx.x; i < RPW; i += NW * 64) {
-        float t = red[i];
-#pragma unroll
-        for (int k = 1; k < KS; k++) t += red[k * RPW + i];
-        if (r0 + i < rend) y[r0 + i] = t;
-    }
+    store_slices<KS, RPW, NW, EPI>(red, r0, n, y);
 }
 
 // ---- Q6_K (float mode) ------------------------------------------------------------------
@@ -992,10 +1098,10 @@ __global__ __launch_bounds__(NW * 64) void gemv_q4k_splitk_kernel(const uint8_t*
 // group).
 constexpr int Q6K_AHEAD = 2;  // rows whose loads are in flight ahead of the arithmetic
 
-template <int R, int KS, int NW>
+template <int R, int KS, int NW, int PRO = PRO_NONE, int EPI = EPI_STORE>
 __global__ __launch_bounds__(NW * 64) void gemv_q6k_splitk_kernel(const uint8_t* __restrict__ W, int n, int nsb,
                                                                   int ups, const float* __restrict__ X,
-                                                                  float* __restrict__ Y) {
+                                                                  float* __restrict__ Y, KqFuse fz) {
     static_assert(NW % KS == 0, "slices per workgroup");
     constexpr int RG = NW / KS;  // waves per slice
     constexpr int RPW = RG * R;  // rows per group
@@ -1005,12 +1111,12 @@ __global__ __launch_bounds__(NW * 64) void gemv_q6k_splitk_kernel(const uint8_t*
     const int ks = wv % KS, rg = wv / KS;
     const int ngroups = (n + RPW - 1) / RPW;
     const int nb = nsb * 8;  // units = 32-element columns
-    const float* x = X + (size_t)blockIdx.y * nb * 32;
-    float* y = Y + (size_t)blockIdx.y * n;
+    const float* x = X + (size_t)blockIdx.y * fz.xstride;
+    float* y = Y + (size_t)blockIdx.y * fz.ystride;
     const uint32_t row_bytes = (uint32_t)nsb * Q6_K_BYTES;
     constexpr int PI = (KS * 8 + NW - 1) / NW;  // nb * 8 <= 512 * KS float4 pieces
-    f32x4 xv[PI];
-    load_prep_x<NW, PI>(x, nb, xv);
+    f32x4 xv[PI], gv[PI];
+    load_prep_xg<NW, PI, PRO>(x, fz.g, nb, xv, gv);
 
     const int u = ks * ups + lane;
     const bool uok = lane < ups && u < nb;
@@ -1044,6 +1150,10 @@ __global__ __launch_bounds__(NW * 64) void gemv_q6k_splitk_kernel(const uint8_t*
     for (int r = 0; r < P0; r++) issue(grp, r);
     wait_prep_x<P0 * 8>();  // eight weight loads per row
     after_wait<PI>(xv);
+    if constexpr (PRO == PRO_RMSNORM) {
+        after_wait<PI>(gv);
+        rmsnorm_pieces<NW, PI>(xv, gv, fz.eps, nb, reinterpret_cast<float*>(lds4) + nb * 32);
+    }
     prep_float_lds<NW, PI>(xv, nb, reinterpret_cast<int*>(lds4));
     __syncthreads();
 
@@ -1088,13 +1198,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_q6k_splitk_kernel(const uint8_t*
         float* rb = red + it * (KS * RPW);
         if ((lane & ((1 << SH) - 1)) == 0) rb[ks * RPW + rg + (lane >> SH) * RG] = sum;
         __syncthreads();  // (the other buffer was last read before this barrier)
-        const int r0 = grp * RPW;
-        for (int i = threadIdx.x; i < RPW; i += NW * 64) {
-            float t = rb[i];
-#pragma unroll
-            for (int k = 1; k < KS; k++) t += rb[k * RPW + i];
-            if (r0 + i < n) y[r0 + i] = t;
-        }
+        store_slices<KS, RPW, NW, EPI>(rb, grp * RPW, n, y);
     }
 }
 
@@ -1201,39 +1305,65 @@ void launch_cpl(const uint8_t* w, int n, int nb, const float* x, size_t m, float
 
 // Rows of more than 64 units (K > 4096): K split over 2 or 4 waves of a
 // 16-wave workgroup, 4 rows per wave (gemv_q4k_splitk_kernel).
-template <int KS>
+template <int KS, int PRO, int EPI>
 void launch_q4k_splitk(const uint8_t* w, int n, int nsb, const float* x, size_t m, float* y, hipStream_t s,
-                       size_t lds) {
+                       size_t lds, const KqFuse& fz) {
     constexpr int NW = 16, R = 4, RPW = NW / KS * R;
     const int units = nsb * 4, ups = (units + KS - 1) / KS;
     const dim3 grid((unsigned)((n + RPW - 1) / RPW), (unsigned)m), block(NW * 64);
-    launch_kernel((gemv_q4k_splitk_kernel<R, KS, NW>), grid, block, lds, s, w, n, nsb, ups, x, y);
+    launch_kernel((gemv_q4k_splitk_kernel<R, KS, NW, PRO, EPI>), grid, block, lds, s, w, n, nsb, ups, x, y, fz);
 }
 
-template <int NW>
+template <int NW, int PRO, int EPI>
 void launch_q4k_nw(const uint8_t* w, int n, int nsb, const float* x, size_t m, float* y,
-                   hipStream_t s, size_t lds, int wg_per_cu) {
+                   hipStream_t s, size_t lds, int wg_per_cu, const KqFuse& fz) {
     const int units = nsb * 4;
     if (units > 64) {  // units <= 256 (K <= 16384)
-        if (units <= 128) launch_q4k_splitk<2>(w, n, nsb, x, m, y, s, lds);
-        else launch_q4k_splitk<4>(w, n, nsb, x, m, y, s, lds);
+        if (units <= 128) launch_q4k_splitk<2, PRO, EPI>(w, n, nsb, x, m, y, s, lds, fz);
+        else launch_q4k_splitk<4, PRO, EPI>(w, n, nsb, x, m, y, s, lds, fz);
         return;
     }
-    const Cfg c = pick_cfg(n, NW, 4, wg_per_cu);
+    Cfg c = pick_cfg(n, NW, 4, wg_per_cu);
+    if constexpr (EPI == EPI_SWIGLU) {
+        // whole row pairs per wave: R even, a workgroup takes NW * R rows
+        c.r = c.r <= 2 ? 2 : 4;
+        c.rpw = NW * c.r;
+    }
     const dim3 grid((unsigned)((n + c.rpw - 1) / c.rpw), (unsigned)m), block(NW * 64);
     switch (c.r) {
-        case 1: launch_kernel((gemv_q4k_fused_kernel<1, NW>), grid, block, lds, s, w, n, nsb, c.rpw, x, y); break;
-        case 2: launch_kernel((gemv_q4k_fused_kernel<2, NW>), grid, block, lds, s, w, n, nsb, c.rpw, x, y); break;
-        case 3: launch_kernel((gemv_q4k_fused_kernel<3, NW>), grid, block, lds, s, w, n, nsb, c.rpw, x, y); break;
-        default: launch_kernel((gemv_q4k_fused_kernel<4, NW>), grid, block, lds, s, w, n, nsb, c.rpw, x, y); break;
+        case 1:
+            if constexpr (EPI != EPI_SWIGLU) {
+                launch_kernel((gemv_q4k_fused_kernel<1, NW, PRO, EPI>), grid, block, lds, s, w, n, nsb, c.rpw, x, y, fz);
+                break;
+            }
+            [[fallthrough]];
+        case 2: launch_kernel((gemv_q4k_fused_kernel<2, NW, PRO, EPI>), grid, block, lds, s, w, n, nsb, c.rpw, x, y, fz); break;
+        case 3:
+            if constexpr (EPI != EPI_SWIGLU) {
+                launch_kernel((gemv_q4k_fused_kernel<3, NW, PRO, EPI>), grid, block, lds, s, w, n, nsb, c.rpw, x, y, fz);
+                break;
+            }
+            [[fallthrough]];
+        default: launch_kernel((gemv_q4k_fused_kernel<4, NW, PRO, EPI>), grid, block, lds, s, w, n, nsb, c.rpw, x, y, fz); break;
     }
+}
+
+template <int PRO, int EPI>
+void launch_q4k(const uint8_t* w, int n, int nsb, const float* x, size_t m, float* y, hipStream_t s, size_t lds,
+                const KqFuse& fz) {
+    // up to 64 units per row (K <= 4096): rows spread over 8-wave
+    // workgroups, two per CU; longer rows: one 16-wave workgroup per CU
+    if (nsb * 4 <= 64)
+        launch_q4k_nw<8, PRO, EPI>(w, n, nsb, x, m, y, s, lds, 2, fz);
+    else
+        launch_q4k_nw<16, PRO, EPI>(w, n, nsb, x, m, y, s, lds, 1, fz);
 }
 
 // Q6_K: 16-wave workgroups, K split over KS = 1, 2, 4 or 8 waves (at most 64
 // units a wave), one workgroup per CU walking the row groups.
-template <int KS, int R>
+template <int KS, int R, int PRO, int EPI>
 void launch_q6k_ks_r(const uint8_t* w, int n, int nsb, const float* x, size_t m, float* y, hipStream_t s,
-                     size_t lds) {
+                     size_t lds, const KqFuse& fz) {
     constexpr int NW = 16, RPW = NW / KS * R;
     const int units = nsb * 8, ups = (units + KS - 1) / KS;
     // one workgroup per CU, each walking its share of the row groups
@@ -1241,23 +1371,32 @@ void launch_q6k_ks_r(const uint8_t* w, int n, int nsb, const float* x, size_t m,
     const int wgs = groups < num_cus() ? groups : num_cus();
     const dim3 grid((unsigned)wgs, (unsigned)m), block(NW * 64);
     lds += (size_t)2 * KS * RPW * sizeof(float);  // slice sums after the records
-    launch_kernel((gemv_q6k_splitk_kernel<R, KS, 16>), grid, block, lds, s, w, n, nsb, ups, x, y);
+    launch_kernel((gemv_q6k_splitk_kernel<R, KS, 16, PRO, EPI>), grid, block, lds, s, w, n, nsb, ups, x, y, fz);
 }
-template <int KS>
+template <int KS, int PRO, int EPI>
 void launch_q6k_ks(const uint8_t* w, int n, int nsb, const float* x, size_t m, float* y, hipStream_t s,
-                   size_t lds) {
+                   size_t lds, const KqFuse& fz) {
     // R rows a wave a group: 4 when every CU gets at least one group of them
     const long rg = 16 / KS;
-    if ((n + rg * 4 - 1) / (rg * 4) >= num_cus()) launch_q6k_ks_r<KS, 4>(w, n, nsb, x, m, y, s, lds);
-    else if ((n + rg * 2 - 1) / (rg * 2) >= num_cus()) launch_q6k_ks_r<KS, 2>(w, n, nsb, x, m, y, s, lds);
-    else launch_q6k_ks_r<KS, 1>(w, n, nsb, x, m, y, s, lds);
+    if ((n + rg * 4 - 1) / (rg * 4) >= num_cus()) launch_q6k_ks_r<KS, 4, PRO, EPI>(w, n, nsb, x, m, y, s, lds, fz);
+    else if ((n + rg * 2 - 1) / (rg * 2) >= num_cus()) launch_q6k_ks_r<KS, 2, PRO, EPI>(w, n, nsb, x, m, y, s, lds, fz);
+    else launch_q6k_ks_r<KS, 1, PRO, EPI>(w, n, nsb, x, m, y, s, lds, fz);
 }
-void launch_q6k(const uint8_t* w, int n, int nsb, const float* x, size_t m, float* y, hipStream_t s, size_t lds) {
+template <int PRO, int EPI>
+void launch_q6k(const uint8_t* w, int n, int nsb, const float* x, size_t m, float* y, hipStream_t s, size_t lds,
+                const KqFuse& fz) {
     const int units = nsb * 8;  // <= 512 (K <= 16384)
-    if (units <= 64) launch_q6k_ks<1>(w, n, nsb, x, m, y, s, lds);
-    else if (units <= 128) launch_q6k_ks<2>(w, n, nsb, x, m, y, s, lds);
-    else if (units <= 256) launch_q6k_ks<4>(w, n, nsb, x, m, y, s, lds);
-    else launch_q6k_ks<8>(w, n, nsb, x, m, y, s, lds);
+    if (units <= 64) launch_q6k_ks<1, PRO, EPI>(w, n, nsb, x, m, y, s, lds, fz);
+    else if (units <= 128) launch_q6k_ks<2, PRO, EPI>(w, n, nsb, x, m, y, s, lds, fz);
+    else if (units <= 256) launch_q6k_ks<4, PRO, EPI>(w, n, nsb, x, m, y, s, lds, fz);
+    else launch_q6k_ks<8, PRO, EPI>(w, n, nsb, x, m, y, s, lds, fz);
+}
+
+template <int PRO, int EPI>
+void launch_kq(WType t, const uint8_t* w, int n, int nsb, const float* x, size_t m, float* y, hipStream_t s,
+               size_t lds, const KqFuse& fz) {
+    if (t == WType::Q6_K) launch_q6k<PRO, EPI>(w, n, nsb, x, m, y, s, lds, fz);
+    else launch_q4k<PRO, EPI>(w, n, nsb, x, m, y, s, lds, fz);
 }
 
 // Decoder fusion: Q4_0 float mode, nb even.  8-wave workgroups, two per CU;
@@ -1369,19 +1508,12 @@ hipError_t launch_gemv_fused(WType t, bool native, const uint8_t* w, size_t n, s
     // one 16-wave workgroup per CU (Q4_0 4096 x 14336: 11.1 -> 9.6 us).
     const bool i4 = !native && (t == WType::Q4_0 || t == WType::Q4_1) && cpl_for(nb) < 8;
     const int nw = i4 ? 8 : 16, wg_per_cu = i4 ? 2 : 1;
-    if (t == WType::Q6_K) {
+    if (t == WType::Q6_K || t == WType::Q4_K) {
         if (native) return hipErrorInvalidValue;
-        launch_q6k(w, ni, (int)(k / QK_K), x, m, y, s, lds);
-        return hipGetLastError();
-    }
-    if (t == WType::Q4_K) {
-        // up to 64 units per row (K <= 4096): rows spread over 8-wave
-        // workgroups, two per CU; longer rows: one 16-wave workgroup per CU
-        const int nsb = (int)(k / QK_K);
-        if (nsb * 4 <= 64)
-            launch_q4k_nw<8>(w, ni, nsb, x, m, y, s, lds, 2);
-        else
-            launch_q4k_nw<16>(w, ni, nsb, x, m, y, s, lds, 1);
+        KqFuse fz{};
+        fz.xstride = (int)k;
+        fz.ystride = ni;
+        launch_kq<PRO_NONE, EPI_STORE>(t, w, ni, (int)(k / QK_K), x, m, y, s, lds, fz);
         return hipGetLastError();
     }
     if (native) {
@@ -1394,6 +1526,37 @@ hipError_t launch_gemv_fused(WType t, bool native, const uint8_t* w, size_t n, s
     } else {
         launch_cpl<(int)WType::Q4_0, false>(w, ni, nb, x, m, y, s, lds, nw, wg_per_cu);
     }
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv_kquant_ex(WType t, const uint8_t* w, size_t n, size_t k, const float* x, size_t xstride,
+                                 size_t m, float* y, size_t ystride, int prologue, const float* g, float eps,
+                                 int epilogue, hipStream_t s) {
+    if (n == 0 || m == 0) return hipSuccess;
+    if ((t != WType::Q4_K && t != WType::Q6_K) || k == 0 || k % QK_K || k > fused_max_k(t) || m > 4 ||
+        ((uintptr_t)x & 15) || (xstride & 3) || xstride < k || xstride > INT32_MAX || ystride > INT32_MAX ||
+        (prologue == PRO_RMSNORM && (g == nullptr || ((uintptr_t)g & 15))) ||
+        (uint64_t)n * (k / QK_K) * block_bytes(t) > FUSED_MAX_WEIGHT_BYTES)
+        return hipErrorInvalidValue;
+    if (epilogue == EPI_SWIGLU ? (n & 1) || ystride < n / 2 : ystride < n) return hipErrorInvalidValue;
+    KqFuse fz{};
+    fz.g = g;
+    fz.eps = eps;
+    fz.xstride = (int)xstride;
+    fz.ystride = (int)ystride;
+    const int ni = (int)n, nsb = (int)(k / QK_K);
+    // records plus the RMSNorm partials (one float a wave) after them
+    const size_t lds = (size_t)8 * 16 * (k / QK) + 16 * sizeof(float);
+    if (prologue == PRO_NONE && epilogue == EPI_STORE)
+        launch_kq<PRO_NONE, EPI_STORE>(t, w, ni, nsb, x, m, y, s, lds, fz);
+    else if (prologue == PRO_RMSNORM && epilogue == EPI_STORE)
+        launch_kq<PRO_RMSNORM, EPI_STORE>(t, w, ni, nsb, x, m, y, s, lds, fz);
+    else if (prologue == PRO_NONE && epilogue == EPI_RESIDUAL)
+        launch_kq<PRO_NONE, EPI_RESIDUAL>(t, w, ni, nsb, x, m, y, s, lds, fz);
+    else if (prologue == PRO_RMSNORM && epilogue == EPI_SWIGLU)
+        launch_kq<PRO_RMSNORM, EPI_SWIGLU>(t, w, ni, nsb, x, m, y, s, lds, fz);
+    else
+        return hipErrorInvalidValue;
     return hipGetLastError();
 }
 

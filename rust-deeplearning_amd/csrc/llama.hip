@@ -637,48 +637,93 @@ struct LlamaModel {
                                          0.0f, 1, stream);
     }
 
-    // One layer with separate norm / add / SwiGLU / RoPE launches around the
-    // GEMVs (any resident type, any row count; m > 4 Q4_0 rows take the GEMM).
+    static bool kquant(const Mat& w) { return w.type == WType::Q4_K || w.type == WType::Q6_K; }
+
+    // y rows (ystride floats apart) = epilogue(W . prologue(x rows)) through the
+    // K-quant decoder fusion, four rows a launch
+    hipError_t kq_linear(const Mat& w, const float* xin, size_t xstride, size_t m, float* y, size_t ystride,
+                         int pro, const float* g, int epi) {
+        for (size_t r = 0; r < m; r += 4) {
+            const size_t mr = (m - r < 4) ? m - r : 4;
+            hipError_t e = launch_gemv_kquant_ex(w.type, w.dev, w.n, w.k, xin + r * xstride, xstride, mr,
+                                                 y + r * ystride, ystride, pro, g, cfg.norm_eps, epi, stream);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
+
+    // One layer of any resident types, any row count (m > 4 Q4_0 rows take the
+    // GEMM).  Q4_K / Q6_K matrices fold the RMSNorm in front of them, the
+    // residual add after o / down and the SwiGLU of combined gate/up rows into
+    // their GEMV launches; the other types run separate norm / add / SwiGLU
+    // launches.  RoPE and the cache write run on their own.
     hipError_t layer_plain(int l, size_t m) {
-        const int d = cfg.dim;
+        const int d = cfg.dim, f = cfg.ffn_dim;
         Layer& L = layers[l];
         hipError_t e;
-        hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)m), dim3(NT), 0, stream, x, L.attn_norm, d, cfg.norm_eps,
-                           xn);
-        if (!L.split_qkv) {
-            if ((e = linear(L.qkv, xn, m, qkv)) != hipSuccess) return e;
-        } else if (m == 1) {  // one row: the parts land in place
-            if ((e = linear(L.q, xn, 1, qkv)) != hipSuccess) return e;
-            if ((e = linear(L.k, xn, 1, qkv + q_dim)) != hipSuccess) return e;
-            if ((e = linear(L.v, xn, 1, qkv + q_dim + kv_dim)) != hipSuccess) return e;
-        } else {  // [m, part] rows, then strided into the [m, qkv_dim] rows
-            const Mat* parts[3] = {&L.q, &L.k, &L.v};
-            const int cols[3] = {0, q_dim, q_dim + kv_dim};
-            for (int i = 0; i < 3; i++) {
-                if ((e = linear(*parts[i], xn, m, part_tmp)) != hipSuccess) return e;
-                const size_t w = (size_t)parts[i]->n * sizeof(float);
-                if ((e = hipMemcpy2DAsync(qkv + cols[i], (size_t)qkv_dim * sizeof(float), part_tmp, w, w, m,
-                                          hipMemcpyDeviceToDevice, stream)) != hipSuccess)
-                    return e;
+        auto rmsnorm = [&](const float* g) {
+            hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)m), dim3(NT), 0, stream, x, g, d, cfg.norm_eps, xn);
+        };
+        // ---- q, k, v -> qkv rows ----
+        const Mat* parts[3] = {&L.qkv, nullptr, nullptr};
+        if (L.split_qkv) parts[0] = &L.q, parts[1] = &L.k, parts[2] = &L.v;
+        const int cols[3] = {0, q_dim, q_dim + kv_dim};
+        const int np = L.split_qkv ? 3 : 1;
+        bool want_xn = false;
+        for (int i = 0; i < np; i++) want_xn |= !kquant(*parts[i]);
+        if (want_xn) rmsnorm(L.attn_norm);
+        for (int i = 0; i < np; i++) {
+            const Mat& w = *parts[i];
+            if (kquant(w)) {
+                e = kq_linear(w, x, d, m, qkv + cols[i], qkv_dim, GEMV_PRO_RMSNORM, L.attn_norm, GEMV_EPI_STORE);
+            } else if (np == 1 || m == 1) {  // whole rows, or one row: in place
+                e = linear(w, xn, m, qkv + cols[i]);
+            } else {  // [m, part] rows, then strided into the [m, qkv_dim] rows
+                if ((e = linear(w, xn, m, part_tmp)) != hipSuccess) return e;
+                const size_t wb = (size_t)w.n * sizeof(float);
+                e = hipMemcpy2DAsync(qkv + cols[i], (size_t)qkv_dim * sizeof(float), part_tmp, wb, wb, m,
+                                     hipMemcpyDeviceToDevice, stream);
             }
+            if (e != hipSuccess) return e;
         }
         e = cfg.kv_f16 ? layer_attention<_Float16>(l, m) : layer_attention<float>(l, m);
         if (e != hipSuccess) return e;
-        if ((e = linear(L.o, att, m, xn)) != hipSuccess) return e;
-        hipLaunchKernelGGL(add_kernel, dim3(blocks_for(m * d)), dim3(NT), 0, stream, x, xn, m * d);
-        hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)m), dim3(NT), 0, stream, x, L.ffn_norm, d, cfg.norm_eps,
-                           xn);
-        const size_t nf = m * (size_t)cfg.ffn_dim;
-        if (!L.split_gu) {
-            if ((e = linear(L.gu, xn, m, gu)) != hipSuccess) return e;
-            hipLaunchKernelGGL(swiglu_kernel, dim3(blocks_for(nf)), dim3(NT), 0, stream, gu, cfg.ffn_dim, nf, hb);
+        // ---- x += att . Wo^T ----
+        if (kquant(L.o)) {
+            e = kq_linear(L.o, att, q_dim, m, x, d, GEMV_PRO_NONE, nullptr, GEMV_EPI_RESIDUAL);
+            if (e != hipSuccess) return e;
         } else {
-            if ((e = linear(L.gate, xn, m, gu)) != hipSuccess) return e;
-            if ((e = linear(L.up, xn, m, gu + nf)) != hipSuccess) return e;
+            if ((e = linear(L.o, att, m, xn)) != hipSuccess) return e;
+            hipLaunchKernelGGL(add_kernel, dim3(blocks_for(m * d)), dim3(NT), 0, stream, x, xn, m * d);
+        }
+        // ---- h = silu(gate) * up ----
+        const size_t nf = m * (size_t)f;
+        if (!L.split_gu && kquant(L.gu)) {
+            e = kq_linear(L.gu, x, d, m, hb, f, GEMV_PRO_RMSNORM, L.ffn_norm, GEMV_EPI_SWIGLU);
+            if (e != hipSuccess) return e;
+        } else if (!L.split_gu) {
+            rmsnorm(L.ffn_norm);
+            if ((e = linear(L.gu, xn, m, gu)) != hipSuccess) return e;
+            hipLaunchKernelGGL(swiglu_kernel, dim3(blocks_for(nf)), dim3(NT), 0, stream, gu, f, nf, hb);
+        } else {
+            if (!kquant(L.gate) || !kquant(L.up)) rmsnorm(L.ffn_norm);
+            const Mat* gp[2] = {&L.gate, &L.up};
+            for (int i = 0; i < 2; i++) {
+                float* yo = gu + i * nf;
+                e = kquant(*gp[i]) ? kq_linear(*gp[i], x, d, m, yo, f, GEMV_PRO_RMSNORM, L.ffn_norm, GEMV_EPI_STORE)
+                                   : linear(*gp[i], xn, m, yo);
+                if (e != hipSuccess) return e;
+            }
             hipLaunchKernelGGL(swiglu2_kernel, dim3(blocks_for(nf)), dim3(NT), 0, stream, gu, gu + nf, nf, hb);
         }
-        if ((e = linear(L.down, hb, m, xn)) != hipSuccess) return e;
-        hipLaunchKernelGGL(add_kernel, dim3(blocks_for(m * d)), dim3(NT), 0, stream, x, xn, m * d);
+        // ---- x += h . Wdown^T ----
+        if (kquant(L.down)) {
+            e = kq_linear(L.down, hb, f, m, x, d, GEMV_PRO_NONE, nullptr, GEMV_EPI_RESIDUAL);
+            if (e != hipSuccess) return e;
+        } else {
+            if ((e = linear(L.down, hb, m, xn)) != hipSuccess) return e;
+            hipLaunchKernelGGL(add_kernel, dim3(blocks_for(m * d)), dim3(NT), 0, stream, x, xn, m * d);
+        }
         return hipGetLastError();
     }
 
@@ -699,10 +744,12 @@ struct LlamaModel {
             e = (m <= 4 && layers[l].fused) ? layer_fused(l, m) : layer_plain(l, m);
             if (e != hipSuccess) return e;
         }
-        // logits = rms_norm(x_last, norm) . Wout^T (the norm fused into the GEMV for Q4_0)
+        // logits = rms_norm(x_last, norm) . Wout^T (the norm fused into the GEMV for Q4_0, Q4_K, Q6_K)
         if (fused_shapes && out.type == WType::Q4_0) {
             e = launch_gemv_q4_0_fused_ex(out.dev, out.n, d, x + (m - 1) * d, d, 1, logits, 1, final_norm, eps, 0,
                                           stream);
+        } else if (kquant(out)) {
+            e = kq_linear(out, x + (m - 1) * d, d, 1, logits, out.n, GEMV_PRO_RMSNORM, final_norm, GEMV_EPI_STORE);
         } else {
             hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(NT), 0, stream, x + (m - 1) * d, final_norm, d, eps, xn);
             e = linear(out, xn, 1, logits);

@@ -167,6 +167,18 @@ hipError_t launch_gemv_q4_0_fused_ex(const uint8_t* w, size_t n, size_t k, const
                                      size_t m, float* y, int prologue, const float* g, float eps,
                                      int epilogue, hipStream_t s);
 
+// prologue / epilogue codes of the decoder-fusion launches
+constexpr int GEMV_PRO_NONE = 0, GEMV_PRO_RMSNORM = 1;
+constexpr int GEMV_EPI_STORE = 0, GEMV_EPI_RESIDUAL = 1, GEMV_EPI_SWIGLU = 2;
+
+// Decoder fusion of the Q4_K / Q6_K fused GEMVs (m <= 4, k % 256 == 0, x and
+// g 16-byte aligned, x rows xstride floats apart, y rows ystride): (prologue,
+// epilogue) = (0, 0) y = W x, (1, 0) y = W rms_norm(x, g), (0, 1) y += W x,
+// (1, 2) y[j] = silu(v[2j]) * v[2j+1] with v = W rms_norm(x, g) (n even).
+hipError_t launch_gemv_kquant_ex(WType t, const uint8_t* w, size_t n, size_t k, const float* x, size_t xstride,
+                                 size_t m, float* y, size_t ystride, int prologue, const float* g, float eps,
+                                 int epilogue, hipStream_t s);
+
 // The decoder's q/k/v projection in one launch: y = rms_norm(x, g) . [Wq; Wk; Wv]^T
 // with RoPE at positions *pos + row applied to q (in y) and k, and k, v
 // written into the cache ([n_kv][max_seq][hd], f16 or f32); m <= 4.

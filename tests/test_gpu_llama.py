@@ -251,6 +251,69 @@ def test_mixed_type_layers(rq, gpu, kv_f16):
     assert list(toks) == eager
 
 
+def check_typed_model(m, ref, prompt, tok, steps=4):
+    """Prefill (rows four at a time through the fused GEMVs), decode steps and
+    greedy generation against the oracle's forward."""
+    assert_close(m.forward_with_cache(prompt), ref.forward_with_cache(prompt))
+    for _ in range(steps):
+        got = m.decode_step(tok)
+        want = ref.forward_with_cache([tok])
+        assert_close(got, want)
+        tok = argmax(want)
+    m.reset()
+    toks = m.generate_greedy(prompt, 5)
+    m.reset()
+    eager = [argmax(m.forward_with_cache(prompt))]
+    for _ in range(4):
+        eager.append(argmax(m.forward_with_cache([eager[-1]])))
+    assert list(toks) == eager
+
+
+def test_q4_k_m_layers(rq, gpu):
+    """llama.cpp's Q4_K_M mix: layer 0 with Q6_K attn_v / ffn_down (split q/k/v,
+    RMSNorm in each part's GEMV; gate/up combined Q4_K with the SwiGLU in the
+    GEMV; residual adds in the o / down GEMVs), layer 1 all Q4_K (one q/k/v
+    launch), Q4_K embedding, Q6_K output matrix (final norm in its GEMV)."""
+    import rdlquant.llama as L
+    t = {(L.TOKEN_EMBEDDING, 0): 12, (L.OUTPUT, 0): 14}
+    for layer in range(2):
+        for slot in (L.WQ, L.WK, L.WV, L.WO, L.W_GATE, L.W_UP, L.W_DOWN):
+            t[(slot, layer)] = 12
+    t[(L.WV, 0)] = t[(L.W_DOWN, 0)] = 14
+    cfg = tiny_config(output_dtype=14)
+    m, ref, _ = build_typed(cfg, t, 2024)
+    check_typed_model(m, ref, [5, 17, 33, 2, 250, 7, 91, 64, 8, 1], 31)
+
+
+def test_q6_k_combined_layers(rq, gpu):
+    """Every layer matrix Q6_K: one q/k/v launch with the RMSNorm prologue,
+    gate/up rows combined with the SwiGLU epilogue, residual epilogues, all in
+    the Q6_K kernel; a Q8_0 output matrix behind a separate norm."""
+    import rdlquant.llama as L
+    t = {(L.OUTPUT, 0): 8}
+    for layer in range(2):
+        for slot in (L.WQ, L.WK, L.WV, L.WO, L.W_GATE, L.W_UP, L.W_DOWN):
+            t[(slot, layer)] = 14
+    cfg = tiny_config(output_dtype=8)
+    m, ref, _ = build_typed(cfg, t, 77)
+    check_typed_model(m, ref, [9, 3, 100, 200, 300, 44], 12)
+
+
+def test_wide_k_quant_layers(rq, gpu):
+    """Rows longer than 4096 (dim 4352, ffn 4608): the split-K Q4_K kernel with
+    the RMSNorm prologue and the SwiGLU / residual epilogues (layer 0), the
+    Q6_K kernel split over four waves (layer 1)."""
+    import rdlquant.llama as L
+    t = {(L.TOKEN_EMBEDDING, 0): 12, (L.OUTPUT, 0): 12}
+    for slot in (L.WQ, L.WK, L.WV, L.WO, L.W_GATE, L.W_UP, L.W_DOWN):
+        t[(slot, 0)] = 12
+        t[(slot, 1)] = 14
+    cfg = tiny_config(dim=4352, n_heads=34, n_kv_heads=2, head_dim=128, ffn_dim=4608, vocab=256, max_seq=32,
+                      output_dtype=12)
+    m, ref, _ = build_typed(cfg, t, 4352)
+    check_typed_model(m, ref, [1, 2, 3, 4, 5, 6], 7, steps=2)
+
+
 def test_typed_create_rejects(rq, gpu):
     import rdlquant.llama as L
     from rdlquant.llama import LlamaModel
