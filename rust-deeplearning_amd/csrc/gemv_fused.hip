@@ -881,6 +881,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_q4k_fused_kernel(const uint8_t* 
     extern __shared__ i32x4 lds4[];
     constexpr bool PAIRS = (EPI == EPI_SWIGLU);
     static_assert(!PAIRS || R % 2 == 0, "row pairs need an even row count per wave");
+    static_assert(R >= 1 && R <= 8, "rows per wave");
     const int lane = threadIdx.x & 63;
     const int wv = threadIdx.x >> 6;
     const int r0 = blockIdx.x * rpw;
@@ -897,21 +898,29 @@ __global__ __launch_bounds__(NW * 64) void gemv_q4k_fused_kernel(const uint8_t* 
         return r0 + wv + r * NW;
     };
 
-    // rows issued Q4K_AHEAD at a time, as in gemv_q4k_splitk_kernel
+    // rows issued Q4K_AHEAD at a time, as in gemv_q4k_splitk_kernel, into a
+    // ring of NS load slots (row r in slot r % NS: the slot of row r + P0 is
+    // that of row r - 1, consumed before it is issued).  With more than four
+    // rows the later rows' offsets and each row's finished sum pass through
+    // empty volatile asm statements, which keep their order: row r + P0 is
+    // issued after row r - 1's arithmetic, so that the loads are not all
+    // hoisted to the top (registers).
     const int u = lane;
     const bool uok = u < nunits;
-    u32x4 hdr[R], qa[R], qb[R];
+    constexpr int P0 = R < Q4K_AHEAD ? R : Q4K_AHEAD;
+    constexpr int NS = R < P0 + 1 ? R : P0 + 1;
+    u32x4 hdr[NS], qa[NS], qb[NS];
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(W, (uint32_t)n * row_bytes);
     auto issue = [&](int r) {
         const int row = row_of(r);
-        const uint32_t off =
+        uint32_t off =
             (row < rend && uok) ? (uint32_t)row * row_bytes + (uint32_t)(u >> 2) * Q4_K_BYTES : RSRC_OOB;
+        if (R > 4 && r >= P0) asm volatile("" : "+v"(off));
         const uint32_t q = off + 16 + 32 * (u & 3);
-        hdr[r] = buf_load_b128(rs, off);
-        qa[r] = buf_load_b128(rs, q);
-        qb[r] = buf_load_b128(rs, q + 16);
+        hdr[r % NS] = buf_load_b128(rs, off);
+        qa[r % NS] = buf_load_b128(rs, q);
+        qb[r % NS] = buf_load_b128(rs, q + 16);
     };
-    constexpr int P0 = R < Q4K_AHEAD ? R : Q4K_AHEAD;
 #pragma unroll
     for (int r = 0; r < P0; r++) issue(r);
     wait_prep_x<P0 * 3>();  // header + two 16-byte nibble loads per row
@@ -937,18 +946,19 @@ __global__ __launch_bounds__(NW * 64) void gemv_q4k_fused_kernel(const uint8_t* 
             __builtin_amdgcn_sched_barrier(0);
             // row r's data enter the arithmetic here and not earlier (keeps the
             // compiler from hoisting every row's scale work above the first dot)
-            asm volatile("" : "+v"(hdr[r]), "+v"(qa[r]), "+v"(qb[r]));
-            const uint32_t raw[8] = {qa[r].x, qa[r].y, qa[r].z, qa[r].w, qb[r].x, qb[r].y, qb[r].z, qb[r].w};
+            const int sl = r % NS;
+            asm volatile("" : "+v"(hdr[sl]), "+v"(qa[sl]), "+v"(qb[sl]));
+            const uint32_t raw[8] = {qa[sl].x, qa[sl].y, qa[sl].z, qa[sl].w, qb[sl].x, qb[sl].y, qb[sl].z, qb[sl].w};
             uint32_t lo[8], hi[8];
 #pragma unroll
             for (int k = 0; k < 8; k++) {
                 lo[k] = raw[k] & NIB;
                 hi[k] = (raw[k] >> 4) & NIB;
             }
-            const float d = h2f(hdr[r].x & 0xFFFFu);
-            const float dmin = h2f(hdr[r].x >> 16);
+            const float d = h2f(hdr[sl].x & 0xFFFFu);
+            const float dmin = h2f(hdr[sl].x >> 16);
             int sc1, mn1, sc2, mn2;
-            q4k_scale_min(hdr[r], c, sc1, mn1, sc2, mn2);
+            q4k_scale_min(hdr[sl], c, sc1, mn1, sc2, mn2);
             // element value (d*sc)*q - (dmin*mn)   (parser.rs:577-587)
             const float d1 = d * (float)sc1, m1 = dmin * (float)mn1;
             const float d2 = d * (float)sc2, m2 = dmin * (float)mn2;
@@ -958,25 +968,38 @@ __global__ __launch_bounds__(NW * 64) void gemv_q4k_fused_kernel(const uint8_t* 
             a = fmaf(d2 * x2.S, dot3(hi, x2, 0, 0, 0), a);
             a = fmaf(-m2, x2.xsum, a);
             acc[r] = a;
+            if constexpr (R > 4) asm volatile("" : "+v"(acc[r]));  // row r done before row r + P0 + 1 issues
             __builtin_amdgcn_sched_barrier(0);  // one row at a time, in load order
         }
     }
-    // rows past rend hold 0 (their loads read zeros); they are not stored
-    const float s = wave_reduce_rows<R>(acc);
-    constexpr int SH = reduce_span_log2<R>();
-    if constexpr (PAIRS) {
-        // gate (row r, even) and up (row r + 1) sit in adjacent lane groups
-        const float up = __shfl_down(s, 1 << SH);
-        if ((lane & ((2 << SH) - 1)) == 0) {
-            const int g = row_of(lane >> SH);
-            if (g + 1 < rend) y[g >> 1] = swiglu1(s, up);
+    // rows past rend hold 0 (their loads read zeros); they are not stored.
+    // Rows 0-3 and 4-7 are reduced as two sets (pairs never straddle them).
+    auto store = [&](float s, int sh, int rbase) {
+        if constexpr (PAIRS) {
+            // gate (row r, even) and up (row r + 1) sit in adjacent lane groups
+            const float up = __shfl_down(s, 1 << sh);
+            if ((lane & ((2 << sh) - 1)) == 0) {
+                const int g = row_of(rbase + (lane >> sh));
+                if (g + 1 < rend) y[g >> 1] = swiglu1(s, up);
+            }
+        } else if ((lane & ((1 << sh) - 1)) == 0) {
+            const int row = row_of(rbase + (lane >> sh));
+            if (row < rend) {
+                if constexpr (EPI == EPI_RESIDUAL) y[row] = s + y[row];
+                else y[row] = s;
+            }
         }
-    } else if ((lane & ((1 << SH) - 1)) == 0) {
-        const int row = row_of(lane >> SH);
-        if (row < rend) {
-            if constexpr (EPI == EPI_RESIDUAL) y[row] = s + y[row];
-            else y[row] = s;
-        }
+    };
+    constexpr int R0 = R < 4 ? R : 4;
+    float a0[R0];
+#pragma unroll
+    for (int r = 0; r < R0; r++) a0[r] = acc[r];
+    store(wave_reduce_rows<R0>(a0), reduce_span_log2<R0>(), 0);
+    if constexpr (R > 4) {
+        float a1[R - 4];
+#pragma unroll
+        for (int r = 0; r < R - 4; r++) a1[r] = acc[4 + r];
+        store(wave_reduce_rows<R - 4>(a1), reduce_span_log2<R - 4>(), 4);
     }
 }
 
@@ -1314,49 +1337,53 @@ void launch_q4k_splitk(const uint8_t* w, int n, int nsb, const float* x, size_t 
     launch_kernel((gemv_q4k_splitk_kernel<R, KS, NW, PRO, EPI>), grid, block, lds, s, w, n, nsb, ups, x, y, fz);
 }
 
-template <int NW, int PRO, int EPI>
-void launch_q4k_nw(const uint8_t* w, int n, int nsb, const float* x, size_t m, float* y,
-                   hipStream_t s, size_t lds, int wg_per_cu, const KqFuse& fz) {
-    const int units = nsb * 4;
-    if (units > 64) {  // units <= 256 (K <= 16384)
-        if (units <= 128) launch_q4k_splitk<2, PRO, EPI>(w, n, nsb, x, m, y, s, lds, fz);
-        else launch_q4k_splitk<4, PRO, EPI>(w, n, nsb, x, m, y, s, lds, fz);
-        return;
-    }
-    Cfg c = pick_cfg(n, NW, 4, wg_per_cu);
+template <int R, int PRO, int EPI>
+void launch_q4k_r(const uint8_t* w, int n, int nsb, const float* x, size_t m, float* y, hipStream_t s,
+                  size_t lds, int rpw, const KqFuse& fz) {
+    constexpr int NW = 8;
+    const dim3 grid((unsigned)((n + rpw - 1) / rpw), (unsigned)m), block(NW * 64);
+    launch_kernel((gemv_q4k_fused_kernel<R, NW, PRO, EPI>), grid, block, lds, s, w, n, nsb, rpw, x, y, fz);
+}
+
+// Rows of at most 64 units (K <= 4096): 8-wave workgroups, two per CU, all
+// of them in one round: rows spread evenly, up to 8 a wave (whole row pairs
+// for EPI_SWIGLU).
+template <int PRO, int EPI>
+void launch_q4k_small(const uint8_t* w, int n, int nsb, const float* x, size_t m, float* y, hipStream_t s,
+                      size_t lds, const KqFuse& fz) {
+    constexpr int NW = 8;
+    const int slots = 2 * num_cus();
+    int rpw = (n + slots - 1) / slots;
+    if (EPI == EPI_SWIGLU) rpw += rpw & 1;
+    if (rpw > 8 * NW) rpw = 8 * NW;
+    const int r = (rpw + NW - 1) / NW;
     if constexpr (EPI == EPI_SWIGLU) {
-        // whole row pairs per wave: R even, a workgroup takes NW * R rows
-        c.r = c.r <= 2 ? 2 : 4;
-        c.rpw = NW * c.r;
-    }
-    const dim3 grid((unsigned)((n + c.rpw - 1) / c.rpw), (unsigned)m), block(NW * 64);
-    switch (c.r) {
-        case 1:
-            if constexpr (EPI != EPI_SWIGLU) {
-                launch_kernel((gemv_q4k_fused_kernel<1, NW, PRO, EPI>), grid, block, lds, s, w, n, nsb, c.rpw, x, y, fz);
-                break;
-            }
-            [[fallthrough]];
-        case 2: launch_kernel((gemv_q4k_fused_kernel<2, NW, PRO, EPI>), grid, block, lds, s, w, n, nsb, c.rpw, x, y, fz); break;
-        case 3:
-            if constexpr (EPI != EPI_SWIGLU) {
-                launch_kernel((gemv_q4k_fused_kernel<3, NW, PRO, EPI>), grid, block, lds, s, w, n, nsb, c.rpw, x, y, fz);
-                break;
-            }
-            [[fallthrough]];
-        default: launch_kernel((gemv_q4k_fused_kernel<4, NW, PRO, EPI>), grid, block, lds, s, w, n, nsb, c.rpw, x, y, fz); break;
+        if (r <= 2) launch_q4k_r<2, PRO, EPI>(w, n, nsb, x, m, y, s, lds, rpw, fz);
+        else if (r <= 4) launch_q4k_r<4, PRO, EPI>(w, n, nsb, x, m, y, s, lds, rpw, fz);
+        else if (r <= 6) launch_q4k_r<6, PRO, EPI>(w, n, nsb, x, m, y, s, lds, rpw, fz);
+        else launch_q4k_r<8, PRO, EPI>(w, n, nsb, x, m, y, s, lds, rpw, fz);
+    } else {
+        switch (r) {
+            case 1: launch_q4k_r<1, PRO, EPI>(w, n, nsb, x, m, y, s, lds, rpw, fz); break;
+            case 2: launch_q4k_r<2, PRO, EPI>(w, n, nsb, x, m, y, s, lds, rpw, fz); break;
+            case 3: launch_q4k_r<3, PRO, EPI>(w, n, nsb, x, m, y, s, lds, rpw, fz); break;
+            case 4: launch_q4k_r<4, PRO, EPI>(w, n, nsb, x, m, y, s, lds, rpw, fz); break;
+            case 5: launch_q4k_r<5, PRO, EPI>(w, n, nsb, x, m, y, s, lds, rpw, fz); break;
+            case 6: launch_q4k_r<6, PRO, EPI>(w, n, nsb, x, m, y, s, lds, rpw, fz); break;
+            case 7: launch_q4k_r<7, PRO, EPI>(w, n, nsb, x, m, y, s, lds, rpw, fz); break;
+            default: launch_q4k_r<8, PRO, EPI>(w, n, nsb, x, m, y, s, lds, rpw, fz); break;
+        }
     }
 }
 
 template <int PRO, int EPI>
 void launch_q4k(const uint8_t* w, int n, int nsb, const float* x, size_t m, float* y, hipStream_t s, size_t lds,
                 const KqFuse& fz) {
-    // up to 64 units per row (K <= 4096): rows spread over 8-wave
-    // workgroups, two per CU; longer rows: one 16-wave workgroup per CU
-    if (nsb * 4 <= 64)
-        launch_q4k_nw<8, PRO, EPI>(w, n, nsb, x, m, y, s, lds, 2, fz);
-    else
-        launch_q4k_nw<16, PRO, EPI>(w, n, nsb, x, m, y, s, lds, 1, fz);
+    // longer rows: K split over 2 or 4 waves of a 16-wave workgroup, one per CU
+    const int units = nsb * 4;  // <= 256 (K <= 16384)
+    if (units <= 64) launch_q4k_small<PRO, EPI>(w, n, nsb, x, m, y, s, lds, fz);
+    else if (units <= 128) launch_q4k_splitk<2, PRO, EPI>(w, n, nsb, x, m, y, s, lds, fz);
+    else launch_q4k_splitk<4, PRO, EPI>(w, n, nsb, x, m, y, s, lds, fz);
 }
 
 // Q6_K: 16-wave workgroups, K split over KS = 1, 2, 4 or 8 waves (at most 64

@@ -66,12 +66,17 @@ def test_gemv_float_ragged(rq, orc, gpu, m, n, k, dtype, kind):
     check_parity(fn(x, w, m, k, n), orc.matmul(kind, x, w, m, k, n), exact_f64(orc, kind, x, w, m, k, n))
 
 
-# (1, 10000, 1024) and (2, 9000, 4096) take the 3-rows-per-wave Q4_K kernel on a
-# 256-CU device; (1, 6000, 2048) the 2-row one.  K > 4096 splits K over 2
-# (K <= 8192) or 4 waves of a workgroup: ragged row counts, a last slice
-# shorter than the others (K = 4352, 8448, 16128) and the largest K.
+# K <= 4096 on a 256-CU device spreads the rows over 512 workgroups of 8
+# waves: (1, 6000, 2048) takes 2 rows a wave, (1, 10000, 1024) and
+# (2, 9000, 4096) 3, (1, 17000, 512) 5, (2, 22016, 1024) 6, (1, 26000, 256) 7,
+# (1, 28673, 512) 8 and (1, 40000, 256) 8 with more workgroups than one round.
+# K > 4096 splits K over 2 (K <= 8192) or 4 waves of a workgroup: ragged row
+# counts, a last slice shorter than the others (K = 4352, 8448, 16128) and
+# the largest K.
 @pytest.mark.parametrize("m,n,k", [(1, 1, 256), (2, 5, 512), (1, 33, 1280), (3, 8, 14336),
                                    (1, 10000, 1024), (2, 9000, 4096), (1, 6000, 2048),
+                                   (1, 17000, 512), (2, 22016, 1024), (1, 26000, 256), (1, 28673, 512),
+                                   (1, 40000, 256),
                                    (1, 37, 4352), (2, 100, 8192), (1, 77, 8448), (4, 50, 16128),
                                    (1, 130, 16384), (1, 4096, 14336)])
 def test_gemv_q4k_ragged(rq, orc, gpu, m, n, k):
