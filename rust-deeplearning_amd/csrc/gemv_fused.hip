@@ -763,7 +763,58 @@ struct KqFuse {
     float eps;
     int xstride;     // floats between activation rows
     int ystride;     // floats between output rows
+    // EPI_ROPE_KV (rope.rs:134-200, kv_cache.rs:94-106): the launch's rows are
+    // heads head0, head0 + 1, ... of [q heads | k heads | v heads]
+    const int* pos;  // cache position of activation row 0 is *pos + row0
+    int row0;
+    const float* cos_t;  // [max_seq][hd / 2]
+    const float* sin_t;
+    void* kc;            // [n_kv][max_seq][hd], f16 or f32
+    void* vc;
+    int n_heads, n_kv, hd, max_seq, kv_f16, head0;
 };
+
+// Matrix row of linear row `lin` under the RoPE pairing: linear rows 2p, 2p + 1
+// are the partners (i, i + hd/2) of head p / (hd/2), i = p % (hd/2).
+__device__ __forceinline__ int rope_row(int lin, int hd) {
+    const int half = hd >> 1, pp = lin >> 1;
+    return (pp / half) * hd + pp % half + (lin & 1) * half;
+}
+
+// Partners x1 (matrix row r1) and x2 (row r1 + hd/2) of one activation row:
+// q heads rotated into y, k heads rotated into the key cache, v heads copied
+// into the value cache, at position *pos + row0 + blockIdx.y.
+__device__ __forceinline__ void rope_kv_pair(const KqFuse& fz, int r1, float x1, float x2, float* __restrict__ y) {
+    const int hd = fz.hd, half = hd >> 1;
+    const int head = fz.head0 + r1 / hd, i = r1 % hd;
+    const int pos = *fz.pos + fz.row0 + blockIdx.y;
+    if (head < fz.n_heads + fz.n_kv) {
+        const float c = fz.cos_t[(size_t)pos * half + i], sn = fz.sin_t[(size_t)pos * half + i];
+        const float o1 = x1 * c - x2 * sn, o2 = x1 * sn + x2 * c;
+        if (head < fz.n_heads) {
+            y[r1] = o1;
+            y[r1 + half] = o2;
+        } else {
+            const size_t ko = ((size_t)(head - fz.n_heads) * fz.max_seq + pos) * hd + i;
+            if (fz.kv_f16) {
+                reinterpret_cast<_Float16*>(fz.kc)[ko] = (_Float16)o1;
+                reinterpret_cast<_Float16*>(fz.kc)[ko + half] = (_Float16)o2;
+            } else {
+                reinterpret_cast<float*>(fz.kc)[ko] = o1;
+                reinterpret_cast<float*>(fz.kc)[ko + half] = o2;
+            }
+        }
+    } else {
+        const size_t vo = ((size_t)(head - fz.n_heads - fz.n_kv) * fz.max_seq + pos) * hd + i;
+        if (fz.kv_f16) {
+            reinterpret_cast<_Float16*>(fz.vc)[vo] = (_Float16)x1;
+            reinterpret_cast<_Float16*>(fz.vc)[vo + half] = (_Float16)x2;
+        } else {
+            reinterpret_cast<float*>(fz.vc)[vo] = x1;
+            reinterpret_cast<float*>(fz.vc)[vo + half] = x2;
+        }
+    }
+}
 
 // x pieces as load_prep_x, then (PRO_RMSNORM) the matching pieces of g: both
 // ahead of the weight stream, both covered by wait_prep_x.
@@ -814,9 +865,11 @@ __device__ __forceinline__ float swiglu1(float gate, float up) {
 
 // Final store of the split-K kernels: rb[k * RPW + i] holds slice k's sum of
 // local row i of the rows from r0.
+// Linear rows are matrix rows except under EPI_ROPE_KV (rope_row).
 template <int KS, int RPW, int NW, int EPI>
-__device__ __forceinline__ void store_slices(const float* rb, int r0, int n, float* __restrict__ y) {
-    if constexpr (EPI == EPI_SWIGLU) {
+__device__ __forceinline__ void store_slices(const float* rb, int r0, int n, float* __restrict__ y,
+                                             const KqFuse& fz) {
+    if constexpr (EPI == EPI_SWIGLU || EPI == EPI_ROPE_KV) {
         for (int i = threadIdx.x; i < RPW / 2; i += NW * 64) {
             float t0 = rb[2 * i], t1 = rb[2 * i + 1];
 #pragma unroll
@@ -824,7 +877,10 @@ __device__ __forceinline__ void store_slices(const float* rb, int r0, int n, flo
                 t0 += rb[k * RPW + 2 * i];
                 t1 += rb[k * RPW + 2 * i + 1];
             }
-            if (r0 + 2 * i + 1 < n) y[(r0 >> 1) + i] = swiglu1(t0, t1);
+            if (r0 + 2 * i + 1 < n) {
+                if constexpr (EPI == EPI_SWIGLU) y[(r0 >> 1) + i] = swiglu1(t0, t1);
+                else rope_kv_pair(fz, rope_row(r0 + 2 * i, fz.hd), t0, t1, y);
+            }
         }
     } else {
         for (int i = threadIdx.x; i < RPW; i += NW * 64) {
@@ -879,7 +935,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_q4k_fused_kernel(const uint8_t* 
                                                             const float* __restrict__ X,
                                                             float* __restrict__ Y, KqFuse fz) {
     extern __shared__ i32x4 lds4[];
-    constexpr bool PAIRS = (EPI == EPI_SWIGLU);
+    constexpr bool PAIRS = (EPI == EPI_SWIGLU || EPI == EPI_ROPE_KV);
     static_assert(!PAIRS || R % 2 == 0, "row pairs need an even row count per wave");
     static_assert(R >= 1 && R <= 8, "rows per wave");
     const int lane = threadIdx.x & 63;
@@ -911,10 +967,15 @@ __global__ __launch_bounds__(NW * 64) void gemv_q4k_fused_kernel(const uint8_t* 
     constexpr int NS = R < P0 + 1 ? R : P0 + 1;
     u32x4 hdr[NS], qa[NS], qb[NS];
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(W, (uint32_t)n * row_bytes);
+    auto mat_row = [&](int lin) {
+        if constexpr (EPI == EPI_ROPE_KV) return rope_row(lin, fz.hd);
+        return lin;
+    };
     auto issue = [&](int r) {
         const int row = row_of(r);
-        uint32_t off =
-            (row < rend && uok) ? (uint32_t)row * row_bytes + (uint32_t)(u >> 2) * Q4_K_BYTES : RSRC_OOB;
+        uint32_t off = (row < rend && uok)
+                           ? (uint32_t)mat_row(row) * row_bytes + (uint32_t)(u >> 2) * Q4_K_BYTES
+                           : RSRC_OOB;
         if (R > 4 && r >= P0) asm volatile("" : "+v"(off));
         const uint32_t q = off + 16 + 32 * (u & 3);
         hdr[r % NS] = buf_load_b128(rs, off);
@@ -976,11 +1037,15 @@ __global__ __launch_bounds__(NW * 64) void gemv_q4k_fused_kernel(const uint8_t* 
     // Rows 0-3 and 4-7 are reduced as two sets (pairs never straddle them).
     auto store = [&](float s, int sh, int rbase) {
         if constexpr (PAIRS) {
-            // gate (row r, even) and up (row r + 1) sit in adjacent lane groups
-            const float up = __shfl_down(s, 1 << sh);
+            // rows r (even) and r + 1 (gate and up; RoPE partners) sit in
+            // adjacent lane groups
+            const float s2 = __shfl_down(s, 1 << sh);
             if ((lane & ((2 << sh) - 1)) == 0) {
                 const int g = row_of(rbase + (lane >> sh));
-                if (g + 1 < rend) y[g >> 1] = swiglu1(s, up);
+                if (g + 1 < rend) {
+                    if constexpr (EPI == EPI_SWIGLU) y[g >> 1] = swiglu1(s, s2);
+                    else rope_kv_pair(fz, mat_row(g), s, s2, y);
+                }
             }
         } else if ((lane & ((1 << sh) - 1)) == 0) {
             const int row = row_of(rbase + (lane >> sh));
@@ -1040,8 +1105,9 @@ __global__ __launch_bounds__(NW * 64) void gemv_q4k_splitk_kernel(const uint8_t*
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(W, (uint32_t)n * row_bytes);
     auto issue = [&](int r) {
         const int row = r0 + rg + r * RG;
+        const int mrow = (EPI == EPI_ROPE_KV) ? rope_row(row, fz.hd) : row;
         const uint32_t off =
-            (row < rend && uok) ? (uint32_t)row * row_bytes + (uint32_t)(u >> 2) * Q4_K_BYTES : RSRC_OOB;
+            (row < rend && uok) ? (uint32_t)mrow * row_bytes + (uint32_t)(u >> 2) * Q4_K_BYTES : RSRC_OOB;
         const uint32_t q = off + 16 + 32 * (u & 3);
         hdr[r] = buf_load_b128(rs, off);
         qa[r] = buf_load_b128(rs, q);
@@ -1106,7 +1172,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_q4k_splitk_kernel(const uint8_t*
     __syncthreads();
     if ((lane & ((1 << SH) - 1)) == 0) red[ks * RPW + rg + (lane >> SH) * RG] = s;
     __syncthreads();
-    store_slices<KS, RPW, NW, EPI>(red, r0, n, y);
+    store_slices<KS, RPW, NW, EPI>(red, r0, n, y, fz);
 }
 
 // ---- Q6_K (float mode) ------------------------------------------------------------------
@@ -1149,7 +1215,9 @@ __global__ __launch_bounds__(NW * 64) void gemv_q6k_splitk_kernel(const uint8_t*
     uint32_t l2[R], h2[R], scw[R], dw[R];
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(W, (uint32_t)n * row_bytes);
     auto block_of = [&](int grp, int r) {  // byte offset of the unit's super-block in row r of group grp
-        return (uint32_t)(grp * RPW + rg + r * RG) * row_bytes + (uint32_t)(u >> 3) * Q6_K_BYTES;
+        const int row = grp * RPW + rg + r * RG;
+        const int mrow = (EPI == EPI_ROPE_KV) ? rope_row(row, fz.hd) : row;
+        return (uint32_t)mrow * row_bytes + (uint32_t)(u >> 3) * Q6_K_BYTES;
     };
     // slot r <- row r of group grp
     auto issue = [&](int grp, int r) {
@@ -1221,7 +1289,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_q6k_splitk_kernel(const uint8_t*
         float* rb = red + it * (KS * RPW);
         if ((lane & ((1 << SH) - 1)) == 0) rb[ks * RPW + rg + (lane >> SH) * RG] = sum;
         __syncthreads();  // (the other buffer was last read before this barrier)
-        store_slices<KS, RPW, NW, EPI>(rb, grp * RPW, n, y);
+        store_slices<KS, RPW, NW, EPI>(rb, grp * RPW, n, y, fz);
     }
 }
 
@@ -1354,10 +1422,10 @@ void launch_q4k_small(const uint8_t* w, int n, int nsb, const float* x, size_t m
     constexpr int NW = 8;
     const int slots = 2 * num_cus();
     int rpw = (n + slots - 1) / slots;
-    if (EPI == EPI_SWIGLU) rpw += rpw & 1;
+    if (EPI == EPI_SWIGLU || EPI == EPI_ROPE_KV) rpw += rpw & 1;
     if (rpw > 8 * NW) rpw = 8 * NW;
     const int r = (rpw + NW - 1) / NW;
-    if constexpr (EPI == EPI_SWIGLU) {
+    if constexpr (EPI == EPI_SWIGLU || EPI == EPI_ROPE_KV) {
         if (r <= 2) launch_q4k_r<2, PRO, EPI>(w, n, nsb, x, m, y, s, lds, rpw, fz);
         else if (r <= 4) launch_q4k_r<4, PRO, EPI>(w, n, nsb, x, m, y, s, lds, rpw, fz);
         else if (r <= 6) launch_q4k_r<6, PRO, EPI>(w, n, nsb, x, m, y, s, lds, rpw, fz);
@@ -1584,6 +1652,38 @@ hipError_t launch_gemv_kquant_ex(WType t, const uint8_t* w, size_t n, size_t k, 
         launch_kq<PRO_RMSNORM, EPI_SWIGLU>(t, w, ni, nsb, x, m, y, s, lds, fz);
     else
         return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv_kquant_rope_kv(WType t, const uint8_t* w, size_t n, size_t k, const float* x, size_t m,
+                                      size_t row0, float* y, size_t ystride, const float* g, float eps,
+                                      const int* pos, const float* cos_t, const float* sin_t, void* kc, void* vc,
+                                      int n_heads, int n_kv, int hd, int max_seq, bool kv_f16, hipStream_t s) {
+    if (n == 0 || m == 0) return hipSuccess;
+    if ((t != WType::Q4_K && t != WType::Q6_K) || k == 0 || k % QK_K || k > fused_max_k(t) || m > 4 ||
+        ((uintptr_t)x & 15) || k > INT32_MAX || ystride < n || ystride > INT32_MAX || row0 > INT32_MAX ||
+        g == nullptr || ((uintptr_t)g & 15) || hd <= 0 || (hd & 1) ||
+        n != (size_t)(n_heads + 2 * n_kv) * hd || (uint64_t)n * (k / QK_K) * block_bytes(t) > FUSED_MAX_WEIGHT_BYTES)
+        return hipErrorInvalidValue;
+    KqFuse fz{};
+    fz.g = g;
+    fz.eps = eps;
+    fz.xstride = (int)k;
+    fz.ystride = (int)ystride;
+    fz.pos = pos;
+    fz.row0 = (int)row0;
+    fz.cos_t = cos_t;
+    fz.sin_t = sin_t;
+    fz.kc = kc;
+    fz.vc = vc;
+    fz.n_heads = n_heads;
+    fz.n_kv = n_kv;
+    fz.hd = hd;
+    fz.max_seq = max_seq;
+    fz.kv_f16 = kv_f16 ? 1 : 0;
+    fz.head0 = 0;
+    const size_t lds = (size_t)8 * 16 * (k / QK) + 16 * sizeof(float);
+    launch_kq<PRO_RMSNORM, EPI_ROPE_KV>(t, w, (int)n, (int)(k / QK_K), x, m, y, s, lds, fz);
     return hipGetLastError();
 }
 

@@ -654,9 +654,9 @@ struct LlamaModel {
 
     // One layer of any resident types, any row count (m > 4 Q4_0 rows take the
     // GEMM).  Q4_K / Q6_K matrices fold the RMSNorm in front of them, the
-    // residual add after o / down and the SwiGLU of combined gate/up rows into
-    // their GEMV launches; the other types run separate norm / add / SwiGLU
-    // launches.  RoPE and the cache write run on their own.
+    // residual add after o / down, the SwiGLU of combined gate/up rows and the
+    // RoPE + cache write of combined q/k/v rows into their GEMV launches; the
+    // other types run separate norm / add / SwiGLU / RoPE launches.
     hipError_t layer_plain(int l, size_t m) {
         const int d = cfg.dim, f = cfg.ffn_dim;
         Layer& L = layers[l];
@@ -672,7 +672,17 @@ struct LlamaModel {
         bool want_xn = false;
         for (int i = 0; i < np; i++) want_xn |= !kquant(*parts[i]);
         if (want_xn) rmsnorm(L.attn_norm);
-        for (int i = 0; i < np; i++) {
+        // a K-quant [Wq; Wk; Wv] also applies RoPE and writes the cache
+        const bool rope_fused = np == 1 && kquant(L.qkv);
+        for (size_t r = 0; rope_fused && r < m; r += 4) {
+            const size_t mr = (m - r < 4) ? m - r : 4;
+            e = launch_gemv_kquant_rope_kv(L.qkv.type, L.qkv.dev, L.qkv.n, d, x + r * d, mr, r, qkv + r * qkv_dim,
+                                           qkv_dim, L.attn_norm, cfg.norm_eps, pos, cos_t, sin_t, kv_layer(kc, l),
+                                           kv_layer(vc, l), cfg.n_heads, cfg.n_kv_heads, cfg.head_dim,
+                                           cfg.max_seq, cfg.kv_f16 != 0, stream);
+            if (e != hipSuccess) return e;
+        }
+        for (int i = 0; i < np && !rope_fused; i++) {
             const Mat& w = *parts[i];
             if (kquant(w)) {
                 e = kq_linear(w, x, d, m, qkv + cols[i], qkv_dim, GEMV_PRO_RMSNORM, L.attn_norm, GEMV_EPI_STORE);
@@ -686,7 +696,7 @@ struct LlamaModel {
             }
             if (e != hipSuccess) return e;
         }
-        e = cfg.kv_f16 ? layer_attention<_Float16>(l, m) : layer_attention<float>(l, m);
+        e = cfg.kv_f16 ? layer_attention<_Float16>(l, m, !rope_fused) : layer_attention<float>(l, m, !rope_fused);
         if (e != hipSuccess) return e;
         // ---- x += att . Wo^T ----
         if (kquant(L.o)) {

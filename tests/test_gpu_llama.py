@@ -299,6 +299,26 @@ def test_q6_k_combined_layers(rq, gpu):
     check_typed_model(m, ref, [9, 3, 100, 200, 300, 44], 12)
 
 
+@pytest.mark.parametrize("qtype", [12, 14])
+def test_k_quant_rope_epilogue_f16_cache(rq, gpu, qtype):
+    """Combined Q4_K / Q6_K q/k/v with the RoPE epilogue writing an f16 cache:
+    prefill (rows four at a time, positions 0..8) and decode steps within 1e-2
+    of the largest logit of the oracle (f32 cache)."""
+    import rdlquant.llama as L
+    t = {(slot, layer): qtype for layer in range(2)
+         for slot in (L.WQ, L.WK, L.WV, L.WO, L.W_GATE, L.W_UP, L.W_DOWN)}
+    cfg = tiny_config(kv_f16=True)
+    m, ref, _ = build_typed(cfg, t, 515 + qtype)
+    got, want = m.forward_with_cache([7, 70, 170, 2, 9, 31, 44, 5, 300]), ref.forward_with_cache(
+        [7, 70, 170, 2, 9, 31, 44, 5, 300])
+    assert np.max(np.abs(got - want)) <= 1e-2 * np.max(np.abs(want))
+    tok = argmax(want)
+    for _ in range(3):
+        got, want = m.decode_step(tok), ref.forward_with_cache([tok])
+        assert np.max(np.abs(got - want)) <= 1e-2 * np.max(np.abs(want))
+        tok = argmax(want)
+
+
 def test_wide_k_quant_layers(rq, gpu):
     """Rows longer than 4096 (dim 4352, ffn 4608): the split-K Q4_K kernel with
     the RMSNorm prologue and the SwiGLU / residual epilogues (layer 0), the
