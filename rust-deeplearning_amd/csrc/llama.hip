@@ -154,6 +154,24 @@ constexpr int ATT_CHUNK = 64;
 constexpr int ATT_WAVES = 8;
 constexpr int ATT_SPAN = ATT_CHUNK * ATT_WAVES;
 
+// One step of the transposed sum of N values over N lanes (lane index c within
+// its group of N): the lane keeps the half of its values selected by bit HF
+// of c and adds the partner lane's (c ^ HF) copy of that half.  After the
+// steps HF = N/2, ..., 1, v[0] of lane c is the group's total of value c.
+template <int HF, int N>
+__device__ __forceinline__ void transposed_sum(float (&v)[N], int c) {
+    if constexpr (HF >= 1) {
+        const bool up = (c & HF) != 0;
+#pragma unroll
+        for (int j = 0; j < HF; j++) {
+            const float send = up ? v[j] : v[j + HF];
+            const float keep = up ? v[j + HF] : v[j];
+            v[j] = keep + __shfl_xor(send, HF);
+        }
+        transposed_sum<HF / 2, N>(v, c);
+    }
+}
+
 template <typename KV, int HD>
 __global__ __launch_bounds__(64 * ATT_WAVES) void attention_kernel(
     const float* __restrict__ qkv, int qkv_dim, const int* __restrict__ pos_dev, const KV* __restrict__ kc,
@@ -164,58 +182,88 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attention_kernel(
     __shared__ float wsc[1024];
     __shared__ int last;
     const int hd = HD ? HD : hd_rt;
-    const int h = blockIdx.x, s = blockIdx.y, z = blockIdx.z;
+    // Workgroups are dealt to the 8 XCDs round-robin by linear id; block b
+    // serves head (b % n_kv) * G + b / n_kv, so the G query heads of a KV
+    // head (blocks g, g + n_kv, ...) run on one XCD and share its L2.
+    const int G = n_heads / n_kv;
+    const int h = ((int)blockIdx.x % n_kv) * G + (int)blockIdx.x / n_kv;
+    const int s = blockIdx.y, z = blockIdx.z;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int t = *pos_dev + s + 1;
     if (z * ATT_SPAN >= t) return;  // whole workgroup
     float* qs = sm;
     float* os = sm + hd;
-    const int kvh = h / (n_heads / n_kv);
+    const int kvh = h / G;
     const float* q = qkv + (size_t)s * qkv_dim + h * hd;
-    for (int d = threadIdx.x; d < hd; d += 64 * ATT_WAVES) qs[d] = q[d];
-    __syncthreads();
+    // V rows in pieces of 16 bytes: CPR lanes cover a row, one load covers
+    // KG rows; load i of lane l is row KG i + l / CPR (when CPR <= 16)
+    constexpr int V = 16 / sizeof(KV);
+    constexpr int CPR = HD * (int)sizeof(KV) / 16;
+    constexpr bool VPRE = HD > 0 && CPR <= 16 && 64 % (CPR > 0 ? CPR : 1) == 0;
+    if constexpr (!VPRE) {
+        for (int d = threadIdx.x; d < hd; d += 64 * ATT_WAVES) qs[d] = q[d];
+        __syncthreads();
+    }
     const int p0 = z * ATT_SPAN + w * ATT_CHUNK;
     float mx = -__builtin_inff(), l = 0.0f;
     if (p0 < t) {  // wave-uniform
         const int p = p0 + lane;
         const bool valid = p < t;
-        const KV* kr = kc + ((size_t)kvh * max_seq + (valid ? p : p0)) * hd;
-        constexpr int V = 16 / sizeof(KV);
         typedef KV kvv __attribute__((ext_vector_type(V)));
         const KV* vb = vc + (size_t)kvh * max_seq * hd;
         const int nvalid = min(ATT_CHUNK, t - p0);
-        // V rows in pieces of 16 bytes: CPR lanes cover a row, one load covers
-        // KG rows; load i of lane l is row KG i + l / CPR (when CPR <= 16)
-        constexpr int CPR = HD * (int)sizeof(KV) / 16;
-        constexpr bool VPRE = HD > 0 && CPR <= 16 && 64 % (CPR > 0 ? CPR : 1) == 0;
         constexpr int KG = VPRE ? 64 / (CPR > 0 ? CPR : 1) : 1;
         float acc = 0.0f;
         if constexpr (VPRE) {
-            // K and V loads all in flight before the first use: one round trip
-            kvv kreg[HD / V], vreg[CPR];
-            const int vk = lane / CPR, ve = (lane % CPR) * V;
+            // K and V rows of the chunk in the same coalesced layout (load i of
+            // lane l = piece l % CPR of row KG i + l / CPR), all in flight
+            // before the query (which the previous launch wrote) is read: one
+            // memory round trip.  Rows past the length re-read the last valid row.
+            const KV* kb = kc + (size_t)kvh * max_seq * hd;
+            kvv kreg[CPR], vreg[CPR];
+            const int vk = lane / CPR, pc = lane % CPR, ve = pc * V;
 #pragma unroll
-            for (int i = 0; i < HD / V; i++) kreg[i] = *reinterpret_cast<const kvv*>(kr + i * V);
+            for (int i = 0; i < CPR; i++) {
+                const int j = min(KG * i + vk, nvalid - 1);
+                kreg[i] = *reinterpret_cast<const kvv*>(kb + (size_t)(p0 + j) * hd + ve);
+            }
 #pragma unroll
-            for (int i = 0; i < CPR; i++) {  // rows past the length re-read the last valid row
+            for (int i = 0; i < CPR; i++) {
                 const int j = min(KG * i + vk, nvalid - 1);
                 vreg[i] = *reinterpret_cast<const kvv*>(vb + (size_t)(p0 + j) * hd + ve);
             }
+            float qv[V];
+#pragma unroll
+            for (int e = 0; e < V; e += 4) {
+                const float4 t4 = *reinterpret_cast<const float4*>(q + ve + e);
+                qv[e] = t4.x, qv[e + 1] = t4.y, qv[e + 2] = t4.z, qv[e + 3] = t4.w;
+            }
             __builtin_amdgcn_sched_barrier(0);  // keep every load ahead of the arithmetic
+            // partial scores of the lane's CPR rows over its V dims, then a
+            // transposed sum over the CPR lanes of the row group: after the
+            // step of mask hf a lane keeps the half of its rows selected by
+            // bit hf of its piece, so piece c ends with row KG c + vk's score.
+            float ps[CPR];
 #pragma unroll
-            for (int i = 0; i < HD / V; i++)
+            for (int i = 0; i < CPR; i++) {
+                float a = 0.0f;
 #pragma unroll
-                for (int e = 0; e < V; e++) acc += qs[i * V + e] * (float)kreg[i][e];
-            const float sc = valid ? acc / scale : -__builtin_inff();
+                for (int e = 0; e < V; e++) a += qv[e] * (float)kreg[i][e];
+                ps[i] = a;
+            }
+            transposed_sum<CPR / 2, CPR>(ps, pc);
+            const int key = KG * pc + vk;  // the row whose score this lane holds
+            const bool kvalid = key < nvalid;
+            const float sc = kvalid ? ps[0] / scale : -__builtin_inff();
             mx = wave_max(sc);
-            const float e = valid ? expf(sc - mx) : 0.0f;
+            const float e = kvalid ? expf(sc - mx) : 0.0f;
             l = wave_sum(e);
             float o[V];
 #pragma unroll
             for (int c = 0; c < V; c++) o[c] = 0.0f;
 #pragma unroll
             for (int i = 0; i < CPR; i++) {
-                const float pj = __shfl(e, KG * i + vk);  // rows past the length carry 0
+                const float pj = __shfl(e, vk * CPR + i);  // row KG i + vk; rows past the length carry 0
 #pragma unroll
                 for (int c = 0; c < V; c++) o[c] += pj * (float)vreg[i][c];
             }
@@ -227,6 +275,7 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attention_kernel(
 #pragma unroll
                 for (int c = 0; c < V; c++) os[w * hd + ve + c] = o[c];
         } else {
+            const KV* kr = kc + ((size_t)kvh * max_seq + (valid ? p : p0)) * hd;
             if constexpr (HD > 0) {
                 kvv kreg[HD / V];
 #pragma unroll
