@@ -90,7 +90,9 @@ __device__ __forceinline__ void after_wait(f32x4 (&v)[PI][2]) {
     for (int j = 0; j < PI; j++) asm volatile("" : "+v"(v[j][0]), "+v"(v[j][1]));
 }
 
-template <int NW, int PI>
+// SUMS: also the digit sums (the Q4_0 -8 offset terms); the K-quant kernels
+// do not read them.
+template <int NW, int PI, bool SUMS = true>
 __device__ void prep_float_lds(const f32x4 (&xv)[PI], int nb, int* __restrict__ lds) {
     constexpr int NT = NW * 64;
 #pragma unroll
@@ -104,8 +106,9 @@ __device__ void prep_float_lds(const f32x4 (&xv)[PI], int nb, int* __restrict__ 
         amax = max8_f32(amax);
         const int anybad = sum8_i32(bad ? 1 : 0);
         // scale tiny blocks by 2^64 so that 8323072/amax stays finite (exact)
+        // (the reciprocal's 1 ulp keeps |t| within 8323075, far inside the digits' range)
         const float pw = (amax < 0x1p-60f) ? 0x1p64f : 1.0f;
-        const float inv = (amax > 0.0f && !anybad) ? 8323072.0f / (amax * pw) : 0.0f;
+        const float inv = (amax > 0.0f && !anybad) ? 8323072.0f * __builtin_amdgcn_rcpf(amax * pw) : 0.0f;
         const float f = anybad ? 0.0f : pw * inv;
         uint32_t e0 = (uint32_t)(rintf(v.x * f) + 8421504.0f) ^ 0x808080u;
         uint32_t e1 = (uint32_t)(rintf(v.y * f) + 8421504.0f) ^ 0x808080u;
@@ -126,16 +129,20 @@ __device__ void prep_float_lds(const f32x4 (&xv)[PI], int nb, int* __restrict__ 
             lds[lds_word(2 + g, k4, nb, c)] = (int)db;
             lds[lds_word(4 + g, k4, nb, c)] = (int)dc;
         }
-        const int sa = sum8_i32(__builtin_amdgcn_sdot4((int)da, (int)ONES, 0, false));
-        const int sb = sum8_i32(__builtin_amdgcn_sdot4((int)db, (int)ONES, 0, false));
-        const int sc = sum8_i32(__builtin_amdgcn_sdot4((int)dc, (int)ONES, 0, false));
         const float xs = sum8_f32((v.x + v.y) + (v.z + v.w));
+        if constexpr (SUMS) {
+            const int sa = sum8_i32(__builtin_amdgcn_sdot4((int)da, (int)ONES, 0, false));
+            const int sb = sum8_i32(__builtin_amdgcn_sdot4((int)db, (int)ONES, 0, false));
+            const int sc = sum8_i32(__builtin_amdgcn_sdot4((int)dc, (int)ONES, 0, false));
+            if (k == 0 && p < nb * 8) {
+                lds[lds_word(6, 1, nb, c)] = sa;
+                lds[lds_word(6, 2, nb, c)] = sb;
+                lds[lds_word(6, 3, nb, c)] = sc;
+            }
+        }
         if (k == 0 && p < nb * 8) {
             const float nan = __builtin_nanf("");
-            lds[lds_word(6, 0, nb, c)] = __builtin_bit_cast(int, anybad ? nan : amax / 127.0f);
-            lds[lds_word(6, 1, nb, c)] = sa;
-            lds[lds_word(6, 2, nb, c)] = sb;
-            lds[lds_word(6, 3, nb, c)] = sc;
+            lds[lds_word(6, 0, nb, c)] = __builtin_bit_cast(int, anybad ? nan : amax * (1.0f / 127.0f));
             lds[lds_word(7, 0, nb, c)] = __builtin_bit_cast(int, anybad ? nan : xs);
         }
     }
@@ -175,9 +182,9 @@ __device__ void prep_native_lds(const f32x4 (&xv)[PI], int nb, int* __restrict__
 }
 
 // ---- int4-digit records for Q4_0 / Q4_1 (float mode) --------------------------------
-// x_j ~= S4 * t_j with t_j = rint(x_j * 7829365 / amax), a signed 24-bit code
+// x_j ~= S4 * t_j with t_j = rint(x_j * 7829364 / amax), a signed 24-bit code
 // (|t| <= 0x777777 = 7829367, the largest code the digits hold; the scale
-// leaves two units for the rounding of amax * (7829365 / amax))
+// leaves three units for the rounding of amax * (7829364 * rcp(amax)))
 // held as six signed base-16 digits: t + 0x888888 is in [0, 2^24), so the
 // nibbles of e = (t + 0x888888) ^ 0x888888 are the digits as int4 (nibble L
 // weighs 16^L).  The digit dwords follow the Q4 nibble order (byte j of a
@@ -294,8 +301,10 @@ __device__ void prep_float4_lds(const f32x4 (&xv)[PI][2], const f32x4 (&av)[PI][
         }
         amax = max4_f32(amax);
         const int anybad = sum4_i32(bad ? 1 : 0);
+        // 7829364 / amax through the reciprocal (1 ulp): |t| <= 7829366, one
+        // code inside the digits' range 0x777777 = 7829367
         const float pw = (amax < 0x1p-60f) ? 0x1p64f : 1.0f;
-        const float f = (amax > 0.0f && !anybad) ? pw * (7829365.0f / (amax * pw)) : 0.0f;
+        const float f = (amax > 0.0f && !anybad) ? pw * (7829364.0f * __builtin_amdgcn_rcpf(amax * pw)) : 0.0f;
         uint32_t e[8];
 #pragma unroll
         for (int i = 0; i < 8; i++)
@@ -321,7 +330,7 @@ __device__ void prep_float4_lds(const f32x4 (&xv)[PI][2], const f32x4 (&av)[PI][
             for (int lv = 0; lv < 6; lv++) lds[lds_word(lv, k, nb, c)] = (int)L[lv];
             if (k == 0) {
                 const float nan = __builtin_nanf("");
-                lds[lds_word(6, 0, nb, c)] = __builtin_bit_cast(int, anybad ? nan : amax / 7829365.0f);
+                lds[lds_word(6, 0, nb, c)] = __builtin_bit_cast(int, anybad ? nan : amax * (1.0f / 7829364.0f));
                 lds[lds_word(6, 1, nb, c)] = __builtin_bit_cast(int, anybad ? nan : xs);
             }
         }
@@ -624,7 +633,23 @@ __global__ __launch_bounds__(NW * 64) void gemv_fused_kernel(const uint8_t* __re
         load_window<WORDS, !NB_EVEN>(rs, off, wbytes, win[b]);
     };
 
+    // The lane that stores row row_of(lane >> SH) after the reduction
+    // (EPI_SWIGLU / EPI_ROPE_KV: the pair starting there) fetches what its
+    // epilogue reads ahead of the stream, so no load waits at the kernel's
+    // end: the residual's old y (here), the RoPE position (a scalar load) and
+    // cos / sin (after the prep).
+    constexpr int SH = reduce_span_log2<R>();
+    const bool st_lane = (lane & (((PAIRS ? 2 : 1) << SH) - 1)) == 0;
+    const int st_row = row_of(lane >> SH);
+    float y_old = 0.0f;
+    if constexpr (EPI == EPI_RESIDUAL) {
+        if (st_lane && st_row < rend) y_old = y[st_row];
+    }
+    int rope_pos = 0;
+    if constexpr (EPI == EPI_ROPE_KV) rope_pos = *fz.pos + blockIdx.y;
+
     // ---- x for the prep first, then the first PF blocks ----
+    __builtin_amdgcn_s_setprio(2);  // the prep ahead of other workgroups' streams
     if constexpr (I4) {
         f32x4 xv[PI][2], av[PI][2];
         const float* aux = (PRO == PRO_RMSNORM) ? fz.g : x + nb * 32;
@@ -648,8 +673,19 @@ __global__ __launch_bounds__(NW * 64) void gemv_fused_kernel(const uint8_t* __re
             prep_float_lds<NW, PI>(xv, nb, reinterpret_cast<int*>(lds4));
     }
     __syncthreads();
+    __builtin_amdgcn_s_setprio(0);
 #pragma unroll
     for (int b = P0; b < PF; b++) issue(b);
+    float rope_c = 0.0f, rope_s = 0.0f;
+    if constexpr (EPI == EPI_ROPE_KV) {
+        if (st_lane && st_row < rend) {
+            const int r1 = mat_row(st_row), head = r1 / fz.hd, i = r1 % fz.hd;
+            if (head < fz.n_heads + fz.n_kv) {
+                rope_c = fz.cos_t[(size_t)rope_pos * half + i];
+                rope_s = fz.sin_t[(size_t)rope_pos * half + i];
+            }
+        }
+    }
 
     // column records: kept in registers when a lane has at most two columns
     constexpr bool KEEP = (CPL <= 2);
@@ -697,7 +733,6 @@ __global__ __launch_bounds__(NW * 64) void gemv_fused_kernel(const uint8_t* __re
 
     // ---- reduce and store ----
     const float s = wave_reduce_rows<R>(acc);
-    constexpr int SH = reduce_span_log2<R>();
     if constexpr (EPI == EPI_SWIGLU) {
         // rows r (gate, even) and r + 1 (up) sit in adjacent lane groups
         const float up = __shfl_down(s, 1 << SH);
@@ -712,10 +747,10 @@ __global__ __launch_bounds__(NW * 64) void gemv_fused_kernel(const uint8_t* __re
             if (l1 < rend) {
                 const int r1 = mat_row(l1);  // row of x1; x2's row is r1 + half
                 const int head = r1 / fz.hd, i = r1 % fz.hd;
-                const int pos = *fz.pos + blockIdx.y;
+                const int pos = rope_pos;
                 const float x1 = s;
                 if (head < fz.n_heads + fz.n_kv) {
-                    const float c = fz.cos_t[(size_t)pos * half + i], sn = fz.sin_t[(size_t)pos * half + i];
+                    const float c = rope_c, sn = rope_s;
                     const float o1 = x1 * c - x2 * sn, o2 = x1 * sn + x2 * c;
                     if (head < fz.n_heads) {
                         y[r1] = o1;
@@ -746,7 +781,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_fused_kernel(const uint8_t* __re
         const int row = row_of(lane >> SH);
         if (row < rend) {
             if constexpr (EPI == EPI_RESIDUAL)
-                y[row] = s + y[row];
+                y[row] = s + y_old;
             else
                 y[row] = s;
         }
@@ -948,6 +983,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_q4k_fused_kernel(const uint8_t* 
     const uint32_t row_bytes = (uint32_t)nsb * Q4_K_BYTES;
     constexpr int PI = (16 + NW - 1) / NW;  // nb * 8 = 16 * units <= 1024 float4 pieces
     f32x4 xv[PI], gv[PI];
+    __builtin_amdgcn_s_setprio(2);  // the prep ahead of other workgroups' streams
     load_prep_xg<NW, PI, PRO>(x, fz.g, nb, xv, gv);
     auto row_of = [&](int r) {
         if constexpr (PAIRS) return r0 + 2 * (wv + (r >> 1) * NW) + (r & 1);
@@ -990,8 +1026,9 @@ __global__ __launch_bounds__(NW * 64) void gemv_q4k_fused_kernel(const uint8_t* 
         after_wait<PI>(gv);
         rmsnorm_pieces<NW, PI>(xv, gv, fz.eps, nb, reinterpret_cast<float*>(lds4) + nb * 32);
     }
-    prep_float_lds<NW, PI>(xv, nb, reinterpret_cast<int*>(lds4));
+    prep_float_lds<NW, PI, false>(xv, nb, reinterpret_cast<int*>(lds4));
     __syncthreads();
+    __builtin_amdgcn_s_setprio(0);
     if (row_of(0) >= rend) return;  // wave-uniform; the wave has no rows
 
     float acc[R];
@@ -1093,6 +1130,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_q4k_splitk_kernel(const uint8_t*
     const uint32_t row_bytes = (uint32_t)nsb * Q4_K_BYTES;
     constexpr int PI = (KS * 16 + NW - 1) / NW;  // nb * 8 = 16 * units <= 1024 * KS float4 pieces
     f32x4 xv[PI], gv[PI];
+    __builtin_amdgcn_s_setprio(2);  // the prep ahead of other workgroups' streams
     load_prep_xg<NW, PI, PRO>(x, fz.g, nb, xv, gv);
 
     const int u = ks * ups + lane;
@@ -1122,8 +1160,9 @@ __global__ __launch_bounds__(NW * 64) void gemv_q4k_splitk_kernel(const uint8_t*
         after_wait<PI>(gv);
         rmsnorm_pieces<NW, PI>(xv, gv, fz.eps, nb, reinterpret_cast<float*>(lds4) + nb * 32);
     }
-    prep_float_lds<NW, PI>(xv, nb, reinterpret_cast<int*>(lds4));
+    prep_float_lds<NW, PI, false>(xv, nb, reinterpret_cast<int*>(lds4));
     __syncthreads();
+    __builtin_amdgcn_s_setprio(0);
 
     float acc[R];
 #pragma unroll
@@ -1205,6 +1244,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_q6k_splitk_kernel(const uint8_t*
     const uint32_t row_bytes = (uint32_t)nsb * Q6_K_BYTES;
     constexpr int PI = (KS * 8 + NW - 1) / NW;  // nb * 8 <= 512 * KS float4 pieces
     f32x4 xv[PI], gv[PI];
+    __builtin_amdgcn_s_setprio(2);  // the prep ahead of other workgroups' streams
     load_prep_xg<NW, PI, PRO>(x, fz.g, nb, xv, gv);
 
     const int u = ks * ups + lane;
@@ -1245,8 +1285,9 @@ __global__ __launch_bounds__(NW * 64) void gemv_q6k_splitk_kernel(const uint8_t*
         after_wait<PI>(gv);
         rmsnorm_pieces<NW, PI>(xv, gv, fz.eps, nb, reinterpret_cast<float*>(lds4) + nb * 32);
     }
-    prep_float_lds<NW, PI>(xv, nb, reinterpret_cast<int*>(lds4));
+    prep_float_lds<NW, PI, true>(xv, nb, reinterpret_cast<int*>(lds4));  // q6k_offsets reads the digit sums
     __syncthreads();
+    __builtin_amdgcn_s_setprio(0);
 
     // the records are read once; the slice sums then go to LDS past them
     RF xr{};
