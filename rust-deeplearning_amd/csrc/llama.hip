@@ -428,6 +428,8 @@ __global__ __launch_bounds__(SAMPLE_NT) void sample_kernel(const float* __restri
     __shared__ int win;
     typedef float f4 __attribute__((ext_vector_type(4)));
     constexpr int VU = 8;  // float4 loads in flight per thread
+    // the step counter is read with the logits, not after the reduction
+    const int st = threadIdx.x == 0 ? *step : 0;
     float best = -__builtin_inff();
     int idx = 0x7FFFFFFF;
     const int n4 = vocab >> 2;
@@ -480,7 +482,6 @@ __global__ __launch_bounds__(SAMPLE_NT) void sample_kernel(const float* __restri
                 idx = bi[w];
             }
         if (idx == 0x7FFFFFFF) idx = 0;
-        const int st = *step;
         token[0] = idx;
         out_tokens[st] = idx;
         *step = st + 1;
