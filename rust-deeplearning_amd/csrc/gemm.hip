@@ -227,28 +227,33 @@ __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_f16_kernel(
     const __amdgpu_buffer_rsrc_t xlrs = make_rsrc(XL, (uint32_t)m * (uint32_t)k * 2u);
     const int nchunks = (nb + CB - 1) / CB;
 
-    auto load_chunk = [&](int c, S& r) {
+    // live == false (a chunk past the end) loads nothing through out-of-range
+    // offsets: the loads are issued on every iteration, so the compiler's
+    // wait counts before the LDS stores stay exact (no branch around them).
+    auto load_chunk = [&](int c, S& r, bool live) {
 #pragma unroll
         for (int u = 0; u < C::WBLK; u++) {
             const int idx = threadIdx.x + u * C::NT;
             const int jl = idx / CB, bl = idx % CB;
             const int j = j0 + jl, b = c * CB + bl;
-            const uint32_t off = (idx < C::TJ * CB && j < n && b < nb)
+            const uint32_t off = (live && idx < C::TJ * CB && j < n && b < nb)
                                      ? (uint32_t)j * row_bytes + (uint32_t)b * 18u
                                      : RSRC_OOB;
             const uint32_t base = off & ~3u;
             const u32x4 v = buf_load_b128(wrs, base);
             r.w[u][0] = v.x; r.w[u][1] = v.y; r.w[u][2] = v.z; r.w[u][3] = v.w;
-            // the last block of an odd-sized matrix ends 2 bytes before its window
+            // the last block of an odd-sized matrix ends 2 bytes before its
+            // window: its tail dword is read 2 bytes early and shifted when the
+            // block is stored (not here: that would wait for the load now)
             const bool over = base < wbytes && base + 20u > wbytes;
-            r.w[u][4] = buf_load_b32(wrs, over ? wbytes - 4u : base + 16u) >> (over ? 16 : 0);
+            r.w[u][4] = buf_load_b32(wrs, over ? wbytes - 4u : base + 16u);
         }
 #pragma unroll
         for (int u = 0; u < C::XU; u++) {
             const int idx = threadIdx.x + u * C::NT;   // unit = 8 halfs
             const int il = idx / (CB * 4), q = idx % (CB * 4);
             const int i = i0 + il, kk = c * CB * 32 + q * 8;
-            const uint32_t off = (idx < C::TI * CB * 4 && i < m && kk < k)
+            const uint32_t off = (live && idx < C::TI * CB * 4 && i < m && kk < k)
                                      ? ((uint32_t)i * (uint32_t)k + (uint32_t)kk) * 2u
                                      : RSRC_OOB;
             r.xh[u] = buf_load_b128(xhrs, off);
@@ -267,6 +272,9 @@ __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_f16_kernel(
             if (idx < C::TJ * CB) {
                 const int jl = idx / CB, bl = idx % CB;
                 const int j = j0 + jl, b = c * CB + bl;
+                const uint32_t off = (j < n && b < nb) ? (uint32_t)j * row_bytes + (uint32_t)b * 18u : RSRC_OOB;
+                const uint32_t base = off & ~3u;
+                const uint32_t w4 = (base < wbytes && base + 20u > wbytes) ? (r.w[u][4] >> 16) : r.w[u][4];
                 // block g = j * nb + b starts at 18 g: 2 bytes past a dword when g is odd
                 const bool odd = (((uint32_t)j * (uint32_t)nb + (uint32_t)b) & 1u) != 0;
                 const uint32_t sel = odd ? 0x07060504u : 0x05040302u;
@@ -276,7 +284,7 @@ __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_f16_kernel(
                 lo.x = perm(r.w[u][1], r.w[u][0], sel);
                 lo.y = perm(r.w[u][2], r.w[u][1], sel);
                 hi.x = perm(r.w[u][3], r.w[u][2], sel);
-                hi.y = perm(r.w[u][4], r.w[u][3], sel);
+                hi.y = perm(w4, r.w[u][3], sel);
                 uint2* dst = reinterpret_cast<uint2*>(wn + jl * Lds<CB>::WN_STRIDE + bl * 16);
                 dst[0] = lo;
                 dst[1] = hi;
@@ -339,17 +347,17 @@ __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_f16_kernel(
     // Loads run two chunks ahead of the compute: register set P holds chunk
     // c + 2 while LDS buffer 1 - P receives chunk c + 1.
     S r0, r1;
-    load_chunk(0, r0);
-    if (nchunks > 1) load_chunk(1, r1);
+    load_chunk(0, r0, true);
+    load_chunk(1, r1, nchunks > 1);
     store_chunk(0, 0, r0);
     __syncthreads();
     for (int c = 0; c < nchunks; c += 2) {
-        if (c + 2 < nchunks) load_chunk(c + 2, r0);
+        load_chunk(c + 2, r0, c + 2 < nchunks);
         compute_chunk(0);
         if (c + 1 < nchunks) store_chunk(c + 1, 1, r1);
         __syncthreads();
         if (c + 1 >= nchunks) break;
-        if (c + 3 < nchunks) load_chunk(c + 3, r1);
+        load_chunk(c + 3, r1, c + 3 < nchunks);
         compute_chunk(1);
         if (c + 2 < nchunks) store_chunk(c + 2, 0, r0);
         __syncthreads();
