@@ -137,9 +137,10 @@ __global__ void rope_kv_kernel(float* __restrict__ qkv, int qkv_dim, const int* 
 // scores q.k / sqrt(hd), max-subtracted softmax (ops.rs:582-628), then the
 // probability-weighted sum of the values.  Split over the keys in chunks of
 // ATT_CHUNK: one wave per (head, row, chunk) forms the chunk's scores (one
-// key per lane), its max m_c, sum l_c = sum exp(score - m_c) and the
-// unnormalised context o_c = sum exp(score - m_c) v; attention_combine_kernel
-// then forms (sum_c exp(m_c - M) o_c) / (sum_c exp(m_c - M) l_c), M = max m_c.
+// key's score per lane), its max m_c, sum l_c = sum exp(score - m_c) and the
+// unnormalised context o_c = sum exp(score - m_c) v; the chunks are then
+// combined as (sum_c exp(m_c - M) o_c) / (sum_c exp(m_c - M) l_c), M = max
+// m_c (in LDS within a workgroup, see attention_kernel for several spans).
 // Chunks past the row's length exit at once, so a launch sized for the cache
 // capacity serves every position (the captured decode graph).
 constexpr int ATT_CHUNK = 64;
