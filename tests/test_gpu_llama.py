@@ -141,6 +141,10 @@ def test_config5_shape_synthetic_weights(rq, gpu):
     dict(kv_f16=False),                                  # grouped kernel, f32 cache, 2 heads per KV head
     dict(kv_f16=True),                                   # grouped kernel, f16 cache
     dict(kv_f16=False, dim=384, n_heads=6, n_kv_heads=2),  # 3 heads per KV head: per-head kernel
+    # head dim 128: f16 rows take the coalesced 16-lane layout (transposed
+    # score sums), f32 rows the per-key layout
+    dict(kv_f16=True, dim=256, n_heads=2, n_kv_heads=1, head_dim=128),
+    dict(kv_f16=False, dim=256, n_heads=2, n_kv_heads=1, head_dim=128),
 ])
 def test_long_context_spans(rq, gpu, kw):
     # more than 512 cached keys: several attention workgroups per row, whose
