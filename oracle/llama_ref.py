@@ -27,6 +27,51 @@ import numpy as np
 from . import oracle as orc
 
 
+def rope_apply(t, cos, sin, start):
+    """RoPEFreqs::apply (rope.rs:134-200), half-split pairs (i, i + D/2):
+    t [heads, S, D] at positions start .. start + S - 1;
+    out[i] = x[i] cos - x[i + D/2] sin, out[i + D/2] = x[i] sin + x[i + D/2] cos
+    (rope.rs:189-190) with cos / sin rows of RoPEFreqs::new (rope.rs:93-108)."""
+    half = t.shape[-1] // 2
+    s = t.shape[1]
+    cs = cos[start:start + s][None]
+    sn = sin[start:start + s][None]
+    x1, x2 = t[..., :half], t[..., half:]
+    return np.concatenate([x1 * cs - x2 * sn, x1 * sn + x2 * cs], axis=-1).astype(np.float32)
+
+
+def attention(q, kc, vc, start):
+    """Grouped-query attention of MultiHeadAttention::forward_with_cache
+    (attention.rs:401-446): q [n_heads, S, D] (rows at positions start ..
+    start + S - 1), kc / vc [n_kv, T, D] the cached keys and values 0 .. T-1.
+    Query head h reads KV head h // (n_heads / n_kv) (repeat_kv, ops.rs:955-995,
+    attention.rs:408-410); scores q.k / sqrt(D) (attention.rs:414-416), the
+    causal mask keeps keys <= start + i (Tensor::causal_mask, attention.rs:424-433),
+    max-subtracted softmax (ops.rs:582-628), then p . V.  Returns [n_heads, S, D]."""
+    nh, s, hd = q.shape
+    n_rep = nh // kc.shape[0]
+    scale = np.float32(np.sqrt(np.float32(hd)))
+    ctx = np.zeros((nh, s, hd), np.float32)
+    for h in range(nh):
+        kh, vh = kc[h // n_rep], vc[h // n_rep]
+        sc = (q[h] @ kh.T).astype(np.float32) / scale
+        if s > 1:  # causal mask (Tensor::causal_mask(seq_len, total_len))
+            for i in range(s):
+                sc[i, start + i + 1:] = -np.inf
+        mx = sc.max(axis=1, keepdims=True)
+        e = np.exp(sc - mx).astype(np.float32)
+        p = (e / e.sum(axis=1, keepdims=True, dtype=np.float32)).astype(np.float32)
+        ctx[h] = (p @ vh).astype(np.float32)
+    return ctx
+
+
+def swiglu(gate, up):
+    """FeedForward::forward's SwiGLU (feed_forward.rs:146-148): silu(gate) * up
+    with silu(g) = g * (1 / (1 + exp(-g))) (Tensor::silu, ops.rs:441-446)."""
+    sig = (np.float32(1.0) / (np.float32(1.0) + np.exp(-gate))).astype(np.float32)
+    return ((gate * sig) * up).astype(np.float32)
+
+
 class LlamaRef:
     def __init__(self, cfg, weights, threads=8):
         """cfg: rdlquant.llama.LlamaConfig; weights: dict slot -> array (model
@@ -50,15 +95,6 @@ class LlamaRef:
         kind = kinds.get(key, self.w.get("output_kind", "q4") if key == "output" else "q4")
         return orc.matmul(kind, x, self.w[key], m, k, n, threads=self.threads).reshape(m, n)
 
-    def _rope(self, t, start):
-        # t [heads, S, D]: out1 = x1 cos - x2 sin, out2 = x1 sin + x2 cos
-        half = self.c.head_dim // 2
-        s = t.shape[1]
-        cs = self.cos[start:start + s][None]
-        sn = self.sin[start:start + s][None]
-        x1, x2 = t[..., :half], t[..., half:]
-        return np.concatenate([x1 * cs - x2 * sn, x1 * sn + x2 * cs], axis=-1).astype(np.float32)
-
     def forward_with_cache(self, tokens):
         """Last row's logits; the cache advances by len(tokens)."""
         c = self.c
@@ -68,7 +104,6 @@ class LlamaRef:
         x = emb[tokens].astype(np.float32)  # [S, dim]
         start = self.pos
         hd, nh, nkv = c.head_dim, c.n_heads, c.n_kv_heads
-        scale = np.float32(np.sqrt(np.float32(hd)))
         for layer in range(c.n_layers):
             xn = orc.rms_norm(x, self.w[("attn_norm", layer)], c.norm_eps)
             q = self._linear(("wq", layer), xn, nh * hd, c.dim)
@@ -77,31 +112,19 @@ class LlamaRef:
             q = q.reshape(s, nh, hd).transpose(1, 0, 2)
             k = k.reshape(s, nkv, hd).transpose(1, 0, 2)
             v = v.reshape(s, nkv, hd).transpose(1, 0, 2)
-            q, k = self._rope(q, start), self._rope(k, start)
+            q = rope_apply(q, self.cos, self.sin, start)
+            k = rope_apply(k, self.cos, self.sin, start)
             kc, vc = self.kv[layer]
             kc[:, start:start + s] = k
             vc[:, start:start + s] = v
-            total = start + s
-            n_rep = nh // nkv
-            ctx = np.zeros((nh, s, hd), np.float32)
-            for h in range(nh):
-                kh, vh = kc[h // n_rep, :total], vc[h // n_rep, :total]
-                sc = (q[h] @ kh.T).astype(np.float32) / scale
-                if s > 1:  # causal mask (Tensor::causal_mask(seq_len, total_len))
-                    for i in range(s):
-                        sc[i, start + i + 1:] = -np.inf
-                mx = sc.max(axis=1, keepdims=True)
-                e = np.exp(sc - mx).astype(np.float32)
-                p = (e / e.sum(axis=1, keepdims=True, dtype=np.float32)).astype(np.float32)
-                ctx[h] = (p @ vh).astype(np.float32)
+            ctx = attention(q, kc[:, :start + s], vc[:, :start + s], start)
             ctx = ctx.transpose(1, 0, 2).reshape(s, nh * hd)
             attn = self._linear(("wo", layer), ctx, c.dim, nh * hd)
             x = (attn + x).astype(np.float32)
             xn = orc.rms_norm(x, self.w[("ffn_norm", layer)], c.norm_eps)
             gate = self._linear(("w_gate", layer), xn, c.ffn_dim, c.dim)
             up = self._linear(("w_up", layer), xn, c.ffn_dim, c.dim)
-            sig = (np.float32(1.0) / (np.float32(1.0) + np.exp(-gate))).astype(np.float32)
-            h = ((gate * sig) * up).astype(np.float32)
+            h = swiglu(gate, up)
             down = self._linear(("w_down", layer), h, c.dim, c.ffn_dim)
             x = (x + down).astype(np.float32)
         xl = orc.rms_norm(x[-1:], self.w["final_norm"], c.norm_eps)

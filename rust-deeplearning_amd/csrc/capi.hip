@@ -164,14 +164,14 @@ size_t scratch_bytes(Path p, bool native, size_t m, size_t k) {
     return 0;
 }
 
-// Run the product on `s`; `scratch` holds scratch_bytes(path) bytes.
+// Run the product on `s`; `work` holds scratch_bytes(path) bytes of device memory.
 rdl_status run_linear(WType t, bool native, const uint8_t* w_dev, size_t n, size_t k,
-                      const float* x_dev, size_t m, float* y_dev, void* scratch, hipStream_t s,
+                      const float* x_dev, size_t m, float* y_dev, void* work, hipStream_t s,
                       Path path) {
     if (m == 0 || n == 0) return RDL_OK;
     // k == 0: no blocks; the GEMV then writes zeros (empty dot, as in the reference).
     if (k == 0) {
-        HIP_TRY(rdl::launch_gemv(t, native, w_dev, n, k, scratch, m, y_dev, s));
+        HIP_TRY(rdl::launch_gemv(t, native, w_dev, n, k, work, m, y_dev, s));
         return RDL_OK;
     }
     if (path == Path::Fused) {
@@ -179,10 +179,10 @@ rdl_status run_linear(WType t, bool native, const uint8_t* w_dev, size_t n, size
         return RDL_OK;
     }
     if (path == Path::Gemm) {
-        HIP_TRY(rdl::launch_gemm_q4_0(w_dev, n, k, x_dev, m, y_dev, scratch, s));
+        HIP_TRY(rdl::launch_gemm_q4_0(w_dev, n, k, x_dev, m, y_dev, work, s));
         return RDL_OK;
     }
-    void* xrec = scratch;
+    void* xrec = work;
     if (native)
         HIP_TRY(rdl::launch_prep_native(x_dev, m, k, (NativeRec*)xrec, nullptr, nullptr, s));
     else
@@ -308,14 +308,13 @@ rdl_status rdl_quantize_row_q8_0(const float* input, size_t input_len, uint8_t* 
     if (!input || !output || !scales) return fail(RDL_ERR_NULL_POINTER, "NULL buffer");
     rdl_status st = require_device();
     if (st != RDL_OK) return st;
-    DevBuf dx, dq, ds, dr;
+    DevBuf dx, dq, ds;
     HIP_TRY(dx.alloc(input_len * sizeof(float)));
     HIP_TRY(dq.alloc(nb * rdl::Q8_0_BYTES));
     HIP_TRY(ds.alloc(nb * sizeof(float)));
-    HIP_TRY(dr.alloc(nb * sizeof(NativeRec)));
     HIP_TRY(hipMemcpy(dx.p, input, input_len * sizeof(float), hipMemcpyHostToDevice));
-    HIP_TRY(rdl::launch_prep_native((const float*)dx.p, 1, input_len, (NativeRec*)dr.p,
-                                    (uint8_t*)dq.p, (float*)ds.p, nullptr));
+    HIP_TRY(rdl::launch_prep_native((const float*)dx.p, 1, input_len, nullptr, (uint8_t*)dq.p,
+                                    (float*)ds.p, nullptr));
     HIP_TRY(hipMemcpy(output, dq.p, nb * rdl::Q8_0_BYTES, hipMemcpyDeviceToHost));
     HIP_TRY(hipMemcpy(scales, ds.p, nb * sizeof(float), hipMemcpyDeviceToHost));
     return ok();
@@ -510,13 +509,7 @@ rdl_status rdl_quantize_row_q8_0_dev(const float* x_dev, size_t n, uint8_t* out_
         return fail(RDL_ERR_BLOCK_ALIGNMENT, "Q8_0 requires element count divisible by 32, got %zu", n);
     if (n == 0) return ok();
     if (!x_dev || !out_dev) return fail(RDL_ERR_NULL_POINTER, "NULL device pointer");
-    hipStream_t s = (hipStream_t)stream;
-    void* rec = nullptr;
-    HIP_TRY(hipMallocAsync(&rec, (n / rdl::QK) * sizeof(NativeRec), s));
-    hipError_t e = rdl::launch_prep_native(x_dev, 1, n, (NativeRec*)rec, out_dev, scales_dev, s);
-    hipError_t e2 = hipFreeAsync(rec, s);
-    HIP_TRY(e);
-    HIP_TRY(e2);
+    HIP_TRY(rdl::launch_prep_native(x_dev, 1, n, nullptr, out_dev, scales_dev, (hipStream_t)stream));
     return ok();
 }
 

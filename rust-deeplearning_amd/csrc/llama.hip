@@ -351,6 +351,11 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attention_kernel(
         po[0] = M;
         po[1] = L;
     }
+    // Publication order: every thread that stored partials releases them at
+    // agent scope itself (its wave waits for its own stores and writes the
+    // XCD's L2 back) before the barrier.  A barrier alone does not wait for
+    // other waves' stores, so thread 0's release could not cover them.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
     __syncthreads();
     if (threadIdx.x == 0) {
         int* cnt = counters + (size_t)s * n_heads + h;
@@ -360,6 +365,9 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attention_kernel(
     }
     __syncthreads();
     if (!last) return;
+    // every wave that reads the other workgroups' partials acquires them
+    // (invalidates its L1 and the XCD's L2 lines) after the counter said so
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     const float* pb = part + ((size_t)s * n_heads + h) * nspan * (hd + 2);
     if (w == 0) {
         float MM = -__builtin_inff();

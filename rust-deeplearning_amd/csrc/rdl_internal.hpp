@@ -129,8 +129,8 @@ inline void launch_kernel(F kernel, dim3 grid, dim3 block, size_t lds, hipStream
 
 // x [m, k] f32 -> FloatRec [m, k/32]
 hipError_t launch_prep_float(const float* x, size_t m, size_t k, FloatRec* rec, hipStream_t s);
-// x [m, k] f32 -> NativeRec [m, k/32]; optionally also the Q8_0 bytes
-// [m, k/32 * 34] and the f32 scales [m, k/32] of quantize_row_q8_0.
+// x [m, k] f32 -> NativeRec [m, k/32] (rec may be NULL); optionally also the
+// Q8_0 bytes [m, k/32 * 34] and the f32 scales [m, k/32] of quantize_row_q8_0.
 hipError_t launch_prep_native(const float* x, size_t m, size_t k, NativeRec* rec,
                               uint8_t* q8_bytes, float* scales, hipStream_t s);
 

@@ -60,13 +60,15 @@ __global__ __launch_bounds__(PREP_THREADS) void prep_native_kernel(
     const int qsum = group_sum32(q);
     if (!valid) return;
 
-    NativeRec* out = rec + blk;
-    reinterpret_cast<int8_t*>(out->q)[j] = (int8_t)q;
-    if (j == 0) {
-        out->scale = rt;
-        out->qsum = qsum;
-        out->pad[0] = 0;
-        out->pad[1] = 0;
+    if (rec) {  // NULL: only the Q8_0 bytes / scales are wanted
+        NativeRec* out = rec + blk;
+        reinterpret_cast<int8_t*>(out->q)[j] = (int8_t)q;
+        if (j == 0) {
+            out->scale = rt;
+            out->qsum = qsum;
+            out->pad[0] = 0;
+            out->pad[1] = 0;
+        }
     }
     if (q8_bytes) {
         uint8_t* ob = q8_bytes + blk * Q8_0_BYTES;

@@ -350,3 +350,64 @@ def test_typed_create_rejects(rq, gpu):
     m = LlamaModel(tiny_config(), types={(L.WO, 0): 8})
     with pytest.raises(rq.DeviceError):
         m.init_random(1)
+
+
+def test_config5_head_grouping_against_oracle(rq, gpu):
+    """BASELINE config 5's attention grouping (32 query heads over 8 KV heads
+    of dim 128, hidden 4096) on a 2-layer model with an f32 cache: prefill
+    and decode logits within the bar of LlamaRef, greedy tokens equal."""
+    cfg = tiny_config(dim=4096, n_layers=2, n_heads=32, n_kv_heads=8, head_dim=128, ffn_dim=512,
+                      vocab=320, max_seq=64, kv_f16=False)
+    print("case config-5 grouping 32/8 x 128, 2 layers", flush=True)
+    m, ref = build(cfg, seed=505)
+    prompt = [3, 141, 59, 26, 53, 58, 97, 93, 23]
+    assert_close(m.forward_with_cache(prompt), ref.forward_with_cache(prompt))
+    tok = 17
+    for _ in range(4):
+        got = m.decode_step(tok)
+        want = ref.forward_with_cache([tok])
+        assert_close(got, want)
+        tok = argmax(want)
+    m.reset()
+    gen = m.generate_greedy(prompt, 5)
+    ref2 = LlamaRef(cfg, ref.w)
+    want_toks, logits = [], ref2.forward_with_cache(prompt)
+    for _ in range(5):
+        want_toks.append(argmax(logits))
+        logits = ref2.forward_with_cache([want_toks[-1]])
+    assert gen.tolist() == want_toks
+
+
+@pytest.mark.parametrize("kv_f16", [False, True])
+def test_long_context_four_spans(rq, gpu, kv_f16):
+    """1,900-1,906 cached keys at head dim 128: four 512-key attention
+    workgroups per row whose partials the last one to finish combines."""
+    cfg = tiny_config(dim=256, n_heads=2, n_kv_heads=1, head_dim=128, max_seq=2048, max_batch=128,
+                      kv_f16=kv_f16)
+    print(f"case four spans kv_f16={kv_f16}", flush=True)
+    m, ref = build(cfg, seed=19)
+    prompt = np.random.default_rng(23).integers(0, cfg.vocab, 1900)
+    for c0 in range(0, 1900, 128):
+        got = m.forward_with_cache(prompt[c0:c0 + 128])
+        want = ref.forward_with_cache(prompt[c0:c0 + 128])
+
+    def close(got, want):
+        if kv_f16:  # the f16 cache rounds K and V to 11 significant bits
+            assert np.max(np.abs(got - want)) <= 1e-2 * np.abs(want).max()
+        else:
+            assert_close(got, want)
+
+    close(got, want)
+    tok = argmax(want)
+    for _ in range(3):
+        got, want = m.decode_step(tok), ref.forward_with_cache([tok])
+        close(got, want)
+        tok = argmax(want)
+    gen = m.generate_greedy([tok], 3)
+    want_toks, logits = [], ref.forward_with_cache([tok])
+    for _ in range(3):
+        want_toks.append(argmax(logits))
+        logits = ref.forward_with_cache([want_toks[-1]])
+    if not kv_f16:
+        assert gen.tolist() == want_toks
+    assert m.position == 1900 + 3 + 3

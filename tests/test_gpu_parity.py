@@ -169,3 +169,38 @@ def test_nan_activation_poisons_outputs(rq, gpu):
     x = synth.activations(1, k, 13)
     x[0, 40] = np.nan
     assert np.all(np.isnan(rq.matmul_f32_q4(x, w, 1, k, n)))
+
+
+# ---- native mode at prefill row counts (config-4 weight, 4096 x 4096) -----------------
+def _native_exact(orc, x, w, m, k, n):
+    """f64 value of matmul_f32_q4_native (quantize.rs:326-394): the exact int32
+    block dots times the f16-rounded activation scale and the weight scale."""
+    part = orc.block_dots(x, w, m, k, n).astype(np.float64)
+    sw = w.reshape(n, k // 32, 18)[:, :, 0:2].copy().view(np.float16).astype(np.float64)[..., 0]
+    sx = np.stack([orc.quantize_row_q8_0(x[r])[1] for r in range(m)]).astype(np.float64)
+    return (part.reshape(m, n, k // 32) * sx[:, None, :] * sw[None]).sum(axis=2).reshape(-1), part
+
+
+@pytest.mark.parametrize("m", [5, 16, 64, 512])
+def test_native_q4_0_prefill_rows_config4(rq, orc, gpu, m):
+    n = k = 4096
+    print(f"case native q4_0 m={m} n={n} k={k}", flush=True)
+    x = synth.activations(m, k, 0x5EED0104 + m)
+    w = synth.q4_0_weights(n, k, 0x5EED0004)
+    if m <= 16:
+        exact, part = _native_exact(orc, x, w, m, k, n)
+        # the integer stage, bit for bit (simd.rs:562-581)
+        assert np.array_equal(rq.q4_0_q8_0_block_dots(x, w, m, k, n).astype(np.float64), part)
+        check_parity(rq.matmul_f32_q4_native(x, w, m, k, n), orc.matmul("q4_native", x, w, m, k, n, 8), exact)
+    else:
+        want = orc.matmul("q4_native", x, w, m, k, n, 8)
+        assert_close(rq.matmul_f32_q4_native(x, w, m, k, n), want)
+
+
+@pytest.mark.parametrize("m", [5, 16, 64, 512])
+def test_native_q4_1_prefill_rows_config4(rq, orc, gpu, m):
+    n = k = 4096
+    print(f"case native q4_1 m={m} n={n} k={k}", flush=True)
+    x = synth.activations(m, k, 0x5EED0204 + m)
+    w = synth.q4_1_weights(n, k, 0x5EED0014)
+    assert_close(rq.matmul_f32_q4_1_native(x, w, m, k, n), orc.matmul("q4_1_native", x, w, m, k, n, 8))

@@ -64,3 +64,120 @@ def test_cached_decode_matches_full_causal_pass():
     assert np.allclose(step, full, rtol=1e-4, atol=1e-5)
     # and the cache positions advanced alike
     assert a.pos == b.pos == len(toks)
+
+
+# ---- closed-form pins of the pieces LlamaRef composes ---------------------------------------
+from oracle import llama_ref as LR  # noqa: E402
+
+
+@pytest.mark.parametrize("hd,pos", [(8, 3), (128, 37), (64, 0)])
+def test_rope_unit_vectors_rotate_half_split_pairs(hd, pos):
+    # rope.rs:189-190: element i pairs with i + D/2 (not 2i / 2i+1), and the
+    # pair rotates by pos * theta^(-2i/D)
+    cos, sin = orc.rope_tables(hd, pos + 1, 10000.0)
+    half = hd // 2
+    ang = pos * (1.0 / 10000.0 ** (2.0 * np.arange(half) / hd))
+    for i in range(half):
+        e = np.zeros((1, 1, hd), np.float32)
+        e[0, 0, i] = 1.0
+        out = LR.rope_apply(e, cos, sin, pos)[0, 0].astype(np.float64)
+        want = np.zeros(hd)
+        want[i], want[i + half] = np.cos(ang[i]), np.sin(ang[i])
+        assert np.max(np.abs(out - want)) < 2e-5, i
+        e[0, 0, i], e[0, 0, i + half] = 0.0, 1.0
+        out = LR.rope_apply(e, cos, sin, pos)[0, 0].astype(np.float64)
+        want[i], want[i + half] = -np.sin(ang[i]), np.cos(ang[i])
+        assert np.max(np.abs(out - want)) < 2e-5, i
+
+
+def test_rope_rows_follow_start_position():
+    # a row at offset j of a chunk starting at `start` rotates as position start + j
+    cos, sin = orc.rope_tables(16, 12, 10000.0)
+    x = np.random.default_rng(3).standard_normal((2, 4, 16)).astype(np.float32)
+    chunk = LR.rope_apply(x, cos, sin, 5)
+    for j in range(4):
+        assert np.array_equal(chunk[:, j:j + 1], LR.rope_apply(x[:, j:j + 1], cos, sin, 5 + j))
+
+
+def test_attention_one_cached_key_returns_its_value_row():
+    # softmax over one key is exactly 1, whatever q: the context is V's row
+    rng = np.random.default_rng(8)
+    q = rng.standard_normal((3, 1, 32)).astype(np.float32) * 50
+    kc = rng.standard_normal((3, 1, 32)).astype(np.float32)
+    vc = rng.standard_normal((3, 1, 32)).astype(np.float32)
+    ctx = LR.attention(q, kc, vc, 0)
+    assert np.array_equal(ctx[:, 0], vc[:, 0])
+
+
+def test_attention_gqa_head_map():
+    # 8 query heads over 2 KV heads: head h reads KV head h // 4
+    # (repeat_kv repeats each KV head n_rep times in a row, ops.rs:981-987,
+    # attention.rs:406-409); equal scores (q = 0) over 4 keys and a constant
+    # V per KV head make each head's context exactly that constant
+    nh, nkv, t, hd = 8, 2, 4, 16
+    q = np.zeros((nh, 1, hd), np.float32)
+    kc = np.random.default_rng(1).standard_normal((nkv, t, hd)).astype(np.float32)
+    vc = np.stack([np.full((t, hd), 10.0 * (g + 1), np.float32) for g in range(nkv)])
+    ctx = LR.attention(q, kc, vc, t - 1)
+    for h in range(nh):
+        assert np.all(ctx[h, 0] == 10.0 * (h // 4 + 1)), h
+    # a modulo map (h % n_kv) would give head 1 the second KV head
+    assert ctx[1, 0, 0] != 10.0 * (1 % nkv + 1)
+
+
+def test_attention_two_key_softmax_and_scale():
+    # scores q.k / sqrt(D) (attention.rs:414-415), softmax (ops.rs:582-628):
+    # with q.k1 - q.k2 = 3 and D = 4 the weights are 1 / (1 + e^-1.5) and the rest
+    hd = 4
+    q = np.array([[[1.0, 0, 0, 0]]], np.float32)
+    kc = np.array([[[2.0, 0, 0, 0], [-1.0, 0, 0, 0]]], np.float32)
+    vc = np.array([[[1.0, 0, 0, 0], [0, 1.0, 0, 0]]], np.float32)
+    ctx = LR.attention(q, kc, vc, 1)[0, 0].astype(np.float64)
+    w1 = 1.0 / (1.0 + np.exp(-3.0 / np.sqrt(hd)))
+    assert abs(ctx[0] - w1) < 1e-6 and abs(ctx[1] - (1 - w1)) < 1e-6
+    assert ctx[2] == 0 and ctx[3] == 0
+    # unscaled scores would weight the first key 1 / (1 + e^-3)
+    assert abs(ctx[0] - 1.0 / (1.0 + np.exp(-3.0))) > 0.1
+
+
+def test_attention_causal_rows():
+    # a prefill chunk of 2 rows at positions 0, 1: row 0 sees key 0 only
+    # (Tensor::causal_mask keeps j <= i + offset, ops.rs:905-916)
+    rng = np.random.default_rng(4)
+    q = rng.standard_normal((1, 2, 8)).astype(np.float32)
+    kc = rng.standard_normal((1, 2, 8)).astype(np.float32)
+    vc = rng.standard_normal((1, 2, 8)).astype(np.float32)
+    ctx = LR.attention(q, kc, vc, 0)
+    assert np.array_equal(ctx[0, 0], vc[0, 0])
+    assert not np.allclose(ctx[0, 1], vc[0, 0])
+
+
+def test_swiglu_is_silu_of_gate_times_up():
+    # feed_forward.rs:146-148: silu(gate) * up, silu(g) = g / (1 + e^-g)
+    g = np.array([1.0, -2.0, 0.5, 3.0], np.float32)
+    u = np.array([3.0, 0.25, -1.0, 2.0], np.float32)
+    got = LR.swiglu(g, u).astype(np.float64)
+    gd, ud = g.astype(np.float64), u.astype(np.float64)
+    want = gd / (1.0 + np.exp(-gd)) * ud
+    assert np.allclose(got, want, rtol=1e-6, atol=0)
+    swapped = ud / (1.0 + np.exp(-ud)) * gd
+    assert not np.allclose(got, swapped, rtol=1e-2)
+
+
+def test_forward_uses_the_pinned_pieces(monkeypatch):
+    # the decode oracle composes exactly the functions pinned above
+    calls = {"rope": 0, "att": 0, "swiglu": 0}
+
+    def wrap(name, f):
+        def g(*a, **k):
+            calls[name] += 1
+            return f(*a, **k)
+        return g
+
+    monkeypatch.setattr(LR, "rope_apply", wrap("rope", LR.rope_apply))
+    monkeypatch.setattr(LR, "attention", wrap("att", LR.attention))
+    monkeypatch.setattr(LR, "swiglu", wrap("swiglu", LR.swiglu))
+    cfg = tiny_config(n_layers=2)
+    _, ref_w = tiny_weights(cfg, seed=5)
+    LlamaRef(cfg, ref_w).forward_with_cache([1, 2, 3])
+    assert calls == {"rope": 4, "att": 2, "swiglu": 2}
