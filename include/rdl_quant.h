@@ -169,6 +169,21 @@ rdl_status rdl_weight_free(rdl_weight* w);
 rdl_status rdl_linear_forward_dev(const rdl_weight* w, const float* x_dev, size_t m,
                                   float* y_dev, int32_t mode, void* stream);
 
+/* rdl_linear_forward_dev without any device allocation.  No counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, serving loops, harnesses that forbid hipMalloc).
+ * Where rdl_linear_forward_dev allocates stream-ordered scratch (the
+ * activation split of the prefill GEMM, activation records for m > 4 in
+ * native mode or for other types), this entry point uses one static device
+ * array of RDL_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends;
+ * products needing more return RDL_ERR_UNSUPPORTED before launching anything.
+ * Every call on one GPU shares that array: calls that overlap in time on one
+ * GPU (other streams, other threads) race and must be serialized by the
+ * caller.  Results equal rdl_linear_forward_dev's (same kernels). */
+#define RDL_NOALLOC_SCRATCH_BYTES (16u << 20)
+rdl_status rdl_linear_forward_dev_noalloc(const rdl_weight* w, const float* x_dev, size_t m,
+                                          float* y_dev, int32_t mode, void* stream);
+
 /* ---- device building blocks ----------------------------------------------
  * The product kernels read activations as per-32-element "records" (an exact
  * 24-bit fixed-point code in float mode, the Q8_0 code of quantize_row_q8_0 in

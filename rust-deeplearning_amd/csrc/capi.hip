@@ -9,6 +9,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "../../include/rdl_quant.h"
@@ -188,6 +189,34 @@ rdl_status run_linear(WType t, bool native, const uint8_t* w_dev, size_t n, size
     else
         HIP_TRY(rdl::launch_prep_float(x_dev, m, k, (FloatRec*)xrec, s));
     HIP_TRY(rdl::launch_gemv(t, native, w_dev, n, k, xrec, m, y_dev, s));
+    return RDL_OK;
+}
+
+// ---- static scratch of rdl_linear_forward_dev_noalloc ----------------------
+// One array per device, for callers that cannot allocate.  In host code the
+// name `scratch` is only a stand-in for the symbol: its device address comes
+// from hipGetSymbolAddress, taken once per device (with that device current)
+// and kept in scratch_dev[]; only that address is ever passed to kernels.
+__device__ __align__(256) uint8_t scratch[RDL_NOALLOC_SCRATCH_BYTES];
+
+constexpr int MAX_DEVICES = 64;
+std::mutex scratch_mu;
+void* scratch_dev[MAX_DEVICES] = {};
+
+// The current device's address of `scratch`.
+rdl_status noalloc_scratch(void** out) {
+    int dev = 0;
+    HIP_TRY(hipGetDevice(&dev));
+    if (dev < 0 || dev >= MAX_DEVICES) return fail(RDL_ERR_UNSUPPORTED, "device index %d beyond %d", dev, MAX_DEVICES);
+    std::lock_guard<std::mutex> lock(scratch_mu);
+    if (!scratch_dev[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return fail(RDL_ERR_HIP, "hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));
+        scratch_dev[dev] = p;
+    }
+    *out = scratch_dev[dev];
     return RDL_OK;
 }
 
@@ -439,6 +468,30 @@ rdl_status rdl_linear_forward_dev(const rdl_weight* w, const float* x_dev, size_
         if (st == RDL_OK && e != hipSuccess)
             return fail(RDL_ERR_HIP, "hipFreeAsync failed: %s", hipGetErrorString(e));
     }
+    return st == RDL_OK ? ok() : st;
+}
+
+rdl_status rdl_linear_forward_dev_noalloc(const rdl_weight* w, const float* x_dev, size_t m, float* y_dev,
+                                          int32_t mode, void* stream) {
+    if (!w) return fail(RDL_ERR_NULL_POINTER, "weight handle is NULL");
+    if (mode != RDL_MODE_FLOAT && mode != RDL_MODE_NATIVE)
+        return fail(RDL_ERR_INVALID_DATA, "unknown mode %d", mode);
+    if (m == 0 || w->n == 0) return ok();
+    if (!x_dev || !y_dev) return fail(RDL_ERR_NULL_POINTER, "NULL activation pointer");
+    const bool native = mode == RDL_MODE_NATIVE && (w->type == WType::Q4_0 || w->type == WType::Q4_1);
+    const Path path = pick_path(w->type, native, m, w->n, w->k, x_dev, w->gemm_ok);
+    const size_t rb = scratch_bytes(path, native, m, w->k);
+    if (rb > (size_t)RDL_NOALLOC_SCRATCH_BYTES)
+        return fail(RDL_ERR_UNSUPPORTED,
+                    "m=%zu rows of in_features %zu need %zu scratch bytes; the static scratch holds %zu",
+                    m, w->k, rb, (size_t)RDL_NOALLOC_SCRATCH_BYTES);
+    void* work = nullptr;
+    if (rb) {
+        rdl_status st = noalloc_scratch(&work);
+        if (st != RDL_OK) return st;
+    }
+    rdl_status st = run_linear(w->type, native, (const uint8_t*)w->dev, w->n, w->k, x_dev, m, y_dev, work,
+                               (hipStream_t)stream, path);
     return st == RDL_OK ? ok() : st;
 }
 

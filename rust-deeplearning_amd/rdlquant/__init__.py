@@ -100,6 +100,8 @@ _decl("rdl_weight_upload", _i32, _u8p, _sz, _i32, _sz, _sz, C.POINTER(_p))
 _decl("rdl_weight_wrap_device", _i32, _p, _sz, _i32, _sz, _sz, C.POINTER(_p))
 _decl("rdl_weight_free", _i32, _p)
 _decl("rdl_linear_forward_dev", _i32, _p, _p, _sz, _p, _i32, _p)
+_decl("rdl_linear_forward_dev_noalloc", _i32, _p, _p, _sz, _p, _i32, _p)
+NOALLOC_SCRATCH_BYTES = 16 << 20  # RDL_NOALLOC_SCRATCH_BYTES
 _decl("rdl_activation_record_bytes", _sz, _sz, _sz, _i32)
 _decl("rdl_prepare_activations_dev", _i32, _p, _sz, _sz, _i32, _p, _p)
 _decl("rdl_linear_prepared_dev", _i32, _p, _p, _sz, _p, _i32, _p)
@@ -297,6 +299,11 @@ class Weight:
 
     def forward_dev(self, x_ptr, m, y_ptr, mode=MODE_FLOAT, stream=0):
         check(lib.rdl_linear_forward_dev(self.handle, x_ptr, m, y_ptr, mode, stream))
+
+    def forward_dev_noalloc(self, x_ptr, m, y_ptr, mode=MODE_FLOAT, stream=0):
+        """rdl_linear_forward_dev_noalloc: the same product with no device
+        allocation (a static per-GPU scratch array; overlapping calls race)."""
+        check(lib.rdl_linear_forward_dev_noalloc(self.handle, x_ptr, m, y_ptr, mode, stream))
 
     def forward_prepared_dev(self, rec_ptr, m, y_ptr, mode=MODE_FLOAT, stream=0):
         check(lib.rdl_linear_prepared_dev(self.handle, rec_ptr, m, y_ptr, mode, stream))
