@@ -34,6 +34,7 @@ sys.path.insert(0, os.path.join(ROOT, "rust-deeplearning_amd"))
 METRIC = "Q4_0/Q4_K GEMV achieved HBM GB/s (% peak); 7B Q4_0 decode tokens/s"
 PEAK_HBM_GBPS = 8000.0
 PEAK_F16_TFLOPS = 2500.0  # dense f16/bf16 MFMA, MI355X
+PEAK_I8_TOPS = 5000.0     # dense int8 MFMA, MI355X
 N_OUT, K_IN = 11008, 4096
 SEED = 0x5EED0002
 # the kernel the library launches for this workload (8-wave workgroups, 3 rows per wave)
@@ -144,6 +145,105 @@ def cpu_baseline_q4k(n, k, seed, budget_s=3.0):
     }
 
 
+def _timed(fn, budget_s, min_runs=3):
+    """Median seconds of fn() over a time budget (at least min_runs calls)."""
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < min_runs:
+        t0 = time.perf_counter()
+        fn(len(times))
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
+def cpu_baseline_q8(budget_s=3.0):
+    """matmul_f32_q8 at M = 1 (quantize.rs:201-260), one rayon task
+    per input row -> one core, restated in C and timed on this host."""
+    from oracle import oracle as orc
+    from rdlquant import synth
+
+    n = k = 4096
+    copies = 8  # 8 x 17.8 MB rotated past the host LLC
+    ws = [synth.q8_0_weights(n, k, 0x5EED0001 + i) for i in range(copies)]
+    x = synth.activations(1, k, 0x5EED0101)
+    orc.matmul("q8", x, ws[0], 1, k, n, threads=1)
+    med, runs = _timed(lambda i: orc.matmul("q8", x, ws[i % copies], 1, k, n, threads=1), budget_s)
+    return {
+        "value": round(algorithmic_bytes(n, k, 8) / med / 1e9, 3),
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"{runs} single-thread matmul_f32_q8 calls, 4096x4096 Q8_0, M=1, median {med * 1e3:.2f} ms, "
+                  f"weights rotated over {copies} copies",
+    }
+
+
+def cpu_baseline_gemm(m, budget_s=3.0):
+    """matmul_f32_q4 (the Linear default) at M rows, the reference
+    decomposition -- one rayon task per input row (quantize.rs:284-287) over
+    min(M, host cores) threads -- restated in C and timed on this host."""
+    from oracle import oracle as orc
+    from rdlquant import synth
+
+    n = k = 4096
+    threads = min(m, 16, os.cpu_count() or 1)
+    # bounded sample: each thread's rows run one after another, so a call over
+    # ms = 2 * threads rows (two rows a thread) times the same per-row work;
+    # the M-row call is ceil(M / threads) / 2 times as long
+    ms = min(m, 2 * threads)
+    w = synth.q4_0_weights(n, k, 0x5EED0004)
+    x = synth.activations(ms, k, 0x5EED0104 + m)
+    med, runs = _timed(lambda i: orc.matmul("q4", x, w, ms, k, n, threads=threads), budget_s, min_runs=2)
+    call = med * (-(-m // threads)) / (-(-ms // threads))
+    flops = 2.0 * m * n * k
+    return {
+        "value": round(flops / call / 1e12, 5),
+        "unit": "TFLOP/s",
+        "gbs": round((n * (k // 32) * 18 + 4 * m * (k + n)) / call / 1e9, 3),
+        "ms_per_call": round(call * 1e3, 1),
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{runs} matmul_f32_q4 calls over {ms} of the {m} rows (4096x4096 Q4_0), input rows split "
+                  f"over {threads} threads, median {med * 1e3:.1f} ms, scaled to {-(-m // threads)} rows a thread",
+    }
+
+
+def cpu_baseline_decode(budget_s=6.0):
+    """one 7B decode token on the reference's path is 32 layers of
+    seven Q4_0 Linears at M = 1 (each one rayon task -> one core,
+    quantize.rs:284-287) plus the Q4_0 lm_head; restated in C and timed on this
+    host over one layer's matrices and the lm_head, scaled to 32 layers.  The
+    non-matmul ops (RMSNorm, RoPE, attention over <= 384 cached rows, SwiGLU)
+    are below 0.1% of that time on the reference and are not timed."""
+    from oracle import oracle as orc
+    from rdlquant import synth
+
+    d, f, kv, vocab = 4096, 14336, 1024, 32000
+    shapes = [("q", d, d), ("k", kv, d), ("v", kv, d), ("o", d, d), ("gate", f, d), ("up", f, d), ("down", d, f)]
+    mats = {name: synth.q4_0_weights(n, k, 0x5EED0500 + i) for i, (name, n, k) in enumerate(shapes)}
+    out_w = synth.q4_0_weights(vocab, d, 0x5EED0599)
+    xs = {k: synth.activations(1, k, 0x5EED0600 + k) for k in (d, f)}
+
+    def layer(_):
+        for name, n, k in shapes:
+            orc.matmul("q4", xs[k], mats[name], 1, k, n, threads=1)
+
+    layer(0)
+    lmed, lruns = _timed(layer, budget_s * 0.8, min_runs=2)
+    hmed, hruns = _timed(lambda i: orc.matmul("q4", xs[d], out_w, 1, d, vocab, threads=1), budget_s * 0.2,
+                         min_runs=2)
+    per_token = 32 * lmed + hmed
+    return {
+        "value": round(1.0 / per_token, 4),
+        "unit": "tokens/s",
+        "ms_per_token": round(per_token * 1e3, 1),
+        "cores": 1,
+        "kind": "port",
+        "sample": f"one layer's seven Q4_0 matmul_f32_q4 calls at M=1 ({lruns} runs, median {lmed * 1e3:.1f} ms) "
+                  f"x 32 layers + the 32000x4096 lm_head ({hruns} runs, median {hmed * 1e3:.1f} ms), one thread",
+    }
+
+
 class Rig:
     """Device, stream and rotating weight copies for the GEMV/GEMM timings."""
 
@@ -214,6 +314,33 @@ class Rig:
         return ms_per_step, kern_ms
 
 
+def native_check(rig, w_host, x, y, m, n, k):
+    """Native mode: y within 1e-3 rel + 1e-4 abs of the exact (f64) product of
+    the Q8_0-quantized x (the library's byte-exact quantize_row_q8_0, codes
+    times scales) with the weight's f32 values -- the real value of
+    matmul_f32_q4_native's sum of int32 block dots times both block scales."""
+    torch, rq = rig.torch, rig.rq
+    nb = k // 32
+    q8 = torch.empty(m * nb * 34, dtype=torch.uint8, device=rig.dev)
+    for r in range(m):
+        rq.quantize_row_q8_0_dev(x.reshape(m, k)[r].data_ptr(), k, q8[r * nb * 34:].data_ptr(), 0,
+                                 rig.stream.cuda_stream)
+    blk = q8.reshape(m, nb, 34)
+    sc = blk[:, :, 0:2].contiguous().view(torch.float16).double()             # [m, nb, 1]
+    codes = blk[:, :, 2:].contiguous().view(torch.int8).double()             # [m, nb, 32]
+    xq = (codes * sc).reshape(m, k)
+    wt = rq.Weight.upload(w_host, rq.DTYPE_Q4_0, n, k)
+    rows = torch.arange(n, dtype=torch.int32, device=rig.dev)
+    wf = torch.empty(n, k, dtype=torch.float32, device=rig.dev)
+    wt.dequantize_rows_dev(rows.data_ptr(), n, wf.data_ptr(), rig.stream.cuda_stream)
+    want = xq @ wf.double().T
+    got = y.reshape(m, n).double()
+    ok = bool(((got - want).abs() <= 1e-4 + 1e-3 * want.abs()).all().item())
+    wt.free()
+    del wf, q8
+    return ok
+
+
 def exact_check(rig, weight, x, y, m, n, k):
     """y within 1e-3 rel + 1e-4 abs of the exact (f64) product over the weight's
     f32 values (Tensor::to_f32 / dequantize_q4k, expanded by the library's
@@ -263,11 +390,13 @@ def gemv_line(rig, name, dtype, n, k, seed, steps, warmup):
     }
 
 
-def gemm_lines(rig, ms_list, seed=0x5EED0004):
+def gemm_lines(rig, ms_list, seed=0x5EED0004, native=False):
     """Y = X W^T, W 4096x4096 Q4_0, X f32 [M, 4096]; the whole call
-    (activation split + MFMA GEMM) timed over a loop of launches."""
+    (activation split or Q8_0 quantization + MFMA GEMM) timed over a loop of
+    launches.  native: matmul_f32_q4_native (int8 MFMA on the Q8_0 codes)."""
     torch, rq = rig.torch, rig.rq
     n = k = 4096
+    mode = rq.MODE_NATIVE if native else rq.MODE_FLOAT
     w_host, weights = rig.weight_copies(2, n, k, seed, min_copies=16)
     s = rig.stream
     out = []
@@ -276,25 +405,27 @@ def gemm_lines(rig, ms_list, seed=0x5EED0004):
         x = torch.from_numpy(x_host).to(rig.dev)
         y = torch.empty(m, n, dtype=torch.float32, device=rig.dev)
         for i in range(10):
-            weights[i % len(weights)][1].forward_dev(x.data_ptr(), m, y.data_ptr(), rq.MODE_FLOAT, s.cuda_stream)
+            weights[i % len(weights)][1].forward_dev(x.data_ptr(), m, y.data_ptr(), mode, s.cuda_stream)
         torch.cuda.synchronize()
         it = 200 if m <= 512 else 60
         a = torch.cuda.Event(enable_timing=True)
         b = torch.cuda.Event(enable_timing=True)
         a.record(s)
         for i in range(it):
-            weights[i % len(weights)][1].forward_dev(x.data_ptr(), m, y.data_ptr(), rq.MODE_FLOAT, s.cuda_stream)
+            weights[i % len(weights)][1].forward_dev(x.data_ptr(), m, y.data_ptr(), mode, s.cuda_stream)
         b.record(s)
         torch.cuda.synchronize()
         ms = a.elapsed_time(b) / it
         flops = 2.0 * m * n * k
         abytes = n * (k // 32) * 18 + 4 * m * k + 4 * m * n
-        ok = exact_check(rig, weights[0][1], x, y, m, n, k)
+        ok = native_check(rig, w_host, x, y, m, n, k) if native else exact_check(rig, weights[0][1], x, y, m, n, k)
         tflops = flops / (ms * 1e-3) / 1e12
         gbps = abytes / (ms * 1e-3) / 1e9
-        bound = "mfma" if flops / abytes > PEAK_F16_TFLOPS * 1e12 / (PEAK_HBM_GBPS * 1e9) else "hbm"
+        peak_mm = PEAK_I8_TOPS if native else PEAK_F16_TFLOPS
+        bound = "mfma" if flops / abytes > peak_mm * 1e12 / (PEAK_HBM_GBPS * 1e9) else "hbm"
         out.append({
-            "workload": f"config4 M={m}",
+            "workload": f"config4 M={m}" + (" native (matmul_f32_q4_native, int8 MFMA)" if native else ""),
+            "m": m,
             "value": round(tflops, 2),
             "unit": "TFLOP/s",
             "ms_per_call": round(ms, 5),
@@ -302,9 +433,9 @@ def gemm_lines(rig, ms_list, seed=0x5EED0004):
             "roofline": {
                 "bound": bound,
                 "achieved": round(tflops, 2) if bound == "mfma" else round(gbps, 1),
-                "peak": PEAK_F16_TFLOPS if bound == "mfma" else PEAK_HBM_GBPS,
-                "unit": "TFLOP/s" if bound == "mfma" else "GB/s",
-                "frac": round(tflops / PEAK_F16_TFLOPS if bound == "mfma" else gbps / PEAK_HBM_GBPS, 4),
+                "peak": peak_mm if bound == "mfma" else PEAK_HBM_GBPS,
+                "unit": ("TOP/s" if native else "TFLOP/s") if bound == "mfma" else "GB/s",
+                "frac": round(tflops / peak_mm if bound == "mfma" else gbps / PEAK_HBM_GBPS, 4),
             },
             "parity_vs_exact": ok,
         })
@@ -580,7 +711,7 @@ def main():
         elif wl == "q6_k":
             line = gemv_line(rig, Q6K_LM_HEAD, 14, 32000, 4096, 0x5EED0006, args.steps, args.warmup)
         elif wl == "gemm":
-            line = gemm_lines(rig, [16, 64, 512, 2048])
+            line = gemm_lines(rig, [16, 64, 512, 2048]) + gemm_lines(rig, [512, 2048], native=True)
         elif wl == "load":
             line = load_line(rig)
         elif wl == "decode_q4_k_m":
@@ -660,6 +791,7 @@ def main():
                                            0x5EED0013, sub_steps, sub_warm),
             "q6_k_lm_head": gemv_line(rig, Q6K_LM_HEAD, 14, 32000, 4096, 0x5EED0006, sub_steps, sub_warm),
             "config4_gemm": gemm_lines(rig, [16, 64, 512, 2048]),
+            "config4_gemm_native": gemm_lines(rig, [512, 2048], native=True),
             "config5_decode": decode_line(rig),
         }
     if not args.no_cpu:
@@ -668,6 +800,10 @@ def main():
             for key, (n, k, seed) in (("config3_q4_k_up", (14336, 4096, 0x5EED0003)),
                                       ("config3_q4_k_down", (4096, 14336, 0x5EED0013))):
                 out["workloads"][key]["cpu_baseline"] = cpu_baseline_q4k(n, k, seed)
+            out["workloads"]["config1_q8_0"]["cpu_baseline"] = cpu_baseline_q8()
+            for line in out["workloads"]["config4_gemm"]:
+                line["cpu_baseline"] = cpu_baseline_gemm(line["m"])
+            out["workloads"]["config5_decode"]["cpu_baseline"] = cpu_baseline_decode()
     print(json.dumps(out), flush=True)
 
 

@@ -30,7 +30,6 @@ struct rdl_weight {
     WType type;
     size_t n, k;
     bool owned;
-    bool gemm_ok;  // block scales fit the prefill GEMM's f16 operands
 };
 
 namespace rdl {
@@ -144,22 +143,26 @@ bool use_fused(WType t, size_t m, size_t n, size_t k, const float* x_dev) {
 }
 
 // How a product runs: one fused GEMV launch (m <= 4), the matrix-core GEMM
-// (Q4_0 float mode, more rows), or activation records + the records GEMV.
+// (Q4_0, more rows: f16 MFMA in float mode, int8 MFMA in native mode), or
+// activation records + the records GEMV.
 enum class Path { Fused, Gemm, Records };
 
-Path pick_path(WType t, bool native, size_t m, size_t n, size_t k, const float* x_dev, bool gemm_ok) {
+// The GEMM addresses x and W with 32-bit offsets.
+bool gemm_fits(WType t, size_t m, size_t n, size_t k) {
+    return t == WType::Q4_0 && k > 0 && (uint64_t)m * k * 2 <= rdl::FUSED_MAX_WEIGHT_BYTES &&
+           (uint64_t)n * (k / rdl::QK) * rdl::Q4_0_BYTES <= rdl::FUSED_MAX_WEIGHT_BYTES;
+}
+
+Path pick_path(WType t, bool native, size_t m, size_t n, size_t k, const float* x_dev) {
     if (use_fused(t, m, n, k, x_dev)) return Path::Fused;
-    if (!native && t == WType::Q4_0 && gemm_ok && k > 0 &&
-        (uint64_t)m * k * 2 <= rdl::FUSED_MAX_WEIGHT_BYTES &&
-        (uint64_t)n * (k / rdl::QK) * rdl::Q4_0_BYTES <= rdl::FUSED_MAX_WEIGHT_BYTES)
-        return Path::Gemm;
+    if (gemm_fits(t, m, n, k)) return Path::Gemm;
     return Path::Records;
 }
 
 size_t scratch_bytes(Path p, bool native, size_t m, size_t k) {
     switch (p) {
         case Path::Fused: return 0;
-        case Path::Gemm: return rdl::gemm_scratch_bytes(m, k);
+        case Path::Gemm: return rdl::gemm_scratch_bytes(m, k, native);
         case Path::Records: return rec_bytes(native, m, k);
     }
     return 0;
@@ -180,7 +183,10 @@ rdl_status run_linear(WType t, bool native, const uint8_t* w_dev, size_t n, size
         return RDL_OK;
     }
     if (path == Path::Gemm) {
-        HIP_TRY(rdl::launch_gemm_q4_0(w_dev, n, k, x_dev, m, y_dev, work, s));
+        if (native)
+            HIP_TRY(rdl::launch_gemm_q4_0_native(w_dev, n, k, x_dev, m, y_dev, nullptr, work, s));
+        else
+            HIP_TRY(rdl::launch_gemm_q4_0(w_dev, n, k, x_dev, m, y_dev, work, s));
         return RDL_OK;
     }
     void* xrec = work;
@@ -242,10 +248,7 @@ rdl_status host_matmul(WType t, bool native, const float* x, size_t x_len, const
     HIP_TRY(dy.alloc(m * n * sizeof(float)));
     HIP_TRY(hipMemcpy(dx.p, x, m * k * sizeof(float), hipMemcpyHostToDevice));
     HIP_TRY(hipMemcpy(dw.p, w, wb, hipMemcpyHostToDevice));
-    bool gemm_ok = false;
-    if (!native && t == WType::Q4_0 && m > FUSED_MAX_M)
-        HIP_TRY(rdl::gemm_scales_ok(t, (const uint8_t*)dw.p, n, k, &gemm_ok));
-    const Path path = pick_path(t, native, m, n, k, (const float*)dx.p, gemm_ok);
+    const Path path = pick_path(t, native, m, n, k, (const float*)dx.p);
     const size_t sb = scratch_bytes(path, native, m, k);
     if (sb) HIP_TRY(dr.alloc(sb));
     st = run_linear(t, native, (const uint8_t*)dw.p, n, k, (const float*)dx.p, m, (float*)dy.p,
@@ -365,15 +368,22 @@ rdl_status rdl_q4_0_q8_0_block_dots(const float* x, size_t x_len, const uint8_t*
     HIP_TRY(dx.alloc(m * k * sizeof(float)));
     HIP_TRY(dw.alloc(n * nb * rdl::Q4_0_BYTES + 64));
     HIP_TRY(dp.alloc(m * n * nb * sizeof(int32_t)));
-    HIP_TRY(dr.alloc(m * nb * sizeof(NativeRec)));
     HIP_TRY(hipMemcpy(dx.p, x, m * k * sizeof(float), hipMemcpyHostToDevice));
     HIP_TRY(hipMemcpy(dw.p, w, n * nb * rdl::Q4_0_BYTES, hipMemcpyHostToDevice));
-    HIP_TRY(rdl::launch_prep_native((const float*)dx.p, m, k, (NativeRec*)dr.p, nullptr, nullptr,
-                                    nullptr));
-    for (size_t r = 0; r < m; r++)
-        HIP_TRY(rdl::launch_q4_0_block_dots((const uint8_t*)dw.p, n, k,
-                                            (const NativeRec*)dr.p + r * nb,
-                                            (int32_t*)dp.p + r * n * nb, nullptr));
+    if (m > FUSED_MAX_M && gemm_fits(WType::Q4_0, m, n, k)) {
+        // the rows matmul_f32_q4_native takes to the int8 GEMM: its own MFMA block dots
+        HIP_TRY(dr.alloc(rdl::gemm_scratch_bytes(m, k, true)));
+        HIP_TRY(rdl::launch_gemm_q4_0_native((const uint8_t*)dw.p, n, k, (const float*)dx.p, m, nullptr,
+                                             (int32_t*)dp.p, dr.p, nullptr));
+    } else {
+        HIP_TRY(dr.alloc(m * nb * sizeof(NativeRec)));
+        HIP_TRY(rdl::launch_prep_native((const float*)dx.p, m, k, (NativeRec*)dr.p, nullptr, nullptr,
+                                        nullptr));
+        for (size_t r = 0; r < m; r++)
+            HIP_TRY(rdl::launch_q4_0_block_dots((const uint8_t*)dw.p, n, k,
+                                                (const NativeRec*)dr.p + r * nb,
+                                                (int32_t*)dp.p + r * n * nb, nullptr));
+    }
     HIP_TRY(hipMemcpy(partials, dp.p, m * n * nb * sizeof(int32_t), hipMemcpyDeviceToHost));
     return ok();
 }
@@ -402,15 +412,7 @@ rdl_status rdl_weight_upload(const uint8_t* bytes, size_t len, int32_t dtype,
             return fail(RDL_ERR_HIP, "hipMemcpy failed: %s", hipGetErrorString(e));
         }
     }
-    bool gemm_ok = false;
-    {
-        const hipError_t e = rdl::gemm_scales_ok(t, (const uint8_t*)d, out_features, in_features, &gemm_ok);
-        if (e != hipSuccess) {
-            (void)hipFree(d);
-            return fail(RDL_ERR_HIP, "weight scale scan failed: %s", hipGetErrorString(e));
-        }
-    }
-    *out = new rdl_weight{d, need, t, out_features, in_features, true, gemm_ok};
+    *out = new rdl_weight{d, need, t, out_features, in_features, true};
     return ok();
 }
 
@@ -433,10 +435,7 @@ rdl_status rdl_weight_wrap_device(const void* dev_bytes, size_t len, int32_t dty
         return fail(RDL_ERR_INVALID_DATA, "device bytes must be 4-byte aligned");
     rdl_status st = require_device();
     if (st != RDL_OK) return st;
-    bool gemm_ok = false;
-    HIP_TRY(rdl::gemm_scales_ok(t, (const uint8_t*)dev_bytes, out_features, in_features, &gemm_ok));
-    *out = new rdl_weight{const_cast<void*>(dev_bytes), need, t, out_features, in_features, false,
-                          gemm_ok};
+    *out = new rdl_weight{const_cast<void*>(dev_bytes), need, t, out_features, in_features, false};
     return ok();
 }
 
@@ -458,7 +457,7 @@ rdl_status rdl_linear_forward_dev(const rdl_weight* w, const float* x_dev, size_
     const bool native = mode == RDL_MODE_NATIVE && (w->type == WType::Q4_0 || w->type == WType::Q4_1);
     hipStream_t s = (hipStream_t)stream;
     void* rec = nullptr;
-    const Path path = pick_path(w->type, native, m, w->n, w->k, x_dev, w->gemm_ok);
+    const Path path = pick_path(w->type, native, m, w->n, w->k, x_dev);
     const size_t rb = scratch_bytes(path, native, m, w->k);
     if (rb) HIP_TRY(hipMallocAsync(&rec, rb, s));
     rdl_status st = run_linear(w->type, native, (const uint8_t*)w->dev, w->n, w->k, x_dev, m, y_dev,
@@ -479,7 +478,7 @@ rdl_status rdl_linear_forward_dev_noalloc(const rdl_weight* w, const float* x_de
     if (m == 0 || w->n == 0) return ok();
     if (!x_dev || !y_dev) return fail(RDL_ERR_NULL_POINTER, "NULL activation pointer");
     const bool native = mode == RDL_MODE_NATIVE && (w->type == WType::Q4_0 || w->type == WType::Q4_1);
-    const Path path = pick_path(w->type, native, m, w->n, w->k, x_dev, w->gemm_ok);
+    const Path path = pick_path(w->type, native, m, w->n, w->k, x_dev);
     const size_t rb = scratch_bytes(path, native, m, w->k);
     if (rb > (size_t)RDL_NOALLOC_SCRATCH_BYTES)
         return fail(RDL_ERR_UNSUPPORTED,

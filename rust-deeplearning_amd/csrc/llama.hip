@@ -558,7 +558,6 @@ struct LlamaModel {
     struct Mat {
         uint8_t* dev = nullptr;
         int n = 0, k = 0;
-        bool gemm_ok = true;
         WType type = WType::Q4_0;
         size_t row_bytes() const { return (size_t)(k / block_elems(type)) * block_bytes(type); }
         size_t bytes() const { return (size_t)n * row_bytes(); }
@@ -622,7 +621,7 @@ struct LlamaModel {
     // y[m, mat.n] = x[m, mat.k] . W^T on the model's stream
     hipError_t linear(const Mat& w, const float* xin, size_t m, float* y) {
         if (m <= 4) return launch_gemv_fused(w.type, false, w.dev, w.n, w.k, xin, m, y, stream);
-        if (w.type == WType::Q4_0 && w.gemm_ok) return launch_gemm_q4_0(w.dev, w.n, w.k, xin, m, y, gemm_scratch, stream);
+        if (w.type == WType::Q4_0) return launch_gemm_q4_0(w.dev, w.n, w.k, xin, m, y, gemm_scratch, stream);
         // rows four at a time through the fused GEMV (other types, or scales
         // beyond the GEMM's range)
         for (size_t r = 0; r < m; r += 4) {
@@ -932,15 +931,6 @@ rdl_status slot_target(rdl::LlamaModel& M, int32_t slot, int32_t layer, SlotTarg
     return api_ok();
 }
 
-// After a matrix's bytes changed: whether its block scales suit the GEMM.
-rdl_status finish_slot(const SlotTarget& t) {
-    if (t.mat) {
-        bool ok = false;
-        HIP_TRY(rdl::gemm_scales_ok(t.mat->type, t.mat->dev, t.mat->n, t.mat->k, &ok));
-        t.mat->gemm_ok = ok;
-    }
-    return api_ok();
-}
 
 }  // namespace
 
@@ -1059,7 +1049,7 @@ rdl_status rdl_llama_create_typed(const rdl_llama_config* cfg, const int32_t* ty
     M.out_cap = (size_t)c.max_seq + 1;
     if ((e = M.alloc_t(&M.out_tokens, M.out_cap)) != hipSuccess) return fail_free(e);
     const size_t kmax = (size_t)std::max(std::max(c.dim, c.ffn_dim), M.q_dim);
-    if ((e = M.alloc(&M.gemm_scratch, rdl::gemm_scratch_bytes(mb, kmax))) != hipSuccess) return fail_free(e);
+    if ((e = M.alloc(&M.gemm_scratch, rdl::gemm_scratch_bytes(mb, kmax, false))) != hipSuccess) return fail_free(e);
     if (any_split_qkv && (e = M.alloc_t(&M.part_tmp, mb * M.qkv_dim)) != hipSuccess) return fail_free(e);
     // (row-pair epilogues need at most 4 columns per lane: dim <= 8192)
     M.fused_shapes = (c.dim / 32) % 2 == 0 && (M.q_dim / 32) % 2 == 0 && (c.ffn_dim / 32) % 2 == 0 &&
@@ -1110,7 +1100,7 @@ rdl_status rdl_llama_set_weight(rdl_llama* model, int32_t slot, int32_t layer, c
     if (len != t.bytes())
         return api_fail(RDL_ERR_SHAPE_MISMATCH, "slot %d: expected %zu bytes, got %zu", slot, t.bytes(), len);
     HIP_TRY(hipMemcpy2D(t.dst, t.dpitch, bytes, t.row_bytes, t.row_bytes, t.rows, hipMemcpyHostToDevice));
-    return finish_slot(t);
+    return api_ok();
 }
 
 rdl_status rdl_llama_init_random(rdl_llama* model, uint64_t seed) {
@@ -1127,7 +1117,6 @@ rdl_status rdl_llama_init_random(rdl_llama* model, uint64_t seed) {
         const size_t nblocks = (size_t)w.n * (w.k / rdl::QK);
         hipLaunchKernelGGL(rdl::fill_q4_0_kernel, dim3(rdl::blocks_for(nblocks)), dim3(rdl::NT), 0, M.stream,
                            w.dev, nblocks, seed * 0x100000001B3ull + (++tag) * 0x9E3779B97F4A7C15ull, 0.02f);
-        w.gemm_ok = true;  // |d| = |N(0, 0.02)| / 8 is far below the GEMM's f16 limit
     };
     auto fill_ones = [&](float* p) {
         hipLaunchKernelGGL(rdl::fill_f32_kernel, dim3(rdl::blocks_for(c.dim)), dim3(rdl::NT), 0, M.stream, p,
@@ -1503,15 +1492,6 @@ rdl_status rdl_llama_load_gguf(const rdl_gguf* g, const rdl_llama_gguf_options* 
         const hipError_t e = stage.copy2d(src, t.row_bytes, t.rows, t.dst, t.dpitch, M.stream);
         if (e != hipSuccess)
             return fail(api_fail(RDL_ERR_HIP, "upload of '%s' failed: %s", ti.name, hipGetErrorString(e)));
-    }
-    // block-scale scan of each matrix once (the GEMM's f16 range)
-    std::vector<rdl::LlamaModel::Mat*> mats = {&M.out};
-    for (auto& L : M.layers) mats.insert(mats.end(), {&L.qkv, &L.o, &L.gu, &L.down, &L.q, &L.k, &L.v, &L.gate, &L.up});
-    for (rdl::LlamaModel::Mat* m : mats) {
-        if (!m->dev) continue;  // the combined or the split form of a layer's q/k/v, gate/up
-        SlotTarget t;
-        t.mat = m;
-        if ((st = finish_slot(t)) != RDL_OK) return fail(st);
     }
     *out = h;
     return api_ok();

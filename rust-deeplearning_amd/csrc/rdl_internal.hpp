@@ -133,6 +133,9 @@ hipError_t launch_prep_float(const float* x, size_t m, size_t k, FloatRec* rec, 
 // Q8_0 bytes [m, k/32 * 34] and the f32 scales [m, k/32] of quantize_row_q8_0.
 hipError_t launch_prep_native(const float* x, size_t m, size_t k, NativeRec* rec,
                               uint8_t* q8_bytes, float* scales, hipStream_t s);
+// The same quantization as contiguous int8 codes [m, k] and f32 scales [m, k/32].
+hipError_t launch_prep_native_codes(const float* x, size_t m, size_t k, int8_t* codes, float* scales,
+                                    hipStream_t s);
 
 // y[m, n] = x . W^T from prepared activations, one GEMV per activation row.
 hipError_t launch_gemv(WType t, bool native, const uint8_t* w, size_t n, size_t k,
@@ -149,15 +152,17 @@ hipError_t launch_gemv_fused(WType t, bool native, const uint8_t* w, size_t n, s
 // Compute units of the current device (queried once; 256 on MI355X).
 int device_cu_count();
 
-// Prefill GEMM for Q4_0 weights in float mode (matrix cores): y[m, n] =
-// x[m, k] . W^T.  `scratch` holds gemm_scratch_bytes(m, k) bytes (the f16
-// x split); W must have |d| <= 4096 in every block scale.
-size_t gemm_scratch_bytes(size_t m, size_t k);
-// Whether every block scale of W fits the GEMM's f16 operands (synchronous
-// scan on the null stream; false for types without a GEMM kernel).
-hipError_t gemm_scales_ok(WType t, const uint8_t* w, size_t n, size_t k, bool* ok);
+// Prefill GEMM for Q4_0 weights on the matrix cores: y[m, n] = x[m, k] . W^T.
+// Float mode (matmul_f32_q4): `scratch` holds gemm_scratch_bytes(m, k, false)
+// bytes (the f16 x split).  Native mode (matmul_f32_q4_native): x quantized
+// to Q8_0 codes, int8 MFMA block dots; gemm_scratch_bytes(m, k, true) bytes
+// of scratch; partials != NULL writes the int32 block dots to
+// partials[(i * n + j) * (k / 32) + b] instead of y.
+size_t gemm_scratch_bytes(size_t m, size_t k, bool native);
 hipError_t launch_gemm_q4_0(const uint8_t* w, size_t n, size_t k, const float* x, size_t m, float* y,
                             void* scratch, hipStream_t s);
+hipError_t launch_gemm_q4_0_native(const uint8_t* w, size_t n, size_t k, const float* x, size_t m, float* y,
+                                   int32_t* partials, void* scratch, hipStream_t s);
 
 // Decoder fusion of the Q4_0 float-mode fused GEMV (m <= 4, k / 32 even,
 // x 16-byte aligned): prologue 0 none, 1 RMSNorm with weights g and eps,

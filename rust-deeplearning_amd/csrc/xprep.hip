@@ -36,7 +36,7 @@ __device__ __forceinline__ float group_sumf32(float v) {
 
 __global__ __launch_bounds__(PREP_THREADS) void prep_native_kernel(
     const float* __restrict__ x, size_t total_blocks, NativeRec* __restrict__ rec,
-    uint8_t* __restrict__ q8_bytes, float* __restrict__ scales) {
+    uint8_t* __restrict__ q8_bytes, float* __restrict__ scales, int8_t* __restrict__ codes) {
     const size_t gid = (size_t)blockIdx.x * PREP_THREADS + threadIdx.x;
     const size_t blk = gid >> 5;
     const int j = threadIdx.x & 31;
@@ -79,6 +79,7 @@ __global__ __launch_bounds__(PREP_THREADS) void prep_native_kernel(
         }
     }
     if (scales && j == 0) scales[blk] = rt;
+    if (codes) codes[gid] = (int8_t)q;
 }
 
 __global__ __launch_bounds__(PREP_THREADS) void prep_float_kernel(const float* __restrict__ x,
@@ -136,7 +137,17 @@ hipError_t launch_prep_native(const float* x, size_t m, size_t k, NativeRec* rec
     if (total == 0) return hipSuccess;
     const size_t grid = (total * QK + PREP_THREADS - 1) / PREP_THREADS;
     hipLaunchKernelGGL(prep_native_kernel, dim3((unsigned)grid), dim3(PREP_THREADS), 0, s, x,
-                       total, rec, q8_bytes, scales);
+                       total, rec, q8_bytes, scales, (int8_t*)nullptr);
+    return hipGetLastError();
+}
+
+hipError_t launch_prep_native_codes(const float* x, size_t m, size_t k, int8_t* codes, float* scales,
+                                    hipStream_t s) {
+    const size_t total = m * (k / QK);
+    if (total == 0) return hipSuccess;
+    const size_t grid = (total * QK + PREP_THREADS - 1) / PREP_THREADS;
+    hipLaunchKernelGGL(prep_native_kernel, dim3((unsigned)grid), dim3(PREP_THREADS), 0, s, x, total,
+                       (NativeRec*)nullptr, (uint8_t*)nullptr, scales, codes);
     return hipGetLastError();
 }
 

@@ -53,9 +53,9 @@ def test_gemm_matches_gemv_rows(rq, gpu):
         assert_close(gemm[r], gemv, rtol=2e-3, atol=2e-4)
 
 
-def test_large_scales_take_the_exact_path(rq, orc, gpu):
-    # |d| > 4096 does not fit the GEMM's f16 operands; the library must route
-    # such a weight elsewhere and stay within the bar
+def test_large_scales_stay_within_the_bar(rq, orc, gpu):
+    # |d| = 20000: (q - 8) * d would overflow f16; the GEMM keeps (q - 8) in
+    # its operands and applies d in f32 after each block's MFMA
     m, n, k = 8, 40, 256
     w = synth.q4_0_weights(n, k, 51)
     blocks = w.reshape(n, -1, 18)
@@ -87,3 +87,47 @@ def test_nan_row_stays_in_its_row(rq, gpu):
     y = rq.matmul_f32_q4(x, w, m, k, n).reshape(m, n)
     assert np.all(np.isnan(y[6]))
     assert np.all(np.isfinite(np.delete(y, 6, axis=0)))
+
+
+# ---- native mode (matmul_f32_q4_native) on the int8 matrix cores ---------------------
+def _native_exact(orc, x, w, m, k, n):
+    part = orc.block_dots(x, w, m, k, n).astype(np.float64)
+    sw = w.reshape(n, k // 32, 18)[:, :, 0:2].copy().view(np.float16).astype(np.float64)[..., 0]
+    sx = np.stack([orc.quantize_row_q8_0(x[r])[1] for r in range(m)]).astype(np.float64)
+    return (part.reshape(m, n, k // 32) * sx[:, None, :] * sw[None]).sum(axis=2).reshape(-1)
+
+
+@pytest.mark.parametrize("m,n", [(512, 256), (2048, 64)])
+def test_native_gemm_block_dots_bit_exact(rq, orc, gpu, m, n):
+    """The int8 MFMA stage of the native GEMM (rows > 4) gives the exact int32
+    block dots of simd::dot_q4q8_block (simd.rs:562-581) for every (row,
+    column, block) at config-4 row counts."""
+    k = 4096
+    print(f"case native partials m={m} n={n}", flush=True)
+    x = synth.activations(m, k, 0x5EED0904 + m)
+    w = synth.q4_0_weights(n, k, 0x5EED0905)
+    assert np.array_equal(rq.q4_0_q8_0_block_dots(x, w, m, k, n), orc.block_dots(x, w, m, k, n))
+
+
+@pytest.mark.parametrize("m,n,k", [(5, 1, 32), (6, 17, 96), (17, 100, 4128), (33, 130, 1056),
+                                   (100, 64, 2080), (300, 257, 544), (1030, 33, 160)])
+def test_native_gemm_ragged(rq, orc, gpu, m, n, k):
+    x = synth.activations(m, k, 91 + m + n + k)
+    w = synth.q4_0_weights(n, k, 92 + m + n + k)
+    assert np.array_equal(rq.q4_0_q8_0_block_dots(x, w, m, k, n), orc.block_dots(x, w, m, k, n))
+    check_parity(rq.matmul_f32_q4_native(x, w, m, k, n), orc.matmul("q4_native", x, w, m, k, n, THREADS),
+                 _native_exact(orc, x, w, m, k, n))
+
+
+def test_native_gemm_nan_and_zero_rows(rq, orc, gpu):
+    # quantize_row_q8_0 maps NaN to code 0 and a zero block to scale 0
+    # (quantize.rs:176-187): such rows stay finite, as in the reference
+    m, n, k = 9, 40, 256
+    x = synth.activations(m, k, 93)
+    x[2, 5] = np.nan
+    x[4] = 0.0
+    w = synth.q4_0_weights(n, k, 94)
+    got = rq.matmul_f32_q4_native(x, w, m, k, n)
+    want = orc.matmul("q4_native", x, w, m, k, n)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    assert_close(np.nan_to_num(got), np.nan_to_num(want))
