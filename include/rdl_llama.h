@@ -103,6 +103,21 @@ rdl_status rdl_llama_reset(rdl_llama* model);
 /* Number of cached positions (KVCache::current_len). */
 rdl_status rdl_llama_position(const rdl_llama* model, size_t* out);
 
+/* The KV cache is paged (the decode-loop extension of KVCache, kv_cache.rs:
+ * 23-114, whose cache is one contiguous [n_kv][max_seq][hd] buffer per layer):
+ * positions live in pages of page_positions (64) positions, each page holding
+ * every KV head's rows of one layer, and a device table maps logical page
+ * pos / page_positions to a physical page of the pool.  The table starts as
+ * the identity (the contiguous layout).  rdl_llama_kv_pages reports the page
+ * size and the number of pages (ceil(max_seq / page_positions)). */
+rdl_status rdl_llama_kv_pages(const rdl_llama* model, size_t* page_positions, size_t* n_pages);
+/* Installs a page table: table[logical page] = physical page, a permutation
+ * of 0 .. n_pages - 1 (RDL_ERR_INVALID_DATA otherwise, RDL_ERR_SHAPE_MISMATCH
+ * for another length).  Only on an empty cache (position 0, after create or
+ * rdl_llama_reset; RDL_ERR_INVALID_DATA otherwise); it then holds for every
+ * write and read of the cache, captured decode graphs included. */
+rdl_status rdl_llama_set_kv_page_table(rdl_llama* model, const int32_t* table, size_t n);
+
 /* forward_with_cache_pass over n tokens followed by cache.advance(n): the
  * logits of the last row, copied to host memory (vocab floats).  Token ids
  * must be < vocab; n <= max_batch; position + n <= max_seq.  Synchronous. */

@@ -219,9 +219,10 @@ struct Fuse {
     const int* pos;             // cache position of activation row 0
     const float* cos_t;         // [max_seq][hd / 2]
     const float* sin_t;
-    void* kc;                   // [n_kv][max_seq][hd], f16 or f32
+    void* kc;                   // paged pool [n_pages][n_kv][KV_PAGE][hd], f16 or f32
     void* vc;
-    int n_heads, n_kv, hd, max_seq, kv_f16;
+    const int* kv_table;        // physical page of each logical page
+    int n_heads, n_kv, hd, kv_f16;
 };
 
 template <int NW, int PI, int PRO = PRO_NONE>
@@ -756,7 +757,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_fused_kernel(const uint8_t* __re
                         y[r1] = o1;
                         y[r1 + half] = o2;
                     } else {
-                        const size_t ko = ((size_t)(head - fz.n_heads) * fz.max_seq + pos) * fz.hd + i;
+                        const size_t ko = kv_row(fz.kv_table, fz.n_kv, head - fz.n_heads, pos, fz.hd) + i;
                         if (fz.kv_f16) {
                             reinterpret_cast<_Float16*>(fz.kc)[ko] = (_Float16)o1;
                             reinterpret_cast<_Float16*>(fz.kc)[ko + half] = (_Float16)o2;
@@ -766,7 +767,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_fused_kernel(const uint8_t* __re
                         }
                     }
                 } else {
-                    const size_t vo = ((size_t)(head - fz.n_heads - fz.n_kv) * fz.max_seq + pos) * fz.hd + i;
+                    const size_t vo = kv_row(fz.kv_table, fz.n_kv, head - fz.n_heads - fz.n_kv, pos, fz.hd) + i;
                     if (fz.kv_f16) {
                         reinterpret_cast<_Float16*>(fz.vc)[vo] = (_Float16)x1;
                         reinterpret_cast<_Float16*>(fz.vc)[vo + half] = (_Float16)x2;
@@ -804,9 +805,10 @@ struct KqFuse {
     int row0;
     const float* cos_t;  // [max_seq][hd / 2]
     const float* sin_t;
-    void* kc;            // [n_kv][max_seq][hd], f16 or f32
+    void* kc;            // paged pool [n_pages][n_kv][KV_PAGE][hd], f16 or f32
     void* vc;
-    int n_heads, n_kv, hd, max_seq, kv_f16, head0;
+    const int* kv_table; // physical page of each logical page
+    int n_heads, n_kv, hd, kv_f16, head0;
 };
 
 // Matrix row of linear row `lin` under the RoPE pairing: linear rows 2p, 2p + 1
@@ -830,7 +832,7 @@ __device__ __forceinline__ void rope_kv_pair(const KqFuse& fz, int r1, float x1,
             y[r1] = o1;
             y[r1 + half] = o2;
         } else {
-            const size_t ko = ((size_t)(head - fz.n_heads) * fz.max_seq + pos) * hd + i;
+            const size_t ko = kv_row(fz.kv_table, fz.n_kv, head - fz.n_heads, pos, hd) + i;
             if (fz.kv_f16) {
                 reinterpret_cast<_Float16*>(fz.kc)[ko] = (_Float16)o1;
                 reinterpret_cast<_Float16*>(fz.kc)[ko + half] = (_Float16)o2;
@@ -840,7 +842,7 @@ __device__ __forceinline__ void rope_kv_pair(const KqFuse& fz, int r1, float x1,
             }
         }
     } else {
-        const size_t vo = ((size_t)(head - fz.n_heads - fz.n_kv) * fz.max_seq + pos) * hd + i;
+        const size_t vo = kv_row(fz.kv_table, fz.n_kv, head - fz.n_heads - fz.n_kv, pos, hd) + i;
         if (fz.kv_f16) {
             reinterpret_cast<_Float16*>(fz.vc)[vo] = (_Float16)x1;
             reinterpret_cast<_Float16*>(fz.vc)[vo + half] = (_Float16)x2;
@@ -1601,7 +1603,7 @@ hipError_t launch_gemv_q4_0_fused_ex(const uint8_t* w, size_t n, size_t k, const
 hipError_t launch_gemv_q4_0_rope_kv(const uint8_t* w, size_t n, size_t k, const float* x, size_t m, float* y,
                                     const float* g, float eps, const int* pos, const float* cos_t,
                                     const float* sin_t, void* kc, void* vc, int n_heads, int n_kv, int hd,
-                                    int max_seq, bool kv_f16, hipStream_t s) {
+                                    const int* kv_table, bool kv_f16, hipStream_t s) {
     if (n == 0 || m == 0) return hipSuccess;
     const int nb = (int)(k / QK);
     if (nb == 0 || (nb & 1) || cpl_for(nb) > 4 || ((uintptr_t)x & 15) || m > 4 || (hd & 1) ||
@@ -1619,7 +1621,7 @@ hipError_t launch_gemv_q4_0_rope_kv(const uint8_t* w, size_t n, size_t k, const 
     fz.n_heads = n_heads;
     fz.n_kv = n_kv;
     fz.hd = hd;
-    fz.max_seq = max_seq;
+    fz.kv_table = kv_table;
     fz.kv_f16 = kv_f16 ? 1 : 0;
     launch_q4_0_fused_ex<PRO_RMSNORM, EPI_ROPE_KV>(w, (int)n, nb, x, m, y, s, (size_t)8 * 16 * nb, fz);
     return hipGetLastError();
@@ -1701,7 +1703,7 @@ hipError_t launch_gemv_kquant_ex(WType t, const uint8_t* w, size_t n, size_t k, 
 hipError_t launch_gemv_kquant_rope_kv(WType t, const uint8_t* w, size_t n, size_t k, const float* x, size_t m,
                                       size_t row0, float* y, size_t ystride, const float* g, float eps,
                                       const int* pos, const float* cos_t, const float* sin_t, void* kc, void* vc,
-                                      int n_heads, int n_kv, int hd, int max_seq, bool kv_f16, hipStream_t s) {
+                                      int n_heads, int n_kv, int hd, const int* kv_table, bool kv_f16, hipStream_t s) {
     if (n == 0 || m == 0) return hipSuccess;
     if ((t != WType::Q4_K && t != WType::Q6_K) || k == 0 || k % QK_K || k > fused_max_k(t) || m > 4 ||
         ((uintptr_t)x & 15) || k > INT32_MAX || ystride < n || ystride > INT32_MAX || row0 > INT32_MAX ||
@@ -1722,7 +1724,7 @@ hipError_t launch_gemv_kquant_rope_kv(WType t, const uint8_t* w, size_t n, size_
     fz.n_heads = n_heads;
     fz.n_kv = n_kv;
     fz.hd = hd;
-    fz.max_seq = max_seq;
+    fz.kv_table = kv_table;
     fz.kv_f16 = kv_f16 ? 1 : 0;
     fz.head0 = 0;
     const size_t lds = (size_t)8 * 16 * (k / QK) + 16 * sizeof(float);

@@ -103,12 +103,12 @@ __global__ __launch_bounds__(NT) void rmsnorm_kernel(const float* __restrict__ x
 
 // RoPE (half-split pairs (i, i + hd/2), rope.rs:134-200) of q and k at
 // positions pos..pos+m-1, then k and v into the cache (KVCache::update,
-// kv_cache.rs:94-106; cache layout [kv_head][max_seq][hd]).
+// kv_cache.rs:94-106; paged layout: kv_row).
 template <typename KV>
 __global__ void rope_kv_kernel(float* __restrict__ qkv, int qkv_dim, const int* __restrict__ pos_dev,
                                const float* __restrict__ cos_t, const float* __restrict__ sin_t,
                                int n_heads, int n_kv, int hd, KV* __restrict__ kc, KV* __restrict__ vc,
-                               int max_seq) {
+                               const int* __restrict__ kv_table) {
     const int s = blockIdx.y, head = blockIdx.x, i = threadIdx.x, half = hd >> 1;
     const int pos = *pos_dev + s;
     float* row = qkv + (size_t)s * qkv_dim;
@@ -123,8 +123,8 @@ __global__ void rope_kv_kernel(float* __restrict__ qkv, int qkv_dim, const int* 
         const float* k = row + n_heads * hd + kvh * hd;
         const float* v = row + (n_heads + n_kv) * hd + kvh * hd;
         const float x1 = k[i], x2 = k[half + i];
-        KV* kd = kc + ((size_t)kvh * max_seq + pos) * hd;
-        KV* vd = vc + ((size_t)kvh * max_seq + pos) * hd;
+        KV* kd = kc + kv_row(kv_table, n_kv, kvh, pos, hd);
+        KV* vd = vc + kv_row(kv_table, n_kv, kvh, pos, hd);
         kd[i] = (KV)(x1 * c - x2 * sn);
         kd[half + i] = (KV)(x1 * sn + x2 * c);
         vd[i] = (KV)v[i];
@@ -144,6 +144,7 @@ __global__ void rope_kv_kernel(float* __restrict__ qkv, int qkv_dim, const int* 
 // Chunks past the row's length exit at once, so a launch sized for the cache
 // capacity serves every position (the captured decode graph).
 constexpr int ATT_CHUNK = 64;
+static_assert(KV_PAGE % ATT_CHUNK == 0, "an attention chunk lies in one cache page");
 
 // HD: head dim as a compile-time constant (64, 128, 256), so that all of a
 // key row's loads are issued before its dot product; 0: runtime hd.
@@ -176,7 +177,7 @@ __device__ __forceinline__ void transposed_sum(float (&v)[N], int c) {
 template <typename KV, int HD>
 __global__ __launch_bounds__(64 * ATT_WAVES) void attention_kernel(
     const float* __restrict__ qkv, int qkv_dim, const int* __restrict__ pos_dev, const KV* __restrict__ kc,
-    const KV* __restrict__ vc, int max_seq, int n_heads, int n_kv, int hd_rt, float scale,
+    const KV* __restrict__ vc, const int* __restrict__ kv_table, int n_heads, int n_kv, int hd_rt, float scale,
     float* __restrict__ part, int nspan, int* __restrict__ counters, float* __restrict__ out) {
     extern __shared__ float sm[];  // q[hd] | o[ATT_WAVES][hd]
     __shared__ float ml[ATT_WAVES][2];
@@ -211,7 +212,10 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attention_kernel(
         const int p = p0 + lane;
         const bool valid = p < t;
         typedef KV kvv __attribute__((ext_vector_type(V)));
-        const KV* vb = vc + (size_t)kvh * max_seq * hd;
+        // the chunk's 64 keys are one page of the cache: rows p0 .. p0 + 63
+        // at kb / vb + (p - p0) * hd
+        const size_t page = kv_row(kv_table, n_kv, kvh, p0, hd);
+        const KV* vb = vc + page;
         const int nvalid = min(ATT_CHUNK, t - p0);
         constexpr int KG = VPRE ? 64 / (CPR > 0 ? CPR : 1) : 1;
         float acc = 0.0f;
@@ -220,18 +224,18 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attention_kernel(
             // lane l = piece l % CPR of row KG i + l / CPR), all in flight
             // before the query (which the previous launch wrote) is read: one
             // memory round trip.  Rows past the length re-read the last valid row.
-            const KV* kb = kc + (size_t)kvh * max_seq * hd;
+            const KV* kb = kc + page;
             kvv kreg[CPR], vreg[CPR];
             const int vk = lane / CPR, pc = lane % CPR, ve = pc * V;
 #pragma unroll
             for (int i = 0; i < CPR; i++) {
                 const int j = min(KG * i + vk, nvalid - 1);
-                kreg[i] = *reinterpret_cast<const kvv*>(kb + (size_t)(p0 + j) * hd + ve);
+                kreg[i] = *reinterpret_cast<const kvv*>(kb + (size_t)j * hd + ve);
             }
 #pragma unroll
             for (int i = 0; i < CPR; i++) {
                 const int j = min(KG * i + vk, nvalid - 1);
-                vreg[i] = *reinterpret_cast<const kvv*>(vb + (size_t)(p0 + j) * hd + ve);
+                vreg[i] = *reinterpret_cast<const kvv*>(vb + (size_t)j * hd + ve);
             }
             float qv[V];
 #pragma unroll
@@ -276,7 +280,7 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attention_kernel(
 #pragma unroll
                 for (int c = 0; c < V; c++) os[w * hd + ve + c] = o[c];
         } else {
-            const KV* kr = kc + ((size_t)kvh * max_seq + (valid ? p : p0)) * hd;
+            const KV* kr = kc + page + (size_t)(valid ? p - p0 : 0) * hd;
             if constexpr (HD > 0) {
                 kvv kreg[HD / V];
 #pragma unroll
@@ -307,7 +311,7 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attention_kernel(
                         const float ej =
                             __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e), j));
                         typedef KV kv2 __attribute__((ext_vector_type(2)));
-                        const int pj = p0 + min(j, nvalid - 1);
+                        const int pj = min(j, nvalid - 1);
                         const kv2 v2 = *reinterpret_cast<const kv2*>(vb + (size_t)pj * hd + d);
                         o0 += ej * (float)v2[0];
                         o1 += ej * (float)v2[1];
@@ -575,8 +579,10 @@ struct LlamaModel {
     std::vector<Layer> layers;
     Mat emb, out;
     float* final_norm = nullptr;
-    void* kc = nullptr;  // [layer][kv_head][max_seq][hd]
+    void* kc = nullptr;  // [layer][page][kv_head][KV_PAGE][hd] (paged, kv_row)
     void* vc = nullptr;
+    int* kv_table = nullptr;  // [n_pages]: physical page of each logical page
+    int n_pages = 0;
     float *cos_t = nullptr, *sin_t = nullptr;
     std::vector<float> cos_h, sin_h;
     // activations for up to max_batch rows
@@ -616,7 +622,7 @@ struct LlamaModel {
         return alloc(reinterpret_cast<void**>(p), count * sizeof(T));
     }
     size_t kv_elem() const { return cfg.kv_f16 ? 2 : 4; }
-    size_t kv_layer_elems() const { return (size_t)cfg.n_kv_heads * cfg.max_seq * cfg.head_dim; }
+    size_t kv_layer_elems() const { return (size_t)n_pages * cfg.n_kv_heads * KV_PAGE * cfg.head_dim; }
 
     // y[m, mat.n] = x[m, mat.k] . W^T on the model's stream
     hipError_t linear(const Mat& w, const float* xin, size_t m, float* y) {
@@ -654,7 +660,7 @@ struct LlamaModel {
         if (rope)
             hipLaunchKernelGGL(rope_kv_kernel<KV>, dim3(cfg.n_heads + cfg.n_kv_heads, (unsigned)m), dim3(hd / 2), 0,
                                stream, qkv, qkv_dim, pos, cos_t, sin_t, cfg.n_heads, cfg.n_kv_heads, hd, kcl, vcl,
-                               cfg.max_seq);
+                               kv_table);
         const float scale = sqrtf((float)hd);
         // chunks that can hold keys for these rows (every chunk of the cache
         // when the launch is captured for replay at any position)
@@ -665,7 +671,7 @@ struct LlamaModel {
                   : (hd == 64)  ? attention_kernel<KV, 64>
                   : (hd == 256) ? attention_kernel<KV, 256>
                                 : attention_kernel<KV, 0>;
-        hipLaunchKernelGGL(kern, grid, dim3(64 * ATT_WAVES), lds, stream, qkv, qkv_dim, pos, kcl, vcl, cfg.max_seq,
+        hipLaunchKernelGGL(kern, grid, dim3(64 * ATT_WAVES), lds, stream, qkv, qkv_dim, pos, kcl, vcl, kv_table,
                            cfg.n_heads, cfg.n_kv_heads, hd, scale, att_part, att_nspan, att_cnt, att);
         return hipGetLastError();
     }
@@ -680,7 +686,7 @@ struct LlamaModel {
         // q = rope(rms_norm(x) . Wq^T); k, v -> cache (RoPE on k) in the same launch
         hipError_t e = launch_gemv_q4_0_rope_kv(L.qkv.dev, L.qkv.n, d, x, m, qkv, L.attn_norm, eps, pos, cos_t,
                                                 sin_t, kv_layer(kc, l), kv_layer(vc, l), cfg.n_heads, cfg.n_kv_heads,
-                                                cfg.head_dim, cfg.max_seq, cfg.kv_f16 != 0, stream);
+                                                cfg.head_dim, kv_table, cfg.kv_f16 != 0, stream);
         if (e != hipSuccess) return e;
         e = cfg.kv_f16 ? layer_attention<_Float16>(l, m, false) : layer_attention<float>(l, m, false);
         if (e != hipSuccess) return e;
@@ -737,7 +743,7 @@ struct LlamaModel {
             e = launch_gemv_kquant_rope_kv(L.qkv.type, L.qkv.dev, L.qkv.n, d, x + r * d, mr, r, qkv + r * qkv_dim,
                                            qkv_dim, L.attn_norm, cfg.norm_eps, pos, cos_t, sin_t, kv_layer(kc, l),
                                            kv_layer(vc, l), cfg.n_heads, cfg.n_kv_heads, cfg.head_dim,
-                                           cfg.max_seq, cfg.kv_f16 != 0, stream);
+                                           kv_table, cfg.kv_f16 != 0, stream);
             if (e != hipSuccess) return e;
         }
         for (int i = 0; i < np && !rope_fused; i++) {
@@ -1032,9 +1038,17 @@ rdl_status rdl_llama_create_typed(const rdl_llama_config* cfg, const int32_t* ty
     if ((e = mat(M.emb, c.vocab, c.dim, (int32_t)M.emb.type)) != hipSuccess) return fail_free(e);
     if ((e = mat(M.out, c.vocab, c.dim, (int32_t)M.out.type)) != hipSuccess) return fail_free(e);
     if ((e = M.alloc_t(&M.final_norm, c.dim)) != hipSuccess) return fail_free(e);
+    M.n_pages = (c.max_seq + rdl::KV_PAGE - 1) / rdl::KV_PAGE;
     const size_t kv_bytes = (size_t)c.n_layers * M.kv_layer_elems() * M.kv_elem();
     if ((e = M.alloc(&M.kc, kv_bytes)) != hipSuccess) return fail_free(e);
     if ((e = M.alloc(&M.vc, kv_bytes)) != hipSuccess) return fail_free(e);
+    {  // identity page table: the layout of a contiguous cache
+        std::vector<int> ident(M.n_pages);
+        for (int p = 0; p < M.n_pages; p++) ident[p] = p;
+        if ((e = M.alloc_t(&M.kv_table, M.n_pages)) != hipSuccess) return fail_free(e);
+        if ((e = hipMemcpy(M.kv_table, ident.data(), ident.size() * sizeof(int), hipMemcpyHostToDevice)) != hipSuccess)
+            return fail_free(e);
+    }
     const size_t mb = c.max_batch;
     if ((e = M.alloc_t(&M.x, mb * c.dim)) != hipSuccess) return fail_free(e);
     if ((e = M.alloc_t(&M.xn, mb * c.dim)) != hipSuccess) return fail_free(e);
@@ -1151,6 +1165,32 @@ rdl_status rdl_llama_reset(rdl_llama* model) {
 rdl_status rdl_llama_position(const rdl_llama* model, size_t* out) {
     if (!model || !out) return api_fail(RDL_ERR_NULL_POINTER, "NULL argument");
     *out = model->m.host_pos;
+    return api_ok();
+}
+
+rdl_status rdl_llama_kv_pages(const rdl_llama* model, size_t* page_positions, size_t* n_pages) {
+    if (!model) return api_fail(RDL_ERR_NULL_POINTER, "NULL model");
+    if (page_positions) *page_positions = rdl::KV_PAGE;
+    if (n_pages) *n_pages = (size_t)model->m.n_pages;
+    return api_ok();
+}
+
+rdl_status rdl_llama_set_kv_page_table(rdl_llama* model, const int32_t* table, size_t n) {
+    if (!model || !table) return api_fail(RDL_ERR_NULL_POINTER, "NULL argument");
+    rdl::LlamaModel& M = model->m;
+    if (n != (size_t)M.n_pages)
+        return api_fail(RDL_ERR_SHAPE_MISMATCH, "page table: expected %d entries, got %zu", M.n_pages, n);
+    if (M.host_pos != 0)
+        return api_fail(RDL_ERR_INVALID_DATA, "the page table can change only on an empty cache (position %zu)",
+                        M.host_pos);
+    std::vector<char> seen(n, 0);
+    for (size_t p = 0; p < n; p++) {
+        if (table[p] < 0 || (size_t)table[p] >= n || seen[table[p]])
+            return api_fail(RDL_ERR_INVALID_DATA, "page table entry %zu = %d: not a permutation of 0..%zu", p,
+                            table[p], n - 1);
+        seen[table[p]] = 1;
+    }
+    HIP_TRY(hipMemcpy(M.kv_table, table, n * sizeof(int32_t), hipMemcpyHostToDevice));
     return api_ok();
 }
 

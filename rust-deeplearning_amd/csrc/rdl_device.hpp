@@ -243,4 +243,15 @@ __device__ __forceinline__ float q6k_dot(const uint32_t (&q)[8], const X& x, con
     return fmaf(fmaf((float)IC, 1.0f / 256.0f, (float)IB), 1.0f / 256.0f, (float)IA);
 }
 
+// ---- paged KV cache -------------------------------------------------------
+// Cached positions live in pages of KV_PAGE positions.  A layer's K (or V)
+// pool is [n_pages][n_kv][KV_PAGE][hd]: physical page pg holds every KV
+// head's rows of one run of KV_PAGE positions; table[pos / KV_PAGE] is the
+// physical page of a position (KVCache's contiguous [n_kv][max_seq][hd] is
+// the identity table).  One attention chunk (64 keys) is one page.
+constexpr int KV_PAGE = 64;
+__device__ __forceinline__ size_t kv_row(const int* __restrict__ table, int n_kv, int kvh, int pos, int hd) {
+    return (((size_t)table[pos / KV_PAGE] * n_kv + kvh) * KV_PAGE + (pos % KV_PAGE)) * hd;
+}
+
 }  // namespace rdl

@@ -186,18 +186,19 @@ hipError_t launch_gemv_kquant_ex(WType t, const uint8_t* w, size_t n, size_t k, 
 
 // The decoder's q/k/v projection in one launch: y = rms_norm(x, g) . [Wq; Wk; Wv]^T
 // with RoPE at positions *pos + row applied to q (in y) and k, and k, v
-// written into the cache ([n_kv][max_seq][hd], f16 or f32); m <= 4.
+// written into the paged cache (pages of KV_PAGE positions through kv_table,
+// [n_pages][n_kv][KV_PAGE][hd] per layer, f16 or f32); m <= 4.
 hipError_t launch_gemv_q4_0_rope_kv(const uint8_t* w, size_t n, size_t k, const float* x, size_t m, float* y,
                                     const float* g, float eps, const int* pos, const float* cos_t,
                                     const float* sin_t, void* kc, void* vc, int n_heads, int n_kv, int hd,
-                                    int max_seq, bool kv_f16, hipStream_t s);
+                                    const int* kv_table, bool kv_f16, hipStream_t s);
 
 // launch_gemv_q4_0_rope_kv for a Q4_K or Q6_K [Wq; Wk; Wv]: m <= 4 activation
 // rows (k floats apart) at positions *pos + row0 + row, q rows ystride apart.
 hipError_t launch_gemv_kquant_rope_kv(WType t, const uint8_t* w, size_t n, size_t k, const float* x, size_t m,
                                       size_t row0, float* y, size_t ystride, const float* g, float eps,
                                       const int* pos, const float* cos_t, const float* sin_t, void* kc, void* vc,
-                                      int n_heads, int n_kv, int hd, int max_seq, bool kv_f16, hipStream_t s);
+                                      int n_heads, int n_kv, int hd, const int* kv_table, bool kv_f16, hipStream_t s);
 
 // int32 block partials of the Q4_0 x Q8_0 path for one activation row.
 hipError_t launch_q4_0_block_dots(const uint8_t* w, size_t n, size_t k, const NativeRec* rec,

@@ -39,6 +39,8 @@ _decl("rdl_llama_generate_greedy", _i32, _p, C.POINTER(C.c_int32), _sz, _sz, C.P
 _decl("rdl_llama_last_timing", _i32, _p, C.POINTER(C.c_float), C.POINTER(C.c_float))
 _decl("rdl_llama_rope_tables", _i32, _p, C.POINTER(C.c_float), C.POINTER(C.c_float), _sz)
 _decl("rdl_llama_get_config", _i32, _p, C.POINTER(_Config))
+_decl("rdl_llama_kv_pages", _i32, _p, C.POINTER(_sz), C.POINTER(_sz))
+_decl("rdl_llama_set_kv_page_table", _i32, _p, C.POINTER(C.c_int32), _sz)
 
 
 class _GgufOptions(C.Structure):
@@ -144,6 +146,17 @@ class LlamaModel:
         out = _sz()
         check(lib.rdl_llama_position(self._h, C.byref(out)))
         return int(out.value)
+
+    def kv_pages(self):
+        """(positions per page, number of pages) of the paged KV cache."""
+        ps, n = _sz(), _sz()
+        check(lib.rdl_llama_kv_pages(self._h, C.byref(ps), C.byref(n)))
+        return int(ps.value), int(n.value)
+
+    def set_kv_page_table(self, table) -> None:
+        """table[logical page] = physical page (a permutation); empty cache only."""
+        t = _i32_array(table)
+        check(lib.rdl_llama_set_kv_page_table(self._h, t.ctypes.data_as(C.POINTER(C.c_int32)), t.size))
 
     def forward_with_cache(self, tokens) -> np.ndarray:
         """Logits of the last of `tokens` (vocab floats); the cache advances by len(tokens)."""

@@ -411,3 +411,75 @@ def test_long_context_four_spans(rq, gpu, kv_f16):
     if not kv_f16:
         assert gen.tolist() == want_toks
     assert m.position == 1900 + 3 + 3
+
+
+@pytest.mark.parametrize("kv_f16", [False, True])
+def test_paged_cache_shuffled_pages(rq, gpu, kv_f16):
+    """The KV cache through a shuffled page table (physical page order
+    reversed and interleaved): 1,900+ cached keys cross 30 page boundaries and
+    four attention spans; prefill, eager decode steps and graph-replayed
+    greedy steps against the oracle, whose cache is contiguous."""
+    cfg = tiny_config(dim=256, n_heads=2, n_kv_heads=1, head_dim=128, max_seq=2048, max_batch=128,
+                      kv_f16=kv_f16)
+    print(f"case paged cache kv_f16={kv_f16}", flush=True)
+    m, ref = build(cfg, seed=29)
+    ps, n_pages = m.kv_pages()
+    assert ps == 64 and n_pages == 32
+    table = np.random.default_rng(31).permutation(n_pages).astype(np.int32)
+    m.set_kv_page_table(table)
+    prompt = np.random.default_rng(37).integers(0, cfg.vocab, 1900)
+    for c0 in range(0, 1900, 128):
+        got = m.forward_with_cache(prompt[c0:c0 + 128])
+        want = ref.forward_with_cache(prompt[c0:c0 + 128])
+
+    def close(got, want):
+        if kv_f16:
+            assert np.max(np.abs(got - want)) <= 1e-2 * np.abs(want).max()
+        else:
+            assert_close(got, want)
+
+    close(got, want)
+    tok = argmax(want)
+    for _ in range(2):
+        got, want = m.decode_step(tok), ref.forward_with_cache([tok])
+        close(got, want)
+        tok = argmax(want)
+    gen = m.generate_greedy([tok], 3)
+    want_toks, logits = [], ref.forward_with_cache([tok])
+    for _ in range(3):
+        want_toks.append(argmax(logits))
+        logits = ref.forward_with_cache([want_toks[-1]])
+    if not kv_f16:
+        assert gen.tolist() == want_toks
+
+
+def test_paged_cache_same_tokens_under_any_table(rq, gpu):
+    # the page table changes where rows live, not what attention computes:
+    # greedy tokens over 300 positions (5 pages) agree bit for bit
+    cfg = tiny_config(max_seq=320, max_batch=64)
+    m, _ = build(cfg, seed=41)
+    prompt = list(np.random.default_rng(43).integers(0, cfg.vocab, 100))
+    base = m.generate_greedy(prompt, 200)
+    _, n_pages = m.kv_pages()
+    for seed in (1, 2):
+        m.reset()
+        m.set_kv_page_table(np.random.default_rng(seed).permutation(n_pages))
+        assert m.generate_greedy(prompt, 200).tolist() == base.tolist()
+
+
+def test_paged_cache_table_errors(rq, gpu):
+    cfg = tiny_config(max_seq=200)
+    m, _ = build(cfg)
+    _, n_pages = m.kv_pages()
+    assert n_pages == 4  # ceil(200 / 64)
+    with pytest.raises(rq.ShapeMismatch):
+        m.set_kv_page_table([0, 1, 2])
+    with pytest.raises(rq.InvalidData):
+        m.set_kv_page_table([0, 1, 1, 3])  # not a permutation
+    with pytest.raises(rq.InvalidData):
+        m.set_kv_page_table([0, 1, 2, 4])  # out of range
+    m.forward_with_cache([1, 2, 3])
+    with pytest.raises(rq.InvalidData):
+        m.set_kv_page_table([3, 2, 1, 0])  # cache not empty
+    m.reset()
+    m.set_kv_page_table([3, 2, 1, 0])
