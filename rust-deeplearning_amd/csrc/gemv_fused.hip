@@ -639,7 +639,12 @@ __global__ __launch_bounds__(NW * 64) void gemv_fused_kernel(const uint8_t* __re
     // epilogue reads ahead of the stream, so no load waits at the kernel's
     // end: the residual's old y (here), the RoPE position (a scalar load) and
     // cos / sin (after the prep).
-    constexpr int SH = reduce_span_log2<R>();
+    // R = 8 (store and SwiGLU epilogues): rows reduced and stored in two
+    // groups of four
+    constexpr int RG = R > 4 ? 4 : R;
+    constexpr int NGRP = R / RG;
+    static_assert(R <= 4 || (R == 8 && (EPI == EPI_STORE || EPI == EPI_SWIGLU)), "rows per wave");
+    constexpr int SH = reduce_span_log2<RG>();
     const bool st_lane = (lane & (((PAIRS ? 2 : 1) << SH) - 1)) == 0;
     const int st_row = row_of(lane >> SH);
     float y_old = 0.0f;
@@ -733,58 +738,64 @@ __global__ __launch_bounds__(NW * 64) void gemv_fused_kernel(const uint8_t* __re
     if (row_of(0) >= rend) return;  // wave-uniform; the wave had nothing to store
 
     // ---- reduce and store ----
-    const float s = wave_reduce_rows<R>(acc);
-    if constexpr (EPI == EPI_SWIGLU) {
-        // rows r (gate, even) and r + 1 (up) sit in adjacent lane groups
-        const float up = __shfl_down(s, 1 << SH);
-        if ((lane & ((2 << SH) - 1)) == 0) {
-            const int g = row_of(lane >> SH);
-            if (g + 1 < rend) y[g >> 1] = (s * (1.0f / (1.0f + expf(-s)))) * up;
-        }
-    } else if constexpr (EPI == EPI_ROPE_KV) {
-        const float x2 = __shfl_down(s, 1 << SH);
-        if ((lane & ((2 << SH) - 1)) == 0) {
-            const int l1 = row_of(lane >> SH);
-            if (l1 < rend) {
-                const int r1 = mat_row(l1);  // row of x1; x2's row is r1 + half
-                const int head = r1 / fz.hd, i = r1 % fz.hd;
-                const int pos = rope_pos;
-                const float x1 = s;
-                if (head < fz.n_heads + fz.n_kv) {
-                    const float c = rope_c, sn = rope_s;
-                    const float o1 = x1 * c - x2 * sn, o2 = x1 * sn + x2 * c;
-                    if (head < fz.n_heads) {
-                        y[r1] = o1;
-                        y[r1 + half] = o2;
-                    } else {
-                        const size_t ko = kv_row(fz.kv_table, fz.n_kv, head - fz.n_heads, pos, fz.hd) + i;
-                        if (fz.kv_f16) {
-                            reinterpret_cast<_Float16*>(fz.kc)[ko] = (_Float16)o1;
-                            reinterpret_cast<_Float16*>(fz.kc)[ko + half] = (_Float16)o2;
+#pragma unroll
+    for (int grp = 0; grp < NGRP; grp++) {
+        float accg[RG];
+#pragma unroll
+        for (int r = 0; r < RG; r++) accg[r] = acc[grp * RG + r];
+        const float s = wave_reduce_rows<RG>(accg);
+        if constexpr (EPI == EPI_SWIGLU) {
+            // rows r (gate, even) and r + 1 (up) sit in adjacent lane groups
+            const float up = __shfl_down(s, 1 << SH);
+            if ((lane & ((2 << SH) - 1)) == 0) {
+                const int g = row_of(grp * RG + (lane >> SH));
+                if (g + 1 < rend) y[g >> 1] = (s * (1.0f / (1.0f + expf(-s)))) * up;
+            }
+        } else if constexpr (EPI == EPI_ROPE_KV) {
+            const float x2 = __shfl_down(s, 1 << SH);
+            if ((lane & ((2 << SH) - 1)) == 0) {
+                const int l1 = row_of(grp * RG + (lane >> SH));
+                if (l1 < rend) {
+                    const int r1 = mat_row(l1);  // row of x1; x2's row is r1 + half
+                    const int head = r1 / fz.hd, i = r1 % fz.hd;
+                    const int pos = rope_pos;
+                    const float x1 = s;
+                    if (head < fz.n_heads + fz.n_kv) {
+                        const float c = rope_c, sn = rope_s;
+                        const float o1 = x1 * c - x2 * sn, o2 = x1 * sn + x2 * c;
+                        if (head < fz.n_heads) {
+                            y[r1] = o1;
+                            y[r1 + half] = o2;
                         } else {
-                            reinterpret_cast<float*>(fz.kc)[ko] = o1;
-                            reinterpret_cast<float*>(fz.kc)[ko + half] = o2;
+                            const size_t ko = kv_row(fz.kv_table, fz.n_kv, head - fz.n_heads, pos, fz.hd) + i;
+                            if (fz.kv_f16) {
+                                reinterpret_cast<_Float16*>(fz.kc)[ko] = (_Float16)o1;
+                                reinterpret_cast<_Float16*>(fz.kc)[ko + half] = (_Float16)o2;
+                            } else {
+                                reinterpret_cast<float*>(fz.kc)[ko] = o1;
+                                reinterpret_cast<float*>(fz.kc)[ko + half] = o2;
+                            }
                         }
-                    }
-                } else {
-                    const size_t vo = kv_row(fz.kv_table, fz.n_kv, head - fz.n_heads - fz.n_kv, pos, fz.hd) + i;
-                    if (fz.kv_f16) {
-                        reinterpret_cast<_Float16*>(fz.vc)[vo] = (_Float16)x1;
-                        reinterpret_cast<_Float16*>(fz.vc)[vo + half] = (_Float16)x2;
                     } else {
-                        reinterpret_cast<float*>(fz.vc)[vo] = x1;
-                        reinterpret_cast<float*>(fz.vc)[vo + half] = x2;
+                        const size_t vo = kv_row(fz.kv_table, fz.n_kv, head - fz.n_heads - fz.n_kv, pos, fz.hd) + i;
+                        if (fz.kv_f16) {
+                            reinterpret_cast<_Float16*>(fz.vc)[vo] = (_Float16)x1;
+                            reinterpret_cast<_Float16*>(fz.vc)[vo + half] = (_Float16)x2;
+                        } else {
+                            reinterpret_cast<float*>(fz.vc)[vo] = x1;
+                            reinterpret_cast<float*>(fz.vc)[vo + half] = x2;
+                        }
                     }
                 }
             }
-        }
-    } else if ((lane & ((1 << SH) - 1)) == 0) {
-        const int row = row_of(lane >> SH);
-        if (row < rend) {
-            if constexpr (EPI == EPI_RESIDUAL)
-                y[row] = s + y_old;
-            else
-                y[row] = s;
+        } else if ((lane & ((1 << SH) - 1)) == 0) {
+            const int row = row_of(grp * RG + (lane >> SH));
+            if (row < rend) {
+                if constexpr (EPI == EPI_RESIDUAL)
+                    y[row] = s + y_old;
+                else
+                    y[row] = s;
+            }
         }
     }
 }
@@ -1388,6 +1399,12 @@ void launch_nw(const uint8_t* w, int n, int nb, const float* x, size_t m, float*
     if constexpr (RES == EPI_SWIGLU || RES == EPI_ROPE_KV) {
         // even row counts only (row pairs); RMAX 1 is rejected by the caller
         if constexpr (RMAX >= 4) {
+            if constexpr (RES == EPI_SWIGLU) {
+                if (c.r >= 8) {
+                    launch_kernel((gemv_fused_kernel<WT, NATIVE, 8, CPL, EVEN, NW, PRO, RES>), grid, block, lds, s, w, n, nb, rpw, x, y, fz);
+                    return;
+                }
+            }
             if (c.r >= 4)
                 launch_kernel((gemv_fused_kernel<WT, NATIVE, 4, CPL, EVEN, NW, PRO, RES>), grid, block, lds, s, w, n, nb, rpw, x, y, fz);
             else
@@ -1396,7 +1413,9 @@ void launch_nw(const uint8_t* w, int n, int nb, const float* x, size_t m, float*
             launch_kernel((gemv_fused_kernel<WT, NATIVE, 2, CPL, EVEN, NW, PRO, RES>), grid, block, lds, s, w, n, nb, rpw, x, y, fz);
         }
         return;
-    } else if (c.r <= 1 || RMAX == 1)
+    } else if (c.r >= 8 && RMAX >= 4 && RES == EPI_STORE)
+        launch_kernel((gemv_fused_kernel<WT, NATIVE, (RES == EPI_STORE && RMAX >= 4 ? 8 : 1), CPL, EVEN, NW, PRO, RES>), grid, block, lds, s, w, n, nb, rpw, x, y, fz);
+    else if (c.r <= 1 || RMAX == 1)
         launch_kernel((gemv_fused_kernel<WT, NATIVE, 1, CPL, EVEN, NW, PRO, RES>), grid, block, lds, s, w, n, nb, rpw, x, y, fz);
     else if (c.r <= 2 || RMAX == 2)
         launch_kernel((gemv_fused_kernel<WT, NATIVE, (RMAX >= 2 ? 2 : 1), CPL, EVEN, NW, PRO, RES>), grid, block, lds, s, w, n, nb, rpw, x, y, fz);
@@ -1557,6 +1576,13 @@ void launch_q4_0_fused_ex(const uint8_t* w, int n, int nb, const float* x, size_
         // 7B decode step, also for the 6144-row q/k/v launch)
         c.r = (8 / cpl >= 4) ? 4 : 2;
         c.rpw = 8 * c.r;
+    }
+    // Matrices taller than one round of two 8-wave workgroups a CU at 4 rows
+    // a wave (the 28672-row gate/up, the 32000-row lm_head): 8 rows a wave, so
+    // every workgroup is resident from the start and prepares x once.
+    if ((RES == EPI_SWIGLU || RES == EPI_STORE) && cpl == 2 && n > num_cus() * 2 * 8 * 4) {
+        c.r = 8;
+        c.rpw = 64;
     }
     switch (cpl) {
         case 2: launch_nw<Q, false, 2, true, 8, PRO, RES>(w, n, nb, x, m, y, s, c, lds, fz); break;

@@ -10,7 +10,9 @@ from rdlquant import synth
 
 pytestmark = pytest.mark.gpu
 
-SHAPES = [(1, 320, 256), (3, 1000, 4096), (1, 4096, 14336), (4, 64, 512)]
+# (2, 20000, 2048), (1, 33001, 4096): taller than one round of workgroups at
+# 4 rows a wave, so the store epilogue takes 8 rows a wave (ragged last group)
+SHAPES = [(1, 320, 256), (3, 1000, 4096), (1, 4096, 14336), (4, 64, 512), (2, 20000, 2048), (1, 33001, 4096)]
 
 
 def dev(torch, a):
