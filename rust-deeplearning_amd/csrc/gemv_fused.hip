@@ -587,7 +587,9 @@ __global__ __launch_bounds__(NW * 64) void gemv_fused_kernel(const uint8_t* __re
     // the CU behind every weight load issued before them, so the longer prep
     // of the int4 records wants fewer weight loads in front of it (measured on
     // MI355X: P0 = 2, PF = 3 for int4 records, 4 / 4 otherwise).
-    constexpr int PF = (NB < (I4 ? 3 : 4)) ? NB : (I4 ? 3 : 4);
+    // (int4 records with 16 blocks a lane -- 8 rows a wave -- keep 5 in flight)
+    constexpr int PF_I4 = NB >= 16 ? 5 : 3;
+    constexpr int PF = (NB < (I4 ? PF_I4 : 4)) ? NB : (I4 ? PF_I4 : 4);
     constexpr int P0 = (PF < (I4 ? 2 : 4)) ? PF : (I4 ? 2 : 4);
     constexpr int PI = I4 ? (CPL * 4 + NW - 1) / NW : (CPL * 8 + NW - 1) / NW;
     const int lane = threadIdx.x & 63;
@@ -660,6 +662,9 @@ __global__ __launch_bounds__(NW * 64) void gemv_fused_kernel(const uint8_t* __re
         f32x4 xv[PI][2], av[PI][2];
         const float* aux = (PRO == PRO_RMSNORM) ? fz.g : x + nb * 32;
         load_prep_x4<NW, PI, PRO>(x, aux, nb, xv, av);
+        // every wave's x loads enter the CU's memory pipeline ahead of any
+        // wave's weight loads (an execution barrier only: no wait for the loads)
+        __builtin_amdgcn_s_barrier();
 #pragma unroll
         for (int b = 0; b < P0; b++) issue(b);
         wait_prep_x<P0 * LPB>();
