@@ -344,44 +344,50 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attention_kernel(
         }
         return;
     }
-    // several workgroups: partial (M, L, O) to global, the last one combines
+    // several workgroups: partial (M, L, O) to global, the last one combines.
+    // Publication without cache maintenance: the partials are written with
+    // agent-coherent stores (relaxed agent-scope atomic stores: global_store
+    // ... sc1, written through to the device's coherence point) and every
+    // wave waits for its own stores to complete (s_waitcnt vmcnt(0)) before
+    // the barrier; thread 0's counter add follows the barrier, so a workgroup
+    // that sees the count of nz - 1 others sees every other workgroup's stores
+    // completed, and reads them with agent-coherent loads (relaxed agent-scope
+    // atomic loads: global_load ... sc1, never served from a stale L1 / L2
+    // line).  This is the sequence an agent-scope release / acquire pair
+    // compiles to, minus the L2 writeback (buffer_wbl2) and invalidate
+    // (buffer_inv) that only non-coherent stores and loads need -- and those
+    // cost about 0.1 us a wave, serialized per XCD, on MI355X.
     float* po = part + (((size_t)s * n_heads + h) * nspan + z) * (hd + 2);
     for (int d = threadIdx.x; d < hd; d += 64 * ATT_WAVES) {
         float O = 0.0f;
         for (int c = 0; c < nw; c++) O += os[c * hd + d] * expf(ml[c][0] - M);
-        po[2 + d] = O;
+        __hip_atomic_store(po + 2 + d, O, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     if (threadIdx.x == 0) {
-        po[0] = M;
-        po[1] = L;
+        __hip_atomic_store(po, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(po + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    // Publication order: every thread that stored partials releases them at
-    // agent scope itself (its wave waits for its own stores and writes the
-    // XCD's L2 back) before the barrier.  A barrier alone does not wait for
-    // other waves' stores, so thread 0's release could not cover them.
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (threadIdx.x == 0) {
         int* cnt = counters + (size_t)s * n_heads + h;
-        const int old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        const int old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         last = (old == nz - 1);
         if (last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
     if (!last) return;
-    // every wave that reads the other workgroups' partials acquires them
-    // (invalidates its L1 and the XCD's L2 lines) after the counter said so
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     const float* pb = part + ((size_t)s * n_heads + h) * nspan * (hd + 2);
+    auto ld = [](const float* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
     if (w == 0) {
         float MM = -__builtin_inff();
-        for (int c = lane; c < nz; c += 64) MM = fmaxf(MM, pb[(size_t)c * (hd + 2)]);
+        for (int c = lane; c < nz; c += 64) MM = fmaxf(MM, ld(pb + (size_t)c * (hd + 2)));
         MM = wave_max(MM);
         float LL = 0.0f;
         for (int c = lane; c < nz; c += 64) {
-            const float wgt = expf(pb[(size_t)c * (hd + 2)] - MM);
+            const float wgt = expf(ld(pb + (size_t)c * (hd + 2)) - MM);
             wsc[c] = wgt;
-            LL += pb[(size_t)c * (hd + 2) + 1] * wgt;
+            LL += ld(pb + (size_t)c * (hd + 2) + 1) * wgt;
         }
         LL = wave_sum(LL);
         if (lane == 0) ml[0][1] = LL;
@@ -390,7 +396,7 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attention_kernel(
     const float invL = 1.0f / ml[0][1];
     for (int d = threadIdx.x; d < hd; d += 64 * ATT_WAVES) {
         float O = 0.0f;
-        for (int c = 0; c < nz; c++) O += pb[(size_t)c * (hd + 2) + 2 + d] * wsc[c];
+        for (int c = 0; c < nz; c++) O += ld(pb + (size_t)c * (hd + 2) + 2 + d) * wsc[c];
         o[d] = O * invL;
     }
 }
