@@ -18,8 +18,10 @@
 //     reading 64 consecutive columns hit 64 consecutive 16-byte slots);
 //   * phase 2: each lane dots its blocks against its columns' records on
 //     v_dot4_i32_i8; the R row sums are reduced across the wave.
+#include <algorithm>
 #include <type_traits>
 
+#include "attention.hpp"
 #include "rdl_device.hpp"
 #include "rdl_internal.hpp"
 
@@ -223,7 +225,20 @@ struct Fuse {
     void* vc;
     const int* kv_table;        // physical page of each logical page
     int n_heads, n_kv, hd, kv_f16;
+    int* pub;                   // PUB: per-KV-group slots (count, ready flag) of the fused attention
+    int producers;              // PUB: workgroups writing each KV group's q / k / v rows
 };
+
+// A store the fused decode attention of the same launch reads: agent-coherent
+// (relaxed agent-scope atomic store, written through to the device's
+// coherence point) when published, a plain store otherwise.
+template <bool PUB, typename T>
+__device__ __forceinline__ void st_pub(T* p, T v) {
+    if constexpr (PUB)
+        __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else
+        *p = v;
+}
 
 template <int NW, int PI, int PRO = PRO_NONE>
 __device__ __forceinline__ void load_prep_x4(const float* __restrict__ x, const float* __restrict__ aux, int nb,
@@ -570,12 +585,18 @@ __device__ __forceinline__ float block_dot_i4(const uint32_t (&w)[5], uint32_t s
 constexpr int EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_SWIGLU = 2, EPI_ROPE_KV = 3;
 
 // PRO: prologue on x (PRO_NONE / PRO_RMSNORM / PRO_SWIGLU, int4 records only).
-template <int WT, bool NATIVE, int R, int CPL, bool NB_EVEN, int NW, int PRO = PRO_NONE, int EPI = EPI_STORE>
-__global__ __launch_bounds__(NW * 64) void gemv_fused_kernel(const uint8_t* __restrict__ W, int n,
-                                                        int nb, int rpw,
-                                                        const float* __restrict__ X,
-                                                        float* __restrict__ Y, Fuse fz) {
-    extern __shared__ i32x4 lds4[];
+// The body of one workgroup (bx, by): row group bx, activation row by.
+// PUB (EPI_ROPE_KV only): the q rows and the cache rows are written with
+// agent-coherent stores, and once every wave's stores have completed thread
+// 0 counts the workgroup into the slot of its head's KV group; the group's
+// last producer marks the position ready, so that workgroups of the same
+// launch (the fused decode attention) can read the rows.
+template <int WT, bool NATIVE, int R, int CPL, bool NB_EVEN, int NW, int PRO = PRO_NONE, int EPI = EPI_STORE,
+          bool PUB = false>
+__device__ __forceinline__ void gemv_fused_body(int bx, int by, i32x4* __restrict__ lds4, const uint8_t* __restrict__ W,
+                                                int n, int nb, int rpw, const float* __restrict__ X,
+                                                float* __restrict__ Y, const Fuse& fz) {
+    static_assert(!PUB || EPI == EPI_ROPE_KV, "publication is for the q/k/v epilogue");
     constexpr int BYTES = Geo<WT>::BYTES, WORDS = Geo<WT>::WORDS;
     constexpr int LPB = (WORDS == 9) ? 3 : 2;    // load instructions per block
     constexpr int NB = R * CPL;                   // blocks per lane
@@ -594,13 +615,13 @@ __global__ __launch_bounds__(NW * 64) void gemv_fused_kernel(const uint8_t* __re
     constexpr int PI = I4 ? (CPL * 4 + NW - 1) / NW : (CPL * 8 + NW - 1) / NW;
     const int lane = threadIdx.x & 63;
     const int wv = threadIdx.x >> 6;
-    const int r0 = blockIdx.x * rpw;
+    const int r0 = bx * rpw;
     const int rend = min(n, r0 + rpw);
     static_assert(PRO == PRO_NONE || I4, "prologues run on the int4-record prep");
     constexpr bool PAIRS = (EPI == EPI_SWIGLU || EPI == EPI_ROPE_KV);
     static_assert(!PAIRS || R % 2 == 0, "row pairs need an even row count per wave");
-    const float* x = X + (size_t)blockIdx.y * fz.xstride;
-    float* y = Y + (size_t)blockIdx.y * (EPI == EPI_SWIGLU ? n / 2 : n);
+    const float* x = X + (size_t)by * fz.xstride;
+    float* y = Y + (size_t)by * (EPI == EPI_SWIGLU ? n / 2 : n);
     const int half = fz.hd >> 1;
     // The wave's r-th row as a linear row in [r0, r0 + rpw) (validity against
     // rend) and as a matrix row (addressing).  Pairs (r, r + 1 even/odd):
@@ -654,7 +675,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_fused_kernel(const uint8_t* __re
         if (st_lane && st_row < rend) y_old = y[st_row];
     }
     int rope_pos = 0;
-    if constexpr (EPI == EPI_ROPE_KV) rope_pos = *fz.pos + blockIdx.y;
+    if constexpr (EPI == EPI_ROPE_KV) rope_pos = *fz.pos + by;
 
     // ---- x for the prep first, then the first PF blocks ----
     __builtin_amdgcn_s_setprio(2);  // the prep ahead of other workgroups' streams
@@ -740,11 +761,14 @@ __global__ __launch_bounds__(NW * 64) void gemv_fused_kernel(const uint8_t* __re
             }
         }
     }
-    if (row_of(0) >= rend) return;  // wave-uniform; the wave had nothing to store
+    const bool has_rows = row_of(0) < rend;  // wave-uniform
+    if constexpr (!PUB) {
+        if (!has_rows) return;  // the wave had nothing to store
+    }
 
     // ---- reduce and store ----
 #pragma unroll
-    for (int grp = 0; grp < NGRP; grp++) {
+    for (int grp = 0; grp < NGRP && has_rows; grp++) {
         float accg[RG];
 #pragma unroll
         for (int r = 0; r < RG; r++) accg[r] = acc[grp * RG + r];
@@ -769,26 +793,26 @@ __global__ __launch_bounds__(NW * 64) void gemv_fused_kernel(const uint8_t* __re
                         const float c = rope_c, sn = rope_s;
                         const float o1 = x1 * c - x2 * sn, o2 = x1 * sn + x2 * c;
                         if (head < fz.n_heads) {
-                            y[r1] = o1;
-                            y[r1 + half] = o2;
+                            st_pub<PUB>(y + r1, o1);
+                            st_pub<PUB>(y + r1 + half, o2);
                         } else {
                             const size_t ko = kv_row(fz.kv_table, fz.n_kv, head - fz.n_heads, pos, fz.hd) + i;
                             if (fz.kv_f16) {
-                                reinterpret_cast<_Float16*>(fz.kc)[ko] = (_Float16)o1;
-                                reinterpret_cast<_Float16*>(fz.kc)[ko + half] = (_Float16)o2;
+                                st_pub<PUB>(reinterpret_cast<_Float16*>(fz.kc) + ko, (_Float16)o1);
+                                st_pub<PUB>(reinterpret_cast<_Float16*>(fz.kc) + ko + half, (_Float16)o2);
                             } else {
-                                reinterpret_cast<float*>(fz.kc)[ko] = o1;
-                                reinterpret_cast<float*>(fz.kc)[ko + half] = o2;
+                                st_pub<PUB>(reinterpret_cast<float*>(fz.kc) + ko, o1);
+                                st_pub<PUB>(reinterpret_cast<float*>(fz.kc) + ko + half, o2);
                             }
                         }
                     } else {
                         const size_t vo = kv_row(fz.kv_table, fz.n_kv, head - fz.n_heads - fz.n_kv, pos, fz.hd) + i;
                         if (fz.kv_f16) {
-                            reinterpret_cast<_Float16*>(fz.vc)[vo] = (_Float16)x1;
-                            reinterpret_cast<_Float16*>(fz.vc)[vo + half] = (_Float16)x2;
+                            st_pub<PUB>(reinterpret_cast<_Float16*>(fz.vc) + vo, (_Float16)x1);
+                            st_pub<PUB>(reinterpret_cast<_Float16*>(fz.vc) + vo + half, (_Float16)x2);
                         } else {
-                            reinterpret_cast<float*>(fz.vc)[vo] = x1;
-                            reinterpret_cast<float*>(fz.vc)[vo + half] = x2;
+                            st_pub<PUB>(reinterpret_cast<float*>(fz.vc) + vo, x1);
+                            st_pub<PUB>(reinterpret_cast<float*>(fz.vc) + vo + half, x2);
                         }
                     }
                 }
@@ -802,6 +826,54 @@ __global__ __launch_bounds__(NW * 64) void gemv_fused_kernel(const uint8_t* __re
                     y[row] = s;
             }
         }
+    }
+    if constexpr (PUB) {
+        // every wave's coherent stores complete, then one add for the workgroup
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            const int head = mat_row(r0) / fz.hd;
+            const int grp_kv = head < fz.n_heads ? head / (fz.n_heads / fz.n_kv)
+                               : head < fz.n_heads + fz.n_kv ? head - fz.n_heads : head - fz.n_heads - fz.n_kv;
+            int* slot = fz.pub + (size_t)grp_kv * PUB_SLOT;
+            const int old = __hip_atomic_fetch_add(slot + PUB_COUNT, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (old == fz.producers - 1) {  // the group's last producer: every other one's stores completed
+                __hip_atomic_store(slot + PUB_COUNT, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(slot + PUB_READY, *fz.pos + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+    }
+}
+
+
+template <int WT, bool NATIVE, int R, int CPL, bool NB_EVEN, int NW, int PRO = PRO_NONE, int EPI = EPI_STORE>
+__global__ __launch_bounds__(NW * 64) void gemv_fused_kernel(const uint8_t* __restrict__ W, int n,
+                                                        int nb, int rpw,
+                                                        const float* __restrict__ X,
+                                                        float* __restrict__ Y, Fuse fz) {
+    extern __shared__ i32x4 lds4[];
+    gemv_fused_body<WT, NATIVE, R, CPL, NB_EVEN, NW, PRO, EPI, false>(blockIdx.x, blockIdx.y, lds4, W, n, nb, rpw, X,
+                                                                      Y, fz);
+}
+
+// One decode step's q/k/v projection (RMSNorm prologue, RoPE + KV-cache
+// epilogue) with the decode attention fused into the same launch: workgroups
+// [0, n_gemv) are the GEMV's, the rest attention workgroups (head, span) that
+// load their older K/V rows at once, wait for their KV group's q/k/v
+// workgroups (published counts) and then read q and the current row.  All
+// workgroups fit the device at once (a few hundred against two per CU), and
+// the waits are bounded, so no ordering of workgroup dispatch can block them.
+template <typename KV, int HD, int R, int CPL>
+__global__ __launch_bounds__(512) void qkv_attention_kernel(const uint8_t* __restrict__ W, int n, int nb, int rpw,
+                                                            const float* __restrict__ X, float* __restrict__ Y, Fuse fz,
+                                                            AttArgs<KV> aa, int n_gemv) {
+    extern __shared__ i32x4 lds4[];
+    if ((int)blockIdx.x < n_gemv) {
+        gemv_fused_body<(int)WType::Q4_0, false, R, CPL, true, 8, PRO_RMSNORM, EPI_ROPE_KV, true>(
+            blockIdx.x, 0, lds4, W, n, nb, rpw, X, Y, fz);
+    } else {
+        const int a = (int)blockIdx.x - n_gemv;
+        attention_body<KV, HD, true>(a % aa.n_heads, 0, a / aa.n_heads, reinterpret_cast<float*>(lds4), aa);
     }
 }
 
@@ -1655,6 +1727,77 @@ hipError_t launch_gemv_q4_0_rope_kv(const uint8_t* w, size_t n, size_t k, const 
     fz.kv_table = kv_table;
     fz.kv_f16 = kv_f16 ? 1 : 0;
     launch_q4_0_fused_ex<PRO_RMSNORM, EPI_ROPE_KV>(w, (int)n, nb, x, m, y, s, (size_t)8 * 16 * nb, fz);
+    return hipGetLastError();
+}
+
+hipError_t launch_qkv_attention(const uint8_t* w, size_t n, size_t k, const float* x, float* y, const float* g,
+                                float eps, const int* pos, const float* cos_t, const float* sin_t, void* kc, void* vc,
+                                const int* kv_table, int n_heads, int n_kv, int hd, bool kv_f16, float* att_part,
+                                int nspan, int spans, int* att_cnt, float* att_out, int* pub, int* err,
+                                hipStream_t s) {
+    const int nb = (int)(k / QK);
+    const int cpl = cpl_for(nb);
+    // the q/k/v launch's shape (launch_q4_0_fused_ex, EPI_ROPE_KV): row pairs, R rows a wave, 8 waves
+    const int r = (8 / cpl >= 4) ? 4 : 2, rpw = 8 * r;
+    if (k == 0 || nb == 0 || (nb & 1) || cpl > 4 || ((uintptr_t)x & 15) || (hd & 1) || hd % rpw ||
+        n_kv <= 0 || n_heads % n_kv || n != (size_t)(n_heads + 2 * n_kv) * hd ||
+        (uint64_t)n * nb * Q4_0_BYTES > FUSED_MAX_WEIGHT_BYTES || pub == nullptr || err == nullptr)
+        return hipErrorInvalidValue;
+    // the coalesced K/V layout of the fused attention: 16-byte pieces, at most 16 a row
+    if (!((kv_f16 && (hd == 128 || hd == 64)) || (!kv_f16 && hd == 64))) return hipErrorInvalidValue;
+    Fuse fz{};
+    fz.g = g;
+    fz.eps = eps;
+    fz.xstride = (int)k;
+    fz.pos = pos;
+    fz.cos_t = cos_t;
+    fz.sin_t = sin_t;
+    fz.kc = kc;
+    fz.vc = vc;
+    fz.n_heads = n_heads;
+    fz.n_kv = n_kv;
+    fz.hd = hd;
+    fz.kv_table = kv_table;
+    fz.kv_f16 = kv_f16 ? 1 : 0;
+    fz.pub = pub;
+    fz.producers = (n_heads / n_kv + 2) * (hd / rpw);
+    const int n_gemv = (int)((n + rpw - 1) / rpw);
+    if (spans < 1 || spans > nspan) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)(n_gemv + n_heads * spans)), block(512);
+    const size_t lds = std::max((size_t)8 * 16 * nb, (size_t)(1 + ATT_WAVES) * hd * sizeof(float));
+    auto go = [&](auto kv_tag, auto hd_tag, auto r_tag) {
+        using KV = decltype(kv_tag);
+        constexpr int HD = decltype(hd_tag)::value, R = decltype(r_tag)::value, CPL = R == 4 ? 2 : 4;
+        AttArgs<KV> aa{};
+        aa.qkv = y;
+        aa.qkv_dim = (int)n;
+        aa.pos_dev = pos;
+        aa.kc = reinterpret_cast<const KV*>(kc);
+        aa.vc = reinterpret_cast<const KV*>(vc);
+        aa.kv_table = kv_table;
+        aa.n_heads = n_heads;
+        aa.n_kv = n_kv;
+        aa.hd_rt = hd;
+        aa.scale = sqrtf((float)hd);
+        aa.part = att_part;
+        aa.nspan = nspan;
+        aa.counters = att_cnt;
+        aa.out = att_out;
+        aa.pub = pub;
+        aa.err = err;
+        launch_kernel(qkv_attention_kernel<KV, HD, R, CPL>, grid, block, lds, s, w, (int)n, nb, rpw, x, y, fz, aa,
+                      n_gemv);
+    };
+    using I64 = std::integral_constant<int, 64>;
+    using I128 = std::integral_constant<int, 128>;
+    using R4 = std::integral_constant<int, 4>;
+    using R2 = std::integral_constant<int, 2>;
+    if (kv_f16) {
+        if (hd == 128) { if (r == 4) go(_Float16{}, I128{}, R4{}); else go(_Float16{}, I128{}, R2{}); }
+        else { if (r == 4) go(_Float16{}, I64{}, R4{}); else go(_Float16{}, I64{}, R2{}); }
+    } else {
+        if (r == 4) go(0.0f, I64{}, R4{}); else go(0.0f, I64{}, R2{});
+    }
     return hipGetLastError();
 }
 

@@ -31,6 +31,7 @@
 
 #include "../../include/rdl_gguf.h"
 #include "../../include/rdl_llama.h"
+#include "attention.hpp"
 #include "rdl_device.hpp"
 #include "rdl_internal.hpp"
 
@@ -39,18 +40,6 @@ namespace {
 
 constexpr int NT = 256;  // threads of the element-wise / reduction kernels
 
-__device__ __forceinline__ float wave_sum(float v) {
-    v = sum8_f32(v);
-    v += dpp_f32<DPP_ROW_MIRROR>(v);
-    v += __shfl_xor(v, 16);
-    return v + __shfl_xor(v, 32);
-}
-__device__ __forceinline__ float wave_max(float v) {
-    v = max8_f32(v);
-    v = fmaxf(v, dpp_f32<DPP_ROW_MIRROR>(v));
-    v = fmaxf(v, __shfl_xor(v, 16));
-    return fmaxf(v, __shfl_xor(v, 32));
-}
 // Sum over a 256-thread block, returned to every thread.
 __device__ __forceinline__ float block_sum(float v, float* red) {
     v = wave_sum(v);
@@ -132,273 +121,13 @@ __global__ void rope_kv_kernel(float* __restrict__ qkv, int qkv_dim, const int* 
     }
 }
 
-// Attention of query row s (position pos + s) and head h over the cached keys
-// 0 .. pos + s (the causal mask of attention.rs:424-433 keeps exactly these):
-// scores q.k / sqrt(hd), max-subtracted softmax (ops.rs:582-628), then the
-// probability-weighted sum of the values.  Split over the keys in chunks of
-// ATT_CHUNK: one wave per (head, row, chunk) forms the chunk's scores (one
-// key's score per lane), its max m_c, sum l_c = sum exp(score - m_c) and the
-// unnormalised context o_c = sum exp(score - m_c) v; the chunks are then
-// combined as (sum_c exp(m_c - M) o_c) / (sum_c exp(m_c - M) l_c), M = max
-// m_c (in LDS within a workgroup, see attention_kernel for several spans).
-// Chunks past the row's length exit at once, so a launch sized for the cache
-// capacity serves every position (the captured decode graph).
-constexpr int ATT_CHUNK = 64;
-static_assert(KV_PAGE % ATT_CHUNK == 0, "an attention chunk lies in one cache page");
-
-// HD: head dim as a compile-time constant (64, 128, 256), so that all of a
-// key row's loads are issued before its dot product; 0: runtime hd.
-// A workgroup of ATT_WAVES waves covers ATT_WAVES chunks (ATT_SPAN keys):
-// wave w forms chunk w's max m_w, sum l_w and unnormalised context o_w; the
-// workgroup combines its chunks in LDS.  A row with more than ATT_SPAN keys
-// uses several workgroups, and the last of them to finish combines their
-// partials (device-scope counter, chunk order fixed: deterministic).
-constexpr int ATT_WAVES = 8;
-constexpr int ATT_SPAN = ATT_CHUNK * ATT_WAVES;
-
-// One step of the transposed sum of N values over N lanes (lane index c within
-// its group of N): the lane keeps the half of its values selected by bit HF
-// of c and adds the partner lane's (c ^ HF) copy of that half.  After the
-// steps HF = N/2, ..., 1, v[0] of lane c is the group's total of value c.
-template <int HF, int N>
-__device__ __forceinline__ void transposed_sum(float (&v)[N], int c) {
-    if constexpr (HF >= 1) {
-        const bool up = (c & HF) != 0;
-#pragma unroll
-        for (int j = 0; j < HF; j++) {
-            const float send = up ? v[j] : v[j + HF];
-            const float keep = up ? v[j + HF] : v[j];
-            v[j] = keep + __shfl_xor(send, HF);
-        }
-        transposed_sum<HF / 2, N>(v, c);
-    }
-}
-
+// Decode attention: attention.hpp (attention_body); the launch here serves
+// every row count and position (prefill chunks, eager decode steps, the
+// captured decode graph).
 template <typename KV, int HD>
-__global__ __launch_bounds__(64 * ATT_WAVES) void attention_kernel(
-    const float* __restrict__ qkv, int qkv_dim, const int* __restrict__ pos_dev, const KV* __restrict__ kc,
-    const KV* __restrict__ vc, const int* __restrict__ kv_table, int n_heads, int n_kv, int hd_rt, float scale,
-    float* __restrict__ part, int nspan, int* __restrict__ counters, float* __restrict__ out) {
-    extern __shared__ float sm[];  // q[hd] | o[ATT_WAVES][hd]
-    __shared__ float ml[ATT_WAVES][2];
-    __shared__ float wsc[1024];
-    __shared__ int last;
-    const int hd = HD ? HD : hd_rt;
-    // Workgroups are dealt to the 8 XCDs round-robin by linear id; block b
-    // serves head (b % n_kv) * G + b / n_kv, so the G query heads of a KV
-    // head (blocks g, g + n_kv, ...) run on one XCD and share its L2.
-    const int G = n_heads / n_kv;
-    const int h = ((int)blockIdx.x % n_kv) * G + (int)blockIdx.x / n_kv;
-    const int s = blockIdx.y, z = blockIdx.z;
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int t = *pos_dev + s + 1;
-    if (z * ATT_SPAN >= t) return;  // whole workgroup
-    float* qs = sm;
-    float* os = sm + hd;
-    const int kvh = h / G;
-    const float* q = qkv + (size_t)s * qkv_dim + h * hd;
-    // V rows in pieces of 16 bytes: CPR lanes cover a row, one load covers
-    // KG rows; load i of lane l is row KG i + l / CPR (when CPR <= 16)
-    constexpr int V = 16 / sizeof(KV);
-    constexpr int CPR = HD * (int)sizeof(KV) / 16;
-    constexpr bool VPRE = HD > 0 && CPR <= 16 && 64 % (CPR > 0 ? CPR : 1) == 0;
-    if constexpr (!VPRE) {
-        for (int d = threadIdx.x; d < hd; d += 64 * ATT_WAVES) qs[d] = q[d];
-        __syncthreads();
-    }
-    const int p0 = z * ATT_SPAN + w * ATT_CHUNK;
-    float mx = -__builtin_inff(), l = 0.0f;
-    if (p0 < t) {  // wave-uniform
-        const int p = p0 + lane;
-        const bool valid = p < t;
-        typedef KV kvv __attribute__((ext_vector_type(V)));
-        // the chunk's 64 keys are one page of the cache: rows p0 .. p0 + 63
-        // at kb / vb + (p - p0) * hd
-        const size_t page = kv_row(kv_table, n_kv, kvh, p0, hd);
-        const KV* vb = vc + page;
-        const int nvalid = min(ATT_CHUNK, t - p0);
-        constexpr int KG = VPRE ? 64 / (CPR > 0 ? CPR : 1) : 1;
-        float acc = 0.0f;
-        if constexpr (VPRE) {
-            // K and V rows of the chunk in the same coalesced layout (load i of
-            // lane l = piece l % CPR of row KG i + l / CPR), all in flight
-            // before the query (which the previous launch wrote) is read: one
-            // memory round trip.  Rows past the length re-read the last valid row.
-            const KV* kb = kc + page;
-            kvv kreg[CPR], vreg[CPR];
-            const int vk = lane / CPR, pc = lane % CPR, ve = pc * V;
-#pragma unroll
-            for (int i = 0; i < CPR; i++) {
-                const int j = min(KG * i + vk, nvalid - 1);
-                kreg[i] = *reinterpret_cast<const kvv*>(kb + (size_t)j * hd + ve);
-            }
-#pragma unroll
-            for (int i = 0; i < CPR; i++) {
-                const int j = min(KG * i + vk, nvalid - 1);
-                vreg[i] = *reinterpret_cast<const kvv*>(vb + (size_t)j * hd + ve);
-            }
-            float qv[V];
-#pragma unroll
-            for (int e = 0; e < V; e += 4) {
-                const float4 t4 = *reinterpret_cast<const float4*>(q + ve + e);
-                qv[e] = t4.x, qv[e + 1] = t4.y, qv[e + 2] = t4.z, qv[e + 3] = t4.w;
-            }
-            __builtin_amdgcn_sched_barrier(0);  // keep every load ahead of the arithmetic
-            // partial scores of the lane's CPR rows over its V dims, then a
-            // transposed sum over the CPR lanes of the row group: after the
-            // step of mask hf a lane keeps the half of its rows selected by
-            // bit hf of its piece, so piece c ends with row KG c + vk's score.
-            float ps[CPR];
-#pragma unroll
-            for (int i = 0; i < CPR; i++) {
-                float a = 0.0f;
-#pragma unroll
-                for (int e = 0; e < V; e++) a += qv[e] * (float)kreg[i][e];
-                ps[i] = a;
-            }
-            transposed_sum<CPR / 2, CPR>(ps, pc);
-            const int key = KG * pc + vk;  // the row whose score this lane holds
-            const bool kvalid = key < nvalid;
-            const float sc = kvalid ? ps[0] / scale : -__builtin_inff();
-            mx = wave_max(sc);
-            const float e = kvalid ? expf(sc - mx) : 0.0f;
-            l = wave_sum(e);
-            float o[V];
-#pragma unroll
-            for (int c = 0; c < V; c++) o[c] = 0.0f;
-#pragma unroll
-            for (int i = 0; i < CPR; i++) {
-                const float pj = __shfl(e, vk * CPR + i);  // row KG i + vk; rows past the length carry 0
-#pragma unroll
-                for (int c = 0; c < V; c++) o[c] += pj * (float)vreg[i][c];
-            }
-#pragma unroll
-            for (int off = CPR; off < 64; off <<= 1)
-#pragma unroll
-                for (int c = 0; c < V; c++) o[c] += __shfl_xor(o[c], off);
-            if (lane < CPR)
-#pragma unroll
-                for (int c = 0; c < V; c++) os[w * hd + ve + c] = o[c];
-        } else {
-            const KV* kr = kc + page + (size_t)(valid ? p - p0 : 0) * hd;
-            if constexpr (HD > 0) {
-                kvv kreg[HD / V];
-#pragma unroll
-                for (int i = 0; i < HD / V; i++) kreg[i] = *reinterpret_cast<const kvv*>(kr + i * V);
-#pragma unroll
-                for (int i = 0; i < HD / V; i++)
-#pragma unroll
-                    for (int e = 0; e < V; e++) acc += qs[i * V + e] * (float)kreg[i][e];
-            } else {
-                for (int d = 0; d < hd; d += V) {
-                    const kvv kv = *reinterpret_cast<const kvv*>(kr + d);
-#pragma unroll
-                    for (int e = 0; e < V; e++) acc += qs[d + e] * (float)kv[e];
-                }
-            }
-            const float sc = valid ? acc / scale : -__builtin_inff();
-            mx = wave_max(sc);
-            const float e = valid ? expf(sc - mx) : 0.0f;
-            l = wave_sum(e);
-            for (int d0 = 0; d0 < hd; d0 += 128) {
-                const int d = d0 + 2 * lane;
-                if (d < hd) {
-                    float o0 = 0.0f, o1 = 0.0f;
-                    // branch-free: a key past the row's length re-reads the last
-                    // valid row with weight 0, so all row loads are in flight together
-#pragma unroll
-                    for (int j = 0; j < ATT_CHUNK; j++) {
-                        const float ej =
-                            __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e), j));
-                        typedef KV kv2 __attribute__((ext_vector_type(2)));
-                        const int pj = min(j, nvalid - 1);
-                        const kv2 v2 = *reinterpret_cast<const kv2*>(vb + (size_t)pj * hd + d);
-                        o0 += ej * (float)v2[0];
-                        o1 += ej * (float)v2[1];
-                    }
-                    os[w * hd + d] = o0;
-                    os[w * hd + d + 1] = o1;
-                }
-            }
-        }
-    }
-    if (lane == 0) {
-        ml[w][0] = mx;
-        ml[w][1] = l;
-    }
-    __syncthreads();
-    // combine this workgroup's chunks (inactive waves carry m = -inf, l = 0)
-    const int nw = min(ATT_WAVES, (t - z * ATT_SPAN + ATT_CHUNK - 1) / ATT_CHUNK);
-    float M = -__builtin_inff();
-    for (int c = 0; c < nw; c++) M = fmaxf(M, ml[c][0]);
-    float L = 0.0f;
-    for (int c = 0; c < nw; c++) L += ml[c][1] * expf(ml[c][0] - M);
-    const int nz = (t + ATT_SPAN - 1) / ATT_SPAN;
-    float* o = out + (size_t)s * n_heads * hd + h * hd;
-    if (nz == 1) {
-        const float invL = 1.0f / L;
-        for (int d = threadIdx.x; d < hd; d += 64 * ATT_WAVES) {
-            float O = 0.0f;
-            for (int c = 0; c < nw; c++) O += os[c * hd + d] * expf(ml[c][0] - M);
-            o[d] = O * invL;
-        }
-        return;
-    }
-    // several workgroups: partial (M, L, O) to global, the last one combines.
-    // Publication without cache maintenance: the partials are written with
-    // agent-coherent stores (relaxed agent-scope atomic stores: global_store
-    // ... sc1, written through to the device's coherence point) and every
-    // wave waits for its own stores to complete (s_waitcnt vmcnt(0)) before
-    // the barrier; thread 0's counter add follows the barrier, so a workgroup
-    // that sees the count of nz - 1 others sees every other workgroup's stores
-    // completed, and reads them with agent-coherent loads (relaxed agent-scope
-    // atomic loads: global_load ... sc1, never served from a stale L1 / L2
-    // line).  This is the sequence an agent-scope release / acquire pair
-    // compiles to, minus the L2 writeback (buffer_wbl2) and invalidate
-    // (buffer_inv) that only non-coherent stores and loads need -- and those
-    // cost about 0.1 us a wave, serialized per XCD, on MI355X.
-    float* po = part + (((size_t)s * n_heads + h) * nspan + z) * (hd + 2);
-    for (int d = threadIdx.x; d < hd; d += 64 * ATT_WAVES) {
-        float O = 0.0f;
-        for (int c = 0; c < nw; c++) O += os[c * hd + d] * expf(ml[c][0] - M);
-        __hip_atomic_store(po + 2 + d, O, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    if (threadIdx.x == 0) {
-        __hip_atomic_store(po, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(po + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        int* cnt = counters + (size_t)s * n_heads + h;
-        const int old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        last = (old == nz - 1);
-        if (last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __syncthreads();
-    if (!last) return;
-    const float* pb = part + ((size_t)s * n_heads + h) * nspan * (hd + 2);
-    auto ld = [](const float* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
-    if (w == 0) {
-        float MM = -__builtin_inff();
-        for (int c = lane; c < nz; c += 64) MM = fmaxf(MM, ld(pb + (size_t)c * (hd + 2)));
-        MM = wave_max(MM);
-        float LL = 0.0f;
-        for (int c = lane; c < nz; c += 64) {
-            const float wgt = expf(ld(pb + (size_t)c * (hd + 2)) - MM);
-            wsc[c] = wgt;
-            LL += ld(pb + (size_t)c * (hd + 2) + 1) * wgt;
-        }
-        LL = wave_sum(LL);
-        if (lane == 0) ml[0][1] = LL;
-    }
-    __syncthreads();
-    const float invL = 1.0f / ml[0][1];
-    for (int d = threadIdx.x; d < hd; d += 64 * ATT_WAVES) {
-        float O = 0.0f;
-        for (int c = 0; c < nz; c++) O += ld(pb + (size_t)c * (hd + 2) + 2 + d) * wsc[c];
-        o[d] = O * invL;
-    }
+__global__ __launch_bounds__(64 * ATT_WAVES) void attention_kernel(AttArgs<KV> a) {
+    extern __shared__ float sm[];
+    attention_body<KV, HD, false>(blockIdx.x, blockIdx.y, blockIdx.z, sm, a);
 }
 
 // x += y (Tensor::add_inplace, ops.rs:276-289)
@@ -601,6 +330,10 @@ struct LlamaModel {
     float* att_part = nullptr;  // [max_batch][n_heads][spans of max_seq][hd + 2]
     int* att_cnt = nullptr;     // [max_batch][n_heads] finished-chunk counters (zero between launches)
     int att_nspan = 0;
+    // decode steps: attention fused into the q/k/v launch (fused layers, one row)
+    bool fused_attention = true;
+    int* att_pub = nullptr;  // [layer][n_kv][PUB_SLOT] fused-attention slots (zero on an empty cache)
+    int* att_err = nullptr;  // set by a fused launch whose wait ran out
     hipStream_t stream = nullptr;
     hipGraphExec_t decode_exec = nullptr;
     hipGraph_t decode_graph = nullptr;
@@ -677,8 +410,22 @@ struct LlamaModel {
                   : (hd == 64)  ? attention_kernel<KV, 64>
                   : (hd == 256) ? attention_kernel<KV, 256>
                                 : attention_kernel<KV, 0>;
-        hipLaunchKernelGGL(kern, grid, dim3(64 * ATT_WAVES), lds, stream, qkv, qkv_dim, pos, kcl, vcl, kv_table,
-                           cfg.n_heads, cfg.n_kv_heads, hd, scale, att_part, att_nspan, att_cnt, att);
+        AttArgs<KV> aa{};
+        aa.qkv = qkv;
+        aa.qkv_dim = qkv_dim;
+        aa.pos_dev = pos;
+        aa.kc = kcl;
+        aa.vc = vcl;
+        aa.kv_table = kv_table;
+        aa.n_heads = cfg.n_heads;
+        aa.n_kv = cfg.n_kv_heads;
+        aa.hd_rt = hd;
+        aa.scale = scale;
+        aa.part = att_part;
+        aa.nspan = att_nspan;
+        aa.counters = att_cnt;
+        aa.out = att;
+        hipLaunchKernelGGL(kern, grid, dim3(64 * ATT_WAVES), lds, stream, aa);
         return hipGetLastError();
     }
 
@@ -689,15 +436,36 @@ struct LlamaModel {
         const int d = cfg.dim;
         const float eps = cfg.norm_eps;
         Layer& L = layers[l];
+        hipError_t e;
+        if (m == 1 && fused_attention) {
+            // q/k/v, RoPE + cache, and the attention over the cache in one launch
+            e = launch_qkv_attention(L.qkv.dev, L.qkv.n, d, x, qkv, L.attn_norm, eps, pos, cos_t, sin_t,
+                                     kv_layer(kc, l), kv_layer(vc, l), kv_table, cfg.n_heads, cfg.n_kv_heads,
+                                     cfg.head_dim, cfg.kv_f16 != 0, att_part, att_nspan, chunks_needed(1), att_cnt,
+                                     att, att_pub + (size_t)l * cfg.n_kv_heads * PUB_SLOT, att_err, stream);
+            if (e != hipErrorInvalidValue) {
+                if (e != hipSuccess) return e;
+                return layer_fused_tail(l, m);
+            }
+            (void)hipGetLastError();
+        }
         // q = rope(rms_norm(x) . Wq^T); k, v -> cache (RoPE on k) in the same launch
-        hipError_t e = launch_gemv_q4_0_rope_kv(L.qkv.dev, L.qkv.n, d, x, m, qkv, L.attn_norm, eps, pos, cos_t,
+        e = launch_gemv_q4_0_rope_kv(L.qkv.dev, L.qkv.n, d, x, m, qkv, L.attn_norm, eps, pos, cos_t,
                                                 sin_t, kv_layer(kc, l), kv_layer(vc, l), cfg.n_heads, cfg.n_kv_heads,
                                                 cfg.head_dim, kv_table, cfg.kv_f16 != 0, stream);
         if (e != hipSuccess) return e;
         e = cfg.kv_f16 ? layer_attention<_Float16>(l, m, false) : layer_attention<float>(l, m, false);
         if (e != hipSuccess) return e;
+        return layer_fused_tail(l, m);
+    }
+
+    // o, gate/up and down of a fused layer (after its attention)
+    hipError_t layer_fused_tail(int l, size_t m) {
+        const int d = cfg.dim;
+        const float eps = cfg.norm_eps;
+        Layer& L = layers[l];
         // x += att . Wo^T
-        e = launch_gemv_q4_0_fused_ex(L.o.dev, L.o.n, q_dim, att, q_dim, m, x, 0, nullptr, 0.0f, 1, stream);
+        hipError_t e = launch_gemv_q4_0_fused_ex(L.o.dev, L.o.n, q_dim, att, q_dim, m, x, 0, nullptr, 0.0f, 1, stream);
         if (e != hipSuccess) return e;
         // h = silu(gate) * up with [gate; up] = rms_norm(x) . Wgu^T (rows interleaved)
         e = launch_gemv_q4_0_fused_ex(L.gu.dev, L.gu.n, d, x, d, m, hb, 1, L.ffn_norm, eps, 2, stream);
@@ -944,6 +712,17 @@ rdl_status slot_target(rdl::LlamaModel& M, int32_t slot, int32_t layer, SlotTarg
 }
 
 
+// After a synchronized call: a fused attention launch whose wait for its q/k/v
+// workgroups ran out (which a correct launch never does) left the flag set.
+rdl_status check_fused(rdl::LlamaModel& M) {
+    int err = 0;
+    HIP_TRY(hipMemcpy(&err, M.att_err, sizeof(int), hipMemcpyDeviceToHost));
+    if (!err) return RDL_OK;
+    HIP_TRY(hipMemset(M.att_err, 0, sizeof(int)));
+    HIP_TRY(hipMemset(M.att_pub, 0, (size_t)M.cfg.n_layers * M.cfg.n_kv_heads * rdl::PUB_SLOT * sizeof(int)));
+    return api_fail(RDL_ERR_HIP, "fused decode attention: a wait for the q/k/v workgroups ran out");
+}
+
 }  // namespace
 
 extern "C" {
@@ -1084,6 +863,11 @@ rdl_status rdl_llama_create_typed(const rdl_llama_config* cfg, const int32_t* ty
         return fail_free(e);
     if ((e = M.alloc_t(&M.att_cnt, mb * c.n_heads)) != hipSuccess) return fail_free(e);
     if ((e = hipMemset(M.att_cnt, 0, mb * c.n_heads * sizeof(int))) != hipSuccess) return fail_free(e);
+    if ((e = M.alloc_t(&M.att_pub, (size_t)c.n_layers * c.n_kv_heads * rdl::PUB_SLOT)) != hipSuccess) return fail_free(e);
+    if ((e = hipMemset(M.att_pub, 0, (size_t)c.n_layers * c.n_kv_heads * rdl::PUB_SLOT * sizeof(int))) != hipSuccess)
+        return fail_free(e);
+    if ((e = M.alloc_t(&M.att_err, 1)) != hipSuccess) return fail_free(e);
+    if ((e = hipMemset(M.att_err, 0, sizeof(int))) != hipSuccess) return fail_free(e);
     // RoPEFreqs::new (rope.rs:93-108) in f32 with the C library's powf / cosf / sinf
     const int half = c.head_dim / 2;
     M.cos_h.resize((size_t)c.max_seq * half);
@@ -1164,6 +948,8 @@ rdl_status rdl_llama_reset(rdl_llama* model) {
     hipLaunchKernelGGL(rdl::set_int_kernel, dim3(1), dim3(64), 0, M.stream, M.pos, 0);
     HIP_TRY(hipGetLastError());
     HIP_TRY(hipStreamSynchronize(M.stream));
+    HIP_TRY(hipMemset(M.att_pub, 0, (size_t)M.cfg.n_layers * M.cfg.n_kv_heads * rdl::PUB_SLOT * sizeof(int)));
+    HIP_TRY(hipMemset(M.att_err, 0, sizeof(int)));
     M.host_pos = 0;
     return api_ok();
 }
@@ -1219,6 +1005,8 @@ rdl_status rdl_llama_forward(rdl_llama* model, const int32_t* tokens, size_t n, 
     HIP_TRY(M.forward(n));
     HIP_TRY(hipMemcpyAsync(logits, M.logits, (size_t)c.vocab * 4, hipMemcpyDeviceToHost, M.stream));
     HIP_TRY(hipStreamSynchronize(M.stream));
+    rdl_status st = check_fused(M);
+    if (st != RDL_OK) return st;
     M.host_pos += n;
     return api_ok();
 }
@@ -1276,7 +1064,23 @@ rdl_status rdl_llama_generate_greedy(rdl_llama* model, const int32_t* prompt, si
     HIP_TRY(hipStreamSynchronize(M.stream));
     HIP_TRY(hipEventElapsedTime(&M.prefill_ms, M.ev[0], M.ev[1]));
     HIP_TRY(hipEventElapsedTime(&M.decode_ms, M.ev[1], M.ev[2]));
+    rdl_status st = check_fused(M);
+    if (st != RDL_OK) return st;
     M.host_pos += n_gen - 1;
+    return api_ok();
+}
+
+rdl_status rdl_llama_set_fused_attention(rdl_llama* model, int32_t enable) {
+    if (!model) return api_fail(RDL_ERR_NULL_POINTER, "NULL model");
+    rdl::LlamaModel& M = model->m;
+    if (M.fused_attention != (enable != 0)) {
+        M.fused_attention = enable != 0;
+        // the captured decode step holds the other launches: capture again
+        if (M.decode_exec) (void)hipGraphExecDestroy(M.decode_exec);
+        if (M.decode_graph) (void)hipGraphDestroy(M.decode_graph);
+        M.decode_exec = nullptr;
+        M.decode_graph = nullptr;
+    }
     return api_ok();
 }
 

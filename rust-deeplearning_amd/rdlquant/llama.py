@@ -41,6 +41,7 @@ _decl("rdl_llama_rope_tables", _i32, _p, C.POINTER(C.c_float), C.POINTER(C.c_flo
 _decl("rdl_llama_get_config", _i32, _p, C.POINTER(_Config))
 _decl("rdl_llama_kv_pages", _i32, _p, C.POINTER(_sz), C.POINTER(_sz))
 _decl("rdl_llama_set_kv_page_table", _i32, _p, C.POINTER(C.c_int32), _sz)
+_decl("rdl_llama_set_fused_attention", _i32, _p, _i32)
 
 
 class _GgufOptions(C.Structure):
@@ -122,7 +123,7 @@ class LlamaModel:
         return self
 
     def close(self):
-        if getattr(self, "_h", None):
+        if getattr(self, "_h", None) and lib is not None:  # lib is None at interpreter shutdown
             lib.rdl_llama_free(self._h)
             self._h = None
 
@@ -146,6 +147,10 @@ class LlamaModel:
         out = _sz()
         check(lib.rdl_llama_position(self._h, C.byref(out)))
         return int(out.value)
+
+    def set_fused_attention(self, enable: bool) -> None:
+        """Decode steps' q/k/v projection and attention in one launch (default) or two."""
+        check(lib.rdl_llama_set_fused_attention(self._h, int(bool(enable))))
 
     def kv_pages(self):
         """(positions per page, number of pages) of the paged KV cache."""

@@ -483,3 +483,33 @@ def test_paged_cache_table_errors(rq, gpu):
         m.set_kv_page_table([3, 2, 1, 0])  # cache not empty
     m.reset()
     m.set_kv_page_table([3, 2, 1, 0])
+
+
+@pytest.mark.parametrize("kw,n_prompt", [
+    (dict(kv_f16=False), 40),                                               # f32 cache, head dim 64
+    (dict(kv_f16=True), 40),                                                # f16 cache, head dim 64
+    (dict(kv_f16=True, dim=256, n_heads=2, n_kv_heads=1, head_dim=128), 40),  # f16, head dim 128
+    (dict(kv_f16=True, dim=256, n_heads=2, n_kv_heads=1, head_dim=128, max_seq=1100, max_batch=128), 1000),
+    (dict(kv_f16=False, dim=512, n_heads=8, n_kv_heads=2, head_dim=64, max_seq=700, max_batch=128), 600),
+])
+def test_fused_attention_equals_two_launches(rq, gpu, kw, n_prompt):
+    """Decode steps with the attention fused into the q/k/v launch give the
+    same logits, bit for bit, as the q/k/v launch followed by the attention
+    launch (eager steps and graph-replayed greedy steps; one to two spans of
+    512 keys)."""
+    cfg = tiny_config(**kw)
+    print(f"case fused attention {kw} prompt {n_prompt}", flush=True)
+    a, _ = build(cfg, seed=61)
+    b, _ = build(cfg, seed=61)
+    b.set_fused_attention(False)
+    prompt = np.random.default_rng(67).integers(0, cfg.vocab, n_prompt)
+    for c0 in range(0, n_prompt, cfg.max_batch):
+        la = a.forward_with_cache(prompt[c0:c0 + cfg.max_batch])
+        lb = b.forward_with_cache(prompt[c0:c0 + cfg.max_batch])
+    assert np.array_equal(la, lb)
+    tok = int(np.argmax(la))
+    for _ in range(5):
+        la, lb = a.decode_step(tok), b.decode_step(tok)
+        assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+        tok = int(np.argmax(la))
+    assert a.generate_greedy([tok], 6).tolist() == b.generate_greedy([tok], 6).tolist()
