@@ -165,21 +165,31 @@ rdl_status rdl_weight_free(rdl_weight* w);
 /* Linear::forward for a device-resident weight (linear.rs:119-177 minus the bias,
  * which Llama does not use): y_dev[m, N] = x_dev[m, K] . W^T.  mode is
  * RDL_MODE_FLOAT or RDL_MODE_NATIVE (NATIVE applies to Q4_0 and Q4_1 only, as in
- * the reference).  Batch-1..small m runs the decode GEMV; larger m the MFMA GEMM. */
+ * the reference).  Batch-1..small m runs the decode GEMV; larger m the MFMA GEMM.
+ * Scratch (the prefill GEMM's activation split or K-slice partials, activation
+ * records of the other paths) comes from work memory the library keeps per
+ * (device, stream), shared by all handles used on that stream: allocated by
+ * the stream's first call that needs it and grown (hipFree of the old memory
+ * waits for the device) by a call that needs more, never otherwise; held
+ * until the process ends.  Under HIP graph capture of the stream the call
+ * instead records stream-ordered allocation and free nodes (and a kernel that
+ * zeroes the GEMM's counters), so every replay owns its scratch. */
 rdl_status rdl_linear_forward_dev(const rdl_weight* w, const float* x_dev, size_t m,
                                   float* y_dev, int32_t mode, void* stream);
 
 /* rdl_linear_forward_dev without any device allocation.  No counterpart in
  * the reference: it is for callers that cannot allocate device memory (code
  * under HIP graph capture, serving loops, harnesses that forbid hipMalloc).
- * Where rdl_linear_forward_dev allocates stream-ordered scratch (the
- * activation split of the prefill GEMM, activation records for m > 4 in
+ * Where rdl_linear_forward_dev uses its work memory (the activation split or
+ * K-slice partials of the prefill GEMM, activation records for m > 4 in
  * native mode or for other types), this entry point uses one static device
- * array of RDL_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends;
- * products needing more return RDL_ERR_UNSUPPORTED before launching anything.
- * Every call on one GPU shares that array: calls that overlap in time on one
- * GPU (other streams, other threads) race and must be serialized by the
- * caller.  Results equal rdl_linear_forward_dev's (same kernels). */
+ * array of RDL_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends; its
+ * last 64 KiB hold the prefill GEMM's counters (zero at load, left at zero by
+ * every launch).  Products needing more than the rest return
+ * RDL_ERR_UNSUPPORTED before launching anything.  Every call on one GPU
+ * shares that array: calls that overlap in time on one GPU (other streams,
+ * other threads) race and must be serialized by the caller.  Results equal
+ * rdl_linear_forward_dev's (same kernels). */
 #define RDL_NOALLOC_SCRATCH_BYTES (16u << 20)
 rdl_status rdl_linear_forward_dev_noalloc(const rdl_weight* w, const float* x_dev, size_t m,
                                           float* y_dev, int32_t mode, void* stream);

@@ -11,6 +11,7 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "../../include/rdl_quant.h"
 #include "../../include/rdl_gguf.h"
@@ -159,18 +160,19 @@ Path pick_path(WType t, bool native, size_t m, size_t n, size_t k, const float* 
     return Path::Records;
 }
 
-size_t scratch_bytes(Path p, bool native, size_t m, size_t k) {
+size_t scratch_bytes(Path p, bool native, size_t m, size_t n, size_t k) {
     switch (p) {
         case Path::Fused: return 0;
-        case Path::Gemm: return rdl::gemm_scratch_bytes(m, k, native);
+        case Path::Gemm: return rdl::gemm_scratch_bytes(m, n, k, native);
         case Path::Records: return rec_bytes(native, m, k);
     }
     return 0;
 }
 
-// Run the product on `s`; `work` holds scratch_bytes(path) bytes of device memory.
+// Run the product on `s`; `work` holds scratch_bytes(path) bytes of device
+// memory, `counters` gemm_counter_count(n) ints of the GEMM (zero between calls).
 rdl_status run_linear(WType t, bool native, const uint8_t* w_dev, size_t n, size_t k,
-                      const float* x_dev, size_t m, float* y_dev, void* work, hipStream_t s,
+                      const float* x_dev, size_t m, float* y_dev, void* work, int* counters, hipStream_t s,
                       Path path) {
     if (m == 0 || n == 0) return RDL_OK;
     // k == 0: no blocks; the GEMV then writes zeros (empty dot, as in the reference).
@@ -186,7 +188,7 @@ rdl_status run_linear(WType t, bool native, const uint8_t* w_dev, size_t n, size
         if (native)
             HIP_TRY(rdl::launch_gemm_q4_0_native(w_dev, n, k, x_dev, m, y_dev, nullptr, work, s));
         else
-            HIP_TRY(rdl::launch_gemm_q4_0(w_dev, n, k, x_dev, m, y_dev, work, s));
+            HIP_TRY(rdl::launch_gemm_q4_0(w_dev, n, k, x_dev, m, y_dev, work, counters, s));
         return RDL_OK;
     }
     void* xrec = work;
@@ -208,6 +210,12 @@ __device__ __align__(256) uint8_t scratch[RDL_NOALLOC_SCRATCH_BYTES];
 constexpr int MAX_DEVICES = 64;
 std::mutex scratch_mu;
 void* scratch_dev[MAX_DEVICES] = {};
+
+// The last NOALLOC_COUNTER_BYTES of `scratch` hold the prefill GEMM's counters
+// (zero from load time and left at zero by every launch); nothing else is
+// ever written there.
+constexpr size_t NOALLOC_COUNTER_BYTES = 64 * 1024;
+constexpr size_t NOALLOC_DATA_BYTES = (size_t)RDL_NOALLOC_SCRATCH_BYTES - NOALLOC_COUNTER_BYTES;
 
 // The current device's address of `scratch`.
 rdl_status noalloc_scratch(void** out) {
@@ -235,6 +243,94 @@ struct DevBuf {
     hipError_t alloc(size_t bytes) { return hipMalloc(&p, bytes ? bytes : 4); }
 };
 
+// Work memory of the device entry points, one per (device, stream) and
+// shared by every weight handle used on that stream (calls on one stream run
+// in order; calls on two streams get two): scratch grown to the largest call
+// so far, and the prefill GEMM's counters (zeroed when allocated, left at
+// zero by every launch), grown to the largest out_features so far.  Growth
+// frees the old memory with hipFree, which waits for the device; calls that
+// fit allocate nothing.  Held until the process ends.
+struct StreamWork {
+    int dev;
+    hipStream_t stream;
+    void* p;
+    size_t bytes;
+    int* counters;
+    size_t ncnt;
+};
+std::mutex work_mu;
+std::vector<StreamWork> work_pool;
+
+rdl_status stream_work(hipStream_t s, size_t bytes, size_t ncnt, void** p, int** counters) {
+    int dev = 0;
+    HIP_TRY(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lock(work_mu);
+    StreamWork* e = nullptr;
+    for (auto& x : work_pool)
+        if (x.dev == dev && x.stream == s) e = &x;
+    if (!e) {
+        work_pool.push_back({dev, s, nullptr, 0, nullptr, 0});
+        e = &work_pool.back();
+    }
+    if (bytes > e->bytes) {
+        if (e->p) HIP_TRY(hipFree(e->p));
+        e->p = nullptr;
+        e->bytes = 0;
+        HIP_TRY(hipMalloc(&e->p, bytes));
+        e->bytes = bytes;
+    }
+    if (ncnt > e->ncnt) {
+        if (e->counters) HIP_TRY(hipFree(e->counters));
+        e->counters = nullptr;
+        e->ncnt = 0;
+        HIP_TRY(hipMalloc(&e->counters, ncnt * sizeof(int)));
+        HIP_TRY(hipMemset(e->counters, 0, ncnt * sizeof(int)));
+        e->ncnt = ncnt;
+    }
+    *p = e->p;
+    *counters = e->counters;
+    return RDL_OK;
+}
+
+// Device memory of one call on stream `s`: `bytes` of scratch and, when
+// `counters` is wanted, the GEMM counters.  Outside graph capture they are
+// the stream's work memory.  Under capture (where hipMalloc is not
+// allowed) the call takes stream-ordered memory that the graph allocates and
+// frees on every replay, with the counters zeroed by a kernel; release()
+// frees it after the call's launches.
+struct CallWork {
+    void* p = nullptr;
+    int* counters = nullptr;
+    bool graph_owned = false;
+    rdl_status get(const rdl_weight* w, hipStream_t s, size_t bytes, bool want_counters) {
+        if (!bytes && !want_counters) return RDL_OK;
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        HIP_TRY(hipStreamIsCapturing(s, &cs));
+        if (cs != hipStreamCaptureStatusActive) {
+            void* q = nullptr;
+            int* c = nullptr;
+            rdl_status st = stream_work(s, bytes, want_counters ? rdl::gemm_counter_count(w->n) : 0, &q, &c);
+            p = q;
+            counters = want_counters ? c : nullptr;
+            return st;
+        }
+        const size_t data = (bytes + 255) & ~(size_t)255;
+        const size_t nc = want_counters ? rdl::gemm_counter_count(w->n) : 0;
+        HIP_TRY(hipMallocAsync(&p, data + nc * sizeof(int) + 4, s));
+        graph_owned = true;
+        if (want_counters) {
+            counters = reinterpret_cast<int*>(reinterpret_cast<uint8_t*>(p) + data);
+            HIP_TRY(rdl::launch_zero_counters(counters, nc, s));
+        }
+        return RDL_OK;
+    }
+    rdl_status release(hipStream_t s) {
+        if (graph_owned && p) HIP_TRY(hipFreeAsync(p, s));
+        p = nullptr;
+        return RDL_OK;
+    }
+};
+
 rdl_status host_matmul(WType t, bool native, const float* x, size_t x_len, const uint8_t* w,
                        size_t w_len, size_t m, size_t k, size_t n, float* y, size_t y_len) {
     rdl_status st = check_matmul(t, x, x_len, w, w_len, m, k, n, y, y_len);
@@ -249,10 +345,13 @@ rdl_status host_matmul(WType t, bool native, const float* x, size_t x_len, const
     HIP_TRY(hipMemcpy(dx.p, x, m * k * sizeof(float), hipMemcpyHostToDevice));
     HIP_TRY(hipMemcpy(dw.p, w, wb, hipMemcpyHostToDevice));
     const Path path = pick_path(t, native, m, n, k, (const float*)dx.p);
-    const size_t sb = scratch_bytes(path, native, m, k);
+    const size_t sb = scratch_bytes(path, native, m, n, k);
     if (sb) HIP_TRY(dr.alloc(sb));
+    DevBuf dc;
+    HIP_TRY(dc.alloc(rdl::gemm_counter_count(n) * sizeof(int)));
+    HIP_TRY(hipMemset(dc.p, 0, rdl::gemm_counter_count(n) * sizeof(int)));
     st = run_linear(t, native, (const uint8_t*)dw.p, n, k, (const float*)dx.p, m, (float*)dy.p,
-                    dr.p, nullptr, path);
+                    dr.p, (int*)dc.p, nullptr, path);
     if (st != RDL_OK) return st;
     HIP_TRY(hipMemcpy(y, dy.p, m * n * sizeof(float), hipMemcpyDeviceToHost));
     return ok();
@@ -372,7 +471,7 @@ rdl_status rdl_q4_0_q8_0_block_dots(const float* x, size_t x_len, const uint8_t*
     HIP_TRY(hipMemcpy(dw.p, w, n * nb * rdl::Q4_0_BYTES, hipMemcpyHostToDevice));
     if (m > FUSED_MAX_M && gemm_fits(WType::Q4_0, m, n, k)) {
         // the rows matmul_f32_q4_native takes to the int8 GEMM: its own MFMA block dots
-        HIP_TRY(dr.alloc(rdl::gemm_scratch_bytes(m, k, true)));
+        HIP_TRY(dr.alloc(rdl::gemm_scratch_bytes(m, n, k, true)));
         HIP_TRY(rdl::launch_gemm_q4_0_native((const uint8_t*)dw.p, n, k, (const float*)dx.p, m, nullptr,
                                              (int32_t*)dp.p, dr.p, nullptr));
     } else {
@@ -456,18 +555,16 @@ rdl_status rdl_linear_forward_dev(const rdl_weight* w, const float* x_dev, size_
     // Linear::forward honours use_native_q4 only for Q4_0 / Q4_1 (linear.rs:128-153).
     const bool native = mode == RDL_MODE_NATIVE && (w->type == WType::Q4_0 || w->type == WType::Q4_1);
     hipStream_t s = (hipStream_t)stream;
-    void* rec = nullptr;
     const Path path = pick_path(w->type, native, m, w->n, w->k, x_dev);
-    const size_t rb = scratch_bytes(path, native, m, w->k);
-    if (rb) HIP_TRY(hipMallocAsync(&rec, rb, s));
-    rdl_status st = run_linear(w->type, native, (const uint8_t*)w->dev, w->n, w->k, x_dev, m, y_dev,
-                               rec, s, path);
-    if (rec) {
-        hipError_t e = hipFreeAsync(rec, s);
-        if (st == RDL_OK && e != hipSuccess)
-            return fail(RDL_ERR_HIP, "hipFreeAsync failed: %s", hipGetErrorString(e));
-    }
-    return st == RDL_OK ? ok() : st;
+    const bool want_counters = path == Path::Gemm && !native && m <= rdl::GEMM_SMALL_M;
+    CallWork cw;
+    rdl_status st = cw.get(w, s, scratch_bytes(path, native, m, w->n, w->k), want_counters);
+    if (st != RDL_OK) return st;
+    st = run_linear(w->type, native, (const uint8_t*)w->dev, w->n, w->k, x_dev, m, y_dev, cw.p, cw.counters, s,
+                    path);
+    const rdl_status rs = cw.release(s);
+    if (st != RDL_OK) return st;
+    return rs == RDL_OK ? ok() : rs;
 }
 
 rdl_status rdl_linear_forward_dev_noalloc(const rdl_weight* w, const float* x_dev, size_t m, float* y_dev,
@@ -479,18 +576,19 @@ rdl_status rdl_linear_forward_dev_noalloc(const rdl_weight* w, const float* x_de
     if (!x_dev || !y_dev) return fail(RDL_ERR_NULL_POINTER, "NULL activation pointer");
     const bool native = mode == RDL_MODE_NATIVE && (w->type == WType::Q4_0 || w->type == WType::Q4_1);
     const Path path = pick_path(w->type, native, m, w->n, w->k, x_dev);
-    const size_t rb = scratch_bytes(path, native, m, w->k);
-    if (rb > (size_t)RDL_NOALLOC_SCRATCH_BYTES)
+    const size_t rb = scratch_bytes(path, native, m, w->n, w->k);
+    if (rb > NOALLOC_DATA_BYTES)
         return fail(RDL_ERR_UNSUPPORTED,
                     "m=%zu rows of in_features %zu need %zu scratch bytes; the static scratch holds %zu",
-                    m, w->k, rb, (size_t)RDL_NOALLOC_SCRATCH_BYTES);
+                    m, w->k, rb, NOALLOC_DATA_BYTES);
+    if (rdl::gemm_counter_count(w->n) * sizeof(int) > NOALLOC_COUNTER_BYTES)
+        return fail(RDL_ERR_UNSUPPORTED, "out_features %zu beyond the static scratch's GEMM counters", w->n);
     void* work = nullptr;
-    if (rb) {
-        rdl_status st = noalloc_scratch(&work);
-        if (st != RDL_OK) return st;
-    }
-    rdl_status st = run_linear(w->type, native, (const uint8_t*)w->dev, w->n, w->k, x_dev, m, y_dev, work,
-                               (hipStream_t)stream, path);
+    rdl_status st = noalloc_scratch(&work);
+    if (st != RDL_OK) return st;
+    int* counters = reinterpret_cast<int*>(reinterpret_cast<uint8_t*>(work) + NOALLOC_DATA_BYTES);
+    st = run_linear(w->type, native, (const uint8_t*)w->dev, w->n, w->k, x_dev, m, y_dev, work, counters,
+                    (hipStream_t)stream, path);
     return st == RDL_OK ? ok() : st;
 }
 
@@ -582,16 +680,16 @@ rdl_status rdl_q4_0_q8_0_block_dots_dev(const rdl_weight* w, const float* x_dev,
     if (w->n == 0 || w->k == 0) return ok();
     if (!x_dev || !partials_dev) return fail(RDL_ERR_NULL_POINTER, "NULL device pointer");
     hipStream_t s = (hipStream_t)stream;
-    void* rec = nullptr;
-    HIP_TRY(hipMallocAsync(&rec, rec_bytes(true, 1, w->k), s));
-    hipError_t e = rdl::launch_prep_native(x_dev, 1, w->k, (NativeRec*)rec, nullptr, nullptr, s);
+    CallWork cw;
+    rdl_status st = cw.get(w, s, rec_bytes(true, 1, w->k), false);
+    if (st != RDL_OK) return st;
+    hipError_t e = rdl::launch_prep_native(x_dev, 1, w->k, (NativeRec*)cw.p, nullptr, nullptr, s);
     if (e == hipSuccess)
-        e = rdl::launch_q4_0_block_dots((const uint8_t*)w->dev, w->n, w->k, (const NativeRec*)rec,
-                                        partials_dev, s);
-    hipError_t e2 = hipFreeAsync(rec, s);
+        e = rdl::launch_q4_0_block_dots((const uint8_t*)w->dev, w->n, w->k, (const NativeRec*)cw.p, partials_dev,
+                                        s);
+    const rdl_status rs = cw.release(s);
     HIP_TRY(e);
-    HIP_TRY(e2);
-    return ok();
+    return rs == RDL_OK ? ok() : rs;
 }
 
 }  // extern "C"

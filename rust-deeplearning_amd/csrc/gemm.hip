@@ -482,6 +482,349 @@ __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_kernel(
     }
 }
 
+// ---- skinny GEMM (m <= GEMM_SMALL_M) ----------------------------------------------
+// With few x rows, x is the costly operand: a workgroup that owns a strip of
+// W over the whole of K must read and split all of x, and the split alone
+// (about ten VALU operations an element) then outweighs the weight stream.
+// Here a workgroup owns R weight rows over one K-slice: the grid is
+// ceil(n / R) strips x S slices, S chosen to fill the CUs, so each x element
+// is split by ceil(n / R) workgroups instead of n / 16.  Per chunk of KCB
+// blocks of its slice:
+//  1. the whole workgroup loads the chunk's x (coalesced) and splits it into
+//     LDS: per (row, block) e = ilogb(max |x|) - 14 (0 for an all-zero or
+//     non-finite block), x' = x 2^-e, x_hi = f16(x'), x_lo = f16(x' - x_hi)
+//     (0 where x' is infinite), and the f32 scale 2^e;
+//  2. wave (wr, wk) multiplies its JT row tiles (16 weight rows each) over its
+//     KBW blocks of the chunk, x tiles from LDS: per (tile, block) two f16
+//     MFMAs on the exact (q - 8) give the block dot, scaled by d 2^e in f32.
+//     Its weight loads for the next chunk are in flight meanwhile.
+// The WK waves of a row group are summed in wave order through LDS.  With
+// S > 1 each workgroup publishes its strip partial with agent-coherent stores,
+// waits for them to complete, and counts itself on the strip's counter; the
+// last of the S sums all S partials in slice order (the same bits whichever
+// workgroup finishes last) and resets the counter to 0 for the next launch.
+constexpr int SK_WAVES = 8;
+
+template <int MT, int JT, int WR>
+struct SkCfg {
+    static constexpr int NT = SK_WAVES * 64;
+    static constexpr int WK = SK_WAVES / WR;          // waves splitting a chunk's blocks
+    static constexpr int R = 16 * JT * WR;            // weight rows per workgroup
+    static constexpr int MP = 16 * MT;                // x rows held in LDS
+    static constexpr int KCB = MT == 1 ? 32 : MT == 2 ? 16 : 8;  // blocks per chunk
+    static constexpr int KBW = KCB / WK;              // blocks per wave and chunk
+    static constexpr int XROW = KCB * 64 + 16;        // LDS bytes per x row of f16 (padded)
+    static constexpr int X_BYTES = MP * XROW;
+    static constexpr int SC_BYTES = KCB * MP * 4;     // block scales [block][row]
+    static constexpr int D_BYTES = SK_WAVES * JT * KBW * 16 * 4;
+    static constexpr int STAGE = 2 * X_BYTES + SC_BYTES + D_BYTES;
+    static constexpr int UNITS = WR * MT * JT * 64;   // f32x4 outputs per workgroup
+    static constexpr int UPT = (UNITS + NT - 1) / NT; // per thread
+    static constexpr int RED = SK_WAVES * MT * JT * 64 * 16;
+    static constexpr int LDS = STAGE > RED ? STAGE : RED;
+    static constexpr int XU = (MP * KCB * 4 + NT - 1) / NT;  // 8-element x pieces per thread and chunk
+    static_assert(XU <= 4, "x pieces held in registers");
+    static_assert(KBW * WK == KCB, "chunk blocks split evenly over the waves");
+};
+
+// 16 bytes written to / read from the device's coherence point (two relaxed
+// agent-scope 64-bit atomics each), for data other workgroups of the launch read.
+__device__ __forceinline__ void st_coh16(float* p, f32x4 v) {
+    uint64_t* q = reinterpret_cast<uint64_t*>(p);
+    __hip_atomic_store(q, __builtin_bit_cast(uint64_t, float2{v[0], v[1]}), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(q + 1, __builtin_bit_cast(uint64_t, float2{v[2], v[3]}), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ f32x4 ld_coh16(const float* p) {
+    const uint64_t* q = reinterpret_cast<const uint64_t*>(p);
+    const float2 a = __builtin_bit_cast(float2, __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    const float2 b = __builtin_bit_cast(float2, __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    return f32x4{a.x, a.y, b.x, b.y};
+}
+
+template <int MT, int JT, int WR>
+__global__ __launch_bounds__(SK_WAVES * 64) void gemm_q4_0_skinny_kernel(
+    const uint8_t* __restrict__ W, int n, int nb, const float* __restrict__ X, int m, float* __restrict__ Y, int S,
+    int kbs, float* __restrict__ part, int* __restrict__ cnt) {
+    using C = SkCfg<MT, JT, WR>;
+    constexpr int KBW = C::KBW, KCB = C::KCB, MP = C::MP;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    __shared__ int last_sh;
+    uint8_t* xh_s = lds;
+    uint8_t* xl_s = lds + C::X_BYTES;
+    float* sc_s = reinterpret_cast<float*>(lds + 2 * C::X_BYTES);
+    float* d_s = reinterpret_cast<float*>(lds + 2 * C::X_BYTES + C::SC_BYTES);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, r = lane & 15, h = g & 1;
+    const int wr = wave / C::WK, wk = wave % C::WK;
+    const int strip = (int)blockIdx.x / S, ks = (int)blockIdx.x % S;
+    const int j0 = strip * C::R;
+    const int kb0 = min(nb, ks * kbs), kb1 = min(nb, kb0 + kbs);
+    const int nchunks = (kb1 - kb0 + KCB - 1) / KCB;  // workgroup-uniform
+    const uint32_t k = (uint32_t)nb * 32u;
+    const uint32_t row_bytes = (uint32_t)nb * 18u;
+    const uint32_t wbytes = (uint32_t)n * row_bytes;
+    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(W, wbytes);
+    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(X, (uint32_t)m * k * 4u);
+    float* dw = d_s + wave * (JT * KBW * 16);
+
+    struct WRegs { uint32_t w[JT][KBW][3]; };
+    // the wave's weight bytes of chunk c: for row j and block b, lane (g, r)
+    // holds the 12 dword-aligned bytes holding its 8 nibble bytes (and, for
+    // h == 0, the block's d)
+    auto load_w = [&](int c, WRegs& R) {
+#pragma unroll
+        for (int jt = 0; jt < JT; jt++) {
+            const int j = j0 + (wr * JT + jt) * 16 + r;
+#pragma unroll
+            for (int q = 0; q < KBW; q++) {
+                const int b = kb0 + c * KCB + wk * KBW + q;
+                const uint32_t boff = (uint32_t)j * row_bytes + (uint32_t)b * 18u;
+                const uint32_t a = (j < n && b < kb1) ? ((boff + 8u * h) & ~3u) : RSRC_OOB;
+                const auto v = __builtin_amdgcn_raw_buffer_load_b96(wrs, (int)a, 0, 0);
+                R.w[jt][q][0] = v[0], R.w[jt][q][1] = v[1], R.w[jt][q][2] = v[2];
+                // the matrix's last block when it ends 2 bytes into a dword:
+                // that dword is out of range as a whole, its 2 bytes are not
+                if (a < wbytes && a + 12u > wbytes) R.w[jt][q][2] = buf_load_b16(wrs, a + 8u);
+            }
+        }
+    };
+    // chunk c of x: the 8-element pieces of this thread (rows >= m and blocks
+    // past the slice read as zero), loaded ahead of the chunk's weights so
+    // that splitting them never waits for the weight stream
+    struct XRegs { u32x4 v0[C::XU], v1[C::XU]; };
+    auto load_x = [&](int c, XRegs& X) {
+        const int cb0 = kb0 + c * KCB;
+#pragma unroll
+        for (int u = 0; u < C::XU; u++) {
+            const int idx = tid + u * C::NT;
+            const int row = idx / (KCB * 4), blk = (idx >> 2) % KCB, qt = idx & 3;
+            const int b = cb0 + blk;
+            const uint32_t off = (idx < MP * KCB * 4 && row < m && b < kb1)
+                                     ? ((uint32_t)row * k + (uint32_t)b * 32u + (uint32_t)qt * 8u) * 4u
+                                     : RSRC_OOB;
+            X.v0[u] = buf_load_b128(xrs, off);
+            X.v1[u] = buf_load_b128(xrs, off == RSRC_OOB ? RSRC_OOB : off + 16u);
+        }
+    };
+    // the pieces split into LDS: x_hi = f16(x') rounded toward zero, x_lo =
+    // f16(x' - x_hi) (x_hi + x_lo keeps about 22 significant bits either way)
+    auto split_x = [&](const XRegs& X) {
+#pragma unroll
+        for (int u = 0; u < C::XU; u++) {
+            const int idx = tid + u * C::NT;
+            const int row = idx / (KCB * 4), blk = (idx >> 2) % KCB, qt = idx & 3;
+            float xv[8];
+            uint32_t amax = 0;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const uint32_t bits = e < 4 ? X.v0[u][e] : X.v1[u][e - 4];
+                xv[e] = __builtin_bit_cast(float, bits);
+                amax = max(amax, bits & 0x7FFFFFFFu);
+            }
+            // the four lanes of a block are adjacent (idx = tid + u * NT)
+            amax = max(amax, (uint32_t)dpp_i32<DPP_QUAD_XOR1>((int)amax));
+            amax = max(amax, (uint32_t)dpp_i32<DPP_QUAD_XOR2>((int)amax));
+            int ex = 0;
+            if (amax != 0 && amax < 0x7F800000u)
+                ex = (amax >= 0x00800000u ? (int)(amax >> 23) - 127 : (31 - (int)__builtin_clz(amax)) - 149) - 14;
+            // an infinite x keeps its sign through the product: x_lo = 0 for a
+            // block holding one (inf - inf would be NaN)
+            const bool fin = amax < 0x7F800000u;
+            typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+            uint32_t hw[4], lw[4];
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) {
+                const float a = ldexpf(xv[e], -ex), b = ldexpf(xv[e + 1], -ex);
+                const h2 hp = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(a, b));
+                const h2 lp = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(a - (float)hp[0], b - (float)hp[1]));
+                hw[e / 2] = __builtin_bit_cast(uint32_t, hp);
+                lw[e / 2] = fin ? __builtin_bit_cast(uint32_t, lp) : 0u;
+            }
+            if (idx < MP * KCB * 4) {
+                *reinterpret_cast<u32x4*>(xh_s + row * C::XROW + blk * 64 + qt * 16) = u32x4{hw[0], hw[1], hw[2], hw[3]};
+                *reinterpret_cast<u32x4*>(xl_s + row * C::XROW + blk * 64 + qt * 16) = u32x4{lw[0], lw[1], lw[2], lw[3]};
+                if (qt == 0) sc_s[blk * MP + row] = ldexpf(1.0f, ex);
+            }
+        }
+    };
+
+    f32x4 acc[MT][JT];
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+        for (int jt = 0; jt < JT; jt++) acc[t][jt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    WRegs wreg;
+    XRegs xreg;
+    auto compute = [&](int c) {
+        WRegs& R = wreg;
+        half8_t aq[JT][KBW];
+#pragma unroll
+        for (int jt = 0; jt < JT; jt++) {
+            const uint32_t j = (uint32_t)(j0 + (wr * JT + jt) * 16 + r);
+#pragma unroll
+            for (int q = 0; q < KBW; q++) {
+                const uint32_t boff = j * row_bytes + (uint32_t)(kb0 + c * KCB + wk * KBW + q) * 18u;
+                const bool odd = (boff & 2u) != 0;  // the block starts 2 bytes into a dword
+                const uint32_t lo = odd ? R.w[jt][q][1] : perm(R.w[jt][q][1], R.w[jt][q][0], 0x05040302u);
+                const uint32_t hi = odd ? R.w[jt][q][2] : perm(R.w[jt][q][2], R.w[jt][q][1], 0x05040302u);
+                const uint32_t sh = (g >> 1) * 4;
+                aq[jt][q] = q_f16((lo >> sh) & 0x0F0F0F0Fu, (hi >> sh) & 0x0F0F0F0Fu);
+                if (g == 0) dw[(jt * KBW + q) * 16 + r] = h2f(odd ? R.w[jt][q][0] >> 16 : R.w[jt][q][0] & 0xFFFFu);
+            }
+        }
+        // the raw registers are free: the next chunk's x, then its weights,
+        // load during this chunk's products
+        if (c + 1 < nchunks) {
+            load_x(c + 1, xreg);
+            load_w(c + 1, R);
+        }
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+#pragma unroll
+            for (int q = 0; q < KBW; q++) {
+                const int qa = wk * KBW + q;
+                const int xo = (16 * t + r) * C::XROW + qa * 64 + g * 16;
+                const half8_t bh = *reinterpret_cast<const half8_t*>(xh_s + xo);
+                const half8_t bl = *reinterpret_cast<const half8_t*>(xl_s + xo);
+                const float sx = sc_s[qa * MP + 16 * t + r];
+#pragma unroll
+                for (int jt = 0; jt < JT; jt++) {
+                    const f32x4 dv = *reinterpret_cast<const f32x4*>(dw + (jt * KBW + q) * 16 + 4 * g);
+                    const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+                    f32x4 cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(aq[jt][q], bh, z, 0, 0, 0);
+                    cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(aq[jt][q], bl, cc, 0, 0, 0);
+#pragma unroll
+                    for (int u = 0; u < 4; u++) acc[t][jt][u] = fmaf(dv[u] * sx, cc[u], acc[t][jt][u]);
+                }
+            }
+        }
+    };
+
+    // chunks: x split into LDS, then the products
+    if (nchunks > 0) {
+        load_x(0, xreg);
+        load_w(0, wreg);
+    }
+    for (int c = 0; c < nchunks; c++) {
+        split_x(xreg);
+        __syncthreads();  // the chunk's x is in LDS
+        compute(c);
+        __syncthreads();  // every wave is done with the chunk's LDS
+    }
+
+    // wave sums of each row group, in wave order
+    f32x4* red = reinterpret_cast<f32x4*>(lds);
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+        for (int jt = 0; jt < JT; jt++) red[((wave * MT + t) * JT + jt) * 64 + lane] = acc[t][jt];
+    __syncthreads();
+    // unit u = ((wr * MT + t) * JT + jt) * 64 + l: y[16 t + l % 16][row tile (wr JT + jt), 4 (l / 16) ..]
+    f32x4 own[C::UPT];
+#pragma unroll
+    for (int p = 0; p < C::UPT; p++) {
+        const int u = tid + p * C::NT;
+        if (u >= C::UNITS) break;
+        const int ln = u & 63, tj = u >> 6, jt = tj % JT, t = (tj / JT) % MT, wru = tj / (JT * MT);
+        f32x4 sum = red[(((wru * C::WK) * MT + t) * JT + jt) * 64 + ln];
+        for (int w = 1; w < C::WK; w++) sum += red[(((wru * C::WK + w) * MT + t) * JT + jt) * 64 + ln];
+        own[p] = sum;
+    }
+    if (S > 1) {
+        float* pp = part + ((size_t)strip * S + ks) * C::UNITS * 4;
+#pragma unroll
+        for (int p = 0; p < C::UPT; p++) {
+            const int u = tid + p * C::NT;
+            if (u < C::UNITS) st_coh16(pp + (size_t)u * 4, own[p]);
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partials have completed
+        __syncthreads();
+        if (tid == 0) {
+            const int old = __hip_atomic_fetch_add(cnt + strip, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            last_sh = old == S - 1;
+            if (old == S - 1) __hip_atomic_store(cnt + strip, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        if (!last_sh) return;
+        const float* pb = part + (size_t)strip * S * C::UNITS * 4;
+#pragma unroll
+        for (int p = 0; p < C::UPT; p++) {
+            const int u = tid + p * C::NT;
+            if (u >= C::UNITS) break;
+            f32x4 sum = ks == 0 ? own[p] : ld_coh16(pb + (size_t)u * 4);
+            for (int s2 = 1; s2 < S; s2++)
+                sum += s2 == ks ? own[p] : ld_coh16(pb + ((size_t)s2 * C::UNITS + u) * 4);
+            own[p] = sum;
+        }
+    }
+#pragma unroll
+    for (int p = 0; p < C::UPT; p++) {
+        const int u = tid + p * C::NT;
+        if (u >= C::UNITS) break;
+        const int ln = u & 63, tj = u >> 6, jt = tj % JT, t = (tj / JT) % MT, wru = tj / (JT * MT);
+        const int i = 16 * t + (ln & 15);
+        const int j = j0 + (wru * JT + jt) * 16 + 4 * (ln >> 4);
+        if (i >= m) continue;
+        float* yp = Y + (size_t)i * n + j;
+        if (j + 3 < n && (n & 3) == 0) {
+            *reinterpret_cast<f32x4*>(yp) = own[p];
+        } else {
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+                if (j + c < n) yp[c] = own[p][c];
+        }
+    }
+}
+
+// Launch plan of the skinny GEMM for (m, n, nb): the template shape by m, the
+// number of K-slices S (a grid of about one workgroup per CU; S = 1 when the
+// strips alone fill the CUs or no partial buffer is given) and the blocks per
+// slice.
+struct SkPlan {
+    int mt, R, strips, S, kbs, units;
+};
+inline SkPlan skinny_plan(size_t m, size_t n, int nb, bool can_split) {
+    SkPlan p{};
+    p.mt = (int)((m + 15) / 16);
+    const int jt = 4, wr = p.mt >= 3 ? 2 : 1;
+    p.R = 16 * jt * wr;
+    p.units = wr * p.mt * jt * 64;
+    p.strips = (int)((n + p.R - 1) / p.R);
+    int S = can_split ? (device_cu_count() + p.strips / 2) / p.strips : 1;
+    S = std::max(1, std::min(S, std::min(16, nb)));
+    p.kbs = (nb + S - 1) / S;
+    p.S = (nb + p.kbs - 1) / p.kbs;  // no empty slices
+    return p;
+}
+
+template <int MT, int JT, int WR>
+hipError_t launch_skinny_cfg(const uint8_t* w, int n, int nb, const float* x, int m, float* y, const SkPlan& p,
+                             float* part, int* cnt, hipStream_t s) {
+    using C = SkCfg<MT, JT, WR>;
+    static_assert(C::LDS <= 160 * 1024, "LDS per workgroup");
+    auto kern = gemm_q4_0_skinny_kernel<MT, JT, WR>;
+    if (C::LDS > 65536) {
+        static const hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                        C::LDS);  // once per kernel and process
+        if (e != hipSuccess) return e;
+    }
+    launch_kernel(kern, dim3((unsigned)(p.strips * p.S)), dim3(C::NT), (size_t)C::LDS, s, w, n, nb, x, m, y, p.S,
+                  p.kbs, part, cnt);
+    return hipGetLastError();
+}
+
+hipError_t launch_skinny(const uint8_t* w, int n, int nb, const float* x, int m, float* y, float* part, int* cnt,
+                         hipStream_t s) {
+    const SkPlan p = skinny_plan((size_t)m, (size_t)n, nb, part != nullptr && cnt != nullptr);
+    switch (p.mt) {
+        case 1: return launch_skinny_cfg<1, 4, 1>(w, n, nb, x, m, y, p, part, cnt, s);
+        case 2: return launch_skinny_cfg<2, 4, 1>(w, n, nb, x, m, y, p, part, cnt, s);
+        case 3: return launch_skinny_cfg<3, 4, 2>(w, n, nb, x, m, y, p, part, cnt, s);
+        default: return launch_skinny_cfg<4, 4, 2>(w, n, nb, x, m, y, p, part, cnt, s);
+    }
+}
+
 template <bool NATIVE, bool DUMP, int FJ, int FI, int WJ, int WI, int KS, int KB>
 hipError_t launch_cfg(const uint8_t* w, int n, int nb, const void* x0, const void* x1, const int* xe, int m,
                       float* y, int32_t* p, hipStream_t s) {
@@ -490,8 +833,8 @@ hipError_t launch_cfg(const uint8_t* w, int n, int nb, const void* x0, const voi
     static_assert(C::LDS >= C::RED, "K-split sums fit the staging LDS");
     static_assert(C::LDS <= 160 * 1024, "LDS per workgroup");
     if (C::LDS > 65536) {
-        const hipError_t e = hipFuncSetAttribute((const void*)kern,
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
+        static const hipError_t e = hipFuncSetAttribute((const void*)kern,
+                                                        hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
         if (e != hipSuccess) return e;
     }
     const unsigned tiles = (unsigned)((n + C::TJ - 1) / C::TJ) * (unsigned)((m + C::TI - 1) / C::TI);
@@ -522,7 +865,23 @@ hipError_t launch_tiles(const uint8_t* w, int n, int nb, const void* x0, const v
 
 }  // namespace
 
-size_t gemm_scratch_bytes(size_t m, size_t k, bool native) {
+__global__ void zero_i32_kernel(int* __restrict__ p, int n) {
+    const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+    if (i < n) p[i] = 0;
+}
+
+hipError_t launch_zero_counters(int* counters, size_t count, hipStream_t s) {
+    if (count == 0) return hipSuccess;
+    launch_kernel(zero_i32_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, s, counters, (int)count);
+    return hipGetLastError();
+}
+
+size_t gemm_scratch_bytes(size_t m, size_t n, size_t k, bool native) {
+    if (!native && m <= GEMM_SMALL_M) {  // the K-slice partials of the skinny GEMM
+        if (m == 0 || n == 0) return 0;
+        const SkPlan p = skinny_plan(m, n, (int)(k / QK), true);
+        return p.S > 1 ? ((size_t)p.strips * p.S * p.units * 16 + 255) & ~(size_t)255 : 0;
+    }
     if (native)  // int8 codes and f32 block scales, 256-byte aligned pieces
         return ((m * k + 255) & ~(size_t)255) + ((m * (k / QK) * 4 + 255) & ~(size_t)255);
     // x_hi, x_lo (f16) and the row exponents
@@ -531,8 +890,12 @@ size_t gemm_scratch_bytes(size_t m, size_t k, bool native) {
 }
 
 hipError_t launch_gemm_q4_0(const uint8_t* w, size_t n, size_t k, const float* x, size_t m, float* y,
-                            void* scratch, hipStream_t s) {
+                            void* scratch, int* counters, hipStream_t s) {
     if (n == 0 || m == 0) return hipSuccess;
+    if (m <= GEMM_SMALL_M) {
+        float* part = reinterpret_cast<float*>(scratch);  // the K-slice partials
+        return launch_skinny(w, (int)n, (int)(k / QK), x, (int)m, y, part, counters, s);
+    }
     const size_t xb = (m * k * 2 + 255) & ~(size_t)255;
     _Float16* xh = reinterpret_cast<_Float16*>(scratch);
     _Float16* xl = reinterpret_cast<_Float16*>(reinterpret_cast<uint8_t*>(scratch) + xb);

@@ -327,6 +327,7 @@ struct LlamaModel {
     int *tokens = nullptr, *pos = nullptr, *step = nullptr, *out_tokens = nullptr;
     size_t out_cap = 0;
     void* gemm_scratch = nullptr;
+    int* gemm_cnt = nullptr;  // the skinny GEMM's strip counters (zero between launches)
     float* att_part = nullptr;  // [max_batch][n_heads][spans of max_seq][hd + 2]
     int* att_cnt = nullptr;     // [max_batch][n_heads] finished-chunk counters (zero between launches)
     int att_nspan = 0;
@@ -366,7 +367,8 @@ struct LlamaModel {
     // y[m, mat.n] = x[m, mat.k] . W^T on the model's stream
     hipError_t linear(const Mat& w, const float* xin, size_t m, float* y) {
         if (m <= 4) return launch_gemv_fused(w.type, false, w.dev, w.n, w.k, xin, m, y, stream);
-        if (w.type == WType::Q4_0) return launch_gemm_q4_0(w.dev, w.n, w.k, xin, m, y, gemm_scratch, stream);
+        if (w.type == WType::Q4_0)
+            return launch_gemm_q4_0(w.dev, w.n, w.k, xin, m, y, gemm_scratch, gemm_cnt, stream);
         // rows four at a time through the fused GEMV (other types, or scales
         // beyond the GEMM's range)
         for (size_t r = 0; r < m; r += 4) {
@@ -847,8 +849,22 @@ rdl_status rdl_llama_create_typed(const rdl_llama_config* cfg, const int32_t* ty
     if ((e = M.alloc_t(&M.step, 1)) != hipSuccess) return fail_free(e);
     M.out_cap = (size_t)c.max_seq + 1;
     if ((e = M.alloc_t(&M.out_tokens, M.out_cap)) != hipSuccess) return fail_free(e);
-    const size_t kmax = (size_t)std::max(std::max(c.dim, c.ffn_dim), M.q_dim);
-    if ((e = M.alloc(&M.gemm_scratch, rdl::gemm_scratch_bytes(mb, kmax, false))) != hipSuccess) return fail_free(e);
+    // GEMM scratch for every chunk size and matrix shape the prefill runs
+    size_t gsb = 0, nmax = 0;
+    const size_t shapes[][2] = {{(size_t)M.qkv_dim, (size_t)c.dim}, {(size_t)c.dim, (size_t)M.q_dim},
+                                {2 * (size_t)c.ffn_dim, (size_t)c.dim}, {(size_t)c.dim, (size_t)c.ffn_dim},
+                                {(size_t)M.q_dim, (size_t)c.dim}, {(size_t)c.n_kv_heads * c.head_dim, (size_t)c.dim},
+                                {(size_t)c.ffn_dim, (size_t)c.dim}};
+    for (const auto& sh : shapes) {
+        nmax = std::max(nmax, sh[0]);
+        // every skinny shape (it depends on ceil(m / 16)) and the largest chunk
+        for (size_t mm : {(size_t)16, (size_t)32, (size_t)48, (size_t)64, mb})
+            gsb = std::max(gsb, rdl::gemm_scratch_bytes(std::min(mm, mb), sh[0], sh[1], false));
+    }
+    if ((e = M.alloc(&M.gemm_scratch, gsb)) != hipSuccess) return fail_free(e);
+    if ((e = M.alloc_t(&M.gemm_cnt, rdl::gemm_counter_count(nmax))) != hipSuccess) return fail_free(e);
+    if ((e = hipMemset(M.gemm_cnt, 0, rdl::gemm_counter_count(nmax) * sizeof(int))) != hipSuccess)
+        return fail_free(e);
     if (any_split_qkv && (e = M.alloc_t(&M.part_tmp, mb * M.qkv_dim)) != hipSuccess) return fail_free(e);
     // (row-pair epilogues need at most 4 columns per lane: dim <= 8192)
     M.fused_shapes = (c.dim / 32) % 2 == 0 && (M.q_dim / 32) % 2 == 0 && (c.ffn_dim / 32) % 2 == 0 &&

@@ -132,6 +132,52 @@ def test_graph_replays_match_eager(rq, gpu):
         _ = (xt * 2).sum().item()  # unrelated eager work between replays
 
 
+def test_skinny_gemm_calls_on_one_handle(rq, gpu):
+    """Prefill products of 5 .. 64 rows through one device handle: its
+    stream's work memory grows with the largest call, the split GEMM's
+    counters return to zero after every launch, and each result equals the
+    synchronous entry point's (same kernels, same split) bit for bit."""
+    import torch
+
+    n, k = 4096, 4096
+    w = synth.q4_0_weights(n, k, 140)
+    _, h = dev_weight(rq, torch, w, 2, n, k)
+    s = torch.cuda.current_stream().cuda_stream
+    for m in (16, 64, 16, 5, 40, 64):
+        x = synth.activations(m, k, 141 + m)
+        xt = torch.from_numpy(x.reshape(-1)).cuda()
+        yt = torch.empty(m * n, dtype=torch.float32, device="cuda")
+        h.forward_dev(xt.data_ptr(), m, yt.data_ptr(), rq.MODE_FLOAT, s)
+        torch.cuda.synchronize()
+        want = rq.matmul_f32_q4(x, w, m, k, n)
+        assert np.array_equal(yt.cpu().numpy(), want.reshape(-1)), f"m={m}"
+
+
+def test_skinny_gemm_graph_replays_match_eager(rq, gpu):
+    """A 16-row prefill product captured in a graph (graph-owned scratch and
+    counters, zeroed by a kernel on every replay) reproduces the eager result
+    bit for bit on every replay."""
+    import torch
+
+    n, k, m = 4096, 4096, 16
+    _, h = dev_weight(rq, torch, synth.q4_0_weights(n, k, 150), 2, n, k)
+    xt = torch.from_numpy(synth.activations(m, k, 151).reshape(-1)).cuda()
+    y = torch.empty(m * n, dtype=torch.float32, device="cuda")
+    h.forward_dev(xt.data_ptr(), m, y.data_ptr(), rq.MODE_FLOAT, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    eager = y.cpu().numpy().copy()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        h.forward_dev(xt.data_ptr(), m, y.data_ptr(), rq.MODE_FLOAT, torch.cuda.current_stream().cuda_stream)
+    for rep in range(4):
+        y.fill_(-1.0)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(y.cpu().numpy(), eager), f"replay {rep}"
+        _ = (xt * 2).sum().item()  # unrelated eager work between replays
+
+
 def test_time_next_launch(rq, gpu):
     import torch
 

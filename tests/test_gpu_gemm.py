@@ -89,6 +89,34 @@ def test_nan_row_stays_in_its_row(rq, gpu):
     assert np.all(np.isfinite(np.delete(y, 6, axis=0)))
 
 
+# small M (m <= 64): the direct-load kernel that splits x per block itself
+@pytest.mark.parametrize("m,n,k", [(5, 16, 256), (15, 33, 1024), (16, 4096, 4096), (17, 48, 4128),
+                                   (31, 7, 96), (32, 256, 4096), (48, 100, 2080), (63, 130, 1056),
+                                   (64, 4096, 4096), (20, 16400, 256)])
+def test_small_m_shapes(rq, orc, gpu, m, n, k):
+    # 16400 rows: two row tiles a workgroup with a ragged last tile
+    run(rq, orc, m, n, k, 7 + m + n + k)
+
+
+def test_small_m_block_extremes(rq, orc, gpu):
+    # per-block scaling: all-zero, subnormal, huge and mixed-magnitude blocks
+    # each keep the bar; an infinite element makes its row non-finite only
+    m, n, k = 24, 80, 1024
+    x = synth.activations(m, k, 91)
+    w = synth.q4_0_weights(n, k, 92)
+    x[1, 0:32] = 0.0                                   # a zero block
+    x[2, 64:96] = np.float32(3e-41)                    # subnormal block
+    x[3, 128:160] *= np.float32(1e30)                  # huge block
+    x[4, :] *= (2.0 ** np.repeat(np.linspace(-60, 60, k // 32), 32)).astype(np.float32)  # blocks 2^-60 .. 2^60
+    x[5, :] = 0.0                                      # a zero row
+    check_parity(rq.matmul_f32_q4(x, w, m, k, n), orc.matmul("q4", x, w, m, k, n),
+                 exact_f64(orc, "q4", x, w, m, k, n))
+    x[6, 200] = np.inf
+    y = rq.matmul_f32_q4(x, w, m, k, n).reshape(m, n)
+    assert not np.any(np.isfinite(y[6]))
+    assert np.all(np.isfinite(np.delete(y, 6, axis=0)))
+
+
 # ---- native mode (matmul_f32_q4_native) on the int8 matrix cores ---------------------
 def _native_exact(orc, x, w, m, k, n):
     part = orc.block_dots(x, w, m, k, n).astype(np.float64)
