@@ -541,7 +541,9 @@ __device__ __forceinline__ f32x4 ld_coh16(const float* p) {
     return f32x4{a.x, a.y, b.x, b.y};
 }
 
-template <int MT, int JT, int WR>
+// EVEN: nb and the slice length even, so every chunk's first block starts on a
+// dword and a lane's weight words sit at fixed offsets from one base.
+template <int MT, int JT, int WR, bool EVEN>
 __global__ __launch_bounds__(SK_WAVES * 64) void gemm_q4_0_skinny_kernel(
     const uint8_t* __restrict__ W, int n, int nb, const float* __restrict__ X, int m, float* __restrict__ Y, int S,
     int kbs, float* __restrict__ part, int* __restrict__ cnt) {
@@ -572,6 +574,23 @@ __global__ __launch_bounds__(SK_WAVES * 64) void gemm_q4_0_skinny_kernel(
     // holds the 12 dword-aligned bytes holding its 8 nibble bytes (and, for
     // h == 0, the block's d)
     auto load_w = [&](int c, WRegs& R) {
+        if constexpr (EVEN) {
+            // block b0 + q of row j starts at j row_bytes + 18 b0 + 18 q, on a
+            // dword for even q and 2 bytes past one for odd q; rows >= n fall
+            // past the buffer (zeros), blocks past the slice get d = 0 below
+            const uint32_t bc = (uint32_t)(kb0 + c * KCB + wk * KBW);
+#pragma unroll
+            for (int jt = 0; jt < JT; jt++) {
+                const uint32_t base =
+                    (uint32_t)(j0 + (wr * JT + jt) * 16 + r) * row_bytes + bc * 18u + 8u * (uint32_t)h;
+#pragma unroll
+                for (int q = 0; q < KBW; q++) {
+                    const auto v = __builtin_amdgcn_raw_buffer_load_b96(wrs, (int)(base + 18u * q - 2u * (q & 1)), 0, 0);
+                    R.w[jt][q][0] = v[0], R.w[jt][q][1] = v[1], R.w[jt][q][2] = v[2];
+                }
+            }
+            return;
+        }
 #pragma unroll
         for (int jt = 0; jt < JT; jt++) {
             const int j = j0 + (wr * JT + jt) * 16 + r;
@@ -664,13 +683,17 @@ __global__ __launch_bounds__(SK_WAVES * 64) void gemm_q4_0_skinny_kernel(
             const uint32_t j = (uint32_t)(j0 + (wr * JT + jt) * 16 + r);
 #pragma unroll
             for (int q = 0; q < KBW; q++) {
-                const uint32_t boff = j * row_bytes + (uint32_t)(kb0 + c * KCB + wk * KBW + q) * 18u;
-                const bool odd = (boff & 2u) != 0;  // the block starts 2 bytes into a dword
+                const int b = kb0 + c * KCB + wk * KBW + q;
+                const bool odd = EVEN ? (q & 1) != 0  // the block starts 2 bytes into a dword
+                                      : ((j * row_bytes + (uint32_t)b * 18u) & 2u) != 0;
                 const uint32_t lo = odd ? R.w[jt][q][1] : perm(R.w[jt][q][1], R.w[jt][q][0], 0x05040302u);
                 const uint32_t hi = odd ? R.w[jt][q][2] : perm(R.w[jt][q][2], R.w[jt][q][1], 0x05040302u);
                 const uint32_t sh = (g >> 1) * 4;
                 aq[jt][q] = q_f16((lo >> sh) & 0x0F0F0F0Fu, (hi >> sh) & 0x0F0F0F0Fu);
-                if (g == 0) dw[(jt * KBW + q) * 16 + r] = h2f(odd ? R.w[jt][q][0] >> 16 : R.w[jt][q][0] & 0xFFFFu);
+                if (g == 0) {
+                    const float d = h2f(odd ? R.w[jt][q][0] >> 16 : R.w[jt][q][0] & 0xFFFFu);
+                    dw[(jt * KBW + q) * 16 + r] = (!EVEN || b < kb1) ? d : 0.0f;
+                }
             }
         }
         // the raw registers are free: the next chunk's x, then its weights,
@@ -783,6 +806,7 @@ __global__ __launch_bounds__(SK_WAVES * 64) void gemm_q4_0_skinny_kernel(
 // slice.
 struct SkPlan {
     int mt, R, strips, S, kbs, units;
+    bool even;  // nb and kbs even (EVEN kernels)
 };
 inline SkPlan skinny_plan(size_t m, size_t n, int nb, bool can_split) {
     SkPlan p{};
@@ -794,16 +818,18 @@ inline SkPlan skinny_plan(size_t m, size_t n, int nb, bool can_split) {
     int S = can_split ? (device_cu_count() + p.strips / 2) / p.strips : 1;
     S = std::max(1, std::min(S, std::min(16, nb)));
     p.kbs = (nb + S - 1) / S;
+    p.even = nb % 2 == 0;
+    if (p.even) p.kbs += p.kbs & 1;
     p.S = (nb + p.kbs - 1) / p.kbs;  // no empty slices
     return p;
 }
 
-template <int MT, int JT, int WR>
+template <int MT, int JT, int WR, bool EVEN>
 hipError_t launch_skinny_cfg(const uint8_t* w, int n, int nb, const float* x, int m, float* y, const SkPlan& p,
                              float* part, int* cnt, hipStream_t s) {
     using C = SkCfg<MT, JT, WR>;
     static_assert(C::LDS <= 160 * 1024, "LDS per workgroup");
-    auto kern = gemm_q4_0_skinny_kernel<MT, JT, WR>;
+    auto kern = gemm_q4_0_skinny_kernel<MT, JT, WR, EVEN>;
     if (C::LDS > 65536) {
         static const hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                                         C::LDS);  // once per kernel and process
@@ -817,11 +843,19 @@ hipError_t launch_skinny_cfg(const uint8_t* w, int n, int nb, const float* x, in
 hipError_t launch_skinny(const uint8_t* w, int n, int nb, const float* x, int m, float* y, float* part, int* cnt,
                          hipStream_t s) {
     const SkPlan p = skinny_plan((size_t)m, (size_t)n, nb, part != nullptr && cnt != nullptr);
+    if (p.even) {
+        switch (p.mt) {
+            case 1: return launch_skinny_cfg<1, 4, 1, true>(w, n, nb, x, m, y, p, part, cnt, s);
+            case 2: return launch_skinny_cfg<2, 4, 1, true>(w, n, nb, x, m, y, p, part, cnt, s);
+            case 3: return launch_skinny_cfg<3, 4, 2, true>(w, n, nb, x, m, y, p, part, cnt, s);
+            default: return launch_skinny_cfg<4, 4, 2, true>(w, n, nb, x, m, y, p, part, cnt, s);
+        }
+    }
     switch (p.mt) {
-        case 1: return launch_skinny_cfg<1, 4, 1>(w, n, nb, x, m, y, p, part, cnt, s);
-        case 2: return launch_skinny_cfg<2, 4, 1>(w, n, nb, x, m, y, p, part, cnt, s);
-        case 3: return launch_skinny_cfg<3, 4, 2>(w, n, nb, x, m, y, p, part, cnt, s);
-        default: return launch_skinny_cfg<4, 4, 2>(w, n, nb, x, m, y, p, part, cnt, s);
+        case 1: return launch_skinny_cfg<1, 4, 1, false>(w, n, nb, x, m, y, p, part, cnt, s);
+        case 2: return launch_skinny_cfg<2, 4, 1, false>(w, n, nb, x, m, y, p, part, cnt, s);
+        case 3: return launch_skinny_cfg<3, 4, 2, false>(w, n, nb, x, m, y, p, part, cnt, s);
+        default: return launch_skinny_cfg<4, 4, 2, false>(w, n, nb, x, m, y, p, part, cnt, s);
     }
 }
 
