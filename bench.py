@@ -38,7 +38,11 @@ PEAK_I8_TOPS = 5000.0     # dense int8 MFMA, MI355X
 N_OUT, K_IN = 11008, 4096
 SEED = 0x5EED0002
 # the kernel the library launches for this workload (8-wave workgroups, 3 rows per wave)
-KERNEL_KEY = "gemv_fused_kernel<2, false, 3, 2, true, 8>|config2"
+KERNEL_KEY = "gemv_fused_kernel<2, false, 3, 2, true, 8, 0, 0>|config2"
+# the kernels of configs 1 and 3 (keys of profiles/traffic.json)
+Q8_KEY = "gemv_fused_kernel<8, false, 4, 2, true, 4, 0, 0>|config1"
+Q4K_UP_KEY = "gemv_q4k_fused_kernel<4, 8, 0, 0>|config3 up"
+Q4K_DOWN_KEY = "gemv_q4k_splitk_kernel<4, 4, 16, 0, 0>|config3 down"
 # configs[4]
 LLAMA_SEED = 0x5EED0005
 PROMPT_LEN, GEN_TOKENS = 128, 256
@@ -273,12 +277,18 @@ class Rig:
 
     def time_gemv(self, weights, x, y, steps, warmup):
         """(graph-replay ms per step, sorted per-launch kernel ms) for y = W_i x."""
-        torch, rq = self.torch, self.rq
-        sh = self.stream.cuda_stream
+        rq = self.rq
 
         def step(i, s_handle):
             weights[i % len(weights)][1].forward_dev(x.data_ptr(), 1, y.data_ptr(), rq.MODE_FLOAT, s_handle)
 
+        return self.time_launches(step, steps, warmup)
+
+    def time_launches(self, step, steps, warmup):
+        """(graph-replay ms per step, sorted per-launch kernel ms) for
+        step(i, stream_handle), one library launch per step."""
+        torch, rq = self.torch, self.rq
+        sh = self.stream.cuda_stream
         for i in range(warmup):
             step(i, sh)
         torch.cuda.synchronize()
@@ -356,8 +366,9 @@ def exact_check(rig, weight, x, y, m, n, k):
     return ok
 
 
-def gemv_line(rig, name, dtype, n, k, seed, steps, warmup):
-    """One GEMV configuration: throughput, kernel roofline and a parity spot check."""
+def gemv_line(rig, name, dtype, n, k, seed, steps, warmup, traffic_key=None):
+    """One GEMV configuration: throughput, kernel roofline (with the committed
+    counter traffic for traffic_key when on file) and a parity spot check."""
     torch = rig.torch
     w_host, weights = rig.weight_copies(dtype, n, k, seed)
     x_host = rig.synth.activations(1, k, seed + 100)
@@ -385,6 +396,7 @@ def gemv_line(rig, name, dtype, n, k, seed, steps, warmup):
             "frac": round(abytes / (kavg * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
             "kernel_avg_us": round(kavg * 1e3, 3),
             "kernel_median_us": round(kern_ms[len(kern_ms) // 2] * 1e3, 3),
+            "traffic": measured_traffic(traffic_key) if traffic_key else None,
         },
         "parity_vs_exact": ok,
     }
@@ -443,6 +455,47 @@ def gemm_lines(rig, ms_list, seed=0x5EED0004, native=False):
     del weights
     torch.cuda.empty_cache()
     return out
+
+
+# weight bytes of the GEMV configs the plain read is compared with
+READ_SIZES = [("config1 Q8_0 4096x4096", 4096 * 128 * 34), ("config2 Q4_0 11008x4096", 11008 * 128 * 18),
+              ("config3 down Q4_K 4096x14336", 4096 * 56 * 144)]
+
+
+def read_lines(rig, steps=200, warmup=20):
+    """The HBM read ceiling of a plain kernel (rdl_stream_read_dev: one
+    streaming read, no arithmetic) at the weight sizes of configs 1-3, over
+    rotated copies (>= 400 MB, beyond the 256 MB Infinity Cache), timed as the
+    GEMV lines are: graph replay per step and per-launch kernel events."""
+    torch, rq = rig.torch, rig.rq
+    out_len = 2 * 256 * 4
+    out = torch.empty(out_len, dtype=torch.int32, device=rig.dev)
+    lines = []
+    for name, nbytes in READ_SIZES:
+        nbytes -= nbytes % 16
+        copies = max(16, -(-400 * 2**20 // nbytes))
+        bufs = [torch.randint(0, 255, (nbytes,), dtype=torch.uint8, device=rig.dev) for _ in range(copies)]
+
+        def step(i, s_handle):
+            rq.stream_read_dev(bufs[i % copies].data_ptr(), nbytes, out.data_ptr(), out_len, s_handle)
+
+        ms_step, kern_ms = rig.time_launches(step, steps, warmup)
+        avg = sum(kern_ms) / len(kern_ms)
+        med = kern_ms[len(kern_ms) // 2]
+        lines.append({
+            "workload": f"plain streaming read of {nbytes} bytes ({name} weight bytes)",
+            "bytes": nbytes,
+            "copies_rotated": copies,
+            "ms_per_step": round(ms_step, 6),
+            "kernel_avg_us": round(avg * 1e3, 3),
+            "kernel_median_us": round(med * 1e3, 3),
+            "GBs_kernel_avg": round(nbytes / (avg * 1e-3) / 1e9, 1),
+            "GBs_per_step": round(nbytes / (ms_step * 1e-3) / 1e9, 1),
+            "frac_of_8TBs": round(nbytes / (avg * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
+        })
+        del bufs
+        torch.cuda.empty_cache()
+    return lines
 
 
 def decode_bytes_per_token(cfg, ctx_mean):
@@ -670,7 +723,7 @@ def main():
     ap.add_argument("--copies", type=int, default=24)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--workload", default="all", choices=["all", "gemv", "q8_0", "q4_k", "q6_k", "gemm", "decode", "decode_q4_k_m", "load"],
+    ap.add_argument("--workload", default="all", choices=["all", "gemv", "q8_0", "q4_k", "q6_k", "gemm", "decode", "decode_q4_k_m", "load", "read"],
                     help="all: the headline line plus configs 1, 3, 4, 5 and the Q6_K lm_head; otherwise only one "
                          "(load: the GGUF file load, decode_q4_k_m: a Q4_K_M-mixed 7B decode; run only "
                          "when asked)")
@@ -699,15 +752,17 @@ def main():
         del src, dst
 
     wl = args.workload
-    if wl in ("q8_0", "q4_k", "q6_k", "gemm", "decode", "decode_q4_k_m", "load"):
-        if wl == "q8_0":
+    if wl in ("q8_0", "q4_k", "q6_k", "gemm", "decode", "decode_q4_k_m", "load", "read"):
+        if wl == "read":
+            line = read_lines(rig)
+        elif wl == "q8_0":
             line = gemv_line(rig, "config1: Q8_0 GEMV 4096x4096", 8, 4096, 4096, 0x5EED0001,
-                             args.steps, args.warmup)
+                             args.steps, args.warmup, Q8_KEY)
         elif wl == "q4_k":
             line = [gemv_line(rig, "config3 up: Q4_K GEMV 14336x4096", 12, 14336, 4096, 0x5EED0003,
-                              args.steps, args.warmup),
+                              args.steps, args.warmup, Q4K_UP_KEY),
                     gemv_line(rig, "config3 down: Q4_K GEMV 4096x14336", 12, 4096, 14336, 0x5EED0013,
-                              args.steps, args.warmup)]
+                              args.steps, args.warmup, Q4K_DOWN_KEY)]
         elif wl == "q6_k":
             line = gemv_line(rig, Q6K_LM_HEAD, 14, 32000, 4096, 0x5EED0006, args.steps, args.warmup)
         elif wl == "gemm":
@@ -784,15 +839,16 @@ def main():
         sub_warm = min(args.warmup, 50)
         out["workloads"] = {
             "config1_q8_0": gemv_line(rig, "config1: Q8_0 GEMV 4096x4096", 8, 4096, 4096, 0x5EED0001,
-                                      sub_steps, sub_warm),
+                                      sub_steps, sub_warm, Q8_KEY),
             "config3_q4_k_up": gemv_line(rig, "config3 up: Q4_K GEMV 14336x4096", 12, 14336, 4096,
-                                         0x5EED0003, sub_steps, sub_warm),
+                                         0x5EED0003, sub_steps, sub_warm, Q4K_UP_KEY),
             "config3_q4_k_down": gemv_line(rig, "config3 down: Q4_K GEMV 4096x14336", 12, 4096, 14336,
-                                           0x5EED0013, sub_steps, sub_warm),
+                                           0x5EED0013, sub_steps, sub_warm, Q4K_DOWN_KEY),
             "q6_k_lm_head": gemv_line(rig, Q6K_LM_HEAD, 14, 32000, 4096, 0x5EED0006, sub_steps, sub_warm),
             "config4_gemm": gemm_lines(rig, [16, 64, 512, 2048]),
             "config4_gemm_native": gemm_lines(rig, [512, 2048], native=True),
             "config5_decode": decode_line(rig),
+            "read_ceiling": read_lines(rig, sub_steps, sub_warm),
         }
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)

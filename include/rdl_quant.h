@@ -194,6 +194,14 @@ rdl_status rdl_linear_forward_dev(const rdl_weight* w, const float* x_dev, size_
 rdl_status rdl_linear_forward_dev_noalloc(const rdl_weight* w, const float* x_dev, size_t m,
                                           float* y_dev, int32_t mode, void* stream);
 
+/* Measurement aid, no reference counterpart: one streaming read of `bytes`
+ * (a multiple of 16, below 2^31) of device memory at buf_dev by 2 x CUs
+ * workgroups, each XOR-folding its contiguous share into out_dev[workgroup]
+ * (out_len >= 2 x CUs words).  The HBM read rate of a plain kernel, timed
+ * like the product launches (rdl_time_next_launch). */
+rdl_status rdl_stream_read_dev(const void* buf_dev, size_t bytes, uint32_t* out_dev, size_t out_len,
+                               void* stream);
+
 /* ---- device building blocks ----------------------------------------------
  * The product kernels read activations as per-32-element "records" (an exact
  * 24-bit fixed-point code in float mode, the Q8_0 code of quantize_row_q8_0 in

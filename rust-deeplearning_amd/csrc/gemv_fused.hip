@@ -1819,9 +1819,13 @@ hipError_t launch_gemv_fused(WType t, bool native, const uint8_t* w, size_t n, s
     // everything else one 16-wave workgroup per CU.
     // Rows of more than 256 columns (K > 8192) run one row per wave in any case:
     // one 16-wave workgroup per CU (Q4_0 4096 x 14336: 11.1 -> 9.6 us).
+    // Q8_0 float rows of at most 128 blocks (two columns a lane): one 4-wave
+    // workgroup per CU, 4 rows a wave (4096 x 4096: 6.11 -> 5.83 us, swept
+    // over 4 / 8 / 16 waves x 1-6 workgroups per CU).
     const bool i4 = !native && (t == WType::Q4_0 || t == WType::Q4_1) && cpl_for(nb) < 8;
+    const bool q8_narrow = t == WType::Q8_0 && !native && cpl_for(nb) == 2;
     const bool two = i4 || (t == WType::Q8_0 && !native && cpl_for(nb) < 8);
-    const int nw = two ? 8 : 16, wg_per_cu = two ? 2 : 1;
+    const int nw = q8_narrow ? 4 : two ? 8 : 16, wg_per_cu = q8_narrow ? 1 : two ? 2 : 1;
     if (t == WType::Q6_K || t == WType::Q4_K) {
         if (native) return hipErrorInvalidValue;
         KqFuse fz{};

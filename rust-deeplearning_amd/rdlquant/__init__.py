@@ -109,6 +109,7 @@ _decl("rdl_quantize_row_q8_0_dev", _i32, _p, _sz, _p, _p, _p)
 _decl("rdl_dequantize_rows_dev", _i32, _p, _p, _sz, _p, _p)
 _decl("rdl_q4_0_q8_0_block_dots_dev", _i32, _p, _p, _p, _p)
 _decl("rdl_linear_fused_dev", _i32, _p, _p, _sz, _sz, _p, _i32, _p, C.c_float, _i32, _p)
+_decl("rdl_stream_read_dev", _i32, _p, _sz, _p, _sz, _p)
 
 PROLOGUE_NONE, PROLOGUE_RMSNORM, PROLOGUE_SWIGLU = 0, 1, 2
 EPILOGUE_STORE, EPILOGUE_RESIDUAL, EPILOGUE_SWIGLU = 0, 1, 2
@@ -167,6 +168,12 @@ def time_next_launch(start_event, stop_event):
     """Kernel-boundary timing of this thread's next product-kernel launch
     (hipEvent_t handles, e.g. torch.cuda.Event(enable_timing=True).cuda_event)."""
     check(lib.rdl_time_next_launch(start_event, stop_event))
+
+
+def stream_read_dev(buf_ptr: int, nbytes: int, out_ptr: int, out_len: int, stream) -> None:
+    """One plain streaming read of nbytes at buf_ptr (measurement aid): each
+    of the 2 x CUs workgroups XOR-folds its share into out[workgroup]."""
+    check(lib.rdl_stream_read_dev(buf_ptr, nbytes, out_ptr, out_len, stream))
 
 
 # ---- host drop-ins (rustml_quant) -----------------------------------------

@@ -178,6 +178,20 @@ def test_skinny_gemm_graph_replays_match_eager(rq, gpu):
         _ = (xt * 2).sum().item()  # unrelated eager work between replays
 
 
+def test_stream_read_folds_every_word(rq, gpu):
+    """The plain-read measurement kernel reads every 16-byte unit once: the
+    XOR of its per-workgroup words is the XOR of all 32-bit words."""
+    import torch
+
+    nbytes = 3 * 2**20 + 48
+    data = np.random.default_rng(5).integers(0, 2**32, nbytes // 4, dtype=np.uint32)
+    buf = torch.from_numpy(data.view(np.int32)).cuda()
+    out = torch.zeros(2048, dtype=torch.int32, device="cuda")
+    rq.stream_read_dev(buf.data_ptr(), nbytes, out.data_ptr(), out.numel(), torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert np.bitwise_xor.reduce(out.cpu().numpy().view(np.uint32)) == np.bitwise_xor.reduce(data)
+
+
 def test_time_next_launch(rq, gpu):
     import torch
 
