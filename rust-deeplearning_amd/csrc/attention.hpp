@@ -4,23 +4,47 @@
 // attention fused in (gemv_fused.hip).
 #pragma once
 
+#include <type_traits>
+
 #include "rdl_device.hpp"
 #include "rdl_internal.hpp"
 
 namespace rdl {
 namespace att {
 
+// v[l ^ 16] and v[l ^ 32] through gfx950's permlane swaps (no LDS round trip):
+// each swap returns the lane's own value and its partner's, in some order.
+__device__ __forceinline__ void pair16(float v, float& a, float& b) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v),
+                                                    false, false);
+    const uint32_t lo = r[0], hi = r[1];
+    a = __builtin_bit_cast(float, lo), b = __builtin_bit_cast(float, hi);
+}
+__device__ __forceinline__ void pair32(float v, float& a, float& b) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v),
+                                                    false, false);
+    const uint32_t lo = r[0], hi = r[1];
+    a = __builtin_bit_cast(float, lo), b = __builtin_bit_cast(float, hi);
+}
+// Sum / max over the 64 lanes, in every lane (both lanes of each pair form
+// the same commutative result, so every lane holds the same bits).
 __device__ __forceinline__ float wave_sum(float v) {
     v = sum8_f32(v);
     v += dpp_f32<DPP_ROW_MIRROR>(v);
-    v += __shfl_xor(v, 16);
-    return v + __shfl_xor(v, 32);
+    float a, b;
+    pair16(v, a, b);
+    v = a + b;
+    pair32(v, a, b);
+    return a + b;
 }
 __device__ __forceinline__ float wave_max(float v) {
     v = max8_f32(v);
     v = fmaxf(v, dpp_f32<DPP_ROW_MIRROR>(v));
-    v = fmaxf(v, __shfl_xor(v, 16));
-    return fmaxf(v, __shfl_xor(v, 32));
+    float a, b;
+    pair16(v, a, b);
+    v = fmaxf(a, b);
+    pair32(v, a, b);
+    return fmaxf(a, b);
 }
 
 // Attention of query row s (position pos + s) and head h over the cached keys
@@ -45,38 +69,80 @@ static_assert(KV_PAGE % ATT_CHUNK == 0, "an attention chunk lies in one cache pa
 // uses several workgroups, and the last of them to finish combines their
 // partials (device-scope counter, chunk order fixed: deterministic).
 constexpr int ATT_WAVES = 8;
+static_assert(ATT_WAVES <= 8, "the chunk combine reduces over one 8-lane group");
 constexpr int ATT_SPAN = ATT_CHUNK * ATT_WAVES;
 
 // One step of the transposed sum of N values over N lanes (lane index c within
-// its group of N): the lane keeps the half of its values selected by bit HF
-// of c and adds the partner lane's (c ^ HF) copy of that half.  After the
-// steps HF = N/2, ..., 1, v[0] of lane c is the group's total of value c.
+// its aligned group of N <= 16): the lane keeps the half of its values
+// selected by bit HF of c and adds the partner lane's copy of that half.  The
+// partner is any lane of the group with the other value of bit HF and the same
+// higher bits: row_mirror (15 - c), row_half_mirror (c ^ 7 within 8 lanes),
+// quad_perm (c ^ 2, c ^ 1) -- DPP moves, no LDS round trip.  After the steps HF
+// = N/2, ..., 1, v[0] of lane c is the group's total of value c.
 template <int HF, int N>
 __device__ __forceinline__ void transposed_sum(float (&v)[N], int c) {
     if constexpr (HF >= 1) {
+        static_assert(HF <= 8, "groups of at most 16 lanes");
+        constexpr int CTRL = HF == 8 ? DPP_ROW_MIRROR : HF == 4 ? DPP_ROW_HALF_MIRROR : HF == 2 ? DPP_QUAD_XOR2
+                                                                                                   : DPP_QUAD_XOR1;
         const bool up = (c & HF) != 0;
 #pragma unroll
         for (int j = 0; j < HF; j++) {
             const float send = up ? v[j] : v[j + HF];
             const float keep = up ? v[j + HF] : v[j];
-            v[j] = keep + __shfl_xor(send, HF);
+            v[j] = keep + dpp_f32<CTRL>(send);
         }
         transposed_sum<HF / 2, N>(v, c);
     }
 }
 
+// Sum over each aligned group of N = 8 or 16 lanes, in every lane of the group.
+template <int N>
+__device__ __forceinline__ float group_sum(float v) {
+    static_assert(N == 8 || N == 16, "8- or 16-lane groups");
+    v = sum8_f32(v);
+    if constexpr (N == 16) v += dpp_f32<DPP_ROW_MIRROR>(v);
+    return v;
+}
+
+// f(std::integral_constant<int, I>) for I = B .. E - 1, in order.
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
+}
+
+// Lane i of each 16-lane row, in every lane of the row (DPP row_newbcast).
+template <int I>
+__device__ __forceinline__ float row_bcast(float v) {
+    return dpp_f32<0x150 + I>(v);
+}
+
+// Tagged exchange between the q/k/v workgroups and the attention workgroups
+// of one fused launch: the value v of q/k/v row r for the token at cache
+// position p is the 8-byte word (p + 1) << 32 | bits(v) at xch[r], written
+// and read as single-copy-atomic agent-scope stores / loads (global_store /
+// global_load ... sc1, served at the device's coherence point, never from a
+// non-coherent L1 / L2 line).  A reader that sees the tag it expects therefore
+// sees that launch's value, with no counter, fence or second read.  Tags grow
+// from launch to launch on one exchange until the cache is emptied (which
+// zeroes it), so a word left by an earlier launch never matches.
+__device__ __forceinline__ void xch_put(uint64_t* p, float v, int tag) {
+    const uint64_t word = ((uint64_t)(uint32_t)tag << 32) | __builtin_bit_cast(uint32_t, v);
+    __hip_atomic_store(p, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t xch_get(const uint64_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool xch_ok(uint64_t word, int tag) { return (uint32_t)(word >> 32) == (uint32_t)tag; }
+__device__ __forceinline__ float xch_val(uint64_t word) { return __builtin_bit_cast(float, (uint32_t)word); }
+
 // Arguments of one attention launch.  Fused launches (FUSED, attention in
-// the q/k/v launch): the q rows and the current position's cache rows come
-// from workgroups of the same launch (written with agent-coherent stores).
-// Each KV group has a PUB_SLOT-int slot of pub: the group's producer
-// workgroups count themselves at PUB_COUNT, and the one that completes the
-// count returns it to 0 and writes the launch's position + 1 at PUB_READY;
-// the group's attention waves wait for that value.  Positions grow from
-// launch to launch until the cache is emptied (which zeroes pub), so a value
-// left by an earlier launch never matches.  Count and flag sit on separate
-// 128-byte lines, and the consumers only read: no atomic of theirs queues
-// behind the producers' adds.
-constexpr int PUB_SLOT = 64, PUB_COUNT = 0, PUB_READY = 32;
+// the q/k/v launch): head h's q row and its KV head's current k / v rows come
+// from workgroups of the same launch through the exchange xch ([q heads | k
+// heads | v heads] x hd tagged words, see xch_put).
 template <typename KV>
 struct AttArgs {
     const float* qkv;          // [rows][qkv_dim]: q heads | k heads | v heads
@@ -91,33 +157,48 @@ struct AttArgs {
     int nspan;
     int* counters;             // [rows][n_heads] span counters
     float* out;                // [rows][n_heads * hd]
-    const int* pub;            // FUSED: [n_kv][PUB_SLOT] count / ready slots
+    const uint64_t* xch;       // FUSED: the layer's exchange
     int* err;                  // FUSED: set when a wait runs out (never in a correct launch)
 };
 
-// Coherent (agent-scope) loads of values another workgroup of the same launch
-// published with coherent stores.
-template <typename T>
-__device__ __forceinline__ T ld_coh8(const T* p) {
-    static_assert(sizeof(T) == 16, "16-byte pieces");
-    const uint64_t* q = reinterpret_cast<const uint64_t*>(p);
-    const uint64_t a = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const uint64_t b = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    struct P { uint64_t a, b; } r{a, b};
-    return __builtin_bit_cast(T, r);
-}
-
-// Bounded wait of one fused attention wave until its KV group's producers
-// have marked the position ready (every lane reads the same word).
-__device__ __forceinline__ void wave_wait_ready(const int* ready, int want, int* err) {
-    int spins = 0;
-    for (;;) {
-        const int v = __builtin_amdgcn_readfirstlane(__hip_atomic_load(ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-        if (v == want) break;
-        __builtin_amdgcn_s_sleep(2);
-        if (++spins > (1 << 20)) {  // about a second: only a broken launch gets here
+// Wave 0 of a fused attention workgroup: poll the exchange until head h's q
+// row and, when the workgroup's span holds the current position (cur), the
+// KV head's current k and v rows carry tag t; leave them in LDS: q as f32
+// (qs), k and v in the cache's type (kn, vn), rounded as the cache writer
+// rounds them.  Bounded: a wait that runs out sets *err (which a correct launch
+// never does) and leaves what it last read.
+template <typename KV, int HD>
+__device__ __forceinline__ void wave_poll_exchange(const uint64_t* xq, const uint64_t* xk, const uint64_t* xv,
+                                                   bool cur, int t, float* qs, KV* kn, KV* vn, int* err) {
+    static_assert(HD == 64 || HD == 128, "one or two values a lane");
+    constexpr int PER = HD / 64;
+    const int d = (threadIdx.x & 63) * PER;
+    uint64_t q[PER], k[PER], v[PER];
+    for (int spins = 0;; spins++) {
+        bool ok = true;
+#pragma unroll
+        for (int i = 0; i < PER; i++) {
+            q[i] = xch_get(xq + d + i);
+            if (cur) {
+                k[i] = xch_get(xk + d + i);
+                v[i] = xch_get(xv + d + i);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < PER; i++) ok = ok && xch_ok(q[i], t) && (!cur || (xch_ok(k[i], t) && xch_ok(v[i], t)));
+        if (__builtin_amdgcn_ballot_w64(!ok) == 0) break;
+        if (spins > (1 << 16)) {  // tens of milliseconds: only a broken launch gets here
             if ((threadIdx.x & 63) == 0) __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        qs[d + i] = xch_val(q[i]);
+        if (cur) {
+            kn[d + i] = (KV)xch_val(k[i]);
+            vn[d + i] = (KV)xch_val(v[i]);
         }
     }
 }
@@ -166,101 +247,157 @@ __device__ __forceinline__ void attention_body(int bx, int by, int bz, float* __
         __syncthreads();
     }
     const int p0 = z * ATT_SPAN + w * ATT_CHUNK;
+    const bool active = p0 < t;  // wave-uniform
     float mx = -__builtin_inff(), l = 0.0f;
-    if (p0 < t) {  // wave-uniform
-        const int p = p0 + lane;
-        const bool valid = p < t;
-        typedef KV kvv __attribute__((ext_vector_type(V)));
-        // the chunk's 64 keys are one page of the cache: rows p0 .. p0 + 63
-        // at kb / vb + (p - p0) * hd
-        const size_t page = kv_row(kv_table, n_kv, kvh, p0, hd);
-        const KV* vb = vc + page;
-        const int nvalid = min(ATT_CHUNK, t - p0);
-        constexpr int KG = VPRE ? 64 / (CPR > 0 ? CPR : 1) : 1;
-        float acc = 0.0f;
-        if constexpr (VPRE) {
-            // K and V rows of the chunk in the same coalesced layout (load i of
-            // lane l = piece l % CPR of row KG i + l / CPR), all in flight
-            // before the query (which the previous launch wrote) is read: one
-            // memory round trip.  Rows past the length re-read the last valid row.
-            const KV* kb = kc + page;
-            kvv kreg[CPR], vreg[CPR];
-            const int vk = lane / CPR, pc = lane % CPR, ve = pc * V;
+    typedef KV kvv __attribute__((ext_vector_type(V)));
+    if constexpr (VPRE) {
+        // K and V rows of the chunk in the same coalesced layout (load i of
+        // lane l = piece l % CPR of row KG i + l / CPR), all in flight
+        // before the query is read: one memory round trip.  The chunk's 64
+        // keys are one page of the cache (rows p0 .. p0 + 63 at kb / vb +
+        // (p - p0) * hd).  The row's last key t - 1 (row cr of its chunk)
+        // does not take part in the loads: it is the one a fused launch
+        // writes itself, and in every launch it enters the scores and the
+        // context as an extra term (kcur, vcur: the lanes of row group cr % KG
+        // hold its pieces), so the fused and the separate attention do the
+        // same arithmetic.  Buffer loads over the rows before it: rows from
+        // cr on read as zeros without touching memory (a masked key has a
+        // finite V row and weight 0).
+        constexpr int KG = 64 / CPR;
+        const int cr = t - 1 - p0;  // the last key's row in this chunk (>= ATT_CHUNK: not in it)
+        const bool here = cr < ATT_CHUNK;
+        const int nvalid = active ? min(ATT_CHUNK, t - p0) : 0;
+        const int nload = here ? cr : nvalid;
+        const size_t page = active ? kv_row(kv_table, n_kv, kvh, p0, hd) : 0;
+        const uint32_t row_bytes = (uint32_t)hd * (uint32_t)sizeof(KV);
+        const __amdgpu_buffer_rsrc_t krs = make_rsrc(kc + page, (uint32_t)nload * row_bytes);
+        const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vc + page, (uint32_t)nload * row_bytes);
+        kvv kreg[CPR], vreg[CPR];
+        kvv kcur{}, vcur{};
+        const int vk = lane / CPR, pc = lane % CPR, ve = pc * V;
+        const bool mine = here && vk == cr % KG;  // the lane holds a piece of the last key
+        if (active) {
 #pragma unroll
-            for (int i = 0; i < CPR; i++) {
-                const int j = min(KG * i + vk, nvalid - 1);
-                kreg[i] = *reinterpret_cast<const kvv*>(kb + (size_t)j * hd + ve);
+            for (int i = 0; i < CPR; i++)
+                kreg[i] = __builtin_bit_cast(kvv, buf_load_b128(krs, (uint32_t)(KG * i + vk) * row_bytes + ve * sizeof(KV)));
+#pragma unroll
+            for (int i = 0; i < CPR; i++)
+                vreg[i] = __builtin_bit_cast(kvv, buf_load_b128(vrs, (uint32_t)(KG * i + vk) * row_bytes + ve * sizeof(KV)));
+            if constexpr (!FUSED) {  // the last key from the cache (the previous launch wrote it)
+                const __amdgpu_buffer_rsrc_t k1 = make_rsrc(kc + page, (uint32_t)nvalid * row_bytes);
+                const __amdgpu_buffer_rsrc_t v1 = make_rsrc(vc + page, (uint32_t)nvalid * row_bytes);
+                const uint32_t off = mine ? (uint32_t)cr * row_bytes + ve * sizeof(KV) : RSRC_OOB;
+                kcur = __builtin_bit_cast(kvv, buf_load_b128(k1, off));
+                vcur = __builtin_bit_cast(kvv, buf_load_b128(v1, off));
             }
-#pragma unroll
-            for (int i = 0; i < CPR; i++) {
-                const int j = min(KG * i + vk, nvalid - 1);
-                vreg[i] = *reinterpret_cast<const kvv*>(vb + (size_t)j * hd + ve);
-            }
-            float qv[V];
-            if constexpr (FUSED) {
-                // the rows before the current position are older launches'
-                // stores (loaded above); the current row and q are this
-                // launch's, published by the q/k/v workgroups: wait for them,
-                // then read them coherently (rows past the length re-read the
-                // current row, so they are reloaded too)
-                wave_wait_ready(a.pub + (size_t)kvh * PUB_SLOT + PUB_READY, t, a.err);
-                const int cur = t - 1 - p0;
-#pragma unroll
-                for (int i = 0; i < CPR; i++) {
-                    if (min(KG * i + vk, nvalid - 1) == cur) {
-                        kreg[i] = ld_coh8(reinterpret_cast<const kvv*>(kb + (size_t)cur * hd + ve));
-                        vreg[i] = ld_coh8(reinterpret_cast<const kvv*>(vb + (size_t)cur * hd + ve));
-                    }
-                }
+        }
+        float qv[V];
+        if constexpr (FUSED) {
+            // The keys before the last are older launches' stores (loaded
+            // above); q and the last key's k / v rows are this launch's: wave
+            // 0 polls them from the exchange into LDS while the loads are in
+            // flight.
+            KV* kn = reinterpret_cast<KV*>(os + ATT_WAVES * hd);
+            KV* vn = kn + hd;
+            const bool cur = (t - 1) / ATT_SPAN == z;
+            if (w == 0)
+                wave_poll_exchange<KV, HD>(a.xch + (size_t)h * hd, a.xch + (size_t)(n_heads + kvh) * hd,
+                                           a.xch + (size_t)(n_heads + n_kv + kvh) * hd, cur, t, qs, kn, vn, a.err);
+            __syncthreads();
+            if (active) {
 #pragma unroll
                 for (int e = 0; e < V; e += 4) {
-                    const float4 t4 = ld_coh8(reinterpret_cast<const float4*>(q + ve + e));
+                    const float4 t4 = *reinterpret_cast<const float4*>(qs + ve + e);
                     qv[e] = t4.x, qv[e + 1] = t4.y, qv[e + 2] = t4.z, qv[e + 3] = t4.w;
                 }
-            } else {
-#pragma unroll
-                for (int e = 0; e < V; e += 4) {
-                    const float4 t4 = *reinterpret_cast<const float4*>(q + ve + e);
-                    qv[e] = t4.x, qv[e + 1] = t4.y, qv[e + 2] = t4.z, qv[e + 3] = t4.w;
+                if (mine) {
+                    kcur = *reinterpret_cast<const kvv*>(kn + ve);
+                    vcur = *reinterpret_cast<const kvv*>(vn + ve);
                 }
             }
+        } else if (active) {
+#pragma unroll
+            for (int e = 0; e < V; e += 4) {
+                const float4 t4 = *reinterpret_cast<const float4*>(q + ve + e);
+                qv[e] = t4.x, qv[e + 1] = t4.y, qv[e + 2] = t4.z, qv[e + 3] = t4.w;
+            }
+        }
+        if (active) {
             __builtin_amdgcn_sched_barrier(0);  // keep every load ahead of the arithmetic
             // partial scores of the lane's CPR rows over its V dims, then a
-            // transposed sum over the CPR lanes of the row group: after the
-            // step of mask hf a lane keeps the half of its rows selected by
-            // bit hf of its piece, so piece c ends with row KG c + vk's score.
+            // transposed sum over the CPR lanes of the row group: piece c ends
+            // with row KG c + vk's score
             float ps[CPR];
 #pragma unroll
             for (int i = 0; i < CPR; i++) {
-                float a = 0.0f;
+                float acc = 0.0f;
 #pragma unroll
-                for (int e = 0; e < V; e++) a += qv[e] * (float)kreg[i][e];
-                ps[i] = a;
+                for (int e = 0; e < V; e++) acc += qv[e] * (float)kreg[i][e];
+                ps[i] = acc;
             }
             transposed_sum<CPR / 2, CPR>(ps, pc);
+            // the last key: its partial over the lane's dims, summed over its
+            // row group (zero elsewhere), joins the score of the lane that
+            // holds row cr (lane lcur; its loaded row was zeros)
+            const int lcur = (cr % KG) * CPR + cr / KG;
+            float pcur = 0.0f;
+#pragma unroll
+            for (int e = 0; e < V; e++) pcur += qv[e] * (float)kcur[e];
+            pcur = group_sum<CPR>(pcur);
             const int key = KG * pc + vk;  // the row whose score this lane holds
             const bool kvalid = key < nvalid;
-            const float sc = kvalid ? ps[0] / scale : -__builtin_inff();
+            const float sc = kvalid ? (ps[0] + (here && lane == lcur ? pcur : 0.0f)) / scale : -__builtin_inff();
             mx = wave_max(sc);
             const float e = kvalid ? expf(sc - mx) : 0.0f;
             l = wave_sum(e);
             float o[V];
 #pragma unroll
             for (int c = 0; c < V; c++) o[c] = 0.0f;
-#pragma unroll
-            for (int i = 0; i < CPR; i++) {
-                const float pj = __shfl(e, vk * CPR + i);  // row KG i + vk; rows past the length carry 0
+            // row KG i + vk's weight sits in piece i of the lane's row group
+            // (rows past the length carry 0 and zero V rows)
+            auto pv = [&](auto ic) {
+                constexpr int i = decltype(ic)::value;
+                float pj;
+                if constexpr (CPR == 16) pj = row_bcast<i>(e);
+                else pj = __shfl(e, vk * CPR + i);
 #pragma unroll
                 for (int c = 0; c < V; c++) o[c] += pj * (float)vreg[i][c];
+            };
+            static_for<0, CPR>(pv);
+            if (here) {  // the last key's weight times its V piece (zero pieces elsewhere)
+                const float pl = __shfl(e, lcur);
+#pragma unroll
+                for (int c = 0; c < V; c++) o[c] += pl * (float)vcur[c];
             }
+            if constexpr (CPR == 16 && V == 8) {
+                // sum over the 4 row groups (lanes l, l + 16, l + 32, l + 48)
+                // with permlane swaps: lane l ends with values c0 = 2 (2 * 0 +
+                // odd16) + hi32 and c1 = c0 + 4 of its piece
+                float r[4];
 #pragma unroll
-            for (int off = CPR; off < 64; off <<= 1)
+                for (int m = 0; m < 4; m++) r[m] = fold32(o[2 * m], o[2 * m + 1]);
+                const float s0 = fold16(r[0], r[1]), s1 = fold16(r[2], r[3]);
+                const int c0 = 2 * ((lane >> 4) & 1) + (lane >> 5);
+                os[w * hd + ve + c0] = s0;
+                os[w * hd + ve + c0 + 4] = s1;
+            } else {
 #pragma unroll
-                for (int c = 0; c < V; c++) o[c] += __shfl_xor(o[c], off);
-            if (lane < CPR)
+                for (int off = CPR; off < 64; off <<= 1)
 #pragma unroll
-                for (int c = 0; c < V; c++) os[w * hd + ve + c] = o[c];
-        } else {
+                    for (int c = 0; c < V; c++) o[c] += __shfl_xor(o[c], off);
+                if (lane < CPR)
+#pragma unroll
+                    for (int c = 0; c < V; c++) os[w * hd + ve + c] = o[c];
+            }
+        }
+    } else if (active) {
+        const int p = p0 + lane;
+        const bool valid = p < t;
+        const size_t page = kv_row(kv_table, n_kv, kvh, p0, hd);
+        const KV* vb = vc + page;
+        const int nvalid = min(ATT_CHUNK, t - p0);
+        float acc = 0.0f;
+        {
             const KV* kr = kc + page + (size_t)(valid ? p - p0 : 0) * hd;
             if constexpr (HD > 0) {
                 kvv kreg[HD / V];
@@ -310,19 +447,29 @@ __device__ __forceinline__ void attention_body(int bx, int by, int bz, float* __
     __syncthreads();
     // combine this workgroup's chunks (inactive waves carry m = -inf, l = 0)
     const int nw = min(ATT_WAVES, (t - z * ATT_SPAN + ATT_CHUNK - 1) / ATT_CHUNK);
-    float M = -__builtin_inff();
-    for (int c = 0; c < nw; c++) M = fmaxf(M, ml[c][0]);
-    float L = 0.0f;
-    for (int c = 0; c < nw; c++) L += ml[c][1] * expf(ml[c][0] - M);
     const int nz = (t + ATT_SPAN - 1) / ATT_SPAN;
+    if (nz == 1 && w * 64 >= hd) return;  // a wave with no outputs to form (whole wave)
+    // lane c < nw forms chunk c's weight exp(m_c - M); the sums read the
+    // weights back as scalars and add in chunk order
+    const float mcl = lane < nw ? ml[min(lane, ATT_WAVES - 1)][0] : -__builtin_inff();
+    const float M = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, max8_f32(mcl))));
+    const float wcl = lane < nw ? expf(mcl - M) : 0.0f;
+    float wc[ATT_WAVES];
+#pragma unroll
+    for (int c = 0; c < ATT_WAVES; c++) wc[c] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wcl), c));
+    float L = 0.0f;
+#pragma unroll
+    for (int c = 0; c < ATT_WAVES; c++) L = c < nw ? L + ml[c][1] * wc[c] : L;
     float* o = out + (size_t)s * n_heads * hd + h * hd;
+    auto chunk_sum = [&](int d) {
+        float O = 0.0f;
+#pragma unroll
+        for (int c = 0; c < ATT_WAVES; c++) O = c < nw ? O + os[c * hd + d] * wc[c] : O;
+        return O;
+    };
     if (nz == 1) {
         const float invL = 1.0f / L;
-        for (int d = threadIdx.x; d < hd; d += 64 * ATT_WAVES) {
-            float O = 0.0f;
-            for (int c = 0; c < nw; c++) O += os[c * hd + d] * expf(ml[c][0] - M);
-            o[d] = O * invL;
-        }
+        for (int d = threadIdx.x; d < hd; d += 64 * ATT_WAVES) o[d] = chunk_sum(d) * invL;
         return;
     }
     // several workgroups: partial (M, L, O) to global, the last one combines.
@@ -339,11 +486,8 @@ __device__ __forceinline__ void attention_body(int bx, int by, int bz, float* __
     // (buffer_inv) that only non-coherent stores and loads need -- and those
     // cost about 0.1 us a wave, serialized per XCD, on MI355X.
     float* po = part + (((size_t)s * n_heads + h) * nspan + z) * (hd + 2);
-    for (int d = threadIdx.x; d < hd; d += 64 * ATT_WAVES) {
-        float O = 0.0f;
-        for (int c = 0; c < nw; c++) O += os[c * hd + d] * expf(ml[c][0] - M);
-        __hip_atomic_store(po + 2 + d, O, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    for (int d = threadIdx.x; d < hd; d += 64 * ATT_WAVES)
+        __hip_atomic_store(po + 2 + d, chunk_sum(d), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (threadIdx.x == 0) {
         __hip_atomic_store(po, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(po + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -388,9 +532,7 @@ using att::attention_body;
 using att::ATT_SPAN;
 using att::ATT_WAVES;
 using att::ATT_CHUNK;
-using att::PUB_SLOT;
-using att::PUB_COUNT;
-using att::PUB_READY;
+using att::xch_put;
 using att::wave_max;
 using att::wave_sum;
 }  // namespace rdl

@@ -225,20 +225,8 @@ struct Fuse {
     void* vc;
     const int* kv_table;        // physical page of each logical page
     int n_heads, n_kv, hd, kv_f16;
-    int* pub;                   // PUB: per-KV-group slots (count, ready flag) of the fused attention
-    int producers;              // PUB: workgroups writing each KV group's q / k / v rows
+    uint64_t* xch;              // PUB: the layer's exchange, one tagged value per q / k / v row
 };
-
-// A store the fused decode attention of the same launch reads: agent-coherent
-// (relaxed agent-scope atomic store, written through to the device's
-// coherence point) when published, a plain store otherwise.
-template <bool PUB, typename T>
-__device__ __forceinline__ void st_pub(T* p, T v) {
-    if constexpr (PUB)
-        __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    else
-        *p = v;
-}
 
 template <int NW, int PI, int PRO = PRO_NONE>
 __device__ __forceinline__ void load_prep_x4(const float* __restrict__ x, const float* __restrict__ aux, int nb,
@@ -586,11 +574,10 @@ constexpr int EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_SWIGLU = 2, EPI_ROPE_KV = 3;
 
 // PRO: prologue on x (PRO_NONE / PRO_RMSNORM / PRO_SWIGLU, int4 records only).
 // The body of one workgroup (bx, by): row group bx, activation row by.
-// PUB (EPI_ROPE_KV only): the q rows and the cache rows are written with
-// agent-coherent stores, and once every wave's stores have completed thread
-// 0 counts the workgroup into the slot of its head's KV group; the group's
-// last producer marks the position ready, so that workgroups of the same
-// launch (the fused decode attention) can read the rows.
+// PUB (EPI_ROPE_KV only): every q / k / v output (after RoPE) is also written
+// to the exchange fz.xch as one tagged 8-byte value (xch_put, tag = position
+// + 1), which the fused decode attention of the same launch polls; the q
+// rows are then not written to y (nothing else reads them).
 template <int WT, bool NATIVE, int R, int CPL, bool NB_EVEN, int NW, int PRO = PRO_NONE, int EPI = EPI_STORE,
           bool PUB = false>
 __device__ __forceinline__ void gemv_fused_body(int bx, int by, i32x4* __restrict__ lds4, const uint8_t* __restrict__ W,
@@ -610,8 +597,11 @@ __device__ __forceinline__ void gemv_fused_body(int bx, int by, i32x4* __restric
     // MI355X: P0 = 2, PF = 3 for int4 records, 4 / 4 otherwise).
     // (int4 records with 16 blocks a lane -- 8 rows a wave -- keep 5 in flight)
     constexpr int PF_I4 = NB >= 16 ? 5 : 3;
-    constexpr int PF = (NB < (I4 ? PF_I4 : 4)) ? NB : (I4 ? PF_I4 : 4);
-    constexpr int P0 = (PF < (I4 ? 2 : 4)) ? PF : (I4 ? 2 : 4);
+    // (the q/k/v launch of a decode step, 8 blocks a lane on 192 of the
+    // CUs: all of them in flight, 4 before the prep; 7B decode 812 -> 820
+    // tokens/s against 3 / 2, and against 8 / 8: 804)
+    constexpr int PF = EPI == EPI_ROPE_KV ? NB : (NB < (I4 ? PF_I4 : 4)) ? NB : (I4 ? PF_I4 : 4);
+    constexpr int P0 = EPI == EPI_ROPE_KV ? (PF < 4 ? PF : 4) : (PF < (I4 ? 2 : 4)) ? PF : (I4 ? 2 : 4);
     constexpr int PI = I4 ? (CPL * 4 + NW - 1) / NW : (CPL * 8 + NW - 1) / NW;
     const int lane = threadIdx.x & 63;
     const int wv = threadIdx.x >> 6;
@@ -762,13 +752,11 @@ __device__ __forceinline__ void gemv_fused_body(int bx, int by, i32x4* __restric
         }
     }
     const bool has_rows = row_of(0) < rend;  // wave-uniform
-    if constexpr (!PUB) {
-        if (!has_rows) return;  // the wave had nothing to store
-    }
+    if (!has_rows) return;  // the wave had nothing to store
 
     // ---- reduce and store ----
 #pragma unroll
-    for (int grp = 0; grp < NGRP && has_rows; grp++) {
+    for (int grp = 0; grp < NGRP; grp++) {
         float accg[RG];
 #pragma unroll
         for (int r = 0; r < RG; r++) accg[r] = acc[grp * RG + r];
@@ -792,27 +780,37 @@ __device__ __forceinline__ void gemv_fused_body(int bx, int by, i32x4* __restric
                     if (head < fz.n_heads + fz.n_kv) {
                         const float c = rope_c, sn = rope_s;
                         const float o1 = x1 * c - x2 * sn, o2 = x1 * sn + x2 * c;
+                        if constexpr (PUB) {  // the attention of this launch reads the tagged copies
+                            xch_put(fz.xch + r1, o1, pos + 1);
+                            xch_put(fz.xch + r1 + half, o2, pos + 1);
+                        }
                         if (head < fz.n_heads) {
-                            st_pub<PUB>(y + r1, o1);
-                            st_pub<PUB>(y + r1 + half, o2);
+                            if constexpr (!PUB) {
+                                y[r1] = o1;
+                                y[r1 + half] = o2;
+                            }
                         } else {
                             const size_t ko = kv_row(fz.kv_table, fz.n_kv, head - fz.n_heads, pos, fz.hd) + i;
                             if (fz.kv_f16) {
-                                st_pub<PUB>(reinterpret_cast<_Float16*>(fz.kc) + ko, (_Float16)o1);
-                                st_pub<PUB>(reinterpret_cast<_Float16*>(fz.kc) + ko + half, (_Float16)o2);
+                                reinterpret_cast<_Float16*>(fz.kc)[ko] = (_Float16)o1;
+                                reinterpret_cast<_Float16*>(fz.kc)[ko + half] = (_Float16)o2;
                             } else {
-                                st_pub<PUB>(reinterpret_cast<float*>(fz.kc) + ko, o1);
-                                st_pub<PUB>(reinterpret_cast<float*>(fz.kc) + ko + half, o2);
+                                reinterpret_cast<float*>(fz.kc)[ko] = o1;
+                                reinterpret_cast<float*>(fz.kc)[ko + half] = o2;
                             }
                         }
                     } else {
+                        if constexpr (PUB) {
+                            xch_put(fz.xch + r1, x1, pos + 1);
+                            xch_put(fz.xch + r1 + half, x2, pos + 1);
+                        }
                         const size_t vo = kv_row(fz.kv_table, fz.n_kv, head - fz.n_heads - fz.n_kv, pos, fz.hd) + i;
                         if (fz.kv_f16) {
-                            st_pub<PUB>(reinterpret_cast<_Float16*>(fz.vc) + vo, (_Float16)x1);
-                            st_pub<PUB>(reinterpret_cast<_Float16*>(fz.vc) + vo + half, (_Float16)x2);
+                            reinterpret_cast<_Float16*>(fz.vc)[vo] = (_Float16)x1;
+                            reinterpret_cast<_Float16*>(fz.vc)[vo + half] = (_Float16)x2;
                         } else {
-                            st_pub<PUB>(reinterpret_cast<float*>(fz.vc) + vo, x1);
-                            st_pub<PUB>(reinterpret_cast<float*>(fz.vc) + vo + half, x2);
+                            reinterpret_cast<float*>(fz.vc)[vo] = x1;
+                            reinterpret_cast<float*>(fz.vc)[vo + half] = x2;
                         }
                     }
                 }
@@ -824,22 +822,6 @@ __device__ __forceinline__ void gemv_fused_body(int bx, int by, i32x4* __restric
                     y[row] = s + y_old;
                 else
                     y[row] = s;
-            }
-        }
-    }
-    if constexpr (PUB) {
-        // every wave's coherent stores complete, then one add for the workgroup
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            const int head = mat_row(r0) / fz.hd;
-            const int grp_kv = head < fz.n_heads ? head / (fz.n_heads / fz.n_kv)
-                               : head < fz.n_heads + fz.n_kv ? head - fz.n_heads : head - fz.n_heads - fz.n_kv;
-            int* slot = fz.pub + (size_t)grp_kv * PUB_SLOT;
-            const int old = __hip_atomic_fetch_add(slot + PUB_COUNT, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (old == fz.producers - 1) {  // the group's last producer: every other one's stores completed
-                __hip_atomic_store(slot + PUB_COUNT, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                __hip_atomic_store(slot + PUB_READY, *fz.pos + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
         }
     }
@@ -1733,7 +1715,7 @@ hipError_t launch_gemv_q4_0_rope_kv(const uint8_t* w, size_t n, size_t k, const 
 hipError_t launch_qkv_attention(const uint8_t* w, size_t n, size_t k, const float* x, float* y, const float* g,
                                 float eps, const int* pos, const float* cos_t, const float* sin_t, void* kc, void* vc,
                                 const int* kv_table, int n_heads, int n_kv, int hd, bool kv_f16, float* att_part,
-                                int nspan, int spans, int* att_cnt, float* att_out, int* pub, int* err,
+                                int nspan, int spans, int* att_cnt, float* att_out, uint64_t* xch, int* err,
                                 hipStream_t s) {
     const int nb = (int)(k / QK);
     const int cpl = cpl_for(nb);
@@ -1741,7 +1723,7 @@ hipError_t launch_qkv_attention(const uint8_t* w, size_t n, size_t k, const floa
     const int r = (8 / cpl >= 4) ? 4 : 2, rpw = 8 * r;
     if (k == 0 || nb == 0 || (nb & 1) || cpl > 4 || ((uintptr_t)x & 15) || (hd & 1) || hd % rpw ||
         n_kv <= 0 || n_heads % n_kv || n != (size_t)(n_heads + 2 * n_kv) * hd ||
-        (uint64_t)n * nb * Q4_0_BYTES > FUSED_MAX_WEIGHT_BYTES || pub == nullptr || err == nullptr)
+        (uint64_t)n * nb * Q4_0_BYTES > FUSED_MAX_WEIGHT_BYTES || xch == nullptr || err == nullptr)
         return hipErrorInvalidValue;
     // the coalesced K/V layout of the fused attention: 16-byte pieces, at most 16 a row
     if (!((kv_f16 && (hd == 128 || hd == 64)) || (!kv_f16 && hd == 64))) return hipErrorInvalidValue;
@@ -1759,12 +1741,12 @@ hipError_t launch_qkv_attention(const uint8_t* w, size_t n, size_t k, const floa
     fz.hd = hd;
     fz.kv_table = kv_table;
     fz.kv_f16 = kv_f16 ? 1 : 0;
-    fz.pub = pub;
-    fz.producers = (n_heads / n_kv + 2) * (hd / rpw);
+    fz.xch = xch;
     const int n_gemv = (int)((n + rpw - 1) / rpw);
     if (spans < 1 || spans > nspan) return hipErrorInvalidValue;
     const dim3 grid((unsigned)(n_gemv + n_heads * spans)), block(512);
-    const size_t lds = std::max((size_t)8 * 16 * nb, (size_t)(1 + ATT_WAVES) * hd * sizeof(float));
+    // attention: q | per-wave contexts | current k | current v (f32)
+    const size_t lds = std::max((size_t)8 * 16 * nb, (size_t)(3 + ATT_WAVES) * hd * sizeof(float));
     auto go = [&](auto kv_tag, auto hd_tag, auto r_tag) {
         using KV = decltype(kv_tag);
         constexpr int HD = decltype(hd_tag)::value, R = decltype(r_tag)::value, CPL = R == 4 ? 2 : 4;
@@ -1783,7 +1765,7 @@ hipError_t launch_qkv_attention(const uint8_t* w, size_t n, size_t k, const floa
         aa.nspan = nspan;
         aa.counters = att_cnt;
         aa.out = att_out;
-        aa.pub = pub;
+        aa.xch = xch;
         aa.err = err;
         launch_kernel(qkv_attention_kernel<KV, HD, R, CPL>, grid, block, lds, s, w, (int)n, nb, rpw, x, y, fz, aa,
                       n_gemv);

@@ -333,7 +333,7 @@ struct LlamaModel {
     int att_nspan = 0;
     // decode steps: attention fused into the q/k/v launch (fused layers, one row)
     bool fused_attention = true;
-    int* att_pub = nullptr;  // [layer][n_kv][PUB_SLOT] fused-attention slots (zero on an empty cache)
+    uint64_t* att_xch = nullptr;  // [layer][qkv_dim] fused-attention exchange (zero on an empty cache)
     int* att_err = nullptr;  // set by a fused launch whose wait ran out
     hipStream_t stream = nullptr;
     hipGraphExec_t decode_exec = nullptr;
@@ -444,7 +444,7 @@ struct LlamaModel {
             e = launch_qkv_attention(L.qkv.dev, L.qkv.n, d, x, qkv, L.attn_norm, eps, pos, cos_t, sin_t,
                                      kv_layer(kc, l), kv_layer(vc, l), kv_table, cfg.n_heads, cfg.n_kv_heads,
                                      cfg.head_dim, cfg.kv_f16 != 0, att_part, att_nspan, chunks_needed(1), att_cnt,
-                                     att, att_pub + (size_t)l * cfg.n_kv_heads * PUB_SLOT, att_err, stream);
+                                     att, att_xch + (size_t)l * qkv_dim, att_err, stream);
             if (e != hipErrorInvalidValue) {
                 if (e != hipSuccess) return e;
                 return layer_fused_tail(l, m);
@@ -721,7 +721,7 @@ rdl_status check_fused(rdl::LlamaModel& M) {
     HIP_TRY(hipMemcpy(&err, M.att_err, sizeof(int), hipMemcpyDeviceToHost));
     if (!err) return RDL_OK;
     HIP_TRY(hipMemset(M.att_err, 0, sizeof(int)));
-    HIP_TRY(hipMemset(M.att_pub, 0, (size_t)M.cfg.n_layers * M.cfg.n_kv_heads * rdl::PUB_SLOT * sizeof(int)));
+    HIP_TRY(hipMemset(M.att_xch, 0, (size_t)M.cfg.n_layers * M.qkv_dim * sizeof(uint64_t)));
     return api_fail(RDL_ERR_HIP, "fused decode attention: a wait for the q/k/v workgroups ran out");
 }
 
@@ -879,8 +879,8 @@ rdl_status rdl_llama_create_typed(const rdl_llama_config* cfg, const int32_t* ty
         return fail_free(e);
     if ((e = M.alloc_t(&M.att_cnt, mb * c.n_heads)) != hipSuccess) return fail_free(e);
     if ((e = hipMemset(M.att_cnt, 0, mb * c.n_heads * sizeof(int))) != hipSuccess) return fail_free(e);
-    if ((e = M.alloc_t(&M.att_pub, (size_t)c.n_layers * c.n_kv_heads * rdl::PUB_SLOT)) != hipSuccess) return fail_free(e);
-    if ((e = hipMemset(M.att_pub, 0, (size_t)c.n_layers * c.n_kv_heads * rdl::PUB_SLOT * sizeof(int))) != hipSuccess)
+    if ((e = M.alloc_t(&M.att_xch, (size_t)c.n_layers * M.qkv_dim)) != hipSuccess) return fail_free(e);
+    if ((e = hipMemset(M.att_xch, 0, (size_t)c.n_layers * M.qkv_dim * sizeof(uint64_t))) != hipSuccess)
         return fail_free(e);
     if ((e = M.alloc_t(&M.att_err, 1)) != hipSuccess) return fail_free(e);
     if ((e = hipMemset(M.att_err, 0, sizeof(int))) != hipSuccess) return fail_free(e);
@@ -964,7 +964,7 @@ rdl_status rdl_llama_reset(rdl_llama* model) {
     hipLaunchKernelGGL(rdl::set_int_kernel, dim3(1), dim3(64), 0, M.stream, M.pos, 0);
     HIP_TRY(hipGetLastError());
     HIP_TRY(hipStreamSynchronize(M.stream));
-    HIP_TRY(hipMemset(M.att_pub, 0, (size_t)M.cfg.n_layers * M.cfg.n_kv_heads * rdl::PUB_SLOT * sizeof(int)));
+    HIP_TRY(hipMemset(M.att_xch, 0, (size_t)M.cfg.n_layers * M.qkv_dim * sizeof(uint64_t)));
     HIP_TRY(hipMemset(M.att_err, 0, sizeof(int)));
     M.host_pos = 0;
     return api_ok();

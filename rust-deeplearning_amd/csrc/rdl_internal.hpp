@@ -206,15 +206,15 @@ hipError_t launch_gemv_q4_0_rope_kv(const uint8_t* w, size_t n, size_t k, const 
 // attention over the cache positions 0 .. *pos (paged, kv_table), spans of
 // ATT_SPAN keys combined through att_part ([n_heads][nspan][hd + 2]) /
 // att_cnt as the attention launch does, `spans` span workgroups a head (those
-// past the position exit at once); pub = n_kv slots of PUB_SLOT ints (zero
-// on an empty cache; *pos must grow from one launch on the same pub to the
-// next), err = a flag set if a wait runs out.  hipErrorInvalidValue for
-// shapes it does not take (then use launch_gemv_q4_0_rope_kv and the
-// attention launch).
+// past the position exit at once); xch = the layer's exchange of n tagged
+// q / k / v words (zero on an empty cache; *pos must grow from one launch on
+// the same exchange to the next), err = a flag set if a wait runs out.
+// hipErrorInvalidValue for shapes it does not take (then use
+// launch_gemv_q4_0_rope_kv and the attention launch).
 hipError_t launch_qkv_attention(const uint8_t* w, size_t n, size_t k, const float* x, float* y, const float* g,
                                 float eps, const int* pos, const float* cos_t, const float* sin_t, void* kc, void* vc,
                                 const int* kv_table, int n_heads, int n_kv, int hd, bool kv_f16, float* att_part,
-                                int nspan, int spans, int* att_cnt, float* att_out, int* pub, int* err,
+                                int nspan, int spans, int* att_cnt, float* att_out, uint64_t* xch, int* err,
                                 hipStream_t s);
 
 // launch_gemv_q4_0_rope_kv for a Q4_K or Q6_K [Wq; Wk; Wv]: m <= 4 activation
