@@ -170,7 +170,7 @@ size_t scratch_bytes(Path p, bool native, size_t m, size_t n, size_t k) {
 }
 
 // Run the product on `s`; `work` holds scratch_bytes(path) bytes of device
-// memory, `counters` gemm_counter_count(n) ints of the GEMM (zero between calls).
+// memory, `counters` gemm_counter_count(n, k) ints of the GEMM (zero between calls).
 rdl_status run_linear(WType t, bool native, const uint8_t* w_dev, size_t n, size_t k,
                       const float* x_dev, size_t m, float* y_dev, void* work, int* counters, hipStream_t s,
                       Path path) {
@@ -309,13 +309,13 @@ struct CallWork {
         if (cs != hipStreamCaptureStatusActive) {
             void* q = nullptr;
             int* c = nullptr;
-            rdl_status st = stream_work(s, bytes, want_counters ? rdl::gemm_counter_count(w->n) : 0, &q, &c);
+            rdl_status st = stream_work(s, bytes, want_counters ? rdl::gemm_counter_count(w->n, w->k) : 0, &q, &c);
             p = q;
             counters = want_counters ? c : nullptr;
             return st;
         }
         const size_t data = (bytes + 255) & ~(size_t)255;
-        const size_t nc = want_counters ? rdl::gemm_counter_count(w->n) : 0;
+        const size_t nc = want_counters ? rdl::gemm_counter_count(w->n, w->k) : 0;
         HIP_TRY(hipMallocAsync(&p, data + nc * sizeof(int) + 4, s));
         graph_owned = true;
         if (want_counters) {
@@ -348,8 +348,8 @@ rdl_status host_matmul(WType t, bool native, const float* x, size_t x_len, const
     const size_t sb = scratch_bytes(path, native, m, n, k);
     if (sb) HIP_TRY(dr.alloc(sb));
     DevBuf dc;
-    HIP_TRY(dc.alloc(rdl::gemm_counter_count(n) * sizeof(int)));
-    HIP_TRY(hipMemset(dc.p, 0, rdl::gemm_counter_count(n) * sizeof(int)));
+    HIP_TRY(dc.alloc(rdl::gemm_counter_count(n, k) * sizeof(int)));
+    HIP_TRY(hipMemset(dc.p, 0, rdl::gemm_counter_count(n, k) * sizeof(int)));
     st = run_linear(t, native, (const uint8_t*)dw.p, n, k, (const float*)dx.p, m, (float*)dy.p,
                     dr.p, (int*)dc.p, nullptr, path);
     if (st != RDL_OK) return st;
@@ -581,7 +581,7 @@ rdl_status rdl_linear_forward_dev_noalloc(const rdl_weight* w, const float* x_de
         return fail(RDL_ERR_UNSUPPORTED,
                     "m=%zu rows of in_features %zu need %zu scratch bytes; the static scratch holds %zu",
                     m, w->k, rb, NOALLOC_DATA_BYTES);
-    if (rdl::gemm_counter_count(w->n) * sizeof(int) > NOALLOC_COUNTER_BYTES)
+    if (rdl::gemm_counter_count(w->n, w->k) * sizeof(int) > NOALLOC_COUNTER_BYTES)
         return fail(RDL_ERR_UNSUPPORTED, "out_features %zu beyond the static scratch's GEMM counters", w->n);
     void* work = nullptr;
     rdl_status st = noalloc_scratch(&work);

@@ -32,6 +32,9 @@
 #include <algorithm>
 #include <type_traits>
 
+#include <mutex>
+#include <vector>
+
 #include "rdl_device.hpp"
 #include "rdl_internal.hpp"
 
@@ -482,6 +485,53 @@ __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_kernel(
     }
 }
 
+// ---- XCD placement ----------------------------------------------------------------------
+// MI355X deals the workgroups of a launch round-robin to its 8 XCDs (each
+// with its own L2): workgroup b runs on XCD b % 8.  The m <= 16 GEMM relies on
+// it to keep a strip's K-slices in one L2 (plain partial stores, read back
+// with non-temporal loads by the last slice); the probe below checks it once
+// per device (2 x CUs workgroups record their XCC id), and the kernel falls
+// back to agent-coherent stores and loads where it does not hold.
+__global__ void xcd_probe_kernel(int* __restrict__ out) {
+    unsigned x;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+    if (threadIdx.x == 0) out[blockIdx.x] = (int)(x & 0xF);
+}
+
+namespace {
+constexpr int XCD_COUNT = 8;
+std::mutex xcd_mu;
+int xcd_state[64] = {};  // per device: 0 unknown, 1 round-robin, 2 not
+}  // namespace
+
+// True when workgroup b of a launch runs on XCD b % 8 on the current device
+// (probed on a private stream the first time; never probed while `s` is
+// being captured into a graph, which then takes the coherent path).
+bool xcd_round_robin(hipStream_t s) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
+    std::lock_guard<std::mutex> lock(xcd_mu);
+    if (xcd_state[dev]) return xcd_state[dev] == 1;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (s && hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone) return false;
+    const int nwg = 2 * device_cu_count();
+    int* d = nullptr;
+    hipStream_t ps = nullptr;
+    bool ok = hipStreamCreateWithFlags(&ps, hipStreamNonBlocking) == hipSuccess &&
+              hipMalloc(&d, nwg * sizeof(int)) == hipSuccess;
+    std::vector<int> h(nwg, -1);
+    if (ok) {
+        hipLaunchKernelGGL(xcd_probe_kernel, dim3(nwg), dim3(64), 0, ps, d);
+        ok = hipGetLastError() == hipSuccess && hipStreamSynchronize(ps) == hipSuccess &&
+             hipMemcpy(h.data(), d, nwg * sizeof(int), hipMemcpyDeviceToHost) == hipSuccess;
+    }
+    for (int b = 0; ok && b < nwg; b++) ok = h[b] == b % XCD_COUNT;
+    if (d) (void)hipFree(d);
+    if (ps) (void)hipStreamDestroy(ps);
+    xcd_state[dev] = ok ? 1 : 2;
+    return ok;
+}
+
 // ---- skinny GEMM (m <= GEMM_SMALL_M) ----------------------------------------------
 // With few x rows, x is the costly operand: a workgroup that owns a strip of
 // W over the whole of K must read and split all of x, and the split alone
@@ -499,10 +549,13 @@ __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_kernel(
 //     MFMAs on the exact (q - 8) give the block dot, scaled by d 2^e in f32.
 //     Its weight loads for the next chunk are in flight meanwhile.
 // The WK waves of a row group are summed in wave order through LDS.  With
-// S > 1 each workgroup publishes its strip partial with agent-coherent stores,
-// waits for them to complete, and counts itself on the strip's counter; the
-// last of the S sums all S partials in slice order (the same bits whichever
-// workgroup finishes last) and resets the counter to 0 for the next launch.
+// S > 1 each workgroup publishes its strip partial, waits for the stores to
+// complete, and counts itself on the strip's counter; the last of the S sums
+// all S partials in slice order (the same bits whichever workgroup finishes
+// last) and resets the counter to 0 for the next launch.  Where the probed
+// placement holds (xcd_round_robin) a strip's slices share one XCD and the
+// partials stay in its L2 (plain stores, non-temporal loads); elsewhere
+// agent-coherent (sc1) stores and loads.
 constexpr int SK_WAVES = 8;
 
 template <int MT, int JT, int WR>
@@ -527,23 +580,14 @@ struct SkCfg {
     static_assert(KBW * WK == KCB, "chunk blocks split evenly over the waves");
 };
 
-// 16 bytes written to / read from the device's coherence point (two relaxed
-// agent-scope 64-bit atomics each), for data other workgroups of the launch read.
-__device__ __forceinline__ void st_coh16(float* p, f32x4 v) {
-    uint64_t* q = reinterpret_cast<uint64_t*>(p);
-    __hip_atomic_store(q, __builtin_bit_cast(uint64_t, float2{v[0], v[1]}), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(q + 1, __builtin_bit_cast(uint64_t, float2{v[2], v[3]}), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ f32x4 ld_coh16(const float* p) {
-    const uint64_t* q = reinterpret_cast<const uint64_t*>(p);
-    const float2 a = __builtin_bit_cast(float2, __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-    const float2 b = __builtin_bit_cast(float2, __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-    return f32x4{a.x, a.y, b.x, b.y};
-}
+// Cache policy bits of buffer loads / stores (gfx950): nt (non-temporal: no
+// stale L1 line), sc1 (device scope: written through / read from the
+// device's coherence point).
+constexpr int CPOL_NT = 2, CPOL_SC1 = 16;
 
 // EVEN: nb and the slice length even, so every chunk's first block starts on a
 // dword and a lane's weight words sit at fixed offsets from one base.
-template <int MT, int JT, int WR, bool EVEN>
+template <int MT, int JT, int WR, bool EVEN, bool LOCAL>
 __global__ __launch_bounds__(SK_WAVES * 64) void gemm_q4_0_skinny_kernel(
     const uint8_t* __restrict__ W, int n, int nb, const float* __restrict__ X, int m, float* __restrict__ Y, int S,
     int kbs, float* __restrict__ part, int* __restrict__ cnt) {
@@ -558,7 +602,17 @@ __global__ __launch_bounds__(SK_WAVES * 64) void gemm_q4_0_skinny_kernel(
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, r = lane & 15, h = g & 1;
     const int wr = wave / C::WK, wk = wave % C::WK;
-    const int strip = (int)blockIdx.x / S, ks = (int)blockIdx.x % S;
+    // LOCAL: strip st's slices on XCD st % 8 (one L2), as in the m <= 16 kernel
+    int strip, ks;
+    if constexpr (LOCAL) {
+        const int xcd = (int)blockIdx.x % XCD_COUNT, i = (int)blockIdx.x / XCD_COUNT;
+        strip = (i / S) * XCD_COUNT + xcd;
+        ks = i % S;
+    } else {
+        strip = (int)blockIdx.x / S;
+        ks = (int)blockIdx.x % S;
+    }
+    if (strip * C::R >= n) return;  // grid rounded up to whole XCD rounds (whole workgroup)
     const int j0 = strip * C::R;
     const int kb0 = min(nb, ks * kbs), kb1 = min(nb, kb0 + kbs);
     const int nchunks = (kb1 - kb0 + KCB - 1) / KCB;  // workgroup-uniform
@@ -755,11 +809,17 @@ __global__ __launch_bounds__(SK_WAVES * 64) void gemm_q4_0_skinny_kernel(
         own[p] = sum;
     }
     if (S > 1) {
-        float* pp = part + ((size_t)strip * S + ks) * C::UNITS * 4;
+        // the strip's partials: LOCAL into this XCD's L2 (plain stores), else
+        // written through to the device's coherence point (sc1)
+        const __amdgpu_buffer_rsrc_t prs = make_rsrc(part + (size_t)strip * S * C::UNITS * 4,
+                                                     (uint32_t)S * C::UNITS * 16u);
 #pragma unroll
         for (int p = 0; p < C::UPT; p++) {
             const int u = tid + p * C::NT;
-            if (u < C::UNITS) st_coh16(pp + (size_t)u * 4, own[p]);
+            if (u < C::UNITS)
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, own[p]), prs,
+                                                       (int)(((uint32_t)ks * C::UNITS + u) * 16u), 0,
+                                                       LOCAL ? 0 : CPOL_SC1);
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partials have completed
         __syncthreads();
@@ -770,14 +830,30 @@ __global__ __launch_bounds__(SK_WAVES * 64) void gemm_q4_0_skinny_kernel(
         }
         __syncthreads();
         if (!last_sh) return;
-        const float* pb = part + (size_t)strip * S * C::UNITS * 4;
 #pragma unroll
         for (int p = 0; p < C::UPT; p++) {
             const int u = tid + p * C::NT;
             if (u >= C::UNITS) break;
-            f32x4 sum = ks == 0 ? own[p] : ld_coh16(pb + (size_t)u * 4);
-            for (int s2 = 1; s2 < S; s2++)
-                sum += s2 == ks ? own[p] : ld_coh16(pb + ((size_t)s2 * C::UNITS + u) * 4);
+            // every slice's partial in flight together (groups of 8, branch-free:
+            // slots past S or of this slice read zeros), then added in slice
+            // order; LOCAL reads the L2 with non-temporal loads, else sc1
+            f32x4 sum = {0.0f, 0.0f, 0.0f, 0.0f};
+            for (int s0 = 0; s0 < S; s0 += 8) {
+                f32x4 v[8];
+#pragma unroll
+                for (int q = 0; q < 8; q++) {
+                    const int sl = s0 + q;
+                    const uint32_t off = (sl < S && sl != ks) ? ((uint32_t)sl * C::UNITS + u) * 16u : RSRC_OOB;
+                    v[q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(prs, (int)off, 0,
+                                                                                            LOCAL ? CPOL_NT : CPOL_SC1));
+                }
+#pragma unroll
+                for (int q = 0; q < 8; q++) {
+                    const int sl = s0 + q;
+                    const f32x4 t = sl == ks ? own[p] : v[q];
+                    if (sl < S) sum = sl == 0 ? t : sum + t;
+                }
+            }
             own[p] = sum;
         }
     }
@@ -798,6 +874,297 @@ __global__ __launch_bounds__(SK_WAVES * 64) void gemm_q4_0_skinny_kernel(
                 if (j + c < n) yp[c] = own[p][c];
         }
     }
+}
+
+// ---- skinny GEMM for m <= 16: K-slices joined through tagged partials --------------
+// One 16-row x tile.  A workgroup of 8 waves owns 128 weight rows (a 16-row
+// tile a wave) over one K-slice of at most KB blocks; the grid is ceil(n /
+// 128) strips x S slices, S chosen for about one workgroup per CU, so each x
+// element is split by n / 128 workgroups and a workgroup streams 128 rows x
+// KB blocks of W against 16 x KB blocks of x (n = k = 4096: 36 KB of W and
+// 32 KB of x).  Per workgroup:
+//  1. every load at once: the wave's weight windows (one 12-byte window a
+//     lane and block, the B operand of the MFMA) and the x tile (8-element
+//     pieces, coalesced);
+//  2. x split into LDS as in the skinny kernel above (per (row, block) scale
+//     2^e, x_hi + x_lo in f16);
+//  3. per block two v_mfma_f32_16x16x32_f16 with x as the A operand, so the
+//     lane's output column is its own weight row and its block scale d is in
+//     its own window (or its partner's, l ^ 16, through a permlane swap);
+//     acc += d * 2^e * dot in f32 (4 x rows a lane);
+//  4. the S slices of a strip meet through a counter: each writes its 16 x
+//     128 partial, waits for the stores, counts itself on the strip's counter,
+//     and the last of the S adds all partials in slice order (the same bits
+//     whichever finishes last), resets the counter and stores Y.  Where the
+//     workgroup placement is the probed round-robin (xcd_round_robin), a
+//     strip's slices are put on one XCD and the partials stay in its L2:
+//     plain 16-byte stores (acknowledged by the L2), read back with
+//     non-temporal loads, which do not return a stale L1 line; measured at M =
+//     16, the partial stores and their reads took 2.4 + 3.7 us as agent-coherent
+//     (write-through) traffic.  Elsewhere agent-coherent stores and loads.
+constexpr int SK16_WAVES = 8;
+constexpr int SK16_ROWS = 16 * SK16_WAVES;  // weight rows per workgroup
+constexpr int SK16_UNITS = SK16_WAVES * 64;  // f32x4 partial units per workgroup (16 x rows x 128 weight rows)
+
+template <int KB>
+struct Sk16Cfg {
+    static constexpr int NT = SK16_WAVES * 64;
+    static constexpr int XROW = KB * 64 + 16;          // LDS bytes per x row of f16 (padded)
+    static constexpr int X_BYTES = 16 * XROW;
+    static constexpr int SC_BYTES = KB * 16 * 4;       // block scales [block][x row]
+    static constexpr int LDS = 2 * X_BYTES + SC_BYTES;
+    static constexpr int XU = (16 * KB * 4 + NT - 1) / NT;  // 8-element x pieces per thread
+    static_assert(XU <= 4, "x pieces held in registers");
+};
+
+// EVEN: nb and the slice length even, so every slice's first block starts on a
+// dword and a lane's weight windows sit at fixed offsets from one base.
+template <int KB, bool EVEN, bool LOCAL>
+__global__ __launch_bounds__(SK16_WAVES * 64) void gemm_q4_0_sk16_kernel(
+    const uint8_t* __restrict__ W, int n, int nb, const float* __restrict__ X, int m, float* __restrict__ Y, int S,
+    int kbs, float* __restrict__ part, int* __restrict__ cnt) {
+    using C = Sk16Cfg<KB>;
+    __shared__ int last_sh;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    uint8_t* xh_s = lds;
+    uint8_t* xl_s = lds + C::X_BYTES;
+    float* sc_s = reinterpret_cast<float*>(lds + 2 * C::X_BYTES);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, r = lane & 15, h = g & 1;
+    // local: strip st's slices run on XCD st % 8 (workgroup b on XCD b % 8,
+    // probed), so they share one L2; otherwise strips are consecutive slices
+    int strip, ks;
+    if constexpr (LOCAL) {
+        const int xcd = (int)blockIdx.x % XCD_COUNT, i = (int)blockIdx.x / XCD_COUNT;
+        strip = (i / S) * XCD_COUNT + xcd;
+        ks = i % S;
+    } else {
+        strip = (int)blockIdx.x / S;
+        ks = (int)blockIdx.x % S;
+    }
+    if (strip * SK16_ROWS >= n) return;  // grid rounded up to whole XCD rounds (whole workgroup)
+    const int kb0 = min(nb, ks * kbs), kb1 = min(nb, kb0 + kbs);
+    const uint32_t k = (uint32_t)nb * 32u;
+    const uint32_t row_bytes = (uint32_t)nb * 18u;
+    const uint32_t wbytes = (uint32_t)n * row_bytes;
+    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(W, wbytes);
+    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(X, (uint32_t)m * k * 4u);
+    const int j = strip * SK16_ROWS + wave * 16 + r;  // the lane's weight row (output column)
+
+    // 1. loads: x pieces first, then the weight windows
+    u32x4 xa[C::XU], xb[C::XU];
+#pragma unroll
+    for (int u = 0; u < C::XU; u++) {
+        const int idx = tid + u * C::NT;
+        const int row = idx / (KB * 4), blk = (idx >> 2) % KB, qt = idx & 3;
+        const int b = kb0 + blk;
+        const uint32_t off = (idx < 16 * KB * 4 && row < m && b < kb1)
+                                 ? ((uint32_t)row * k + (uint32_t)b * 32u + (uint32_t)qt * 8u) * 4u
+                                 : RSRC_OOB;
+        xa[u] = buf_load_b128(xrs, off);
+        xb[u] = buf_load_b128(xrs, off == RSRC_OOB ? RSRC_OOB : off + 16u);
+    }
+    uint32_t wv[KB][3];
+    if constexpr (EVEN) {
+        // block kb0 + q of row j starts at j row_bytes + 18 kb0 + 18 q, on a
+        // dword for even q and 2 bytes past one for odd q; rows >= n fall
+        // past the buffer (zeros), blocks past the slice get d = 0 below
+        const uint32_t base = (uint32_t)j * row_bytes + (uint32_t)kb0 * 18u + 8u * (uint32_t)h;
+#pragma unroll
+        for (int q = 0; q < KB; q++) {
+            const auto v = __builtin_amdgcn_raw_buffer_load_b96(wrs, (int)(j < n ? base + 18u * q - 2u * (q & 1) : RSRC_OOB), 0, 0);
+            wv[q][0] = v[0], wv[q][1] = v[1], wv[q][2] = v[2];
+        }
+    } else {
+#pragma unroll
+        for (int q = 0; q < KB; q++) {
+            const int b = kb0 + q;
+            const uint32_t boff = (uint32_t)j * row_bytes + (uint32_t)b * 18u;
+            const uint32_t a = (j < n && b < kb1) ? ((boff + 8u * h) & ~3u) : RSRC_OOB;
+            const auto v = __builtin_amdgcn_raw_buffer_load_b96(wrs, (int)a, 0, 0);
+            wv[q][0] = v[0], wv[q][1] = v[1], wv[q][2] = v[2];
+            // the matrix's last block when it ends 2 bytes into a dword
+            if (a < wbytes && a + 12u > wbytes) wv[q][2] = buf_load_b16(wrs, a + 8u);
+        }
+    }
+
+    // 2. x split into LDS (x_hi = f16(x 2^-e) toward zero, x_lo = f16(rest))
+#pragma unroll
+    for (int u = 0; u < C::XU; u++) {
+        const int idx = tid + u * C::NT;
+        const int row = idx / (KB * 4), blk = (idx >> 2) % KB, qt = idx & 3;
+        float xv[8];
+        uint32_t amax = 0;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const uint32_t bits = e < 4 ? xa[u][e] : xb[u][e - 4];
+            xv[e] = __builtin_bit_cast(float, bits);
+            amax = max(amax, bits & 0x7FFFFFFFu);
+        }
+        amax = max(amax, (uint32_t)dpp_i32<DPP_QUAD_XOR1>((int)amax));  // the four lanes of a block
+        amax = max(amax, (uint32_t)dpp_i32<DPP_QUAD_XOR2>((int)amax));
+        int ex = 0;
+        if (amax != 0 && amax < 0x7F800000u)
+            ex = (amax >= 0x00800000u ? (int)(amax >> 23) - 127 : (31 - (int)__builtin_clz(amax)) - 149) - 14;
+        const bool fin = amax < 0x7F800000u;  // an infinite x keeps x_lo = 0 (no inf - inf)
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+        uint32_t hw[4], lw[4];
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+            const float a = ldexpf(xv[e], -ex), b = ldexpf(xv[e + 1], -ex);
+            const h2 hp = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(a, b));
+            const h2 lp = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(a - (float)hp[0], b - (float)hp[1]));
+            hw[e / 2] = __builtin_bit_cast(uint32_t, hp);
+            lw[e / 2] = fin ? __builtin_bit_cast(uint32_t, lp) : 0u;
+        }
+        if (idx < 16 * KB * 4) {
+            *reinterpret_cast<u32x4*>(xh_s + row * C::XROW + blk * 64 + qt * 16) = u32x4{hw[0], hw[1], hw[2], hw[3]};
+            *reinterpret_cast<u32x4*>(xl_s + row * C::XROW + blk * 64 + qt * 16) = u32x4{lw[0], lw[1], lw[2], lw[3]};
+            if (qt == 0) sc_s[blk * 16 + row] = ldexpf(1.0f, ex);
+        }
+    }
+    __syncthreads();
+
+    // 3. products: lane (g, r) holds Y[x rows 4g .. 4g + 3][weight row j]
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int q = 0; q < KB; q++) {
+        const int b = kb0 + q;
+        const bool odd = EVEN ? (q & 1) != 0 : (((uint32_t)j * row_bytes + (uint32_t)b * 18u) & 2u) != 0;
+        const uint32_t lo = odd ? wv[q][1] : perm(wv[q][1], wv[q][0], 0x05040302u);
+        const uint32_t hi = odd ? wv[q][2] : perm(wv[q][2], wv[q][1], 0x05040302u);
+        const uint32_t sh = (uint32_t)(g >> 1) * 4u;
+        const half8_t bq = q_f16((lo >> sh) & 0x0F0F0F0Fu, (hi >> sh) & 0x0F0F0F0Fu);
+        // d: in the window of the lanes with h == 0; lanes with h == 1 take
+        // their partner's (l ^ 16) through a permlane swap
+        const uint32_t dbits = odd ? wv[q][0] >> 16 : wv[q][0] & 0xFFFFu;
+        const auto sw = __builtin_amdgcn_permlane16_swap(dbits, dbits, false, false);
+        const uint32_t other = (sw[0] == dbits) ? sw[1] : sw[0];
+        const uint32_t dsel = h ? other : dbits;
+        const float d = (b < kb1) ? h2f(dsel) : 0.0f;
+        const int xo = r * C::XROW + q * 64 + g * 16;
+        const half8_t ah = *reinterpret_cast<const half8_t*>(xh_s + xo);
+        const half8_t al = *reinterpret_cast<const half8_t*>(xl_s + xo);
+        const f32x4 s4 = *reinterpret_cast<const f32x4*>(sc_s + q * 16 + 4 * g);
+        const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+        f32x4 cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bq, z, 0, 0, 0);
+        cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bq, cc, 0, 0, 0);
+#pragma unroll
+        for (int u = 0; u < 4; u++) acc[u] = fmaf(d * s4[u], cc[u], acc[u]);
+    }
+
+    // 4. slices of the strip: partials, counter, the last one adds them
+    if (S > 1) {
+        // the strip's partials: LOCAL into this XCD's L2 (plain stores), else
+        // written through to the device's coherence point (sc1)
+        const __amdgpu_buffer_rsrc_t prs = make_rsrc(part + (size_t)strip * S * SK16_UNITS * 4,
+                                                     (uint32_t)S * SK16_UNITS * 16u);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc), prs,
+                                               (int)(((uint32_t)ks * SK16_UNITS + tid) * 16u), 0,
+                                               LOCAL ? 0 : CPOL_SC1);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partial has completed
+        __syncthreads();
+        if (tid == 0) {
+            const int old = __hip_atomic_fetch_add(cnt + strip, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            last_sh = old == S - 1;
+            if (old == S - 1) __hip_atomic_store(cnt + strip, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        if (!last_sh) return;
+        // every slice's partial in flight together (groups of 8, branch-free:
+        // slots past S or of this slice read zeros), then added in slice order;
+        // LOCAL reads the L2 with non-temporal loads (no stale L1 line), else sc1
+        f32x4 tot = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int s0 = 0; s0 < S; s0 += 8) {
+            f32x4 v[8];
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                const int sl = s0 + q;
+                const uint32_t off = (sl < S && sl != ks) ? ((uint32_t)sl * SK16_UNITS + tid) * 16u : RSRC_OOB;
+                v[q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(prs, (int)off, 0,
+                                                                                        LOCAL ? CPOL_NT : CPOL_SC1));
+            }
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                const int sl = s0 + q;
+                const f32x4 t = sl == ks ? acc : v[q];
+                if (sl < S) tot = sl == 0 ? t : tot + t;
+            }
+        }
+        acc = tot;
+    }
+    if (j < n) {
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int i = 4 * g + u;
+            if (i < m) Y[(size_t)i * n + j] = acc[u];
+        }
+    }
+}
+
+// Launch plan of the m <= 16 kernel: 128-row strips, S K-slices of kbs
+// blocks (even when nb is) for about one workgroup per CU, KB the template
+// bound of kbs (8, 16 or 32).  ok = false (the other kernel runs) when a
+// slice would exceed 32 blocks.
+struct Sk16Plan {
+    int strips, S, kbs, KB;
+    bool even, ok;
+};
+inline Sk16Plan sk16_plan(size_t n, int nb) {
+    Sk16Plan p{};
+    p.strips = (int)((n + SK16_ROWS - 1) / SK16_ROWS);
+    const int S = std::max(1, (device_cu_count() + p.strips / 2) / p.strips);
+    p.kbs = std::max(1, (nb + S - 1) / S);
+    p.kbs = std::min(p.kbs, 32);
+    p.even = nb % 2 == 0;
+    if (p.even) p.kbs += p.kbs & 1;
+    p.S = std::max(1, (nb + p.kbs - 1) / p.kbs);  // no empty slices
+    p.KB = p.kbs <= 8 ? 8 : p.kbs <= 16 ? 16 : 32;
+    p.ok = p.kbs <= 32;
+    return p;
+}
+
+template <int KB, bool EVEN, bool LOCAL>
+hipError_t launch_sk16_cfg(const uint8_t* w, int n, int nb, const float* x, int m, float* y, const Sk16Plan& p,
+                           float* part, int* cnt, hipStream_t s) {
+    using C = Sk16Cfg<KB>;
+    static_assert(C::LDS <= 160 * 1024, "LDS per workgroup");
+    auto kern = gemm_q4_0_sk16_kernel<KB, EVEN, LOCAL>;
+    if (C::LDS > 65536) {
+        static const hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                        C::LDS);  // once per kernel and process
+        if (e != hipSuccess) return e;
+    }
+    const int strips = LOCAL ? (p.strips + XCD_COUNT - 1) / XCD_COUNT * XCD_COUNT : p.strips;
+    launch_kernel(kern, dim3((unsigned)(strips * p.S)), dim3(C::NT), (size_t)C::LDS, s, w, n, nb, x, m, y, p.S,
+                  p.kbs, part, cnt);
+    return hipGetLastError();
+}
+
+hipError_t launch_sk16(const uint8_t* w, int n, int nb, const float* x, int m, float* y, float* part, int* cnt,
+                       hipStream_t s) {
+    Sk16Plan p = sk16_plan((size_t)n, nb);
+    if (!part || !cnt) {  // no partial buffer or counters: one slice
+        p.S = 1;
+        p.kbs = nb;
+        p.KB = nb <= 8 ? 8 : nb <= 16 ? 16 : 32;
+        p.ok = nb <= 32;
+    }
+    if (!p.ok) return hipErrorInvalidValue;  // the caller takes the other kernel
+    const bool local = p.S > 1 && xcd_round_robin(s);
+    auto go = [&](auto kb_tag, auto even_tag) {
+        constexpr int KB = decltype(kb_tag)::value;
+        constexpr bool EVEN = decltype(even_tag)::value;
+        return local ? launch_sk16_cfg<KB, EVEN, true>(w, n, nb, x, m, y, p, part, cnt, s)
+                     : launch_sk16_cfg<KB, EVEN, false>(w, n, nb, x, m, y, p, part, cnt, s);
+    };
+    using T = std::true_type;
+    using F = std::false_type;
+    using K8 = std::integral_constant<int, 8>;
+    using K16 = std::integral_constant<int, 16>;
+    using K32 = std::integral_constant<int, 32>;
+    if (p.even) return p.KB == 8 ? go(K8{}, T{}) : p.KB == 16 ? go(K16{}, T{}) : go(K32{}, T{});
+    return p.KB == 8 ? go(K8{}, F{}) : p.KB == 16 ? go(K16{}, F{}) : go(K32{}, F{});
 }
 
 // Launch plan of the skinny GEMM for (m, n, nb): the template shape by m, the
@@ -824,18 +1191,19 @@ inline SkPlan skinny_plan(size_t m, size_t n, int nb, bool can_split) {
     return p;
 }
 
-template <int MT, int JT, int WR, bool EVEN>
+template <int MT, int JT, int WR, bool EVEN, bool LOCAL>
 hipError_t launch_skinny_cfg(const uint8_t* w, int n, int nb, const float* x, int m, float* y, const SkPlan& p,
                              float* part, int* cnt, hipStream_t s) {
     using C = SkCfg<MT, JT, WR>;
     static_assert(C::LDS <= 160 * 1024, "LDS per workgroup");
-    auto kern = gemm_q4_0_skinny_kernel<MT, JT, WR, EVEN>;
+    auto kern = gemm_q4_0_skinny_kernel<MT, JT, WR, EVEN, LOCAL>;
     if (C::LDS > 65536) {
         static const hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                                         C::LDS);  // once per kernel and process
         if (e != hipSuccess) return e;
     }
-    launch_kernel(kern, dim3((unsigned)(p.strips * p.S)), dim3(C::NT), (size_t)C::LDS, s, w, n, nb, x, m, y, p.S,
+    const int strips = LOCAL ? (p.strips + XCD_COUNT - 1) / XCD_COUNT * XCD_COUNT : p.strips;
+    launch_kernel(kern, dim3((unsigned)(strips * p.S)), dim3(C::NT), (size_t)C::LDS, s, w, n, nb, x, m, y, p.S,
                   p.kbs, part, cnt);
     return hipGetLastError();
 }
@@ -843,20 +1211,22 @@ hipError_t launch_skinny_cfg(const uint8_t* w, int n, int nb, const float* x, in
 hipError_t launch_skinny(const uint8_t* w, int n, int nb, const float* x, int m, float* y, float* part, int* cnt,
                          hipStream_t s) {
     const SkPlan p = skinny_plan((size_t)m, (size_t)n, nb, part != nullptr && cnt != nullptr);
-    if (p.even) {
-        switch (p.mt) {
-            case 1: return launch_skinny_cfg<1, 4, 1, true>(w, n, nb, x, m, y, p, part, cnt, s);
-            case 2: return launch_skinny_cfg<2, 4, 1, true>(w, n, nb, x, m, y, p, part, cnt, s);
-            case 3: return launch_skinny_cfg<3, 4, 2, true>(w, n, nb, x, m, y, p, part, cnt, s);
-            default: return launch_skinny_cfg<4, 4, 2, true>(w, n, nb, x, m, y, p, part, cnt, s);
-        }
-    }
-    switch (p.mt) {
-        case 1: return launch_skinny_cfg<1, 4, 1, false>(w, n, nb, x, m, y, p, part, cnt, s);
-        case 2: return launch_skinny_cfg<2, 4, 1, false>(w, n, nb, x, m, y, p, part, cnt, s);
-        case 3: return launch_skinny_cfg<3, 4, 2, false>(w, n, nb, x, m, y, p, part, cnt, s);
-        default: return launch_skinny_cfg<4, 4, 2, false>(w, n, nb, x, m, y, p, part, cnt, s);
-    }
+    const bool local = p.S > 1 && xcd_round_robin(s);
+    auto go = [&](auto mt_tag, auto even_tag) {
+        constexpr int MT = decltype(mt_tag)::value;
+        constexpr bool EVEN = decltype(even_tag)::value;
+        constexpr int WR = MT >= 3 ? 2 : 1;
+        return local ? launch_skinny_cfg<MT, 4, WR, EVEN, true>(w, n, nb, x, m, y, p, part, cnt, s)
+                     : launch_skinny_cfg<MT, 4, WR, EVEN, false>(w, n, nb, x, m, y, p, part, cnt, s);
+    };
+    using M1 = std::integral_constant<int, 1>;
+    using M2 = std::integral_constant<int, 2>;
+    using M3 = std::integral_constant<int, 3>;
+    using M4 = std::integral_constant<int, 4>;
+    using T = std::true_type;
+    using F = std::false_type;
+    if (p.even) return p.mt == 1 ? go(M1{}, T{}) : p.mt == 2 ? go(M2{}, T{}) : p.mt == 3 ? go(M3{}, T{}) : go(M4{}, T{});
+    return p.mt == 1 ? go(M1{}, F{}) : p.mt == 2 ? go(M2{}, F{}) : p.mt == 3 ? go(M3{}, F{}) : go(M4{}, F{});
 }
 
 template <bool NATIVE, bool DUMP, int FJ, int FI, int WJ, int WI, int KS, int KB>
@@ -910,7 +1280,13 @@ hipError_t launch_zero_counters(int* counters, size_t count, hipStream_t s) {
     return hipGetLastError();
 }
 
+size_t gemm_counter_count(size_t n, size_t) { return (n + 63) / 64 + 1; }  // a counter per strip of 64 (or 128) rows
+
 size_t gemm_scratch_bytes(size_t m, size_t n, size_t k, bool native) {
+    if (!native && m <= GEMM_SK16_M) {  // the K-slice partials of the m <= 16 kernel
+        const Sk16Plan p = sk16_plan(n, (int)(k / QK));
+        if (p.ok) return p.S > 1 ? ((size_t)p.strips * p.S * SK16_UNITS * 16 + 255) & ~(size_t)255 : 0;
+    }
     if (!native && m <= GEMM_SMALL_M) {  // the K-slice partials of the skinny GEMM
         if (m == 0 || n == 0) return 0;
         const SkPlan p = skinny_plan(m, n, (int)(k / QK), true);
@@ -926,6 +1302,11 @@ size_t gemm_scratch_bytes(size_t m, size_t n, size_t k, bool native) {
 hipError_t launch_gemm_q4_0(const uint8_t* w, size_t n, size_t k, const float* x, size_t m, float* y,
                             void* scratch, int* counters, hipStream_t s) {
     if (n == 0 || m == 0) return hipSuccess;
+    if (m <= GEMM_SK16_M) {
+        float* part = reinterpret_cast<float*>(scratch);  // the K-slice partials
+        const hipError_t e = launch_sk16(w, (int)n, (int)(k / QK), x, (int)m, y, part, counters, s);
+        if (e != hipErrorInvalidValue) return e;
+    }
     if (m <= GEMM_SMALL_M) {
         float* part = reinterpret_cast<float*>(scratch);  // the K-slice partials
         return launch_skinny(w, (int)n, (int)(k / QK), x, (int)m, y, part, counters, s);

@@ -327,7 +327,7 @@ struct LlamaModel {
     int *tokens = nullptr, *pos = nullptr, *step = nullptr, *out_tokens = nullptr;
     size_t out_cap = 0;
     void* gemm_scratch = nullptr;
-    int* gemm_cnt = nullptr;  // the skinny GEMM's strip counters (zero between launches)
+    int* gemm_cnt = nullptr;  // the skinny GEMMs' strip counters (zero between launches)
     float* att_part = nullptr;  // [max_batch][n_heads][spans of max_seq][hd + 2]
     int* att_cnt = nullptr;     // [max_batch][n_heads] finished-chunk counters (zero between launches)
     int att_nspan = 0;
@@ -855,15 +855,17 @@ rdl_status rdl_llama_create_typed(const rdl_llama_config* cfg, const int32_t* ty
                                 {2 * (size_t)c.ffn_dim, (size_t)c.dim}, {(size_t)c.dim, (size_t)c.ffn_dim},
                                 {(size_t)M.q_dim, (size_t)c.dim}, {(size_t)c.n_kv_heads * c.head_dim, (size_t)c.dim},
                                 {(size_t)c.ffn_dim, (size_t)c.dim}};
+    size_t gcc = 1;  // GEMM counters: the most any shape needs
     for (const auto& sh : shapes) {
         nmax = std::max(nmax, sh[0]);
+        gcc = std::max(gcc, rdl::gemm_counter_count(sh[0], sh[1]));
         // every skinny shape (it depends on ceil(m / 16)) and the largest chunk
-        for (size_t mm : {(size_t)16, (size_t)32, (size_t)48, (size_t)64, mb})
+        for (size_t mm : {(size_t)1, (size_t)16, (size_t)32, (size_t)48, (size_t)64, mb})
             gsb = std::max(gsb, rdl::gemm_scratch_bytes(std::min(mm, mb), sh[0], sh[1], false));
     }
     if ((e = M.alloc(&M.gemm_scratch, gsb)) != hipSuccess) return fail_free(e);
-    if ((e = M.alloc_t(&M.gemm_cnt, rdl::gemm_counter_count(nmax))) != hipSuccess) return fail_free(e);
-    if ((e = hipMemset(M.gemm_cnt, 0, rdl::gemm_counter_count(nmax) * sizeof(int))) != hipSuccess)
+    if ((e = M.alloc_t(&M.gemm_cnt, gcc)) != hipSuccess) return fail_free(e);
+    if ((e = hipMemset(M.gemm_cnt, 0, gcc * sizeof(int))) != hipSuccess)
         return fail_free(e);
     if (any_split_qkv && (e = M.alloc_t(&M.part_tmp, mb * M.qkv_dim)) != hipSuccess) return fail_free(e);
     // (row-pair epilogues need at most 4 columns per lane: dim <= 8192)

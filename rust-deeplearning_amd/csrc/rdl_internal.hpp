@@ -156,15 +156,17 @@ int device_cu_count();
 // Float mode (matmul_f32_q4): `scratch` holds gemm_scratch_bytes(m, n, k,
 // false) bytes (the f16 x split; for m <= GEMM_SMALL_M the skinny kernel's
 // K-slice partials, none when it runs unsplit) and `counters` points to
-// gemm_counter_count(n) ints that are zero before the first call and that
+// gemm_counter_count(n, k) ints that are zero before the first call and that
 // every call leaves at zero (memory no other code writes; NULL runs the
-// skinny kernel unsplit).  Native mode (matmul_f32_q4_native): x quantized
+// skinny kernels unsplit).  Native mode (matmul_f32_q4_native): x quantized
 // to Q8_0 codes, int8 MFMA block dots; gemm_scratch_bytes(m, n, k, true)
 // bytes of scratch; partials != NULL writes the int32 block dots to
 // partials[(i * n + j) * (k / 32) + b] instead of y.
 constexpr size_t GEMM_SMALL_M = 64;
+constexpr size_t GEMM_SK16_M = 16;  // float products of at most this many rows: one x tile, 128-row strips
 size_t gemm_scratch_bytes(size_t m, size_t n, size_t k, bool native);
-inline size_t gemm_counter_count(size_t n) { return (n + 63) / 64 + 1; }
+// ints of the GEMM's strip counters for out_features n, in_features k
+size_t gemm_counter_count(size_t n, size_t k);
 // Zeroes `count` GEMM counters with a kernel (no memset node under graph capture).
 hipError_t launch_zero_counters(int* counters, size_t count, hipStream_t s);
 hipError_t launch_gemm_q4_0(const uint8_t* w, size_t n, size_t k, const float* x, size_t m, float* y,

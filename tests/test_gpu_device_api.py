@@ -153,6 +153,33 @@ def test_skinny_gemm_calls_on_one_handle(rq, gpu):
         assert np.array_equal(yt.cpu().numpy(), want.reshape(-1)), f"m={m}"
 
 
+def test_sliced_gemm_shapes_share_the_stream_work_memory(rq, gpu):
+    """Products of at most 16 rows (128-row strips, K-slices joined through
+    partials and a counter per strip in the stream's work memory): three
+    weights of different layouts alternate on one stream, and every result
+    equals the synchronous entry point's (fresh work memory) bit for bit --
+    each launch leaves the shared counters at zero for the next, whatever its
+    shape."""
+    import torch
+
+    shapes = [(4096, 4096, 160), (1000, 2048, 161), (6144, 4096, 162)]
+    hs = []
+    for n, k, seed in shapes:
+        w = synth.q4_0_weights(n, k, seed)
+        _, h = dev_weight(rq, torch, w, 2, n, k)
+        hs.append((n, k, w, h))
+    s = torch.cuda.current_stream().cuda_stream
+    for rep, (i, m) in enumerate([(0, 16), (1, 9), (2, 16), (0, 3 + 2), (1, 16), (2, 11), (0, 16)]):
+        n, k, w, h = hs[i]
+        x = synth.activations(m, k, 170 + rep)
+        xt = torch.from_numpy(x.reshape(-1)).cuda()
+        yt = torch.empty(m * n, dtype=torch.float32, device="cuda")
+        h.forward_dev(xt.data_ptr(), m, yt.data_ptr(), rq.MODE_FLOAT, s)
+        torch.cuda.synchronize()
+        want = rq.matmul_f32_q4(x, w, m, k, n)
+        assert np.array_equal(yt.cpu().numpy(), want.reshape(-1)), f"call {rep}: n={n} k={k} m={m}"
+
+
 def test_skinny_gemm_graph_replays_match_eager(rq, gpu):
     """A 16-row prefill product captured in a graph (graph-owned scratch and
     counters, zeroed by a kernel on every replay) reproduces the eager result

@@ -98,10 +98,12 @@ def test_small_m_shapes(rq, orc, gpu, m, n, k):
     run(rq, orc, m, n, k, 7 + m + n + k)
 
 
-def test_small_m_block_extremes(rq, orc, gpu):
+@pytest.mark.parametrize("m", [16, 24])
+def test_small_m_block_extremes(rq, orc, gpu, m):
     # per-block scaling: all-zero, subnormal, huge and mixed-magnitude blocks
     # each keep the bar; an infinite element makes its row non-finite only
-    m, n, k = 24, 80, 1024
+    # (m = 16: the kernel whose K-slices meet through tagged partials)
+    n, k = 80, 1024
     x = synth.activations(m, k, 91)
     w = synth.q4_0_weights(n, k, 92)
     x[1, 0:32] = 0.0                                   # a zero block
