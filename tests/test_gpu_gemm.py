@@ -102,7 +102,7 @@ def test_small_m_shapes(rq, orc, gpu, m, n, k):
 def test_small_m_block_extremes(rq, orc, gpu, m):
     # per-block scaling: all-zero, subnormal, huge and mixed-magnitude blocks
     # each keep the bar; an infinite element makes its row non-finite only
-    # (m = 16: the kernel whose K-slices meet through tagged partials)
+    # (m = 16 and m = 24: the two K-split kernels for small m)
     n, k = 80, 1024
     x = synth.activations(m, k, 91)
     w = synth.q4_0_weights(n, k, 92)
