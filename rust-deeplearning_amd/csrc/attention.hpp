@@ -158,6 +158,7 @@ struct AttArgs {
     int* counters;             // [rows][n_heads] span counters
     float* out;                // [rows][n_heads * hd]
     const uint64_t* xch;       // FUSED: the layer's exchange
+    uint64_t* oxch;            // FUSED, when set: outputs as tagged words (tag t) here instead of out
     int* err;                  // FUSED: set when a wait runs out (never in a correct launch)
 };
 
@@ -467,9 +468,16 @@ __device__ __forceinline__ void attention_body(int bx, int by, int bz, float* __
         for (int c = 0; c < ATT_WAVES; c++) O = c < nw ? O + os[c * hd + d] * wc[c] : O;
         return O;
     };
+    // output element d of the head: to out, or tagged to the o projection of
+    // the same launch
+    uint64_t* ox = (FUSED && a.oxch) ? a.oxch + (size_t)h * hd : nullptr;
+    auto put = [&](int d, float v) {
+        if (FUSED && ox) xch_put(ox + d, v, t);
+        else o[d] = v;
+    };
     if (nz == 1) {
         const float invL = 1.0f / L;
-        for (int d = threadIdx.x; d < hd; d += 64 * ATT_WAVES) o[d] = chunk_sum(d) * invL;
+        for (int d = threadIdx.x; d < hd; d += 64 * ATT_WAVES) put(d, chunk_sum(d) * invL);
         return;
     }
     // several workgroups: partial (M, L, O) to global, the last one combines.
@@ -522,7 +530,7 @@ __device__ __forceinline__ void attention_body(int bx, int by, int bz, float* __
     for (int d = threadIdx.x; d < hd; d += 64 * ATT_WAVES) {
         float O = 0.0f;
         for (int c = 0; c < nz; c++) O += ld(pb + (size_t)c * (hd + 2) + 2 + d) * wsc[c];
-        o[d] = O * invL;
+        put(d, O * invL);
     }
 }
 

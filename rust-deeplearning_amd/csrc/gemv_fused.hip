@@ -838,24 +838,126 @@ __global__ __launch_bounds__(NW * 64) void gemv_fused_kernel(const uint8_t* __re
                                                                       Y, fz);
 }
 
+// The o projection of a fused decode step: x += att W_o^T over rows [0, n)
+// of W_o (Q4_0, nb blocks a row), the attention outputs read from the
+// exchange xch ([n_heads * hd] tagged words, tag t).
+struct OProj {
+    const uint8_t* w;
+    int n, nb;
+    float* x;              // residual stream [n]
+    const uint64_t* xch;
+};
+
+// One o-projection workgroup of the fused decode launch: rows r0 + wv + 8 r
+// (r < RO) of W_o, wave wv.  Its weight blocks do not depend on the
+// attention, so all of them are loaded at the start (RO * 2 windows a lane)
+// and arrive while the q/k/v workgroups and the attention run.  The
+// attention outputs are then polled from the exchange (each wave first
+// watches one word with a single lane, then takes its lanes' pieces once
+// they all carry tag t), and go through the same records, block order and
+// per-row reduction as the o launch of the unfused step (gemv_fused_kernel,
+// one row a wave), so both give the same bits.  Bounded: a wait that runs
+// out sets *err (never in a correct launch).
+template <int RO>
+__device__ __forceinline__ void o_proj_body(int j, i32x4* __restrict__ lds4, const OProj& op, int t, int* err) {
+    constexpr int NW = 8, CPL = 2, NB = RO * CPL, PI = 1;
+    constexpr int WORDS = Geo<(int)WType::Q4_0>::WORDS, BYTES = Geo<(int)WType::Q4_0>::BYTES;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int nb = op.nb, n = op.n;
+    const int r0 = j * NW * RO;
+    const uint32_t row_bytes = (uint32_t)nb * BYTES, wbytes = (uint32_t)n * row_bytes;
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(op.w, wbytes);
+    uint32_t win[NB][WORDS];
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        const int row = r0 + wv + (b / CPL) * NW, col = lane + 64 * (b % CPL);
+        const uint32_t off = (row < n && col < nb) ? (uint32_t)row * row_bytes + (uint32_t)col * BYTES : RSRC_OOB;
+        load_window<WORDS, false>(rs, off, wbytes, win[b]);
+    }
+    float y_old[RO];
+#pragma unroll
+    for (int r = 0; r < RO; r++) {
+        const int row = r0 + wv + r * NW;
+        y_old[r] = row < n ? op.x[row] : 0.0f;
+    }
+    // this thread's activation pieces (load_prep_x4's): block c, elements
+    // 32 c + 4 k + {0..3} and + 16
+    const int p = min((int)threadIdx.x, nb * 4 - 1);
+    const int o = (p >> 2) * 32 + (p & 3) * 4;
+    const uint64_t* src = op.xch + o;
+    const uint64_t* watch = op.xch + min(wv * 512 + 511, nb * 32 - 1);
+    for (int spins = 0;; spins++) {
+        const bool ready = att::xch_ok(att::xch_get(watch), t);
+        if (ready || spins > (1 << 16)) break;
+        __builtin_amdgcn_s_sleep(2);
+    }
+    uint64_t v[8];
+    for (int spins = 0;; spins++) {
+        bool ok = true;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            v[i] = att::xch_get(src + (i & 3) + (i >> 2) * 16);
+            ok = ok && att::xch_ok(v[i], t);
+        }
+        if (__builtin_amdgcn_ballot_w64(!ok) == 0) break;
+        if (spins > (1 << 16)) {  // tens of milliseconds: only a broken launch gets here
+            if (lane == 0) __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+    f32x4 xv[PI][2], av[PI][2];
+    xv[0][0] = f32x4{att::xch_val(v[0]), att::xch_val(v[1]), att::xch_val(v[2]), att::xch_val(v[3])};
+    xv[0][1] = f32x4{att::xch_val(v[4]), att::xch_val(v[5]), att::xch_val(v[6]), att::xch_val(v[7])};
+    prep_float4_lds<NW, PI, PRO_NONE>(xv, av, 0.0f, nb, reinterpret_cast<int*>(lds4));
+    __syncthreads();
+    RF4 keep[CPL];
+#pragma unroll
+    for (int i = 0; i < CPL; i++) keep[i] = read_rf4(lds4, nb, min(lane + 64 * i, nb - 1));
+#pragma unroll
+    for (int r = 0; r < RO; r++) {
+        const int row = r0 + wv + r * NW;
+        float acc[1] = {0.0f};
+#pragma unroll
+        for (int i = 0; i < CPL; i++) {
+            const int col = lane + 64 * i;
+            if (row < n && col < nb) {
+                const bool odd = (col & 1) != 0;
+                acc[0] += block_dot_i4<(int)WType::Q4_0>(win[r * CPL + i], odd ? 0x07060504u : 0x05040302u,
+                                                         odd ? 16u : 0u, keep[i]);
+            }
+        }
+        const float s = wave_reduce_rows<1>(acc);
+        if (lane == 0 && row < n) op.x[row] = s + y_old[r];
+    }
+}
+
+// Rows of W_o an o-projection workgroup owns (8 waves x O_ROWS_PER_WAVE).
+constexpr int O_ROWS_PER_WAVE = 4;
+
 // One decode step's q/k/v projection (RMSNorm prologue, RoPE + KV-cache
 // epilogue) with the decode attention fused into the same launch: workgroups
-// [0, n_gemv) are the GEMV's, the rest attention workgroups (head, span) that
-// load their older K/V rows at once, wait for their KV group's q/k/v
-// workgroups (published counts) and then read q and the current row.  All
-// workgroups fit the device at once (a few hundred against two per CU), and
-// the waits are bounded, so no ordering of workgroup dispatch can block them.
+// [0, n_gemv) are the GEMV's, the next n_att attention workgroups (head,
+// span) that load their older K/V rows at once, wait for their KV group's
+// q/k/v values (tagged exchange) and then read q and the current row; with
+// op.w set, the rest are o-projection workgroups (o_proj_body) that wait for
+// the attention outputs.  All workgroups fit the device at once (a few
+// hundred against two per CU), the o-projection ones come last in dispatch
+// order, and the waits are bounded, so no ordering of workgroup dispatch can
+// block them.
 template <typename KV, int HD, int R, int CPL>
 __global__ __launch_bounds__(512) void qkv_attention_kernel(const uint8_t* __restrict__ W, int n, int nb, int rpw,
                                                             const float* __restrict__ X, float* __restrict__ Y, Fuse fz,
-                                                            AttArgs<KV> aa, int n_gemv) {
+                                                            AttArgs<KV> aa, int n_gemv, int n_att, OProj op) {
     extern __shared__ i32x4 lds4[];
     if ((int)blockIdx.x < n_gemv) {
         gemv_fused_body<(int)WType::Q4_0, false, R, CPL, true, 8, PRO_RMSNORM, EPI_ROPE_KV, true>(
             blockIdx.x, 0, lds4, W, n, nb, rpw, X, Y, fz);
-    } else {
+    } else if ((int)blockIdx.x < n_gemv + n_att) {
         const int a = (int)blockIdx.x - n_gemv;
         attention_body<KV, HD, true>(a % aa.n_heads, 0, a / aa.n_heads, reinterpret_cast<float*>(lds4), aa);
+    } else {
+        o_proj_body<O_ROWS_PER_WAVE>((int)blockIdx.x - n_gemv - n_att, lds4, op, *fz.pos + 1, aa.err);
     }
 }
 
@@ -1716,7 +1818,7 @@ hipError_t launch_qkv_attention(const uint8_t* w, size_t n, size_t k, const floa
                                 float eps, const int* pos, const float* cos_t, const float* sin_t, void* kc, void* vc,
                                 const int* kv_table, int n_heads, int n_kv, int hd, bool kv_f16, float* att_part,
                                 int nspan, int spans, int* att_cnt, float* att_out, uint64_t* xch, int* err,
-                                hipStream_t s) {
+                                const uint8_t* wo, size_t n_o, float* x_res, uint64_t* oxch, hipStream_t s) {
     const int nb = (int)(k / QK);
     const int cpl = cpl_for(nb);
     // the q/k/v launch's shape (launch_q4_0_fused_ex, EPI_ROPE_KV): row pairs, R rows a wave, 8 waves
@@ -1744,9 +1846,26 @@ hipError_t launch_qkv_attention(const uint8_t* w, size_t n, size_t k, const floa
     fz.xch = xch;
     const int n_gemv = (int)((n + rpw - 1) / rpw);
     if (spans < 1 || spans > nspan) return hipErrorInvalidValue;
-    const dim3 grid((unsigned)(n_gemv + n_heads * spans)), block(512);
-    // attention: q | per-wave contexts | current k | current v (f32)
-    const size_t lds = std::max((size_t)8 * 16 * nb, (size_t)(3 + ATT_WAVES) * hd * sizeof(float));
+    // o projection (optional): K = n_heads * hd in 32-element blocks, at most
+    // two block columns a lane and one activation piece a thread
+    OProj op{};
+    int n_ow = 0;
+    const int nb_o = n_heads * hd / QK;
+    if (wo) {
+        if ((n_heads * hd) % QK || nb_o > 128 || (nb_o & 1) || n_o == 0 || x_res == nullptr || oxch == nullptr ||
+            (uint64_t)n_o * nb_o * Q4_0_BYTES > FUSED_MAX_WEIGHT_BYTES)
+            return hipErrorInvalidValue;
+        op.w = wo;
+        op.n = (int)n_o;
+        op.nb = nb_o;
+        op.x = x_res;
+        op.xch = oxch;
+        n_ow = (int)((n_o + 8 * O_ROWS_PER_WAVE - 1) / (8 * O_ROWS_PER_WAVE));
+    }
+    const int n_att = n_heads * spans;
+    const dim3 grid((unsigned)(n_gemv + n_att + n_ow)), block(512);
+    // attention: q | per-wave contexts | current k | current v (f32); records of q/k/v's and o's x
+    const size_t lds = std::max({(size_t)8 * 16 * nb, (size_t)8 * 16 * nb_o, (size_t)(3 + ATT_WAVES) * hd * sizeof(float)});
     auto go = [&](auto kv_tag, auto hd_tag, auto r_tag) {
         using KV = decltype(kv_tag);
         constexpr int HD = decltype(hd_tag)::value, R = decltype(r_tag)::value, CPL = R == 4 ? 2 : 4;
@@ -1766,9 +1885,10 @@ hipError_t launch_qkv_attention(const uint8_t* w, size_t n, size_t k, const floa
         aa.counters = att_cnt;
         aa.out = att_out;
         aa.xch = xch;
+        aa.oxch = wo ? oxch : nullptr;
         aa.err = err;
         launch_kernel(qkv_attention_kernel<KV, HD, R, CPL>, grid, block, lds, s, w, (int)n, nb, rpw, x, y, fz, aa,
-                      n_gemv);
+                      n_gemv, n_att, op);
     };
     using I64 = std::integral_constant<int, 64>;
     using I128 = std::integral_constant<int, 128>;

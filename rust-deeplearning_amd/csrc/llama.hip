@@ -333,7 +333,10 @@ struct LlamaModel {
     int att_nspan = 0;
     // decode steps: attention fused into the q/k/v launch (fused layers, one row)
     bool fused_attention = true;
-    uint64_t* att_xch = nullptr;  // [layer][qkv_dim] fused-attention exchange (zero on an empty cache)
+    // [layer][xch_stride()] exchange of the fused decode launch: the q/k/v
+    // values, then the attention outputs (zero on an empty cache)
+    uint64_t* att_xch = nullptr;
+    size_t xch_stride() const { return (size_t)qkv_dim + q_dim; }
     int* att_err = nullptr;  // set by a fused launch whose wait ran out
     hipStream_t stream = nullptr;
     hipGraphExec_t decode_exec = nullptr;
@@ -440,14 +443,16 @@ struct LlamaModel {
         Layer& L = layers[l];
         hipError_t e;
         if (m == 1 && fused_attention) {
-            // q/k/v, RoPE + cache, and the attention over the cache in one launch
+            // q/k/v, RoPE + cache, the attention over the cache and the o
+            // projection with its residual add in one launch
+            uint64_t* xl = att_xch + (size_t)l * xch_stride();
             e = launch_qkv_attention(L.qkv.dev, L.qkv.n, d, x, qkv, L.attn_norm, eps, pos, cos_t, sin_t,
                                      kv_layer(kc, l), kv_layer(vc, l), kv_table, cfg.n_heads, cfg.n_kv_heads,
                                      cfg.head_dim, cfg.kv_f16 != 0, att_part, att_nspan, chunks_needed(1), att_cnt,
-                                     att, att_xch + (size_t)l * qkv_dim, att_err, stream);
+                                     att, xl, att_err, L.o.dev, L.o.n, x, xl + qkv_dim, stream);
             if (e != hipErrorInvalidValue) {
                 if (e != hipSuccess) return e;
-                return layer_fused_tail(l, m);
+                return layer_fused_tail(l, m, true);
             }
             (void)hipGetLastError();
         }
@@ -458,17 +463,20 @@ struct LlamaModel {
         if (e != hipSuccess) return e;
         e = cfg.kv_f16 ? layer_attention<_Float16>(l, m, false) : layer_attention<float>(l, m, false);
         if (e != hipSuccess) return e;
-        return layer_fused_tail(l, m);
+        return layer_fused_tail(l, m, false);
     }
 
-    // o, gate/up and down of a fused layer (after its attention)
-    hipError_t layer_fused_tail(int l, size_t m) {
+    // o (unless o_done), gate/up and down of a fused layer (after its attention)
+    hipError_t layer_fused_tail(int l, size_t m, bool o_done) {
         const int d = cfg.dim;
         const float eps = cfg.norm_eps;
         Layer& L = layers[l];
+        hipError_t e;
         // x += att . Wo^T
-        hipError_t e = launch_gemv_q4_0_fused_ex(L.o.dev, L.o.n, q_dim, att, q_dim, m, x, 0, nullptr, 0.0f, 1, stream);
-        if (e != hipSuccess) return e;
+        if (!o_done) {
+            e = launch_gemv_q4_0_fused_ex(L.o.dev, L.o.n, q_dim, att, q_dim, m, x, 0, nullptr, 0.0f, 1, stream);
+            if (e != hipSuccess) return e;
+        }
         // h = silu(gate) * up with [gate; up] = rms_norm(x) . Wgu^T (rows interleaved)
         e = launch_gemv_q4_0_fused_ex(L.gu.dev, L.gu.n, d, x, d, m, hb, 1, L.ffn_norm, eps, 2, stream);
         if (e != hipSuccess) return e;
@@ -721,7 +729,7 @@ rdl_status check_fused(rdl::LlamaModel& M) {
     HIP_TRY(hipMemcpy(&err, M.att_err, sizeof(int), hipMemcpyDeviceToHost));
     if (!err) return RDL_OK;
     HIP_TRY(hipMemset(M.att_err, 0, sizeof(int)));
-    HIP_TRY(hipMemset(M.att_xch, 0, (size_t)M.cfg.n_layers * M.qkv_dim * sizeof(uint64_t)));
+    HIP_TRY(hipMemset(M.att_xch, 0, (size_t)M.cfg.n_layers * M.xch_stride() * sizeof(uint64_t)));
     return api_fail(RDL_ERR_HIP, "fused decode attention: a wait for the q/k/v workgroups ran out");
 }
 
@@ -881,8 +889,8 @@ rdl_status rdl_llama_create_typed(const rdl_llama_config* cfg, const int32_t* ty
         return fail_free(e);
     if ((e = M.alloc_t(&M.att_cnt, mb * c.n_heads)) != hipSuccess) return fail_free(e);
     if ((e = hipMemset(M.att_cnt, 0, mb * c.n_heads * sizeof(int))) != hipSuccess) return fail_free(e);
-    if ((e = M.alloc_t(&M.att_xch, (size_t)c.n_layers * M.qkv_dim)) != hipSuccess) return fail_free(e);
-    if ((e = hipMemset(M.att_xch, 0, (size_t)c.n_layers * M.qkv_dim * sizeof(uint64_t))) != hipSuccess)
+    if ((e = M.alloc_t(&M.att_xch, (size_t)c.n_layers * M.xch_stride())) != hipSuccess) return fail_free(e);
+    if ((e = hipMemset(M.att_xch, 0, (size_t)c.n_layers * M.xch_stride() * sizeof(uint64_t))) != hipSuccess)
         return fail_free(e);
     if ((e = M.alloc_t(&M.att_err, 1)) != hipSuccess) return fail_free(e);
     if ((e = hipMemset(M.att_err, 0, sizeof(int))) != hipSuccess) return fail_free(e);
@@ -966,7 +974,7 @@ rdl_status rdl_llama_reset(rdl_llama* model) {
     hipLaunchKernelGGL(rdl::set_int_kernel, dim3(1), dim3(64), 0, M.stream, M.pos, 0);
     HIP_TRY(hipGetLastError());
     HIP_TRY(hipStreamSynchronize(M.stream));
-    HIP_TRY(hipMemset(M.att_xch, 0, (size_t)M.cfg.n_layers * M.qkv_dim * sizeof(uint64_t)));
+    HIP_TRY(hipMemset(M.att_xch, 0, (size_t)M.cfg.n_layers * M.xch_stride() * sizeof(uint64_t)));
     HIP_TRY(hipMemset(M.att_err, 0, sizeof(int)));
     M.host_pos = 0;
     return api_ok();

@@ -211,13 +211,17 @@ hipError_t launch_gemv_q4_0_rope_kv(const uint8_t* w, size_t n, size_t k, const 
 // past the position exit at once); xch = the layer's exchange of n tagged
 // q / k / v words (zero on an empty cache; *pos must grow from one launch on
 // the same exchange to the next), err = a flag set if a wait runs out.
+// With wo set, the same launch also applies the o projection: x_res[n_o] +=
+// att W_o^T (W_o Q4_0, n_heads * hd columns), the attention outputs passing
+// through oxch (n_heads * hd tagged words, same rules as xch) instead of
+// att_out; the results equal the separate o launch's bit for bit.
 // hipErrorInvalidValue for shapes it does not take (then use
-// launch_gemv_q4_0_rope_kv and the attention launch).
+// launch_gemv_q4_0_rope_kv, the attention launch and the o launch).
 hipError_t launch_qkv_attention(const uint8_t* w, size_t n, size_t k, const float* x, float* y, const float* g,
                                 float eps, const int* pos, const float* cos_t, const float* sin_t, void* kc, void* vc,
                                 const int* kv_table, int n_heads, int n_kv, int hd, bool kv_f16, float* att_part,
                                 int nspan, int spans, int* att_cnt, float* att_out, uint64_t* xch, int* err,
-                                hipStream_t s);
+                                const uint8_t* wo, size_t n_o, float* x_res, uint64_t* oxch, hipStream_t s);
 
 // launch_gemv_q4_0_rope_kv for a Q4_K or Q6_K [Wq; Wk; Wv]: m <= 4 activation
 // rows (k floats apart) at positions *pos + row0 + row, q rows ystride apart.
