@@ -62,6 +62,32 @@ def test_generate_greedy_matches_eager_steps(rq, gpu):
     assert m.generate_greedy(prompt, 12).tolist() == eager
 
 
+def test_greedy_sampling_ties_pick_the_first_maximum(rq, gpu):
+    """Output rows repeat with period 37, so each maximum logit is shared by
+    8-9 token ids in different workgroups of the lm_head launch: the decode
+    graph's sampling (per-workgroup argmax partials) picks the first, as
+    numpy's argmax over the eager logits does (sampling.rs:8-18)."""
+    from rdlquant.llama import LlamaModel, OUTPUT
+    cfg = tiny_config()
+    slots, _ = tiny_weights(cfg, 4321)
+    m = LlamaModel(cfg)
+    for slot, layer, arr in slots:
+        if slot == OUTPUT:
+            arr = arr.reshape(cfg.vocab, -1)[np.arange(cfg.vocab) % 37].copy()
+        m.set_weight(slot, layer, arr)
+    prompt = [5, 6, 7]
+    gen = m.generate_greedy(prompt, 10)
+    m.reset()
+    logits = m.forward_with_cache(prompt)
+    eager = []
+    for _ in range(10):
+        t = int(np.argmax(logits))
+        assert np.count_nonzero(logits == logits[t]) > 1  # a real tie
+        eager.append(t)
+        logits = m.decode_step(t)
+    assert gen.tolist() == eager
+
+
 def test_generate_greedy_matches_oracle_tokens(rq, gpu):
     cfg = tiny_config()
     m, ref = build(cfg, seed=99)
