@@ -226,7 +226,6 @@ struct Fuse {
     const int* kv_table;        // physical page of each logical page
     int n_heads, n_kv, hd, kv_f16;
     uint64_t* xch;              // PUB: the layer's exchange, one tagged value per q / k / v row
-    int* am;                    // EPI_ARGMAX: the per-workgroup partials
 };
 
 template <int NW, int PI, int PRO = PRO_NONE>
@@ -571,11 +570,7 @@ __device__ __forceinline__ float block_dot_i4(const uint32_t (&w)[5], uint32_t s
 // EPI_ROPE_KV: W holds [Wq; Wk; Wv] and a wave owns the RoPE pairs (i, i + hd/2)
 // of a head: q rows are rotated in place in y, k rows rotated and v rows
 // copied into the KV cache at the row's position (y's k / v rows unwritten).
-// EPI_ARGMAX: y = W x, and the workgroup's greedy-sampling partial: the
-// largest y of its rows and the first row that holds it (NaN never, -inf
-// never; sampling.rs:8-18) as fz.am[2 (by * gridDim.x + bx) + {0, 1}] =
-// {bits(value), row} ({-inf, INT_MAX} when no row qualifies).
-constexpr int EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_SWIGLU = 2, EPI_ROPE_KV = 3, EPI_ARGMAX = 4;
+constexpr int EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_SWIGLU = 2, EPI_ROPE_KV = 3;
 
 // PRO: prologue on x (PRO_NONE / PRO_RMSNORM / PRO_SWIGLU, int4 records only).
 // The body of one workgroup (bx, by): row group bx, activation row by.
@@ -661,7 +656,7 @@ __device__ __forceinline__ void gemv_fused_body(int bx, int by, i32x4* __restric
     // groups of four
     constexpr int RG = R > 4 ? 4 : R;
     constexpr int NGRP = R / RG;
-    static_assert(R <= 4 || (R == 8 && (EPI == EPI_STORE || EPI == EPI_SWIGLU || EPI == EPI_ARGMAX)), "rows per wave");
+    static_assert(R <= 4 || (R == 8 && (EPI == EPI_STORE || EPI == EPI_SWIGLU)), "rows per wave");
     constexpr int SH = reduce_span_log2<RG>();
     const bool st_lane = (lane & (((PAIRS ? 2 : 1) << SH) - 1)) == 0;
     const int st_row = row_of(lane >> SH);
@@ -757,13 +752,7 @@ __device__ __forceinline__ void gemv_fused_body(int bx, int by, i32x4* __restric
         }
     }
     const bool has_rows = row_of(0) < rend;  // wave-uniform
-    if constexpr (EPI != EPI_ARGMAX) {
-        if (!has_rows) return;  // the wave had nothing to store
-    }
-    // EPI_ARGMAX: this lane's best stored row so far (rows visited in
-    // increasing order, strict >: the first maximum)
-    float am_v = -__builtin_inff();
-    int am_i = 0x7FFFFFFF;
+    if (!has_rows) return;  // the wave had nothing to store
 
     // ---- reduce and store ----
 #pragma unroll
@@ -833,43 +822,7 @@ __device__ __forceinline__ void gemv_fused_body(int bx, int by, i32x4* __restric
                     y[row] = s + y_old;
                 else
                     y[row] = s;
-                if constexpr (EPI == EPI_ARGMAX) {
-                    if (s > am_v) {
-                        am_v = s;
-                        am_i = row;
-                    }
-                }
             }
-        }
-    }
-    if constexpr (EPI == EPI_ARGMAX) {
-        // (value, row): larger value, then smaller row; across the wave, then
-        // the waves in LDS (every wave reaches this barrier)
-        __shared__ float am_sv[NW];
-        __shared__ int am_si[NW];
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) {
-            const float ov = __shfl_xor(am_v, o);
-            const int oi = __shfl_xor(am_i, o);
-            if (ov > am_v || (ov == am_v && oi < am_i)) {
-                am_v = ov;
-                am_i = oi;
-            }
-        }
-        if (lane == 0) {
-            am_sv[wv] = am_v;
-            am_si[wv] = am_i;
-        }
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            for (int w = 1; w < NW; w++)
-                if (am_sv[w] > am_v || (am_sv[w] == am_v && am_si[w] < am_i)) {
-                    am_v = am_sv[w];
-                    am_i = am_si[w];
-                }
-            int* pa = fz.am + 2 * ((size_t)by * gridDim.x + bx);
-            pa[0] = __builtin_bit_cast(int, am_v);
-            pa[1] = am_i;
         }
     }
 }
@@ -1598,9 +1551,8 @@ Cfg pick_cfg(int n, int nw, int rmax, int wg_per_cu) {
     return Cfg{nw, rpw, r};
 }
 
-// Returns the launch's workgroups per activation row (grid.x).
 template <int WT, bool NATIVE, int CPL, bool EVEN, int NW, int PRO = PRO_NONE, int RES = EPI_STORE>
-int launch_nw(const uint8_t* w, int n, int nb, const float* x, size_t m, float* y, hipStream_t s,
+void launch_nw(const uint8_t* w, int n, int nb, const float* x, size_t m, float* y, hipStream_t s,
                const Cfg& c, size_t lds, const Fuse& fz) {
     const dim3 grid((unsigned)((n + c.rpw - 1) / c.rpw), (unsigned)m), block(NW * 64);
     constexpr int RMAX = 8 / CPL;
@@ -1611,7 +1563,7 @@ int launch_nw(const uint8_t* w, int n, int nb, const float* x, size_t m, float* 
             if constexpr (RES == EPI_SWIGLU) {
                 if (c.r >= 8) {
                     launch_kernel((gemv_fused_kernel<WT, NATIVE, 8, CPL, EVEN, NW, PRO, RES>), grid, block, lds, s, w, n, nb, rpw, x, y, fz);
-                    return (int)grid.x;
+                    return;
                 }
             }
             if (c.r >= 4)
@@ -1621,9 +1573,9 @@ int launch_nw(const uint8_t* w, int n, int nb, const float* x, size_t m, float* 
         } else if constexpr (RMAX >= 2) {
             launch_kernel((gemv_fused_kernel<WT, NATIVE, 2, CPL, EVEN, NW, PRO, RES>), grid, block, lds, s, w, n, nb, rpw, x, y, fz);
         }
-        return (int)grid.x;
-    } else if (c.r >= 8 && RMAX >= 4 && (RES == EPI_STORE || RES == EPI_ARGMAX))
-        launch_kernel((gemv_fused_kernel<WT, NATIVE, ((RES == EPI_STORE || RES == EPI_ARGMAX) && RMAX >= 4 ? 8 : 1), CPL, EVEN, NW, PRO, RES>), grid, block, lds, s, w, n, nb, rpw, x, y, fz);
+        return;
+    } else if (c.r >= 8 && RMAX >= 4 && RES == EPI_STORE)
+        launch_kernel((gemv_fused_kernel<WT, NATIVE, (RES == EPI_STORE && RMAX >= 4 ? 8 : 1), CPL, EVEN, NW, PRO, RES>), grid, block, lds, s, w, n, nb, rpw, x, y, fz);
     else if (c.r <= 1 || RMAX == 1)
         launch_kernel((gemv_fused_kernel<WT, NATIVE, 1, CPL, EVEN, NW, PRO, RES>), grid, block, lds, s, w, n, nb, rpw, x, y, fz);
     else if (c.r <= 2 || RMAX == 2)
@@ -1632,7 +1584,6 @@ int launch_nw(const uint8_t* w, int n, int nb, const float* x, size_t m, float* 
         launch_kernel((gemv_fused_kernel<WT, NATIVE, (RMAX >= 4 ? 3 : 1), CPL, EVEN, NW, PRO, RES>), grid, block, lds, s, w, n, nb, rpw, x, y, fz);
     else
         launch_kernel((gemv_fused_kernel<WT, NATIVE, (RMAX >= 4 ? 4 : 1), CPL, EVEN, NW, PRO, RES>), grid, block, lds, s, w, n, nb, rpw, x, y, fz);
-    return (int)grid.x;
 }
 
 template <int WT, bool NATIVE, int CPL, bool EVEN>
@@ -1769,15 +1720,15 @@ void launch_kq(WType t, const uint8_t* w, int n, int nsb, const float* x, size_t
 // Decoder fusion: Q4_0 float mode, nb even.  8-wave workgroups, two per CU;
 // rows longer than 4096 (their x, re-read by every workgroup, is long): one
 // 16-wave workgroup per CU.
-// Returns the launch's workgroups per activation row.
 template <int PRO, int RES>
-int launch_q4_0_fused_ex(const uint8_t* w, int n, int nb, const float* x, size_t m, float* y,
+void launch_q4_0_fused_ex(const uint8_t* w, int n, int nb, const float* x, size_t m, float* y,
                           hipStream_t s, size_t lds, const Fuse& fz) {
     const int cpl = cpl_for(nb);
     constexpr int Q = (int)WType::Q4_0;
     if (RES != EPI_SWIGLU && RES != EPI_ROPE_KV && cpl == 8) {
         const Cfg c16 = pick_cfg(n, 16, 1, 1);
-        return launch_nw<Q, false, 8, true, 16, PRO, RES>(w, n, nb, x, m, y, s, c16, lds, fz);
+        launch_nw<Q, false, 8, true, 16, PRO, RES>(w, n, nb, x, m, y, s, c16, lds, fz);
+        return;
     }
     Cfg c = pick_cfg(n, 8, 8 / cpl, 2);
     if (RES == EPI_SWIGLU || RES == EPI_ROPE_KV) {
@@ -1790,14 +1741,14 @@ int launch_q4_0_fused_ex(const uint8_t* w, int n, int nb, const float* x, size_t
     // Matrices taller than one round of two 8-wave workgroups a CU at 4 rows
     // a wave (the 28672-row gate/up, the 32000-row lm_head): 8 rows a wave, so
     // every workgroup is resident from the start and prepares x once.
-    if ((RES == EPI_SWIGLU || RES == EPI_STORE || RES == EPI_ARGMAX) && cpl == 2 && n > num_cus() * 2 * 8 * 4) {
+    if ((RES == EPI_SWIGLU || RES == EPI_STORE) && cpl == 2 && n > num_cus() * 2 * 8 * 4) {
         c.r = 8;
         c.rpw = 64;
     }
     switch (cpl) {
-        case 2: return launch_nw<Q, false, 2, true, 8, PRO, RES>(w, n, nb, x, m, y, s, c, lds, fz);
-        case 4: return launch_nw<Q, false, 4, true, 8, PRO, RES>(w, n, nb, x, m, y, s, c, lds, fz);
-        default: return launch_nw<Q, false, 8, true, 8, PRO, RES>(w, n, nb, x, m, y, s, c, lds, fz);
+        case 2: launch_nw<Q, false, 2, true, 8, PRO, RES>(w, n, nb, x, m, y, s, c, lds, fz); break;
+        case 4: launch_nw<Q, false, 4, true, 8, PRO, RES>(w, n, nb, x, m, y, s, c, lds, fz); break;
+        default: launch_nw<Q, false, 8, true, 8, PRO, RES>(w, n, nb, x, m, y, s, c, lds, fz); break;
     }
 }
 
@@ -1833,24 +1784,6 @@ hipError_t launch_gemv_q4_0_fused_ex(const uint8_t* w, size_t n, size_t k, const
         launch_q4_0_fused_ex<PRO_NONE, EPI_SWIGLU>(w, ni, nb, x, m, y, s, lds, fz);
     else
         return hipErrorInvalidValue;
-    return hipGetLastError();
-}
-
-hipError_t launch_gemv_q4_0_argmax(const uint8_t* w, size_t n, size_t k, const float* x, float* y, const float* g,
-                                   float eps, int* am, size_t am_cap, int* n_parts, hipStream_t s) {
-    *n_parts = 0;
-    const int nb = (int)(k / QK);
-    if (n == 0 || n > 0x7FFFFFFF || nb == 0 || (nb & 1) || k > fused_max_k(WType::Q4_0) || ((uintptr_t)x & 15) ||
-        am == nullptr || am_cap < n || (uint64_t)n * nb * Q4_0_BYTES > FUSED_MAX_WEIGHT_BYTES)
-        return hipErrorInvalidValue;
-    Fuse fz{};
-    fz.g = g;
-    fz.eps = eps;
-    fz.xstride = (int)k;
-    fz.am = am;
-    // at most one workgroup a row, so am_cap >= n pairs always suffices
-    *n_parts = g ? launch_q4_0_fused_ex<PRO_RMSNORM, EPI_ARGMAX>(w, (int)n, nb, x, 1, y, s, (size_t)8 * 16 * nb, fz)
-                 : launch_q4_0_fused_ex<PRO_NONE, EPI_ARGMAX>(w, (int)n, nb, x, 1, y, s, (size_t)8 * 16 * nb, fz);
     return hipGetLastError();
 }
 

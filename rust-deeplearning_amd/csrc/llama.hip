@@ -164,13 +164,9 @@ __global__ void swiglu2_kernel(const float* __restrict__ g, const float* __restr
 // (KVCache::advance, kv_cache.rs:112-114), and the sampled token's embedding
 // row dequantized into x (Embedding::forward, embedding.rs:50-76, on the Q4_0
 // table as Tensor::to_f32 computes it: d * (q - 8)) for the next step (emb
-// NULL: no embedding, the next forward reads the token id).  With am set the
-// argmax reads the lm_head launch's nparts per-workgroup partials (pairs
-// {bits(value), index}, launch_gemv_q4_0_argmax) instead of the logits: the
-// same rule over the same candidates, so the same token.
+// NULL: no embedding, the next forward reads the token id).
 constexpr int SAMPLE_NT = 1024;
 __global__ __launch_bounds__(SAMPLE_NT) void sample_kernel(const float* __restrict__ logits, int vocab,
-                                                           const int* __restrict__ am, int nparts,
                                                            int* __restrict__ token, int* __restrict__ out_tokens,
                                                            int* __restrict__ step, int* __restrict__ pos,
                                                            int advance, const uint8_t* __restrict__ emb, int dim,
@@ -184,7 +180,7 @@ __global__ __launch_bounds__(SAMPLE_NT) void sample_kernel(const float* __restri
     const int st = threadIdx.x == 0 ? *step : 0;
     float best = -__builtin_inff();
     int idx = 0x7FFFFFFF;
-    const int n4 = am ? 0 : vocab >> 2;
+    const int n4 = vocab >> 2;
     const f4* l4 = reinterpret_cast<const f4*>(logits);
     // each thread visits its indices in increasing order
     for (int base = 0; base < n4; base += SAMPLE_NT * VU) {
@@ -206,19 +202,11 @@ __global__ __launch_bounds__(SAMPLE_NT) void sample_kernel(const float* __restri
                     }
         }
     }
-    for (int i = 4 * n4 + (int)threadIdx.x; !am && i < vocab; i += SAMPLE_NT) {
+    for (int i = 4 * n4 + (int)threadIdx.x; i < vocab; i += SAMPLE_NT) {
         const float v = logits[i];
         if (v > best) {
             best = v;
             idx = i;
-        }
-    }
-    for (int i = threadIdx.x; am && i < nparts; i += SAMPLE_NT) {
-        const float v = __builtin_bit_cast(float, am[2 * i]);
-        const int vi = am[2 * i + 1];
-        if (v > best || (v == best && vi < idx)) {
-            best = v;
-            idx = vi;
         }
     }
     // (value, index) reduction: larger value, then smaller index
@@ -599,8 +587,6 @@ struct LlamaModel {
 
     bool fused_shapes = false;  // the model's shapes meet the fused launches' rules
     bool sample_embeds = false; // Q4_0 embedding table: sample_kernel writes the next x
-    int* am = nullptr;          // [vocab][2] argmax partials of the Q4_0 lm_head launch
-    int am_parts = 0;           // partials the last forward left (0: sample from the logits)
 
     // forward_with_cache_pass over m rows whose token ids are in `tokens`, the
     // last row's logits into `logits`.  embed: x from the token ids (otherwise
@@ -617,11 +603,9 @@ struct LlamaModel {
             if (e != hipSuccess) return e;
         }
         // logits = rms_norm(x_last, norm) . Wout^T (the norm fused into the GEMV for Q4_0, Q4_K, Q6_K)
-        am_parts = 0;
         if (fused_shapes && out.type == WType::Q4_0) {
-            // with the argmax partials the sampling launch reads
-            e = launch_gemv_q4_0_argmax(out.dev, out.n, d, x + (m - 1) * d, logits, final_norm, eps, am,
-                                        (size_t)cfg.vocab, &am_parts, stream);
+            e = launch_gemv_q4_0_fused_ex(out.dev, out.n, d, x + (m - 1) * d, d, 1, logits, 1, final_norm, eps, 0,
+                                          stream);
         } else if (kquant(out)) {
             e = kq_linear(out, x + (m - 1) * d, d, 1, logits, out.n, GEMV_PRO_RMSNORM, final_norm, GEMV_EPI_STORE);
         } else {
@@ -636,8 +620,7 @@ struct LlamaModel {
     // argmax of `logits` -> token, out_tokens, step; position += advance; the
     // token's embedding row -> x (the input of the next decode step)
     void sample(int advance) {
-        hipLaunchKernelGGL(sample_kernel, dim3(1), dim3(SAMPLE_NT), 0, stream, logits, cfg.vocab,
-                           am_parts > 0 ? am : nullptr, am_parts, tokens, out_tokens,
+        hipLaunchKernelGGL(sample_kernel, dim3(1), dim3(SAMPLE_NT), 0, stream, logits, cfg.vocab, tokens, out_tokens,
                            step, pos, advance, sample_embeds ? emb.dev : nullptr, cfg.dim, x);
     }
 
@@ -869,7 +852,6 @@ rdl_status rdl_llama_create_typed(const rdl_llama_config* cfg, const int32_t* ty
     if ((e = M.alloc_t(&M.gu, mb * 2 * c.ffn_dim)) != hipSuccess) return fail_free(e);
     if ((e = M.alloc_t(&M.hb, mb * c.ffn_dim)) != hipSuccess) return fail_free(e);
     if ((e = M.alloc_t(&M.logits, c.vocab)) != hipSuccess) return fail_free(e);
-    if ((e = M.alloc_t(&M.am, 2 * (size_t)c.vocab)) != hipSuccess) return fail_free(e);
     if ((e = M.alloc_t(&M.tokens, mb)) != hipSuccess) return fail_free(e);
     if ((e = M.alloc_t(&M.pos, 1)) != hipSuccess) return fail_free(e);
     if ((e = M.alloc_t(&M.step, 1)) != hipSuccess) return fail_free(e);

@@ -203,14 +203,6 @@ hipError_t launch_gemv_q4_0_rope_kv(const uint8_t* w, size_t n, size_t k, const 
                                     const float* sin_t, void* kc, void* vc, int n_heads, int n_kv, int hd,
                                     const int* kv_table, bool kv_f16, hipStream_t s);
 
-// y[n] = W x (Q4_0, one activation row; with g: x RMS-normalized as the
-// fused prologue does) plus greedy-sampling partials: am[2 i], am[2 i + 1] =
-// bits of the largest y of workgroup i's rows and the first row holding it
-// (NaN and -inf never; {-inf, INT_MAX} when none), i < *n_parts; am holds
-// am_cap >= n pairs.  Same y as launch_gemv_q4_0_fused_ex.
-hipError_t launch_gemv_q4_0_argmax(const uint8_t* w, size_t n, size_t k, const float* x, float* y, const float* g,
-                                   float eps, int* am, size_t am_cap, int* n_parts, hipStream_t s);
-
 // launch_gemv_q4_0_rope_kv for one activation row (a decode step) with the
 // decode attention of that row in the same launch: att_out[n_heads * hd] =
 // attention over the cache positions 0 .. *pos (paged, kv_table), spans of
