@@ -119,10 +119,11 @@ rdl_status rdl_llama_kv_pages(const rdl_llama* model, size_t* page_positions, si
 rdl_status rdl_llama_set_kv_page_table(rdl_llama* model, const int32_t* table, size_t n);
 
 /* Decode steps (one row) of layers whose matrices are all Q4_0 run the
- * q/k/v projection and the attention in one launch when the cache layout
- * allows (f16 cache with head_dim 64 or 128, f32 cache with head_dim 64);
- * enable = 0 runs them as two launches (same arithmetic, same results).
- * The default is 1.  No reference counterpart: a tuning and testing switch. */
+ * q/k/v projection, the attention and the o projection in one launch when
+ * the cache layout allows (f16 cache with head_dim 64 or 128, f32 cache with
+ * head_dim 64); enable = 0 runs them as three launches (same arithmetic,
+ * same results).  The default is 1.  No reference counterpart: a tuning and
+ * testing switch. */
 rdl_status rdl_llama_set_fused_attention(rdl_llama* model, int32_t enable);
 
 /* forward_with_cache_pass over n tokens followed by cache.advance(n): the

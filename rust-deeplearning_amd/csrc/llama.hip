@@ -436,7 +436,8 @@ struct LlamaModel {
 
     // One layer through the fused Q4_0 launches (m <= 4): RMSNorm, RoPE + KV,
     // SwiGLU and the residual adds ride in the GEMV launches (prologue /
-    // epilogue of the fused GEMV): five launches.
+    // epilogue of the fused GEMV): five launches, three in a decode step
+    // (q/k/v, attention and o in one launch).
     hipError_t layer_fused(int l, size_t m) {
         const int d = cfg.dim;
         const float eps = cfg.norm_eps;

@@ -149,7 +149,7 @@ class LlamaModel:
         return int(out.value)
 
     def set_fused_attention(self, enable: bool) -> None:
-        """Decode steps' q/k/v projection and attention in one launch (default) or two."""
+        """Decode steps' q/k/v projection, attention and o projection in one launch (default) or three."""
         check(lib.rdl_llama_set_fused_attention(self._h, int(bool(enable))))
 
     def kv_pages(self):
