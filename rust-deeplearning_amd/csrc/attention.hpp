@@ -63,14 +63,20 @@ static_assert(KV_PAGE % ATT_CHUNK == 0, "an attention chunk lies in one cache pa
 
 // HD: head dim as a compile-time constant (64, 128, 256), so that all of a
 // key row's loads are issued before its dot product; 0: runtime hd.
-// A workgroup of ATT_WAVES waves covers ATT_WAVES chunks (ATT_SPAN keys):
-// wave w forms chunk w's max m_w, sum l_w and unnormalised context o_w; the
-// workgroup combines its chunks in LDS.  A row with more than ATT_SPAN keys
-// uses several workgroups, and the last of them to finish combines their
-// partials (device-scope counter, chunk order fixed: deterministic).
+// A workgroup of ATT_WAVES waves covers ATT_SPAN_WAVES chunks (ATT_SPAN
+// keys): wave w < ATT_SPAN_WAVES forms chunk w's max m_w, sum l_w and
+// unnormalised context o_w; the workgroup combines its chunks in LDS.  A row
+// with more than ATT_SPAN keys uses several workgroups, and the last of them
+// to finish combines their partials (device-scope counter, chunk order
+// fixed: deterministic).
 constexpr int ATT_WAVES = 8;
 static_assert(ATT_WAVES <= 8, "the chunk combine reduces over one 8-lane group");
-constexpr int ATT_SPAN = ATT_CHUNK * ATT_WAVES;
+// (7B decode, 128-token prompt + 256 tokens: 827 tokens/s at 8 chunks a
+// span; 815 at 4 and 786 at 2, whose cross-workgroup combine costs more than
+// the halved K/V stream per CU saves)
+constexpr int ATT_SPAN_WAVES = 8;
+static_assert(ATT_SPAN_WAVES >= 1 && ATT_SPAN_WAVES <= ATT_WAVES, "chunks a workgroup");
+constexpr int ATT_SPAN = ATT_CHUNK * ATT_SPAN_WAVES;
 
 // One step of the transposed sum of N values over N lanes (lane index c within
 // its aligned group of N <= 16): the lane keeps the half of its values
@@ -248,7 +254,7 @@ __device__ __forceinline__ void attention_body(int bx, int by, int bz, float* __
         __syncthreads();
     }
     const int p0 = z * ATT_SPAN + w * ATT_CHUNK;
-    const bool active = p0 < t;  // wave-uniform
+    const bool active = w < ATT_SPAN_WAVES && p0 < t;  // wave-uniform
     float mx = -__builtin_inff(), l = 0.0f;
     typedef KV kvv __attribute__((ext_vector_type(V)));
     if constexpr (VPRE) {
@@ -447,7 +453,7 @@ __device__ __forceinline__ void attention_body(int bx, int by, int bz, float* __
     }
     __syncthreads();
     // combine this workgroup's chunks (inactive waves carry m = -inf, l = 0)
-    const int nw = min(ATT_WAVES, (t - z * ATT_SPAN + ATT_CHUNK - 1) / ATT_CHUNK);
+    const int nw = min(ATT_SPAN_WAVES, (t - z * ATT_SPAN + ATT_CHUNK - 1) / ATT_CHUNK);
     const int nz = (t + ATT_SPAN - 1) / ATT_SPAN;
     if (nz == 1 && w * 64 >= hd) return;  // a wave with no outputs to form (whole wave)
     // lane c < nw forms chunk c's weight exp(m_c - M); the sums read the
