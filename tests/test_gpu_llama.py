@@ -62,6 +62,24 @@ def test_generate_greedy_matches_eager_steps(rq, gpu):
     assert m.generate_greedy(prompt, 12).tolist() == eager
 
 
+@pytest.mark.parametrize("kw", [dict(dim=256, n_heads=2, n_kv_heads=1, head_dim=64),
+                                dict(dim=128, n_heads=4, n_kv_heads=2, head_dim=64)])
+def test_decode_with_head_width_unlike_dim(rq, gpu, kw):
+    """n_heads * head_dim != dim: the o projection (fused into the decode
+    launch) maps the attention outputs back to dim; logits against the
+    oracle after prefill and fused decode steps."""
+    cfg = tiny_config(**kw)
+    m, ref = build(cfg, seed=77)
+    prompt = [4, 9, 16, 25, 36, 49]
+    assert_close(m.forward_with_cache(prompt), ref.forward_with_cache(prompt))
+    tok = 3
+    for _ in range(4):
+        got = m.decode_step(tok)
+        want = ref.forward_with_cache([tok])
+        assert_close(got, want)
+        tok = argmax(want)
+
+
 def test_greedy_sampling_ties_pick_the_first_maximum(rq, gpu):
     """Output rows repeat with period 37, so each maximum logit is shared by
     8-9 token ids in different workgroups of the lm_head launch: the decode
@@ -517,6 +535,8 @@ def test_paged_cache_table_errors(rq, gpu):
     (dict(kv_f16=True, dim=256, n_heads=2, n_kv_heads=1, head_dim=128), 40),  # f16, head dim 128
     (dict(kv_f16=True, dim=256, n_heads=2, n_kv_heads=1, head_dim=128, max_seq=1100, max_batch=128), 1000),
     (dict(kv_f16=False, dim=512, n_heads=8, n_kv_heads=2, head_dim=64, max_seq=700, max_batch=128), 600),
+    (dict(kv_f16=True, dim=256, n_heads=2, n_kv_heads=1, head_dim=64), 40),   # o input 128 < dim 256
+    (dict(kv_f16=False, dim=128, n_heads=4, n_kv_heads=2, head_dim=64), 40),  # o input 256 > dim 128
 ])
 def test_fused_attention_equals_two_launches(rq, gpu, kw, n_prompt):
     """Decode steps with the attention fused into the q/k/v launch give the
