@@ -487,7 +487,7 @@ __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_kernel(
 
 // ---- XCD placement ----------------------------------------------------------------------
 // MI355X deals the workgroups of a launch round-robin to its 8 XCDs (each
-// with its own L2): workgroup b runs on XCD b % 8.  The m <= 16 GEMM relies on
+// with its own L2): workgroup b runs on XCD b % 8.  The x-tile GEMM relies on
 // it to keep a strip's K-slices in one L2 (plain partial stores, read back
 // with non-temporal loads by the last slice); the probe below checks it once
 // per device (2 x CUs workgroups record their XCC id), and the kernel falls
@@ -602,7 +602,7 @@ __global__ __launch_bounds__(SK_WAVES * 64) void gemm_q4_0_skinny_kernel(
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, r = lane & 15, h = g & 1;
     const int wr = wave / C::WK, wk = wave % C::WK;
-    // LOCAL: strip st's slices on XCD st % 8 (one L2), as in the m <= 16 kernel
+    // LOCAL: strip st's slices on XCD st % 8 (one L2), as in the x-tile kernel
     int strip, ks;
     if constexpr (LOCAL) {
         const int xcd = (int)blockIdx.x % XCD_COUNT, i = (int)blockIdx.x / XCD_COUNT;
@@ -882,23 +882,24 @@ __global__ __launch_bounds__(SK_WAVES * 64) void gemm_q4_0_skinny_kernel(
     }
 }
 
-// ---- skinny GEMM for m <= 16: K-slices joined through tagged partials --------------
-// One 16-row x tile.  A workgroup of 8 waves owns 128 weight rows (a 16-row
-// tile a wave) over one K-slice of at most KB blocks; the grid is ceil(n /
-// 128) strips x S slices, S chosen for about one workgroup per CU, so each x
-// element is split by n / 128 workgroups and a workgroup streams 128 rows x
-// KB blocks of W against 16 x KB blocks of x (n = k = 4096: 36 KB of W and
-// 32 KB of x).  Per workgroup:
+// ---- x-tile GEMM for m <= 64: K-slices joined through a strip counter -----------
+// MT = ceil(m / 16) x tiles of 16 rows.  A workgroup of 8 waves owns 128
+// weight rows (a 16-row tile a wave) over one K-slice of at most KB blocks;
+// the grid is ceil(n / 128) strips x S slices, S chosen for about one
+// workgroup per CU, so each x element is split by n / 128 workgroups and a
+// workgroup streams 128 rows x KB blocks of W against 16 MT x KB blocks of x
+// (n = k = 4096, m = 16: 36 KB of W and 32 KB of x).  Per workgroup:
 //  1. every load at once: the wave's weight windows (one 12-byte window a
-//     lane and block, the B operand of the MFMA) and the x tile (8-element
+//     lane and block, the B operand of the MFMA) and the x tiles (8-element
 //     pieces, coalesced);
 //  2. x split into LDS as in the skinny kernel above (per (row, block) scale
 //     2^e, x_hi + x_lo in f16);
-//  3. per block two v_mfma_f32_16x16x32_f16 with x as the A operand, so the
-//     lane's output column is its own weight row and its block scale d is in
-//     its own window (or its partner's, l ^ 16, through a permlane swap);
-//     acc += d * 2^e * dot in f32 (4 x rows a lane);
-//  4. the S slices of a strip meet through a counter: each writes its 16 x
+//  3. per block and x tile two v_mfma_f32_16x16x32_f16 with x as the A
+//     operand, so the lane's output column is its own weight row and its
+//     block scale d is in its own window (or its partner's, l ^ 16, through a
+//     permlane swap), decoded once for all tiles; acc += d * 2^e * dot in f32
+//     (4 x rows a lane and tile);
+//  4. the S slices of a strip meet through a counter: each writes its 16 MT x
 //     128 partial, waits for the stores, counts itself on the strip's counter,
 //     and the last of the S adds all partials in slice order (the same bits
 //     whichever finishes last), resets the counter and stores Y.  Where the
@@ -908,28 +909,34 @@ __global__ __launch_bounds__(SK_WAVES * 64) void gemm_q4_0_skinny_kernel(
 //     non-temporal loads, which do not return a stale L1 line; measured at M =
 //     16, the partial stores and their reads took 2.4 + 3.7 us as agent-coherent
 //     (write-through) traffic.  Elsewhere agent-coherent stores and loads.
-constexpr int SK16_WAVES = 8;
-constexpr int SK16_ROWS = 16 * SK16_WAVES;  // weight rows per workgroup
-constexpr int SK16_UNITS = SK16_WAVES * 64;  // f32x4 partial units per workgroup (16 x rows x 128 weight rows)
+// Against the skinny kernel above (M = 32 / 48 / 64: 74 / 95 / 107 TFLOP/s)
+// this shape runs 80 / 99 / 113; the skinny kernel remains for calls that
+// give no partial buffer and a slice longer than the LDS allows.
+constexpr int XT_WAVES = 8;
+constexpr int XT_ROWS = 16 * XT_WAVES;  // weight rows per workgroup
+constexpr int XT_UNITS = XT_WAVES * 64;  // f32x4 partial units per workgroup and x tile (16 x rows x 128 weight rows)
 
-template <int KB>
-struct Sk16Cfg {
-    static constexpr int NT = SK16_WAVES * 64;
+template <int KB, int MT>
+struct XtCfg {
+    static constexpr int NT = XT_WAVES * 64;
+    static constexpr int XR = 16 * MT;                 // x rows (MT tiles of 16)
     static constexpr int XROW = KB * 64 + 16;          // LDS bytes per x row of f16 (padded)
-    static constexpr int X_BYTES = 16 * XROW;
-    static constexpr int SC_BYTES = KB * 16 * 4;       // block scales [block][x row]
+    static constexpr int X_BYTES = XR * XROW;
+    static constexpr int SC_BYTES = KB * XR * 4;       // block scales [block][x row]
     static constexpr int LDS = 2 * X_BYTES + SC_BYTES;
-    static constexpr int XU = (16 * KB * 4 + NT - 1) / NT;  // 8-element x pieces per thread
-    static_assert(XU <= 4, "x pieces held in registers");
+    static constexpr int XU = (XR * KB * 4 + NT - 1) / NT;  // 8-element x pieces per thread
+    static constexpr int UNITS = XT_UNITS * MT;      // f32x4 partial units per workgroup
+    static_assert(XU <= 8, "x pieces held in registers");
 };
 
 // EVEN: nb and the slice length even, so every slice's first block starts on a
 // dword and a lane's weight windows sit at fixed offsets from one base.
-template <int KB, bool EVEN, bool LOCAL>
-__global__ __launch_bounds__(SK16_WAVES * 64) void gemm_q4_0_sk16_kernel(
+template <int KB, int MT, bool EVEN, bool LOCAL>
+__global__ __launch_bounds__(XT_WAVES * 64) void gemm_q4_0_xtile_kernel(
     const uint8_t* __restrict__ W, int n, int nb, const float* __restrict__ X, int m, float* __restrict__ Y, int S,
     int kbs, float* __restrict__ part, int* __restrict__ cnt) {
-    using C = Sk16Cfg<KB>;
+    using C = XtCfg<KB, MT>;
+    constexpr int XR = C::XR, UNITS = C::UNITS;
     __shared__ int last_sh;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     uint8_t* xh_s = lds;
@@ -948,14 +955,14 @@ __global__ __launch_bounds__(SK16_WAVES * 64) void gemm_q4_0_sk16_kernel(
         strip = (int)blockIdx.x / S;
         ks = (int)blockIdx.x % S;
     }
-    if (strip * SK16_ROWS >= n) return;  // grid rounded up to whole XCD rounds (whole workgroup)
+    if (strip * XT_ROWS >= n) return;  // grid rounded up to whole XCD rounds (whole workgroup)
     const int kb0 = min(nb, ks * kbs), kb1 = min(nb, kb0 + kbs);
     const uint32_t k = (uint32_t)nb * 32u;
     const uint32_t row_bytes = (uint32_t)nb * 18u;
     const uint32_t wbytes = (uint32_t)n * row_bytes;
     const __amdgpu_buffer_rsrc_t wrs = make_rsrc(W, wbytes);
     const __amdgpu_buffer_rsrc_t xrs = make_rsrc(X, (uint32_t)m * k * 4u);
-    const int j = strip * SK16_ROWS + wave * 16 + r;  // the lane's weight row (output column)
+    const int j = strip * XT_ROWS + wave * 16 + r;  // the lane's weight row (output column)
 
     // 1. loads: x pieces first, then the weight windows
     u32x4 xa[C::XU], xb[C::XU];
@@ -964,7 +971,7 @@ __global__ __launch_bounds__(SK16_WAVES * 64) void gemm_q4_0_sk16_kernel(
         const int idx = tid + u * C::NT;
         const int row = idx / (KB * 4), blk = (idx >> 2) % KB, qt = idx & 3;
         const int b = kb0 + blk;
-        const uint32_t off = (idx < 16 * KB * 4 && row < m && b < kb1)
+        const uint32_t off = (idx < XR * KB * 4 && row < m && b < kb1)
                                  ? ((uint32_t)row * k + (uint32_t)b * 32u + (uint32_t)qt * 8u) * 4u
                                  : RSRC_OOB;
         xa[u] = buf_load_b128(xrs, off);
@@ -1023,16 +1030,19 @@ __global__ __launch_bounds__(SK16_WAVES * 64) void gemm_q4_0_sk16_kernel(
             hw[e / 2] = __builtin_bit_cast(uint32_t, hp);
             lw[e / 2] = fin ? __builtin_bit_cast(uint32_t, lp) : 0u;
         }
-        if (idx < 16 * KB * 4) {
+        if (idx < XR * KB * 4) {
             *reinterpret_cast<u32x4*>(xh_s + row * C::XROW + blk * 64 + qt * 16) = u32x4{hw[0], hw[1], hw[2], hw[3]};
             *reinterpret_cast<u32x4*>(xl_s + row * C::XROW + blk * 64 + qt * 16) = u32x4{lw[0], lw[1], lw[2], lw[3]};
-            if (qt == 0) sc_s[blk * 16 + row] = ldexpf(1.0f, ex);
+            if (qt == 0) sc_s[blk * XR + row] = ldexpf(1.0f, ex);
         }
     }
     __syncthreads();
 
-    // 3. products: lane (g, r) holds Y[x rows 4g .. 4g + 3][weight row j]
-    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    // 3. products: lane (g, r) holds Y[x rows 16 t + 4g .. + 3][weight row j]
+    // for each x tile t
+    f32x4 acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; t++) acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int q = 0; q < KB; q++) {
         const int b = kb0 + q;
@@ -1048,26 +1058,31 @@ __global__ __launch_bounds__(SK16_WAVES * 64) void gemm_q4_0_sk16_kernel(
         const uint32_t other = (sw[0] == dbits) ? sw[1] : sw[0];
         const uint32_t dsel = h ? other : dbits;
         const float d = (b < kb1) ? h2f(dsel) : 0.0f;
-        const int xo = r * C::XROW + q * 64 + g * 16;
-        const half8_t ah = *reinterpret_cast<const half8_t*>(xh_s + xo);
-        const half8_t al = *reinterpret_cast<const half8_t*>(xl_s + xo);
-        const f32x4 s4 = *reinterpret_cast<const f32x4*>(sc_s + q * 16 + 4 * g);
-        const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
-        f32x4 cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bq, z, 0, 0, 0);
-        cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bq, cc, 0, 0, 0);
 #pragma unroll
-        for (int u = 0; u < 4; u++) acc[u] = fmaf(d * s4[u], cc[u], acc[u]);
+        for (int t = 0; t < MT; t++) {
+            const int xo = (16 * t + r) * C::XROW + q * 64 + g * 16;
+            const half8_t ah = *reinterpret_cast<const half8_t*>(xh_s + xo);
+            const half8_t al = *reinterpret_cast<const half8_t*>(xl_s + xo);
+            const f32x4 s4 = *reinterpret_cast<const f32x4*>(sc_s + q * XR + 16 * t + 4 * g);
+            const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+            f32x4 cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bq, z, 0, 0, 0);
+            cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bq, cc, 0, 0, 0);
+#pragma unroll
+            for (int u = 0; u < 4; u++) acc[t][u] = fmaf(d * s4[u], cc[u], acc[t][u]);
+        }
     }
 
     // 4. slices of the strip: partials, counter, the last one adds them
     if (S > 1) {
         // the strip's partials: LOCAL into this XCD's L2 (plain stores), else
         // written through to the device's coherence point (sc1)
-        const __amdgpu_buffer_rsrc_t prs = make_rsrc(part + (size_t)strip * S * SK16_UNITS * 4,
-                                                     (uint32_t)S * SK16_UNITS * 16u);
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc), prs,
-                                               (int)(((uint32_t)ks * SK16_UNITS + tid) * 16u), 0,
-                                               LOCAL ? 0 : CPOL_SC1);
+        const __amdgpu_buffer_rsrc_t prs = make_rsrc(part + (size_t)strip * S * UNITS * 4,
+                                                     (uint32_t)S * UNITS * 16u);
+#pragma unroll
+        for (int t = 0; t < MT; t++)
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[t]), prs,
+                                                   (int)(((uint32_t)ks * UNITS + t * XT_UNITS + tid) * 16u), 0,
+                                                   LOCAL ? 0 : CPOL_SC1);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partial has completed
         __syncthreads();
         if (tid == 0) {
@@ -1086,62 +1101,71 @@ __global__ __launch_bounds__(SK16_WAVES * 64) void gemm_q4_0_sk16_kernel(
         // every slice's partial in flight together (groups of 8, branch-free:
         // slots past S or of this slice read zeros), then added in slice order;
         // LOCAL reads the L2 with non-temporal loads (no stale L1 line), else sc1
-        f32x4 tot = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int s0 = 0; s0 < S; s0 += 8) {
-            f32x4 v[8];
 #pragma unroll
-            for (int q = 0; q < 8; q++) {
-                const int sl = s0 + q;
-                const uint32_t off = (sl < S && sl != ks) ? ((uint32_t)sl * SK16_UNITS + tid) * 16u : RSRC_OOB;
-                v[q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(prs, (int)off, 0,
-                                                                                        LOCAL ? CPOL_NT : CPOL_SC1));
-            }
+        for (int t = 0; t < MT; t++) {
+            f32x4 tot = {0.0f, 0.0f, 0.0f, 0.0f};
+            for (int s0 = 0; s0 < S; s0 += 8) {
+                f32x4 v[8];
 #pragma unroll
-            for (int q = 0; q < 8; q++) {
-                const int sl = s0 + q;
-                const f32x4 t = sl == ks ? acc : v[q];
-                if (sl < S) tot = sl == 0 ? t : tot + t;
+                for (int q = 0; q < 8; q++) {
+                    const int sl = s0 + q;
+                    const uint32_t off =
+                        (sl < S && sl != ks) ? ((uint32_t)sl * UNITS + t * XT_UNITS + tid) * 16u : RSRC_OOB;
+                    v[q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(prs, (int)off, 0,
+                                                                                            LOCAL ? CPOL_NT : CPOL_SC1));
+                }
+#pragma unroll
+                for (int q = 0; q < 8; q++) {
+                    const int sl = s0 + q;
+                    const f32x4 tv = sl == ks ? acc[t] : v[q];
+                    if (sl < S) tot = sl == 0 ? tv : tot + tv;
+                }
             }
+            acc[t] = tot;
         }
-        acc = tot;
     }
     if (j < n) {
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int i = 4 * g + u;
-            if (i < m) Y[(size_t)i * n + j] = acc[u];
-        }
+        for (int t = 0; t < MT; t++)
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int i = 16 * t + 4 * g + u;
+                if (i < m) Y[(size_t)i * n + j] = acc[t][u];
+            }
     }
 }
 
-// Launch plan of the m <= 16 kernel: 128-row strips, S K-slices of kbs
+// Launch plan of the x-tile kernel: 128-row strips, S K-slices of kbs
 // blocks (even when nb is) for about one workgroup per CU, KB the template
-// bound of kbs (8, 16 or 32).  ok = false (the other kernel runs) when a
-// slice would exceed 32 blocks.
-struct Sk16Plan {
+// bound of kbs (8, 16 or 32; at most 16 with more than one x tile, for the
+// LDS).  ok = false (the skinny kernel runs) when a slice would exceed that.
+struct XtPlan {
     int strips, S, kbs, KB;
     bool even, ok;
 };
-inline Sk16Plan sk16_plan(size_t n, int nb) {
-    Sk16Plan p{};
-    p.strips = (int)((n + SK16_ROWS - 1) / SK16_ROWS);
+inline XtPlan xtile_plan(size_t n, int nb, int mt = 1) {
+    // LDS per workgroup: 2 * 16 mt * (64 KB + 16) + 64 KB mt bytes; at most 16
+    // blocks a slice when mt > 1
+    const int kmax = mt > 1 ? 16 : 32;
+    XtPlan p{};
+    p.strips = (int)((n + XT_ROWS - 1) / XT_ROWS);
     const int S = std::max(1, (device_cu_count() + p.strips / 2) / p.strips);
     p.kbs = std::max(1, (nb + S - 1) / S);
-    p.kbs = std::min(p.kbs, 32);
+    p.kbs = std::min(p.kbs, kmax);
     p.even = nb % 2 == 0;
     if (p.even) p.kbs += p.kbs & 1;
     p.S = std::max(1, (nb + p.kbs - 1) / p.kbs);  // no empty slices
     p.KB = p.kbs <= 8 ? 8 : p.kbs <= 16 ? 16 : 32;
-    p.ok = p.kbs <= 32;
+    p.ok = p.kbs <= kmax;
     return p;
 }
 
-template <int KB, bool EVEN, bool LOCAL>
-hipError_t launch_sk16_cfg(const uint8_t* w, int n, int nb, const float* x, int m, float* y, const Sk16Plan& p,
+template <int KB, int MT, bool EVEN, bool LOCAL>
+hipError_t launch_xtile_cfg(const uint8_t* w, int n, int nb, const float* x, int m, float* y, const XtPlan& p,
                            float* part, int* cnt, hipStream_t s) {
-    using C = Sk16Cfg<KB>;
+    using C = XtCfg<KB, MT>;
     static_assert(C::LDS <= 160 * 1024, "LDS per workgroup");
-    auto kern = gemm_q4_0_sk16_kernel<KB, EVEN, LOCAL>;
+    auto kern = gemm_q4_0_xtile_kernel<KB, MT, EVEN, LOCAL>;
     if (C::LDS > 65536) {
         static const hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                                         C::LDS);  // once per kernel and process
@@ -1153,30 +1177,48 @@ hipError_t launch_sk16_cfg(const uint8_t* w, int n, int nb, const float* x, int 
     return hipGetLastError();
 }
 
-hipError_t launch_sk16(const uint8_t* w, int n, int nb, const float* x, int m, float* y, float* part, int* cnt,
+hipError_t launch_xtile(const uint8_t* w, int n, int nb, const float* x, int m, float* y, float* part, int* cnt,
                        hipStream_t s) {
-    Sk16Plan p = sk16_plan((size_t)n, nb);
+    const int mt = (m + 15) / 16;
+    if (mt < 1 || mt > 4) return hipErrorInvalidValue;
+    XtPlan p = xtile_plan((size_t)n, nb, mt);
     if (!part || !cnt) {  // no partial buffer or counters: one slice
         p.S = 1;
         p.kbs = nb;
         p.KB = nb <= 8 ? 8 : nb <= 16 ? 16 : 32;
-        p.ok = nb <= 32;
+        p.ok = nb <= (mt > 1 ? 16 : 32);
     }
     if (!p.ok) return hipErrorInvalidValue;  // the caller takes the other kernel
     const bool local = p.S > 1 && xcd_round_robin(s);
-    auto go = [&](auto kb_tag, auto even_tag) {
-        constexpr int KB = decltype(kb_tag)::value;
+    auto go = [&](auto kb_tag, auto mt_tag, auto even_tag) {
+        constexpr int KB = decltype(kb_tag)::value, MT = decltype(mt_tag)::value;
         constexpr bool EVEN = decltype(even_tag)::value;
-        return local ? launch_sk16_cfg<KB, EVEN, true>(w, n, nb, x, m, y, p, part, cnt, s)
-                     : launch_sk16_cfg<KB, EVEN, false>(w, n, nb, x, m, y, p, part, cnt, s);
+        return local ? launch_xtile_cfg<KB, MT, EVEN, true>(w, n, nb, x, m, y, p, part, cnt, s)
+                     : launch_xtile_cfg<KB, MT, EVEN, false>(w, n, nb, x, m, y, p, part, cnt, s);
     };
     using T = std::true_type;
     using F = std::false_type;
     using K8 = std::integral_constant<int, 8>;
     using K16 = std::integral_constant<int, 16>;
     using K32 = std::integral_constant<int, 32>;
-    if (p.even) return p.KB == 8 ? go(K8{}, T{}) : p.KB == 16 ? go(K16{}, T{}) : go(K32{}, T{});
-    return p.KB == 8 ? go(K8{}, F{}) : p.KB == 16 ? go(K16{}, F{}) : go(K32{}, F{});
+    auto by_kb = [&](auto mt_tag, auto even_tag) {
+        constexpr int MT = decltype(mt_tag)::value;
+        if constexpr (MT == 1) {
+            return p.KB == 8 ? go(K8{}, mt_tag, even_tag) : p.KB == 16 ? go(K16{}, mt_tag, even_tag)
+                                                                        : go(K32{}, mt_tag, even_tag);
+        } else {
+            return p.KB == 8 ? go(K8{}, mt_tag, even_tag) : go(K16{}, mt_tag, even_tag);
+        }
+    };
+    auto by_mt = [&](auto even_tag) {
+        switch (mt) {
+            case 1: return by_kb(std::integral_constant<int, 1>{}, even_tag);
+            case 2: return by_kb(std::integral_constant<int, 2>{}, even_tag);
+            case 3: return by_kb(std::integral_constant<int, 3>{}, even_tag);
+            default: return by_kb(std::integral_constant<int, 4>{}, even_tag);
+        }
+    };
+    return p.even ? by_mt(T{}) : by_mt(F{});
 }
 
 // Launch plan of the skinny GEMM for (m, n, nb): the template shape by m, the
@@ -1295,9 +1337,10 @@ hipError_t launch_zero_counters(int* counters, size_t count, hipStream_t s) {
 size_t gemm_counter_count(size_t n, size_t) { return (n + 63) / 64 + 1; }  // a counter per strip of 64 (or 128) rows
 
 size_t gemm_scratch_bytes(size_t m, size_t n, size_t k, bool native) {
-    if (!native && m <= GEMM_SK16_M) {  // the K-slice partials of the m <= 16 kernel
-        const Sk16Plan p = sk16_plan(n, (int)(k / QK));
-        if (p.ok) return p.S > 1 ? ((size_t)p.strips * p.S * SK16_UNITS * 16 + 255) & ~(size_t)255 : 0;
+    if (!native && m >= 1 && m <= GEMM_XTILE_M) {  // the K-slice partials of the x-tile kernel
+        const int mt = (int)((m + 15) / 16);
+        const XtPlan p = xtile_plan(n, (int)(k / QK), mt);
+        if (p.ok) return p.S > 1 ? ((size_t)p.strips * p.S * XT_UNITS * mt * 16 + 255) & ~(size_t)255 : 0;
     }
     if (!native && m <= GEMM_SMALL_M) {  // the K-slice partials of the skinny GEMM
         if (m == 0 || n == 0) return 0;
@@ -1314,9 +1357,9 @@ size_t gemm_scratch_bytes(size_t m, size_t n, size_t k, bool native) {
 hipError_t launch_gemm_q4_0(const uint8_t* w, size_t n, size_t k, const float* x, size_t m, float* y,
                             void* scratch, int* counters, hipStream_t s) {
     if (n == 0 || m == 0) return hipSuccess;
-    if (m <= GEMM_SK16_M) {
+    if (m <= GEMM_XTILE_M) {
         float* part = reinterpret_cast<float*>(scratch);  // the K-slice partials
-        const hipError_t e = launch_sk16(w, (int)n, (int)(k / QK), x, (int)m, y, part, counters, s);
+        const hipError_t e = launch_xtile(w, (int)n, (int)(k / QK), x, (int)m, y, part, counters, s);
         if (e != hipErrorInvalidValue) return e;
     }
     if (m <= GEMM_SMALL_M) {

@@ -163,7 +163,7 @@ int device_cu_count();
 // bytes of scratch; partials != NULL writes the int32 block dots to
 // partials[(i * n + j) * (k / 32) + b] instead of y.
 constexpr size_t GEMM_SMALL_M = 64;
-constexpr size_t GEMM_SK16_M = 16;  // float products of at most this many rows: one x tile, 128-row strips
+constexpr size_t GEMM_XTILE_M = 64;  // float products of at most this many rows: x tiles as MFMA A operands, 128-row strips
 size_t gemm_scratch_bytes(size_t m, size_t n, size_t k, bool native);
 // ints of the GEMM's strip counters for out_features n, in_features k
 size_t gemm_counter_count(size_t n, size_t k);

@@ -89,7 +89,7 @@ def test_nan_row_stays_in_its_row(rq, gpu):
     assert np.all(np.isfinite(np.delete(y, 6, axis=0)))
 
 
-# small M (m <= 64): the direct-load kernel that splits x per block itself
+# small M (m <= 64): the x-tile kernel that splits x per block itself
 @pytest.mark.parametrize("m,n,k", [(5, 16, 256), (15, 33, 1024), (16, 4096, 4096), (17, 48, 4128),
                                    (31, 7, 96), (32, 256, 4096), (48, 100, 2080), (63, 130, 1056),
                                    (64, 4096, 4096), (20, 16400, 256)])

@@ -14,7 +14,8 @@ pytestmark = pytest.mark.gpu
 
 @pytest.mark.parametrize("dtype,mode,n,k,rows", [
     (2, 0, 4096, 4096, (96, 40)),    # Q4_0 float: matrix-core GEMM, x split in scratch
-    (2, 0, 4096, 4096, (16, 5)),     # Q4_0 float, m <= 16: K-slice partials in scratch
+    (2, 0, 4096, 4096, (16, 5)),     # Q4_0 float, one x tile: K-slice partials in scratch
+    (2, 0, 4096, 4096, (64, 33)),    # Q4_0 float, four then three x tiles
     (2, 1, 4096, 4096, (24, 6)),     # Q4_0 native: Q8_0 records in scratch
     (3, 1, 1000, 2048, (9, 5)),      # Q4_1 native records
     (8, 0, 512, 1024, (33, 7)),      # Q8_0 float records
