@@ -28,6 +28,12 @@ def test_config4_prefill(rq, orc, gpu, m):
     run(rq, orc, m, 4096, 4096, 0x5EED0004 + m)
 
 
+def test_prefill_chunk_of_a_tall_matrix(rq, orc, gpu):
+    # 128 rows against 16512 weight rows: the 128 x 64 tiles fill the CUs
+    # (the prefill chunk's gate/up shape, narrower K)
+    run(rq, orc, 128, 16512, 256, 0x5EED0128)
+
+
 def test_config4_prefill_2048_sampled_rows(rq, orc, gpu):
     # each output row depends only on its x row: check 48 spread rows, all tiles
     rows = np.unique(np.linspace(0, 2047, 48).astype(int))
