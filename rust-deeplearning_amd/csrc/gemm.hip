@@ -1319,8 +1319,18 @@ hipError_t launch_tiles(const uint8_t* w, int n, int nb, const void* x0, const v
         if (m >= 256 || (m >= 128 && (size_t)((n + 127) / 128) * ((m + 63) / 64) >= (size_t)cus))
             return launch_cfg<NATIVE, DUMP, 4, 2, 2, 2, 2, 2>(w, n, nb, x0, x1, xe, m, y, p, s);
     }
-    if (m >= 48 && (size_t)((n + 31) / 32) * ((m + 63) / 64) >= (size_t)cus)
+    const size_t t32 = (size_t)((n + 31) / 32) * ((m + 63) / 64);  // 32 x 64 tiles
+    if (m >= 48 && t32 >= (size_t)cus) {
+        if constexpr (!NATIVE) {
+            // 8 waves a tile; 64 x 64 tiles when 32-row ones overflow a round
+            // (us at 128 rows, 4096 x 4096 / 4096 x 14336 / 6144 x 4096: 4-wave
+            // 32 x 64 tiles 37.2 / 106.5 / 66.0, 8-wave 30.3 / 89.1 / 51.5,
+            // 64 x 64 38.7 / 112.9 / 40.0)
+            if (t32 > (size_t)cus) return launch_cfg<NATIVE, DUMP, 2, 4, 2, 1, 4, 2>(w, n, nb, x0, x1, xe, m, y, p, s);
+            return launch_cfg<NATIVE, DUMP, 2, 2, 1, 2, 4, 2>(w, n, nb, x0, x1, xe, m, y, p, s);
+        }
         return launch_cfg<NATIVE, DUMP, 2, 4, 1, 1, 4, 2>(w, n, nb, x0, x1, xe, m, y, p, s);
+    }
     if (m > 16) return launch_cfg<NATIVE, DUMP, 1, 2, 1, 1, 4, 2>(w, n, nb, x0, x1, xe, m, y, p, s);
     return launch_cfg<NATIVE, DUMP, 1, 1, 1, 1, 4, 8>(w, n, nb, x0, x1, xe, m, y, p, s);
 }

@@ -34,6 +34,13 @@ def test_prefill_chunk_of_a_tall_matrix(rq, orc, gpu):
     run(rq, orc, 128, 16512, 256, 0x5EED0128)
 
 
+@pytest.mark.parametrize("n,k", [(4096, 4096), (6144, 1024), (200, 2080)])
+def test_prefill_chunk_tile_shapes(rq, orc, gpu, n, k):
+    # 128 rows: 8-wave 32 x 64 tiles (one round), 64 x 64 tiles (32-row
+    # tiles overflow a round), and a matrix too small for either
+    run(rq, orc, 128, n, k, 0x5EED0200 + n)
+
+
 def test_config4_prefill_2048_sampled_rows(rq, orc, gpu):
     # each output row depends only on its x row: check 48 spread rows, all tiles
     rows = np.unique(np.linspace(0, 2047, 48).astype(int))
