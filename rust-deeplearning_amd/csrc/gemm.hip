@@ -1313,9 +1313,13 @@ hipError_t launch_tiles(const uint8_t* w, int n, int nb, const void* x0, const v
         if (m >= 256) return launch_cfg<NATIVE, DUMP, 2, 4, 2, 2, 2, 2>(w, n, nb, x0, x1, xe, m, y, p, s);
     } else {
         if (m >= 1024) return launch_cfg<NATIVE, DUMP, 4, 4, 2, 2, 2, 1>(w, n, nb, x0, x1, xe, m, y, p, s);
-        // 128 x 64 tiles from m = 256, and from m = 128 where they alone fill
-        // the CUs (the 7B prefill's 28672-row gate/up GEMM at 128 rows:
-        // prefill 15.7 -> 12.3 ms; taken for every matrix: 14.9 ms)
+        // 128 x 128 tiles from m = 128 where they fill three quarters of
+        // the CUs (the 7B prefill's 28672-row gate/up GEMM at 128 rows: 224
+        // tiles, 110 us against 119 us in 128 x 64 tiles); 128 x 64 tiles from
+        // m = 256, and from m = 128 where they alone fill the CUs (prefill
+        // 15.7 -> 12.3 ms; taken for every matrix: 14.9 ms)
+        if (m >= 128 && m < 256 && 4 * (size_t)((n + 127) / 128) * ((m + 127) / 128) >= 3 * (size_t)cus)
+            return launch_cfg<NATIVE, DUMP, 4, 4, 2, 2, 2, 1>(w, n, nb, x0, x1, xe, m, y, p, s);
         if (m >= 256 || (m >= 128 && (size_t)((n + 127) / 128) * ((m + 63) / 64) >= (size_t)cus))
             return launch_cfg<NATIVE, DUMP, 4, 2, 2, 2, 2, 2>(w, n, nb, x0, x1, xe, m, y, p, s);
     }

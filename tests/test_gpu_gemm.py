@@ -34,10 +34,11 @@ def test_prefill_chunk_of_a_tall_matrix(rq, orc, gpu):
     run(rq, orc, 128, 16512, 256, 0x5EED0128)
 
 
-@pytest.mark.parametrize("n,k", [(4096, 4096), (6144, 1024), (200, 2080)])
+@pytest.mark.parametrize("n,k", [(4096, 4096), (6144, 1024), (200, 2080), (24640, 256)])
 def test_prefill_chunk_tile_shapes(rq, orc, gpu, n, k):
     # 128 rows: 8-wave 32 x 64 tiles (one round), 64 x 64 tiles (32-row
-    # tiles overflow a round), and a matrix too small for either
+    # tiles overflow a round), a matrix too small for either, and 128 x 128
+    # tiles (the gate/up shape)
     run(rq, orc, 128, n, k, 0x5EED0200 + n)
 
 
