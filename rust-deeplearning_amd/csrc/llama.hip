@@ -130,6 +130,81 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attention_kernel(AttArgs<KV> a
     attention_body<KV, HD, false>(blockIdx.x, blockIdx.y, blockIdx.z, sm, a);
 }
 
+// rows and cache pages (keys / 64) where a prompt chunk takes the kernel below
+constexpr size_t PREFILL_ATT_MIN_ROWS = 8, PREFILL_ATT_MAX_PAGES = 8;
+
+// Attention of a prompt chunk (m > 1 rows at positions *pos .. *pos + m - 1,
+// keys already in the cache): one wave a query row, 8 consecutive rows of one
+// head a workgroup, so the workgroup's waves read the same cache pages (one
+// L2 fetch a page, then L1).  A wave walks its row's keys a page (64 keys) at
+// a time: lane j scores key p0 + j (q from LDS, broadcast), then the page's
+// max, an online rescale of the running (max M, sum L, context o) and the
+// weighted V rows, lane l owning dims HD / 64 * l ..; at the end o / L.  The
+// same f32 arithmetic as attention_kernel per term (scores / sqrt(hd),
+// exp(score - max), attention.rs:414-441); the running max replaces the
+// chunk combine, so sums round in another order.
+template <typename KV, int HD>
+__global__ __launch_bounds__(512) void prefill_attention_kernel(AttArgs<KV> a, int m) {
+    static_assert(HD % 64 == 0 && HD <= 256, "head dims a lane");
+    constexpr int DPL = HD / 64;
+    constexpr int V = 16 / (int)sizeof(KV);  // cache elements a 16-byte load
+    typedef KV kvv __attribute__((ext_vector_type(V)));
+    __shared__ __attribute__((aligned(16))) float qsh[8][HD];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int n_heads = a.n_heads, n_kv = a.n_kv, G = n_heads / n_kv;
+    // the G query heads of a KV head on one XCD (block b on XCD b % 8)
+    const int h = ((int)blockIdx.x % n_kv) * G + (int)blockIdx.x / n_kv;
+    const int kvh = h / G;
+    const int s = (int)blockIdx.y * 8 + w;
+    if (s >= m) return;  // whole wave; no workgroup barrier below
+    const float* q = a.qkv + (size_t)s * a.qkv_dim + (size_t)h * HD;
+#pragma unroll
+    for (int c = 0; c < DPL; c++) qsh[w][lane + 64 * c] = q[lane + 64 * c];
+    __builtin_amdgcn_wave_barrier();
+    const int t = *a.pos_dev + s + 1;  // keys 0 .. t - 1
+    float M = -__builtin_inff(), L = 0.0f, o[DPL];
+#pragma unroll
+    for (int c = 0; c < DPL; c++) o[c] = 0.0f;
+    for (int p0 = 0; p0 < t; p0 += KV_PAGE) {
+        const int nvalid = min(KV_PAGE, t - p0);
+        const size_t page = kv_row(a.kv_table, n_kv, kvh, p0, HD);
+        const KV* kb = a.kc + page;
+        const KV* vb = a.vc + page;
+        // score of key p0 + lane (a key past the row re-reads the last one)
+        const KV* kr = kb + (size_t)min(lane, nvalid - 1) * HD;
+        kvv kreg[HD / V];
+#pragma unroll
+        for (int i = 0; i < HD / V; i++) kreg[i] = *reinterpret_cast<const kvv*>(kr + i * V);
+        float acc = 0.0f;
+#pragma unroll
+        for (int i = 0; i < HD / V; i++)
+#pragma unroll
+            for (int e = 0; e < V; e++) acc += qsh[w][i * V + e] * (float)kreg[i][e];
+        const bool valid = lane < nvalid;
+        const float sc = valid ? acc / a.scale : -__builtin_inff();
+        const float Mn = fmaxf(M, wave_max(sc));
+        const float corr = expf(M - Mn);  // 0 on the first page
+        const float e = valid ? expf(sc - Mn) : 0.0f;
+        L = L * corr + wave_sum(e);
+#pragma unroll
+        for (int c = 0; c < DPL; c++) o[c] *= corr;
+        // weighted V rows, branch-free: rows past the row's keys re-read the
+        // last valid one with weight 0
+#pragma unroll
+        for (int j = 0; j < KV_PAGE; j++) {
+            const float ej = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e), j));
+            const KV* vr = vb + (size_t)min(j, nvalid - 1) * HD + DPL * lane;
+#pragma unroll
+            for (int c = 0; c < DPL; c++) o[c] += ej * (float)vr[c];
+        }
+        M = Mn;
+    }
+    float* out = a.out + (size_t)s * n_heads * HD + (size_t)h * HD + DPL * lane;
+    const float invL = 1.0f / L;
+#pragma unroll
+    for (int c = 0; c < DPL; c++) out[c] = o[c] * invL;
+}
+
 // x += y (Tensor::add_inplace, ops.rs:276-289)
 __global__ void add_kernel(float* __restrict__ x, const float* __restrict__ y, size_t n) {
     const size_t i = (size_t)blockIdx.x * NT + threadIdx.x;
@@ -406,6 +481,28 @@ struct LlamaModel {
                                stream, qkv, qkv_dim, pos, cos_t, sin_t, cfg.n_heads, cfg.n_kv_heads, hd, kcl, vcl,
                                kv_table);
         const float scale = sqrtf((float)hd);
+        // a prompt chunk whose rows see few pages: a wave a row
+        const size_t pages = (host_pos + m + KV_PAGE - 1) / KV_PAGE;
+        if (m >= PREFILL_ATT_MIN_ROWS && pages <= PREFILL_ATT_MAX_PAGES && !capture_any_pos &&
+            (hd == 64 || hd == 128 || hd == 256)) {
+            AttArgs<KV> pa{};
+            pa.qkv = qkv;
+            pa.qkv_dim = qkv_dim;
+            pa.pos_dev = pos;
+            pa.kc = kcl;
+            pa.vc = vcl;
+            pa.kv_table = kv_table;
+            pa.n_heads = cfg.n_heads;
+            pa.n_kv = cfg.n_kv_heads;
+            pa.hd_rt = hd;
+            pa.scale = scale;
+            pa.out = att;
+            auto pk = (hd == 128) ? prefill_attention_kernel<KV, 128>
+                    : (hd == 64)  ? prefill_attention_kernel<KV, 64>
+                                  : prefill_attention_kernel<KV, 256>;
+            hipLaunchKernelGGL(pk, dim3(cfg.n_heads, (unsigned)((m + 7) / 8)), dim3(512), 0, stream, pa, (int)m);
+            return hipGetLastError();
+        }
         // chunks that can hold keys for these rows (every chunk of the cache
         // when the launch is captured for replay at any position)
         const int nz = chunks_needed(m);

@@ -223,6 +223,34 @@ def test_long_context_spans(rq, gpu, kw):
         assert gen.tolist() == want_toks
 
 
+@pytest.mark.parametrize("kw,chunks", [
+    (dict(kv_f16=False), [8]),                                     # one group of 8 rows, one page
+    (dict(kv_f16=True), [9, 70]),                                  # a ragged group; rows crossing a page
+    (dict(kv_f16=False, dim=256, n_heads=2, n_kv_heads=1, head_dim=128), [77, 3, 40]),  # 3 rows: per-row kernel
+    (dict(kv_f16=True, dim=256, n_heads=2, n_kv_heads=1, head_dim=128), [128, 128]),
+    (dict(kv_f16=False, dim=256, n_heads=1, n_kv_heads=1, head_dim=256), [33, 31]),   # head dim 256
+    (dict(kv_f16=False, dim=384, n_heads=6, n_kv_heads=2), [128] * 5),  # past 512 keys: per-row kernel
+])
+def test_prefill_attention_chunks(rq, gpu, kw, chunks):
+    """Prompt chunks whose rows see at most 8 cache pages take the kernel
+    with a wave a row; the rest, and chunks under 8 rows, take the per-row
+    kernel.  Every chunk's logits against the oracle."""
+    cfg = tiny_config(max_seq=700, max_batch=128, **kw)
+    print(f"case prefill chunks {kw} {chunks}", flush=True)
+    m, ref = build(cfg, seed=5)
+    prompt = np.random.default_rng(3).integers(0, cfg.vocab, sum(chunks))
+    c0 = 0
+    for n in chunks:
+        got = m.forward_with_cache(prompt[c0:c0 + n])
+        want = ref.forward_with_cache(prompt[c0:c0 + n])
+        c0 += n
+        if kw["kv_f16"]:  # the f16 cache rounds K and V to 11 significant bits
+            assert np.max(np.abs(got - want)) <= 1e-2 * np.abs(want).max()
+        else:
+            assert_close(got, want)
+    assert m.position == ref.pos == c0
+
+
 @pytest.mark.parametrize("out_dtype", [14, 8, 12])
 def test_output_matrix_types(rq, gpu, out_dtype):
     """An output matrix in Q6_K / Q8_0 / Q4_K (llama.cpp files keep lm_head in
