@@ -135,70 +135,101 @@ constexpr size_t PREFILL_ATT_MIN_ROWS = 8, PREFILL_ATT_MAX_PAGES = 8;
 
 // Attention of a prompt chunk (m > 1 rows at positions *pos .. *pos + m - 1,
 // keys already in the cache): one wave a query row, 8 consecutive rows of one
-// head a workgroup, so the workgroup's waves read the same cache pages (one
-// L2 fetch a page, then L1).  A wave walks its row's keys a page (64 keys) at
-// a time: lane j scores key p0 + j (q from LDS, broadcast), then the page's
+// head a workgroup.  The workgroup copies each cache page (64 keys) it needs
+// into LDS once, with coalesced 16-byte loads, and its waves read it from
+// there: lane j scores key p0 + j against q (LDS broadcast), then the page's
 // max, an online rescale of the running (max M, sum L, context o) and the
-// weighted V rows, lane l owning dims HD / 64 * l ..; at the end o / L.  The
-// same f32 arithmetic as attention_kernel per term (scores / sqrt(hd),
-// exp(score - max), attention.rs:414-441); the running max replaces the
-// chunk combine, so sums round in another order.
+// weighted V rows, lane l owning dims HD / 64 * l ..; at the end o / L.  K
+// rows sit 16 bytes apart from a multiple of the bank width in LDS, so the 64
+// lanes' reads of 64 rows spread over the banks.  The same f32 arithmetic as
+// attention_kernel per term (scores / sqrt(hd), exp(score - max),
+// attention.rs:414-441); the running max replaces the chunk combine, so sums
+// round in another order.
 template <typename KV, int HD>
 __global__ __launch_bounds__(512) void prefill_attention_kernel(AttArgs<KV> a, int m) {
     static_assert(HD % 64 == 0 && HD <= 256, "head dims a lane");
     constexpr int DPL = HD / 64;
     constexpr int V = 16 / (int)sizeof(KV);  // cache elements a 16-byte load
+    constexpr int KROW = HD + V;             // K row stride in LDS (elements)
+    constexpr int PIECES = KV_PAGE * HD / V;  // 16-byte pieces of a page
+    constexpr int PER = (PIECES + 511) / 512;
     typedef KV kvv __attribute__((ext_vector_type(V)));
     __shared__ __attribute__((aligned(16))) float qsh[8][HD];
+    __shared__ __attribute__((aligned(16))) KV ks[KV_PAGE * KROW];
+    __shared__ __attribute__((aligned(16))) KV vs[KV_PAGE * HD];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int n_heads = a.n_heads, n_kv = a.n_kv, G = n_heads / n_kv;
     // the G query heads of a KV head on one XCD (block b on XCD b % 8)
     const int h = ((int)blockIdx.x % n_kv) * G + (int)blockIdx.x / n_kv;
     const int kvh = h / G;
-    const int s = (int)blockIdx.y * 8 + w;
-    if (s >= m) return;  // whole wave; no workgroup barrier below
-    const float* q = a.qkv + (size_t)s * a.qkv_dim + (size_t)h * HD;
+    const int s0 = (int)blockIdx.y * 8, s = s0 + w;
+    const int pos0 = *a.pos_dev;
+    const int tmax = pos0 + min(s0 + 8, m);  // keys of the group's last row
+    const int t = pos0 + s + 1;              // keys 0 .. t - 1 of this row
+    const bool live = s < m;                 // wave-uniform
+    if (live) {
+        const float* q = a.qkv + (size_t)s * a.qkv_dim + (size_t)h * HD;
 #pragma unroll
-    for (int c = 0; c < DPL; c++) qsh[w][lane + 64 * c] = q[lane + 64 * c];
-    __builtin_amdgcn_wave_barrier();
-    const int t = *a.pos_dev + s + 1;  // keys 0 .. t - 1
+        for (int c = 0; c < DPL; c++) qsh[w][lane + 64 * c] = q[lane + 64 * c];
+    }
     float M = -__builtin_inff(), L = 0.0f, o[DPL];
 #pragma unroll
     for (int c = 0; c < DPL; c++) o[c] = 0.0f;
-    for (int p0 = 0; p0 < t; p0 += KV_PAGE) {
-        const int nvalid = min(KV_PAGE, t - p0);
+    for (int p0 = 0; p0 < tmax; p0 += KV_PAGE) {
+        const int nv = min(KV_PAGE, tmax - p0);  // rows of the page any wave reads
         const size_t page = kv_row(a.kv_table, n_kv, kvh, p0, HD);
-        const KV* kb = a.kc + page;
-        const KV* vb = a.vc + page;
-        // score of key p0 + lane (a key past the row re-reads the last one)
-        const KV* kr = kb + (size_t)min(lane, nvalid - 1) * HD;
-        kvv kreg[HD / V];
+        kvv kr[PER], vr[PER];
 #pragma unroll
-        for (int i = 0; i < HD / V; i++) kreg[i] = *reinterpret_cast<const kvv*>(kr + i * V);
-        float acc = 0.0f;
-#pragma unroll
-        for (int i = 0; i < HD / V; i++)
-#pragma unroll
-            for (int e = 0; e < V; e++) acc += qsh[w][i * V + e] * (float)kreg[i][e];
-        const bool valid = lane < nvalid;
-        const float sc = valid ? acc / a.scale : -__builtin_inff();
-        const float Mn = fmaxf(M, wave_max(sc));
-        const float corr = expf(M - Mn);  // 0 on the first page
-        const float e = valid ? expf(sc - Mn) : 0.0f;
-        L = L * corr + wave_sum(e);
-#pragma unroll
-        for (int c = 0; c < DPL; c++) o[c] *= corr;
-        // weighted V rows, branch-free: rows past the row's keys re-read the
-        // last valid one with weight 0
-#pragma unroll
-        for (int j = 0; j < KV_PAGE; j++) {
-            const float ej = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e), j));
-            const KV* vr = vb + (size_t)min(j, nvalid - 1) * HD + DPL * lane;
-#pragma unroll
-            for (int c = 0; c < DPL; c++) o[c] += ej * (float)vr[c];
+        for (int i = 0; i < PER; i++) {
+            const int pc = threadIdx.x + 512 * i;
+            if (pc < nv * (HD / V)) {
+                kr[i] = *reinterpret_cast<const kvv*>(a.kc + page + (size_t)pc * V);
+                vr[i] = *reinterpret_cast<const kvv*>(a.vc + page + (size_t)pc * V);
+            }
         }
-        M = Mn;
+        __syncthreads();  // the previous page's reads are done
+#pragma unroll
+        for (int i = 0; i < PER; i++) {
+            const int pc = threadIdx.x + 512 * i;
+            if (pc < nv * (HD / V)) {
+                const int r = pc / (HD / V), c = pc % (HD / V);
+                *reinterpret_cast<kvv*>(ks + r * KROW + c * V) = kr[i];
+                *reinterpret_cast<kvv*>(vs + pc * V) = vr[i];
+            }
+        }
+        __syncthreads();
+        if (live && p0 < t) {
+            const int nvalid = min(KV_PAGE, t - p0);  // <= nv
+            // score of key p0 + lane (a key past the row re-reads the last one)
+            const KV* krow = ks + min(lane, nvalid - 1) * KROW;
+            float acc = 0.0f;
+#pragma unroll
+            for (int i = 0; i < HD / V; i++) {
+                const kvv k = *reinterpret_cast<const kvv*>(krow + i * V);
+#pragma unroll
+                for (int e = 0; e < V; e++) acc += qsh[w][i * V + e] * (float)k[e];
+            }
+            const bool valid = lane < nvalid;
+            const float sc = valid ? acc / a.scale : -__builtin_inff();
+            const float Mn = fmaxf(M, wave_max(sc));
+            const float corr = expf(M - Mn);  // 0 on the first page
+            const float e = valid ? expf(sc - Mn) : 0.0f;
+            L = L * corr + wave_sum(e);
+#pragma unroll
+            for (int c = 0; c < DPL; c++) o[c] *= corr;
+            // weighted V rows; rows past the row's keys re-read the last
+            // valid one with weight 0 (rows past nv were not copied)
+#pragma unroll
+            for (int j = 0; j < KV_PAGE; j++) {
+                const float ej = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e), j));
+                const KV* vrow = vs + min(j, nvalid - 1) * HD + DPL * lane;
+#pragma unroll
+                for (int c = 0; c < DPL; c++) o[c] += ej * (float)vrow[c];
+            }
+            M = Mn;
+        }
     }
+    if (!live) return;
     float* out = a.out + (size_t)s * n_heads * HD + (size_t)h * HD + DPL * lane;
     const float invL = 1.0f / L;
 #pragma unroll
