@@ -130,14 +130,20 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attention_kernel(AttArgs<KV> a
     attention_body<KV, HD, false>(blockIdx.x, blockIdx.y, blockIdx.z, sm, a);
 }
 
-// rows and cache pages (keys / 64) where a prompt chunk takes the kernel below
-constexpr size_t PREFILL_ATT_MIN_ROWS = 8, PREFILL_ATT_MAX_PAGES = 8;
+// A prompt chunk of at least PREFILL_ATT_ALL_ROWS rows takes the kernel below
+// at any length, one of PREFILL_ATT_MIN_ROWS .. that while its rows see at
+// most PREFILL_ATT_MAX_PAGES cache pages (keys / 64); it walks a row's pages
+// in turn, so short chunks at long lengths keep the per-row kernel, which
+// spreads a row's pages over workgroups.  MI355X, 7B Q4_0, 2040-token prompt
+// (per-row kernel / this one at every length): chunks of 128 rows 245 / 179 ms,
+// 32 rows 410 / 384 ms, 16 rows 677 / 734 ms, 8 rows 1220 / 1435 ms.
+constexpr size_t PREFILL_ATT_ALL_ROWS = 32, PREFILL_ATT_MIN_ROWS = 8, PREFILL_ATT_MAX_PAGES = 8;
 
 // Attention of a prompt chunk (m > 1 rows at positions *pos .. *pos + m - 1,
 // keys already in the cache): one wave a query row, 8 consecutive rows of one
 // head a workgroup.  The workgroup copies each cache page (64 keys) it needs
-// into LDS once, with coalesced 16-byte loads, and its waves read it from
-// there: lane j scores key p0 + j against q (LDS broadcast), then the page's
+// into LDS once, with coalesced 16-byte loads issued while the waves work on
+// the page before, and its waves read it from there: lane j scores key p0 + j against q (LDS broadcast), then the page's
 // max, an online rescale of the running (max M, sum L, context o) and the
 // weighted V rows, lane l owning dims HD / 64 * l ..; at the end o / L.  K
 // rows sit 16 bytes apart from a multiple of the bank width in LDS, so the 64
@@ -175,10 +181,11 @@ __global__ __launch_bounds__(512) void prefill_attention_kernel(AttArgs<KV> a, i
     float M = -__builtin_inff(), L = 0.0f, o[DPL];
 #pragma unroll
     for (int c = 0; c < DPL; c++) o[c] = 0.0f;
-    for (int p0 = 0; p0 < tmax; p0 += KV_PAGE) {
-        const int nv = min(KV_PAGE, tmax - p0);  // rows of the page any wave reads
+    // this thread's pieces of the page at p0 (rows of it that any wave reads)
+    kvv kr[PER], vr[PER];
+    auto fetch = [&](int p0) {
+        const int nv = min(KV_PAGE, tmax - p0);
         const size_t page = kv_row(a.kv_table, n_kv, kvh, p0, HD);
-        kvv kr[PER], vr[PER];
 #pragma unroll
         for (int i = 0; i < PER; i++) {
             const int pc = threadIdx.x + 512 * i;
@@ -187,6 +194,10 @@ __global__ __launch_bounds__(512) void prefill_attention_kernel(AttArgs<KV> a, i
                 vr[i] = *reinterpret_cast<const kvv*>(a.vc + page + (size_t)pc * V);
             }
         }
+    };
+    fetch(0);
+    for (int p0 = 0; p0 < tmax; p0 += KV_PAGE) {
+        const int nv = min(KV_PAGE, tmax - p0);  // rows of the page any wave reads
         __syncthreads();  // the previous page's reads are done
 #pragma unroll
         for (int i = 0; i < PER; i++) {
@@ -198,6 +209,7 @@ __global__ __launch_bounds__(512) void prefill_attention_kernel(AttArgs<KV> a, i
             }
         }
         __syncthreads();
+        if (p0 + KV_PAGE < tmax) fetch(p0 + KV_PAGE);  // in flight during this page
         if (live && p0 < t) {
             const int nvalid = min(KV_PAGE, t - p0);  // <= nv
             // score of key p0 + lane (a key past the row re-reads the last one)
@@ -514,7 +526,8 @@ struct LlamaModel {
         const float scale = sqrtf((float)hd);
         // a prompt chunk whose rows see few pages: a wave a row
         const size_t pages = (host_pos + m + KV_PAGE - 1) / KV_PAGE;
-        if (m >= PREFILL_ATT_MIN_ROWS && pages <= PREFILL_ATT_MAX_PAGES && !capture_any_pos &&
+        if ((m >= PREFILL_ATT_ALL_ROWS || (m >= PREFILL_ATT_MIN_ROWS && pages <= PREFILL_ATT_MAX_PAGES)) &&
+            !capture_any_pos &&
             (hd == 64 || hd == 128 || hd == 256)) {
             AttArgs<KV> pa{};
             pa.qkv = qkv;
