@@ -138,6 +138,7 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attention_kernel(AttArgs<KV> a
 // (per-row kernel / this one at every length): chunks of 128 rows 245 / 179 ms,
 // 32 rows 410 / 384 ms, 16 rows 677 / 734 ms, 8 rows 1220 / 1435 ms.
 constexpr size_t PREFILL_ATT_ALL_ROWS = 32, PREFILL_ATT_MIN_ROWS = 8, PREFILL_ATT_MAX_PAGES = 8;
+constexpr size_t PREFILL_ATT_MFMA_MIN_ROWS = 32;
 
 // Attention of a prompt chunk (m > 1 rows at positions *pos .. *pos + m - 1,
 // keys already in the cache): one wave a query row, 8 consecutive rows of one
@@ -246,6 +247,201 @@ __global__ __launch_bounds__(512) void prefill_attention_kernel(AttArgs<KV> a, i
     const float invL = 1.0f / L;
 #pragma unroll
     for (int c = 0; c < DPL; c++) out[c] = o[c] * invL;
+}
+
+// The same attention on the matrix cores, for an f16 cache: a workgroup of 4
+// waves takes 16 consecutive rows of one head and walks the cache pages
+// their rows need, staged in LDS as above (K rows, V transposed: the MFMA
+// operands read 8 consecutive keys of one dim).  Per page:
+//  1. scores: wave w forms S[16 rows][keys 16w .. 16w + 15] with
+//     v_mfma_f32_16x16x32_f16, q as the A operand; q rows are scaled by a
+//     power of two (row max into [2^14, 2^15)) and split into f16 hi + lo,
+//     so hi * k + lo * k (f16 k exact) carries about 22 significant bits of
+//     q, products exact and sums in f32;
+//  2. softmax: wave w takes rows 4w .. 4w + 3, a lane a key: scores / sqrt(hd)
+//     (attention.rs:414-415), page max, online rescale of the running
+//     (max, sum), weights exp(score - max) split into f16 hi + lo;
+//  3. context: wave w forms O[16 rows][HD / 4 dims] += P V, after scaling O
+//     by the rows' rescale factors, with the weights as the A operand.
+// At the end o / sum.  Keys past a row's length weigh 0; cache rows past the
+// ones copied are zeros in LDS (finite, so 0 * v stays 0).
+template <int HD>
+__global__ __launch_bounds__(256) void prefill_attention_mfma_kernel(AttArgs<_Float16> a, int m) {
+    static_assert(HD % 64 == 0 && HD <= 256, "16-dim output tiles, 4 waves");
+    typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    constexpr int KST = HD / 32;            // MFMA K steps over the head dims
+    constexpr int OT = HD / 64;             // 16-dim output tiles a wave
+    constexpr int KR = HD + 8;              // LDS row strides (elements): 16 bytes
+    constexpr int VR = KV_PAGE + 8;         // past a multiple of the bank period
+    constexpr int PR = KV_PAGE + 8;
+    constexpr int SR = KV_PAGE + 4;
+    constexpr int PPR = HD / 8;             // 16-byte pieces a cache row
+    constexpr int PER = KV_PAGE * PPR / 256;
+    __shared__ __attribute__((aligned(16))) _Float16 ks[KV_PAGE * KR];
+    __shared__ __attribute__((aligned(16))) _Float16 vt[HD * VR];
+    __shared__ __attribute__((aligned(16))) _Float16 ph[16 * PR];
+    __shared__ __attribute__((aligned(16))) _Float16 pl[16 * PR];
+    __shared__ __attribute__((aligned(16))) float ss[16 * SR];
+    __shared__ int rexp[16];
+    __shared__ float rcorr[16], rsum[16];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int g = lane >> 4, r16 = lane & 15;
+    const int n_heads = a.n_heads, n_kv = a.n_kv, G = n_heads / n_kv;
+    const int h = ((int)blockIdx.x % n_kv) * G + (int)blockIdx.x / n_kv;
+    const int kvh = h / G;
+    const int s0 = (int)blockIdx.y * 16;
+    const int pos0 = *a.pos_dev;
+    const int tmax = pos0 + min(s0 + 16, m);  // keys of the group's last row
+    const float* qh0 = a.qkv + (size_t)h * HD;
+
+    // row exponents: wave w takes rows 4w .. 4w + 3
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int r = 4 * w + i, s = s0 + r;
+        float mx = 0.0f;
+        if (s < m)
+#pragma unroll
+            for (int c = 0; c < HD / 64; c++) mx = fmaxf(mx, fabsf(qh0[(size_t)s * a.qkv_dim + lane + 64 * c]));
+        mx = wave_max(mx);
+        int e = 0;
+        if (mx > 0.0f) {
+            frexpf(mx, &e);  // mx = f * 2^e, f in [0.5, 1)
+            e -= 15;
+        }
+        if (lane == 0) rexp[r] = e;
+    }
+    __syncthreads();
+    // A operands of the scores: row r16, dims 32k + 8g .. + 7, hi and lo
+    h8 qhi[KST], qlo[KST];
+    {
+        const int s = s0 + r16, e = rexp[r16];
+#pragma unroll
+        for (int k = 0; k < KST; k++) {
+            float4 q0 = {0.0f, 0.0f, 0.0f, 0.0f}, q1 = q0;
+            if (s < m) {
+                const float4* qp = reinterpret_cast<const float4*>(qh0 + (size_t)s * a.qkv_dim + 32 * k + 8 * g);
+                q0 = qp[0];
+                q1 = qp[1];
+            }
+            const float qv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const float v = ldexpf(qv[u], -e);
+                const _Float16 hi = (_Float16)v;
+                qhi[k][u] = hi;
+                qlo[k][u] = (_Float16)(v - (float)hi);
+            }
+        }
+    }
+    f4 o[OT];
+#pragma unroll
+    for (int t = 0; t < OT; t++) o[t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    float Mr[4], Lr[4];  // running max / sum of rows 4w + i (every lane)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        Mr[i] = -__builtin_inff();
+        Lr[i] = 0.0f;
+    }
+    // this thread's pieces of the page at p0 (zeros for rows past the group's
+    // keys).  K: piece pc = key * PPR + c.  V: a wave's 64 pieces are 16 keys x
+    // 4 consecutive pieces, so its transposed 2-byte stores fall on different
+    // banks for different keys.
+    h8 kr[PER], vr[PER];
+    auto vpiece = [&](int idx, int& key, int& c) {
+        c = (idx >> 4) % PPR;
+        key = (idx & 15) + 16 * ((idx >> 4) / PPR);
+    };
+    auto fetch = [&](int p0) {
+        const int nv = min(KV_PAGE, tmax - p0);
+        const size_t page = kv_row(a.kv_table, n_kv, kvh, p0, HD);
+#pragma unroll
+        for (int i = 0; i < PER; i++) {
+            const int pc = threadIdx.x + 256 * i;
+            int vk, vc;
+            vpiece(pc, vk, vc);
+            kr[i] = pc / PPR < nv ? *reinterpret_cast<const h8*>(a.kc + page + (size_t)pc * 8) : h8{};
+            vr[i] = vk < nv ? *reinterpret_cast<const h8*>(a.vc + page + (size_t)vk * HD + vc * 8) : h8{};
+        }
+    };
+    fetch(0);
+    for (int p0 = 0; p0 < tmax; p0 += KV_PAGE) {
+        __syncthreads();  // the previous page's LDS reads are done
+#pragma unroll
+        for (int i = 0; i < PER; i++) {
+            const int pc = threadIdx.x + 256 * i;
+            *reinterpret_cast<h8*>(ks + (pc / PPR) * KR + (pc % PPR) * 8) = kr[i];
+            int vk, vc;
+            vpiece(pc, vk, vc);
+#pragma unroll
+            for (int u = 0; u < 8; u++) vt[(vc * 8 + u) * VR + vk] = vr[i][u];
+        }
+        __syncthreads();
+        if (p0 + KV_PAGE < tmax) fetch(p0 + KV_PAGE);  // in flight during this page
+        // 1. scores of keys 16w .. 16w + 15: lane holds S[4g + t][16w + r16]
+        f4 sacc = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int k = 0; k < KST; k++) {
+            const h8 b = *reinterpret_cast<const h8*>(ks + (16 * w + r16) * KR + 32 * k + 8 * g);
+            sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qhi[k], b, sacc, 0, 0, 0);
+            sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qlo[k], b, sacc, 0, 0, 0);
+        }
+#pragma unroll
+        for (int t = 0; t < 4; t++) ss[(4 * g + t) * SR + 16 * w + r16] = sacc[t];
+        __syncthreads();
+        // 2. softmax of rows 4w .. 4w + 3 over the page, a lane a key
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int r = 4 * w + i, s = s0 + r;
+            const bool valid = s < m && p0 + lane < pos0 + s + 1;
+            const float sc = valid ? ldexpf(ss[r * SR + lane], rexp[r]) / a.scale : -__builtin_inff();
+            const float Mn = fmaxf(Mr[i], wave_max(sc));
+            const float corr = Mn == -__builtin_inff() ? 1.0f : expf(Mr[i] - Mn);  // a row past m: no keys
+            const float e = valid ? expf(sc - Mn) : 0.0f;
+            Lr[i] = Lr[i] * corr + wave_sum(e);
+            Mr[i] = Mn;
+            const _Float16 hi = (_Float16)e;
+            ph[r * PR + lane] = hi;
+            pl[r * PR + lane] = (_Float16)(e - (float)hi);
+            if (lane == 0) rcorr[r] = corr;
+        }
+        __syncthreads();
+        // 3. context: lane holds O[4g + t][(w OT + j) 16 + r16]
+        {
+            float cr[4];
+#pragma unroll
+            for (int t = 0; t < 4; t++) cr[t] = rcorr[4 * g + t];
+#pragma unroll
+            for (int j = 0; j < OT; j++)
+#pragma unroll
+                for (int t = 0; t < 4; t++) o[j][t] *= cr[t];
+#pragma unroll
+            for (int kk = 0; kk < KV_PAGE / 32; kk++) {
+                const h8 pa = *reinterpret_cast<const h8*>(ph + r16 * PR + 32 * kk + 8 * g);
+                const h8 pb = *reinterpret_cast<const h8*>(pl + r16 * PR + 32 * kk + 8 * g);
+#pragma unroll
+                for (int j = 0; j < OT; j++) {
+                    const int d0 = (w * OT + j) * 16;
+                    const h8 vb = *reinterpret_cast<const h8*>(vt + (d0 + r16) * VR + 32 * kk + 8 * g);
+                    o[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb, o[j], 0, 0, 0);
+                    o[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pb, vb, o[j], 0, 0, 0);
+                }
+            }
+        }
+    }
+    if (lane == 0)
+#pragma unroll
+        for (int i = 0; i < 4; i++) rsum[4 * w + i] = Lr[i];
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const int r = 4 * g + t, s = s0 + r;
+        if (s >= m) continue;
+        const float invL = 1.0f / rsum[r];
+        float* out = a.out + (size_t)s * n_heads * HD + (size_t)h * HD;
+#pragma unroll
+        for (int j = 0; j < OT; j++) out[(w * OT + j) * 16 + r16] = o[j][t] * invL;
+    }
 }
 
 // x += y (Tensor::add_inplace, ops.rs:276-289)
@@ -526,6 +722,27 @@ struct LlamaModel {
         const float scale = sqrtf((float)hd);
         // a prompt chunk whose rows see few pages: a wave a row
         const size_t pages = (host_pos + m + KV_PAGE - 1) / KV_PAGE;
+        if constexpr (std::is_same<KV, _Float16>::value) {
+            if (m >= PREFILL_ATT_MFMA_MIN_ROWS && !capture_any_pos && (hd == 64 || hd == 128 || hd == 256)) {
+                AttArgs<KV> pa{};
+                pa.qkv = qkv;
+                pa.qkv_dim = qkv_dim;
+                pa.pos_dev = pos;
+                pa.kc = kcl;
+                pa.vc = vcl;
+                pa.kv_table = kv_table;
+                pa.n_heads = cfg.n_heads;
+                pa.n_kv = cfg.n_kv_heads;
+                pa.hd_rt = hd;
+                pa.scale = scale;
+                pa.out = att;
+                auto pk = (hd == 128) ? prefill_attention_mfma_kernel<128>
+                        : (hd == 64)  ? prefill_attention_mfma_kernel<64>
+                                      : prefill_attention_mfma_kernel<256>;
+                hipLaunchKernelGGL(pk, dim3(cfg.n_heads, (unsigned)((m + 15) / 16)), dim3(256), 0, stream, pa, (int)m);
+                return hipGetLastError();
+            }
+        }
         if ((m >= PREFILL_ATT_ALL_ROWS || (m >= PREFILL_ATT_MIN_ROWS && pages <= PREFILL_ATT_MAX_PAGES)) &&
             !capture_any_pos &&
             (hd == 64 || hd == 128 || hd == 256)) {

@@ -231,11 +231,13 @@ def test_long_context_spans(rq, gpu, kw):
     (dict(kv_f16=False, dim=256, n_heads=1, n_kv_heads=1, head_dim=256), [33, 31]),   # head dim 256
     (dict(kv_f16=False, dim=384, n_heads=6, n_kv_heads=2), [128] * 5),  # 32+ rows past 512 keys
     (dict(kv_f16=True), [128] * 4 + [16, 40]),   # 16 rows past 512 keys: per-row kernel; 40 rows: 10 pages
+    (dict(kv_f16=True, dim=256, n_heads=1, n_kv_heads=1, head_dim=256), [40, 33]),  # f16, head dim 256
 ])
 def test_prefill_attention_chunks(rq, gpu, kw, chunks):
-    """Prompt chunks of 32 rows or more, and of 8 rows or more whose rows see
-    at most 8 cache pages, take the kernel with a wave a row; the rest take
-    the per-row kernel.  Every chunk's logits against the oracle."""
+    """Prompt chunks of 32 rows or more (on the matrix cores with an f16
+    cache), and of 8 rows or more whose rows see at most 8 cache pages, take
+    the kernels that walk a row group's pages; the rest take the per-row
+    kernel.  Every chunk's logits against the oracle."""
     cfg = tiny_config(max_seq=700, max_batch=128, **kw)
     print(f"case prefill chunks {kw} {chunks}", flush=True)
     m, ref = build(cfg, seed=5)
