@@ -143,6 +143,105 @@ __global__ __launch_bounds__(XPREP_FAST_THREADS) void gemm_xprep_fast_kernel(con
     }
 }
 
+// The fast split after a prologue on the row, for the decoder's prompt
+// chunks (one launch instead of two):
+// PRO 1: RMSNorm, x * (1 / sqrt(sum(x^2) / k + eps)) * g (ops.rs:688-751);
+// PRO 2: SwiGLU of rows of 2k interleaved (gate_j, up_j) values,
+//        silu(g) * u with silu(g) = g * (1 / (1 + exp(-g))) (ops.rs:441-446).
+// The element arithmetic is the separate kernels'; only RMSNorm's sum of
+// squares runs in another order.
+template <int PRO>
+__global__ __launch_bounds__(XPREP_FAST_THREADS) void gemm_xprep_pro_kernel(
+    const float* __restrict__ X, int k, const float* __restrict__ g, float eps, _Float16* __restrict__ XH,
+    _Float16* __restrict__ XL, int* __restrict__ XE) {
+    static_assert(PRO == 1 || PRO == 2, "RMSNorm or SwiGLU");
+    constexpr int NT = XPREP_FAST_THREADS, NV = 4;
+    __shared__ float red[NT / 64], red2[NT / 64];
+    const int row = blockIdx.x;
+    const int k4 = k >> 2;  // k % 32 == 0
+    f32x4 v[NV];
+    if constexpr (PRO == 2) {
+        const f32x4* x = reinterpret_cast<const f32x4*>(X + (size_t)row * 2 * k);
+        auto silu_mul = [](float gv, float uv) {
+            const float sig = 1.0f / (1.0f + expf(-gv));
+            return (gv * sig) * uv;
+        };
+#pragma unroll
+        for (int j = 0; j < NV; j++) {
+            const int p = threadIdx.x + j * NT;
+            if (p < k4) {
+                const f32x4 a = x[2 * p], b = x[2 * p + 1];
+                v[j] = f32x4{silu_mul(a[0], a[1]), silu_mul(a[2], a[3]), silu_mul(b[0], b[1]), silu_mul(b[2], b[3])};
+            } else {
+                v[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+        }
+    } else {
+        const f32x4* x = reinterpret_cast<const f32x4*>(X + (size_t)row * k);
+        float ss = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NV; j++) {
+            const int p = threadIdx.x + j * NT;
+            v[j] = p < k4 ? x[p] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            ss += (v[j][0] * v[j][0] + v[j][1] * v[j][1]) + (v[j][2] * v[j][2] + v[j][3] * v[j][3]);
+        }
+        ss = sum8_f32(ss);
+        ss += dpp_f32<DPP_ROW_MIRROR>(ss);
+        ss += __shfl_xor(ss, 16);
+        ss += __shfl_xor(ss, 32);
+        if ((threadIdx.x & 63) == 0) red2[threadIdx.x >> 6] = ss;
+        __syncthreads();
+        ss = red2[0];
+#pragma unroll
+        for (int w = 1; w < NT / 64; w++) ss += red2[w];
+        const float inv = 1.0f / sqrtf(ss / (float)k + eps);
+        const f32x4* g4 = reinterpret_cast<const f32x4*>(g);
+#pragma unroll
+        for (int j = 0; j < NV; j++) {
+            const int p = threadIdx.x + j * NT;
+            if (p < k4) v[j] = (v[j] * inv) * g4[p];
+        }
+    }
+    float amax = 0.0f;
+    bool bad = false;
+#pragma unroll
+    for (int j = 0; j < NV; j++)
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            bad |= !isfinite(v[j][t]);
+            amax = fmaxf(amax, fabsf(v[j][t]));
+        }
+    if (bad) amax = __builtin_inff();
+    amax = max8_f32(amax);
+    amax = fmaxf(amax, dpp_f32<DPP_ROW_MIRROR>(amax));
+    amax = fmaxf(amax, __shfl_xor(amax, 16));
+    amax = fmaxf(amax, __shfl_xor(amax, 32));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+    __syncthreads();
+    amax = red[0];
+#pragma unroll
+    for (int w = 1; w < NT / 64; w++) amax = fmaxf(amax, red[w]);
+    int e = 0;
+    if (amax > 0.0f && isfinite(amax)) e = ilogbf(amax) - 14;
+    if (threadIdx.x == 0) XE[row] = e;
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        const int p = threadIdx.x + j * NT;
+        if (p < k4) {
+            h4 hv, lv;
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const float sc = ldexpf(v[j][t], -e);
+                hv[t] = (_Float16)sc;
+                lv[t] = (_Float16)(sc - (float)hv[t]);
+            }
+            reinterpret_cast<h4*>(XH + (size_t)row * k)[p] = hv;
+            reinterpret_cast<h4*>(XL + (size_t)row * k)[p] = lv;
+        }
+    }
+}
+
 // ---- GEMM ------------------------------------------------------------------------
 // LDS row strides, padded so that the 16 rows a fragment read touches fall in
 // distinct banks: nibble rows CB*16 + 8 bytes; x rows CB*64 + 16 bytes (f16)
@@ -218,7 +317,7 @@ __device__ __forceinline__ void tile_of(int nj, int ni, int& bx, int& by) {
 template <bool NATIVE, bool DUMP, int FJ, int FI, int WJ, int WI, int KS, int KB>
 __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_kernel(
     const uint8_t* __restrict__ W, int n, int nb, const void* __restrict__ X0, const void* __restrict__ X1,
-    const int* __restrict__ XE, int m, float* __restrict__ Y, int32_t* __restrict__ P) {
+    const int* __restrict__ XE, int m, float* __restrict__ Y, int32_t* __restrict__ P, int accy) {
     using C = GemmCfg<NATIVE, FJ, FI, WJ, WI, KS, KB>;
     constexpr int CB = C::CB;
     constexpr int XSTR = NATIVE ? Lds<CB>::XC_STRIDE : Lds<CB>::X_STRIDE;
@@ -473,13 +572,15 @@ __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_kernel(
             const int j = j0 + (wj * FJ + a) * 16 + g * 4;
             float* yp = Y + (size_t)i * n + j;
             const f32x4 v = acc[a][b];
+            // accy: y += the product (the residual add, one rounding as x + y)
             if (j + 3 < n && ((n & 3) == 0)) {
-                *reinterpret_cast<f32x4*>(yp) =
-                    f32x4{ldexpf(v[0], e), ldexpf(v[1], e), ldexpf(v[2], e), ldexpf(v[3], e)};
+                f32x4 r = f32x4{ldexpf(v[0], e), ldexpf(v[1], e), ldexpf(v[2], e), ldexpf(v[3], e)};
+                if (accy) r = *reinterpret_cast<const f32x4*>(yp) + r;
+                *reinterpret_cast<f32x4*>(yp) = r;
             } else {
 #pragma unroll
                 for (int t = 0; t < 4; t++)
-                    if (j + t < n) yp[t] = ldexpf(v[t], e);
+                    if (j + t < n) yp[t] = accy ? yp[t] + ldexpf(v[t], e) : ldexpf(v[t], e);
             }
         }
     }
@@ -1285,7 +1386,7 @@ hipError_t launch_skinny(const uint8_t* w, int n, int nb, const float* x, int m,
 
 template <bool NATIVE, bool DUMP, int FJ, int FI, int WJ, int WI, int KS, int KB>
 hipError_t launch_cfg(const uint8_t* w, int n, int nb, const void* x0, const void* x1, const int* xe, int m,
-                      float* y, int32_t* p, hipStream_t s) {
+                      float* y, int32_t* p, hipStream_t s, int accy) {
     using C = GemmCfg<NATIVE, FJ, FI, WJ, WI, KS, KB>;
     auto kern = gemm_q4_0_kernel<NATIVE, DUMP, FJ, FI, WJ, WI, KS, KB>;
     static_assert(C::LDS >= C::RED, "K-split sums fit the staging LDS");
@@ -1296,7 +1397,7 @@ hipError_t launch_cfg(const uint8_t* w, int n, int nb, const void* x0, const voi
         if (e != hipSuccess) return e;
     }
     const unsigned tiles = (unsigned)((n + C::TJ - 1) / C::TJ) * (unsigned)((m + C::TI - 1) / C::TI);
-    launch_kernel(kern, dim3(tiles), dim3(C::NT), (size_t)C::LDS, s, w, n, nb, x0, x1, xe, m, y, p);
+    launch_kernel(kern, dim3(tiles), dim3(C::NT), (size_t)C::LDS, s, w, n, nb, x0, x1, xe, m, y, p, accy);
     return hipGetLastError();
 }
 
@@ -1306,22 +1407,22 @@ hipError_t launch_cfg(const uint8_t* w, int n, int nb, const void* x0, const voi
 // stages half the x bytes and keeps fewer registers).
 template <bool NATIVE, bool DUMP>
 hipError_t launch_tiles(const uint8_t* w, int n, int nb, const void* x0, const void* x1, const int* xe, int m,
-                        float* y, int32_t* p, hipStream_t s) {
+                        float* y, int32_t* p, hipStream_t s, int accy = 0) {
     const int cus = device_cu_count();
     if (NATIVE) {
-        if (m >= 1024) return launch_cfg<NATIVE, DUMP, 2, 2, 2, 2, 2, 2>(w, n, nb, x0, x1, xe, m, y, p, s);
-        if (m >= 256) return launch_cfg<NATIVE, DUMP, 2, 4, 2, 2, 2, 2>(w, n, nb, x0, x1, xe, m, y, p, s);
+        if (m >= 1024) return launch_cfg<NATIVE, DUMP, 2, 2, 2, 2, 2, 2>(w, n, nb, x0, x1, xe, m, y, p, s, accy);
+        if (m >= 256) return launch_cfg<NATIVE, DUMP, 2, 4, 2, 2, 2, 2>(w, n, nb, x0, x1, xe, m, y, p, s, accy);
     } else {
-        if (m >= 1024) return launch_cfg<NATIVE, DUMP, 4, 4, 2, 2, 2, 1>(w, n, nb, x0, x1, xe, m, y, p, s);
+        if (m >= 1024) return launch_cfg<NATIVE, DUMP, 4, 4, 2, 2, 2, 1>(w, n, nb, x0, x1, xe, m, y, p, s, accy);
         // 128 x 128 tiles from m = 128 where they fill three quarters of
         // the CUs (the 7B prefill's 28672-row gate/up GEMM at 128 rows: 224
         // tiles, 110 us against 119 us in 128 x 64 tiles); 128 x 64 tiles from
         // m = 256, and from m = 128 where they alone fill the CUs (prefill
         // 15.7 -> 12.3 ms; taken for every matrix: 14.9 ms)
         if (m >= 128 && m < 256 && 4 * (size_t)((n + 127) / 128) * ((m + 127) / 128) >= 3 * (size_t)cus)
-            return launch_cfg<NATIVE, DUMP, 4, 4, 2, 2, 2, 1>(w, n, nb, x0, x1, xe, m, y, p, s);
+            return launch_cfg<NATIVE, DUMP, 4, 4, 2, 2, 2, 1>(w, n, nb, x0, x1, xe, m, y, p, s, accy);
         if (m >= 256 || (m >= 128 && (size_t)((n + 127) / 128) * ((m + 63) / 64) >= (size_t)cus))
-            return launch_cfg<NATIVE, DUMP, 4, 2, 2, 2, 2, 2>(w, n, nb, x0, x1, xe, m, y, p, s);
+            return launch_cfg<NATIVE, DUMP, 4, 2, 2, 2, 2, 2>(w, n, nb, x0, x1, xe, m, y, p, s, accy);
     }
     const size_t t32 = (size_t)((n + 31) / 32) * ((m + 63) / 64);  // 32 x 64 tiles
     if (m >= 48 && t32 >= (size_t)cus) {
@@ -1330,13 +1431,13 @@ hipError_t launch_tiles(const uint8_t* w, int n, int nb, const void* x0, const v
             // (us at 128 rows, 4096 x 4096 / 4096 x 14336 / 6144 x 4096: 4-wave
             // 32 x 64 tiles 37.2 / 106.5 / 66.0, 8-wave 30.3 / 89.1 / 51.5,
             // 64 x 64 38.7 / 112.9 / 40.0)
-            if (t32 > (size_t)cus) return launch_cfg<NATIVE, DUMP, 2, 4, 2, 1, 4, 2>(w, n, nb, x0, x1, xe, m, y, p, s);
-            return launch_cfg<NATIVE, DUMP, 2, 2, 1, 2, 4, 2>(w, n, nb, x0, x1, xe, m, y, p, s);
+            if (t32 > (size_t)cus) return launch_cfg<NATIVE, DUMP, 2, 4, 2, 1, 4, 2>(w, n, nb, x0, x1, xe, m, y, p, s, accy);
+            return launch_cfg<NATIVE, DUMP, 2, 2, 1, 2, 4, 2>(w, n, nb, x0, x1, xe, m, y, p, s, accy);
         }
-        return launch_cfg<NATIVE, DUMP, 2, 4, 1, 1, 4, 2>(w, n, nb, x0, x1, xe, m, y, p, s);
+        return launch_cfg<NATIVE, DUMP, 2, 4, 1, 1, 4, 2>(w, n, nb, x0, x1, xe, m, y, p, s, accy);
     }
-    if (m > 16) return launch_cfg<NATIVE, DUMP, 1, 2, 1, 1, 4, 2>(w, n, nb, x0, x1, xe, m, y, p, s);
-    return launch_cfg<NATIVE, DUMP, 1, 1, 1, 1, 4, 8>(w, n, nb, x0, x1, xe, m, y, p, s);
+    if (m > 16) return launch_cfg<NATIVE, DUMP, 1, 2, 1, 1, 4, 2>(w, n, nb, x0, x1, xe, m, y, p, s, accy);
+    return launch_cfg<NATIVE, DUMP, 1, 1, 1, 1, 4, 8>(w, n, nb, x0, x1, xe, m, y, p, s, accy);
 }
 
 }  // namespace
@@ -1396,6 +1497,45 @@ hipError_t launch_gemm_q4_0(const uint8_t* w, size_t n, size_t k, const float* x
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     return launch_tiles<false, false>(w, (int)n, (int)(k / QK), xh, xl, xe, (int)m, y, nullptr, s);
+}
+
+hipError_t launch_gemm_q4_0_pro(const uint8_t* w, size_t n, size_t k, const float* x, size_t m, float* y,
+                                void* scratch, int pro, const float* g, float eps, bool accumulate, hipStream_t s) {
+    if (n == 0 || m == 0) return hipSuccess;
+    if (m <= GEMM_XTILE_M || m <= GEMM_SMALL_M || k > (size_t)16 * XPREP_FAST_THREADS || k % QK != 0 ||
+        (pro != 1 && pro != 2) || (pro == 1 && !g))
+        return hipErrorInvalidValue;
+    const size_t xb = (m * k * 2 + 255) & ~(size_t)255;
+    _Float16* xh = reinterpret_cast<_Float16*>(scratch);
+    _Float16* xl = reinterpret_cast<_Float16*>(reinterpret_cast<uint8_t*>(scratch) + xb);
+    int* xe = reinterpret_cast<int*>(reinterpret_cast<uint8_t*>(scratch) + 2 * xb);
+    if (pro == 1)
+        launch_kernel(gemm_xprep_pro_kernel<1>, dim3((unsigned)m), dim3(XPREP_FAST_THREADS), 0, s, x, (int)k, g, eps,
+                      xh, xl, xe);
+    else
+        launch_kernel(gemm_xprep_pro_kernel<2>, dim3((unsigned)m), dim3(XPREP_FAST_THREADS), 0, s, x, (int)k, g, eps,
+                      xh, xl, xe);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    return launch_tiles<false, false>(w, (int)n, (int)(k / QK), xh, xl, xe, (int)m, y, nullptr, s, accumulate ? 1 : 0);
+}
+
+hipError_t launch_gemm_q4_0_accumulate(const uint8_t* w, size_t n, size_t k, const float* x, size_t m, float* y,
+                                       void* scratch, hipStream_t s) {
+    if (n == 0 || m == 0) return hipSuccess;
+    if (m <= GEMM_XTILE_M || m <= GEMM_SMALL_M || k % QK != 0) return hipErrorInvalidValue;
+    const size_t xb = (m * k * 2 + 255) & ~(size_t)255;
+    _Float16* xh = reinterpret_cast<_Float16*>(scratch);
+    _Float16* xl = reinterpret_cast<_Float16*>(reinterpret_cast<uint8_t*>(scratch) + xb);
+    int* xe = reinterpret_cast<int*>(reinterpret_cast<uint8_t*>(scratch) + 2 * xb);
+    if (k <= (size_t)16 * XPREP_FAST_THREADS)
+        launch_kernel(gemm_xprep_fast_kernel, dim3((unsigned)m), dim3(XPREP_FAST_THREADS), 0, s, x, (int)k, xh, xl,
+                      xe);
+    else
+        launch_kernel(gemm_xprep_kernel, dim3((unsigned)m), dim3(XPREP_THREADS), 0, s, x, (int)k, xh, xl, xe);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    return launch_tiles<false, false>(w, (int)n, (int)(k / QK), xh, xl, xe, (int)m, y, nullptr, s, 1);
 }
 
 hipError_t launch_gemm_q4_0_native(const uint8_t* w, size_t n, size_t k, const float* x, size_t m, float* y,

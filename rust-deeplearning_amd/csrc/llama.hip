@@ -876,9 +876,21 @@ struct LlamaModel {
         if (L.split_qkv) parts[0] = &L.q, parts[1] = &L.k, parts[2] = &L.v;
         const int cols[3] = {0, q_dim, q_dim + kv_dim};
         const int np = L.split_qkv ? 3 : 1;
+        // Q4_0 prompt chunks on the LDS tile GEMM (m > GEMM_XTILE_M) fold the
+        // RMSNorms, the SwiGLU and the residual adds into the GEMMs' x splits
+        // and stores (hipErrorInvalidValue: a shape they do not take, nothing
+        // launched, the separate launches below run instead)
+        auto q4t = [&](const Mat& w) { return m > GEMM_XTILE_M && w.type == WType::Q4_0; };
+        bool qkv_done = false;
+        if (np == 1 && q4t(L.qkv)) {
+            e = launch_gemm_q4_0_pro(L.qkv.dev, L.qkv.n, L.qkv.k, x, m, qkv, gemm_scratch, 1, L.attn_norm,
+                                     cfg.norm_eps, false, stream);
+            if (e != hipSuccess && e != hipErrorInvalidValue) return e;
+            qkv_done = e == hipSuccess;
+        }
         bool want_xn = false;
         for (int i = 0; i < np; i++) want_xn |= !kquant(*parts[i]);
-        if (want_xn) rmsnorm(L.attn_norm);
+        if (want_xn && !qkv_done) rmsnorm(L.attn_norm);
         // a K-quant [Wq; Wk; Wv] also applies RoPE and writes the cache
         const bool rope_fused = np == 1 && kquant(L.qkv);
         for (size_t r = 0; rope_fused && r < m; r += 4) {
@@ -889,7 +901,7 @@ struct LlamaModel {
                                            kv_table, cfg.kv_f16 != 0, stream);
             if (e != hipSuccess) return e;
         }
-        for (int i = 0; i < np && !rope_fused; i++) {
+        for (int i = 0; i < np && !rope_fused && !qkv_done; i++) {
             const Mat& w = *parts[i];
             if (kquant(w)) {
                 e = kq_linear(w, x, d, m, qkv + cols[i], qkv_dim, GEMV_PRO_RMSNORM, L.attn_norm, GEMV_EPI_STORE);
@@ -906,7 +918,11 @@ struct LlamaModel {
         e = cfg.kv_f16 ? layer_attention<_Float16>(l, m, !rope_fused) : layer_attention<float>(l, m, !rope_fused);
         if (e != hipSuccess) return e;
         // ---- x += att . Wo^T ----
-        if (kquant(L.o)) {
+        e = q4t(L.o) ? launch_gemm_q4_0_accumulate(L.o.dev, L.o.n, L.o.k, att, m, x, gemm_scratch, stream)
+                     : hipErrorInvalidValue;
+        if (e != hipSuccess && e != hipErrorInvalidValue) return e;
+        if (e == hipSuccess) {
+        } else if (kquant(L.o)) {
             e = kq_linear(L.o, att, q_dim, m, x, d, GEMV_PRO_NONE, nullptr, GEMV_EPI_RESIDUAL);
             if (e != hipSuccess) return e;
         } else {
@@ -915,7 +931,17 @@ struct LlamaModel {
         }
         // ---- h = silu(gate) * up ----
         const size_t nf = m * (size_t)f;
-        if (!L.split_gu && kquant(L.gu)) {
+        // gu_raw: gu holds the interleaved gate / up rows and the down GEMM's
+        // x split forms h from them
+        bool gu_raw = false;
+        if (!L.split_gu && q4t(L.gu) && q4t(L.down)) {
+            e = launch_gemm_q4_0_pro(L.gu.dev, L.gu.n, L.gu.k, x, m, gu, gemm_scratch, 1, L.ffn_norm, cfg.norm_eps,
+                                     false, stream);
+            if (e != hipSuccess && e != hipErrorInvalidValue) return e;
+            gu_raw = e == hipSuccess;
+        }
+        if (gu_raw) {
+        } else if (!L.split_gu && kquant(L.gu)) {
             e = kq_linear(L.gu, x, d, m, hb, f, GEMV_PRO_RMSNORM, L.ffn_norm, GEMV_EPI_SWIGLU);
             if (e != hipSuccess) return e;
         } else if (!L.split_gu) {
@@ -934,7 +960,16 @@ struct LlamaModel {
             hipLaunchKernelGGL(swiglu2_kernel, dim3(blocks_for(nf)), dim3(NT), 0, stream, gu, gu + nf, nf, hb);
         }
         // ---- x += h . Wdown^T ----
-        if (kquant(L.down)) {
+        if (gu_raw) {
+            e = launch_gemm_q4_0_pro(L.down.dev, L.down.n, L.down.k, gu, m, x, gemm_scratch, 2, nullptr, 0.0f, true,
+                                     stream);
+            if (e != hipSuccess && e != hipErrorInvalidValue) return e;
+            if (e == hipErrorInvalidValue) {  // the SwiGLU on its own, then the product
+                hipLaunchKernelGGL(swiglu_kernel, dim3(blocks_for(nf)), dim3(NT), 0, stream, gu, f, nf, hb);
+                if ((e = linear(L.down, hb, m, xn)) != hipSuccess) return e;
+                hipLaunchKernelGGL(add_kernel, dim3(blocks_for(m * d)), dim3(NT), 0, stream, x, xn, m * d);
+            }
+        } else if (kquant(L.down)) {
             e = kq_linear(L.down, hb, f, m, x, d, GEMV_PRO_NONE, nullptr, GEMV_EPI_RESIDUAL);
             if (e != hipSuccess) return e;
         } else {

@@ -173,6 +173,17 @@ hipError_t launch_gemm_q4_0(const uint8_t* w, size_t n, size_t k, const float* x
                             void* scratch, int* counters, hipStream_t s);
 hipError_t launch_gemm_q4_0_native(const uint8_t* w, size_t n, size_t k, const float* x, size_t m, float* y,
                                    int32_t* partials, void* scratch, hipStream_t s);
+// Float-mode products of more than GEMM_XTILE_M rows (the LDS tile GEMM) with
+// the decoder's neighbouring steps folded in; hipErrorInvalidValue (nothing
+// launched) for shapes they do not take.
+//  _pro: x rows go through pro 1 RMSNorm (weights g, eps; x [m, k]) or
+//        pro 2 SwiGLU (x [m, 2k] interleaved gate / up) before the product;
+//        accumulate: y += product (the residual add) instead of y = product.
+//  _accumulate: y += x W^T.
+hipError_t launch_gemm_q4_0_pro(const uint8_t* w, size_t n, size_t k, const float* x, size_t m, float* y,
+                                void* scratch, int pro, const float* g, float eps, bool accumulate, hipStream_t s);
+hipError_t launch_gemm_q4_0_accumulate(const uint8_t* w, size_t n, size_t k, const float* x, size_t m, float* y,
+                                       void* scratch, hipStream_t s);
 
 // Decoder fusion of the Q4_0 float-mode fused GEMV (m <= 4, k / 32 even,
 // x 16-byte aligned): prologue 0 none, 1 RMSNorm with weights g and eps,
