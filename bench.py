@@ -48,6 +48,7 @@ Q4K_DOWN_KEY = "gemv_q4k_splitk_kernel<4, 4, 16, 0, 0>|config3 down"
 # configs[4]
 LLAMA_SEED = 0x5EED0005
 PROMPT_LEN, GEN_TOKENS = 128, 256
+LONG_PROMPT_LEN = 2040  # prefill figure beside the decode line (max_seq 2048)
 # not a BASELINE config: the lm_head of a llama.cpp Q4_0 7B file is Q6_K
 Q6K_LM_HEAD = "Q6_K GEMV 32000x4096 (the output matrix of llama.cpp Q4_0 7B files)"
 
@@ -514,7 +515,8 @@ def decode_bytes_per_token(cfg, ctx_mean):
 
 def decode_line(rig, reps=2):
     """random-init 7B Q4_0 Llama, greedy decode of 256 tokens after a
-    128-token prompt, each step one replay of the captured decode graph."""
+    128-token prompt, each step one replay of the captured decode graph.  Also
+    the prefill time of a 2040-token prompt (not part of the value)."""
     import numpy as np
 
     from rdlquant.llama import LlamaConfig, LlamaModel
@@ -533,6 +535,14 @@ def decode_line(rig, reps=2):
             toks0 = toks
         elif not np.array_equal(toks, toks0):
             raise RuntimeError("greedy decode is not deterministic across runs")
+    # a long prompt: 16 chunks of 128 rows, the later ones attending to up to
+    # 2040 cached keys (prefill only, the first token sampled)
+    long_prompt = np.random.default_rng(LLAMA_SEED + 1).integers(0, cfg.vocab, LONG_PROMPT_LEN)
+    long_ms = []
+    for _ in range(2):
+        model.reset()
+        model.generate_greedy(long_prompt, 1)
+        long_ms.append(model.last_timing()[0])
     model.close()
     rig.torch.cuda.empty_cache()
     decode_ms = min(r[1] for r in runs[1:])
@@ -550,6 +560,8 @@ def decode_line(rig, reps=2):
         "ms_per_token": round(ms_tok, 4),
         "prefill_ms_128_tokens": round(prefill_ms, 3),
         "prefill_tokens_s": round(PROMPT_LEN / (prefill_ms * 1e-3), 1),
+        "prefill_ms_%d_tokens" % LONG_PROMPT_LEN: round(min(long_ms), 3),
+        "prefill_%d_tokens_s" % LONG_PROMPT_LEN: round(LONG_PROMPT_LEN / (min(long_ms) * 1e-3), 1),
         "bytes_per_token": bpt,
         "tokens_s_at_100pct_hbm": round(PEAK_HBM_GBPS * 1e9 / bpt, 1),
         "roofline": {
