@@ -73,12 +73,17 @@ def swiglu(gate, up):
 
 
 class LlamaRef:
-    def __init__(self, cfg, weights, threads=8):
+    def __init__(self, cfg, weights, threads=8, kv_f16=False):
         """cfg: rdlquant.llama.LlamaConfig; weights: dict slot -> array (model
-        slots) or (slot, layer) -> array, as given to LlamaModel.set_weight."""
+        slots) or (slot, layer) -> array, as given to LlamaModel.set_weight.
+        kv_f16: K and V rows (after RoPE) are stored rounded to f16 (round to
+        nearest, ties to even), as a half-precision cache holds them; the
+        attention then reads those values in f32.  Off: f32 rows, as KVCache
+        (kv_cache.rs:23-114)."""
         self.c = cfg
         self.w = weights
         self.threads = threads
+        self.kv_f16 = kv_f16
         c = cfg
         self.cos, self.sin = orc.rope_tables(c.head_dim, c.max_seq, c.rope_theta)
         self.kv = [[np.zeros((c.n_kv_heads, c.max_seq, c.head_dim), np.float32) for _ in range(2)]
@@ -115,6 +120,9 @@ class LlamaRef:
             q = rope_apply(q, self.cos, self.sin, start)
             k = rope_apply(k, self.cos, self.sin, start)
             kc, vc = self.kv[layer]
+            if self.kv_f16:
+                k = k.astype(np.float16).astype(np.float32)
+                v = v.astype(np.float16).astype(np.float32)
             kc[:, start:start + s] = k
             vc[:, start:start + s] = v
             ctx = attention(q, kc[:, :start + s], vc[:, :start + s], start)

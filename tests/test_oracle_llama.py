@@ -66,6 +66,26 @@ def test_cached_decode_matches_full_causal_pass():
     assert a.pos == b.pos == len(toks)
 
 
+def test_f16_cache_rows_are_the_nearest_halves():
+    # kv_f16: every stored K / V value is an f16 value, the nearest one to the
+    # f32 row (within half an f16 spacing), and the rounding reaches the logits
+    cfg = tiny_config(n_layers=1)
+    _, ref_w = tiny_weights(cfg, seed=78)
+    toks = [9, 200, 31, 4]
+    a = LlamaRef(cfg, ref_w)
+    b = LlamaRef(cfg, ref_w, kv_f16=True)
+    la, lb = a.forward_with_cache(toks), b.forward_with_cache(toks)
+    for kv in (0, 1):
+        v32 = a.kv[0][kv][:, :len(toks)]
+        v16 = b.kv[0][kv][:, :len(toks)]
+        assert np.array_equal(v16.astype(np.float16).astype(np.float32), v16)
+        half = np.spacing(np.abs(v32).astype(np.float16)).astype(np.float32) / 2
+        assert np.all(np.abs(v16 - v32) <= half)
+        assert not np.array_equal(v16, v32)
+    assert not np.array_equal(la, lb)
+    assert np.allclose(la, lb, rtol=1e-2, atol=1e-2 * np.abs(la).max())
+
+
 # ---- closed-form pins of the pieces LlamaRef composes ---------------------------------------
 from oracle import llama_ref as LR  # noqa: E402
 
