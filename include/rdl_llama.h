@@ -126,6 +126,18 @@ rdl_status rdl_llama_set_kv_page_table(rdl_llama* model, const int32_t* table, s
  * testing switch. */
 rdl_status rdl_llama_set_fused_attention(rdl_llama* model, int32_t enable);
 
+/* Kernel launches the model has enqueued since create, by attention path:
+ * host-side counts (a captured decode graph counts its launches once, at
+ * capture, however often it is replayed).  No reference counterpart: it lets
+ * tests assert which kernels a configuration reaches. */
+typedef struct rdl_llama_path_counts {
+    uint64_t fused_decode;  /* q/k/v projection + attention + o projection in one launch */
+    uint64_t prefill_mfma;  /* prompt-chunk attention on the matrix cores (f16 cache, 32+ rows) */
+    uint64_t prefill_rows;  /* prompt-chunk attention, a wave a row over LDS-staged pages */
+    uint64_t attention;     /* the per-row attention launch (span workgroups) */
+} rdl_llama_path_counts;
+rdl_status rdl_llama_get_path_counts(const rdl_llama* model, rdl_llama_path_counts* out);
+
 /* forward_with_cache_pass over n tokens followed by cache.advance(n): the
  * logits of the last row, copied to host memory (vocab floats).  Token ids
  * must be < vocab; n <= max_batch; position + n <= max_seq.  Synchronous.

@@ -77,10 +77,36 @@ enum {
 const char* rdl_status_string(rdl_status status);
 /* Detail message of the calling thread's last non-OK status ("" if none). */
 const char* rdl_last_error(void);
+/* The extents of the calling thread's last status when it was
+ * RDL_ERR_SHAPE_MISMATCH, as QuantError::ShapeMismatch { expected, actual }
+ * carries them (error.rs:9-10): up to RDL_SHAPE_MAX_DIMS values each
+ * (lengths in elements or bytes, or tensor dims, as rdl_last_error's text
+ * names them), the counts in *n_expected / *n_actual, unused entries 0.
+ * RDL_ERR_INVALID_DATA when the last status was anything else; neither case
+ * changes the thread's last status. */
+#define RDL_SHAPE_MAX_DIMS 4
+rdl_status rdl_last_shape_mismatch(size_t* expected, size_t* n_expected, size_t* actual, size_t* n_actual);
 /* Library version string. */
 const char* rdl_version(void);
 /* Number of visible gfx950 devices (0 when there is no GPU; never an error). */
 int32_t rdl_device_count(void);
+
+/* Testing switch (no reference counterpart).  The Q4_0 GEMMs for 5-64 rows
+ * split K over workgroups whose partials the last one of each strip adds.
+ * RDL_COMBINE_AUTO (the default): where the device deals workgroup b to XCD
+ * b % 8 (probed once per device) a strip's slices share one XCD and its L2;
+ * each of their workgroups checks its XCC id, and a mismatch moves the
+ * device to the coherent combine for good and makes the next such call
+ * return RDL_ERR_HIP (the launch that ran off its XCDs may have left rows
+ * unwritten).  RDL_COMBINE_COHERENT: every launch takes the agent-coherent
+ * combine.  Both give the same bits.  Process-wide; set it while no call is
+ * in flight. */
+enum { RDL_COMBINE_AUTO = 0, RDL_COMBINE_COHERENT = 1 };
+rdl_status rdl_set_gemm_combine(int32_t mode);
+/* The switch's mode, and *local = 1 when the current device's next split
+ * GEMM launch would take the XCD-local combine (the placement probe, which
+ * the first such launch runs, has passed and no fault has been seen). */
+rdl_status rdl_get_gemm_combine(int32_t* mode, int32_t* local);
 
 /* Instrumentation (no reference counterpart): the next GEMV/GEMM kernel the
  * calling thread launches records its start and end into these hipEvent_t

@@ -37,6 +37,14 @@ namespace rdl {
 
 thread_local std::string g_err;
 
+// The extents of the calling thread's last RDL_ERR_SHAPE_MISMATCH (n_* = 0:
+// the last status was something else).
+struct ShapeDetail {
+    size_t expected[RDL_SHAPE_MAX_DIMS], actual[RDL_SHAPE_MAX_DIMS];
+    size_t n_expected, n_actual;
+};
+thread_local ShapeDetail g_shape{};
+
 rdl_status api_fail(rdl_status st, const char* fmt, ...) {
     char buf[512];
     va_list ap;
@@ -44,11 +52,30 @@ rdl_status api_fail(rdl_status st, const char* fmt, ...) {
     vsnprintf(buf, sizeof buf, fmt, ap);
     va_end(ap);
     g_err = buf;
+    g_shape.n_expected = g_shape.n_actual = 0;
     return st;
+}
+
+rdl_status api_shape_fail(const char* what, const size_t* expected, size_t n_expected, const size_t* actual,
+                          size_t n_actual) {
+    auto list = [](const size_t* v, size_t n) {
+        std::string t = "[";
+        for (size_t i = 0; i < n; i++) t += (i ? ", " : "") + std::to_string(v[i]);
+        return t + "]";
+    };
+    g_err = std::string(what) + ": expected " + list(expected, n_expected) + ", got " + list(actual, n_actual);
+    ShapeDetail d{};
+    d.n_expected = std::min<size_t>(n_expected, RDL_SHAPE_MAX_DIMS);
+    d.n_actual = std::min<size_t>(n_actual, RDL_SHAPE_MAX_DIMS);
+    for (size_t i = 0; i < d.n_expected; i++) d.expected[i] = expected[i];
+    for (size_t i = 0; i < d.n_actual; i++) d.actual[i] = actual[i];
+    g_shape = d;
+    return RDL_ERR_SHAPE_MISMATCH;
 }
 
 rdl_status api_ok() {
     g_err.clear();
+    g_shape.n_expected = g_shape.n_actual = 0;
     return RDL_OK;
 }
 
@@ -121,11 +148,11 @@ rdl_status check_matmul(WType t, const float* x, size_t x_len, const uint8_t* w,
     if (m == 0 || n == 0) return RDL_OK;
     const size_t need_w = n * (k / be) * rdl::block_bytes(t);
     if (w_len < need_w)
-        return fail(RDL_ERR_SHAPE_MISMATCH, "weight bytes: expected %zu, got %zu", need_w, w_len);
+        return rdl::api_shape_fail("weight bytes", {need_w}, {w_len});
     if (x_len < m * k)
-        return fail(RDL_ERR_SHAPE_MISMATCH, "input length: expected %zu, got %zu", m * k, x_len);
+        return rdl::api_shape_fail("input length", {m * k}, {x_len});
     if (y_len < m * n)
-        return fail(RDL_ERR_SHAPE_MISMATCH, "output length: expected %zu, got %zu", m * n, y_len);
+        return rdl::api_shape_fail("output length", {m * n}, {y_len});
     if ((m * k && !x) || (need_w && !w) || (m * n && !y))
         return fail(RDL_ERR_NULL_POINTER, "NULL buffer with non-zero length");
     return RDL_OK;
@@ -210,6 +237,7 @@ __device__ __align__(256) uint8_t scratch[RDL_NOALLOC_SCRATCH_BYTES];
 constexpr int MAX_DEVICES = 64;
 std::mutex scratch_mu;
 void* scratch_dev[MAX_DEVICES] = {};
+unsigned scratch_epoch[MAX_DEVICES] = {};  // placement epoch its counters were last zeroed under
 
 // The last NOALLOC_COUNTER_BYTES of `scratch` hold the prefill GEMM's counters
 // (zero from load time and left at zero by every launch); nothing else is
@@ -217,8 +245,10 @@ void* scratch_dev[MAX_DEVICES] = {};
 constexpr size_t NOALLOC_COUNTER_BYTES = 64 * 1024;
 constexpr size_t NOALLOC_DATA_BYTES = (size_t)RDL_NOALLOC_SCRATCH_BYTES - NOALLOC_COUNTER_BYTES;
 
-// The current device's address of `scratch`.
-rdl_status noalloc_scratch(void** out) {
+// The current device's address of `scratch`.  After a workgroup-placement
+// fault (a GEMM launch may have left counts behind) the counters are zeroed
+// again on `s`, by a kernel, before they are used.
+rdl_status noalloc_scratch(hipStream_t s, void** out) {
     int dev = 0;
     HIP_TRY(hipGetDevice(&dev));
     if (dev < 0 || dev >= MAX_DEVICES) return fail(RDL_ERR_UNSUPPORTED, "device index %d beyond %d", dev, MAX_DEVICES);
@@ -229,6 +259,14 @@ rdl_status noalloc_scratch(void** out) {
         if (e != hipSuccess || !p)
             return fail(RDL_ERR_HIP, "hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));
         scratch_dev[dev] = p;
+        scratch_epoch[dev] = rdl::xcd_placement_epoch();
+    }
+    const unsigned ep = rdl::xcd_placement_epoch();
+    if (scratch_epoch[dev] != ep) {
+        HIP_TRY(rdl::launch_zero_counters(
+            reinterpret_cast<int*>(reinterpret_cast<uint8_t*>(scratch_dev[dev]) + NOALLOC_DATA_BYTES),
+            NOALLOC_COUNTER_BYTES / sizeof(int), s));
+        scratch_epoch[dev] = ep;
     }
     *out = scratch_dev[dev];
     return RDL_OK;
@@ -257,6 +295,7 @@ struct StreamWork {
     size_t bytes;
     int* counters;
     size_t ncnt;
+    unsigned epoch;  // placement epoch the counters were last zeroed under
 };
 std::mutex work_mu;
 std::vector<StreamWork> work_pool;
@@ -269,7 +308,7 @@ rdl_status stream_work(hipStream_t s, size_t bytes, size_t ncnt, void** p, int**
     for (auto& x : work_pool)
         if (x.dev == dev && x.stream == s) e = &x;
     if (!e) {
-        work_pool.push_back({dev, s, nullptr, 0, nullptr, 0});
+        work_pool.push_back({dev, s, nullptr, 0, nullptr, 0, 0});
         e = &work_pool.back();
     }
     if (bytes > e->bytes) {
@@ -286,6 +325,12 @@ rdl_status stream_work(hipStream_t s, size_t bytes, size_t ncnt, void** p, int**
         HIP_TRY(hipMalloc(&e->counters, ncnt * sizeof(int)));
         HIP_TRY(hipMemset(e->counters, 0, ncnt * sizeof(int)));
         e->ncnt = ncnt;
+        e->epoch = rdl::xcd_placement_epoch();
+    }
+    if (e->counters && e->epoch != rdl::xcd_placement_epoch()) {
+        // a GEMM launch ran off its XCDs since they were zeroed: zero them again
+        HIP_TRY(rdl::launch_zero_counters(e->counters, e->ncnt, s));
+        e->epoch = rdl::xcd_placement_epoch();
     }
     *p = e->p;
     *counters = e->counters;
@@ -383,9 +428,36 @@ const char* rdl_status_string(rdl_status s) {
 
 const char* rdl_last_error(void) { return g_err.c_str(); }
 
+rdl_status rdl_last_shape_mismatch(size_t* expected, size_t* n_expected, size_t* actual, size_t* n_actual) {
+    if (!expected || !n_expected || !actual || !n_actual) return RDL_ERR_NULL_POINTER;
+    const rdl::ShapeDetail& d = rdl::g_shape;
+    if (d.n_expected == 0 && d.n_actual == 0) return RDL_ERR_INVALID_DATA;  // keeps g_err / g_shape as they are
+    for (size_t i = 0; i < RDL_SHAPE_MAX_DIMS; i++) {
+        expected[i] = i < d.n_expected ? d.expected[i] : 0;
+        actual[i] = i < d.n_actual ? d.actual[i] : 0;
+    }
+    *n_expected = d.n_expected;
+    *n_actual = d.n_actual;
+    return RDL_OK;
+}
+
 const char* rdl_version(void) { return "rdlquant 0.1.0 (gfx950)"; }
 
 int32_t rdl_device_count(void) { return count_devices(); }
+
+rdl_status rdl_set_gemm_combine(int32_t mode) {
+    if (mode != RDL_COMBINE_AUTO && mode != RDL_COMBINE_COHERENT)
+        return fail(RDL_ERR_INVALID_DATA, "unknown combine mode %d", mode);
+    rdl::set_combine_coherent(mode == RDL_COMBINE_COHERENT);
+    return ok();
+}
+
+rdl_status rdl_get_gemm_combine(int32_t* mode, int32_t* local) {
+    if (!mode || !local) return fail(RDL_ERR_NULL_POINTER, "NULL argument");
+    *mode = rdl::combine_is_coherent() ? RDL_COMBINE_COHERENT : RDL_COMBINE_AUTO;
+    *local = rdl::combine_local_now() ? 1 : 0;
+    return ok();
+}
 
 rdl_status rdl_time_next_launch(void* start_event, void* stop_event) {
     rdl::g_launch_events.start = (hipEvent_t)start_event;
@@ -431,10 +503,9 @@ rdl_status rdl_quantize_row_q8_0(const float* input, size_t input_len, uint8_t* 
                     input_len);
     const size_t nb = input_len / rdl::QK;
     if (output_len < nb * rdl::Q8_0_BYTES)
-        return fail(RDL_ERR_SHAPE_MISMATCH, "output bytes: expected %zu, got %zu",
-                    nb * rdl::Q8_0_BYTES, output_len);
+        return rdl::api_shape_fail("output bytes", {nb * rdl::Q8_0_BYTES}, {output_len});
     if (scales_len < nb)
-        return fail(RDL_ERR_SHAPE_MISMATCH, "scales length: expected %zu, got %zu", nb, scales_len);
+        return rdl::api_shape_fail("scales length", {nb}, {scales_len});
     if (nb == 0) return ok();
     if (!input || !output || !scales) return fail(RDL_ERR_NULL_POINTER, "NULL buffer");
     rdl_status st = require_device();
@@ -459,8 +530,7 @@ rdl_status rdl_q4_0_q8_0_block_dots(const float* x, size_t x_len, const uint8_t*
     if (st != RDL_OK) return st;
     const size_t nb = k / rdl::QK;
     if (partials_len < m * n * nb)
-        return fail(RDL_ERR_SHAPE_MISMATCH, "partials length: expected %zu, got %zu", m * n * nb,
-                    partials_len);
+        return rdl::api_shape_fail("partials length", {m * n * nb}, {partials_len});
     if (m * n * nb == 0) return ok();
     if ((st = require_device()) != RDL_OK) return st;
     DevBuf dx, dw, dp, dr;
@@ -498,7 +568,7 @@ rdl_status rdl_weight_upload(const uint8_t* bytes, size_t len, int32_t dtype,
         return fail(RDL_ERR_BLOCK_ALIGNMENT, "in_features %zu not divisible by %s block size %zu",
                     in_features, type_name(t), be);
     const size_t need = out_features * (in_features / be) * rdl::block_bytes(t);
-    if (len < need) return fail(RDL_ERR_SHAPE_MISMATCH, "weight bytes: expected %zu, got %zu", need, len);
+    if (len < need) return rdl::api_shape_fail("weight bytes", {need}, {len});
     if (need && !bytes) return fail(RDL_ERR_NULL_POINTER, "bytes is NULL");
     rdl_status st = require_device();
     if (st != RDL_OK) return st;
@@ -526,7 +596,7 @@ rdl_status rdl_weight_wrap_device(const void* dev_bytes, size_t len, int32_t dty
         return fail(RDL_ERR_BLOCK_ALIGNMENT, "in_features %zu not divisible by %s block size %zu",
                     in_features, type_name(t), be);
     const size_t need = out_features * (in_features / be) * rdl::block_bytes(t);
-    if (len < need) return fail(RDL_ERR_SHAPE_MISMATCH, "weight bytes: expected %zu, got %zu", need, len);
+    if (len < need) return rdl::api_shape_fail("weight bytes", {need}, {len});
     if (need && !dev_bytes) return fail(RDL_ERR_NULL_POINTER, "dev_bytes is NULL");
     if (t == WType::Q4_K && ((uintptr_t)dev_bytes & 15))
         return fail(RDL_ERR_INVALID_DATA, "Q4_K device bytes must be 16-byte aligned");
@@ -584,7 +654,7 @@ rdl_status rdl_linear_forward_dev_noalloc(const rdl_weight* w, const float* x_de
     if (rdl::gemm_counter_count(w->n, w->k) * sizeof(int) > NOALLOC_COUNTER_BYTES)
         return fail(RDL_ERR_UNSUPPORTED, "out_features %zu beyond the static scratch's GEMM counters", w->n);
     void* work = nullptr;
-    rdl_status st = noalloc_scratch(&work);
+    rdl_status st = noalloc_scratch((hipStream_t)stream, &work);
     if (st != RDL_OK) return st;
     int* counters = reinterpret_cast<int*>(reinterpret_cast<uint8_t*>(work) + NOALLOC_DATA_BYTES);
     st = run_linear(w->type, native, (const uint8_t*)w->dev, w->n, w->k, x_dev, m, y_dev, work, counters,

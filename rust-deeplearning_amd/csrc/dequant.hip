@@ -235,7 +235,7 @@ rdl_status rdl_dequantize_gguf_dev(int32_t ggml_type, const void* src_dev, size_
         return rdl::api_fail(RDL_ERR_GGUF_UNSUPPORTED_TYPE, "GGML type: %d", ggml_type);
     const size_t need = (bs > 1 ? n_elements / bs : n_elements) * (size_t)bb;
     if (src_len < need)
-        return rdl::api_fail(RDL_ERR_SHAPE_MISMATCH, "source bytes: expected %zu, got %zu", need, src_len);
+        return rdl::api_shape_fail("source bytes", {need}, {src_len});
     if (n_elements == 0) return rdl::api_ok();
     if (!dst_dev || (need && !src_dev)) return rdl::api_fail(RDL_ERR_NULL_POINTER, "NULL device pointer");
     if ((uintptr_t)dst_dev & 15) return rdl::api_fail(RDL_ERR_INVALID_DATA, "destination must be 16-byte aligned");

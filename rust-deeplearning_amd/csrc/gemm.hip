@@ -32,6 +32,7 @@
 #include <algorithm>
 #include <type_traits>
 
+#include <atomic>
 #include <mutex>
 #include <vector>
 
@@ -592,7 +593,9 @@ __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_kernel(
 // it to keep a strip's K-slices in one L2 (plain partial stores, read back
 // with non-temporal loads by the last slice); the probe below checks it once
 // per device (2 x CUs workgroups record their XCC id), and the kernel falls
-// back to agent-coherent stores and loads where it does not hold.
+// back to agent-coherent stores and loads where it does not hold.  Every
+// workgroup of a LOCAL launch checks its own XCC id as well and flags a
+// mismatch, which moves the device to the coherent combine (xcd_local).
 __global__ void xcd_probe_kernel(int* __restrict__ out) {
     unsigned x;
     asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
@@ -601,27 +604,61 @@ __global__ void xcd_probe_kernel(int* __restrict__ out) {
 
 namespace {
 constexpr int XCD_COUNT = 8;
+constexpr int MAX_DEVICES = 64;
 std::mutex xcd_mu;
-int xcd_state[64] = {};  // per device: 0 unknown, 1 round-robin, 2 not
+int xcd_state[MAX_DEVICES] = {};  // per device: 0 unknown, 1 round-robin, 2 not
+// per device: a flag in pinned host memory that a LOCAL launch sets when one
+// of its workgroups finds itself off XCD blockIdx % 8
+int* xcd_fault[MAX_DEVICES] = {};
+std::atomic<unsigned> xcd_epoch[MAX_DEVICES];  // per device: placement faults seen
+std::atomic<bool> combine_coherent{false};     // testing switch: every combine coherent
 }  // namespace
 
-// True when workgroup b of a launch runs on XCD b % 8 on the current device
-// (probed on a private stream the first time; never probed while `s` is
-// being captured into a graph, which then takes the coherent path).
-bool xcd_round_robin(hipStream_t s) {
+// The check every LOCAL workgroup makes before it relies on sharing an L2
+// with its strip's other slices: its XCC id against the probed placement.
+// A mismatch sets the device's fault flag (a system-scope vector store to
+// pinned host memory); the host sees it at its next GEMM call.
+__device__ __forceinline__ void check_xcd_placement(int* __restrict__ fault) {
+    unsigned x;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+    if ((int)(x & 0xF) != (int)(blockIdx.x % XCD_COUNT) && threadIdx.x == 0)
+        __hip_atomic_store(fault, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// The LOCAL (XCD-local) K-slice combine's fault flag for the current device
+// when workgroup b of a launch runs on XCD b % 8 there (probed on a private
+// stream the first time; never probed while `s` is being captured into a
+// graph), else nullptr: the caller takes the agent-coherent combine.  When
+// an earlier LOCAL launch on the device reported a workgroup off its XCD,
+// the device moves to the coherent combine for good, its placement epoch
+// advances (the GEMM counters' owners zero them again: that launch may have
+// left counts behind) and *fault is set once, for the caller to report.
+int* xcd_local(hipStream_t s, bool* fault) {
+    *fault = false;
+    if (combine_coherent.load()) return nullptr;
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return nullptr;
     std::lock_guard<std::mutex> lock(xcd_mu);
-    if (xcd_state[dev]) return xcd_state[dev] == 1;
+    if (xcd_state[dev] == 1) {
+        if (__atomic_load_n(xcd_fault[dev], __ATOMIC_ACQUIRE) == 0) return xcd_fault[dev];
+        xcd_state[dev] = 2;
+        xcd_epoch[dev].fetch_add(1);
+        *fault = true;
+        return nullptr;
+    }
+    if (xcd_state[dev]) return nullptr;
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (s && hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone) return false;
+    if (s && hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone) return nullptr;
     const int nwg = 2 * device_cu_count();
     int* d = nullptr;
     hipStream_t ps = nullptr;
     bool ok = hipStreamCreateWithFlags(&ps, hipStreamNonBlocking) == hipSuccess &&
-              hipMalloc(&d, nwg * sizeof(int)) == hipSuccess;
+              hipMalloc(&d, nwg * sizeof(int)) == hipSuccess &&
+              hipHostMalloc(reinterpret_cast<void**>(&xcd_fault[dev]), sizeof(int), hipHostMallocDefault) ==
+                  hipSuccess;
     std::vector<int> h(nwg, -1);
     if (ok) {
+        *xcd_fault[dev] = 0;
         hipLaunchKernelGGL(xcd_probe_kernel, dim3(nwg), dim3(64), 0, ps, d);
         ok = hipGetLastError() == hipSuccess && hipStreamSynchronize(ps) == hipSuccess &&
              hipMemcpy(h.data(), d, nwg * sizeof(int), hipMemcpyDeviceToHost) == hipSuccess;
@@ -630,7 +667,7 @@ bool xcd_round_robin(hipStream_t s) {
     if (d) (void)hipFree(d);
     if (ps) (void)hipStreamDestroy(ps);
     xcd_state[dev] = ok ? 1 : 2;
-    return ok;
+    return ok ? xcd_fault[dev] : nullptr;
 }
 
 // ---- skinny GEMM (m <= GEMM_SMALL_M) ----------------------------------------------
@@ -654,7 +691,7 @@ bool xcd_round_robin(hipStream_t s) {
 // complete, and counts itself on the strip's counter; the last of the S sums
 // all S partials in slice order (the same bits whichever workgroup finishes
 // last) and resets the counter to 0 for the next launch.  Where the probed
-// placement holds (xcd_round_robin) a strip's slices share one XCD and the
+// placement holds (xcd_local) a strip's slices share one XCD and the
 // partials stay in its L2 (plain stores, non-temporal loads); elsewhere
 // agent-coherent (sc1) stores and loads.
 constexpr int SK_WAVES = 8;
@@ -691,7 +728,7 @@ constexpr int CPOL_NT = 2, CPOL_SC1 = 16;
 template <int MT, int JT, int WR, bool EVEN, bool LOCAL>
 __global__ __launch_bounds__(SK_WAVES * 64) void gemm_q4_0_skinny_kernel(
     const uint8_t* __restrict__ W, int n, int nb, const float* __restrict__ X, int m, float* __restrict__ Y, int S,
-    int kbs, float* __restrict__ part, int* __restrict__ cnt) {
+    int kbs, float* __restrict__ part, int* __restrict__ cnt, int* __restrict__ fault) {
     using C = SkCfg<MT, JT, WR>;
     constexpr int KBW = C::KBW, KCB = C::KCB, MP = C::MP;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -706,6 +743,7 @@ __global__ __launch_bounds__(SK_WAVES * 64) void gemm_q4_0_skinny_kernel(
     // LOCAL: strip st's slices on XCD st % 8 (one L2), as in the x-tile kernel
     int strip, ks;
     if constexpr (LOCAL) {
+        check_xcd_placement(fault);
         const int xcd = (int)blockIdx.x % XCD_COUNT, i = (int)blockIdx.x / XCD_COUNT;
         strip = (i / S) * XCD_COUNT + xcd;
         ks = i % S;
@@ -1004,7 +1042,7 @@ __global__ __launch_bounds__(SK_WAVES * 64) void gemm_q4_0_skinny_kernel(
 //     128 partial, waits for the stores, counts itself on the strip's counter,
 //     and the last of the S adds all partials in slice order (the same bits
 //     whichever finishes last), resets the counter and stores Y.  Where the
-//     workgroup placement is the probed round-robin (xcd_round_robin), a
+//     workgroup placement is the probed round-robin (xcd_local), a
 //     strip's slices are put on one XCD and the partials stay in its L2:
 //     plain 16-byte stores (acknowledged by the L2), read back with
 //     non-temporal loads, which do not return a stale L1 line; measured at M =
@@ -1035,7 +1073,7 @@ struct XtCfg {
 template <int KB, int MT, bool EVEN, bool LOCAL>
 __global__ __launch_bounds__(XT_WAVES * 64) void gemm_q4_0_xtile_kernel(
     const uint8_t* __restrict__ W, int n, int nb, const float* __restrict__ X, int m, float* __restrict__ Y, int S,
-    int kbs, float* __restrict__ part, int* __restrict__ cnt) {
+    int kbs, float* __restrict__ part, int* __restrict__ cnt, int* __restrict__ fault) {
     using C = XtCfg<KB, MT>;
     constexpr int XR = C::XR, UNITS = C::UNITS;
     __shared__ int last_sh;
@@ -1049,6 +1087,7 @@ __global__ __launch_bounds__(XT_WAVES * 64) void gemm_q4_0_xtile_kernel(
     // probed), so they share one L2; otherwise strips are consecutive slices
     int strip, ks;
     if constexpr (LOCAL) {
+        check_xcd_placement(fault);
         const int xcd = (int)blockIdx.x % XCD_COUNT, i = (int)blockIdx.x / XCD_COUNT;
         strip = (i / S) * XCD_COUNT + xcd;
         ks = i % S;
@@ -1263,7 +1302,7 @@ inline XtPlan xtile_plan(size_t n, int nb, int mt = 1) {
 
 template <int KB, int MT, bool EVEN, bool LOCAL>
 hipError_t launch_xtile_cfg(const uint8_t* w, int n, int nb, const float* x, int m, float* y, const XtPlan& p,
-                           float* part, int* cnt, hipStream_t s) {
+                           float* part, int* cnt, int* fault, hipStream_t s) {
     using C = XtCfg<KB, MT>;
     static_assert(C::LDS <= 160 * 1024, "LDS per workgroup");
     auto kern = gemm_q4_0_xtile_kernel<KB, MT, EVEN, LOCAL>;
@@ -1274,7 +1313,7 @@ hipError_t launch_xtile_cfg(const uint8_t* w, int n, int nb, const float* x, int
     }
     const int strips = LOCAL ? (p.strips + XCD_COUNT - 1) / XCD_COUNT * XCD_COUNT : p.strips;
     launch_kernel(kern, dim3((unsigned)(strips * p.S)), dim3(C::NT), (size_t)C::LDS, s, w, n, nb, x, m, y, p.S,
-                  p.kbs, part, cnt);
+                  p.kbs, part, cnt, fault);
     return hipGetLastError();
 }
 
@@ -1290,12 +1329,14 @@ hipError_t launch_xtile(const uint8_t* w, int n, int nb, const float* x, int m, 
         p.ok = nb <= (mt > 1 ? 16 : 32);
     }
     if (!p.ok) return hipErrorInvalidValue;  // the caller takes the other kernel
-    const bool local = p.S > 1 && xcd_round_robin(s);
+    bool fault = false;
+    int* local = p.S > 1 ? xcd_local(s, &fault) : nullptr;
+    if (fault) return hipErrorLaunchFailure;  // an earlier LOCAL launch ran off its XCDs
     auto go = [&](auto kb_tag, auto mt_tag, auto even_tag) {
         constexpr int KB = decltype(kb_tag)::value, MT = decltype(mt_tag)::value;
         constexpr bool EVEN = decltype(even_tag)::value;
-        return local ? launch_xtile_cfg<KB, MT, EVEN, true>(w, n, nb, x, m, y, p, part, cnt, s)
-                     : launch_xtile_cfg<KB, MT, EVEN, false>(w, n, nb, x, m, y, p, part, cnt, s);
+        return local ? launch_xtile_cfg<KB, MT, EVEN, true>(w, n, nb, x, m, y, p, part, cnt, local, s)
+                     : launch_xtile_cfg<KB, MT, EVEN, false>(w, n, nb, x, m, y, p, part, cnt, nullptr, s);
     };
     using T = std::true_type;
     using F = std::false_type;
@@ -1348,7 +1389,7 @@ inline SkPlan skinny_plan(size_t m, size_t n, int nb, bool can_split) {
 
 template <int MT, int JT, int WR, bool EVEN, bool LOCAL>
 hipError_t launch_skinny_cfg(const uint8_t* w, int n, int nb, const float* x, int m, float* y, const SkPlan& p,
-                             float* part, int* cnt, hipStream_t s) {
+                             float* part, int* cnt, int* fault, hipStream_t s) {
     using C = SkCfg<MT, JT, WR>;
     static_assert(C::LDS <= 160 * 1024, "LDS per workgroup");
     auto kern = gemm_q4_0_skinny_kernel<MT, JT, WR, EVEN, LOCAL>;
@@ -1359,20 +1400,22 @@ hipError_t launch_skinny_cfg(const uint8_t* w, int n, int nb, const float* x, in
     }
     const int strips = LOCAL ? (p.strips + XCD_COUNT - 1) / XCD_COUNT * XCD_COUNT : p.strips;
     launch_kernel(kern, dim3((unsigned)(strips * p.S)), dim3(C::NT), (size_t)C::LDS, s, w, n, nb, x, m, y, p.S,
-                  p.kbs, part, cnt);
+                  p.kbs, part, cnt, fault);
     return hipGetLastError();
 }
 
 hipError_t launch_skinny(const uint8_t* w, int n, int nb, const float* x, int m, float* y, float* part, int* cnt,
                          hipStream_t s) {
     const SkPlan p = skinny_plan((size_t)m, (size_t)n, nb, part != nullptr && cnt != nullptr);
-    const bool local = p.S > 1 && xcd_round_robin(s);
+    bool fault = false;
+    int* local = p.S > 1 ? xcd_local(s, &fault) : nullptr;
+    if (fault) return hipErrorLaunchFailure;  // an earlier LOCAL launch ran off its XCDs
     auto go = [&](auto mt_tag, auto even_tag) {
         constexpr int MT = decltype(mt_tag)::value;
         constexpr bool EVEN = decltype(even_tag)::value;
         constexpr int WR = MT >= 3 ? 2 : 1;
-        return local ? launch_skinny_cfg<MT, 4, WR, EVEN, true>(w, n, nb, x, m, y, p, part, cnt, s)
-                     : launch_skinny_cfg<MT, 4, WR, EVEN, false>(w, n, nb, x, m, y, p, part, cnt, s);
+        return local ? launch_skinny_cfg<MT, 4, WR, EVEN, true>(w, n, nb, x, m, y, p, part, cnt, local, s)
+                     : launch_skinny_cfg<MT, 4, WR, EVEN, false>(w, n, nb, x, m, y, p, part, cnt, nullptr, s);
     };
     using M1 = std::integral_constant<int, 1>;
     using M2 = std::integral_constant<int, 2>;
@@ -1441,6 +1484,23 @@ hipError_t launch_tiles(const uint8_t* w, int n, int nb, const void* x0, const v
 }
 
 }  // namespace
+
+void set_combine_coherent(bool on) { combine_coherent.store(on); }
+bool combine_is_coherent() { return combine_coherent.load(); }
+
+bool combine_local_now() {
+    if (combine_coherent.load()) return false;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return false;
+    std::lock_guard<std::mutex> lock(xcd_mu);
+    return xcd_state[dev] == 1 && __atomic_load_n(xcd_fault[dev], __ATOMIC_ACQUIRE) == 0;
+}
+
+unsigned xcd_placement_epoch() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return 0;
+    return xcd_epoch[dev].load();
+}
 
 __global__ void zero_i32_kernel(int* __restrict__ p, int n) {
     const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);

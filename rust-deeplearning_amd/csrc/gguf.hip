@@ -578,8 +578,8 @@ rdl_status rdl_gguf_upload_tensor(const rdl_gguf* g, size_t i, void* dst_dev, ui
     rdl_status st = rdl_gguf_tensor_data(g, i, &src, &len);
     if (st != RDL_OK) return st;
     if (dst_len < len)
-        return api_fail(RDL_ERR_SHAPE_MISMATCH, "tensor '%s' holds %llu bytes, destination %llu",
-                        g->tensors[i].name.c_str(), (unsigned long long)len, (unsigned long long)dst_len);
+        return rdl::api_shape_fail(("tensor '" + g->tensors[i].name + "' bytes (destination holds the second)").c_str(),
+                                   {(size_t)len}, {(size_t)dst_len});
     if ((st = rdl::api_require_device()) != RDL_OK) return st;
     auto* gm = const_cast<rdl_gguf*>(g);
     std::lock_guard<std::mutex> lk(gm->stage_mu);
@@ -596,8 +596,8 @@ rdl_status rdl_gguf_upload_tensor_f32(const rdl_gguf* g, size_t i, float* dst_de
     if (st != RDL_OK) return st;
     const rdl_gguf::Tensor& t = g->tensors[i];
     if (dst_len < t.n_elements)
-        return api_fail(RDL_ERR_SHAPE_MISMATCH, "tensor '%s' has %llu elements, destination %llu",
-                        t.name.c_str(), (unsigned long long)t.n_elements, (unsigned long long)dst_len);
+        return rdl::api_shape_fail(("tensor '" + t.name + "' elements (destination holds the second)").c_str(),
+                                   {(size_t)t.n_elements}, {(size_t)dst_len});
     if ((uintptr_t)dst_dev & 15) return api_fail(RDL_ERR_INVALID_DATA, "destination must be 16-byte aligned");
     if ((st = rdl::api_require_device()) != RDL_OK) return st;
     if (t.n_elements == 0) return api_ok();

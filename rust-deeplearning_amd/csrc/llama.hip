@@ -642,6 +642,8 @@ struct LlamaModel {
     size_t out_cap = 0;
     void* gemm_scratch = nullptr;
     int* gemm_cnt = nullptr;  // the skinny GEMMs' strip counters (zero between launches)
+    size_t gemm_ncnt = 0;
+    unsigned cnt_epoch = 0;  // workgroup-placement epoch gemm_cnt was last zeroed under
     float* att_part = nullptr;  // [max_batch][n_heads][spans of max_seq][hd + 2]
     int* att_cnt = nullptr;     // [max_batch][n_heads] finished-chunk counters (zero between launches)
     int att_nspan = 0;
@@ -652,6 +654,7 @@ struct LlamaModel {
     uint64_t* att_xch = nullptr;
     size_t xch_stride() const { return (size_t)qkv_dim + q_dim; }
     int* att_err = nullptr;  // set by a fused launch whose wait ran out
+    rdl_llama_path_counts path{};  // attention launches enqueued, by kernel
     hipStream_t stream = nullptr;
     hipGraphExec_t decode_exec = nullptr;
     hipGraph_t decode_graph = nullptr;
@@ -740,6 +743,7 @@ struct LlamaModel {
                         : (hd == 64)  ? prefill_attention_mfma_kernel<64>
                                       : prefill_attention_mfma_kernel<256>;
                 hipLaunchKernelGGL(pk, dim3(cfg.n_heads, (unsigned)((m + 15) / 16)), dim3(256), 0, stream, pa, (int)m);
+                path.prefill_mfma++;
                 return hipGetLastError();
             }
         }
@@ -762,6 +766,7 @@ struct LlamaModel {
                     : (hd == 64)  ? prefill_attention_kernel<KV, 64>
                                   : prefill_attention_kernel<KV, 256>;
             hipLaunchKernelGGL(pk, dim3(cfg.n_heads, (unsigned)((m + 7) / 8)), dim3(512), 0, stream, pa, (int)m);
+            path.prefill_rows++;
             return hipGetLastError();
         }
         // chunks that can hold keys for these rows (every chunk of the cache
@@ -789,6 +794,7 @@ struct LlamaModel {
         aa.counters = att_cnt;
         aa.out = att;
         hipLaunchKernelGGL(kern, grid, dim3(64 * ATT_WAVES), lds, stream, aa);
+        path.attention++;
         return hipGetLastError();
     }
 
@@ -811,6 +817,7 @@ struct LlamaModel {
                                      att, xl, att_err, L.o.dev, L.o.n, x, xl + qkv_dim, stream);
             if (e != hipErrorInvalidValue) {
                 if (e != hipSuccess) return e;
+                path.fused_decode++;
                 return layer_fused_tail(l, m, true);
             }
             (void)hipGetLastError();
@@ -990,6 +997,11 @@ struct LlamaModel {
         const int d = cfg.dim;
         const float eps = cfg.norm_eps;
         hipError_t e = hipSuccess;
+        if (cnt_epoch != xcd_placement_epoch()) {
+            // a GEMM launch ran off its XCDs since the counters were zeroed
+            if ((e = launch_zero_counters(gemm_cnt, gemm_ncnt, stream)) != hipSuccess) return e;
+            cnt_epoch = xcd_placement_epoch();
+        }
         if (embed && (e = launch_dequant_rows(emb.type, emb.dev, emb.n, emb.k, tokens, m, x, stream)) != hipSuccess)
             return e;
         for (int l = 0; l < cfg.n_layers; l++) {
@@ -1269,6 +1281,8 @@ rdl_status rdl_llama_create_typed(const rdl_llama_config* cfg, const int32_t* ty
     if ((e = M.alloc_t(&M.gemm_cnt, gcc)) != hipSuccess) return fail_free(e);
     if ((e = hipMemset(M.gemm_cnt, 0, gcc * sizeof(int))) != hipSuccess)
         return fail_free(e);
+    M.gemm_ncnt = gcc;
+    M.cnt_epoch = rdl::xcd_placement_epoch();
     if (any_split_qkv && (e = M.alloc_t(&M.part_tmp, mb * M.qkv_dim)) != hipSuccess) return fail_free(e);
     // (row-pair epilogues need at most 4 columns per lane: dim <= 8192)
     M.fused_shapes = (c.dim / 32) % 2 == 0 && (M.q_dim / 32) % 2 == 0 && (c.ffn_dim / 32) % 2 == 0 &&
@@ -1322,7 +1336,7 @@ rdl_status rdl_llama_set_weight(rdl_llama* model, int32_t slot, int32_t layer, c
     rdl_status st = slot_target(M, slot, layer, &t);
     if (st != RDL_OK) return st;
     if (len != t.bytes())
-        return api_fail(RDL_ERR_SHAPE_MISMATCH, "slot %d: expected %zu bytes, got %zu", slot, t.bytes(), len);
+        return rdl::api_shape_fail(("slot " + std::to_string(slot) + " bytes").c_str(), {t.bytes()}, {len});
     HIP_TRY(hipMemcpy2D(t.dst, t.dpitch, bytes, t.row_bytes, t.row_bytes, t.rows, hipMemcpyHostToDevice));
     return api_ok();
 }
@@ -1391,7 +1405,7 @@ rdl_status rdl_llama_set_kv_page_table(rdl_llama* model, const int32_t* table, s
     if (!model || !table) return api_fail(RDL_ERR_NULL_POINTER, "NULL argument");
     rdl::LlamaModel& M = model->m;
     if (n != (size_t)M.n_pages)
-        return api_fail(RDL_ERR_SHAPE_MISMATCH, "page table: expected %d entries, got %zu", M.n_pages, n);
+        return rdl::api_shape_fail("page table entries", {(size_t)M.n_pages}, {n});
     if (M.host_pos != 0)
         return api_fail(RDL_ERR_INVALID_DATA, "the page table can change only on an empty cache (position %zu)",
                         M.host_pos);
@@ -1504,6 +1518,12 @@ rdl_status rdl_llama_set_fused_attention(rdl_llama* model, int32_t enable) {
     return api_ok();
 }
 
+rdl_status rdl_llama_get_path_counts(const rdl_llama* model, rdl_llama_path_counts* out) {
+    if (!model || !out) return api_fail(RDL_ERR_NULL_POINTER, "NULL argument");
+    *out = model->m.path;
+    return api_ok();
+}
+
 rdl_status rdl_llama_last_timing(const rdl_llama* model, float* prefill_ms, float* decode_ms) {
     if (!model || !prefill_ms || !decode_ms) return api_fail(RDL_ERR_NULL_POINTER, "NULL argument");
     *prefill_ms = model->m.prefill_ms;
@@ -1515,7 +1535,7 @@ rdl_status rdl_llama_rope_tables(const rdl_llama* model, float* cos_out, float* 
     if (!model || !cos_out || !sin_out) return api_fail(RDL_ERR_NULL_POINTER, "NULL argument");
     const rdl::LlamaModel& M = model->m;
     if (len != M.cos_h.size())
-        return api_fail(RDL_ERR_SHAPE_MISMATCH, "tables hold %zu floats, got %zu", M.cos_h.size(), len);
+        return rdl::api_shape_fail("rope table floats", {M.cos_h.size()}, {len});
     memcpy(cos_out, M.cos_h.data(), len * 4);
     memcpy(sin_out, M.sin_h.data(), len * 4);
     return api_ok();
@@ -1588,12 +1608,6 @@ std::string internal_name(const SlotName& s, int layer) {
     return buf;
 }
 
-std::string dims_str(const rdl_gguf_tensor_info& ti) {
-    std::string r = "[";
-    for (uint32_t d = 0; d < ti.n_dims; d++) r += (d ? ", " : "") + std::to_string(ti.dims[d]);
-    return r + "]";
-}
-
 // Expected GGUF dims (innermost first) of a slot's tensor: {k, n} or {dim}.
 void slot_dims(const rdl_llama_config& c, int slot, uint64_t d[2], uint32_t* nd) {
     const uint64_t q = (uint64_t)c.n_heads * c.head_dim, kv = (uint64_t)c.n_kv_heads * c.head_dim;
@@ -1628,10 +1642,10 @@ rdl_status check_tensor(const rdl_llama_config& c, int slot, const rdl_gguf_tens
     bool same = ti.n_dims == nd;
     for (uint32_t i = 0; same && i < nd; i++) same = ti.dims[i] == d[i];
     if (!same) {
-        const std::string want = nd == 2 ? "[" + std::to_string(d[0]) + ", " + std::to_string(d[1]) + "]"
-                                         : "[" + std::to_string(d[0]) + "]";
-        return api_fail(RDL_ERR_SHAPE_MISMATCH, "tensor '%s': expected dims %s, got %s", ti.name, want.c_str(),
-                        dims_str(ti).c_str());
+        size_t want[2] = {(size_t)d[0], (size_t)d[1]}, got[4] = {};
+        const size_t ng = std::min<size_t>(ti.n_dims, 4);
+        for (size_t i = 0; i < ng; i++) got[i] = (size_t)ti.dims[i];
+        return rdl::api_shape_fail((std::string("tensor '") + ti.name + "' dims").c_str(), want, nd, got, ng);
     }
     return api_ok();
 }

@@ -7,6 +7,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <initializer_list>
+
 #include "../../include/rdl_quant.h"
 
 // HIP_TRY for functions returning rdl_status: a failing HIP call sets the
@@ -22,6 +24,15 @@ namespace rdl {
 
 // Error reporting shared by the C ABI translation units (capi.hip).
 rdl_status api_fail(rdl_status st, const char* fmt, ...);
+// RDL_ERR_SHAPE_MISMATCH with the extents QuantError::ShapeMismatch carries
+// (expected, actual: at most RDL_SHAPE_MAX_DIMS values each), kept for
+// rdl_last_shape_mismatch; the text reads "<what>: expected [..], got [..]".
+rdl_status api_shape_fail(const char* what, const size_t* expected, size_t n_expected, const size_t* actual,
+                          size_t n_actual);
+inline rdl_status api_shape_fail(const char* what, std::initializer_list<size_t> expected,
+                                 std::initializer_list<size_t> actual) {
+    return api_shape_fail(what, expected.begin(), expected.size(), actual.begin(), actual.size());
+}
 rdl_status api_ok();
 rdl_status api_require_device();
 
@@ -169,6 +180,17 @@ size_t gemm_scratch_bytes(size_t m, size_t n, size_t k, bool native);
 size_t gemm_counter_count(size_t n, size_t k);
 // Zeroes `count` GEMM counters with a kernel (no memset node under graph capture).
 hipError_t launch_zero_counters(int* counters, size_t count, hipStream_t s);
+// The skinny / x-tile GEMMs' K-slice combine: on = every launch takes the
+// agent-coherent combine (a testing switch; off: XCD-local where the probed
+// placement holds).
+void set_combine_coherent(bool on);
+bool combine_is_coherent();
+// True when the current device's next combine runs XCD-local (probed
+// placement, no fault seen, switch off); does not probe.
+bool combine_local_now();
+// Placement faults seen on the current device: GEMM counters zeroed under an
+// older value must be zeroed again before use.
+unsigned xcd_placement_epoch();
 hipError_t launch_gemm_q4_0(const uint8_t* w, size_t n, size_t k, const float* x, size_t m, float* y,
                             void* scratch, int* counters, hipStream_t s);
 hipError_t launch_gemm_q4_0_native(const uint8_t* w, size_t n, size_t k, const float* x, size_t m, float* y,

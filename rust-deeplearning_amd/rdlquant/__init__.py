@@ -89,9 +89,14 @@ def _decl(name, restype, *argtypes):
 
 _decl("rdl_status_string", C.c_char_p, _i32)
 _decl("rdl_last_error", C.c_char_p)
+SHAPE_MAX_DIMS = 4  # RDL_SHAPE_MAX_DIMS
+_decl("rdl_last_shape_mismatch", _i32, C.POINTER(_sz), C.POINTER(_sz), C.POINTER(_sz), C.POINTER(_sz))
 _decl("rdl_version", C.c_char_p)
 _decl("rdl_device_count", _i32)
 _decl("rdl_time_next_launch", _i32, _p, _p)
+COMBINE_AUTO, COMBINE_COHERENT = 0, 1
+_decl("rdl_set_gemm_combine", _i32, _i32)
+_decl("rdl_get_gemm_combine", _i32, C.POINTER(_i32), C.POINTER(_i32))
 for _n in ("q8", "q4", "q4_native", "q4_1", "q4_1_native", "q4_k", "q6_k"):
     _decl(f"rdl_matmul_f32_{_n}", _i32, _fp, _sz, _u8p, _sz, _sz, _sz, _sz, _fp, _sz)
 _decl("rdl_quantize_row_q8_0", _i32, _fp, _sz, _u8p, _sz, _fp, _sz)
@@ -127,7 +132,13 @@ class DTypeMismatch(QuantError):
 
 
 class ShapeMismatch(QuantError):
-    pass
+    """QuantError::ShapeMismatch { expected, actual } (error.rs:9-10): the two
+    extents come across the ABI through rdl_last_shape_mismatch."""
+
+    def __init__(self, status: int, message: str, expected=(), actual=()):
+        super().__init__(status, message)
+        self.expected = list(expected)
+        self.actual = list(actual)
 
 
 class BlockAlignment(QuantError):
@@ -150,10 +161,36 @@ _ERRORS = {
 }
 
 
+def last_shape_mismatch():
+    """(expected, actual) extents of this thread's last RDL_ERR_SHAPE_MISMATCH, or None."""
+    e, a = (_sz * SHAPE_MAX_DIMS)(), (_sz * SHAPE_MAX_DIMS)()
+    ne, na = _sz(), _sz()
+    if lib.rdl_last_shape_mismatch(e, C.byref(ne), a, C.byref(na)) != OK:
+        return None
+    return [int(v) for v in e[:ne.value]], [int(v) for v in a[:na.value]]
+
+
 def check(status: int) -> None:
     if status != OK:
         msg = lib.rdl_last_error().decode()
+        if status == ERR_SHAPE_MISMATCH:
+            detail = last_shape_mismatch()
+            raise ShapeMismatch(status, msg, *(detail or ((), ())))
         raise _ERRORS.get(status, DeviceError)(status, msg)
+
+
+def set_gemm_combine(mode: int) -> None:
+    """K-slice combine of the 5-64-row GEMMs: COMBINE_AUTO (XCD-local where
+    the probed placement holds) or COMBINE_COHERENT (testing switch)."""
+    check(lib.rdl_set_gemm_combine(mode))
+
+
+def gemm_combine():
+    """(mode, local): the switch, and whether the current device's next split
+    GEMM takes the XCD-local combine."""
+    mode, local = _i32(), _i32()
+    check(lib.rdl_get_gemm_combine(C.byref(mode), C.byref(local)))
+    return int(mode.value), bool(local.value)
 
 
 def device_count() -> int:

@@ -44,6 +44,13 @@ _decl("rdl_llama_set_kv_page_table", _i32, _p, C.POINTER(C.c_int32), _sz)
 _decl("rdl_llama_set_fused_attention", _i32, _p, _i32)
 
 
+class _PathCounts(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in ("fused_decode", "prefill_mfma", "prefill_rows", "attention")]
+
+
+_decl("rdl_llama_get_path_counts", _i32, _p, C.POINTER(_PathCounts))
+
+
 class _GgufOptions(C.Structure):
     _fields_ = [("max_seq", C.c_int32), ("max_batch", C.c_int32), ("kv_f16", C.c_int32)]
 
@@ -151,6 +158,14 @@ class LlamaModel:
     def set_fused_attention(self, enable: bool) -> None:
         """Decode steps' q/k/v projection, attention and o projection in one launch (default) or three."""
         check(lib.rdl_llama_set_fused_attention(self._h, int(bool(enable))))
+
+    def path_counts(self) -> dict:
+        """Attention launches enqueued so far, by kernel (host-side counts; a
+        captured decode graph counts once, at capture): fused_decode,
+        prefill_mfma, prefill_rows, attention."""
+        c = _PathCounts()
+        check(lib.rdl_llama_get_path_counts(self._h, C.byref(c)))
+        return {n: int(getattr(c, n)) for n, _ in _PathCounts._fields_}
 
     def kv_pages(self):
         """(positions per page, number of pages) of the paged KV cache."""

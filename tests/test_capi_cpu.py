@@ -35,13 +35,31 @@ def test_q4k_block_alignment(rq):
 
 
 def test_short_weight_is_shape_mismatch(rq):
-    with pytest.raises(rq.ShapeMismatch):
+    # QuantError::ShapeMismatch { expected, actual } (error.rs:9-10): both
+    # extents cross the ABI (rdl_last_shape_mismatch), not only the text
+    with pytest.raises(rq.ShapeMismatch) as e:
         rq.matmul_f32_q4(np.zeros(64, np.float32), np.zeros(35, np.uint8), 1, 64, 1)
+    assert (e.value.expected, e.value.actual) == ([36], [35])
+    assert "expected [36], got [35]" in str(e.value)
 
 
 def test_short_input_is_shape_mismatch(rq):
-    with pytest.raises(rq.ShapeMismatch):
+    with pytest.raises(rq.ShapeMismatch) as e:
         rq.matmul_f32_q8(np.zeros(63, np.float32), np.zeros(68, np.uint8), 1, 64, 1)
+    assert (e.value.expected, e.value.actual) == ([64], [63])
+
+
+def test_shape_detail_only_for_shape_mismatch(rq):
+    # another status leaves no extents behind, and the query does not reset the status
+    with pytest.raises(rq.ShapeMismatch):
+        rq.matmul_f32_q4(np.zeros(64, np.float32), np.zeros(35, np.uint8), 1, 64, 1)
+    assert rq.last_shape_mismatch() == ([36], [35])
+    assert rq.last_shape_mismatch() == ([36], [35])
+    with pytest.raises(rq.BlockAlignment):
+        rq.matmul_f32_q4(np.zeros(33, np.float32), np.zeros(35, np.uint8), 1, 33, 1)
+    assert rq.last_shape_mismatch() is None
+    h = C.c_size_t()
+    assert rq.lib.rdl_last_shape_mismatch(None, C.byref(h), None, C.byref(h)) == rq.ERR_NULL_POINTER
 
 
 def test_quantize_row_alignment(rq):
@@ -72,3 +90,13 @@ def test_no_device_is_reported(rq):
 def test_record_bytes(rq):
     assert rq.activation_record_bytes(1, 4096, rq.MODE_FLOAT) == 128 * 128
     assert rq.activation_record_bytes(2, 4096, rq.MODE_NATIVE) == 2 * 128 * 48
+
+
+def test_gemm_combine_switch(rq):
+    # the testing switch of the split GEMMs' combine: modes 0 / 1 only, no device needed
+    with pytest.raises(rq.InvalidData):
+        rq.set_gemm_combine(2)
+    rq.set_gemm_combine(rq.COMBINE_COHERENT)
+    assert rq.gemm_combine() == (rq.COMBINE_COHERENT, False)
+    rq.set_gemm_combine(rq.COMBINE_AUTO)
+    assert rq.gemm_combine()[0] == rq.COMBINE_AUTO

@@ -234,3 +234,47 @@ def test_time_next_launch(rq, gpu):
     torch.cuda.synchronize()
     ms = a.elapsed_time(b)
     assert 0.0005 < ms < 5.0, ms
+
+
+@pytest.mark.parametrize("m", [16, 32, 48, 64])
+def test_gemm_combine_paths_bit_equal(rq, gpu, m):
+    """The K-slice combine of the 5-64-row GEMMs both ways: XCD-local (each
+    strip's slices on one XCD, partials through its L2; the default where the
+    placement probe passes) and agent-coherent (rdl_set_gemm_combine
+    (RDL_COMBINE_COHERENT): write-through partials, device-scope counter).
+    Eager calls and graph replays, equal bit for bit to each other and to the
+    synchronous entry point."""
+    import torch
+
+    n, k = 4096, 4096
+    w = synth.q4_0_weights(n, k, 180 + m)
+    x = synth.activations(m, k, 190 + m)
+    _, h = dev_weight(rq, torch, w, 2, n, k)
+    xt = torch.from_numpy(x.reshape(-1)).cuda()
+    y = torch.empty(m * n, dtype=torch.float32, device="cuda")
+    print(f"case combine paths m={m}", flush=True)
+    got = {}
+    try:
+        for mode in (rq.COMBINE_AUTO, rq.COMBINE_COHERENT):
+            rq.set_gemm_combine(mode)
+            y.fill_(-1.0)
+            h.forward_dev(xt.data_ptr(), m, y.data_ptr(), rq.MODE_FLOAT, torch.cuda.current_stream().cuda_stream)
+            torch.cuda.synchronize()
+            eager = y.cpu().numpy().copy()
+            assert rq.gemm_combine() == (mode, mode == rq.COMBINE_AUTO)  # the local path did run by default
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                h.forward_dev(xt.data_ptr(), m, y.data_ptr(), rq.MODE_FLOAT, torch.cuda.current_stream().cuda_stream)
+            for rep in range(3):
+                y.fill_(-1.0)
+                torch.cuda.synchronize()
+                g.replay()
+                torch.cuda.synchronize()
+                assert np.array_equal(y.cpu().numpy(), eager), f"mode {mode} replay {rep}"
+                _ = (xt * 2).sum().item()  # unrelated eager work between replays
+            got[mode] = eager
+    finally:
+        rq.set_gemm_combine(rq.COMBINE_AUTO)
+    assert np.array_equal(got[rq.COMBINE_AUTO].view(np.uint32), got[rq.COMBINE_COHERENT].view(np.uint32))
+    assert np.array_equal(got[rq.COMBINE_AUTO], rq.matmul_f32_q4(x, w, m, k, n))
+

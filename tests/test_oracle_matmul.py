@@ -84,6 +84,50 @@ def test_native_equals_partials_composition(orc):
     assert np.array_equal(part[0], (nib * codes[None]).sum(axis=2))
 
 
+def _q8_values(orc, row):
+    """quantize_row_q8_0's codes times their f16-rounded block scales, in f64
+    (the activation the native paths dot against; pinned by the closed forms
+    of tests/test_oracle_quant.py)."""
+    codes, sx = orc.quantize_row_q8_0(row)
+    q = codes.reshape(-1, 34)[:, 2:].view(np.int8).astype(np.float64)
+    return (q * sx.astype(np.float64)[:, None]).reshape(-1)
+
+
+@pytest.mark.parametrize("shape", [(3, 512, 24), (1, 4096, 8)])
+def test_q4_1_native_vs_f64(orc, shape):
+    """matmul_f32_q4_1_native (quantize.rs:501-572) is the product of the
+    Q8_0-quantized activation with the Q4_1 weights: y = sum_b sum_j
+    (sx_b q8_j) (d_b nib_j + m_b).  The exact value comes from two
+    independently pinned pieces, the Q8_0 codes / scales and to_f32's Q4_1
+    values; the oracle's f32 result (per block sx (d isum + m qsum), then a
+    sequential sum) must sit within a few f32 roundings of it.  A dropped or
+    sign-flipped m term, a float (unquantized) x or the Q4_0 offset of 8
+    each break the bound."""
+    m, k, n = shape
+    x = synth.activations(m, k, 51)
+    w = synth.q4_1_weights(n, k, 52)
+    y = orc.matmul("q4_1_native", x, w, m, k, n).reshape(m, n)
+    wd = orc.to_f32("q4_1", w, n * k).reshape(n, k).astype(np.float64)
+    b = w.reshape(n, k // 32, 20)
+    d = b[..., 0:2].copy().view(np.float16).astype(np.float64)
+    mv = b[..., 2:4].copy().view(np.float16).astype(np.float64)
+    nib = np.concatenate([b[..., 4:] & 0xF, b[..., 4:] >> 4], axis=2).astype(np.float64)
+    mag = (np.abs(d * nib) + np.abs(mv)).reshape(n, k)  # size of each weight's two terms
+    for r in range(m):
+        xq = _q8_values(orc, x[r])
+        want = wd @ xq
+        bound = 2.0 ** -18 * (mag @ np.abs(xq)) + 1e-12
+        err = np.abs(y[r].astype(np.float64) - want)
+        assert np.all(err <= bound), float((err / bound).max())
+        # the mistakes a restatement could make fail the same bound
+        planted = {"m dropped": (wd - mv[..., 0].repeat(32, axis=1)) @ xq,
+                   "m negated": (wd - 2 * mv[..., 0].repeat(32, axis=1)) @ xq,
+                   "x unquantized": wd @ x[r].astype(np.float64),
+                   "q4_0 offset": (wd - 8 * d[..., 0].repeat(32, axis=1)) @ xq}
+        for name, v in planted.items():
+            assert np.count_nonzero(np.abs(v - want) > bound) >= n // 2, name
+
+
 def test_q4k_exact_small_integers(orc):
     # d, dmin powers of two, small integer q/sc/mn: every product is exact, so
     # the dequantization has a closed form to compare bit for bit.
