@@ -93,19 +93,17 @@ int32_t rdl_device_count(void);
 
 /* Testing switch (no reference counterpart).  The Q4_0 GEMMs for 5-64 rows
  * split K over workgroups whose partials the last one of each strip adds.
- * RDL_COMBINE_AUTO (the default): where the device deals workgroup b to XCD
- * b % 8 (probed once per device) a strip's slices share one XCD and its L2;
- * each of their workgroups checks its XCC id, and a mismatch moves the
- * device to the coherent combine for good and makes the next such call
- * return RDL_ERR_HIP (the launch that ran off its XCDs may have left rows
- * unwritten).  RDL_COMBINE_COHERENT: every launch takes the agent-coherent
- * combine.  Both give the same bits.  Process-wide; set it while no call is
- * in flight. */
+ * RDL_COMBINE_AUTO (the default): where the device deals each launch's
+ * workgroups round-robin over its XCDs (probed once per device), a strip's
+ * slices share one XCD and its L2, and the partials stay there.
+ * RDL_COMBINE_COHERENT: every launch takes the agent-coherent combine
+ * (write-through partials, device-scope counter).  Both give the same bits.
+ * Process-wide; set it while no call is in flight. */
 enum { RDL_COMBINE_AUTO = 0, RDL_COMBINE_COHERENT = 1 };
 rdl_status rdl_set_gemm_combine(int32_t mode);
 /* The switch's mode, and *local = 1 when the current device's next split
- * GEMM launch would take the XCD-local combine (the placement probe, which
- * the first such launch runs, has passed and no fault has been seen). */
+ * GEMM launch takes the XCD-local combine (the placement probe, which the
+ * first such launch runs, has passed). */
 rdl_status rdl_get_gemm_combine(int32_t* mode, int32_t* local);
 
 /* Instrumentation (no reference counterpart): the next GEMV/GEMM kernel the

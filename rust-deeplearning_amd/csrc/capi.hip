@@ -237,7 +237,6 @@ __device__ __align__(256) uint8_t scratch[RDL_NOALLOC_SCRATCH_BYTES];
 constexpr int MAX_DEVICES = 64;
 std::mutex scratch_mu;
 void* scratch_dev[MAX_DEVICES] = {};
-unsigned scratch_epoch[MAX_DEVICES] = {};  // placement epoch its counters were last zeroed under
 
 // The last NOALLOC_COUNTER_BYTES of `scratch` hold the prefill GEMM's counters
 // (zero from load time and left at zero by every launch); nothing else is
@@ -245,10 +244,8 @@ unsigned scratch_epoch[MAX_DEVICES] = {};  // placement epoch its counters were 
 constexpr size_t NOALLOC_COUNTER_BYTES = 64 * 1024;
 constexpr size_t NOALLOC_DATA_BYTES = (size_t)RDL_NOALLOC_SCRATCH_BYTES - NOALLOC_COUNTER_BYTES;
 
-// The current device's address of `scratch`.  After a workgroup-placement
-// fault (a GEMM launch may have left counts behind) the counters are zeroed
-// again on `s`, by a kernel, before they are used.
-rdl_status noalloc_scratch(hipStream_t s, void** out) {
+// The current device's address of `scratch`.
+rdl_status noalloc_scratch(void** out) {
     int dev = 0;
     HIP_TRY(hipGetDevice(&dev));
     if (dev < 0 || dev >= MAX_DEVICES) return fail(RDL_ERR_UNSUPPORTED, "device index %d beyond %d", dev, MAX_DEVICES);
@@ -259,14 +256,6 @@ rdl_status noalloc_scratch(hipStream_t s, void** out) {
         if (e != hipSuccess || !p)
             return fail(RDL_ERR_HIP, "hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));
         scratch_dev[dev] = p;
-        scratch_epoch[dev] = rdl::xcd_placement_epoch();
-    }
-    const unsigned ep = rdl::xcd_placement_epoch();
-    if (scratch_epoch[dev] != ep) {
-        HIP_TRY(rdl::launch_zero_counters(
-            reinterpret_cast<int*>(reinterpret_cast<uint8_t*>(scratch_dev[dev]) + NOALLOC_DATA_BYTES),
-            NOALLOC_COUNTER_BYTES / sizeof(int), s));
-        scratch_epoch[dev] = ep;
     }
     *out = scratch_dev[dev];
     return RDL_OK;
@@ -295,7 +284,6 @@ struct StreamWork {
     size_t bytes;
     int* counters;
     size_t ncnt;
-    unsigned epoch;  // placement epoch the counters were last zeroed under
 };
 std::mutex work_mu;
 std::vector<StreamWork> work_pool;
@@ -308,7 +296,7 @@ rdl_status stream_work(hipStream_t s, size_t bytes, size_t ncnt, void** p, int**
     for (auto& x : work_pool)
         if (x.dev == dev && x.stream == s) e = &x;
     if (!e) {
-        work_pool.push_back({dev, s, nullptr, 0, nullptr, 0, 0});
+        work_pool.push_back({dev, s, nullptr, 0, nullptr, 0});
         e = &work_pool.back();
     }
     if (bytes > e->bytes) {
@@ -325,12 +313,6 @@ rdl_status stream_work(hipStream_t s, size_t bytes, size_t ncnt, void** p, int**
         HIP_TRY(hipMalloc(&e->counters, ncnt * sizeof(int)));
         HIP_TRY(hipMemset(e->counters, 0, ncnt * sizeof(int)));
         e->ncnt = ncnt;
-        e->epoch = rdl::xcd_placement_epoch();
-    }
-    if (e->counters && e->epoch != rdl::xcd_placement_epoch()) {
-        // a GEMM launch ran off its XCDs since they were zeroed: zero them again
-        HIP_TRY(rdl::launch_zero_counters(e->counters, e->ncnt, s));
-        e->epoch = rdl::xcd_placement_epoch();
     }
     *p = e->p;
     *counters = e->counters;
@@ -654,7 +636,7 @@ rdl_status rdl_linear_forward_dev_noalloc(const rdl_weight* w, const float* x_de
     if (rdl::gemm_counter_count(w->n, w->k) * sizeof(int) > NOALLOC_COUNTER_BYTES)
         return fail(RDL_ERR_UNSUPPORTED, "out_features %zu beyond the static scratch's GEMM counters", w->n);
     void* work = nullptr;
-    rdl_status st = noalloc_scratch((hipStream_t)stream, &work);
+    rdl_status st = noalloc_scratch(&work);
     if (st != RDL_OK) return st;
     int* counters = reinterpret_cast<int*>(reinterpret_cast<uint8_t*>(work) + NOALLOC_DATA_BYTES);
     st = run_linear(w->type, native, (const uint8_t*)w->dev, w->n, w->k, x_dev, m, y_dev, work, counters,

@@ -589,13 +589,12 @@ __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_kernel(
 
 // ---- XCD placement ----------------------------------------------------------------------
 // MI355X deals the workgroups of a launch round-robin to its 8 XCDs (each
-// with its own L2): workgroup b runs on XCD b % 8.  The x-tile GEMM relies on
-// it to keep a strip's K-slices in one L2 (plain partial stores, read back
-// with non-temporal loads by the last slice); the probe below checks it once
-// per device (2 x CUs workgroups record their XCC id), and the kernel falls
-// back to agent-coherent stores and loads where it does not hold.  Every
-// workgroup of a LOCAL launch checks its own XCC id as well and flags a
-// mismatch, which moves the device to the coherent combine (xcd_local).
+// with its own L2): workgroup b runs on XCD (b + o) % 8, o fixed for the
+// launch.  The x-tile GEMM relies on it to keep a strip's K-slices, which
+// share b % 8, in one L2 (plain partial stores, read back with non-temporal
+// loads by the last slice); the probe below checks it once per device, and
+// the kernel falls back to agent-coherent stores and loads where it does not
+// hold.
 __global__ void xcd_probe_kernel(int* __restrict__ out) {
     unsigned x;
     asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
@@ -606,68 +605,45 @@ namespace {
 constexpr int XCD_COUNT = 8;
 constexpr int MAX_DEVICES = 64;
 std::mutex xcd_mu;
-int xcd_state[MAX_DEVICES] = {};  // per device: 0 unknown, 1 round-robin, 2 not
-// per device: a flag in pinned host memory that a LOCAL launch sets when one
-// of its workgroups finds itself off XCD blockIdx % 8
-int* xcd_fault[MAX_DEVICES] = {};
-std::atomic<unsigned> xcd_epoch[MAX_DEVICES];  // per device: placement faults seen
-std::atomic<bool> combine_coherent{false};     // testing switch: every combine coherent
+int xcd_state[MAX_DEVICES] = {};             // per device: 0 unknown, 1 rotation, 2 not
+std::atomic<bool> combine_coherent{false};  // testing switch: every combine coherent
 }  // namespace
 
-// The check every LOCAL workgroup makes before it relies on sharing an L2
-// with its strip's other slices: its XCC id against the probed placement.
-// A mismatch sets the device's fault flag (a system-scope vector store to
-// pinned host memory); the host sees it at its next GEMM call.
-__device__ __forceinline__ void check_xcd_placement(int* __restrict__ fault) {
-    unsigned x;
-    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
-    if ((int)(x & 0xF) != (int)(blockIdx.x % XCD_COUNT) && threadIdx.x == 0)
-        __hip_atomic_store(fault, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-}
-
-// The LOCAL (XCD-local) K-slice combine's fault flag for the current device
-// when workgroup b of a launch runs on XCD b % 8 there (probed on a private
-// stream the first time; never probed while `s` is being captured into a
-// graph), else nullptr: the caller takes the agent-coherent combine.  When
-// an earlier LOCAL launch on the device reported a workgroup off its XCD,
-// the device moves to the coherent combine for good, its placement epoch
-// advances (the GEMM counters' owners zero them again: that launch may have
-// left counts behind) and *fault is set once, for the caller to report.
-int* xcd_local(hipStream_t s, bool* fault) {
-    *fault = false;
-    if (combine_coherent.load()) return nullptr;
+// True when, on the current device, every launch deals its workgroups
+// round-robin to the 8 XCDs from some starting XCD: workgroup b on XCD (b +
+// o) % 8.  The starting XCD o depends on the hardware queue (measured on
+// MI355X: 6, 7, 0, 0, 7, 6 for six streams, each the same on every launch,
+// also with two queues' launches in flight together), so what the probe
+// checks -- on a private stream, 2 x CUs workgroups recording their XCC id
+// -- is the rotation, not o = 0.  Under it all workgroups with one b % 8 share
+// an XCD, which is all the XCD-local combine needs.  Probed once per device,
+// never while `s` is being captured into a graph (that call takes the
+// coherent combine); false while the testing switch asks for the coherent
+// combine.
+bool xcd_round_robin(hipStream_t s) {
+    if (combine_coherent.load()) return false;
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return nullptr;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return false;
     std::lock_guard<std::mutex> lock(xcd_mu);
-    if (xcd_state[dev] == 1) {
-        if (__atomic_load_n(xcd_fault[dev], __ATOMIC_ACQUIRE) == 0) return xcd_fault[dev];
-        xcd_state[dev] = 2;
-        xcd_epoch[dev].fetch_add(1);
-        *fault = true;
-        return nullptr;
-    }
-    if (xcd_state[dev]) return nullptr;
+    if (xcd_state[dev]) return xcd_state[dev] == 1;
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (s && hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone) return nullptr;
+    if (s && hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone) return false;
     const int nwg = 2 * device_cu_count();
     int* d = nullptr;
     hipStream_t ps = nullptr;
     bool ok = hipStreamCreateWithFlags(&ps, hipStreamNonBlocking) == hipSuccess &&
-              hipMalloc(&d, nwg * sizeof(int)) == hipSuccess &&
-              hipHostMalloc(reinterpret_cast<void**>(&xcd_fault[dev]), sizeof(int), hipHostMallocDefault) ==
-                  hipSuccess;
+              hipMalloc(&d, nwg * sizeof(int)) == hipSuccess;
     std::vector<int> h(nwg, -1);
     if (ok) {
-        *xcd_fault[dev] = 0;
         hipLaunchKernelGGL(xcd_probe_kernel, dim3(nwg), dim3(64), 0, ps, d);
         ok = hipGetLastError() == hipSuccess && hipStreamSynchronize(ps) == hipSuccess &&
              hipMemcpy(h.data(), d, nwg * sizeof(int), hipMemcpyDeviceToHost) == hipSuccess;
     }
-    for (int b = 0; ok && b < nwg; b++) ok = h[b] == b % XCD_COUNT;
+    for (int b = 0; ok && b < nwg; b++) ok = h[b] == (h[0] + b) % XCD_COUNT;
     if (d) (void)hipFree(d);
     if (ps) (void)hipStreamDestroy(ps);
     xcd_state[dev] = ok ? 1 : 2;
-    return ok ? xcd_fault[dev] : nullptr;
+    return ok;
 }
 
 // ---- skinny GEMM (m <= GEMM_SMALL_M) ----------------------------------------------
@@ -691,7 +667,7 @@ int* xcd_local(hipStream_t s, bool* fault) {
 // complete, and counts itself on the strip's counter; the last of the S sums
 // all S partials in slice order (the same bits whichever workgroup finishes
 // last) and resets the counter to 0 for the next launch.  Where the probed
-// placement holds (xcd_local) a strip's slices share one XCD and the
+// placement holds (xcd_round_robin) a strip's slices share one XCD and the
 // partials stay in its L2 (plain stores, non-temporal loads); elsewhere
 // agent-coherent (sc1) stores and loads.
 constexpr int SK_WAVES = 8;
@@ -728,7 +704,7 @@ constexpr int CPOL_NT = 2, CPOL_SC1 = 16;
 template <int MT, int JT, int WR, bool EVEN, bool LOCAL>
 __global__ __launch_bounds__(SK_WAVES * 64) void gemm_q4_0_skinny_kernel(
     const uint8_t* __restrict__ W, int n, int nb, const float* __restrict__ X, int m, float* __restrict__ Y, int S,
-    int kbs, float* __restrict__ part, int* __restrict__ cnt, int* __restrict__ fault) {
+    int kbs, float* __restrict__ part, int* __restrict__ cnt) {
     using C = SkCfg<MT, JT, WR>;
     constexpr int KBW = C::KBW, KCB = C::KCB, MP = C::MP;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -740,10 +716,9 @@ __global__ __launch_bounds__(SK_WAVES * 64) void gemm_q4_0_skinny_kernel(
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, r = lane & 15, h = g & 1;
     const int wr = wave / C::WK, wk = wave % C::WK;
-    // LOCAL: strip st's slices on XCD st % 8 (one L2), as in the x-tile kernel
+    // LOCAL: strip st's slices share b % 8 = st % 8, so one XCD (one L2), as in the x-tile kernel
     int strip, ks;
     if constexpr (LOCAL) {
-        check_xcd_placement(fault);
         const int xcd = (int)blockIdx.x % XCD_COUNT, i = (int)blockIdx.x / XCD_COUNT;
         strip = (i / S) * XCD_COUNT + xcd;
         ks = i % S;
@@ -963,7 +938,7 @@ __global__ __launch_bounds__(SK_WAVES * 64) void gemm_q4_0_skinny_kernel(
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partials have completed
         __syncthreads();
         if (tid == 0) {
-            // LOCAL: the strip's slices all run on this XCD (strip % 8), so the
+            // LOCAL: the strip's slices all run on this XCD (one b % 8), so the
             // count lives in its L2: an L2 atomic, not a device-scope one
             // written through past it (M = 16: 10.9 -> 10.6 us a call)
             const int old = __hip_atomic_fetch_add(cnt + strip, 1, __ATOMIC_RELAXED,
@@ -1042,7 +1017,7 @@ __global__ __launch_bounds__(SK_WAVES * 64) void gemm_q4_0_skinny_kernel(
 //     128 partial, waits for the stores, counts itself on the strip's counter,
 //     and the last of the S adds all partials in slice order (the same bits
 //     whichever finishes last), resets the counter and stores Y.  Where the
-//     workgroup placement is the probed round-robin (xcd_local), a
+//     workgroup placement is the probed round-robin (xcd_round_robin), a
 //     strip's slices are put on one XCD and the partials stay in its L2:
 //     plain 16-byte stores (acknowledged by the L2), read back with
 //     non-temporal loads, which do not return a stale L1 line; measured at M =
@@ -1073,7 +1048,7 @@ struct XtCfg {
 template <int KB, int MT, bool EVEN, bool LOCAL>
 __global__ __launch_bounds__(XT_WAVES * 64) void gemm_q4_0_xtile_kernel(
     const uint8_t* __restrict__ W, int n, int nb, const float* __restrict__ X, int m, float* __restrict__ Y, int S,
-    int kbs, float* __restrict__ part, int* __restrict__ cnt, int* __restrict__ fault) {
+    int kbs, float* __restrict__ part, int* __restrict__ cnt) {
     using C = XtCfg<KB, MT>;
     constexpr int XR = C::XR, UNITS = C::UNITS;
     __shared__ int last_sh;
@@ -1083,11 +1058,11 @@ __global__ __launch_bounds__(XT_WAVES * 64) void gemm_q4_0_xtile_kernel(
     float* sc_s = reinterpret_cast<float*>(lds + 2 * C::X_BYTES);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, r = lane & 15, h = g & 1;
-    // local: strip st's slices run on XCD st % 8 (workgroup b on XCD b % 8,
-    // probed), so they share one L2; otherwise strips are consecutive slices
+    // local: strip st's slices are the workgroups b with b % 8 = st % 8, which
+    // run on one XCD (a rotation of b % 8, probed) and share its L2; otherwise
+    // strips are consecutive slices
     int strip, ks;
     if constexpr (LOCAL) {
-        check_xcd_placement(fault);
         const int xcd = (int)blockIdx.x % XCD_COUNT, i = (int)blockIdx.x / XCD_COUNT;
         strip = (i / S) * XCD_COUNT + xcd;
         ks = i % S;
@@ -1226,7 +1201,7 @@ __global__ __launch_bounds__(XT_WAVES * 64) void gemm_q4_0_xtile_kernel(
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partial has completed
         __syncthreads();
         if (tid == 0) {
-            // LOCAL: the strip's slices all run on this XCD (strip % 8), so the
+            // LOCAL: the strip's slices all run on this XCD (one b % 8), so the
             // count lives in its L2: an L2 atomic, not a device-scope one
             // written through past it (M = 16: 10.9 -> 10.6 us a call)
             const int old = __hip_atomic_fetch_add(cnt + strip, 1, __ATOMIC_RELAXED,
@@ -1302,7 +1277,7 @@ inline XtPlan xtile_plan(size_t n, int nb, int mt = 1) {
 
 template <int KB, int MT, bool EVEN, bool LOCAL>
 hipError_t launch_xtile_cfg(const uint8_t* w, int n, int nb, const float* x, int m, float* y, const XtPlan& p,
-                           float* part, int* cnt, int* fault, hipStream_t s) {
+                           float* part, int* cnt, hipStream_t s) {
     using C = XtCfg<KB, MT>;
     static_assert(C::LDS <= 160 * 1024, "LDS per workgroup");
     auto kern = gemm_q4_0_xtile_kernel<KB, MT, EVEN, LOCAL>;
@@ -1313,7 +1288,7 @@ hipError_t launch_xtile_cfg(const uint8_t* w, int n, int nb, const float* x, int
     }
     const int strips = LOCAL ? (p.strips + XCD_COUNT - 1) / XCD_COUNT * XCD_COUNT : p.strips;
     launch_kernel(kern, dim3((unsigned)(strips * p.S)), dim3(C::NT), (size_t)C::LDS, s, w, n, nb, x, m, y, p.S,
-                  p.kbs, part, cnt, fault);
+                  p.kbs, part, cnt);
     return hipGetLastError();
 }
 
@@ -1329,14 +1304,12 @@ hipError_t launch_xtile(const uint8_t* w, int n, int nb, const float* x, int m, 
         p.ok = nb <= (mt > 1 ? 16 : 32);
     }
     if (!p.ok) return hipErrorInvalidValue;  // the caller takes the other kernel
-    bool fault = false;
-    int* local = p.S > 1 ? xcd_local(s, &fault) : nullptr;
-    if (fault) return hipErrorLaunchFailure;  // an earlier LOCAL launch ran off its XCDs
+    const bool local = p.S > 1 && xcd_round_robin(s);
     auto go = [&](auto kb_tag, auto mt_tag, auto even_tag) {
         constexpr int KB = decltype(kb_tag)::value, MT = decltype(mt_tag)::value;
         constexpr bool EVEN = decltype(even_tag)::value;
-        return local ? launch_xtile_cfg<KB, MT, EVEN, true>(w, n, nb, x, m, y, p, part, cnt, local, s)
-                     : launch_xtile_cfg<KB, MT, EVEN, false>(w, n, nb, x, m, y, p, part, cnt, nullptr, s);
+        return local ? launch_xtile_cfg<KB, MT, EVEN, true>(w, n, nb, x, m, y, p, part, cnt, s)
+                     : launch_xtile_cfg<KB, MT, EVEN, false>(w, n, nb, x, m, y, p, part, cnt, s);
     };
     using T = std::true_type;
     using F = std::false_type;
@@ -1389,7 +1362,7 @@ inline SkPlan skinny_plan(size_t m, size_t n, int nb, bool can_split) {
 
 template <int MT, int JT, int WR, bool EVEN, bool LOCAL>
 hipError_t launch_skinny_cfg(const uint8_t* w, int n, int nb, const float* x, int m, float* y, const SkPlan& p,
-                             float* part, int* cnt, int* fault, hipStream_t s) {
+                             float* part, int* cnt, hipStream_t s) {
     using C = SkCfg<MT, JT, WR>;
     static_assert(C::LDS <= 160 * 1024, "LDS per workgroup");
     auto kern = gemm_q4_0_skinny_kernel<MT, JT, WR, EVEN, LOCAL>;
@@ -1400,22 +1373,20 @@ hipError_t launch_skinny_cfg(const uint8_t* w, int n, int nb, const float* x, in
     }
     const int strips = LOCAL ? (p.strips + XCD_COUNT - 1) / XCD_COUNT * XCD_COUNT : p.strips;
     launch_kernel(kern, dim3((unsigned)(strips * p.S)), dim3(C::NT), (size_t)C::LDS, s, w, n, nb, x, m, y, p.S,
-                  p.kbs, part, cnt, fault);
+                  p.kbs, part, cnt);
     return hipGetLastError();
 }
 
 hipError_t launch_skinny(const uint8_t* w, int n, int nb, const float* x, int m, float* y, float* part, int* cnt,
                          hipStream_t s) {
     const SkPlan p = skinny_plan((size_t)m, (size_t)n, nb, part != nullptr && cnt != nullptr);
-    bool fault = false;
-    int* local = p.S > 1 ? xcd_local(s, &fault) : nullptr;
-    if (fault) return hipErrorLaunchFailure;  // an earlier LOCAL launch ran off its XCDs
+    const bool local = p.S > 1 && xcd_round_robin(s);
     auto go = [&](auto mt_tag, auto even_tag) {
         constexpr int MT = decltype(mt_tag)::value;
         constexpr bool EVEN = decltype(even_tag)::value;
         constexpr int WR = MT >= 3 ? 2 : 1;
-        return local ? launch_skinny_cfg<MT, 4, WR, EVEN, true>(w, n, nb, x, m, y, p, part, cnt, local, s)
-                     : launch_skinny_cfg<MT, 4, WR, EVEN, false>(w, n, nb, x, m, y, p, part, cnt, nullptr, s);
+        return local ? launch_skinny_cfg<MT, 4, WR, EVEN, true>(w, n, nb, x, m, y, p, part, cnt, s)
+                     : launch_skinny_cfg<MT, 4, WR, EVEN, false>(w, n, nb, x, m, y, p, part, cnt, s);
     };
     using M1 = std::integral_constant<int, 1>;
     using M2 = std::integral_constant<int, 2>;
@@ -1493,13 +1464,7 @@ bool combine_local_now() {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return false;
     std::lock_guard<std::mutex> lock(xcd_mu);
-    return xcd_state[dev] == 1 && __atomic_load_n(xcd_fault[dev], __ATOMIC_ACQUIRE) == 0;
-}
-
-unsigned xcd_placement_epoch() {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return 0;
-    return xcd_epoch[dev].load();
+    return xcd_state[dev] == 1;
 }
 
 __global__ void zero_i32_kernel(int* __restrict__ p, int n) {

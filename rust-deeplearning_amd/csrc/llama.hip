@@ -642,8 +642,6 @@ struct LlamaModel {
     size_t out_cap = 0;
     void* gemm_scratch = nullptr;
     int* gemm_cnt = nullptr;  // the skinny GEMMs' strip counters (zero between launches)
-    size_t gemm_ncnt = 0;
-    unsigned cnt_epoch = 0;  // workgroup-placement epoch gemm_cnt was last zeroed under
     float* att_part = nullptr;  // [max_batch][n_heads][spans of max_seq][hd + 2]
     int* att_cnt = nullptr;     // [max_batch][n_heads] finished-chunk counters (zero between launches)
     int att_nspan = 0;
@@ -997,11 +995,6 @@ struct LlamaModel {
         const int d = cfg.dim;
         const float eps = cfg.norm_eps;
         hipError_t e = hipSuccess;
-        if (cnt_epoch != xcd_placement_epoch()) {
-            // a GEMM launch ran off its XCDs since the counters were zeroed
-            if ((e = launch_zero_counters(gemm_cnt, gemm_ncnt, stream)) != hipSuccess) return e;
-            cnt_epoch = xcd_placement_epoch();
-        }
         if (embed && (e = launch_dequant_rows(emb.type, emb.dev, emb.n, emb.k, tokens, m, x, stream)) != hipSuccess)
             return e;
         for (int l = 0; l < cfg.n_layers; l++) {
@@ -1281,8 +1274,6 @@ rdl_status rdl_llama_create_typed(const rdl_llama_config* cfg, const int32_t* ty
     if ((e = M.alloc_t(&M.gemm_cnt, gcc)) != hipSuccess) return fail_free(e);
     if ((e = hipMemset(M.gemm_cnt, 0, gcc * sizeof(int))) != hipSuccess)
         return fail_free(e);
-    M.gemm_ncnt = gcc;
-    M.cnt_epoch = rdl::xcd_placement_epoch();
     if (any_split_qkv && (e = M.alloc_t(&M.part_tmp, mb * M.qkv_dim)) != hipSuccess) return fail_free(e);
     // (row-pair epilogues need at most 4 columns per lane: dim <= 8192)
     M.fused_shapes = (c.dim / 32) % 2 == 0 && (M.q_dim / 32) % 2 == 0 && (c.ffn_dim / 32) % 2 == 0 &&

@@ -185,12 +185,9 @@ hipError_t launch_zero_counters(int* counters, size_t count, hipStream_t s);
 // placement holds).
 void set_combine_coherent(bool on);
 bool combine_is_coherent();
-// True when the current device's next combine runs XCD-local (probed
-// placement, no fault seen, switch off); does not probe.
+// True when the current device's next combine runs XCD-local (placement
+// probed and a rotation, switch off); does not probe.
 bool combine_local_now();
-// Placement faults seen on the current device: GEMM counters zeroed under an
-// older value must be zeroed again before use.
-unsigned xcd_placement_epoch();
 hipError_t launch_gemm_q4_0(const uint8_t* w, size_t n, size_t k, const float* x, size_t m, float* y,
                             void* scratch, int* counters, hipStream_t s);
 hipError_t launch_gemm_q4_0_native(const uint8_t* w, size_t n, size_t k, const float* x, size_t m, float* y,

@@ -16,9 +16,26 @@ KIND = {2: "q4", 3: "q4_1", 8: "q8", 12: "q4k", 14: "q6k"}  # GGML type -> oracl
 DEQ = {2: "q4_0", 3: "q4_1", 8: "q8_0", 12: "q4k", 14: "q6k"}  # GGML type -> oracle to_f32 kind
 
 
-def tiny_weights(cfg, seed=1234, types=None):
+def centered_q4_0_weights(n, k, seed, d_sigma=0.02):
+    """Q4_0 blocks whose codes are uniform in 1..15, so q - 8 has mean 0.
+    BASELINE's codes (uniform in 0..15) give every weight a mean of -d/2;
+    stacked over layers that common mode swamps the residual stream and the
+    logits barely depend on the tokens or the attention.  Centered codes
+    keep a decoder sensitive to what its attention does."""
+    r = np.random.default_rng(seed)
+    nb = k // 32
+    q = r.integers(1, 16, size=(n, nb, 32), dtype=np.uint8)
+    d = synth.f16_bits(np.abs(r.normal(0.0, d_sigma, size=(n, nb))) / 8.0)
+    out = np.empty((n, nb, 18), dtype=np.uint8)
+    out[..., 0:2] = d[..., None].view(np.uint8).reshape(n, nb, 2)
+    out[..., 2:] = synth.pack_q4_nibbles(q)
+    return out.reshape(-1)
+
+
+def tiny_weights(cfg, seed=1234, types=None, centered=False):
     """(gpu_slots, oracle_weights): the same seeded bytes for both sides.
-    types: {(slot, layer): GGML type} for matrices that are not Q4_0."""
+    types: {(slot, layer): GGML type} for matrices that are not Q4_0;
+    centered: Q4_0 matrices with zero-mean codes (centered_q4_0_weights)."""
     from rdlquant import llama as L
     from oracle import oracle as orc
     rng = np.random.default_rng(seed)
@@ -30,7 +47,10 @@ def tiny_weights(cfg, seed=1234, types=None):
     def mat(slot, layer, n, k):
         nonlocal s
         s += 1
-        return synth.weights(types.get((slot, layer), 2), n, k, s)
+        t = types.get((slot, layer), 2)
+        if centered and t == 2:
+            return centered_q4_0_weights(n, k, s)
+        return synth.weights(t, n, k, s)
 
     def norm():
         return (1.0 + 0.1 * rng.standard_normal(cfg.dim)).astype(np.float32)

@@ -12,9 +12,9 @@ from llama_fixtures import tiny_config, tiny_weights
 pytestmark = pytest.mark.gpu
 
 
-def build(cfg, seed=1234):
+def build(cfg, seed=1234, centered=False):
     from rdlquant.llama import LlamaModel
-    slots, ref_w = tiny_weights(cfg, seed)
+    slots, ref_w = tiny_weights(cfg, seed, centered=centered)
     m = LlamaModel(cfg)
     for slot, layer, arr in slots:
         m.set_weight(slot, layer, arr)
@@ -23,11 +23,12 @@ def build(cfg, seed=1234):
 
 
 # Bound between an f16 KV cache and the reference's f32 KVCache
-# (kv_cache.rs:23-114): rounding K and V to f16 (11 significant bits) moves
-# the logits by far less than 1% of the largest one.  This is the parity gap
-# of the default decoder (kv_f16 = 1) to the reference; the f16 tests also
-# compare, at the f32 bar, against the oracle that stores K / V rounded alike.
-F16_CACHE_BOUND = 1e-2
+# (kv_cache.rs:23-114): rounding K and V to f16 (11 significant bits) moved
+# the logits of the config-5 geometry tests by 1.8e-4 to 2.6e-4 of the
+# largest one on MI355X; the bound is 2e-3.  This is the parity gap of the
+# default decoder (kv_f16 = 1) to the reference; the f16 tests also compare,
+# at the f32 bar, against the oracle that stores K / V rounded alike.
+F16_CACHE_BOUND = 2e-3
 
 
 def assert_within_f16_cache_bound(got, want32):
@@ -202,19 +203,20 @@ def test_config5_shape_synthetic_weights(rq, gpu):
     m.reset()
     b = m.generate_greedy(prompt, 6)
     assert a.tolist() == b.tolist()  # deterministic
-    # Decode steps (the fused q/k/v + attention + o launch over the f16 cache,
-    # 4 query heads per KV head) against a prefill of the same sequence (the
-    # GEMM and the prompt-chunk attention): every logit, not only the argmax
-    # (this seeded model repeats one token, so argmax equality alone would not
-    # see an attention error).  The two paths round differently (GEMV against
-    # GEMM sums, K / V from either rounded to f16), hence the f16-cache bound.
+    # This seeded model is almost blind to its input: its Q4_0 codes are
+    # uniform in 0..15, so every weight carries a mean of -d/2 and the
+    # residual stream is dominated by that common mode (the logits move by
+    # about 2e-5 of 8 from one step to the next).  Logits here therefore
+    # check determinism and that the 7B launch shapes agree with each other;
+    # oracle parity of this attention geometry is
+    # test_config5_attention_path_f16_cache's.
+    # (1) Decode steps against a prefill of the same sequence (GEMM and
+    # prompt-chunk attention): the paths round differently (GEMV against GEMM
+    # sums, K / V from either rounded to f16).
     m.reset()
     seq = list(prompt) + a[:-1].tolist()
-    logits = m.forward_with_cache(prompt)
-    dec = []
-    for t in a[:-1].tolist():
-        prev, logits = logits, m.decode_step(t)
-        dec.append(logits)
+    m.forward_with_cache(prompt)
+    dec = [m.decode_step(t) for t in a[:-1].tolist()]
     m.reset()
     m.forward_with_cache(seq[:cfg.max_batch])
     pre = m.forward_with_cache(seq[cfg.max_batch:])
@@ -223,8 +225,18 @@ def test_config5_shape_synthetic_weights(rq, gpu):
     err = np.abs(dec[-1].astype(np.float64) - pre).max()
     print(f"  7B decode vs prefill logits: max err {err:.3g} of max |logit| {scale:.3g}")
     assert err <= 1e-3 * scale, (err, scale)
-    # the comparison can fail: consecutive steps' logits differ far beyond it
-    assert np.abs(dec[-1].astype(np.float64) - dec[-2]).max() > 20 * 1e-3 * scale
+    # (2) The fused decode launch (q/k/v + attention + o at 4 query heads per
+    # KV head, head dim 128, f16 cache) against the three separate launches,
+    # bit for bit, at every step.
+    c0 = m.path_counts()
+    m.reset()
+    m.set_fused_attention(False)
+    m.forward_with_cache(prompt)
+    dec3 = [m.decode_step(t) for t in a[:-1].tolist()]
+    m.set_fused_attention(True)
+    assert m.path_counts()["fused_decode"] == c0["fused_decode"]
+    for i, (f, u) in enumerate(zip(dec, dec3)):
+        assert np.array_equal(f.view(np.uint32), u.view(np.uint32)), f"step {i}"
 
 
 @pytest.mark.parametrize("kw", [
@@ -464,7 +476,10 @@ def test_typed_create_rejects(rq, gpu):
 def config5_attention_config(**kw):
     """BASELINE config 5's attention geometry (hidden 4096, 32 query heads over
     8 KV heads of dim 128, f16 cache) on two layers with a narrow FFN and
-    vocabulary, so that the oracle runs in seconds."""
+    vocabulary, so that the oracle runs in seconds.  Its tests use centered
+    Q4_0 codes, which keep the logits sensitive to the attention (a dropped
+    current key moves most of them past the parity bar; with BASELINE's codes
+    it moves none: test_oracle_llama.py)."""
     base = dict(dim=4096, n_layers=2, n_heads=32, n_kv_heads=8, head_dim=128, ffn_dim=512, vocab=320,
                 max_seq=1024, max_batch=128, kv_f16=True)
     base.update(kw)
@@ -483,7 +498,7 @@ def test_config5_attention_path_f16_cache(rq, gpu):
     (repeat_kv, ops.rs:955-995; attention.rs:401-446)."""
     cfg = config5_attention_config()
     print("case config-5 attention path, f16 cache, 32/8 x 128, dim 4096", flush=True)
-    m, ref = build(cfg, seed=505)
+    m, ref = build(cfg, seed=505, centered=True)
     ref32 = LlamaRef(cfg, ref.w, kv_f16=False)
     prompt = np.random.default_rng(5005).integers(0, cfg.vocab, 640)
 
@@ -529,7 +544,7 @@ def test_config5_f16_kernels_against_f32_reference(rq, gpu):
     3-row chunk (the per-row span kernel) and fused one-row steps."""
     cfg = config5_attention_config(max_seq=256)
     print("case config-5 f16 kernels vs f32 cache", flush=True)
-    m, ref = build(cfg, seed=606)
+    m, ref = build(cfg, seed=606, centered=True)
     ref32 = LlamaRef(cfg, ref.w, kv_f16=False)
     prompt = np.random.default_rng(6006).integers(0, cfg.vocab, 147)
     c0 = m.path_counts()
@@ -564,8 +579,8 @@ def test_fused_decode_two_rows_a_wave(rq, gpu, kv_f16, hd):
     cfg = tiny_config(dim=4352, n_layers=2, n_heads=nh, n_kv_heads=nh // 4, head_dim=hd, ffn_dim=512,
                       vocab=320, max_seq=128, max_batch=64, kv_f16=kv_f16)
     print(f"case fused decode R=2 kv_f16={kv_f16} hd={hd}", flush=True)
-    a, ref = build(cfg, seed=4352)
-    b, _ = build(cfg, seed=4352)
+    a, ref = build(cfg, seed=4352, centered=True)
+    b, _ = build(cfg, seed=4352, centered=True)
     b.set_fused_attention(False)
     prompt = np.random.default_rng(4353).integers(0, cfg.vocab, 64)
     la, lb = a.forward_with_cache(prompt), b.forward_with_cache(prompt)

@@ -201,3 +201,53 @@ def test_forward_uses_the_pinned_pieces(monkeypatch):
     _, ref_w = tiny_weights(cfg, seed=5)
     LlamaRef(cfg, ref_w).forward_with_cache([1, 2, 3])
     assert calls == {"rope": 4, "att": 2, "swiglu": 2}
+
+
+def test_config5_geometry_logits_see_attention_mistakes(monkeypatch):
+    """The GPU test of config 5's attention path (test_gpu_llama.py,
+    test_config5_attention_path_f16_cache) compares logits of a 2-layer model
+    at hidden 4096, 32 query heads over 8 KV heads of dim 128.  That
+    comparison can only catch an attention mistake if the model's logits
+    move by more than the parity bar when the attention is wrong: here the
+    oracle's own attention is replaced by plausible mistakes (the h % n_kv
+    head map instead of h // 4, no 1/sqrt(D) scale, the current key left out)
+    and each must move the logits of a 128-row prompt and of a decode step at
+    128 cached keys well outside 1e-3 rel + 1e-4 abs.  The model has the
+    GPU test's centered Q4_0 codes; with BASELINE's codes (uniform in 0..15,
+    a common mode of -d/2 a weight) the dropped key moves no logit past the
+    bar, which is why the GPU test does not use them."""
+    import oracle.llama_ref as lr
+
+    cfg = tiny_config(dim=4096, n_layers=2, n_heads=32, n_kv_heads=8, head_dim=128, ffn_dim=512, vocab=320,
+                      max_seq=256, max_batch=128, kv_f16=True)
+    _, w = tiny_weights(cfg, 505, centered=True)
+    prompt = np.random.default_rng(5005).integers(0, cfg.vocab, 128)
+    good = LlamaRef(cfg, w, kv_f16=True)
+    want = [good.forward_with_cache(prompt)]
+    want.append(good.forward_with_cache([argmax(want[0])]))
+    right = lr.attention
+
+    def head_mod(q, kc, vc, start):  # query head h reads KV head h % n_kv
+        nh, nkv = q.shape[0], kc.shape[0]
+        perm = np.array([h % nkv for h in range(nh)]) * (nh // nkv) + np.array([h // nkv for h in range(nh)])
+        return right(q[np.argsort(perm)], kc, vc, start)[perm]
+
+    def unscaled(q, kc, vc, start):
+        return right(q * np.float32(np.sqrt(q.shape[-1])), kc, vc, start)
+
+    def no_current_key(q, kc, vc, start):
+        if q.shape[1] != 1:
+            return right(q, kc, vc, start)
+        return right(q, kc[:, :-1], vc[:, :-1], start - 1)
+
+    for name, fn in (("h % n_kv", head_mod), ("unscaled", unscaled), ("current key dropped", no_current_key)):
+        monkeypatch.setattr(lr, "attention", fn)
+        bad = LlamaRef(cfg, w, kv_f16=True)
+        got = [bad.forward_with_cache(prompt)]
+        got.append(bad.forward_with_cache([argmax(want[0])]))
+        monkeypatch.setattr(lr, "attention", right)
+        for step, (g, t) in enumerate(zip(got, want)):
+            tol = 1e-4 + 1e-3 * np.abs(t)
+            if name == "current key dropped" and step == 0:
+                continue  # a prompt row always sees its own key in this planted form
+            assert np.count_nonzero(np.abs(g - t) > tol) > t.size // 2, (name, step)
