@@ -126,6 +126,17 @@ rdl_status rdl_llama_set_kv_page_table(rdl_llama* model, const int32_t* table, s
  * testing switch. */
 rdl_status rdl_llama_set_fused_attention(rdl_llama* model, int32_t enable);
 
+/* Linear::set_native_q4_matmul for every Linear of one layer
+ * (TransformerBlock::set_native_q4_matmul, transformer_block.rs:248-255;
+ * layer = -1: every layer, as gemma3_gguf.rs:126-128 does): the layer's
+ * Q4_0 and Q4_1 products quantize their activation rows to Q8_0
+ * (quantize_row_q8_0) and sum int32 block dots (matmul_f32_q4_native /
+ * matmul_f32_q4_1_native, quantize.rs:326-394, 501-572); other types keep
+ * their one path (linear.rs:119-177).  Such layers run their RMSNorm, RoPE,
+ * SwiGLU and adds as separate launches.  The output matrix is not a layer's
+ * and keeps the float path, as in the reference.  Default: off. */
+rdl_status rdl_llama_set_native_q4(rdl_llama* model, int32_t layer, int32_t enable);
+
 /* Kernel launches the model has enqueued since create, by attention path:
  * host-side counts (a captured decode graph counts its launches once, at
  * capture, however often it is replayed).  No reference counterpart: it lets

@@ -622,6 +622,10 @@ struct LlamaModel {
         Mat q, k, v, gate, up;
         bool split_qkv = false, split_gu = false;
         bool fused = false;  // Q4_0 throughout: the fused launches serve m <= 4 rows
+        // Linear::use_native_q4 of the layer's Q4_0 / Q4_1 Linears
+        // (TransformerBlock::set_native_q4_matmul): activations quantized to
+        // Q8_0, int32 block dots (matmul_f32_q4_native / _q4_1_native)
+        bool native = false;
         float* attn_norm = nullptr;
         float* ffn_norm = nullptr;
     };
@@ -682,16 +686,19 @@ struct LlamaModel {
     size_t kv_elem() const { return cfg.kv_f16 ? 2 : 4; }
     size_t kv_layer_elems() const { return (size_t)n_pages * cfg.n_kv_heads * KV_PAGE * cfg.head_dim; }
 
-    // y[m, mat.n] = x[m, mat.k] . W^T on the model's stream
-    hipError_t linear(const Mat& w, const float* xin, size_t m, float* y) {
-        if (m <= 4) return launch_gemv_fused(w.type, false, w.dev, w.n, w.k, xin, m, y, stream);
+    // y[m, mat.n] = x[m, mat.k] . W^T on the model's stream; native: the
+    // Linear's use_native_q4 (Q4_0 / Q4_1 weights only, as in linear.rs:119-153)
+    hipError_t linear(const Mat& w, const float* xin, size_t m, float* y, bool native = false) {
+        native = native && (w.type == WType::Q4_0 || w.type == WType::Q4_1);
+        if (m <= 4) return launch_gemv_fused(w.type, native, w.dev, w.n, w.k, xin, m, y, stream);
         if (w.type == WType::Q4_0)
-            return launch_gemm_q4_0(w.dev, w.n, w.k, xin, m, y, gemm_scratch, gemm_cnt, stream);
+            return native ? launch_gemm_q4_0_native(w.dev, w.n, w.k, xin, m, y, nullptr, gemm_scratch, stream)
+                          : launch_gemm_q4_0(w.dev, w.n, w.k, xin, m, y, gemm_scratch, gemm_cnt, stream);
         // rows four at a time through the fused GEMV (other types, or scales
         // beyond the GEMM's range)
         for (size_t r = 0; r < m; r += 4) {
             const size_t mr = (m - r < 4) ? m - r : 4;
-            hipError_t e = launch_gemv_fused(w.type, false, w.dev, w.n, w.k, xin + r * w.k, mr,
+            hipError_t e = launch_gemv_fused(w.type, native, w.dev, w.n, w.k, xin + r * w.k, mr,
                                              y + r * w.n, stream);
             if (e != hipSuccess) return e;
         }
@@ -885,7 +892,9 @@ struct LlamaModel {
         // RMSNorms, the SwiGLU and the residual adds into the GEMMs' x splits
         // and stores (hipErrorInvalidValue: a shape they do not take, nothing
         // launched, the separate launches below run instead)
-        auto q4t = [&](const Mat& w) { return m > GEMM_XTILE_M && w.type == WType::Q4_0; };
+        // (native layers keep their Linears' own products: no folding)
+        auto q4t = [&](const Mat& w) { return !L.native && m > GEMM_XTILE_M && w.type == WType::Q4_0; };
+        const bool nat = L.native;
         bool qkv_done = false;
         if (np == 1 && q4t(L.qkv)) {
             e = launch_gemm_q4_0_pro(L.qkv.dev, L.qkv.n, L.qkv.k, x, m, qkv, gemm_scratch, 1, L.attn_norm,
@@ -911,9 +920,9 @@ struct LlamaModel {
             if (kquant(w)) {
                 e = kq_linear(w, x, d, m, qkv + cols[i], qkv_dim, GEMV_PRO_RMSNORM, L.attn_norm, GEMV_EPI_STORE);
             } else if (np == 1 || m == 1) {  // whole rows, or one row: in place
-                e = linear(w, xn, m, qkv + cols[i]);
+                e = linear(w, xn, m, qkv + cols[i], nat);
             } else {  // [m, part] rows, then strided into the [m, qkv_dim] rows
-                if ((e = linear(w, xn, m, part_tmp)) != hipSuccess) return e;
+                if ((e = linear(w, xn, m, part_tmp, nat)) != hipSuccess) return e;
                 const size_t wb = (size_t)w.n * sizeof(float);
                 e = hipMemcpy2DAsync(qkv + cols[i], (size_t)qkv_dim * sizeof(float), part_tmp, wb, wb, m,
                                      hipMemcpyDeviceToDevice, stream);
@@ -931,7 +940,7 @@ struct LlamaModel {
             e = kq_linear(L.o, att, q_dim, m, x, d, GEMV_PRO_NONE, nullptr, GEMV_EPI_RESIDUAL);
             if (e != hipSuccess) return e;
         } else {
-            if ((e = linear(L.o, att, m, xn)) != hipSuccess) return e;
+            if ((e = linear(L.o, att, m, xn, nat)) != hipSuccess) return e;
             hipLaunchKernelGGL(add_kernel, dim3(blocks_for(m * d)), dim3(NT), 0, stream, x, xn, m * d);
         }
         // ---- h = silu(gate) * up ----
@@ -951,7 +960,7 @@ struct LlamaModel {
             if (e != hipSuccess) return e;
         } else if (!L.split_gu) {
             rmsnorm(L.ffn_norm);
-            if ((e = linear(L.gu, xn, m, gu)) != hipSuccess) return e;
+            if ((e = linear(L.gu, xn, m, gu, nat)) != hipSuccess) return e;
             hipLaunchKernelGGL(swiglu_kernel, dim3(blocks_for(nf)), dim3(NT), 0, stream, gu, f, nf, hb);
         } else {
             if (!kquant(L.gate) || !kquant(L.up)) rmsnorm(L.ffn_norm);
@@ -959,7 +968,7 @@ struct LlamaModel {
             for (int i = 0; i < 2; i++) {
                 float* yo = gu + i * nf;
                 e = kquant(*gp[i]) ? kq_linear(*gp[i], x, d, m, yo, f, GEMV_PRO_RMSNORM, L.ffn_norm, GEMV_EPI_STORE)
-                                   : linear(*gp[i], xn, m, yo);
+                                   : linear(*gp[i], xn, m, yo, nat);
                 if (e != hipSuccess) return e;
             }
             hipLaunchKernelGGL(swiglu2_kernel, dim3(blocks_for(nf)), dim3(NT), 0, stream, gu, gu + nf, nf, hb);
@@ -971,14 +980,14 @@ struct LlamaModel {
             if (e != hipSuccess && e != hipErrorInvalidValue) return e;
             if (e == hipErrorInvalidValue) {  // the SwiGLU on its own, then the product
                 hipLaunchKernelGGL(swiglu_kernel, dim3(blocks_for(nf)), dim3(NT), 0, stream, gu, f, nf, hb);
-                if ((e = linear(L.down, hb, m, xn)) != hipSuccess) return e;
+                if ((e = linear(L.down, hb, m, xn, nat)) != hipSuccess) return e;
                 hipLaunchKernelGGL(add_kernel, dim3(blocks_for(m * d)), dim3(NT), 0, stream, x, xn, m * d);
             }
         } else if (kquant(L.down)) {
             e = kq_linear(L.down, hb, f, m, x, d, GEMV_PRO_NONE, nullptr, GEMV_EPI_RESIDUAL);
             if (e != hipSuccess) return e;
         } else {
-            if ((e = linear(L.down, hb, m, xn)) != hipSuccess) return e;
+            if ((e = linear(L.down, hb, m, xn, nat)) != hipSuccess) return e;
             hipLaunchKernelGGL(add_kernel, dim3(blocks_for(m * d)), dim3(NT), 0, stream, x, xn, m * d);
         }
         return hipGetLastError();
@@ -998,7 +1007,7 @@ struct LlamaModel {
         if (embed && (e = launch_dequant_rows(emb.type, emb.dev, emb.n, emb.k, tokens, m, x, stream)) != hipSuccess)
             return e;
         for (int l = 0; l < cfg.n_layers; l++) {
-            e = (m <= 4 && layers[l].fused) ? layer_fused(l, m) : layer_plain(l, m);
+            e = (m <= 4 && layers[l].fused && !layers[l].native) ? layer_fused(l, m) : layer_plain(l, m);
             if (e != hipSuccess) return e;
         }
         // logits = rms_norm(x_last, norm) . Wout^T (the norm fused into the GEMV for Q4_0, Q4_K, Q6_K)
@@ -1512,6 +1521,26 @@ rdl_status rdl_llama_set_fused_attention(rdl_llama* model, int32_t enable) {
 rdl_status rdl_llama_get_path_counts(const rdl_llama* model, rdl_llama_path_counts* out) {
     if (!model || !out) return api_fail(RDL_ERR_NULL_POINTER, "NULL argument");
     *out = model->m.path;
+    return api_ok();
+}
+
+rdl_status rdl_llama_set_native_q4(rdl_llama* model, int32_t layer, int32_t enable) {
+    if (!model) return api_fail(RDL_ERR_NULL_POINTER, "NULL model");
+    rdl::LlamaModel& M = model->m;
+    if (layer < -1 || layer >= M.cfg.n_layers)
+        return api_fail(RDL_ERR_INVALID_DATA, "layer %d outside -1 .. %d", layer, M.cfg.n_layers - 1);
+    bool changed = false;
+    for (int l = 0; l < M.cfg.n_layers; l++)
+        if ((layer < 0 || l == layer) && M.layers[l].native != (enable != 0)) {
+            M.layers[l].native = enable != 0;
+            changed = true;
+        }
+    if (changed) {  // the captured decode step holds the other launches: capture again
+        if (M.decode_exec) (void)hipGraphExecDestroy(M.decode_exec);
+        if (M.decode_graph) (void)hipGraphDestroy(M.decode_graph);
+        M.decode_exec = nullptr;
+        M.decode_graph = nullptr;
+    }
     return api_ok();
 }
 

@@ -49,6 +49,7 @@ class _PathCounts(C.Structure):
 
 
 _decl("rdl_llama_get_path_counts", _i32, _p, C.POINTER(_PathCounts))
+_decl("rdl_llama_set_native_q4", _i32, _p, _i32, _i32)
 
 
 class _GgufOptions(C.Structure):
@@ -158,6 +159,12 @@ class LlamaModel:
     def set_fused_attention(self, enable: bool) -> None:
         """Decode steps' q/k/v projection, attention and o projection in one launch (default) or three."""
         check(lib.rdl_llama_set_fused_attention(self._h, int(bool(enable))))
+
+    def set_native_q4_matmul(self, enabled: bool, layer: int = -1) -> None:
+        """TransformerBlock::set_native_q4_matmul on one layer (layer=-1: all):
+        its Q4_0 / Q4_1 Linears take the native (Q8_0 activations, int32 block
+        dots) path."""
+        check(lib.rdl_llama_set_native_q4(self._h, layer, int(bool(enabled))))
 
     def path_counts(self) -> dict:
         """Attention launches enqueued so far, by kernel (host-side counts; a
