@@ -443,7 +443,7 @@ def gemm_lines(rig, ms_list, seed=0x5EED0004, native=False):
             "workload": f"config4 M={m}" + (" native (matmul_f32_q4_native, int8 MFMA)" if native else ""),
             "m": m,
             "value": round(tflops, 2),
-            "unit": "TFLOP/s",
+            "unit": "TOP/s" if native else "TFLOP/s",
             "ms_per_call": round(ms, 5),
             "hbm_GBs": round(gbps, 1),
             "roofline": {

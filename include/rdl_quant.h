@@ -201,6 +201,19 @@ rdl_status rdl_weight_free(rdl_weight* w);
 rdl_status rdl_linear_forward_dev(const rdl_weight* w, const float* x_dev, size_t m,
                                   float* y_dev, int32_t mode, void* stream);
 
+/* Frees the work memory the device entry points keep for `stream` on the
+ * current device (rdl_linear_forward_dev and the other device calls above),
+ * after waiting for the stream.  No counterpart in the reference: for
+ * callers that create and destroy streams (a stream per request), whose
+ * streams' work memory would otherwise stay until the process ends; call it
+ * before destroying such a stream.  A later call on the stream allocates
+ * again.  Not while the stream is being captured into a graph (the wait is
+ * refused: RDL_ERR_HIP).  A stream with no work memory: RDL_OK.  Allocation
+ * and release (hipMalloc / hipFree, on a stream's first call, on growth, and
+ * here) wait for the device, so they must not overlap another thread's
+ * graph capture in global capture mode. */
+rdl_status rdl_release_stream_work(void* stream);
+
 /* rdl_linear_forward_dev without any device allocation.  No counterpart in
  * the reference: it is for callers that cannot allocate device memory (code
  * under HIP graph capture, serving loops, harnesses that forbid hipMalloc).

@@ -619,6 +619,24 @@ rdl_status rdl_linear_forward_dev(const rdl_weight* w, const float* x_dev, size_
     return rs == RDL_OK ? ok() : rs;
 }
 
+rdl_status rdl_release_stream_work(void* stream) {
+    hipStream_t s = (hipStream_t)stream;
+    int dev = 0;
+    HIP_TRY(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lock(work_mu);
+    for (auto it = work_pool.begin(); it != work_pool.end(); ++it) {
+        if (it->dev != dev || it->stream != s) continue;
+        // the stream's calls may still run on the device
+        HIP_TRY(hipStreamSynchronize(s));
+        if (it->p) HIP_TRY(hipFree(it->p));
+        it->p = nullptr;
+        if (it->counters) HIP_TRY(hipFree(it->counters));
+        work_pool.erase(it);
+        break;
+    }
+    return ok();
+}
+
 rdl_status rdl_linear_forward_dev_noalloc(const rdl_weight* w, const float* x_dev, size_t m, float* y_dev,
                                           int32_t mode, void* stream) {
     if (!w) return fail(RDL_ERR_NULL_POINTER, "weight handle is NULL");

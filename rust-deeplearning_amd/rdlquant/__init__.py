@@ -106,6 +106,7 @@ _decl("rdl_weight_wrap_device", _i32, _p, _sz, _i32, _sz, _sz, C.POINTER(_p))
 _decl("rdl_weight_free", _i32, _p)
 _decl("rdl_linear_forward_dev", _i32, _p, _p, _sz, _p, _i32, _p)
 _decl("rdl_linear_forward_dev_noalloc", _i32, _p, _p, _sz, _p, _i32, _p)
+_decl("rdl_release_stream_work", _i32, _p)
 NOALLOC_SCRATCH_BYTES = 16 << 20  # RDL_NOALLOC_SCRATCH_BYTES
 _decl("rdl_activation_record_bytes", _sz, _sz, _sz, _i32)
 _decl("rdl_prepare_activations_dev", _i32, _p, _sz, _sz, _i32, _p, _p)
@@ -191,6 +192,12 @@ def gemm_combine():
     mode, local = _i32(), _i32()
     check(lib.rdl_get_gemm_combine(C.byref(mode), C.byref(local)))
     return int(mode.value), bool(local.value)
+
+
+def release_stream_work(stream) -> None:
+    """rdl_release_stream_work: free the work memory kept for `stream` (a
+    hipStream_t handle) on the current device, after waiting for it."""
+    check(lib.rdl_release_stream_work(stream))
 
 
 def device_count() -> int:

@@ -180,6 +180,30 @@ def test_sliced_gemm_shapes_share_the_stream_work_memory(rq, gpu):
         assert np.array_equal(yt.cpu().numpy(), want.reshape(-1)), f"call {rep}: n={n} k={k} m={m}"
 
 
+def test_release_stream_work(rq, gpu):
+    """rdl_release_stream_work frees a stream's work memory: products on a
+    stream of their own before and after the release (which allocates again)
+    equal the synchronous entry point's bit for bit; releasing a stream with
+    no work memory, or twice, is a no-op."""
+    import torch
+
+    n, k = 4096, 4096
+    w = synth.q4_0_weights(n, k, 180)
+    _, h = dev_weight(rq, torch, w, 2, n, k)
+    st = torch.cuda.Stream()
+    rq.release_stream_work(st.cuda_stream)  # nothing kept yet
+    for rep, m in enumerate((16, 7, 1, 40)):
+        x = synth.activations(m, k, 181 + rep)
+        xt = torch.from_numpy(x.reshape(-1)).cuda()
+        yt = torch.empty(m * n, dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()
+        h.forward_dev(xt.data_ptr(), m, yt.data_ptr(), rq.MODE_FLOAT, st.cuda_stream)
+        rq.release_stream_work(st.cuda_stream)  # waits for the stream, then frees
+        want = rq.matmul_f32_q4(x, w, m, k, n)
+        assert np.array_equal(yt.cpu().numpy(), want.reshape(-1)), f"m={m}"
+    rq.release_stream_work(st.cuda_stream)
+
+
 def test_skinny_gemm_graph_replays_match_eager(rq, gpu):
     """A 16-row prefill product captured in a graph (graph-owned scratch and
     counters, zeroed by a kernel on every replay) reproduces the eager result
