@@ -201,6 +201,15 @@ rdl_status rdl_weight_free(rdl_weight* w);
 rdl_status rdl_linear_forward_dev(const rdl_weight* w, const float* x_dev, size_t m,
                                   float* y_dev, int32_t mode, void* stream);
 
+/* rdl_linear_forward_dev plus Linear::forward's optional F32 bias
+ * (linear.rs:172-176, output.add(bias)): y_dev[i][j] = product + bias_dev[j],
+ * one f32 add an output, as a second launch on the stream after the product.
+ * bias_dev: out_features floats on the device, or NULL (then exactly
+ * rdl_linear_forward_dev).  m x out_features must stay below 2^32
+ * (RDL_ERR_UNSUPPORTED). */
+rdl_status rdl_linear_forward_bias_dev(const rdl_weight* w, const float* x_dev, size_t m,
+                                       const float* bias_dev, float* y_dev, int32_t mode, void* stream);
+
 /* Frees the work memory the device entry points keep for `stream` on the
  * current device (rdl_linear_forward_dev and the other device calls above),
  * after waiting for the stream.  No counterpart in the reference: for

@@ -619,6 +619,16 @@ rdl_status rdl_linear_forward_dev(const rdl_weight* w, const float* x_dev, size_
     return rs == RDL_OK ? ok() : rs;
 }
 
+rdl_status rdl_linear_forward_bias_dev(const rdl_weight* w, const float* x_dev, size_t m, const float* bias_dev,
+                                       float* y_dev, int32_t mode, void* stream) {
+    if (bias_dev && w && m * (size_t)w->n >= ((size_t)1 << 32))
+        return fail(RDL_ERR_UNSUPPORTED, "bias over %zu x %zu outputs: at most 2^32 - 1", m, w->n);
+    rdl_status st = rdl_linear_forward_dev(w, x_dev, m, y_dev, mode, stream);
+    if (st != RDL_OK || !bias_dev || m == 0 || w->n == 0) return st;
+    HIP_TRY(rdl::launch_bias_add(y_dev, bias_dev, m, w->n, (hipStream_t)stream));
+    return ok();
+}
+
 rdl_status rdl_release_stream_work(void* stream) {
     hipStream_t s = (hipStream_t)stream;
     int dev = 0;

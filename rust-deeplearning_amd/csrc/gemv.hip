@@ -21,6 +21,7 @@
 //     activation digits on v_dot4_i32_i8; the int32 results are exact;
 //   * the R row partials are summed across the wave with a transpose
 //     reduction (R values, log2(64) exchange steps).
+#include <algorithm>
 #include "rdl_device.hpp"
 #include "rdl_internal.hpp"
 
@@ -593,6 +594,13 @@ hipError_t launch_r(WType t, bool native, const uint8_t* w, size_t n, size_t k, 
     return hipGetLastError();
 }
 
+// y[i][j] += bias[j] over m rows of n: Linear::forward's output.add(bias)
+// (linear.rs:172-176), one f32 add an element.
+__global__ __launch_bounds__(256) void bias_add_kernel(float* __restrict__ y, const float* __restrict__ bias,
+                                                       uint32_t n, uint32_t total) {
+    for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < total; i += gridDim.x * 256u) y[i] += bias[i % n];
+}
+
 }  // namespace
 
 hipError_t launch_gemv(WType t, bool native, const uint8_t* w, size_t n, size_t k,
@@ -612,6 +620,14 @@ hipError_t launch_q4_0_block_dots(const uint8_t* w, size_t n, size_t k, const Na
     if (total == 0) return hipSuccess;
     hipLaunchKernelGGL(q4_0_block_dots_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
                        s, w, (int)n, (int)(k / QK), rec, partials);
+    return hipGetLastError();
+}
+
+hipError_t launch_bias_add(float* y, const float* bias, size_t m, size_t n, hipStream_t s) {
+    const size_t total = m * n;
+    if (total == 0) return hipSuccess;
+    const unsigned blocks = (unsigned)std::min<size_t>((total + 255) / 256, 65536);
+    hipLaunchKernelGGL(bias_add_kernel, dim3(blocks), dim3(256), 0, s, y, bias, (uint32_t)n, (uint32_t)total);
     return hipGetLastError();
 }
 

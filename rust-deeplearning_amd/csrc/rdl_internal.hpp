@@ -271,6 +271,9 @@ bool ggml_geometry(int32_t ggml_type, int* block_size, int* block_bytes);
 hipError_t launch_dequant_gguf(int32_t ggml_type, const uint8_t* src, size_t n_elements, float* dst,
                                hipStream_t s);
 
+// y[i][j] += bias[j] for m rows of n (m * n < 2^32).
+hipError_t launch_bias_add(float* y, const float* bias, size_t m, size_t n, hipStream_t s);
+
 // Dequantize selected rows of a Q4_0 / Q4_1 / Q8_0 matrix to f32.
 hipError_t launch_dequant_rows(WType t, const uint8_t* w, size_t n, size_t k,
                                const int32_t* rows, size_t n_rows, float* out, hipStream_t s);

@@ -107,6 +107,7 @@ _decl("rdl_weight_free", _i32, _p)
 _decl("rdl_linear_forward_dev", _i32, _p, _p, _sz, _p, _i32, _p)
 _decl("rdl_linear_forward_dev_noalloc", _i32, _p, _p, _sz, _p, _i32, _p)
 _decl("rdl_release_stream_work", _i32, _p)
+_decl("rdl_linear_forward_bias_dev", _i32, _p, _p, _sz, _p, _p, _i32, _p)
 NOALLOC_SCRATCH_BYTES = 16 << 20  # RDL_NOALLOC_SCRATCH_BYTES
 _decl("rdl_activation_record_bytes", _sz, _sz, _sz, _i32)
 _decl("rdl_prepare_activations_dev", _i32, _p, _sz, _sz, _i32, _p, _p)
@@ -350,6 +351,11 @@ class Weight:
 
     def forward_dev(self, x_ptr, m, y_ptr, mode=MODE_FLOAT, stream=0):
         check(lib.rdl_linear_forward_dev(self.handle, x_ptr, m, y_ptr, mode, stream))
+
+    def forward_bias_dev(self, x_ptr, m, bias_ptr, y_ptr, mode=MODE_FLOAT, stream=0):
+        """rdl_linear_forward_bias_dev: forward_dev plus Linear's optional
+        bias (bias_ptr: out_features device floats, or 0 for none)."""
+        check(lib.rdl_linear_forward_bias_dev(self.handle, x_ptr, m, bias_ptr or None, y_ptr, mode, stream))
 
     def forward_dev_noalloc(self, x_ptr, m, y_ptr, mode=MODE_FLOAT, stream=0):
         """rdl_linear_forward_dev_noalloc: the same product with no device

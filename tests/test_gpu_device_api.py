@@ -180,6 +180,44 @@ def test_sliced_gemm_shapes_share_the_stream_work_memory(rq, gpu):
         assert np.array_equal(yt.cpu().numpy(), want.reshape(-1)), f"call {rep}: n={n} k={k} m={m}"
 
 
+@pytest.mark.parametrize("dtype,n,k,m,mode", [(2, 4096, 4096, 1, 0), (2, 4096, 4096, 16, 0), (2, 300, 1024, 70, 0),
+                                            (2, 4096, 4096, 3, 1), (8, 1000, 2048, 2, 0), (12, 2048, 4096, 5, 0),
+                                            (3, 257, 1024, 2, 1)])
+def test_linear_bias(rq, orc, gpu, dtype, n, k, m, mode):
+    """Linear::forward's optional bias (linear.rs:172-176: output.add(bias)):
+    the product plus bias[j] in f32, equal bit for bit to the unbiased
+    device product plus the bias on the host, and within the bar of the
+    oracle's product plus the bias; a NULL bias is the plain product."""
+    import torch
+
+    x = synth.activations(m, k, 190 + n + m)
+    w = synth.weights(dtype, n, k, 191 + k)
+    _, h = dev_weight(rq, torch, w, dtype, n, k)
+    bias = np.random.default_rng(192 + n).standard_normal(n).astype(np.float32)
+    xt = torch.from_numpy(x.reshape(-1)).cuda()
+    bt = torch.from_numpy(bias).cuda()
+    y0 = torch.empty(m * n, dtype=torch.float32, device="cuda")
+    y1 = torch.empty(m * n, dtype=torch.float32, device="cuda")
+    y2 = torch.empty(m * n, dtype=torch.float32, device="cuda")
+    s = torch.cuda.current_stream().cuda_stream
+    md = rq.MODE_NATIVE if mode else rq.MODE_FLOAT
+    h.forward_dev(xt.data_ptr(), m, y0.data_ptr(), md, s)
+    h.forward_bias_dev(xt.data_ptr(), m, bt.data_ptr(), y1.data_ptr(), md, s)
+    h.forward_bias_dev(xt.data_ptr(), m, 0, y2.data_ptr(), md, s)
+    torch.cuda.synchronize()
+    plain = y0.cpu().numpy().reshape(m, n)
+    got = y1.cpu().numpy().reshape(m, n)
+    assert np.array_equal(got, (plain + bias[None, :]).astype(np.float32))
+    assert np.array_equal(y2.cpu().numpy().reshape(m, n), plain)
+    kind = KIND[dtype] + ("_native" if mode else "")
+    want = orc.matmul(kind, x, w, m, k, n, threads=8).reshape(m, n) + bias[None, :]
+    if mode:  # the native products: exact int32 block dots, as the oracle's
+        assert np.all(np.abs(got - want) <= ATOL + RTOL * np.abs(want))
+    else:  # float: the exact (f64) value, and the oracle within its own rounding
+        wd = orc.to_f32(DEQ[dtype], w, n * k).reshape(n, k).astype(np.float64)
+        close(got, want, (x.astype(np.float64).reshape(m, k) @ wd.T + bias[None, :]).ravel())
+
+
 def test_release_stream_work(rq, gpu):
     """rdl_release_stream_work frees a stream's work memory: products on a
     stream of their own before and after the release (which allocates again)
