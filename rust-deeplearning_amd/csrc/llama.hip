@@ -1275,9 +1275,11 @@ rdl_status rdl_llama_create_typed(const rdl_llama_config* cfg, const int32_t* ty
     for (const auto& sh : shapes) {
         nmax = std::max(nmax, sh[0]);
         gcc = std::max(gcc, rdl::gemm_counter_count(sh[0], sh[1]));
-        // every skinny shape (it depends on ceil(m / 16)) and the largest chunk
+        // every skinny shape (it depends on ceil(m / 16)) and the largest
+        // chunk, in float and in native mode (rdl_llama_set_native_q4)
         for (size_t mm : {(size_t)1, (size_t)16, (size_t)32, (size_t)48, (size_t)64, mb})
-            gsb = std::max(gsb, rdl::gemm_scratch_bytes(std::min(mm, mb), sh[0], sh[1], false));
+            for (bool nat : {false, true})
+                gsb = std::max(gsb, rdl::gemm_scratch_bytes(std::min(mm, mb), sh[0], sh[1], nat));
     }
     if ((e = M.alloc(&M.gemm_scratch, gsb)) != hipSuccess) return fail_free(e);
     if ((e = M.alloc_t(&M.gemm_cnt, gcc)) != hipSuccess) return fail_free(e);
