@@ -216,8 +216,10 @@ rdl_status rdl_linear_forward_bias_dev(const rdl_weight* w, const float* x_dev, 
  * callers that create and destroy streams (a stream per request), whose
  * streams' work memory would otherwise stay until the process ends; call it
  * before destroying such a stream.  A later call on the stream allocates
- * again.  Not while the stream is being captured into a graph (the wait is
- * refused: RDL_ERR_HIP).  A stream with no work memory: RDL_OK.  Allocation
+ * again.  The caller must not make device calls on the same stream from other
+ * threads while this runs (their launches could still be reading the memory
+ * freed here).  Not while the stream is being captured into a graph (the
+ * wait is refused: RDL_ERR_HIP).  A stream with no work memory: RDL_OK.  Allocation
  * and release (hipMalloc / hipFree, on a stream's first call, on growth, and
  * here) wait for the device, so they must not overlap another thread's
  * graph capture in global capture mode. */
