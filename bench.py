@@ -633,6 +633,7 @@ def decode_q4_k_m_line(rig, reps=2):
     model.close()
     rig.torch.cuda.empty_cache()
     decode_ms = min(r[1] for r in runs[1:])
+    prefill_ms = min(r[0] for r in runs[1:])
     ms_tok = decode_ms / GEN_TOKENS
     ctx_mean = PROMPT_LEN + (GEN_TOKENS + 1) / 2
     kvb = cfg.n_layers * 2 * cfg.n_kv_heads * cfg.head_dim * 2
@@ -644,6 +645,8 @@ def decode_q4_k_m_line(rig, reps=2):
         "value": round(GEN_TOKENS / (decode_ms * 1e-3), 1),
         "unit": "tokens/s",
         "ms_per_token": round(ms_tok, 4),
+        "prefill_ms_128_tokens": round(prefill_ms, 3),
+        "prefill_tokens_s": round(PROMPT_LEN / (prefill_ms * 1e-3), 1),
         "bytes_per_token": bpt,
         "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                      "frac": round(gbps / PEAK_HBM_GBPS, 4)},
