@@ -171,14 +171,19 @@ bool use_fused(WType t, size_t m, size_t n, size_t k, const float* x_dev) {
 }
 
 // How a product runs: one fused GEMV launch (m <= 4), the matrix-core GEMM
-// (Q4_0, more rows: f16 MFMA in float mode, int8 MFMA in native mode), or
-// activation records + the records GEMV.
+// (Q4_0, more rows: f16 MFMA in float mode, int8 MFMA in native mode; Q4_K
+// from KQ_GEMM_MIN_M rows, float mode), or activation records + the records
+// GEMV.
 enum class Path { Fused, Gemm, Records };
 
-// The GEMM addresses x and W with 32-bit offsets.
+// The GEMM addresses x and W with 32-bit offsets; Q4_K's x prep holds a row
+// in registers (k <= 16384).
 bool gemm_fits(WType t, size_t m, size_t n, size_t k) {
-    return t == WType::Q4_0 && k > 0 && (uint64_t)m * k * 2 <= rdl::FUSED_MAX_WEIGHT_BYTES &&
-           (uint64_t)n * (k / rdl::QK) * rdl::Q4_0_BYTES <= rdl::FUSED_MAX_WEIGHT_BYTES;
+    if (k == 0 || (uint64_t)m * k * 2 > rdl::FUSED_MAX_WEIGHT_BYTES) return false;
+    if (t == WType::Q4_K)
+        return m >= rdl::KQ_GEMM_MIN_M && k % rdl::QK_K == 0 && k <= 16384 &&
+               (uint64_t)n * (k / rdl::QK_K) * rdl::Q4_K_BYTES <= rdl::FUSED_MAX_WEIGHT_BYTES;
+    return t == WType::Q4_0 && (uint64_t)n * (k / rdl::QK) * rdl::Q4_0_BYTES <= rdl::FUSED_MAX_WEIGHT_BYTES;
 }
 
 Path pick_path(WType t, bool native, size_t m, size_t n, size_t k, const float* x_dev) {
@@ -187,10 +192,11 @@ Path pick_path(WType t, bool native, size_t m, size_t n, size_t k, const float* 
     return Path::Records;
 }
 
-size_t scratch_bytes(Path p, bool native, size_t m, size_t n, size_t k) {
+size_t scratch_bytes(WType t, Path p, bool native, size_t m, size_t n, size_t k) {
     switch (p) {
         case Path::Fused: return 0;
-        case Path::Gemm: return rdl::gemm_scratch_bytes(m, n, k, native);
+        case Path::Gemm:
+            return t == WType::Q4_K ? rdl::gemm_q4_k_scratch_bytes(m, k) : rdl::gemm_scratch_bytes(m, n, k, native);
         case Path::Records: return rec_bytes(native, m, k);
     }
     return 0;
@@ -212,7 +218,9 @@ rdl_status run_linear(WType t, bool native, const uint8_t* w_dev, size_t n, size
         return RDL_OK;
     }
     if (path == Path::Gemm) {
-        if (native)
+        if (t == WType::Q4_K)
+            HIP_TRY(rdl::launch_gemm_q4_k(w_dev, n, k, x_dev, m, y_dev, work, s));
+        else if (native)
             HIP_TRY(rdl::launch_gemm_q4_0_native(w_dev, n, k, x_dev, m, y_dev, nullptr, work, s));
         else
             HIP_TRY(rdl::launch_gemm_q4_0(w_dev, n, k, x_dev, m, y_dev, work, counters, s));
@@ -372,7 +380,7 @@ rdl_status host_matmul(WType t, bool native, const float* x, size_t x_len, const
     HIP_TRY(hipMemcpy(dx.p, x, m * k * sizeof(float), hipMemcpyHostToDevice));
     HIP_TRY(hipMemcpy(dw.p, w, wb, hipMemcpyHostToDevice));
     const Path path = pick_path(t, native, m, n, k, (const float*)dx.p);
-    const size_t sb = scratch_bytes(path, native, m, n, k);
+    const size_t sb = scratch_bytes(t, path, native, m, n, k);
     if (sb) HIP_TRY(dr.alloc(sb));
     DevBuf dc;
     HIP_TRY(dc.alloc(rdl::gemm_counter_count(n, k) * sizeof(int)));
@@ -608,9 +616,9 @@ rdl_status rdl_linear_forward_dev(const rdl_weight* w, const float* x_dev, size_
     const bool native = mode == RDL_MODE_NATIVE && (w->type == WType::Q4_0 || w->type == WType::Q4_1);
     hipStream_t s = (hipStream_t)stream;
     const Path path = pick_path(w->type, native, m, w->n, w->k, x_dev);
-    const bool want_counters = path == Path::Gemm && !native && m <= rdl::GEMM_SMALL_M;
+    const bool want_counters = path == Path::Gemm && w->type == WType::Q4_0 && !native && m <= rdl::GEMM_SMALL_M;
     CallWork cw;
-    rdl_status st = cw.get(w, s, scratch_bytes(path, native, m, w->n, w->k), want_counters);
+    rdl_status st = cw.get(w, s, scratch_bytes(w->type, path, native, m, w->n, w->k), want_counters);
     if (st != RDL_OK) return st;
     st = run_linear(w->type, native, (const uint8_t*)w->dev, w->n, w->k, x_dev, m, y_dev, cw.p, cw.counters, s,
                     path);
@@ -656,7 +664,7 @@ rdl_status rdl_linear_forward_dev_noalloc(const rdl_weight* w, const float* x_de
     if (!x_dev || !y_dev) return fail(RDL_ERR_NULL_POINTER, "NULL activation pointer");
     const bool native = mode == RDL_MODE_NATIVE && (w->type == WType::Q4_0 || w->type == WType::Q4_1);
     const Path path = pick_path(w->type, native, m, w->n, w->k, x_dev);
-    const size_t rb = scratch_bytes(path, native, m, w->n, w->k);
+    const size_t rb = scratch_bytes(w->type, path, native, m, w->n, w->k);
     if (rb > NOALLOC_DATA_BYTES)
         return fail(RDL_ERR_UNSUPPORTED,
                     "m=%zu rows of in_features %zu need %zu scratch bytes; the static scratch holds %zu",

@@ -85,13 +85,48 @@ __global__ __launch_bounds__(XPREP_THREADS) void gemm_xprep_kernel(const float* 
     }
 }
 
+// The split of a row held in registers (thread t: elements 4 (t + j NT) ..
+// +3 of v[j], zeros past k): x' = x 2^-e, x_hi = f16(x'), x_lo = f16(x' -
+// x_hi); XS (if not null): the f32 sum of x' over each 32-element block
+// ([m, k / 32]; one block is 8 consecutive threads).
+template <int NT, int NV>
+__device__ __forceinline__ void split_store(const f32x4 (&v)[NV], int e, int row, int k, _Float16* __restrict__ XH,
+                                            _Float16* __restrict__ XL, float* __restrict__ XS) {
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    const int k4 = k >> 2;
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        const int p = threadIdx.x + j * NT;
+        h4 hv, lv;
+        float bs = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const float s = ldexpf(v[j][t], -e);
+            hv[t] = (_Float16)s;
+            lv[t] = (_Float16)(s - (float)hv[t]);
+            bs += s;
+        }
+        if (p < k4) {
+            reinterpret_cast<h4*>(XH + (size_t)row * k)[p] = hv;
+            reinterpret_cast<h4*>(XL + (size_t)row * k)[p] = lv;
+        }
+        if (XS) {  // uniform: every thread of the launch takes the branch
+            bs += __shfl_xor(bs, 1);
+            bs += __shfl_xor(bs, 2);
+            bs += __shfl_xor(bs, 4);
+            if ((threadIdx.x & 7) == 0 && p < k4) XS[(size_t)row * (k >> 5) + (p >> 3)] = bs;
+        }
+    }
+}
+
 // The same split with each row's values held in registers between the max
 // and the conversion (k <= 4 * 4 * XPREP_FAST_THREADS): one global read.
 constexpr int XPREP_FAST_THREADS = 1024;
 __global__ __launch_bounds__(XPREP_FAST_THREADS) void gemm_xprep_fast_kernel(const float* __restrict__ X, int k,
                                                                              _Float16* __restrict__ XH,
                                                                              _Float16* __restrict__ XL,
-                                                                             int* __restrict__ XE) {
+                                                                             int* __restrict__ XE,
+                                                                             float* __restrict__ XS) {
     constexpr int NT = XPREP_FAST_THREADS, NV = 4;
     __shared__ float red[NT / 64];
     const int row = blockIdx.x;
@@ -126,22 +161,7 @@ __global__ __launch_bounds__(XPREP_FAST_THREADS) void gemm_xprep_fast_kernel(con
     int e = 0;
     if (amax > 0.0f && isfinite(amax)) e = ilogbf(amax) - 14;
     if (threadIdx.x == 0) XE[row] = e;
-    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-#pragma unroll
-    for (int j = 0; j < NV; j++) {
-        const int p = threadIdx.x + j * NT;
-        if (p < k4) {
-            h4 hv, lv;
-#pragma unroll
-            for (int t = 0; t < 4; t++) {
-                const float s = ldexpf(v[j][t], -e);
-                hv[t] = (_Float16)s;
-                lv[t] = (_Float16)(s - (float)hv[t]);
-            }
-            reinterpret_cast<h4*>(XH + (size_t)row * k)[p] = hv;
-            reinterpret_cast<h4*>(XL + (size_t)row * k)[p] = lv;
-        }
-    }
+    split_store<NT, NV>(v, e, row, k, XH, XL, XS);
 }
 
 // The fast split after a prologue on the row, for the decoder's prompt
@@ -154,7 +174,7 @@ __global__ __launch_bounds__(XPREP_FAST_THREADS) void gemm_xprep_fast_kernel(con
 template <int PRO>
 __global__ __launch_bounds__(XPREP_FAST_THREADS) void gemm_xprep_pro_kernel(
     const float* __restrict__ X, int k, const float* __restrict__ g, float eps, _Float16* __restrict__ XH,
-    _Float16* __restrict__ XL, int* __restrict__ XE) {
+    _Float16* __restrict__ XL, int* __restrict__ XE, float* __restrict__ XS) {
     static_assert(PRO == 1 || PRO == 2, "RMSNorm or SwiGLU");
     constexpr int NT = XPREP_FAST_THREADS, NV = 4;
     __shared__ float red[NT / 64], red2[NT / 64];
@@ -225,22 +245,7 @@ __global__ __launch_bounds__(XPREP_FAST_THREADS) void gemm_xprep_pro_kernel(
     int e = 0;
     if (amax > 0.0f && isfinite(amax)) e = ilogbf(amax) - 14;
     if (threadIdx.x == 0) XE[row] = e;
-    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-#pragma unroll
-    for (int j = 0; j < NV; j++) {
-        const int p = threadIdx.x + j * NT;
-        if (p < k4) {
-            h4 hv, lv;
-#pragma unroll
-            for (int t = 0; t < 4; t++) {
-                const float sc = ldexpf(v[j][t], -e);
-                hv[t] = (_Float16)sc;
-                lv[t] = (_Float16)(sc - (float)hv[t]);
-            }
-            reinterpret_cast<h4*>(XH + (size_t)row * k)[p] = hv;
-            reinterpret_cast<h4*>(XL + (size_t)row * k)[p] = lv;
-        }
-    }
+    split_store<NT, NV>(v, e, row, k, XH, XL, XS);
 }
 
 // ---- GEMM ------------------------------------------------------------------------
@@ -271,32 +276,41 @@ __device__ __forceinline__ long q_i8(uint32_t n0, uint32_t n1) {
     return (long)(((uint64_t)b << 32) | a);
 }
 
-template <bool NATIVE, int FJ, int FI, int WJ, int WI, int KS, int KB>
+// Weight formats of the LDS GEMM: GGUF Q4_0 blocks, or Q4_K super-blocks
+// taken as 32-element sub-blocks (value (d sc) q - dmin mn, parser.rs:549-593).
+constexpr int WF_Q4_0 = 0, WF_Q4_K = 1;
+
+template <bool NATIVE, int WF, int FJ, int FI, int WJ, int WI, int KS, int KB>
 struct GemmCfg {
+    static_assert(WF == WF_Q4_0 || !NATIVE, "Q4_K products in float mode only");
     static constexpr int NW = WJ * WI * KS;
     static constexpr int NT = NW * 64;
     static constexpr int TJ = WJ * FJ * 16;
     static constexpr int TI = WI * FI * 16;
     static constexpr int CB = KB * KS;                      // blocks per chunk
     static constexpr int WN_BYTES = TJ * Lds<CB>::WN_STRIDE;
-    static constexpr int WD_BYTES = (TJ * CB * 2 + 15) & ~15;
-    // float: x_hi and x_lo tiles; native: int8 codes and the f32 block scales
+    // Q4_0: the f16 d of each (row, block); Q4_K: f32 pairs {d sc, 8 d sc - dmin mn}
+    static constexpr int WD_BYTES = WF == WF_Q4_K ? TJ * CB * 8 : (TJ * CB * 2 + 15) & ~15;
+    // float: x_hi and x_lo tiles (Q4_K: and the x block sums); native: int8
+    // codes and the f32 block scales
     static constexpr int X_BYTES = TI * (NATIVE ? Lds<CB>::XC_STRIDE : Lds<CB>::X_STRIDE);
-    static constexpr int XS_BYTES = NATIVE ? TI * CB * 4 : 0;
-    static constexpr int STAGE = WN_BYTES + WD_BYTES + (NATIVE ? X_BYTES + XS_BYTES : 2 * X_BYTES);
+    static constexpr bool XSUMS = NATIVE || WF == WF_Q4_K;
+    static constexpr int XS_BYTES = XSUMS ? TI * CB * 4 : 0;
+    static constexpr int STAGE = WN_BYTES + WD_BYTES + (NATIVE ? X_BYTES : 2 * X_BYTES) + XS_BYTES;
     static constexpr int STAGE_AL = (STAGE + 15) & ~15;
     static constexpr int WBLK = (TJ * CB + NT - 1) / NT;                          // weight blocks per thread
+    static constexpr int WWORDS = WF == WF_Q4_K ? 12 : 5;  // dwords a weight block's loads bring
     static constexpr int XU = (TI * CB * (NATIVE ? 2 : 4) + NT - 1) / NT;          // 16-byte x units per thread
-    static constexpr int XSU = NATIVE ? (TI * CB + NT - 1) / NT : 0;              // scale dwords per thread
+    static constexpr int XSU = XSUMS ? (TI * CB + NT - 1) / NT : 0;              // scale / sum dwords per thread
     static constexpr int RED = (KS > 1) ? (KS - 1) * WJ * WI * FJ * FI * 64 * 16 : 0;
     // two staging buffers; the K-split sums reuse the same LDS at the end
     static constexpr int LDS = (2 * STAGE_AL > RED) ? 2 * STAGE_AL : RED;
 };
 
 // One chunk's global loads, held in registers until they are written to LDS.
-template <int WBLK, int XU, int XSU>
+template <int WBLK, int WWORDS, int XU, int XSU>
 struct Staged {
-    uint32_t w[WBLK][5];
+    uint32_t w[WBLK][WWORDS];
     u32x4 x0[XU], x1[XU];       // float: x_hi, x_lo; native: codes (x1 unused)
     uint32_t xs[XSU > 0 ? XSU : 1];
 };
@@ -311,18 +325,41 @@ __device__ __forceinline__ void tile_of(int nj, int ni, int& bx, int& by) {
     by = t / nj;
 }
 
+// 32-element sub-block j (0..7) of a Q4_K super-block: its 6-bit scale and
+// min from the 12 scale bytes s[0..11] (header dwords s03, s47, s811), as
+// the reference unpacks them (parser.rs:563-569).
+__device__ __forceinline__ void q4k_sub_scale_min(uint32_t s03, uint32_t s47, uint32_t s811, int j, int& sc,
+                                                  int& mn) {
+    if (j < 4) {  // sc = s[j] & 63, mn = s[j + 4] & 63
+        sc = (int)((s03 >> (8 * j)) & 63u);
+        mn = (int)((s47 >> (8 * j)) & 63u);
+    } else {      // i = j - 4: sc = (s[i] >> 6) | (s[i + 8] & 15) << 2, mn = (s[i + 4] >> 6) | (s[i + 8] >> 4) << 2
+        const int i = j - 4;
+        const uint32_t si = (s03 >> (8 * i)) & 0xFFu, ti = (s47 >> (8 * i)) & 0xFFu, ui = (s811 >> (8 * i)) & 0xFFu;
+        sc = (int)((si >> 6) | ((ui & 15u) << 2));
+        mn = (int)((ti >> 6) | ((ui >> 4) << 2));
+    }
+}
+
 // NATIVE = false: X0 / X1 = x_hi / x_lo (f16 [m, k]), XE the row exponents.
 // NATIVE = true:  X0 = Q8_0 codes (int8 [m, k]), X1 = their f32 block scales
 // [m, nb] (quantize_row_q8_0); DUMP writes the int32 block dots to
 // P[(i * n + j) * nb + b] instead of forming Y.
-template <bool NATIVE, bool DUMP, int FJ, int FI, int WJ, int WI, int KS, int KB>
+// WF = WF_Q4_K (float mode): W holds Q4_K super-blocks, nb counts their
+// 32-element sub-blocks, and XS the sums of each row's scaled x' over each
+// sub-block ([m, nb] f32).  A sub-block's nibbles are staged as a Q4_0
+// block's, so the MFMAs give sum (q - 8) x'; with D = d sc and M = dmin mn
+// the sub-block adds D sum (q - 8) x' + (8 D - M) sum x' = sum (D q - M) x'.
+template <bool NATIVE, bool DUMP, int WF, int FJ, int FI, int WJ, int WI, int KS, int KB>
 __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_kernel(
     const uint8_t* __restrict__ W, int n, int nb, const void* __restrict__ X0, const void* __restrict__ X1,
-    const int* __restrict__ XE, int m, float* __restrict__ Y, int32_t* __restrict__ P, int accy) {
-    using C = GemmCfg<NATIVE, FJ, FI, WJ, WI, KS, KB>;
+    const int* __restrict__ XE, int m, float* __restrict__ Y, int32_t* __restrict__ P, int accy,
+    const float* __restrict__ XS) {
+    using C = GemmCfg<NATIVE, WF, FJ, FI, WJ, WI, KS, KB>;
+    constexpr bool QK = WF == WF_Q4_K;
     constexpr int CB = C::CB;
     constexpr int XSTR = NATIVE ? Lds<CB>::XC_STRIDE : Lds<CB>::X_STRIDE;
-    using S = Staged<C::WBLK, C::XU, C::XSU>;
+    using S = Staged<C::WBLK, C::WWORDS, C::XU, C::XSU>;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -334,12 +371,15 @@ __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_kernel(
     const int j0 = bx * C::TJ;
     const int i0 = by * C::TI;
     const int k = nb * 32;
-    const uint32_t row_bytes = (uint32_t)nb * 18u;
+    // Q4_K: 144-byte super-blocks of 8 sub-blocks (nb % 8 == 0), rows 16-byte aligned
+    const uint32_t row_bytes = QK ? (uint32_t)(nb / 8) * 144u : (uint32_t)nb * 18u;
     const uint32_t wbytes = (uint32_t)n * row_bytes;
     const __amdgpu_buffer_rsrc_t wrs = make_rsrc(W, wbytes);
     const uint32_t xbytes = (uint32_t)m * (uint32_t)k * (NATIVE ? 1u : 2u);
     const __amdgpu_buffer_rsrc_t x0rs = make_rsrc(X0, xbytes);
     const __amdgpu_buffer_rsrc_t x1rs = make_rsrc(X1, NATIVE ? (uint32_t)m * (uint32_t)nb * 4u : xbytes);
+    // per-(row, block) f32 x data: native's Q8_0 scales (X1), Q4_K's x' sums (XS)
+    const __amdgpu_buffer_rsrc_t xsrs = QK ? make_rsrc(XS, (uint32_t)m * (uint32_t)nb * 4u) : x1rs;
     const int nchunks = (nb + CB - 1) / CB;
 
     // live == false (a chunk past the end) loads nothing through out-of-range
@@ -351,6 +391,20 @@ __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_kernel(
             const int idx = threadIdx.x + u * C::NT;
             const int jl = idx / CB, bl = idx % CB;
             const int j = j0 + jl, b = c * CB + bl;
+            if constexpr (QK) {
+                // the super-block's 16-byte header (d, dmin, scales) and the 32
+                // bytes whose low (even b) or high (odd b) nibbles are sub-block b
+                const bool ok = live && idx < C::TJ * CB && j < n && b < nb;
+                const uint32_t hoff = (uint32_t)j * row_bytes + (uint32_t)(b >> 3) * 144u;
+                const uint32_t qoff = hoff + 16u + 32u * (uint32_t)((b & 7) >> 1);
+                const u32x4 h = buf_load_b128(wrs, ok ? hoff : RSRC_OOB);
+                const u32x4 q0 = buf_load_b128(wrs, ok ? qoff : RSRC_OOB);
+                const u32x4 q1 = buf_load_b128(wrs, ok ? qoff + 16u : RSRC_OOB);
+                r.w[u][0] = h.x; r.w[u][1] = h.y; r.w[u][2] = h.z; r.w[u][3] = h.w;
+                r.w[u][4] = q0.x; r.w[u][5] = q0.y; r.w[u][6] = q0.z; r.w[u][7] = q0.w;
+                r.w[u][8] = q1.x; r.w[u][9] = q1.y; r.w[u][10] = q1.z; r.w[u][11] = q1.w;
+                continue;
+            }
             const uint32_t off = (live && idx < C::TJ * CB && j < n && b < nb)
                                      ? (uint32_t)j * row_bytes + (uint32_t)b * 18u
                                      : RSRC_OOB;
@@ -361,7 +415,7 @@ __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_kernel(
             // window: its tail dword is read 2 bytes early and shifted when the
             // block is stored (not here: that would wait for the load now)
             const bool over = base < wbytes && base + 20u > wbytes;
-            r.w[u][4] = buf_load_b32(wrs, over ? wbytes - 4u : base + 16u);
+            r.w[u][C::WWORDS - 1] = buf_load_b32(wrs, over ? wbytes - 4u : base + 16u);
         }
         constexpr int UPR = CB * (NATIVE ? 2 : 4);  // 16-byte units per x row and chunk
 #pragma unroll
@@ -376,7 +430,7 @@ __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_kernel(
             r.x0[u] = buf_load_b128(x0rs, off);
             if constexpr (!NATIVE) r.x1[u] = buf_load_b128(x1rs, off);
         }
-        if constexpr (NATIVE) {
+        if constexpr (C::XSUMS) {
 #pragma unroll
             for (int u = 0; u < C::XSU; u++) {
                 const int idx = threadIdx.x + u * C::NT;
@@ -385,7 +439,7 @@ __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_kernel(
                 const uint32_t off = (live && idx < C::TI * CB && i < m && b < nb)
                                          ? ((uint32_t)i * (uint32_t)nb + (uint32_t)b) * 4u
                                          : RSRC_OOB;
-                r.xs[u] = buf_load_b32(x1rs, off);
+                r.xs[u] = buf_load_b32(xsrs, off);
             }
         }
     };
@@ -395,15 +449,39 @@ __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_kernel(
         uint16_t* wd = reinterpret_cast<uint16_t*>(st + C::WN_BYTES);
         uint8_t* x0s = st + C::WN_BYTES + C::WD_BYTES;
         uint8_t* x1s = x0s + C::X_BYTES;
+        uint8_t* xss = x0s + (NATIVE ? 1 : 2) * C::X_BYTES;
 #pragma unroll
         for (int u = 0; u < C::WBLK; u++) {
             const int idx = threadIdx.x + u * C::NT;
-            if (idx < C::TJ * CB) {
+            if constexpr (QK) {
+                if (idx >= C::TJ * CB) continue;
+                const int jl = idx / CB, bl = idx % CB;
+                const int b = c * CB + bl;
+                // sub-block element t is the nibble of byte t of the 32: stage
+                // byte t = element t | element t + 16 << 4, a Q4_0 block's order
+                const uint32_t sh = (b & 1) ? 4u : 0u;
+                uint32_t q[8];
+#pragma unroll
+                for (int t = 0; t < 8; t++) q[t] = (r.w[u][4 + t] >> sh) & 0x0F0F0F0Fu;
+                uint2* dst = reinterpret_cast<uint2*>(wn + jl * Lds<CB>::WN_STRIDE + bl * 16);
+                dst[0] = uint2{q[0] | (q[4] << 4), q[1] | (q[5] << 4)};
+                dst[1] = uint2{q[2] | (q[6] << 4), q[3] | (q[7] << 4)};
+                // D = d sc and 8 D - M (M = dmin mn) in f32, block-major; rows or
+                // sub-blocks past the matrix loaded zeros: D = 8 D - M = 0
+                int sc, mn;
+                q4k_sub_scale_min(r.w[u][1], r.w[u][2], r.w[u][3], b & 7, sc, mn);
+                const float dd = h2f(r.w[u][0] & 0xFFFFu) * (float)sc;
+                const float mm = h2f(r.w[u][0] >> 16) * (float)mn;
+                float* wdf = reinterpret_cast<float*>(st + C::WN_BYTES);
+                wdf[bl * C::TJ + jl] = dd;
+                wdf[(CB + bl) * C::TJ + jl] = 8.0f * dd - mm;
+            } else if (idx < C::TJ * CB) {
                 const int jl = idx / CB, bl = idx % CB;
                 const int j = j0 + jl, b = c * CB + bl;
                 const uint32_t off = (j < n && b < nb) ? (uint32_t)j * row_bytes + (uint32_t)b * 18u : RSRC_OOB;
                 const uint32_t base = off & ~3u;
-                const uint32_t w4 = (base < wbytes && base + 20u > wbytes) ? (r.w[u][4] >> 16) : r.w[u][4];
+                const uint32_t wt = r.w[u][C::WWORDS - 1];
+                const uint32_t w4 = (base < wbytes && base + 20u > wbytes) ? (wt >> 16) : wt;
                 // block g = j * nb + b starts at 18 g: 2 bytes past a dword when g is odd
                 const bool odd = (((uint32_t)j * (uint32_t)nb + (uint32_t)b) & 1u) != 0;
                 const uint32_t sel = odd ? 0x07060504u : 0x05040302u;
@@ -430,8 +508,8 @@ __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_kernel(
                 if constexpr (!NATIVE) *reinterpret_cast<u32x4*>(x1s + il * XSTR + q * 16) = r.x1[u];
             }
         }
-        if constexpr (NATIVE) {
-            uint32_t* xs = reinterpret_cast<uint32_t*>(x1s);
+        if constexpr (C::XSUMS) {
+            uint32_t* xs = reinterpret_cast<uint32_t*>(xss);
 #pragma unroll
             for (int u = 0; u < C::XSU; u++) {
                 const int idx = threadIdx.x + u * C::NT;
@@ -456,13 +534,15 @@ __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_kernel(
         const uint8_t* st = lds + buf * C::STAGE_AL;
         const uint8_t* wn = st;
         const uint16_t* wd = reinterpret_cast<const uint16_t*>(st + C::WN_BYTES);
+        const float* wdf = reinterpret_cast<const float*>(st + C::WN_BYTES);
         const uint8_t* x0s = st + C::WN_BYTES + C::WD_BYTES;
         const uint8_t* x1s = x0s + C::X_BYTES;
+        const float* xss = reinterpret_cast<const float*>(x0s + (NATIVE ? 1 : 2) * C::X_BYTES);
 #pragma unroll
         for (int kb = 0; kb < KB; kb++) {
             const int bl = ks * KB + kb;  // this wave's block within the chunk
             typename std::conditional<NATIVE, long, half8_t>::type aq[FJ];
-            f32x4 dv[FJ];
+            f32x4 dv[FJ], ev[FJ];
 #pragma unroll
             for (int a = 0; a < FJ; a++) {
                 const int jt = (wj * FJ + a) * 16;
@@ -472,15 +552,20 @@ __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_kernel(
                 const uint32_t n0 = (nb8.x >> sh) & 0x0F0F0F0Fu, n1 = (nb8.y >> sh) & 0x0F0F0F0Fu;
                 if constexpr (NATIVE) aq[a] = q_i8(n0, n1);
                 else aq[a] = q_f16(n0, n1);
-                const uint2 dd = *reinterpret_cast<const uint2*>(wd + bl * C::TJ + jt + 4 * g);
-                dv[a] = f32x4{h2f(dd.x & 0xFFFFu), h2f(dd.x >> 16), h2f(dd.y & 0xFFFFu), h2f(dd.y >> 16)};
+                if constexpr (QK) {
+                    dv[a] = *reinterpret_cast<const f32x4*>(wdf + bl * C::TJ + jt + 4 * g);
+                    ev[a] = *reinterpret_cast<const f32x4*>(wdf + (CB + bl) * C::TJ + jt + 4 * g);
+                } else {
+                    const uint2 dd = *reinterpret_cast<const uint2*>(wd + bl * C::TJ + jt + 4 * g);
+                    dv[a] = f32x4{h2f(dd.x & 0xFFFFu), h2f(dd.x >> 16), h2f(dd.y & 0xFFFFu), h2f(dd.y >> 16)};
+                }
             }
 #pragma unroll
             for (int b = 0; b < FI; b++) {
                 const int il = (wi * FI + b) * 16 + r16;
                 if constexpr (NATIVE) {
                     const long bx = *reinterpret_cast<const long*>(x0s + il * XSTR + bl * 32 + g * 8);
-                    const float sx = reinterpret_cast<const float*>(x1s)[bl * C::TI + il];
+                    const float sx = xss[bl * C::TI + il];
 #pragma unroll
                     for (int a = 0; a < FJ; a++) {
                         typedef int i32x4_t __attribute__((ext_vector_type(4)));
@@ -505,13 +590,20 @@ __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_kernel(
                     const int xo = il * XSTR + bl * 64 + g * 16;
                     const half8_t bh = *reinterpret_cast<const half8_t*>(x0s + xo);
                     const half8_t bl8 = *reinterpret_cast<const half8_t*>(x1s + xo);
+                    const float sx = QK ? xss[bl * C::TI + il] : 0.0f;
 #pragma unroll
                     for (int a = 0; a < FJ; a++) {
                         const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
                         f32x4 t = __builtin_amdgcn_mfma_f32_16x16x32_f16(aq[a], bh, z, 0, 0, 0);
                         t = __builtin_amdgcn_mfma_f32_16x16x32_f16(aq[a], bl8, t, 0, 0, 0);
+                        if constexpr (QK) {
 #pragma unroll
-                        for (int u = 0; u < 4; u++) acc[a][b][u] = fmaf(dv[a][u], t[u], acc[a][b][u]);
+                            for (int u = 0; u < 4; u++)
+                                acc[a][b][u] = fmaf(dv[a][u], t[u], fmaf(ev[a][u], sx, acc[a][b][u]));
+                        } else {
+#pragma unroll
+                            for (int u = 0; u < 4; u++) acc[a][b][u] = fmaf(dv[a][u], t[u], acc[a][b][u]);
+                        }
                     }
                 }
             }
@@ -1398,11 +1490,11 @@ hipError_t launch_skinny(const uint8_t* w, int n, int nb, const float* x, int m,
     return p.mt == 1 ? go(M1{}, F{}) : p.mt == 2 ? go(M2{}, F{}) : p.mt == 3 ? go(M3{}, F{}) : go(M4{}, F{});
 }
 
-template <bool NATIVE, bool DUMP, int FJ, int FI, int WJ, int WI, int KS, int KB>
+template <bool NATIVE, bool DUMP, int WF, int FJ, int FI, int WJ, int WI, int KS, int KB>
 hipError_t launch_cfg(const uint8_t* w, int n, int nb, const void* x0, const void* x1, const int* xe, int m,
-                      float* y, int32_t* p, hipStream_t s, int accy) {
-    using C = GemmCfg<NATIVE, FJ, FI, WJ, WI, KS, KB>;
-    auto kern = gemm_q4_0_kernel<NATIVE, DUMP, FJ, FI, WJ, WI, KS, KB>;
+                      float* y, int32_t* p, hipStream_t s, int accy, const float* xs) {
+    using C = GemmCfg<NATIVE, WF, FJ, FI, WJ, WI, KS, KB>;
+    auto kern = gemm_q4_0_kernel<NATIVE, DUMP, WF, FJ, FI, WJ, WI, KS, KB>;
     static_assert(C::LDS >= C::RED, "K-split sums fit the staging LDS");
     static_assert(C::LDS <= 160 * 1024, "LDS per workgroup");
     if (C::LDS > 65536) {
@@ -1411,7 +1503,7 @@ hipError_t launch_cfg(const uint8_t* w, int n, int nb, const void* x0, const voi
         if (e != hipSuccess) return e;
     }
     const unsigned tiles = (unsigned)((n + C::TJ - 1) / C::TJ) * (unsigned)((m + C::TI - 1) / C::TI);
-    launch_kernel(kern, dim3(tiles), dim3(C::NT), (size_t)C::LDS, s, w, n, nb, x0, x1, xe, m, y, p, accy);
+    launch_kernel(kern, dim3(tiles), dim3(C::NT), (size_t)C::LDS, s, w, n, nb, x0, x1, xe, m, y, p, accy, xs);
     return hipGetLastError();
 }
 
@@ -1419,24 +1511,25 @@ hipError_t launch_cfg(const uint8_t* w, int n, int nb, const void* x0, const voi
 // re-reads of x and W from L2).  M >= 256: swept on MI355X at M = 512 and
 // 2048 over tile shapes, waves and chunk sizes, per mode (the native kernel
 // stages half the x bytes and keeps fewer registers).
-template <bool NATIVE, bool DUMP>
+// WF_Q4_K: the float shapes; xs the x' block sums.
+template <bool NATIVE, bool DUMP, int WF = WF_Q4_0>
 hipError_t launch_tiles(const uint8_t* w, int n, int nb, const void* x0, const void* x1, const int* xe, int m,
-                        float* y, int32_t* p, hipStream_t s, int accy = 0) {
+                        float* y, int32_t* p, hipStream_t s, int accy = 0, const float* xs = nullptr) {
     const int cus = device_cu_count();
     if (NATIVE) {
-        if (m >= 1024) return launch_cfg<NATIVE, DUMP, 2, 2, 2, 2, 2, 2>(w, n, nb, x0, x1, xe, m, y, p, s, accy);
-        if (m >= 256) return launch_cfg<NATIVE, DUMP, 2, 4, 2, 2, 2, 2>(w, n, nb, x0, x1, xe, m, y, p, s, accy);
+        if (m >= 1024) return launch_cfg<NATIVE, DUMP, WF, 2, 2, 2, 2, 2, 2>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
+        if (m >= 256) return launch_cfg<NATIVE, DUMP, WF, 2, 4, 2, 2, 2, 2>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
     } else {
-        if (m >= 1024) return launch_cfg<NATIVE, DUMP, 4, 4, 2, 2, 2, 1>(w, n, nb, x0, x1, xe, m, y, p, s, accy);
+        if (m >= 1024) return launch_cfg<NATIVE, DUMP, WF, 4, 4, 2, 2, 2, 1>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
         // 128 x 128 tiles from m = 128 where they fill three quarters of
         // the CUs (the 7B prefill's 28672-row gate/up GEMM at 128 rows: 224
         // tiles, 110 us against 119 us in 128 x 64 tiles); 128 x 64 tiles from
         // m = 256, and from m = 128 where they alone fill the CUs (prefill
         // 15.7 -> 12.3 ms; taken for every matrix: 14.9 ms)
         if (m >= 128 && m < 256 && 4 * (size_t)((n + 127) / 128) * ((m + 127) / 128) >= 3 * (size_t)cus)
-            return launch_cfg<NATIVE, DUMP, 4, 4, 2, 2, 2, 1>(w, n, nb, x0, x1, xe, m, y, p, s, accy);
+            return launch_cfg<NATIVE, DUMP, WF, 4, 4, 2, 2, 2, 1>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
         if (m >= 256 || (m >= 128 && (size_t)((n + 127) / 128) * ((m + 63) / 64) >= (size_t)cus))
-            return launch_cfg<NATIVE, DUMP, 4, 2, 2, 2, 2, 2>(w, n, nb, x0, x1, xe, m, y, p, s, accy);
+            return launch_cfg<NATIVE, DUMP, WF, 4, 2, 2, 2, 2, 2>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
     }
     const size_t t32 = (size_t)((n + 31) / 32) * ((m + 63) / 64);  // 32 x 64 tiles
     if (m >= 48 && t32 >= (size_t)cus) {
@@ -1445,13 +1538,19 @@ hipError_t launch_tiles(const uint8_t* w, int n, int nb, const void* x0, const v
             // (us at 128 rows, 4096 x 4096 / 4096 x 14336 / 6144 x 4096: 4-wave
             // 32 x 64 tiles 37.2 / 106.5 / 66.0, 8-wave 30.3 / 89.1 / 51.5,
             // 64 x 64 38.7 / 112.9 / 40.0)
-            if (t32 > (size_t)cus) return launch_cfg<NATIVE, DUMP, 2, 4, 2, 1, 4, 2>(w, n, nb, x0, x1, xe, m, y, p, s, accy);
-            return launch_cfg<NATIVE, DUMP, 2, 2, 1, 2, 4, 2>(w, n, nb, x0, x1, xe, m, y, p, s, accy);
+            if (t32 > (size_t)cus) {
+                // (Q4_K's f32 scale pairs and x' sums: chunks of 4 blocks fit the LDS)
+                if constexpr (WF == WF_Q4_K)
+                    return launch_cfg<NATIVE, DUMP, WF, 2, 4, 2, 1, 4, 1>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
+                else
+                    return launch_cfg<NATIVE, DUMP, WF, 2, 4, 2, 1, 4, 2>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
+            }
+            return launch_cfg<NATIVE, DUMP, WF, 2, 2, 1, 2, 4, 2>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
         }
-        return launch_cfg<NATIVE, DUMP, 2, 4, 1, 1, 4, 2>(w, n, nb, x0, x1, xe, m, y, p, s, accy);
+        return launch_cfg<NATIVE, DUMP, WF, 2, 4, 1, 1, 4, 2>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
     }
-    if (m > 16) return launch_cfg<NATIVE, DUMP, 1, 2, 1, 1, 4, 2>(w, n, nb, x0, x1, xe, m, y, p, s, accy);
-    return launch_cfg<NATIVE, DUMP, 1, 1, 1, 1, 4, 8>(w, n, nb, x0, x1, xe, m, y, p, s, accy);
+    if (m > 16) return launch_cfg<NATIVE, DUMP, WF, 1, 2, 1, 1, 4, 2>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
+    return launch_cfg<NATIVE, DUMP, WF, 1, 1, 1, 1, 4, 8>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
 }
 
 }  // namespace
@@ -1498,6 +1597,12 @@ size_t gemm_scratch_bytes(size_t m, size_t n, size_t k, bool native) {
     return 2 * xb + ((m * 4 + 255) & ~(size_t)255);
 }
 
+size_t gemm_q4_k_scratch_bytes(size_t m, size_t k) {
+    // the float layout (x_hi, x_lo, exponents) and the x' sums of each 32-element block
+    const size_t xb = (m * k * 2 + 255) & ~(size_t)255;
+    return 2 * xb + ((m * 4 + 255) & ~(size_t)255) + ((m * (k / QK) * 4 + 255) & ~(size_t)255);
+}
+
 hipError_t launch_gemm_q4_0(const uint8_t* w, size_t n, size_t k, const float* x, size_t m, float* y,
                             void* scratch, int* counters, hipStream_t s) {
     if (n == 0 || m == 0) return hipSuccess;
@@ -1516,7 +1621,7 @@ hipError_t launch_gemm_q4_0(const uint8_t* w, size_t n, size_t k, const float* x
     int* xe = reinterpret_cast<int*>(reinterpret_cast<uint8_t*>(scratch) + 2 * xb);
     if (k <= (size_t)16 * XPREP_FAST_THREADS)
         launch_kernel(gemm_xprep_fast_kernel, dim3((unsigned)m), dim3(XPREP_FAST_THREADS), 0, s, x, (int)k, xh, xl,
-                      xe);
+                      xe, (float*)nullptr);
     else
         launch_kernel(gemm_xprep_kernel, dim3((unsigned)m), dim3(XPREP_THREADS), 0, s, x, (int)k, xh, xl, xe);
     hipError_t e = hipGetLastError();
@@ -1524,43 +1629,50 @@ hipError_t launch_gemm_q4_0(const uint8_t* w, size_t n, size_t k, const float* x
     return launch_tiles<false, false>(w, (int)n, (int)(k / QK), xh, xl, xe, (int)m, y, nullptr, s);
 }
 
-hipError_t launch_gemm_q4_0_pro(const uint8_t* w, size_t n, size_t k, const float* x, size_t m, float* y,
+hipError_t launch_gemm_tiles_ex(WType t, const uint8_t* w, size_t n, size_t k, const float* x, size_t m, float* y,
                                 void* scratch, int pro, const float* g, float eps, bool accumulate, hipStream_t s) {
     if (n == 0 || m == 0) return hipSuccess;
-    if (m <= GEMM_XTILE_M || m <= GEMM_SMALL_M || k > (size_t)16 * XPREP_FAST_THREADS || k % QK != 0 ||
-        (pro != 1 && pro != 2) || (pro == 1 && !g))
+    const bool q4k = t == WType::Q4_K;
+    if ((t != WType::Q4_0 && !q4k) || k == 0 || k % (q4k ? QK_K : QK) != 0 || (pro < 0 || pro > 2) ||
+        (pro == 1 && !g))
         return hipErrorInvalidValue;
+    // Q4_0's m <= GEMM_XTILE_M rows belong to the x-tile kernel; the x' block
+    // sums and the prologues come from the one-read x prep (k <= 16384)
+    if ((!q4k && m <= GEMM_XTILE_M) || ((q4k || pro != 0) && k > (size_t)16 * XPREP_FAST_THREADS))
+        return hipErrorInvalidValue;
+    // 32-bit buffer offsets, out-of-range slots at RSRC_OOB
+    const size_t wb = n * (k / (q4k ? QK_K : QK)) * (q4k ? Q4_K_BYTES : Q4_0_BYTES);
+    if (wb > FUSED_MAX_WEIGHT_BYTES || m * k * 2 > FUSED_MAX_WEIGHT_BYTES) return hipErrorInvalidValue;
     const size_t xb = (m * k * 2 + 255) & ~(size_t)255;
     _Float16* xh = reinterpret_cast<_Float16*>(scratch);
     _Float16* xl = reinterpret_cast<_Float16*>(reinterpret_cast<uint8_t*>(scratch) + xb);
     int* xe = reinterpret_cast<int*>(reinterpret_cast<uint8_t*>(scratch) + 2 * xb);
+    float* xs = q4k ? reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(scratch) + 2 * xb +
+                                               ((m * 4 + 255) & ~(size_t)255))
+                    : nullptr;
+    const dim3 grid((unsigned)m);
     if (pro == 1)
-        launch_kernel(gemm_xprep_pro_kernel<1>, dim3((unsigned)m), dim3(XPREP_FAST_THREADS), 0, s, x, (int)k, g, eps,
-                      xh, xl, xe);
+        launch_kernel(gemm_xprep_pro_kernel<1>, grid, dim3(XPREP_FAST_THREADS), 0, s, x, (int)k, g, eps, xh, xl, xe,
+                      xs);
+    else if (pro == 2)
+        launch_kernel(gemm_xprep_pro_kernel<2>, grid, dim3(XPREP_FAST_THREADS), 0, s, x, (int)k, g, eps, xh, xl, xe,
+                      xs);
+    else if (k <= (size_t)16 * XPREP_FAST_THREADS)
+        launch_kernel(gemm_xprep_fast_kernel, grid, dim3(XPREP_FAST_THREADS), 0, s, x, (int)k, xh, xl, xe, xs);
     else
-        launch_kernel(gemm_xprep_pro_kernel<2>, dim3((unsigned)m), dim3(XPREP_FAST_THREADS), 0, s, x, (int)k, g, eps,
-                      xh, xl, xe);
+        launch_kernel(gemm_xprep_kernel, grid, dim3(XPREP_THREADS), 0, s, x, (int)k, xh, xl, xe);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    return launch_tiles<false, false>(w, (int)n, (int)(k / QK), xh, xl, xe, (int)m, y, nullptr, s, accumulate ? 1 : 0);
+    const int accy = accumulate ? 1 : 0;
+    if (q4k)
+        return launch_tiles<false, false, WF_Q4_K>(w, (int)n, (int)(k / QK), xh, xl, xe, (int)m, y, nullptr, s, accy,
+                                                   xs);
+    return launch_tiles<false, false>(w, (int)n, (int)(k / QK), xh, xl, xe, (int)m, y, nullptr, s, accy);
 }
 
-hipError_t launch_gemm_q4_0_accumulate(const uint8_t* w, size_t n, size_t k, const float* x, size_t m, float* y,
-                                       void* scratch, hipStream_t s) {
-    if (n == 0 || m == 0) return hipSuccess;
-    if (m <= GEMM_XTILE_M || m <= GEMM_SMALL_M || k % QK != 0) return hipErrorInvalidValue;
-    const size_t xb = (m * k * 2 + 255) & ~(size_t)255;
-    _Float16* xh = reinterpret_cast<_Float16*>(scratch);
-    _Float16* xl = reinterpret_cast<_Float16*>(reinterpret_cast<uint8_t*>(scratch) + xb);
-    int* xe = reinterpret_cast<int*>(reinterpret_cast<uint8_t*>(scratch) + 2 * xb);
-    if (k <= (size_t)16 * XPREP_FAST_THREADS)
-        launch_kernel(gemm_xprep_fast_kernel, dim3((unsigned)m), dim3(XPREP_FAST_THREADS), 0, s, x, (int)k, xh, xl,
-                      xe);
-    else
-        launch_kernel(gemm_xprep_kernel, dim3((unsigned)m), dim3(XPREP_THREADS), 0, s, x, (int)k, xh, xl, xe);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    return launch_tiles<false, false>(w, (int)n, (int)(k / QK), xh, xl, xe, (int)m, y, nullptr, s, 1);
+hipError_t launch_gemm_q4_k(const uint8_t* w, size_t n, size_t k, const float* x, size_t m, float* y,
+                            void* scratch, hipStream_t s) {
+    return launch_gemm_tiles_ex(WType::Q4_K, w, n, k, x, m, y, scratch, 0, nullptr, 0.0f, false, s);
 }
 
 hipError_t launch_gemm_q4_0_native(const uint8_t* w, size_t n, size_t k, const float* x, size_t m, float* y,

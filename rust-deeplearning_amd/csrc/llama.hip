@@ -694,6 +694,10 @@ struct LlamaModel {
         if (w.type == WType::Q4_0)
             return native ? launch_gemm_q4_0_native(w.dev, w.n, w.k, xin, m, y, nullptr, gemm_scratch, stream)
                           : launch_gemm_q4_0(w.dev, w.n, w.k, xin, m, y, gemm_scratch, gemm_cnt, stream);
+        if (kgemm(w, m)) {
+            const hipError_t e = launch_gemm_q4_k(w.dev, w.n, w.k, xin, m, y, gemm_scratch, stream);
+            if (e != hipErrorInvalidValue) return e;
+        }
         // rows four at a time through the fused GEMV (other types, or scales
         // beyond the GEMM's range)
         for (size_t r = 0; r < m; r += 4) {
@@ -857,6 +861,12 @@ struct LlamaModel {
     }
 
     static bool kquant(const Mat& w) { return w.type == WType::Q4_K || w.type == WType::Q6_K; }
+    // Q4_K products of m >= KQ_GEMM_MIN_M rows run on the LDS tile GEMM
+    static bool kgemm(const Mat& w, size_t m) {
+        return w.type == WType::Q4_K && m >= KQ_GEMM_MIN_M && w.k % QK_K == 0 && w.k <= 16384;
+    }
+    // the K-quant GEMVs with the decoder's steps folded into their launches
+    static bool kfold(const Mat& w, size_t m) { return kquant(w) && !kgemm(w, m); }
 
     // y rows (ystride floats apart) = epilogue(W . prologue(x rows)) through the
     // K-quant decoder fusion, four rows a launch
@@ -871,11 +881,12 @@ struct LlamaModel {
         return hipSuccess;
     }
 
-    // One layer of any resident types, any row count (m > 4 Q4_0 rows take the
-    // GEMM).  Q4_K / Q6_K matrices fold the RMSNorm in front of them, the
-    // residual add after o / down, the SwiGLU of combined gate/up rows and the
-    // RoPE + cache write of combined q/k/v rows into their GEMV launches; the
-    // other types run separate norm / add / SwiGLU / RoPE launches.
+    // One layer of any resident types, any row count (m > 4 Q4_0 rows and
+    // m >= KQ_GEMM_MIN_M Q4_K rows take the GEMMs).  Q4_K / Q6_K matrices on
+    // the GEMVs fold the RMSNorm in front of them, the residual add after o /
+    // down, the SwiGLU of combined gate/up rows and the RoPE + cache write of
+    // combined q/k/v rows into their GEMV launches; the other types run
+    // separate norm / add / SwiGLU / RoPE launches.
     hipError_t layer_plain(int l, size_t m) {
         const int d = cfg.dim, f = cfg.ffn_dim;
         Layer& L = layers[l];
@@ -888,25 +899,28 @@ struct LlamaModel {
         if (L.split_qkv) parts[0] = &L.q, parts[1] = &L.k, parts[2] = &L.v;
         const int cols[3] = {0, q_dim, q_dim + kv_dim};
         const int np = L.split_qkv ? 3 : 1;
-        // Q4_0 prompt chunks on the LDS tile GEMM (m > GEMM_XTILE_M) fold the
-        // RMSNorms, the SwiGLU and the residual adds into the GEMMs' x splits
-        // and stores (hipErrorInvalidValue: a shape they do not take, nothing
-        // launched, the separate launches below run instead)
+        // Q4_0 (m > GEMM_XTILE_M) and Q4_K prompt chunks on the LDS tile GEMM
+        // fold the RMSNorms, the SwiGLU and the residual adds into the GEMMs'
+        // x splits and stores (hipErrorInvalidValue: a shape they do not take,
+        // nothing launched, the separate launches below run instead)
         // (native layers keep their Linears' own products: no folding)
-        auto q4t = [&](const Mat& w) { return !L.native && m > GEMM_XTILE_M && w.type == WType::Q4_0; };
+        auto q4t = [&](const Mat& w) {
+            return !L.native && ((m > GEMM_XTILE_M && w.type == WType::Q4_0) || kgemm(w, m));
+        };
+        auto kfold_m = [&](const Mat& w) { return kfold(w, m); };
         const bool nat = L.native;
         bool qkv_done = false;
         if (np == 1 && q4t(L.qkv)) {
-            e = launch_gemm_q4_0_pro(L.qkv.dev, L.qkv.n, L.qkv.k, x, m, qkv, gemm_scratch, 1, L.attn_norm,
-                                     cfg.norm_eps, false, stream);
+            e = launch_gemm_tiles_ex(L.qkv.type, L.qkv.dev, L.qkv.n, L.qkv.k, x, m, qkv, gemm_scratch, 1,
+                                     L.attn_norm, cfg.norm_eps, false, stream);
             if (e != hipSuccess && e != hipErrorInvalidValue) return e;
             qkv_done = e == hipSuccess;
         }
         bool want_xn = false;
-        for (int i = 0; i < np; i++) want_xn |= !kquant(*parts[i]);
+        for (int i = 0; i < np; i++) want_xn |= !kfold_m(*parts[i]);
         if (want_xn && !qkv_done) rmsnorm(L.attn_norm);
         // a K-quant [Wq; Wk; Wv] also applies RoPE and writes the cache
-        const bool rope_fused = np == 1 && kquant(L.qkv);
+        const bool rope_fused = np == 1 && !qkv_done && kfold_m(L.qkv);
         for (size_t r = 0; rope_fused && r < m; r += 4) {
             const size_t mr = (m - r < 4) ? m - r : 4;
             e = launch_gemv_kquant_rope_kv(L.qkv.type, L.qkv.dev, L.qkv.n, d, x + r * d, mr, r, qkv + r * qkv_dim,
@@ -917,7 +931,7 @@ struct LlamaModel {
         }
         for (int i = 0; i < np && !rope_fused && !qkv_done; i++) {
             const Mat& w = *parts[i];
-            if (kquant(w)) {
+            if (kfold_m(w)) {
                 e = kq_linear(w, x, d, m, qkv + cols[i], qkv_dim, GEMV_PRO_RMSNORM, L.attn_norm, GEMV_EPI_STORE);
             } else if (np == 1 || m == 1) {  // whole rows, or one row: in place
                 e = linear(w, xn, m, qkv + cols[i], nat);
@@ -932,11 +946,12 @@ struct LlamaModel {
         e = cfg.kv_f16 ? layer_attention<_Float16>(l, m, !rope_fused) : layer_attention<float>(l, m, !rope_fused);
         if (e != hipSuccess) return e;
         // ---- x += att . Wo^T ----
-        e = q4t(L.o) ? launch_gemm_q4_0_accumulate(L.o.dev, L.o.n, L.o.k, att, m, x, gemm_scratch, stream)
+        e = q4t(L.o) ? launch_gemm_tiles_ex(L.o.type, L.o.dev, L.o.n, L.o.k, att, m, x, gemm_scratch, 0, nullptr,
+                                            0.0f, true, stream)
                      : hipErrorInvalidValue;
         if (e != hipSuccess && e != hipErrorInvalidValue) return e;
         if (e == hipSuccess) {
-        } else if (kquant(L.o)) {
+        } else if (kfold_m(L.o)) {
             e = kq_linear(L.o, att, q_dim, m, x, d, GEMV_PRO_NONE, nullptr, GEMV_EPI_RESIDUAL);
             if (e != hipSuccess) return e;
         } else {
@@ -949,13 +964,13 @@ struct LlamaModel {
         // x split forms h from them
         bool gu_raw = false;
         if (!L.split_gu && q4t(L.gu) && q4t(L.down)) {
-            e = launch_gemm_q4_0_pro(L.gu.dev, L.gu.n, L.gu.k, x, m, gu, gemm_scratch, 1, L.ffn_norm, cfg.norm_eps,
-                                     false, stream);
+            e = launch_gemm_tiles_ex(L.gu.type, L.gu.dev, L.gu.n, L.gu.k, x, m, gu, gemm_scratch, 1, L.ffn_norm,
+                                     cfg.norm_eps, false, stream);
             if (e != hipSuccess && e != hipErrorInvalidValue) return e;
             gu_raw = e == hipSuccess;
         }
         if (gu_raw) {
-        } else if (!L.split_gu && kquant(L.gu)) {
+        } else if (!L.split_gu && kfold_m(L.gu)) {
             e = kq_linear(L.gu, x, d, m, hb, f, GEMV_PRO_RMSNORM, L.ffn_norm, GEMV_EPI_SWIGLU);
             if (e != hipSuccess) return e;
         } else if (!L.split_gu) {
@@ -963,11 +978,11 @@ struct LlamaModel {
             if ((e = linear(L.gu, xn, m, gu, nat)) != hipSuccess) return e;
             hipLaunchKernelGGL(swiglu_kernel, dim3(blocks_for(nf)), dim3(NT), 0, stream, gu, f, nf, hb);
         } else {
-            if (!kquant(L.gate) || !kquant(L.up)) rmsnorm(L.ffn_norm);
+            if (!kfold_m(L.gate) || !kfold_m(L.up)) rmsnorm(L.ffn_norm);
             const Mat* gp[2] = {&L.gate, &L.up};
             for (int i = 0; i < 2; i++) {
                 float* yo = gu + i * nf;
-                e = kquant(*gp[i]) ? kq_linear(*gp[i], x, d, m, yo, f, GEMV_PRO_RMSNORM, L.ffn_norm, GEMV_EPI_STORE)
+                e = kfold_m(*gp[i]) ? kq_linear(*gp[i], x, d, m, yo, f, GEMV_PRO_RMSNORM, L.ffn_norm, GEMV_EPI_STORE)
                                    : linear(*gp[i], xn, m, yo, nat);
                 if (e != hipSuccess) return e;
             }
@@ -975,15 +990,15 @@ struct LlamaModel {
         }
         // ---- x += h . Wdown^T ----
         if (gu_raw) {
-            e = launch_gemm_q4_0_pro(L.down.dev, L.down.n, L.down.k, gu, m, x, gemm_scratch, 2, nullptr, 0.0f, true,
-                                     stream);
+            e = launch_gemm_tiles_ex(L.down.type, L.down.dev, L.down.n, L.down.k, gu, m, x, gemm_scratch, 2, nullptr,
+                                     0.0f, true, stream);
             if (e != hipSuccess && e != hipErrorInvalidValue) return e;
             if (e == hipErrorInvalidValue) {  // the SwiGLU on its own, then the product
                 hipLaunchKernelGGL(swiglu_kernel, dim3(blocks_for(nf)), dim3(NT), 0, stream, gu, f, nf, hb);
                 if ((e = linear(L.down, hb, m, xn, nat)) != hipSuccess) return e;
                 hipLaunchKernelGGL(add_kernel, dim3(blocks_for(m * d)), dim3(NT), 0, stream, x, xn, m * d);
             }
-        } else if (kquant(L.down)) {
+        } else if (kfold_m(L.down)) {
             e = kq_linear(L.down, hb, f, m, x, d, GEMV_PRO_NONE, nullptr, GEMV_EPI_RESIDUAL);
             if (e != hipSuccess) return e;
         } else {
@@ -1280,6 +1295,8 @@ rdl_status rdl_llama_create_typed(const rdl_llama_config* cfg, const int32_t* ty
         for (size_t mm : {(size_t)1, (size_t)16, (size_t)32, (size_t)48, (size_t)64, mb})
             for (bool nat : {false, true})
                 gsb = std::max(gsb, rdl::gemm_scratch_bytes(std::min(mm, mb), sh[0], sh[1], nat));
+        // Q4_K matrices on the tile GEMM (x' block sums beside the split)
+        gsb = std::max(gsb, rdl::gemm_q4_k_scratch_bytes(mb, sh[1]));
     }
     if ((e = M.alloc(&M.gemm_scratch, gsb)) != hipSuccess) return fail_free(e);
     if ((e = M.alloc_t(&M.gemm_cnt, gcc)) != hipSuccess) return fail_free(e);

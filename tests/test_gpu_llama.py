@@ -396,20 +396,51 @@ def check_typed_model(m, ref, prompt, tok, steps=4):
     assert list(toks) == eager
 
 
-def test_q4_k_m_layers(rq, gpu):
-    """llama.cpp's Q4_K_M mix: layer 0 with Q6_K attn_v / ffn_down (split q/k/v,
-    RMSNorm in each part's GEMV; gate/up combined Q4_K with the SwiGLU in the
-    GEMV; residual adds in the o / down GEMVs), layer 1 all Q4_K (one q/k/v
-    launch), Q4_K embedding, Q6_K output matrix (final norm in its GEMV)."""
+def q4_k_m_mix():
     import rdlquant.llama as L
     t = {(L.TOKEN_EMBEDDING, 0): 12, (L.OUTPUT, 0): 14}
     for layer in range(2):
         for slot in (L.WQ, L.WK, L.WV, L.WO, L.W_GATE, L.W_UP, L.W_DOWN):
             t[(slot, layer)] = 12
     t[(L.WV, 0)] = t[(L.W_DOWN, 0)] = 14
+    return t
+
+
+def test_q4_k_m_layers(rq, gpu):
+    """llama.cpp's Q4_K_M mix: layer 0 with Q6_K attn_v / ffn_down (split q/k/v,
+    RMSNorm in each part's GEMV; gate/up combined Q4_K with the SwiGLU in the
+    GEMV; residual adds in the o / down GEMVs), layer 1 all Q4_K (one q/k/v
+    launch), Q4_K embedding, Q6_K output matrix (final norm in its GEMV)."""
     cfg = tiny_config(output_dtype=14)
-    m, ref, _ = build_typed(cfg, t, 2024)
+    m, ref, _ = build_typed(cfg, q4_k_m_mix(), 2024)
     check_typed_model(m, ref, [5, 17, 33, 2, 250, 7, 91, 64, 8, 1], 31)
+
+
+@pytest.mark.parametrize("kv_f16", [False, True])
+def test_q4_k_m_prompt_chunks_on_the_gemm(rq, gpu, kv_f16):
+    """The Q4_K_M mix above with a 56-row prompt chunk: its Q4_K
+    matrices take the tile GEMM (layer 1: one q/k/v GEMM with the RMSNorm in
+    its x prep and RoPE after it, o and down adding into the residual rows,
+    gate/up with the SwiGLU folded into down's x prep; layer 0: the q and k
+    parts and gate/up on the GEMM beside Q6_K v and down on the GEMVs), then
+    decode steps and greedy generation, against the oracle."""
+    cfg = tiny_config(output_dtype=14, kv_f16=kv_f16, max_batch=56, max_seq=96)
+    m, ref, _ = build_typed(cfg, q4_k_m_mix(), 2025 + kv_f16)
+    prompt = [int(v) for v in np.random.default_rng(56).integers(0, cfg.vocab, size=56)]
+    check_typed_model(m, ref, prompt, 31, steps=2)
+
+
+def test_wide_q4_k_prompt_on_the_gemm(rq, gpu):
+    """A 24-row prompt chunk over dim 4352 / ffn 4608 Q4_K layers: the tile
+    GEMM at 17 super-blocks a row (chunks not dividing them)."""
+    import rdlquant.llama as L
+    t = {(slot, 0): 12 for slot in (L.WQ, L.WK, L.WV, L.WO, L.W_GATE, L.W_UP, L.W_DOWN)}
+    t[(L.OUTPUT, 0)] = 12
+    cfg = tiny_config(dim=4352, n_layers=1, n_heads=34, n_kv_heads=2, head_dim=128, ffn_dim=4608, vocab=256,
+                      max_seq=32, max_batch=24, output_dtype=12)
+    m, ref, _ = build_typed(cfg, t, 4353)
+    prompt = [int(v) for v in np.random.default_rng(24).integers(0, cfg.vocab, size=24)]
+    check_typed_model(m, ref, prompt, 7, steps=1)
 
 
 def test_q6_k_combined_layers(rq, gpu):
