@@ -172,17 +172,17 @@ bool use_fused(WType t, size_t m, size_t n, size_t k, const float* x_dev) {
 
 // How a product runs: one fused GEMV launch (m <= 4), the matrix-core GEMM
 // (Q4_0, more rows: f16 MFMA in float mode, int8 MFMA in native mode; Q4_K
-// from KQ_GEMM_MIN_M rows, float mode), or activation records + the records
-// GEMV.
+// and Q6_K from KQ_GEMM_MIN_M rows, float mode), or activation records + the
+// records GEMV.
 enum class Path { Fused, Gemm, Records };
 
-// The GEMM addresses x and W with 32-bit offsets; Q4_K's x prep holds a row
-// in registers (k <= 16384).
+// The GEMM addresses x and W with 32-bit offsets; the K-quant x prep holds a
+// row in registers (k <= 16384).
 bool gemm_fits(WType t, size_t m, size_t n, size_t k) {
     if (k == 0 || (uint64_t)m * k * 2 > rdl::FUSED_MAX_WEIGHT_BYTES) return false;
-    if (t == WType::Q4_K)
+    if (t == WType::Q4_K || t == WType::Q6_K)
         return m >= rdl::KQ_GEMM_MIN_M && k % rdl::QK_K == 0 && k <= 16384 &&
-               (uint64_t)n * (k / rdl::QK_K) * rdl::Q4_K_BYTES <= rdl::FUSED_MAX_WEIGHT_BYTES;
+               (uint64_t)n * (k / rdl::QK_K) * rdl::block_bytes(t) <= rdl::FUSED_MAX_WEIGHT_BYTES;
     return t == WType::Q4_0 && (uint64_t)n * (k / rdl::QK) * rdl::Q4_0_BYTES <= rdl::FUSED_MAX_WEIGHT_BYTES;
 }
 
@@ -196,7 +196,7 @@ size_t scratch_bytes(WType t, Path p, bool native, size_t m, size_t n, size_t k)
     switch (p) {
         case Path::Fused: return 0;
         case Path::Gemm:
-            return t == WType::Q4_K ? rdl::gemm_q4_k_scratch_bytes(m, k) : rdl::gemm_scratch_bytes(m, n, k, native);
+            return t == WType::Q4_0 ? rdl::gemm_scratch_bytes(m, n, k, native) : rdl::gemm_tiles_scratch_bytes(m, k);
         case Path::Records: return rec_bytes(native, m, k);
     }
     return 0;
@@ -218,8 +218,8 @@ rdl_status run_linear(WType t, bool native, const uint8_t* w_dev, size_t n, size
         return RDL_OK;
     }
     if (path == Path::Gemm) {
-        if (t == WType::Q4_K)
-            HIP_TRY(rdl::launch_gemm_q4_k(w_dev, n, k, x_dev, m, y_dev, work, s));
+        if (t == WType::Q4_K || t == WType::Q6_K)
+            HIP_TRY(rdl::launch_gemm_kquant(t, w_dev, n, k, x_dev, m, y_dev, work, s));
         else if (native)
             HIP_TRY(rdl::launch_gemm_q4_0_native(w_dev, n, k, x_dev, m, y_dev, nullptr, work, s));
         else

@@ -258,10 +258,12 @@ template <int CB> struct Lds {
     static constexpr int XC_STRIDE = CB * 32 + 16;  // bytes per x row (int8 codes)
 };
 
-// 8 nibbles (two dwords of four) of a weight row as (q - 8): exact f16 values
-// for the float product, signed bytes for the native one.
+// 8 codes (two dwords of four bytes, each < 64) of a weight row as (q - Z),
+// Z = 8 for nibbles, 32 for Q6_K's 6-bit codes: exact f16 values for the
+// float product; signed bytes (q - 8) for the native one.
+template <int Z = 8>
 __device__ __forceinline__ half8_t q_f16(uint32_t n0, uint32_t n1) {
-    const half2_t off = {(_Float16)1032.0f, (_Float16)1032.0f};
+    const half2_t off = {(_Float16)(1024.0f + Z), (_Float16)(1024.0f + Z)};
     constexpr uint32_t MAGIC = 0x64646464u;  // f16 0x64XX = 1024 + XX for XX < 16
     const half2_t q0 = __builtin_bit_cast(half2_t, perm(MAGIC, n0, 0x04010400u)) - off;
     const half2_t q1 = __builtin_bit_cast(half2_t, perm(MAGIC, n0, 0x04030402u)) - off;
@@ -276,9 +278,11 @@ __device__ __forceinline__ long q_i8(uint32_t n0, uint32_t n1) {
     return (long)(((uint64_t)b << 32) | a);
 }
 
-// Weight formats of the LDS GEMM: GGUF Q4_0 blocks, or Q4_K super-blocks
-// taken as 32-element sub-blocks (value (d sc) q - dmin mn, parser.rs:549-593).
-constexpr int WF_Q4_0 = 0, WF_Q4_K = 1;
+// Weight formats of the LDS GEMM: GGUF Q4_0 blocks, Q4_K super-blocks taken
+// as 32-element sub-blocks (value (d sc) q - dmin mn, parser.rs:549-593), or
+// Q6_K super-blocks taken as 32-element groups of two 16-element sub-blocks
+// (value (d sc) (q - 32), parser.rs:510-547).
+constexpr int WF_Q4_0 = 0, WF_Q4_K = 1, WF_Q6_K = 2;
 
 template <bool NATIVE, int WF, int FJ, int FI, int WJ, int WI, int KS, int KB>
 struct GemmCfg {
@@ -288,9 +292,12 @@ struct GemmCfg {
     static constexpr int TJ = WJ * FJ * 16;
     static constexpr int TI = WI * FI * 16;
     static constexpr int CB = KB * KS;                      // blocks per chunk
-    static constexpr int WN_BYTES = TJ * Lds<CB>::WN_STRIDE;
-    // Q4_0: the f16 d of each (row, block); Q4_K: f32 pairs {d sc, 8 d sc - dmin mn}
-    static constexpr int WD_BYTES = WF == WF_Q4_K ? TJ * CB * 8 : (TJ * CB * 2 + 15) & ~15;
+    // weight rows: 16 nibble bytes a block (Q6_K: 32 6-bit codes as bytes), padded
+    static constexpr int WNS = WF == WF_Q6_K ? CB * 32 + 8 : Lds<CB>::WN_STRIDE;
+    static constexpr int WN_BYTES = TJ * WNS;
+    // Q4_0: the f16 d of each (row, block); Q4_K: f32 pairs {d sc, 8 d sc - dmin mn};
+    // Q6_K: f32 pairs {d sc0, d sc1} of the block's two sub-blocks
+    static constexpr int WD_BYTES = WF != WF_Q4_0 ? TJ * CB * 8 : (TJ * CB * 2 + 15) & ~15;
     // float: x_hi and x_lo tiles (Q4_K: and the x block sums); native: int8
     // codes and the f32 block scales
     static constexpr int X_BYTES = TI * (NATIVE ? Lds<CB>::XC_STRIDE : Lds<CB>::X_STRIDE);
@@ -299,7 +306,7 @@ struct GemmCfg {
     static constexpr int STAGE = WN_BYTES + WD_BYTES + (NATIVE ? X_BYTES : 2 * X_BYTES) + XS_BYTES;
     static constexpr int STAGE_AL = (STAGE + 15) & ~15;
     static constexpr int WBLK = (TJ * CB + NT - 1) / NT;                          // weight blocks per thread
-    static constexpr int WWORDS = WF == WF_Q4_K ? 12 : 5;  // dwords a weight block's loads bring
+    static constexpr int WWORDS = WF == WF_Q6_K ? 20 : WF == WF_Q4_K ? 12 : 5;  // dwords a weight block's loads bring
     static constexpr int XU = (TI * CB * (NATIVE ? 2 : 4) + NT - 1) / NT;          // 16-byte x units per thread
     static constexpr int XSU = XSUMS ? (TI * CB + NT - 1) / NT : 0;              // scale / sum dwords per thread
     static constexpr int RED = (KS > 1) ? (KS - 1) * WJ * WI * FJ * FI * 64 * 16 : 0;
@@ -350,6 +357,11 @@ __device__ __forceinline__ void q4k_sub_scale_min(uint32_t s03, uint32_t s47, ui
 // sub-block ([m, nb] f32).  A sub-block's nibbles are staged as a Q4_0
 // block's, so the MFMAs give sum (q - 8) x'; with D = d sc and M = dmin mn
 // the sub-block adds D sum (q - 8) x' + (8 D - M) sum x' = sum (D q - M) x'.
+// WF = WF_Q6_K (float mode): W holds Q6_K super-blocks, nb counts their
+// 32-element groups; a group's codes are staged as bytes, its two 16-element
+// sub-blocks' scales D0 = d sc0, D1 = d sc1 in f32, and the MFMAs run once
+// with the lanes of elements 16..31 zeroed and once with those of 0..15:
+// the group adds D0 sum_0 (q - 32) x' + D1 sum_1 (q - 32) x'.
 template <bool NATIVE, bool DUMP, int WF, int FJ, int FI, int WJ, int WI, int KS, int KB>
 __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_kernel(
     const uint8_t* __restrict__ W, int n, int nb, const void* __restrict__ X0, const void* __restrict__ X1,
@@ -357,6 +369,7 @@ __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_kernel(
     const float* __restrict__ XS) {
     using C = GemmCfg<NATIVE, WF, FJ, FI, WJ, WI, KS, KB>;
     constexpr bool QK = WF == WF_Q4_K;
+    constexpr bool Q6 = WF == WF_Q6_K;
     constexpr int CB = C::CB;
     constexpr int XSTR = NATIVE ? Lds<CB>::XC_STRIDE : Lds<CB>::X_STRIDE;
     using S = Staged<C::WBLK, C::WWORDS, C::XU, C::XSU>;
@@ -371,8 +384,9 @@ __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_kernel(
     const int j0 = bx * C::TJ;
     const int i0 = by * C::TI;
     const int k = nb * 32;
-    // Q4_K: 144-byte super-blocks of 8 sub-blocks (nb % 8 == 0), rows 16-byte aligned
-    const uint32_t row_bytes = QK ? (uint32_t)(nb / 8) * 144u : (uint32_t)nb * 18u;
+    // Q4_K: 144-byte super-blocks of 8 sub-blocks (nb % 8 == 0), rows 16-byte
+    // aligned; Q6_K: 210-byte super-blocks of 8 groups, 2-byte aligned
+    const uint32_t row_bytes = QK ? (uint32_t)(nb / 8) * 144u : Q6 ? (uint32_t)(nb / 8) * 210u : (uint32_t)nb * 18u;
     const uint32_t wbytes = (uint32_t)n * row_bytes;
     const __amdgpu_buffer_rsrc_t wrs = make_rsrc(W, wbytes);
     const uint32_t xbytes = (uint32_t)m * (uint32_t)k * (NATIVE ? 1u : 2u);
@@ -403,6 +417,37 @@ __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_kernel(
                 r.w[u][0] = h.x; r.w[u][1] = h.y; r.w[u][2] = h.z; r.w[u][3] = h.w;
                 r.w[u][4] = q0.x; r.w[u][5] = q0.y; r.w[u][6] = q0.z; r.w[u][7] = q0.w;
                 r.w[u][8] = q1.x; r.w[u][9] = q1.y; r.w[u][10] = q1.z; r.w[u][11] = q1.w;
+                continue;
+            }
+            if constexpr (Q6) {
+                // group b: half hh = (b / 4) % 2, t = b % 4 of super-block b / 8:
+                // the 32 ql bytes whose low (t < 2) or high nibbles it takes, the
+                // 32 qh bytes holding its 2-bit highs, its two scale bytes and d.
+                // The super-block starts on a dword or 2 bytes past one: 36-byte
+                // windows from the dword below, realigned when stored.
+                const bool ok = live && idx < C::TJ * CB && j < n && b < nb;
+                const uint32_t base = (uint32_t)j * row_bytes + (uint32_t)(b >> 3) * 210u;
+                const uint32_t al = base & ~3u, hh = (uint32_t)(b >> 2) & 1u, t = (uint32_t)b & 3u;
+                const uint32_t qlo = al + 64u * hh + 32u * (t & 1u), qho = al + 128u + 32u * hh;
+                const uint32_t sco = (base + 192u + 8u * hh + 2u * t) & ~3u;
+                // d's dword; the matrix's last super-block, starting on a dword,
+                // ends 2 bytes into it: read 2 bytes early (the high half is d)
+                const uint32_t dof0 = (base + 208u) & ~3u;
+                const uint32_t dof = dof0 + 4u > wbytes ? wbytes - 4u : dof0;
+                const u32x4 l0 = buf_load_b128(wrs, ok ? qlo : RSRC_OOB);
+                const u32x4 l1 = buf_load_b128(wrs, ok ? qlo + 16u : RSRC_OOB);
+                const uint32_t l2 = buf_load_b32(wrs, ok ? qlo + 32u : RSRC_OOB);
+                const u32x4 h0 = buf_load_b128(wrs, ok ? qho : RSRC_OOB);
+                const u32x4 h1 = buf_load_b128(wrs, ok ? qho + 16u : RSRC_OOB);
+                const uint32_t h2 = buf_load_b32(wrs, ok ? qho + 32u : RSRC_OOB);
+                r.w[u][0] = l0.x; r.w[u][1] = l0.y; r.w[u][2] = l0.z; r.w[u][3] = l0.w;
+                r.w[u][4] = l1.x; r.w[u][5] = l1.y; r.w[u][6] = l1.z; r.w[u][7] = l1.w;
+                r.w[u][8] = l2;
+                r.w[u][9] = h0.x; r.w[u][10] = h0.y; r.w[u][11] = h0.z; r.w[u][12] = h0.w;
+                r.w[u][13] = h1.x; r.w[u][14] = h1.y; r.w[u][15] = h1.z; r.w[u][16] = h1.w;
+                r.w[u][17] = h2;
+                r.w[u][18] = buf_load_b32(wrs, ok ? sco : RSRC_OOB);
+                r.w[u][19] = buf_load_b32(wrs, ok ? dof : RSRC_OOB);
                 continue;
             }
             const uint32_t off = (live && idx < C::TJ * CB && j < n && b < nb)
@@ -475,6 +520,35 @@ __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_kernel(
                 float* wdf = reinterpret_cast<float*>(st + C::WN_BYTES);
                 wdf[bl * C::TJ + jl] = dd;
                 wdf[(CB + bl) * C::TJ + jl] = 8.0f * dd - mm;
+            } else if constexpr (Q6) {
+                if (idx >= C::TJ * CB) continue;
+                const int jl = idx / CB, bl = idx % CB;
+                const int j = j0 + jl, b = c * CB + bl;
+                const uint32_t base = (uint32_t)j * row_bytes + (uint32_t)(b >> 3) * 210u;
+                const uint32_t hh = (uint32_t)(b >> 2) & 1u, t = (uint32_t)b & 3u;
+                const bool mis = (base & 2u) != 0;
+                // codes q = (ql nibble) | (qh 2 bits) << 4, element l in byte l
+                const uint32_t sh = 4u * (t >> 1), hs = 2u * t;
+                uint32_t q[8];
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const uint32_t lo = mis ? perm(r.w[u][i + 1], r.w[u][i], 0x05040302u) : r.w[u][i];
+                    const uint32_t hi = mis ? perm(r.w[u][i + 10], r.w[u][i + 9], 0x05040302u) : r.w[u][i + 9];
+                    q[i] = ((lo >> sh) & 0x0F0F0F0Fu) | (((hi >> hs) & 0x03030303u) << 4);
+                }
+                uint2* dst = reinterpret_cast<uint2*>(wn + jl * C::WNS + bl * 32);
+#pragma unroll
+                for (int i = 0; i < 4; i++) dst[i] = uint2{q[2 * i], q[2 * i + 1]};
+                // scales sc[8 hh + 2 t], sc[8 hh + 2 t + 1] (int8) and d; rows or
+                // groups past the matrix loaded zeros: D0 = D1 = 0
+                const uint32_t scw = r.w[u][18] >> (8u * ((base + 192u + 8u * hh + 2u * t) & 3u));
+                const uint32_t dof0 = (base + 208u) & ~3u;
+                const uint32_t dbits = dof0 + 4u > wbytes ? (r.w[u][19] >> 16)
+                                                          : (r.w[u][19] >> (8u * ((base + 208u) & 3u))) & 0xFFFFu;
+                const float d = h2f(dbits);
+                float* wdf = reinterpret_cast<float*>(st + C::WN_BYTES);
+                wdf[bl * C::TJ + jl] = d * (float)(int8_t)(scw & 0xFFu);
+                wdf[(CB + bl) * C::TJ + jl] = d * (float)(int8_t)((scw >> 8) & 0xFFu);
             } else if (idx < C::TJ * CB) {
                 const int jl = idx / CB, bl = idx % CB;
                 const int j = j0 + jl, b = c * CB + bl;
@@ -542,17 +616,27 @@ __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_kernel(
         for (int kb = 0; kb < KB; kb++) {
             const int bl = ks * KB + kb;  // this wave's block within the chunk
             typename std::conditional<NATIVE, long, half8_t>::type aq[FJ];
+            half8_t a1[Q6 ? FJ : 1];
             f32x4 dv[FJ], ev[FJ];
 #pragma unroll
             for (int a = 0; a < FJ; a++) {
                 const int jt = (wj * FJ + a) * 16;
-                const uint2 nb8 = *reinterpret_cast<const uint2*>(wn + (jt + r16) * Lds<CB>::WN_STRIDE +
-                                                                  bl * 16 + 8 * (g & 1));
-                const uint32_t sh = (g >> 1) * 4;  // groups 2, 3: high nibbles
-                const uint32_t n0 = (nb8.x >> sh) & 0x0F0F0F0Fu, n1 = (nb8.y >> sh) & 0x0F0F0F0Fu;
-                if constexpr (NATIVE) aq[a] = q_i8(n0, n1);
-                else aq[a] = q_f16(n0, n1);
-                if constexpr (QK) {
+                if constexpr (Q6) {
+                    // lane group g: codes of elements 8 g .. 8 g + 7; aq keeps those
+                    // of sub-block 0 (g < 2), a1 those of sub-block 1
+                    const uint2 c8 = *reinterpret_cast<const uint2*>(wn + (jt + r16) * C::WNS + bl * 32 + 8 * g);
+                    const half8_t q = q_f16<32>(c8.x, c8.y);
+                    const half8_t zero = {};
+                    aq[a] = g < 2 ? q : zero;
+                    a1[a] = g < 2 ? zero : q;
+                } else {
+                    const uint2 nb8 = *reinterpret_cast<const uint2*>(wn + (jt + r16) * C::WNS + bl * 16 + 8 * (g & 1));
+                    const uint32_t sh = (g >> 1) * 4;  // groups 2, 3: high nibbles
+                    const uint32_t n0 = (nb8.x >> sh) & 0x0F0F0F0Fu, n1 = (nb8.y >> sh) & 0x0F0F0F0Fu;
+                    if constexpr (NATIVE) aq[a] = q_i8(n0, n1);
+                    else aq[a] = q_f16(n0, n1);
+                }
+                if constexpr (QK || Q6) {
                     dv[a] = *reinterpret_cast<const f32x4*>(wdf + bl * C::TJ + jt + 4 * g);
                     ev[a] = *reinterpret_cast<const f32x4*>(wdf + (CB + bl) * C::TJ + jt + 4 * g);
                 } else {
@@ -600,6 +684,13 @@ __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_kernel(
 #pragma unroll
                             for (int u = 0; u < 4; u++)
                                 acc[a][b][u] = fmaf(dv[a][u], t[u], fmaf(ev[a][u], sx, acc[a][b][u]));
+                        } else if constexpr (Q6) {
+                            // t: elements 16..31 zeroed (sub-block 0); t1: 0..15 zeroed
+                            f32x4 t1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1[a], bh, z, 0, 0, 0);
+                            t1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1[a], bl8, t1, 0, 0, 0);
+#pragma unroll
+                            for (int u = 0; u < 4; u++)
+                                acc[a][b][u] = fmaf(dv[a][u], t[u], fmaf(ev[a][u], t1[u], acc[a][b][u]));
                         } else {
 #pragma unroll
                             for (int u = 0; u < 4; u++) acc[a][b][u] = fmaf(dv[a][u], t[u], acc[a][b][u]);
@@ -1511,46 +1602,57 @@ hipError_t launch_cfg(const uint8_t* w, int n, int nb, const void* x0, const voi
 // re-reads of x and W from L2).  M >= 256: swept on MI355X at M = 512 and
 // 2048 over tile shapes, waves and chunk sizes, per mode (the native kernel
 // stages half the x bytes and keeps fewer registers).
-// WF_Q4_K: the float shapes; xs the x' block sums.
+// WF_Q4_K: the float shapes; xs the x' block sums.  WF_Q6_K: shapes of at
+// most 64 x 64 (its staged codes, scale pairs and masked operands hold more
+// registers: the larger tiles spill).
 template <bool NATIVE, bool DUMP, int WF = WF_Q4_0>
 hipError_t launch_tiles(const uint8_t* w, int n, int nb, const void* x0, const void* x1, const int* xe, int m,
                         float* y, int32_t* p, hipStream_t s, int accy = 0, const float* xs = nullptr) {
     const int cus = device_cu_count();
-    if (NATIVE) {
-        if (m >= 1024) return launch_cfg<NATIVE, DUMP, WF, 2, 2, 2, 2, 2, 2>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
-        if (m >= 256) return launch_cfg<NATIVE, DUMP, WF, 2, 4, 2, 2, 2, 2>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
+    if constexpr (WF == WF_Q6_K) {
+        const size_t t64 = (size_t)((n + 63) / 64) * ((m + 63) / 64);
+        if (m >= 48 && t64 >= (size_t)cus)
+            return launch_cfg<NATIVE, DUMP, WF, 2, 2, 2, 2, 2, 2>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
+        if (m >= 48) return launch_cfg<NATIVE, DUMP, WF, 1, 2, 2, 2, 2, 2>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
+        if (m > 16) return launch_cfg<NATIVE, DUMP, WF, 1, 2, 1, 1, 4, 2>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
+        return launch_cfg<NATIVE, DUMP, WF, 1, 1, 1, 1, 4, 4>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
     } else {
-        if (m >= 1024) return launch_cfg<NATIVE, DUMP, WF, 4, 4, 2, 2, 2, 1>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
-        // 128 x 128 tiles from m = 128 where they fill three quarters of
-        // the CUs (the 7B prefill's 28672-row gate/up GEMM at 128 rows: 224
-        // tiles, 110 us against 119 us in 128 x 64 tiles); 128 x 64 tiles from
-        // m = 256, and from m = 128 where they alone fill the CUs (prefill
-        // 15.7 -> 12.3 ms; taken for every matrix: 14.9 ms)
-        if (m >= 128 && m < 256 && 4 * (size_t)((n + 127) / 128) * ((m + 127) / 128) >= 3 * (size_t)cus)
-            return launch_cfg<NATIVE, DUMP, WF, 4, 4, 2, 2, 2, 1>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
-        if (m >= 256 || (m >= 128 && (size_t)((n + 127) / 128) * ((m + 63) / 64) >= (size_t)cus))
-            return launch_cfg<NATIVE, DUMP, WF, 4, 2, 2, 2, 2, 2>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
-    }
-    const size_t t32 = (size_t)((n + 31) / 32) * ((m + 63) / 64);  // 32 x 64 tiles
-    if (m >= 48 && t32 >= (size_t)cus) {
-        if constexpr (!NATIVE) {
-            // 8 waves a tile; 64 x 64 tiles when 32-row ones overflow a round
-            // (us at 128 rows, 4096 x 4096 / 4096 x 14336 / 6144 x 4096: 4-wave
-            // 32 x 64 tiles 37.2 / 106.5 / 66.0, 8-wave 30.3 / 89.1 / 51.5,
-            // 64 x 64 38.7 / 112.9 / 40.0)
-            if (t32 > (size_t)cus) {
-                // (Q4_K's f32 scale pairs and x' sums: chunks of 4 blocks fit the LDS)
-                if constexpr (WF == WF_Q4_K)
-                    return launch_cfg<NATIVE, DUMP, WF, 2, 4, 2, 1, 4, 1>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
-                else
-                    return launch_cfg<NATIVE, DUMP, WF, 2, 4, 2, 1, 4, 2>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
-            }
-            return launch_cfg<NATIVE, DUMP, WF, 2, 2, 1, 2, 4, 2>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
+        if (NATIVE) {
+            if (m >= 1024) return launch_cfg<NATIVE, DUMP, WF, 2, 2, 2, 2, 2, 2>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
+            if (m >= 256) return launch_cfg<NATIVE, DUMP, WF, 2, 4, 2, 2, 2, 2>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
+        } else {
+            if (m >= 1024) return launch_cfg<NATIVE, DUMP, WF, 4, 4, 2, 2, 2, 1>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
+            // 128 x 128 tiles from m = 128 where they fill three quarters of
+            // the CUs (the 7B prefill's 28672-row gate/up GEMM at 128 rows: 224
+            // tiles, 110 us against 119 us in 128 x 64 tiles); 128 x 64 tiles from
+            // m = 256, and from m = 128 where they alone fill the CUs (prefill
+            // 15.7 -> 12.3 ms; taken for every matrix: 14.9 ms)
+            if (m >= 128 && m < 256 && 4 * (size_t)((n + 127) / 128) * ((m + 127) / 128) >= 3 * (size_t)cus)
+                return launch_cfg<NATIVE, DUMP, WF, 4, 4, 2, 2, 2, 1>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
+            if (m >= 256 || (m >= 128 && (size_t)((n + 127) / 128) * ((m + 63) / 64) >= (size_t)cus))
+                return launch_cfg<NATIVE, DUMP, WF, 4, 2, 2, 2, 2, 2>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
         }
-        return launch_cfg<NATIVE, DUMP, WF, 2, 4, 1, 1, 4, 2>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
+        const size_t t32 = (size_t)((n + 31) / 32) * ((m + 63) / 64);  // 32 x 64 tiles
+        if (m >= 48 && t32 >= (size_t)cus) {
+            if constexpr (!NATIVE) {
+                // 8 waves a tile; 64 x 64 tiles when 32-row ones overflow a round
+                // (us at 128 rows, 4096 x 4096 / 4096 x 14336 / 6144 x 4096: 4-wave
+                // 32 x 64 tiles 37.2 / 106.5 / 66.0, 8-wave 30.3 / 89.1 / 51.5,
+                // 64 x 64 38.7 / 112.9 / 40.0)
+                if (t32 > (size_t)cus) {
+                    // (Q4_K's f32 scale pairs and x' sums: chunks of 4 blocks fit the LDS)
+                    if constexpr (WF == WF_Q4_K)
+                        return launch_cfg<NATIVE, DUMP, WF, 2, 4, 2, 1, 4, 1>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
+                    else
+                        return launch_cfg<NATIVE, DUMP, WF, 2, 4, 2, 1, 4, 2>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
+                }
+                return launch_cfg<NATIVE, DUMP, WF, 2, 2, 1, 2, 4, 2>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
+            }
+            return launch_cfg<NATIVE, DUMP, WF, 2, 4, 1, 1, 4, 2>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
+        }
+        if (m > 16) return launch_cfg<NATIVE, DUMP, WF, 1, 2, 1, 1, 4, 2>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
+        return launch_cfg<NATIVE, DUMP, WF, 1, 1, 1, 1, 4, 8>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
     }
-    if (m > 16) return launch_cfg<NATIVE, DUMP, WF, 1, 2, 1, 1, 4, 2>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
-    return launch_cfg<NATIVE, DUMP, WF, 1, 1, 1, 1, 4, 8>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
 }
 
 }  // namespace
@@ -1597,7 +1699,7 @@ size_t gemm_scratch_bytes(size_t m, size_t n, size_t k, bool native) {
     return 2 * xb + ((m * 4 + 255) & ~(size_t)255);
 }
 
-size_t gemm_q4_k_scratch_bytes(size_t m, size_t k) {
+size_t gemm_tiles_scratch_bytes(size_t m, size_t k) {
     // the float layout (x_hi, x_lo, exponents) and the x' sums of each 32-element block
     const size_t xb = (m * k * 2 + 255) & ~(size_t)255;
     return 2 * xb + ((m * 4 + 255) & ~(size_t)255) + ((m * (k / QK) * 4 + 255) & ~(size_t)255);
@@ -1632,16 +1734,16 @@ hipError_t launch_gemm_q4_0(const uint8_t* w, size_t n, size_t k, const float* x
 hipError_t launch_gemm_tiles_ex(WType t, const uint8_t* w, size_t n, size_t k, const float* x, size_t m, float* y,
                                 void* scratch, int pro, const float* g, float eps, bool accumulate, hipStream_t s) {
     if (n == 0 || m == 0) return hipSuccess;
-    const bool q4k = t == WType::Q4_K;
-    if ((t != WType::Q4_0 && !q4k) || k == 0 || k % (q4k ? QK_K : QK) != 0 || (pro < 0 || pro > 2) ||
+    const bool q4k = t == WType::Q4_K, kq = q4k || t == WType::Q6_K;
+    if ((t != WType::Q4_0 && !kq) || k == 0 || k % (kq ? QK_K : QK) != 0 || (pro < 0 || pro > 2) ||
         (pro == 1 && !g))
         return hipErrorInvalidValue;
     // Q4_0's m <= GEMM_XTILE_M rows belong to the x-tile kernel; the x' block
     // sums and the prologues come from the one-read x prep (k <= 16384)
-    if ((!q4k && m <= GEMM_XTILE_M) || ((q4k || pro != 0) && k > (size_t)16 * XPREP_FAST_THREADS))
+    if ((!kq && m <= GEMM_XTILE_M) || ((kq || pro != 0) && k > (size_t)16 * XPREP_FAST_THREADS))
         return hipErrorInvalidValue;
     // 32-bit buffer offsets, out-of-range slots at RSRC_OOB
-    const size_t wb = n * (k / (q4k ? QK_K : QK)) * (q4k ? Q4_K_BYTES : Q4_0_BYTES);
+    const size_t wb = n * (k / block_elems(t)) * block_bytes(t);
     if (wb > FUSED_MAX_WEIGHT_BYTES || m * k * 2 > FUSED_MAX_WEIGHT_BYTES) return hipErrorInvalidValue;
     const size_t xb = (m * k * 2 + 255) & ~(size_t)255;
     _Float16* xh = reinterpret_cast<_Float16*>(scratch);
@@ -1667,12 +1769,15 @@ hipError_t launch_gemm_tiles_ex(WType t, const uint8_t* w, size_t n, size_t k, c
     if (q4k)
         return launch_tiles<false, false, WF_Q4_K>(w, (int)n, (int)(k / QK), xh, xl, xe, (int)m, y, nullptr, s, accy,
                                                    xs);
+    if (kq)
+        return launch_tiles<false, false, WF_Q6_K>(w, (int)n, (int)(k / QK), xh, xl, xe, (int)m, y, nullptr, s, accy);
     return launch_tiles<false, false>(w, (int)n, (int)(k / QK), xh, xl, xe, (int)m, y, nullptr, s, accy);
 }
 
-hipError_t launch_gemm_q4_k(const uint8_t* w, size_t n, size_t k, const float* x, size_t m, float* y,
-                            void* scratch, hipStream_t s) {
-    return launch_gemm_tiles_ex(WType::Q4_K, w, n, k, x, m, y, scratch, 0, nullptr, 0.0f, false, s);
+hipError_t launch_gemm_kquant(WType t, const uint8_t* w, size_t n, size_t k, const float* x, size_t m, float* y,
+                              void* scratch, hipStream_t s) {
+    if (t != WType::Q4_K && t != WType::Q6_K) return hipErrorInvalidValue;
+    return launch_gemm_tiles_ex(t, w, n, k, x, m, y, scratch, 0, nullptr, 0.0f, false, s);
 }
 
 hipError_t launch_gemm_q4_0_native(const uint8_t* w, size_t n, size_t k, const float* x, size_t m, float* y,

@@ -695,7 +695,7 @@ struct LlamaModel {
             return native ? launch_gemm_q4_0_native(w.dev, w.n, w.k, xin, m, y, nullptr, gemm_scratch, stream)
                           : launch_gemm_q4_0(w.dev, w.n, w.k, xin, m, y, gemm_scratch, gemm_cnt, stream);
         if (kgemm(w, m)) {
-            const hipError_t e = launch_gemm_q4_k(w.dev, w.n, w.k, xin, m, y, gemm_scratch, stream);
+            const hipError_t e = launch_gemm_kquant(w.type, w.dev, w.n, w.k, xin, m, y, gemm_scratch, stream);
             if (e != hipErrorInvalidValue) return e;
         }
         // rows four at a time through the fused GEMV (other types, or scales
@@ -861,9 +861,9 @@ struct LlamaModel {
     }
 
     static bool kquant(const Mat& w) { return w.type == WType::Q4_K || w.type == WType::Q6_K; }
-    // Q4_K products of m >= KQ_GEMM_MIN_M rows run on the LDS tile GEMM
+    // Q4_K / Q6_K products of m >= KQ_GEMM_MIN_M rows run on the LDS tile GEMM
     static bool kgemm(const Mat& w, size_t m) {
-        return w.type == WType::Q4_K && m >= KQ_GEMM_MIN_M && w.k % QK_K == 0 && w.k <= 16384;
+        return kquant(w) && m >= KQ_GEMM_MIN_M && w.k % QK_K == 0 && w.k <= 16384;
     }
     // the K-quant GEMVs with the decoder's steps folded into their launches
     static bool kfold(const Mat& w, size_t m) { return kquant(w) && !kgemm(w, m); }
@@ -882,7 +882,7 @@ struct LlamaModel {
     }
 
     // One layer of any resident types, any row count (m > 4 Q4_0 rows and
-    // m >= KQ_GEMM_MIN_M Q4_K rows take the GEMMs).  Q4_K / Q6_K matrices on
+    // m >= KQ_GEMM_MIN_M Q4_K / Q6_K rows take the GEMMs).  Q4_K / Q6_K matrices on
     // the GEMVs fold the RMSNorm in front of them, the residual add after o /
     // down, the SwiGLU of combined gate/up rows and the RoPE + cache write of
     // combined q/k/v rows into their GEMV launches; the other types run
@@ -899,7 +899,7 @@ struct LlamaModel {
         if (L.split_qkv) parts[0] = &L.q, parts[1] = &L.k, parts[2] = &L.v;
         const int cols[3] = {0, q_dim, q_dim + kv_dim};
         const int np = L.split_qkv ? 3 : 1;
-        // Q4_0 (m > GEMM_XTILE_M) and Q4_K prompt chunks on the LDS tile GEMM
+        // Q4_0 (m > GEMM_XTILE_M) and K-quant prompt chunks on the LDS tile GEMM
         // fold the RMSNorms, the SwiGLU and the residual adds into the GEMMs'
         // x splits and stores (hipErrorInvalidValue: a shape they do not take,
         // nothing launched, the separate launches below run instead)
@@ -1295,8 +1295,8 @@ rdl_status rdl_llama_create_typed(const rdl_llama_config* cfg, const int32_t* ty
         for (size_t mm : {(size_t)1, (size_t)16, (size_t)32, (size_t)48, (size_t)64, mb})
             for (bool nat : {false, true})
                 gsb = std::max(gsb, rdl::gemm_scratch_bytes(std::min(mm, mb), sh[0], sh[1], nat));
-        // Q4_K matrices on the tile GEMM (x' block sums beside the split)
-        gsb = std::max(gsb, rdl::gemm_q4_k_scratch_bytes(mb, sh[1]));
+        // K-quant matrices on the tile GEMM (x' block sums beside the split)
+        gsb = std::max(gsb, rdl::gemm_tiles_scratch_bytes(mb, sh[1]));
     }
     if ((e = M.alloc(&M.gemm_scratch, gsb)) != hipSuccess) return fail_free(e);
     if ((e = M.alloc_t(&M.gemm_cnt, gcc)) != hipSuccess) return fail_free(e);

@@ -430,6 +430,21 @@ def test_q4_k_m_prompt_chunks_on_the_gemm(rq, gpu, kv_f16):
     check_typed_model(m, ref, prompt, 31, steps=2)
 
 
+def test_q6_k_prompt_chunk_on_the_gemm(rq, gpu):
+    """Every layer matrix Q6_K with a 40-row prompt chunk: one q/k/v GEMM with
+    the RMSNorm in its x prep, gate/up with the SwiGLU folded into down's x
+    prep, residual adds in the o / down stores; then decode steps on the Q6_K
+    GEMVs, against the oracle."""
+    import rdlquant.llama as L
+    t = {(slot, layer): 14 for layer in range(2)
+         for slot in (L.WQ, L.WK, L.WV, L.WO, L.W_GATE, L.W_UP, L.W_DOWN)}
+    t[(L.OUTPUT, 0)] = 8
+    cfg = tiny_config(output_dtype=8, max_batch=40, max_seq=64)
+    m, ref, _ = build_typed(cfg, t, 78)
+    prompt = [int(v) for v in np.random.default_rng(40).integers(0, cfg.vocab, size=40)]
+    check_typed_model(m, ref, prompt, 12, steps=2)
+
+
 def test_wide_q4_k_prompt_on_the_gemm(rq, gpu):
     """A 24-row prompt chunk over dim 4352 / ffn 4608 Q4_K layers: the tile
     GEMM at 17 super-blocks a row (chunks not dividing them)."""
