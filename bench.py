@@ -593,7 +593,7 @@ def q4_k_m_types(n_layers):
 
 def decode_q4_k_m_line(rig, reps=2):
     """Not a BASELINE config: the config-5 model shape with llama.cpp's Q4_K_M
-    type mix (Q4_K layers, Q6_K attn_v / ffn_down in 18 of 32 layers, Q4_K
+    type mix (Q4_K layers, Q6_K attn_v / ffn_down in 16 of 32 layers, Q4_K
     embedding, Q6_K output), synthetic weights (one seeded matrix per shape
     and type, repeated over the layers), greedy decode as config 5."""
     import numpy as np

@@ -144,7 +144,9 @@ rdl_status rdl_matmul_f32_q4_1_native(const float* input_data, size_t input_len,
 /* Additive extension (no reference counterpart): Q4_K weights kept resident.
  * The reference dequantizes Q4_K at load (rustml/gguf/main/src/core/parser.rs:321-325,
  * dequantize_q4k :549-593) and runs the F32 Linear path (linear.rs:167-170); this
- * computes the same product straight from the 144-byte super-blocks. */
+ * computes the same product straight from the 144-byte super-blocks: GEMVs
+ * for m < 16 rows, the matrix-core tile GEMM from 16 rows (in_features <=
+ * 16384; longer rows take the GEMV). */
 rdl_status rdl_matmul_f32_q4_k(const float* input_data, size_t input_len,
                                const uint8_t* weight_bytes, size_t weight_len, size_t m,
                                size_t in_features, size_t out_features, float* output,
@@ -152,7 +154,8 @@ rdl_status rdl_matmul_f32_q4_k(const float* input_data, size_t input_len,
 /* Additive extension (no reference counterpart): Q6_K weights kept resident.
  * The reference dequantizes Q6_K at load (parser.rs:321-325, dequantize_q6k
  * :510-547) and runs the F32 Linear path; this computes the same product
- * straight from the 210-byte super-blocks.  in_features % 256 == 0. */
+ * straight from the 210-byte super-blocks (GEMVs below 16 rows, the
+ * matrix-core tile GEMM from 16 rows as for Q4_K).  in_features % 256 == 0. */
 rdl_status rdl_matmul_f32_q6_k(const float* input_data, size_t input_len,
                                const uint8_t* weight_bytes, size_t weight_len, size_t m,
                                size_t in_features, size_t out_features, float* output,

@@ -1,7 +1,7 @@
 """rdl_linear_forward_dev_noalloc (static per-GPU scratch, no device
 allocation) against rdl_linear_forward_dev on the same inputs: two calls in
 a row, the second with fewer rows, for each path that uses scratch memory
-(the prefill GEMM's activation split, native-mode and Q8_0 activation
+(the prefill GEMMs' activation split, native-mode and Q8_0 activation
 records).  Both entry points run the same kernels, so the outputs must be
 bit-identical."""
 import numpy as np
@@ -19,6 +19,8 @@ pytestmark = pytest.mark.gpu
     (2, 1, 4096, 4096, (24, 6)),     # Q4_0 native: Q8_0 records in scratch
     (3, 1, 1000, 2048, (9, 5)),      # Q4_1 native records
     (8, 0, 512, 1024, (33, 7)),      # Q8_0 float records
+    (12, 0, 1024, 4096, (40, 16)),   # Q4_K float: tile GEMM, x split and x' block sums in scratch
+    (14, 0, 1000, 2048, (20, 17)),   # Q6_K float: tile GEMM, x split in scratch
 ])
 def test_noalloc_matches_allocating_entry_point(rq, gpu, dtype, mode, n, k, rows):
     import torch
