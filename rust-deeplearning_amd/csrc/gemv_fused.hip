@@ -1998,12 +1998,15 @@ hipError_t launch_gemv_kquant_ex(WType t, const uint8_t* w, size_t n, size_t k, 
 hipError_t launch_gemv_kquant_rope_kv(WType t, const uint8_t* w, size_t n, size_t k, const float* x, size_t m,
                                       size_t row0, float* y, size_t ystride, const float* g, float eps,
                                       const int* pos, const float* cos_t, const float* sin_t, void* kc, void* vc,
-                                      int n_heads, int n_kv, int hd, const int* kv_table, bool kv_f16, hipStream_t s) {
+                                      int n_heads, int n_kv, int hd, int head0, const int* kv_table, bool kv_f16,
+                                      hipStream_t s) {
     if (n == 0 || m == 0) return hipSuccess;
+    // heads head0 .. head0 + n / hd - 1 of [q | k | v]; q heads only from head0 = 0
     if ((t != WType::Q4_K && t != WType::Q6_K) || k == 0 || k % QK_K || k > fused_max_k(t) || m > 4 ||
         ((uintptr_t)x & 15) || k > INT32_MAX || ystride < n || ystride > INT32_MAX || row0 > INT32_MAX ||
-        g == nullptr || ((uintptr_t)g & 15) || hd <= 0 || (hd & 1) ||
-        n != (size_t)(n_heads + 2 * n_kv) * hd || (uint64_t)n * (k / QK_K) * block_bytes(t) > FUSED_MAX_WEIGHT_BYTES)
+        g == nullptr || ((uintptr_t)g & 15) || hd <= 0 || (hd & 1) || n % (size_t)hd != 0 ||
+        (head0 != 0 && head0 < n_heads) || head0 < 0 || (size_t)head0 + n / hd > (size_t)(n_heads + 2 * n_kv) ||
+        (uint64_t)n * (k / QK_K) * block_bytes(t) > FUSED_MAX_WEIGHT_BYTES)
         return hipErrorInvalidValue;
     KqFuse fz{};
     fz.g = g;
@@ -2021,7 +2024,7 @@ hipError_t launch_gemv_kquant_rope_kv(WType t, const uint8_t* w, size_t n, size_
     fz.hd = hd;
     fz.kv_table = kv_table;
     fz.kv_f16 = kv_f16 ? 1 : 0;
-    fz.head0 = 0;
+    fz.head0 = head0;
     const size_t lds = (size_t)8 * 16 * (k / QK) + 16 * sizeof(float);
     launch_kq<PRO_RMSNORM, EPI_ROPE_KV>(t, w, (int)n, (int)(k / QK_K), x, m, y, s, lds, fz);
     return hipGetLastError();

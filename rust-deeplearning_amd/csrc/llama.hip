@@ -617,10 +617,12 @@ struct LlamaModel {
     };
     struct Layer {
         // q/k/v rows concatenated and gate/up rows interleaved when the parts
-        // share a GGUF type; otherwise the parts stand alone (split_*)
+        // share a GGUF type; otherwise the parts stand alone (split_*), q and
+        // k still concatenated in qk when theirs agree (qk_joint: llama.cpp's
+        // Q4_K_M files give only attn_v another type)
         Mat qkv, o, gu, down;
-        Mat q, k, v, gate, up;
-        bool split_qkv = false, split_gu = false;
+        Mat q, k, v, gate, up, qk;
+        bool split_qkv = false, split_gu = false, qk_joint = false;
         bool fused = false;  // Q4_0 throughout: the fused launches serve m <= 4 rows
         // Linear::use_native_q4 of the layer's Q4_0 / Q4_1 Linears
         // (TransformerBlock::set_native_q4_matmul): activations quantized to
@@ -896,9 +898,16 @@ struct LlamaModel {
         };
         // ---- q, k, v -> qkv rows ----
         const Mat* parts[3] = {&L.qkv, nullptr, nullptr};
-        if (L.split_qkv) parts[0] = &L.q, parts[1] = &L.k, parts[2] = &L.v;
-        const int cols[3] = {0, q_dim, q_dim + kv_dim};
-        const int np = L.split_qkv ? 3 : 1;
+        int cols[3] = {0, q_dim, q_dim + kv_dim};
+        int np = 1;
+        if (L.split_qkv && L.qk_joint) {
+            parts[0] = &L.qk, parts[1] = &L.v;
+            cols[1] = q_dim + kv_dim;
+            np = 2;
+        } else if (L.split_qkv) {
+            parts[0] = &L.q, parts[1] = &L.k, parts[2] = &L.v;
+            np = 3;
+        }
         // Q4_0 (m > GEMM_XTILE_M) and K-quant prompt chunks on the LDS tile GEMM
         // fold the RMSNorms, the SwiGLU and the residual adds into the GEMMs'
         // x splits and stores (hipErrorInvalidValue: a shape they do not take,
@@ -919,15 +928,21 @@ struct LlamaModel {
         bool want_xn = false;
         for (int i = 0; i < np; i++) want_xn |= !kfold_m(*parts[i]);
         if (want_xn && !qkv_done) rmsnorm(L.attn_norm);
-        // a K-quant [Wq; Wk; Wv] also applies RoPE and writes the cache
-        const bool rope_fused = np == 1 && !qkv_done && kfold_m(L.qkv);
+        // a K-quant [Wq; Wk; Wv] (or K-quant [Wq; Wk] and Wv, two launches)
+        // also applies RoPE and writes the cache
+        const bool rope_fused = !qkv_done && ((np == 1 && kfold_m(L.qkv)) ||
+                                              (np == 2 && kfold_m(L.qk) && kfold_m(L.v)));
         for (size_t r = 0; rope_fused && r < m; r += 4) {
             const size_t mr = (m - r < 4) ? m - r : 4;
-            e = launch_gemv_kquant_rope_kv(L.qkv.type, L.qkv.dev, L.qkv.n, d, x + r * d, mr, r, qkv + r * qkv_dim,
-                                           qkv_dim, L.attn_norm, cfg.norm_eps, pos, cos_t, sin_t, kv_layer(kc, l),
-                                           kv_layer(vc, l), cfg.n_heads, cfg.n_kv_heads, cfg.head_dim,
-                                           kv_table, cfg.kv_f16 != 0, stream);
-            if (e != hipSuccess) return e;
+            for (int i = 0; i < np; i++) {
+                const Mat& w = *parts[i];
+                e = launch_gemv_kquant_rope_kv(w.type, w.dev, w.n, d, x + r * d, mr, r, qkv + r * qkv_dim + cols[i],
+                                               qkv_dim, L.attn_norm, cfg.norm_eps, pos, cos_t, sin_t,
+                                               kv_layer(kc, l), kv_layer(vc, l), cfg.n_heads, cfg.n_kv_heads,
+                                               cfg.head_dim, cols[i] / cfg.head_dim, kv_table, cfg.kv_f16 != 0,
+                                               stream);
+                if (e != hipSuccess) return e;
+            }
         }
         for (int i = 0; i < np && !rope_fused && !qkv_done; i++) {
             const Mat& w = *parts[i];
@@ -1114,12 +1129,13 @@ rdl_status slot_target(rdl::LlamaModel& M, int32_t slot, int32_t layer, SlotTarg
         case RDL_LLAMA_FFN_NORM: f32(M.layers[layer].ffn_norm); break;
         case RDL_LLAMA_WQ: {
             auto& L = M.layers[layer];
-            L.split_qkv ? q4(L.q, 0, M.q_dim) : q4(L.qkv, 0, M.q_dim);
+            L.split_qkv ? (L.qk_joint ? q4(L.qk, 0, M.q_dim) : q4(L.q, 0, M.q_dim)) : q4(L.qkv, 0, M.q_dim);
             break;
         }
         case RDL_LLAMA_WK: {
             auto& L = M.layers[layer];
-            L.split_qkv ? q4(L.k, 0, M.kv_dim) : q4(L.qkv, M.q_dim, M.kv_dim);
+            L.split_qkv ? (L.qk_joint ? q4(L.qk, M.q_dim, M.kv_dim) : q4(L.k, 0, M.kv_dim))
+                        : q4(L.qkv, M.q_dim, M.kv_dim);
             break;
         }
         case RDL_LLAMA_WV: {
@@ -1235,7 +1251,11 @@ rdl_status rdl_llama_create_typed(const rdl_llama_config* cfg, const int32_t* ty
         L.split_qkv = tq != tk || tq != tv;
         L.split_gu = tg != tu;
         any_split_qkv |= L.split_qkv;
-        if (L.split_qkv) {
+        L.qk_joint = L.split_qkv && tq == tk;
+        if (L.qk_joint) {
+            if ((e = mat(L.qk, M.q_dim + M.kv_dim, c.dim, tq)) != hipSuccess) return fail_free(e);
+            if ((e = mat(L.v, M.kv_dim, c.dim, tv)) != hipSuccess) return fail_free(e);
+        } else if (L.split_qkv) {
             if ((e = mat(L.q, M.q_dim, c.dim, tq)) != hipSuccess) return fail_free(e);
             if ((e = mat(L.k, M.kv_dim, c.dim, tk)) != hipSuccess) return fail_free(e);
             if ((e = mat(L.v, M.kv_dim, c.dim, tv)) != hipSuccess) return fail_free(e);

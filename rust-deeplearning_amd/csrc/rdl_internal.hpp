@@ -258,12 +258,15 @@ hipError_t launch_qkv_attention(const uint8_t* w, size_t n, size_t k, const floa
                                 int nspan, int spans, int* att_cnt, float* att_out, uint64_t* xch, int* err,
                                 const uint8_t* wo, size_t n_o, float* x_res, uint64_t* oxch, hipStream_t s);
 
-// launch_gemv_q4_0_rope_kv for a Q4_K or Q6_K [Wq; Wk; Wv]: m <= 4 activation
-// rows (k floats apart) at positions *pos + row0 + row, q rows ystride apart.
+// launch_gemv_q4_0_rope_kv for a Q4_K or Q6_K [Wq; Wk; Wv], or for the rows of
+// heads head0 .. head0 + n / hd - 1 of it (head0 = 0, or past the q heads:
+// [Wq; Wk] and Wv as two launches): m <= 4 activation rows (k floats apart)
+// at positions *pos + row0 + row, q rows ystride apart.
 hipError_t launch_gemv_kquant_rope_kv(WType t, const uint8_t* w, size_t n, size_t k, const float* x, size_t m,
                                       size_t row0, float* y, size_t ystride, const float* g, float eps,
                                       const int* pos, const float* cos_t, const float* sin_t, void* kc, void* vc,
-                                      int n_heads, int n_kv, int hd, const int* kv_table, bool kv_f16, hipStream_t s);
+                                      int n_heads, int n_kv, int hd, int head0, const int* kv_table, bool kv_f16,
+                                      hipStream_t s);
 
 // int32 block partials of the Q4_0 x Q8_0 path for one activation row.
 hipError_t launch_q4_0_block_dots(const uint8_t* w, size_t n, size_t k, const NativeRec* rec,
