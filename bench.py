@@ -870,6 +870,7 @@ def main():
             "config4_gemm": gemm_lines(rig, [16, 64, 512, 2048]),
             "config4_gemm_native": gemm_lines(rig, [512, 2048], native=True),
             "config5_decode": decode_line(rig),
+            "decode_q4_k_m": decode_q4_k_m_line(rig),
             "read_ceiling": read_lines(rig, sub_steps, sub_warm),
         }
     if not args.no_cpu:
