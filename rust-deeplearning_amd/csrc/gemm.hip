@@ -1602,17 +1602,21 @@ hipError_t launch_cfg(const uint8_t* w, int n, int nb, const void* x0, const voi
 // re-reads of x and W from L2).  M >= 256: swept on MI355X at M = 512 and
 // 2048 over tile shapes, waves and chunk sizes, per mode (the native kernel
 // stages half the x bytes and keeps fewer registers).
-// WF_Q4_K: the float shapes, 64 x 64 in place of 128-row tiles; xs the x'
-// block sums.  WF_Q6_K: shapes of at most 64 x 64.  (Their staged headers or
-// codes, scale pairs and masked operands hold more registers: the 128-row
-// tiles spill.)
+// WF_Q4_K: the float shapes, 128 x 64 tiles of one block a wave (or 64 x 64)
+// in place of the 128-row ones; xs the x' block sums.  WF_Q6_K: shapes of at
+// most 64 x 64.  (Their staged headers or codes, scale pairs and masked
+// operands hold more registers: the larger tiles spill.)
 template <bool NATIVE, bool DUMP, int WF = WF_Q4_0>
 hipError_t launch_tiles(const uint8_t* w, int n, int nb, const void* x0, const void* x1, const int* xe, int m,
                         float* y, int32_t* p, hipStream_t s, int accy = 0, const float* xs = nullptr) {
     const int cus = device_cu_count();
     if constexpr (WF == WF_Q4_K) {
-        // Q4_0's shapes, with 64 x 64 tiles where it takes 128-row ones
-        // (those spill with Q4_K's staged headers and scale pairs)
+        // Q4_0's shapes, with 128 x 64 tiles of one block a wave a chunk (or
+        // 64 x 64) where it takes its 128-row ones, which spill with Q4_K's
+        // staged headers and scale pairs (7B gate/up at 128 rows: 194 us
+        // spilling, 165 us in 64 x 64 tiles, 136 us in these)
+        if (m >= 128 && (size_t)((n + 127) / 128) * ((m + 63) / 64) >= (size_t)cus)
+            return launch_cfg<NATIVE, DUMP, WF, 4, 2, 2, 2, 2, 1>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
         if (m >= 128 && (size_t)((n + 63) / 64) * ((m + 63) / 64) >= (size_t)cus)
             return launch_cfg<NATIVE, DUMP, WF, 2, 2, 2, 2, 2, 2>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
     }
@@ -1620,9 +1624,11 @@ hipError_t launch_tiles(const uint8_t* w, int n, int nb, const void* x0, const v
         const size_t t64 = (size_t)((n + 63) / 64) * ((m + 63) / 64);
         if (m >= 48 && t64 >= (size_t)cus)
             return launch_cfg<NATIVE, DUMP, WF, 2, 2, 2, 2, 2, 2>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
-        // 32 x 64 tiles of 8 waves where they fill the CUs, else 32 x 16 of 4
+        // 32 x 64 tiles of 8 waves (K split over 4) where they fill the CUs
+        // (7B down at 128 rows: 121 us with K over 2 waves, 113 us), else
+        // 32 x 16 of 4
         if (m >= 48 && (size_t)((n + 31) / 32) * ((m + 63) / 64) >= (size_t)cus)
-            return launch_cfg<NATIVE, DUMP, WF, 1, 2, 2, 2, 2, 2>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
+            return launch_cfg<NATIVE, DUMP, WF, 2, 2, 1, 2, 4, 1>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
         if (m > 16) return launch_cfg<NATIVE, DUMP, WF, 1, 2, 1, 1, 4, 2>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
         return launch_cfg<NATIVE, DUMP, WF, 1, 1, 1, 1, 4, 4>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
     } else {
