@@ -171,24 +171,26 @@ bool use_fused(WType t, size_t m, size_t n, size_t k, const float* x_dev) {
 }
 
 // How a product runs: one fused GEMV launch (m <= 4), the matrix-core GEMM
-// (Q4_0, more rows: f16 MFMA in float mode, int8 MFMA in native mode; Q4_K
-// and Q6_K from KQ_GEMM_MIN_M rows, float mode), or activation records + the
-// records GEMV.
+// (Q4_0, more rows: f16 MFMA in float mode, int8 MFMA in native mode; Q4_K,
+// Q6_K, Q8_0 and float-mode Q4_1 from KQ_GEMM_MIN_M rows), or activation
+// records + the records GEMV.
 enum class Path { Fused, Gemm, Records };
 
-// The GEMM addresses x and W with 32-bit offsets; the K-quant x prep holds a
-// row in registers (k <= 16384).
-bool gemm_fits(WType t, size_t m, size_t n, size_t k) {
+// The GEMM addresses x and W with 32-bit offsets; the x prep of the other
+// types holds a row in registers (k <= 16384).
+bool gemm_fits(WType t, bool native, size_t m, size_t n, size_t k) {
     if (k == 0 || (uint64_t)m * k * 2 > rdl::FUSED_MAX_WEIGHT_BYTES) return false;
-    if (t == WType::Q4_K || t == WType::Q6_K)
-        return m >= rdl::KQ_GEMM_MIN_M && k % rdl::QK_K == 0 && k <= 16384 &&
-               (uint64_t)n * (k / rdl::QK_K) * rdl::block_bytes(t) <= rdl::FUSED_MAX_WEIGHT_BYTES;
+    if (t == WType::Q4_K || t == WType::Q6_K || t == WType::Q8_0 || (t == WType::Q4_1 && !native)) {
+        const size_t be = rdl::block_elems(t);
+        return m >= rdl::KQ_GEMM_MIN_M && k % be == 0 && k <= 16384 &&
+               (uint64_t)n * (k / be) * rdl::block_bytes(t) <= rdl::FUSED_MAX_WEIGHT_BYTES;
+    }
     return t == WType::Q4_0 && (uint64_t)n * (k / rdl::QK) * rdl::Q4_0_BYTES <= rdl::FUSED_MAX_WEIGHT_BYTES;
 }
 
 Path pick_path(WType t, bool native, size_t m, size_t n, size_t k, const float* x_dev) {
     if (use_fused(t, m, n, k, x_dev)) return Path::Fused;
-    if (gemm_fits(t, m, n, k)) return Path::Gemm;
+    if (gemm_fits(t, native, m, n, k)) return Path::Gemm;
     return Path::Records;
 }
 
@@ -218,8 +220,8 @@ rdl_status run_linear(WType t, bool native, const uint8_t* w_dev, size_t n, size
         return RDL_OK;
     }
     if (path == Path::Gemm) {
-        if (t == WType::Q4_K || t == WType::Q6_K)
-            HIP_TRY(rdl::launch_gemm_kquant(t, w_dev, n, k, x_dev, m, y_dev, work, s));
+        if (t != WType::Q4_0)
+            HIP_TRY(rdl::launch_gemm_typed(t, w_dev, n, k, x_dev, m, y_dev, work, s));
         else if (native)
             HIP_TRY(rdl::launch_gemm_q4_0_native(w_dev, n, k, x_dev, m, y_dev, nullptr, work, s));
         else
@@ -529,7 +531,7 @@ rdl_status rdl_q4_0_q8_0_block_dots(const float* x, size_t x_len, const uint8_t*
     HIP_TRY(dp.alloc(m * n * nb * sizeof(int32_t)));
     HIP_TRY(hipMemcpy(dx.p, x, m * k * sizeof(float), hipMemcpyHostToDevice));
     HIP_TRY(hipMemcpy(dw.p, w, n * nb * rdl::Q4_0_BYTES, hipMemcpyHostToDevice));
-    if (m > FUSED_MAX_M && gemm_fits(WType::Q4_0, m, n, k)) {
+    if (m > FUSED_MAX_M && gemm_fits(WType::Q4_0, true, m, n, k)) {
         // the rows matmul_f32_q4_native takes to the int8 GEMM: its own MFMA block dots
         HIP_TRY(dr.alloc(rdl::gemm_scratch_bytes(m, n, k, true)));
         HIP_TRY(rdl::launch_gemm_q4_0_native((const uint8_t*)dw.p, n, k, (const float*)dx.p, m, nullptr,

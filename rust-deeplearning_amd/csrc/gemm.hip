@@ -258,13 +258,14 @@ template <int CB> struct Lds {
     static constexpr int XC_STRIDE = CB * 32 + 16;  // bytes per x row (int8 codes)
 };
 
-// 8 codes (two dwords of four bytes, each < 64) of a weight row as (q - Z),
-// Z = 8 for nibbles, 32 for Q6_K's 6-bit codes: exact f16 values for the
-// float product; signed bytes (q - 8) for the native one.
+// 8 codes (two dwords of four bytes) of a weight row as (q - Z), Z = 8 for
+// nibbles, 32 for Q6_K's 6-bit codes, 128 for Q8_0's codes staged + 128:
+// exact f16 values for the float product; signed bytes (q - 8) for the
+// native one.
 template <int Z = 8>
 __device__ __forceinline__ half8_t q_f16(uint32_t n0, uint32_t n1) {
     const half2_t off = {(_Float16)(1024.0f + Z), (_Float16)(1024.0f + Z)};
-    constexpr uint32_t MAGIC = 0x64646464u;  // f16 0x64XX = 1024 + XX for XX < 16
+    constexpr uint32_t MAGIC = 0x64646464u;  // f16 0x64XX = 1024 + XX (XX a byte)
     const half2_t q0 = __builtin_bit_cast(half2_t, perm(MAGIC, n0, 0x04010400u)) - off;
     const half2_t q1 = __builtin_bit_cast(half2_t, perm(MAGIC, n0, 0x04030402u)) - off;
     const half2_t q2 = __builtin_bit_cast(half2_t, perm(MAGIC, n1, 0x04010400u)) - off;
@@ -279,34 +280,42 @@ __device__ __forceinline__ long q_i8(uint32_t n0, uint32_t n1) {
 }
 
 // Weight formats of the LDS GEMM: GGUF Q4_0 blocks, Q4_K super-blocks taken
-// as 32-element sub-blocks (value (d sc) q - dmin mn, parser.rs:549-593), or
+// as 32-element sub-blocks (value (d sc) q - dmin mn, parser.rs:549-593),
 // Q6_K super-blocks taken as 32-element groups of two 16-element sub-blocks
-// (value (d sc) (q - 32), parser.rs:510-547).
-constexpr int WF_Q4_0 = 0, WF_Q4_K = 1, WF_Q6_K = 2;
+// (value (d sc) (q - 32), parser.rs:510-547), Q8_0 blocks (value d q,
+// tensor.rs:535-639) and Q4_1 blocks (value d q + m, quantize.rs:429-495).
+constexpr int WF_Q4_0 = 0, WF_Q4_K = 1, WF_Q6_K = 2, WF_Q8_0 = 3, WF_Q4_1 = 4;
+// staged as byte codes (32 a block) rather than nibbles; with f32 scale
+// pairs a block rather than one f16 d; with x' block sums
+constexpr bool wf_bytes(int wf) { return wf == WF_Q6_K || wf == WF_Q8_0; }
+constexpr bool wf_pairs(int wf) { return wf == WF_Q4_K || wf == WF_Q6_K || wf == WF_Q4_1; }
+constexpr bool wf_sums(int wf) { return wf == WF_Q4_K || wf == WF_Q4_1; }
 
 template <bool NATIVE, int WF, int FJ, int FI, int WJ, int WI, int KS, int KB>
 struct GemmCfg {
-    static_assert(WF == WF_Q4_0 || !NATIVE, "Q4_K products in float mode only");
+    static_assert(WF == WF_Q4_0 || !NATIVE, "native mode for Q4_0 only");
     static constexpr int NW = WJ * WI * KS;
     static constexpr int NT = NW * 64;
     static constexpr int TJ = WJ * FJ * 16;
     static constexpr int TI = WI * FI * 16;
     static constexpr int CB = KB * KS;                      // blocks per chunk
-    // weight rows: 16 nibble bytes a block (Q6_K: 32 6-bit codes as bytes), padded
-    static constexpr int WNS = WF == WF_Q6_K ? CB * 32 + 8 : Lds<CB>::WN_STRIDE;
+    // weight rows: 16 nibble bytes a block (Q6_K, Q8_0: 32 codes as bytes), padded
+    static constexpr int WNS = wf_bytes(WF) ? CB * 32 + 8 : Lds<CB>::WN_STRIDE;
     static constexpr int WN_BYTES = TJ * WNS;
-    // Q4_0: the f16 d of each (row, block); Q4_K: f32 pairs {d sc, 8 d sc - dmin mn};
-    // Q6_K: f32 pairs {d sc0, d sc1} of the block's two sub-blocks
-    static constexpr int WD_BYTES = WF != WF_Q4_0 ? TJ * CB * 8 : (TJ * CB * 2 + 15) & ~15;
+    // Q4_0, Q8_0: the f16 d of each (row, block); Q4_K: f32 pairs {d sc,
+    // 8 d sc - dmin mn}; Q6_K: {d sc0, d sc1} of the block's two sub-blocks;
+    // Q4_1: {d, 8 d + m}
+    static constexpr int WD_BYTES = wf_pairs(WF) ? TJ * CB * 8 : (TJ * CB * 2 + 15) & ~15;
     // float: x_hi and x_lo tiles (Q4_K: and the x block sums); native: int8
     // codes and the f32 block scales
     static constexpr int X_BYTES = TI * (NATIVE ? Lds<CB>::XC_STRIDE : Lds<CB>::X_STRIDE);
-    static constexpr bool XSUMS = NATIVE || WF == WF_Q4_K;
+    static constexpr bool XSUMS = NATIVE || wf_sums(WF);
     static constexpr int XS_BYTES = XSUMS ? TI * CB * 4 : 0;
     static constexpr int STAGE = WN_BYTES + WD_BYTES + (NATIVE ? X_BYTES : 2 * X_BYTES) + XS_BYTES;
     static constexpr int STAGE_AL = (STAGE + 15) & ~15;
     static constexpr int WBLK = (TJ * CB + NT - 1) / NT;                          // weight blocks per thread
-    static constexpr int WWORDS = WF == WF_Q6_K ? 20 : WF == WF_Q4_K ? 12 : 5;  // dwords a weight block's loads bring
+    // dwords a weight block's loads bring
+    static constexpr int WWORDS = WF == WF_Q6_K ? 20 : WF == WF_Q4_K ? 12 : WF == WF_Q8_0 ? 9 : 5;
     static constexpr int XU = (TI * CB * (NATIVE ? 2 : 4) + NT - 1) / NT;          // 16-byte x units per thread
     static constexpr int XSU = XSUMS ? (TI * CB + NT - 1) / NT : 0;              // scale / sum dwords per thread
     static constexpr int RED = (KS > 1) ? (KS - 1) * WJ * WI * FJ * FI * 64 * 16 : 0;
@@ -362,6 +371,11 @@ __device__ __forceinline__ void q4k_sub_scale_min(uint32_t s03, uint32_t s47, ui
 // sub-blocks' scales D0 = d sc0, D1 = d sc1 in f32, and the MFMAs run once
 // with the lanes of elements 16..31 zeroed and once with those of 0..15:
 // the group adds D0 sum_0 (q - 32) x' + D1 sum_1 (q - 32) x'.
+// WF = WF_Q8_0 (float mode): 34-byte blocks, 2-byte aligned; the int8 codes
+// are staged as bytes + 128 and the f16 operand (b - 128) = q is exact; the
+// block adds d sum q x'.
+// WF = WF_Q4_1 (float mode): 20-byte blocks; nibbles staged as Q4_0's, and as
+// for Q4_K the block adds d sum (q - 8) x' + (8 d + m) sum x'.
 template <bool NATIVE, bool DUMP, int WF, int FJ, int FI, int WJ, int WI, int KS, int KB>
 __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_kernel(
     const uint8_t* __restrict__ W, int n, int nb, const void* __restrict__ X0, const void* __restrict__ X1,
@@ -370,6 +384,9 @@ __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_kernel(
     using C = GemmCfg<NATIVE, WF, FJ, FI, WJ, WI, KS, KB>;
     constexpr bool QK = WF == WF_Q4_K;
     constexpr bool Q6 = WF == WF_Q6_K;
+    constexpr bool Q8 = WF == WF_Q8_0;
+    constexpr bool Q41 = WF == WF_Q4_1;
+    constexpr bool PAIRS = wf_pairs(WF), SUMS = wf_sums(WF);
     constexpr int CB = C::CB;
     constexpr int XSTR = NATIVE ? Lds<CB>::XC_STRIDE : Lds<CB>::X_STRIDE;
     using S = Staged<C::WBLK, C::WWORDS, C::XU, C::XSU>;
@@ -386,14 +403,18 @@ __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_kernel(
     const int k = nb * 32;
     // Q4_K: 144-byte super-blocks of 8 sub-blocks (nb % 8 == 0), rows 16-byte
     // aligned; Q6_K: 210-byte super-blocks of 8 groups, 2-byte aligned
-    const uint32_t row_bytes = QK ? (uint32_t)(nb / 8) * 144u : Q6 ? (uint32_t)(nb / 8) * 210u : (uint32_t)nb * 18u;
+    const uint32_t row_bytes = QK   ? (uint32_t)(nb / 8) * 144u
+                               : Q6  ? (uint32_t)(nb / 8) * 210u
+                               : Q8  ? (uint32_t)nb * 34u
+                               : Q41 ? (uint32_t)nb * 20u
+                                     : (uint32_t)nb * 18u;
     const uint32_t wbytes = (uint32_t)n * row_bytes;
     const __amdgpu_buffer_rsrc_t wrs = make_rsrc(W, wbytes);
     const uint32_t xbytes = (uint32_t)m * (uint32_t)k * (NATIVE ? 1u : 2u);
     const __amdgpu_buffer_rsrc_t x0rs = make_rsrc(X0, xbytes);
     const __amdgpu_buffer_rsrc_t x1rs = make_rsrc(X1, NATIVE ? (uint32_t)m * (uint32_t)nb * 4u : xbytes);
-    // per-(row, block) f32 x data: native's Q8_0 scales (X1), Q4_K's x' sums (XS)
-    const __amdgpu_buffer_rsrc_t xsrs = QK ? make_rsrc(XS, (uint32_t)m * (uint32_t)nb * 4u) : x1rs;
+    // per-(row, block) f32 x data: native's Q8_0 scales (X1), the x' sums (XS)
+    const __amdgpu_buffer_rsrc_t xsrs = SUMS ? make_rsrc(XS, (uint32_t)m * (uint32_t)nb * 4u) : x1rs;
     const int nchunks = (nb + CB - 1) / CB;
 
     // live == false (a chunk past the end) loads nothing through out-of-range
@@ -417,6 +438,30 @@ __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_kernel(
                 r.w[u][0] = h.x; r.w[u][1] = h.y; r.w[u][2] = h.z; r.w[u][3] = h.w;
                 r.w[u][4] = q0.x; r.w[u][5] = q0.y; r.w[u][6] = q0.z; r.w[u][7] = q0.w;
                 r.w[u][8] = q1.x; r.w[u][9] = q1.y; r.w[u][10] = q1.z; r.w[u][11] = q1.w;
+                continue;
+            }
+            if constexpr (Q8) {
+                // 36 bytes from the dword below the block (it starts on a dword
+                // or 2 bytes past one); the matrix's last block, when it starts
+                // on a dword, ends 2 bytes into the window's last dword: that
+                // dword is read 2 bytes early (shifted when stored)
+                const bool ok = live && idx < C::TJ * CB && j < n && b < nb;
+                const uint32_t al = ((uint32_t)j * row_bytes + (uint32_t)b * 34u) & ~3u;
+                const uint32_t last = al + 32u > wbytes - 4u ? wbytes - 4u : al + 32u;
+                const u32x4 v0 = buf_load_b128(wrs, ok ? al : RSRC_OOB);
+                const u32x4 v1 = buf_load_b128(wrs, ok ? al + 16u : RSRC_OOB);
+                r.w[u][0] = v0.x; r.w[u][1] = v0.y; r.w[u][2] = v0.z; r.w[u][3] = v0.w;
+                r.w[u][4] = v1.x; r.w[u][5] = v1.y; r.w[u][6] = v1.z; r.w[u][7] = v1.w;
+                r.w[u][8] = buf_load_b32(wrs, ok ? last : RSRC_OOB);
+                continue;
+            }
+            if constexpr (Q41) {
+                // d, m and the 16 nibble bytes: blocks start on a dword
+                const bool ok = live && idx < C::TJ * CB && j < n && b < nb;
+                const uint32_t base = (uint32_t)j * row_bytes + (uint32_t)b * 20u;
+                const u32x4 v = buf_load_b128(wrs, ok ? base : RSRC_OOB);
+                r.w[u][0] = v.x; r.w[u][1] = v.y; r.w[u][2] = v.z; r.w[u][3] = v.w;
+                r.w[u][4] = buf_load_b32(wrs, ok ? base + 16u : RSRC_OOB);
                 continue;
             }
             if constexpr (Q6) {
@@ -549,6 +594,37 @@ __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_kernel(
                 float* wdf = reinterpret_cast<float*>(st + C::WN_BYTES);
                 wdf[bl * C::TJ + jl] = d * (float)(int8_t)(scw & 0xFFu);
                 wdf[(CB + bl) * C::TJ + jl] = d * (float)(int8_t)((scw >> 8) & 0xFFu);
+            } else if constexpr (Q8) {
+                if (idx >= C::TJ * CB) continue;
+                const int jl = idx / CB, bl = idx % CB;
+                const int j = j0 + jl, b = c * CB + bl;
+                const uint32_t base = (uint32_t)j * row_bytes + (uint32_t)b * 34u, al = base & ~3u;
+                const bool mis = (base & 2u) != 0;
+                // the window's last dword, read 2 bytes early at the matrix's end
+                const uint32_t w8 = al + 32u > wbytes - 4u ? r.w[u][8] >> 16 : r.w[u][8];
+                // codes from byte 2 (block on a dword) or 4 of the window, + 128
+                uint32_t q[8];
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const uint32_t hi = i == 7 ? w8 : r.w[u][i + 1];
+                    q[i] = (mis ? hi : perm(hi, r.w[u][i], 0x05040302u)) ^ 0x80808080u;
+                }
+                uint2* dst = reinterpret_cast<uint2*>(wn + jl * C::WNS + bl * 32);
+#pragma unroll
+                for (int i = 0; i < 4; i++) dst[i] = uint2{q[2 * i], q[2 * i + 1]};
+                // rows or blocks past the matrix loaded zeros: d = 0
+                wd[bl * C::TJ + jl] = (uint16_t)(mis ? r.w[u][0] >> 16 : r.w[u][0] & 0xFFFFu);
+            } else if constexpr (Q41) {
+                if (idx >= C::TJ * CB) continue;
+                const int jl = idx / CB, bl = idx % CB;
+                // the 16 nibble bytes in a Q4_0 block's order; {d, 8 d + m} in f32
+                uint2* dst = reinterpret_cast<uint2*>(wn + jl * Lds<CB>::WN_STRIDE + bl * 16);
+                dst[0] = uint2{r.w[u][1], r.w[u][2]};
+                dst[1] = uint2{r.w[u][3], r.w[u][4]};
+                const float d = h2f(r.w[u][0] & 0xFFFFu), mm = h2f(r.w[u][0] >> 16);
+                float* wdf = reinterpret_cast<float*>(st + C::WN_BYTES);
+                wdf[bl * C::TJ + jl] = d;
+                wdf[(CB + bl) * C::TJ + jl] = 8.0f * d + mm;
             } else if (idx < C::TJ * CB) {
                 const int jl = idx / CB, bl = idx % CB;
                 const int j = j0 + jl, b = c * CB + bl;
@@ -629,6 +705,10 @@ __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_kernel(
                     const half8_t zero = {};
                     aq[a] = g < 2 ? q : zero;
                     a1[a] = g < 2 ? zero : q;
+                } else if constexpr (Q8) {
+                    // lane group g: codes (+ 128) of elements 8 g .. 8 g + 7
+                    const uint2 c8 = *reinterpret_cast<const uint2*>(wn + (jt + r16) * C::WNS + bl * 32 + 8 * g);
+                    aq[a] = q_f16<128>(c8.x, c8.y);
                 } else {
                     const uint2 nb8 = *reinterpret_cast<const uint2*>(wn + (jt + r16) * C::WNS + bl * 16 + 8 * (g & 1));
                     const uint32_t sh = (g >> 1) * 4;  // groups 2, 3: high nibbles
@@ -636,7 +716,7 @@ __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_kernel(
                     if constexpr (NATIVE) aq[a] = q_i8(n0, n1);
                     else aq[a] = q_f16(n0, n1);
                 }
-                if constexpr (QK || Q6) {
+                if constexpr (PAIRS) {
                     dv[a] = *reinterpret_cast<const f32x4*>(wdf + bl * C::TJ + jt + 4 * g);
                     ev[a] = *reinterpret_cast<const f32x4*>(wdf + (CB + bl) * C::TJ + jt + 4 * g);
                 } else {
@@ -674,13 +754,13 @@ __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_kernel(
                     const int xo = il * XSTR + bl * 64 + g * 16;
                     const half8_t bh = *reinterpret_cast<const half8_t*>(x0s + xo);
                     const half8_t bl8 = *reinterpret_cast<const half8_t*>(x1s + xo);
-                    const float sx = QK ? xss[bl * C::TI + il] : 0.0f;
+                    const float sx = SUMS ? xss[bl * C::TI + il] : 0.0f;
 #pragma unroll
                     for (int a = 0; a < FJ; a++) {
                         const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
                         f32x4 t = __builtin_amdgcn_mfma_f32_16x16x32_f16(aq[a], bh, z, 0, 0, 0);
                         t = __builtin_amdgcn_mfma_f32_16x16x32_f16(aq[a], bl8, t, 0, 0, 0);
-                        if constexpr (QK) {
+                        if constexpr (SUMS) {
 #pragma unroll
                             for (int u = 0; u < 4; u++)
                                 acc[a][b][u] = fmaf(dv[a][u], t[u], fmaf(ev[a][u], sx, acc[a][b][u]));
@@ -1610,7 +1690,7 @@ template <bool NATIVE, bool DUMP, int WF = WF_Q4_0>
 hipError_t launch_tiles(const uint8_t* w, int n, int nb, const void* x0, const void* x1, const int* xe, int m,
                         float* y, int32_t* p, hipStream_t s, int accy = 0, const float* xs = nullptr) {
     const int cus = device_cu_count();
-    if constexpr (WF == WF_Q4_K) {
+    if constexpr (WF == WF_Q4_K || WF == WF_Q4_1 || WF == WF_Q8_0) {
         // Q4_0's shapes, with 128 x 64 tiles of one block a wave a chunk (or
         // 64 x 64) where it takes its 128-row ones, which spill with Q4_K's
         // staged headers and scale pairs (7B gate/up at 128 rows: 194 us
@@ -1655,8 +1735,9 @@ hipError_t launch_tiles(const uint8_t* w, int n, int nb, const void* x0, const v
                 // 32 x 64 tiles 37.2 / 106.5 / 66.0, 8-wave 30.3 / 89.1 / 51.5,
                 // 64 x 64 38.7 / 112.9 / 40.0)
                 if (t32 > (size_t)cus) {
-                    // (Q4_K's f32 scale pairs and x' sums: chunks of 4 blocks fit the LDS)
-                    if constexpr (WF == WF_Q4_K)
+                    // (the other formats' scale pairs, sums or byte codes: chunks of
+                    // 4 blocks fit the LDS)
+                    if constexpr (WF != WF_Q4_0)
                         return launch_cfg<NATIVE, DUMP, WF, 2, 4, 2, 1, 4, 1>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
                     else
                         return launch_cfg<NATIVE, DUMP, WF, 2, 4, 2, 1, 4, 2>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
@@ -1666,7 +1747,10 @@ hipError_t launch_tiles(const uint8_t* w, int n, int nb, const void* x0, const v
             return launch_cfg<NATIVE, DUMP, WF, 2, 4, 1, 1, 4, 2>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
         }
         if (m > 16) return launch_cfg<NATIVE, DUMP, WF, 1, 2, 1, 1, 4, 2>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
-        return launch_cfg<NATIVE, DUMP, WF, 1, 1, 1, 1, 4, 8>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
+        if constexpr (wf_bytes(WF))  // (byte codes: chunks of 16 blocks fit the LDS)
+            return launch_cfg<NATIVE, DUMP, WF, 1, 1, 1, 1, 4, 4>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
+        else
+            return launch_cfg<NATIVE, DUMP, WF, 1, 1, 1, 1, 4, 8>(w, n, nb, x0, x1, xe, m, y, p, s, accy, xs);
     }
 }
 
@@ -1749,14 +1833,15 @@ hipError_t launch_gemm_q4_0(const uint8_t* w, size_t n, size_t k, const float* x
 hipError_t launch_gemm_tiles_ex(WType t, const uint8_t* w, size_t n, size_t k, const float* x, size_t m, float* y,
                                 void* scratch, int pro, const float* g, float eps, bool accumulate, hipStream_t s) {
     if (n == 0 || m == 0) return hipSuccess;
-    const bool q4k = t == WType::Q4_K, kq = q4k || t == WType::Q6_K;
-    if ((t != WType::Q4_0 && !kq) || k == 0 || k % (kq ? QK_K : QK) != 0 || (pro < 0 || pro > 2) ||
-        (pro == 1 && !g))
+    const bool q40 = t == WType::Q4_0;
+    if ((!q40 && t != WType::Q4_K && t != WType::Q6_K && t != WType::Q8_0 && t != WType::Q4_1) || k == 0 ||
+        k % block_elems(t) != 0 || (pro < 0 || pro > 2) || (pro == 1 && !g))
         return hipErrorInvalidValue;
     // Q4_0's m <= GEMM_XTILE_M rows belong to the x-tile kernel; the x' block
     // sums and the prologues come from the one-read x prep (k <= 16384)
-    if ((!kq && m <= GEMM_XTILE_M) || ((kq || pro != 0) && k > (size_t)16 * XPREP_FAST_THREADS))
+    if ((q40 && m <= GEMM_XTILE_M) || ((!q40 || pro != 0) && k > (size_t)16 * XPREP_FAST_THREADS))
         return hipErrorInvalidValue;
+    const bool sums = t == WType::Q4_K || t == WType::Q4_1;
     // 32-bit buffer offsets, out-of-range slots at RSRC_OOB
     const size_t wb = n * (k / block_elems(t)) * block_bytes(t);
     if (wb > FUSED_MAX_WEIGHT_BYTES || m * k * 2 > FUSED_MAX_WEIGHT_BYTES) return hipErrorInvalidValue;
@@ -1764,9 +1849,9 @@ hipError_t launch_gemm_tiles_ex(WType t, const uint8_t* w, size_t n, size_t k, c
     _Float16* xh = reinterpret_cast<_Float16*>(scratch);
     _Float16* xl = reinterpret_cast<_Float16*>(reinterpret_cast<uint8_t*>(scratch) + xb);
     int* xe = reinterpret_cast<int*>(reinterpret_cast<uint8_t*>(scratch) + 2 * xb);
-    float* xs = q4k ? reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(scratch) + 2 * xb +
-                                               ((m * 4 + 255) & ~(size_t)255))
-                    : nullptr;
+    float* xs = sums ? reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(scratch) + 2 * xb +
+                                                ((m * 4 + 255) & ~(size_t)255))
+                     : nullptr;
     const dim3 grid((unsigned)m);
     if (pro == 1)
         launch_kernel(gemm_xprep_pro_kernel<1>, grid, dim3(XPREP_FAST_THREADS), 0, s, x, (int)k, g, eps, xh, xl, xe,
@@ -1781,17 +1866,19 @@ hipError_t launch_gemm_tiles_ex(WType t, const uint8_t* w, size_t n, size_t k, c
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int accy = accumulate ? 1 : 0;
-    if (q4k)
-        return launch_tiles<false, false, WF_Q4_K>(w, (int)n, (int)(k / QK), xh, xl, xe, (int)m, y, nullptr, s, accy,
-                                                   xs);
-    if (kq)
-        return launch_tiles<false, false, WF_Q6_K>(w, (int)n, (int)(k / QK), xh, xl, xe, (int)m, y, nullptr, s, accy);
-    return launch_tiles<false, false>(w, (int)n, (int)(k / QK), xh, xl, xe, (int)m, y, nullptr, s, accy);
+    const int ni = (int)n, nb = (int)(k / QK), mi = (int)m;
+    switch (t) {
+        case WType::Q4_K: return launch_tiles<false, false, WF_Q4_K>(w, ni, nb, xh, xl, xe, mi, y, nullptr, s, accy, xs);
+        case WType::Q6_K: return launch_tiles<false, false, WF_Q6_K>(w, ni, nb, xh, xl, xe, mi, y, nullptr, s, accy);
+        case WType::Q8_0: return launch_tiles<false, false, WF_Q8_0>(w, ni, nb, xh, xl, xe, mi, y, nullptr, s, accy);
+        case WType::Q4_1: return launch_tiles<false, false, WF_Q4_1>(w, ni, nb, xh, xl, xe, mi, y, nullptr, s, accy, xs);
+        default: return launch_tiles<false, false>(w, ni, nb, xh, xl, xe, mi, y, nullptr, s, accy);
+    }
 }
 
-hipError_t launch_gemm_kquant(WType t, const uint8_t* w, size_t n, size_t k, const float* x, size_t m, float* y,
-                              void* scratch, hipStream_t s) {
-    if (t != WType::Q4_K && t != WType::Q6_K) return hipErrorInvalidValue;
+hipError_t launch_gemm_typed(WType t, const uint8_t* w, size_t n, size_t k, const float* x, size_t m, float* y,
+                             void* scratch, hipStream_t s) {
+    if (t == WType::Q4_0) return hipErrorInvalidValue;  // launch_gemm_q4_0
     return launch_gemm_tiles_ex(t, w, n, k, x, m, y, scratch, 0, nullptr, 0.0f, false, s);
 }
 

@@ -696,8 +696,8 @@ struct LlamaModel {
         if (w.type == WType::Q4_0)
             return native ? launch_gemm_q4_0_native(w.dev, w.n, w.k, xin, m, y, nullptr, gemm_scratch, stream)
                           : launch_gemm_q4_0(w.dev, w.n, w.k, xin, m, y, gemm_scratch, gemm_cnt, stream);
-        if (kgemm(w, m)) {
-            const hipError_t e = launch_gemm_kquant(w.type, w.dev, w.n, w.k, xin, m, y, gemm_scratch, stream);
+        if (kgemm(w, m, native)) {
+            const hipError_t e = launch_gemm_typed(w.type, w.dev, w.n, w.k, xin, m, y, gemm_scratch, stream);
             if (e != hipErrorInvalidValue) return e;
         }
         // rows four at a time through the fused GEMV (other types, or scales
@@ -863,9 +863,11 @@ struct LlamaModel {
     }
 
     static bool kquant(const Mat& w) { return w.type == WType::Q4_K || w.type == WType::Q6_K; }
-    // Q4_K / Q6_K products of m >= KQ_GEMM_MIN_M rows run on the LDS tile GEMM
-    static bool kgemm(const Mat& w, size_t m) {
-        return kquant(w) && m >= KQ_GEMM_MIN_M && w.k % QK_K == 0 && w.k <= 16384;
+    // Q4_K / Q6_K / Q8_0 products of m >= KQ_GEMM_MIN_M rows, and Q4_1 ones
+    // outside native mode, run on the LDS tile GEMM
+    static bool kgemm(const Mat& w, size_t m, bool native = false) {
+        const bool typed = kquant(w) || w.type == WType::Q8_0 || (w.type == WType::Q4_1 && !native);
+        return typed && m >= KQ_GEMM_MIN_M && w.k % (int)block_elems(w.type) == 0 && w.k <= 16384;
     }
     // the K-quant GEMVs with the decoder's steps folded into their launches
     static bool kfold(const Mat& w, size_t m) { return kquant(w) && !kgemm(w, m); }
@@ -884,7 +886,7 @@ struct LlamaModel {
     }
 
     // One layer of any resident types, any row count (m > 4 Q4_0 rows and
-    // m >= KQ_GEMM_MIN_M Q4_K / Q6_K rows take the GEMMs).  Q4_K / Q6_K matrices on
+    // m >= KQ_GEMM_MIN_M rows of the other types take the GEMMs).  Q4_K / Q6_K matrices on
     // the GEMVs fold the RMSNorm in front of them, the residual add after o /
     // down, the SwiGLU of combined gate/up rows and the RoPE + cache write of
     // combined q/k/v rows into their GEMV launches; the other types run
@@ -908,7 +910,7 @@ struct LlamaModel {
             parts[0] = &L.q, parts[1] = &L.k, parts[2] = &L.v;
             np = 3;
         }
-        // Q4_0 (m > GEMM_XTILE_M) and K-quant prompt chunks on the LDS tile GEMM
+        // Q4_0 (m > GEMM_XTILE_M) and other prompt chunks (m >= KQ_GEMM_MIN_M) on the LDS tile GEMM
         // fold the RMSNorms, the SwiGLU and the residual adds into the GEMMs'
         // x splits and stores (hipErrorInvalidValue: a shape they do not take,
         // nothing launched, the separate launches below run instead)

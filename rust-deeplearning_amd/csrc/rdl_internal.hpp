@@ -175,7 +175,7 @@ int device_cu_count();
 // partials[(i * n + j) * (k / 32) + b] instead of y.
 constexpr size_t GEMM_SMALL_M = 64;
 constexpr size_t GEMM_XTILE_M = 64;  // float products of at most this many rows: x tiles as MFMA A operands, 128-row strips
-constexpr size_t KQ_GEMM_MIN_M = 16;  // Q4_K / Q6_K products of at least this many rows: the LDS tile GEMM
+constexpr size_t KQ_GEMM_MIN_M = 16;  // Q4_K / Q6_K / Q8_0 / Q4_1 float products of at least this many rows: the LDS tile GEMM
 size_t gemm_scratch_bytes(size_t m, size_t n, size_t k, bool native);
 // ints of the GEMM's strip counters for out_features n, in_features k
 size_t gemm_counter_count(size_t n, size_t k);
@@ -194,8 +194,8 @@ hipError_t launch_gemm_q4_0(const uint8_t* w, size_t n, size_t k, const float* x
 hipError_t launch_gemm_q4_0_native(const uint8_t* w, size_t n, size_t k, const float* x, size_t m, float* y,
                                    int32_t* partials, void* scratch, hipStream_t s);
 // Float-mode products on the LDS tile GEMM, Q4_0 (more than GEMM_XTILE_M
-// rows), Q4_K or Q6_K weights (any row count; k % 256 == 0, k <= 16384),
-// with the decoder's neighbouring steps folded in; hipErrorInvalidValue
+// rows), Q4_K, Q6_K, Q8_0 or Q4_1 weights (any row count; k a multiple of
+// the block, k <= 16384), with the decoder's neighbouring steps folded in; hipErrorInvalidValue
 // (nothing launched) for shapes it does not take.  x rows go through pro 1
 // RMSNorm (weights g, eps; x [m, k]) or pro 2 SwiGLU (x [m, 2k] interleaved
 // gate / up) before the product (pro 0: none); accumulate: y += product (the
@@ -204,10 +204,12 @@ hipError_t launch_gemm_q4_0_native(const uint8_t* w, size_t n, size_t k, const f
 hipError_t launch_gemm_tiles_ex(WType t, const uint8_t* w, size_t n, size_t k, const float* x, size_t m, float* y,
                                 void* scratch, int pro, const float* g, float eps, bool accumulate, hipStream_t s);
 size_t gemm_tiles_scratch_bytes(size_t m, size_t k);
-// The Q4_K / Q6_K product y = x W^T on the LDS tile GEMM (the reference's
-// dequantize_q4k / dequantize_q6k + F32 matmul, parser.rs:510-593).
-hipError_t launch_gemm_kquant(WType t, const uint8_t* w, size_t n, size_t k, const float* x, size_t m, float* y,
-                              void* scratch, hipStream_t s);
+// The float-mode product y = x W^T of Q4_K, Q6_K, Q8_0 or Q4_1 weights on
+// the LDS tile GEMM (the reference's dequantize_q4k / dequantize_q6k + F32
+// matmul, parser.rs:510-593; matmul_f32_q8, quantize.rs:201-260;
+// matmul_f32_q4_1, quantize.rs:429-495).
+hipError_t launch_gemm_typed(WType t, const uint8_t* w, size_t n, size_t k, const float* x, size_t m, float* y,
+                             void* scratch, hipStream_t s);
 
 // Decoder fusion of the Q4_0 float-mode fused GEMV (m <= 4, k / 32 even,
 // x 16-byte aligned): prologue 0 none, 1 RMSNorm with weights g and eps,

@@ -1,9 +1,10 @@
-"""GPU parity of the K-quant prompt GEMM (matrix cores): products of
-KQ_GEMM_MIN_M (16) or more rows of the reference's Q4_K and Q6_K Linears
-(dequantize_q4k / dequantize_q6k at load,
-rustml/gguf/main/src/core/parser.rs:510-593, then the F32 matmul) through the
-C ABI, against the CPU restatement and the exact (f64) value of the reference
-computation."""
+"""GPU parity of the prompt GEMM (matrix cores) for the weight formats other
+than Q4_0: products of KQ_GEMM_MIN_M (16) or more rows of the reference's
+Q4_K and Q6_K Linears (dequantize_q4k / dequantize_q6k at load,
+rustml/gguf/main/src/core/parser.rs:510-593, then the F32 matmul), of
+matmul_f32_q8 (quantize.rs:201-260) and of matmul_f32_q4_1 (float mode,
+quantize.rs:429-495), through the C ABI, against the CPU restatement and the
+exact (f64) value of the reference computation."""
 import numpy as np
 import pytest
 
@@ -16,11 +17,16 @@ THREADS = 16
 
 
 def product(rq, kind):
-    return rq.matmul_f32_q4_k if kind == "q4k" else rq.matmul_f32_q6_k
+    return {"q4k": rq.matmul_f32_q4_k, "q6k": rq.matmul_f32_q6_k, "q8": rq.matmul_f32_q8,
+            "q4_1": rq.matmul_f32_q4_1}[kind]
 
 
 def weights(kind, n, k, seed):
-    return synth.q4_k_weights(n, k, seed) if kind == "q4k" else synth.q6_k_weights(n, k, seed)
+    return {"q4k": synth.q4_k_weights, "q6k": synth.q6_k_weights, "q8": synth.q8_0_weights,
+            "q4_1": synth.q4_1_weights}[kind](n, k, seed)
+
+
+ALL = ["q4k", "q6k", "q8", "q4_1"]
 
 
 # Bar: check_parity with each output's condition (Q6_K's synthetic rows of
@@ -41,8 +47,9 @@ def run(rq, orc, m, n, k, seed, rows=None, x=None, w=None, kind="q4k"):
 # tiles, 32-block chunks), 17-47 (16 x 32), 48-127 with the 32 x 64 tiles of
 # 4 or 8 waves, 128 (64 x 64 when 32-row tiles overflow a round, 128 x 64
 # when they fill the CUs), 256 and 1024 (128 x 128).  Q6_K: 16 x 16 (16-block
-# chunks), 16 x 32, then 32 x 64 tiles below a round of 64 x 64 ones.
-@pytest.mark.parametrize("kind", ["q4k", "q6k"])
+# chunks), 16 x 32, then 32 x 64 tiles below a round of 64 x 64 ones.  Q8_0
+# and Q4_1 take Q4_K's shapes (Q8_0 16 x 16 tiles with 16-block chunks).
+@pytest.mark.parametrize("kind", ALL)
 @pytest.mark.parametrize("m,n,k", [(16, 4096, 4096), (16, 64, 256), (24, 300, 1024), (47, 1000, 2048),
                                    (64, 4096, 4096), (64, 12288, 512), (128, 4096, 4096), (128, 12288, 1024),
                                    (128, 22016, 512), (256, 4096, 1024), (1024, 512, 768)])
@@ -56,14 +63,25 @@ def test_kquant_gemm_tile_shapes(rq, orc, gpu, m, n, k, kind):
 # super-block counts a row (768, 1280, 2304) alternate the rows' alignment,
 # and (16, 1, 256) / (19, 37, 768) end the matrix with a super-block on a
 # dword (its d read from 2 bytes before its dword).
-@pytest.mark.parametrize("kind", ["q4k", "q6k"])
+@pytest.mark.parametrize("kind", ALL)
 @pytest.mark.parametrize("m,n,k", [(16, 1, 256), (19, 37, 768), (70, 130, 1280), (130, 257, 2304),
                                    (300, 100, 256), (33, 40, 16384), (1030, 33, 512), (48, 3, 768)])
 def test_kquant_gemm_ragged(rq, orc, gpu, m, n, k, kind):
     run(rq, orc, m, n, k, 61 + m + n + k, kind=kind)
 
 
-@pytest.mark.parametrize("kind", ["q4k", "q6k"])
+# Q8_0 / Q4_1 rows of any whole number of 32-element blocks: odd block counts
+# (Q8_0's 34-byte blocks then alternate between starting on a dword and 2
+# bytes past one, across rows too; (16, 1, 32), (17, 5, 96) and (48, 3, 160)
+# end the matrix with a block on a dword, its last dword read 2 bytes early)
+@pytest.mark.parametrize("kind", ["q8", "q4_1"])
+@pytest.mark.parametrize("m,n,k", [(16, 1, 32), (17, 5, 96), (48, 3, 160), (20, 33, 1056), (130, 77, 4128),
+                                   (64, 301, 416), (300, 64, 14336)])
+def test_q8_q4_1_gemm_block_counts(rq, orc, gpu, m, n, k, kind):
+    run(rq, orc, m, n, k, 91 + m + n + k, kind=kind)
+
+
+@pytest.mark.parametrize("kind", ALL)
 def test_kquant_gemm_large_rows_sampled(rq, orc, gpu, kind):
     # 2048 rows: each output row depends only on its x row, so 40 spread rows
     # pin all tiles
@@ -71,13 +89,13 @@ def test_kquant_gemm_large_rows_sampled(rq, orc, gpu, kind):
     run(rq, orc, 2048, 4096, 1024, 0x5EED4800, rows=rows, kind=kind)
 
 
-@pytest.mark.parametrize("kind", ["q4k", "q6k"])
+@pytest.mark.parametrize("kind", ALL)
 def test_kquant_longer_rows_take_the_records_path(rq, orc, gpu, kind):
     # k = 16640 > 16384: the x prep cannot hold the row; the records GEMV runs
     run(rq, orc, 20, 30, 16640, 0x5EED4900, kind=kind)
 
 
-@pytest.mark.parametrize("kind", ["q4k", "q6k"])
+@pytest.mark.parametrize("kind", ALL)
 def test_kquant_gemm_matches_gemv_rows(rq, gpu, kind):
     # the same rows through the GEMV (4 rows) and the GEMM (16 rows) agree
     # within the bar: the two paths split and sum differently
@@ -149,7 +167,7 @@ def test_q6k_gemm_extreme_scales(rq, orc, gpu):
     assert_close(got[well], exact[well])
 
 
-@pytest.mark.parametrize("kind", ["q4k", "q6k"])
+@pytest.mark.parametrize("kind", ALL)
 def test_kquant_gemm_nan_row_stays_in_its_row(rq, gpu, kind):
     m, n, k = 20, 48, 512
     x = synth.activations(m, k, 5)

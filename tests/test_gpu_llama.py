@@ -378,6 +378,19 @@ def test_mixed_type_layers(rq, gpu, kv_f16):
     assert list(toks) == eager
 
 
+def test_mixed_type_prompt_chunk_on_the_gemms(rq, gpu):
+    """The mixed-type model above with a 40-row prompt chunk: layer 0's Q4_0
+    GEMMs, layer 1's [Wq; Wk] (Q4_K), Q6_K v, Q8_0 o and split gate (Q4_K) /
+    up (Q6_K) / down (Q6_K) on the tile GEMM, layer 2's Q8_0 q/k/v with the
+    RMSNorm in its x prep, Q4_1 gate/up with the SwiGLU folded into the Q4_K
+    down's x prep; then decode steps and greedy generation, against the
+    oracle."""
+    cfg = tiny_config(n_layers=3, output_dtype=8, max_batch=40, max_seq=64)
+    m, ref, _ = build_typed(cfg, mixed_types(), 101)
+    prompt = [int(v) for v in np.random.default_rng(41).integers(0, cfg.vocab, size=40)]
+    check_typed_model(m, ref, prompt, 17, steps=2)
+
+
 def check_typed_model(m, ref, prompt, tok, steps=4):
     """Prefill (rows four at a time through the fused GEMVs), decode steps and
     greedy generation against the oracle's forward."""
