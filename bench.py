@@ -53,7 +53,7 @@ LONG_PROMPT_LEN = 2040  # prefill figure beside the decode line (max_seq 2048)
 Q6K_LM_HEAD = "Q6_K GEMV 32000x4096 (the output matrix of llama.cpp Q4_0 7B files)"
 
 # GGML type id -> (elements per block, bytes per block)
-BLOCK = {2: (32, 18), 8: (32, 34), 12: (256, 144), 14: (256, 210)}
+BLOCK = {2: (32, 18), 3: (32, 20), 8: (32, 34), 12: (256, 144), 14: (256, 210)}
 
 
 def algorithmic_bytes(n, k, dtype=2):
@@ -354,17 +354,22 @@ def native_check(rig, w_host, x, y, m, n, k):
     return ok
 
 
-def exact_check(rig, weight, x, y, m, n, k):
+def exact_check(rig, weight, x, y, m, n, k, cond=False):
     """y within 1e-3 rel + 1e-4 abs of the exact (f64) product over the weight's
     f32 values (Tensor::to_f32 / dequantize_q4k, expanded by the library's
-    bit-exact row dequantization); torch does the f64 product on the device."""
+    bit-exact row dequantization); torch does the f64 product on the device.
+    cond: plus 1e-6 sum |x| |w| of each output (outputs that cancel far below
+    their terms, beyond any f32 evaluation's value bar)."""
     torch = rig.torch
     rows = torch.arange(n, dtype=torch.int32, device=rig.dev)
     wf = torch.empty(n, k, dtype=torch.float32, device=rig.dev)
     weight.dequantize_rows_dev(rows.data_ptr(), n, wf.data_ptr(), rig.stream.cuda_stream)
     want = x.reshape(m, k).double() @ wf.double().T
     got = y.reshape(m, n).double()
-    ok = bool(((got - want).abs() <= 1e-4 + 1e-3 * want.abs()).all().item())
+    tol = 1e-4 + 1e-3 * want.abs()
+    if cond:
+        tol = tol + 1e-6 * (x.reshape(m, k).double().abs() @ wf.double().abs().T)
+    ok = bool(((got - want).abs() <= tol).all().item())
     del wf
     return ok
 
@@ -406,14 +411,19 @@ def gemv_line(rig, name, dtype, n, k, seed, steps, warmup, traffic_key=None):
     }
 
 
-def gemm_lines(rig, ms_list, seed=0x5EED0004, native=False):
+TYPE_NAME = {2: "Q4_0", 3: "Q4_1", 8: "Q8_0", 12: "Q4_K", 14: "Q6_K"}
+
+
+def gemm_lines(rig, ms_list, seed=0x5EED0004, native=False, dtype=2):
     """Y = X W^T, W 4096x4096 Q4_0, X f32 [M, 4096]; the whole call
     (activation split or Q8_0 quantization + MFMA GEMM) timed over a loop of
-    launches.  native: matmul_f32_q4_native (int8 MFMA on the Q8_0 codes)."""
+    launches.  native: matmul_f32_q4_native (int8 MFMA on the Q8_0 codes).
+    dtype: the same product for another weight format (not a BASELINE
+    config; the tile GEMM of Q8_0, Q4_1, Q4_K and Q6_K)."""
     torch, rq = rig.torch, rig.rq
     n = k = 4096
     mode = rq.MODE_NATIVE if native else rq.MODE_FLOAT
-    w_host, weights = rig.weight_copies(2, n, k, seed, min_copies=16)
+    w_host, weights = rig.weight_copies(dtype, n, k, seed, min_copies=16)
     s = rig.stream
     out = []
     for m in ms_list:
@@ -433,14 +443,17 @@ def gemm_lines(rig, ms_list, seed=0x5EED0004, native=False):
         torch.cuda.synchronize()
         ms = a.elapsed_time(b) / it
         flops = 2.0 * m * n * k
-        abytes = n * (k // 32) * 18 + 4 * m * k + 4 * m * n
-        ok = native_check(rig, w_host, x, y, m, n, k) if native else exact_check(rig, weights[0][1], x, y, m, n, k)
+        qk, bb = BLOCK[dtype]
+        abytes = n * (k // qk) * bb + 4 * m * k + 4 * m * n
+        ok = (native_check(rig, w_host, x, y, m, n, k) if native
+              else exact_check(rig, weights[0][1], x, y, m, n, k, cond=dtype != 2))
         tflops = flops / (ms * 1e-3) / 1e12
         gbps = abytes / (ms * 1e-3) / 1e9
         peak_mm = PEAK_I8_TOPS if native else PEAK_F16_TFLOPS
         bound = "mfma" if flops / abytes > peak_mm * 1e12 / (PEAK_HBM_GBPS * 1e9) else "hbm"
         out.append({
-            "workload": f"config4 M={m}" + (" native (matmul_f32_q4_native, int8 MFMA)" if native else ""),
+            "workload": (f"config4 M={m}" + (" native (matmul_f32_q4_native, int8 MFMA)" if native else "")
+                         if dtype == 2 else f"{TYPE_NAME[dtype]} GEMM 4096x4096 M={m} (not a BASELINE config)"),
             "m": m,
             "value": round(tflops, 2),
             "unit": "TOP/s" if native else "TFLOP/s",
@@ -742,7 +755,7 @@ def main():
     ap.add_argument("--copies", type=int, default=24)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--workload", default="all", choices=["all", "gemv", "q8_0", "q4_k", "q6_k", "gemm", "decode", "decode_q4_k_m", "load", "read"],
+    ap.add_argument("--workload", default="all", choices=["all", "gemv", "q8_0", "q4_k", "q6_k", "gemm", "gemm_formats", "decode", "decode_q4_k_m", "load", "read"],
                     help="all: the headline line plus configs 1, 3, 4, 5 and the Q6_K lm_head; otherwise only one "
                          "(load: the GGUF file load, decode_q4_k_m: a Q4_K_M-mixed 7B decode; run only "
                          "when asked)")
@@ -771,7 +784,7 @@ def main():
         del src, dst
 
     wl = args.workload
-    if wl in ("q8_0", "q4_k", "q6_k", "gemm", "decode", "decode_q4_k_m", "load", "read"):
+    if wl in ("q8_0", "q4_k", "q6_k", "gemm", "gemm_formats", "decode", "decode_q4_k_m", "load", "read"):
         if wl == "read":
             line = read_lines(rig)
         elif wl == "q8_0":
@@ -786,6 +799,8 @@ def main():
             line = gemv_line(rig, Q6K_LM_HEAD, 14, 32000, 4096, 0x5EED0006, args.steps, args.warmup)
         elif wl == "gemm":
             line = gemm_lines(rig, [16, 64, 512, 2048]) + gemm_lines(rig, [512, 2048], native=True)
+        elif wl == "gemm_formats":
+            line = [l for t in (8, 3, 12, 14) for l in gemm_lines(rig, [16, 128, 512, 2048], seed=0x5EED0040 + t, dtype=t)]
         elif wl == "load":
             line = load_line(rig)
         elif wl == "decode_q4_k_m":
