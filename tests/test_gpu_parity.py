@@ -89,7 +89,8 @@ def test_gemv_q4k_ragged(rq, orc, gpu, m, n, k):
 # Q6_K (dequantize_q6k + F32 Linear in the reference): K split over 1 (K <= 2048),
 # 2, 4 or 8 waves of 64 columns; odd super-block counts (K = 768, 1280, 4352,
 # 8448) put every other row on a 2-byte boundary; ragged last slices; the
-# lm_head shape; m > 4 takes the records kernel.
+# lm_head shape; 5-15 rows take the records kernel (16 or more the tile GEMM,
+# tests/test_gpu_gemm_formats.py).
 @pytest.mark.parametrize("m,n,k", [(1, 1, 256), (2, 5, 768), (1, 33, 1280), (3, 8, 14336),
                                    (1, 1000, 2048), (4, 300, 4096), (1, 32000, 4096), (1, 37, 4352),
                                    (2, 100, 8192), (1, 77, 8448), (1, 130, 16384), (5, 40, 4096),

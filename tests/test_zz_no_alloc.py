@@ -18,7 +18,7 @@ pytestmark = pytest.mark.gpu
     (2, 0, 4096, 4096, (64, 33)),    # Q4_0 float, four then three x tiles
     (2, 1, 4096, 4096, (24, 6)),     # Q4_0 native: Q8_0 records in scratch
     (3, 1, 1000, 2048, (9, 5)),      # Q4_1 native records
-    (8, 0, 512, 1024, (33, 7)),      # Q8_0 float records
+    (8, 0, 512, 1024, (33, 7)),      # Q8_0 float: tile GEMM (33 rows), then records (7 rows)
     (12, 0, 1024, 4096, (40, 16)),   # Q4_K float: tile GEMM, x split and x' block sums in scratch
     (14, 0, 1000, 2048, (20, 17)),   # Q6_K float: tile GEMM, x split in scratch
 ])
