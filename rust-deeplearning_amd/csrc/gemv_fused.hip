@@ -226,7 +226,18 @@ struct Fuse {
     const int* kv_table;        // physical page of each logical page
     int n_heads, n_kv, hd, kv_f16;
     uint64_t* xch;              // PUB: the layer's exchange, one tagged value per q / k / v row
+    int* err;                   // XIO_IN: set when a wait runs out (never in a correct launch)
+    // XIO_IN: x read as tagged words from xin instead of X; XIO_OUT: outputs
+    // published as tagged words to xout instead of Y; the tag is *pos + 1
+    const uint64_t* xin;
+    uint64_t* xout;
 };
+
+// How a fused GEMV body exchanges its activation within a launch: XIO_NONE
+// (x read from memory, y stored), XIO_IN (x polled from another role's
+// published words; the weight stream starts before x exists), XIO_OUT (y
+// published as tagged words for another role of the same launch).
+constexpr int XIO_NONE = 0, XIO_IN = 1, XIO_OUT = 2;
 
 template <int NW, int PI, int PRO = PRO_NONE>
 __device__ __forceinline__ void load_prep_x4(const float* __restrict__ x, const float* __restrict__ aux, int nb,
@@ -578,12 +589,17 @@ constexpr int EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_SWIGLU = 2, EPI_ROPE_KV = 3;
 // to the exchange fz.xch as one tagged 8-byte value (xch_put, tag = position
 // + 1), which the fused decode attention of the same launch polls; the q
 // rows are then not written to y (nothing else reads them).
+// XIO (int4 records, one activation row): see XIO_NONE / XIO_IN / XIO_OUT;
+// XIO_IN takes PRO_RMSNORM and issues every weight block before polling x,
+// XIO_OUT takes EPI_RESIDUAL (the old y still read from Y).
 template <int WT, bool NATIVE, int R, int CPL, bool NB_EVEN, int NW, int PRO = PRO_NONE, int EPI = EPI_STORE,
-          bool PUB = false>
+          bool PUB = false, int XIO = XIO_NONE>
 __device__ __forceinline__ void gemv_fused_body(int bx, int by, i32x4* __restrict__ lds4, const uint8_t* __restrict__ W,
                                                 int n, int nb, int rpw, const float* __restrict__ X,
                                                 float* __restrict__ Y, const Fuse& fz) {
     static_assert(!PUB || EPI == EPI_ROPE_KV, "publication is for the q/k/v epilogue");
+    static_assert(XIO != XIO_IN || PRO == PRO_RMSNORM, "x from the exchange feeds the RMSNorm prologue");
+    static_assert(XIO != XIO_OUT || EPI == EPI_RESIDUAL, "published outputs are residual sums");
     constexpr int BYTES = Geo<WT>::BYTES, WORDS = Geo<WT>::WORDS;
     constexpr int LPB = (WORDS == 9) ? 3 : 2;    // load instructions per block
     constexpr int NB = R * CPL;                   // blocks per lane
@@ -600,8 +616,10 @@ __device__ __forceinline__ void gemv_fused_body(int bx, int by, i32x4* __restric
     // (the q/k/v launch of a decode step, 8 blocks a lane on 192 of the
     // CUs: all of them in flight, 4 before the prep; 7B decode 812 -> 820
     // tokens/s against 3 / 2, and against 8 / 8: 804)
-    constexpr int PF = EPI == EPI_ROPE_KV ? NB : (NB < (I4 ? PF_I4 : 4)) ? NB : (I4 ? PF_I4 : 4);
-    constexpr int P0 = EPI == EPI_ROPE_KV ? (PF < 4 ? PF : 4) : (PF < (I4 ? 2 : 4)) ? PF : (I4 ? 2 : 4);
+    // (XIO_IN: every block before x exists)
+    constexpr int PF = (EPI == EPI_ROPE_KV || XIO == XIO_IN) ? NB : (NB < (I4 ? PF_I4 : 4)) ? NB : (I4 ? PF_I4 : 4);
+    constexpr int P0 = XIO == XIO_IN ? NB
+                       : EPI == EPI_ROPE_KV ? (PF < 4 ? PF : 4) : (PF < (I4 ? 2 : 4)) ? PF : (I4 ? 2 : 4);
     constexpr int PI = I4 ? (CPL * 4 + NW - 1) / NW : (CPL * 8 + NW - 1) / NW;
     const int lane = threadIdx.x & 63;
     const int wv = threadIdx.x >> 6;
@@ -669,7 +687,61 @@ __device__ __forceinline__ void gemv_fused_body(int bx, int by, i32x4* __restric
 
     // ---- x for the prep first, then the first PF blocks ----
     __builtin_amdgcn_s_setprio(2);  // the prep ahead of other workgroups' streams
-    if constexpr (I4) {
+    if constexpr (XIO == XIO_IN) {
+        // the weight stream first (it does not depend on x), then the
+        // RMSNorm weights, then x: this thread's pieces (load_prep_x4's
+        // elements) polled from the exchange until all carry the tag
+        static_assert(I4, "int4 records");
+#pragma unroll
+        for (int b = 0; b < P0; b++) issue(b);
+        f32x4 xv[PI][2], av[PI][2];
+        constexpr int NT = NW * 64;
+#pragma unroll
+        for (int j = 0; j < PI; j++) {
+            const int p = min((int)threadIdx.x + j * NT, nb * 4 - 1);
+            const int o = (p >> 2) * 32 + (p & 3) * 4;
+            av[j][0] = *reinterpret_cast<const f32x4*>(fz.g + o);
+            av[j][1] = *reinterpret_cast<const f32x4*>(fz.g + o + 16);
+        }
+        const int xtag = *fz.pos + 1;
+        // Each wave first watches one word (wave w: the last of the w-th
+        // eighth of x), sleeping between reads, and polls its pieces only
+        // once that word is there.  Where these workgroups share the CUs
+        // with the down workgroups, hundreds of them polling every word at
+        // once kept the down workgroups' stores from landing for the
+        // whole bounded wait (MI355X, 2 workgroups a CU: 60 ms).
+        {
+            const uint64_t* watch = fz.xin + min((wv + 1) * nb * 4, nb * 32) - 1;
+            for (int spins = 0;; spins++) {
+                if (att::xch_ok(att::xch_get(watch), xtag) || spins > (1 << 16)) break;
+                __builtin_amdgcn_s_sleep(2);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < PI; j++) {
+            const int p = min((int)threadIdx.x + j * NT, nb * 4 - 1);
+            const uint64_t* src = fz.xin + (p >> 2) * 32 + (p & 3) * 4;
+            uint64_t v[8];
+            for (int spins = 0;; spins++) {
+                bool ok = true;
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    v[i] = att::xch_get(src + (i & 3) + (i >> 2) * 16);
+                    ok = ok && att::xch_ok(v[i], xtag);
+                }
+                if (__builtin_amdgcn_ballot_w64(!ok) == 0) break;
+                if (spins > (1 << 16)) {  // only a broken launch gets here
+                    if ((threadIdx.x & 63) == 0)
+                        __hip_atomic_store(fz.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+            xv[j][0] = f32x4{att::xch_val(v[0]), att::xch_val(v[1]), att::xch_val(v[2]), att::xch_val(v[3])};
+            xv[j][1] = f32x4{att::xch_val(v[4]), att::xch_val(v[5]), att::xch_val(v[6]), att::xch_val(v[7])};
+        }
+        prep_float4_lds<NW, PI, PRO>(xv, av, fz.eps, nb, reinterpret_cast<int*>(lds4));
+    } else if constexpr (I4) {
         f32x4 xv[PI][2], av[PI][2];
         const float* aux = (PRO == PRO_RMSNORM) ? fz.g : x + nb * 32;
         load_prep_x4<NW, PI, PRO>(x, aux, nb, xv, av);
@@ -818,7 +890,9 @@ __device__ __forceinline__ void gemv_fused_body(int bx, int by, i32x4* __restric
         } else if ((lane & ((1 << SH) - 1)) == 0) {
             const int row = row_of(grp * RG + (lane >> SH));
             if (row < rend) {
-                if constexpr (EPI == EPI_RESIDUAL)
+                if constexpr (XIO == XIO_OUT)
+                    att::xch_put(fz.xout + row, s + y_old, *fz.pos + 1);
+                else if constexpr (EPI == EPI_RESIDUAL)
                     y[row] = s + y_old;
                 else
                     y[row] = s;
@@ -846,6 +920,10 @@ struct OProj {
     int n, nb;
     float* x;              // residual stream [n]
     const uint64_t* xch;
+    // when set: the residual stream's current values as tagged words (the
+    // launch's tag) published by another role of the launch (x is then only
+    // written)
+    const uint64_t* xin;
 };
 
 // One o-projection workgroup of the fused decode launch: rows r0 + wv + 8 r
@@ -875,10 +953,32 @@ __device__ __forceinline__ void o_proj_body(int j, i32x4* __restrict__ lds4, con
         load_window<WORDS, false>(rs, off, wbytes, win[b]);
     }
     float y_old[RO];
+    if (op.xin) {
+        // every lane polls the wave's RO words (the same addresses)
+        uint64_t v[RO];
+        for (int spins = 0;; spins++) {
+            bool ok = true;
 #pragma unroll
-    for (int r = 0; r < RO; r++) {
-        const int row = r0 + wv + r * NW;
-        y_old[r] = row < n ? op.x[row] : 0.0f;
+            for (int r = 0; r < RO; r++) {
+                const int row = min(r0 + wv + r * NW, n - 1);
+                v[r] = att::xch_get(op.xin + row);
+                ok = ok && att::xch_ok(v[r], t);
+            }
+            if (__builtin_amdgcn_ballot_w64(!ok) == 0) break;
+            if (spins > (1 << 16)) {  // only a broken launch gets here
+                if (lane == 0) __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+#pragma unroll
+        for (int r = 0; r < RO; r++) y_old[r] = att::xch_val(v[r]);
+    } else {
+#pragma unroll
+        for (int r = 0; r < RO; r++) {
+            const int row = r0 + wv + r * NW;
+            y_old[r] = row < n ? op.x[row] : 0.0f;
+        }
     }
     // this thread's activation pieces (load_prep_x4's): block c, elements
     // 32 c + 4 k + {0..3} and + 16
@@ -941,23 +1041,49 @@ constexpr int O_ROWS_PER_WAVE = 4;
 // span) that load their older K/V rows at once, wait for their KV group's
 // q/k/v values (tagged exchange) and then read q and the current row; with
 // op.w set, the rest are o-projection workgroups (o_proj_body) that wait for
-// the attention outputs.  All workgroups fit the device at once (a few
-// hundred against two per CU), the o-projection ones come last in dispatch
-// order, and the waits are bounded, so no ordering of workgroup dispatch can
-// block them.
-template <typename KV, int HD, int R, int CPL>
+// the attention outputs.  Every wait is on workgroups with smaller ids, and
+// the device dispatches a launch's workgroups in id order (workgroup i on
+// XCD i % 8, each XCD in id order, measured on MI355X), so the oldest
+// unfinished workgroup is always resident and its producers are done: the
+// grid may exceed what the CUs hold at once (7B: 352 workgroups, one a CU).
+// The waits are bounded besides: one that runs out sets *err.
+// The previous layer's down projection (x += h W_down^T, Q4_0) as the first
+// role of a fused decode launch (DOWN): its workgroups publish the new x as
+// tagged words (Fuse::xout) instead of storing it; the q/k/v workgroups,
+// whose weight blocks are all in flight meanwhile, take x from there for
+// their RMSNorm, and the o workgroups take it for their residual add.
+struct DownPart {
+    const uint8_t* w;
+    int n, nb, rpw, n_wg;  // rows (dim), blocks a row (ffn / 32), rows a workgroup, workgroups
+    const float* h;        // the SwiGLU row (ffn floats)
+    float* x;              // residual stream (the old values are read)
+    Fuse fz;               // pos, xout
+};
+constexpr int DOWN_R = 2;  // down rows a wave (16 a workgroup)
+
+template <typename KV, int HD, int R, int CPL, bool DOWN>
 __global__ __launch_bounds__(512) void qkv_attention_kernel(const uint8_t* __restrict__ W, int n, int nb, int rpw,
                                                             const float* __restrict__ X, float* __restrict__ Y, Fuse fz,
-                                                            AttArgs<KV> aa, int n_gemv, int n_att, OProj op) {
+                                                            AttArgs<KV> aa, int n_gemv, int n_att, OProj op,
+                                                            DownPart dp) {
     extern __shared__ i32x4 lds4[];
-    if ((int)blockIdx.x < n_gemv) {
-        gemv_fused_body<(int)WType::Q4_0, false, R, CPL, true, 8, PRO_RMSNORM, EPI_ROPE_KV, true>(
-            blockIdx.x, 0, lds4, W, n, nb, rpw, X, Y, fz);
-    } else if ((int)blockIdx.x < n_gemv + n_att) {
-        const int a = (int)blockIdx.x - n_gemv;
+    int b = (int)blockIdx.x;
+    if constexpr (DOWN) {
+        if (b < dp.n_wg) {
+            gemv_fused_body<(int)WType::Q4_0, false, DOWN_R, 8, true, 8, PRO_NONE, EPI_RESIDUAL, false, XIO_OUT>(
+                b, 0, lds4, dp.w, dp.n, dp.nb, dp.rpw, dp.h, dp.x, dp.fz);
+            return;
+        }
+        b -= dp.n_wg;
+    }
+    if (b < n_gemv) {
+        gemv_fused_body<(int)WType::Q4_0, false, R, CPL, true, 8, PRO_RMSNORM, EPI_ROPE_KV, true,
+                        DOWN ? XIO_IN : XIO_NONE>(b, 0, lds4, W, n, nb, rpw, X, Y, fz);
+    } else if (b < n_gemv + n_att) {
+        const int a = b - n_gemv;
         attention_body<KV, HD, true>(a % aa.n_heads, 0, a / aa.n_heads, reinterpret_cast<float*>(lds4), aa);
     } else {
-        o_proj_body<O_ROWS_PER_WAVE>((int)blockIdx.x - n_gemv - n_att, lds4, op, *fz.pos + 1, aa.err);
+        o_proj_body<O_ROWS_PER_WAVE>(b - n_gemv - n_att, lds4, op, *fz.pos + 1, aa.err);
     }
 }
 
@@ -1833,7 +1959,8 @@ hipError_t launch_qkv_attention(const uint8_t* w, size_t n, size_t k, const floa
                                 float eps, const int* pos, const float* cos_t, const float* sin_t, void* kc, void* vc,
                                 const int* kv_table, int n_heads, int n_kv, int hd, bool kv_f16, float* att_part,
                                 int nspan, int spans, int* att_cnt, float* att_out, uint64_t* xch, int* err,
-                                const uint8_t* wo, size_t n_o, float* x_res, uint64_t* oxch, hipStream_t s) {
+                                const uint8_t* wo, size_t n_o, float* x_res, uint64_t* oxch, hipStream_t s,
+                                const uint8_t* wd, size_t k_d, const float* h, uint64_t* xx) {
     const int nb = (int)(k / QK);
     const int cpl = cpl_for(nb);
     // the q/k/v launch's shape (launch_q4_0_fused_ex, EPI_ROPE_KV): row pairs, R rows a wave, 8 waves
@@ -1877,10 +2004,38 @@ hipError_t launch_qkv_attention(const uint8_t* w, size_t n, size_t k, const floa
         op.xch = oxch;
         n_ow = (int)((n_o + 8 * O_ROWS_PER_WAVE - 1) / (8 * O_ROWS_PER_WAVE));
     }
+    // the previous layer's down projection (optional, with the o projection):
+    // k rows of W_down over k_d columns (32-element blocks, an even count of
+    // at most 512), h its SwiGLU row; the new x goes through xx ([k] tagged
+    // words) to the q/k/v and o workgroups, which then read no x from memory
+    DownPart dp{};
+    size_t lds_d = 0;
+    if (wd) {
+        const int nb_d = (int)(k_d / QK);
+        if (!wo || k_d == 0 || k_d % QK || (nb_d & 1) || nb_d > 8 * 64 || h == nullptr || xx == nullptr ||
+            ((uintptr_t)h & 15) || (uint64_t)k * nb_d * Q4_0_BYTES > FUSED_MAX_WEIGHT_BYTES)
+            return hipErrorInvalidValue;
+        dp.w = wd;
+        dp.n = (int)k;
+        dp.nb = nb_d;
+        dp.rpw = 8 * DOWN_R;
+        dp.n_wg = (int)((k + dp.rpw - 1) / dp.rpw);
+        dp.h = h;
+        dp.x = x_res;
+        dp.fz.xstride = (int)k_d;
+        dp.fz.pos = pos;
+        dp.fz.xout = xx;
+        fz.xin = xx;
+        fz.err = err;
+        op.xin = xx;
+        lds_d = (size_t)8 * 16 * nb_d;
+    }
     const int n_att = n_heads * spans;
-    const dim3 grid((unsigned)(n_gemv + n_att + n_ow)), block(512);
-    // attention: q | per-wave contexts | current k | current v (f32); records of q/k/v's and o's x
-    const size_t lds = std::max({(size_t)8 * 16 * nb, (size_t)8 * 16 * nb_o, (size_t)(3 + ATT_WAVES) * hd * sizeof(float)});
+    const dim3 grid((unsigned)(dp.n_wg + n_gemv + n_att + n_ow)), block(512);
+    // attention: q | per-wave contexts | current k | current v (f32); records of q/k/v's, o's and down's x
+    const size_t lds = std::max({(size_t)8 * 16 * nb, (size_t)8 * 16 * nb_o,
+                                 (size_t)(3 + ATT_WAVES) * hd * sizeof(float), lds_d});
+    hipError_t attr = hipSuccess;
     auto go = [&](auto kv_tag, auto hd_tag, auto r_tag) {
         using KV = decltype(kv_tag);
         constexpr int HD = decltype(hd_tag)::value, R = decltype(r_tag)::value, CPL = R == 4 ? 2 : 4;
@@ -1902,8 +2057,17 @@ hipError_t launch_qkv_attention(const uint8_t* w, size_t n, size_t k, const floa
         aa.xch = xch;
         aa.oxch = wo ? oxch : nullptr;
         aa.err = err;
-        launch_kernel(qkv_attention_kernel<KV, HD, R, CPL>, grid, block, lds, s, w, (int)n, nb, rpw, x, y, fz, aa,
-                      n_gemv, n_att, op);
+        if (wd) {
+            const auto kern = qkv_attention_kernel<KV, HD, R, CPL, true>;
+            if (lds > 65536 &&
+                (attr = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                            (int)lds)) != hipSuccess)
+                return;
+            launch_kernel(kern, grid, block, lds, s, w, (int)n, nb, rpw, x, y, fz, aa, n_gemv, n_att, op, dp);
+        } else {
+            launch_kernel(qkv_attention_kernel<KV, HD, R, CPL, false>, grid, block, lds, s, w, (int)n, nb, rpw, x, y,
+                          fz, aa, n_gemv, n_att, op, dp);
+        }
     };
     using I64 = std::integral_constant<int, 64>;
     using I128 = std::integral_constant<int, 128>;
@@ -1915,6 +2079,7 @@ hipError_t launch_qkv_attention(const uint8_t* w, size_t n, size_t k, const floa
     } else {
         if (r == 4) go(0.0f, I64{}, R4{}); else go(0.0f, I64{}, R2{});
     }
+    if (attr != hipSuccess) return attr;
     return hipGetLastError();
 }
 

@@ -651,12 +651,19 @@ struct LlamaModel {
     float* att_part = nullptr;  // [max_batch][n_heads][spans of max_seq][hd + 2]
     int* att_cnt = nullptr;     // [max_batch][n_heads] finished-chunk counters (zero between launches)
     int att_nspan = 0;
-    // decode steps: attention fused into the q/k/v launch (fused layers, one row)
+    // decode steps: attention fused into the q/k/v launch (fused layers, one
+    // row), and the previous fused layer's down projection too (fused_down,
+    // off by default: on the 7B shape that launch, 24.6 us, took longer than
+    // the down GEMV and the fused launch apart, 8.6 + 14.5 us, because its
+    // one workgroup a CU leaves no room for q/k/v workgroups to stream their
+    // weights while the down projection runs)
     bool fused_attention = true;
+    bool fused_down = false;
     // [layer][xch_stride()] exchange of the fused decode launch: the q/k/v
-    // values, then the attention outputs (zero on an empty cache)
+    // values, the attention outputs, then the layer's input x when the
+    // previous layer's down projection runs in the launch (zero on an empty cache)
     uint64_t* att_xch = nullptr;
-    size_t xch_stride() const { return (size_t)qkv_dim + q_dim; }
+    size_t xch_stride() const { return (size_t)qkv_dim + q_dim + cfg.dim; }
     int* att_err = nullptr;  // set by a fused launch whose wait ran out
     rdl_llama_path_counts path{};  // attention launches enqueued, by kernel
     hipStream_t stream = nullptr;
@@ -809,29 +816,58 @@ struct LlamaModel {
         return hipGetLastError();
     }
 
+    // x += h . Wdown^T of fused layer l (h: its SwiGLU rows in hb)
+    hipError_t layer_down(int l, size_t m) {
+        const Layer& L = layers[l];
+        return launch_gemv_q4_0_fused_ex(L.down.dev, L.down.n, cfg.ffn_dim, hb, cfg.ffn_dim, m, x, 0, nullptr,
+                                         0.0f, 1, stream);
+    }
+
     // One layer through the fused Q4_0 launches (m <= 4): RMSNorm, RoPE + KV,
     // SwiGLU and the residual adds ride in the GEMV launches (prologue /
     // epilogue of the fused GEMV): five launches, three in a decode step
-    // (q/k/v, attention and o in one launch).
-    hipError_t layer_fused(int l, size_t m) {
+    // (q/k/v, attention and o in one launch), two when the previous layer's
+    // down projection joins that launch.  pending: a fused layer whose down
+    // projection has not run yet (its SwiGLU rows in hb), or -1; this call
+    // runs it and may leave its own layer's pending instead.
+    hipError_t layer_fused(int l, size_t m, int& pending) {
         const int d = cfg.dim;
         const float eps = cfg.norm_eps;
         Layer& L = layers[l];
         hipError_t e;
         if (m == 1 && fused_attention) {
             // q/k/v, RoPE + cache, the attention over the cache and the o
-            // projection with its residual add in one launch
+            // projection with its residual add in one launch (led by the
+            // pending down projection, whose new x reaches q/k/v and o through
+            // the exchange)
             uint64_t* xl = att_xch + (size_t)l * xch_stride();
-            e = launch_qkv_attention(L.qkv.dev, L.qkv.n, d, x, qkv, L.attn_norm, eps, pos, cos_t, sin_t,
-                                     kv_layer(kc, l), kv_layer(vc, l), kv_table, cfg.n_heads, cfg.n_kv_heads,
-                                     cfg.head_dim, cfg.kv_f16 != 0, att_part, att_nspan, chunks_needed(1), att_cnt,
-                                     att, xl, att_err, L.o.dev, L.o.n, x, xl + qkv_dim, stream);
-            if (e != hipErrorInvalidValue) {
+            for (int chain = pending >= 0 ? 1 : 0; chain >= 0; chain--) {
+                e = launch_qkv_attention(L.qkv.dev, L.qkv.n, d, x, qkv, L.attn_norm, eps, pos, cos_t, sin_t,
+                                         kv_layer(kc, l), kv_layer(vc, l), kv_table, cfg.n_heads, cfg.n_kv_heads,
+                                         cfg.head_dim, cfg.kv_f16 != 0, att_part, att_nspan, chunks_needed(1),
+                                         att_cnt, att, xl, att_err, L.o.dev, L.o.n, x, xl + qkv_dim, stream,
+                                         chain ? layers[pending].down.dev : nullptr, cfg.ffn_dim, hb,
+                                         xl + qkv_dim + q_dim);
+                if (e == hipErrorInvalidValue) {
+                    (void)hipGetLastError();
+                    if (chain) {  // a shape the joint launch does not take: the down on its own first
+                        if ((e = layer_down(pending, m)) != hipSuccess) return e;
+                        pending = -1;
+                    }
+                    continue;
+                }
                 if (e != hipSuccess) return e;
                 path.fused_decode++;
-                return layer_fused_tail(l, m, true);
+                if (chain) {
+                    path.fused_down++;
+                    pending = -1;
+                }
+                return layer_fused_tail(l, m, true, pending);
             }
-            (void)hipGetLastError();
+        }
+        if (pending >= 0) {
+            if ((e = layer_down(pending, m)) != hipSuccess) return e;
+            pending = -1;
         }
         // q = rope(rms_norm(x) . Wq^T); k, v -> cache (RoPE on k) in the same launch
         e = launch_gemv_q4_0_rope_kv(L.qkv.dev, L.qkv.n, d, x, m, qkv, L.attn_norm, eps, pos, cos_t,
@@ -840,11 +876,13 @@ struct LlamaModel {
         if (e != hipSuccess) return e;
         e = cfg.kv_f16 ? layer_attention<_Float16>(l, m, false) : layer_attention<float>(l, m, false);
         if (e != hipSuccess) return e;
-        return layer_fused_tail(l, m, false);
+        return layer_fused_tail(l, m, false, pending);
     }
 
-    // o (unless o_done), gate/up and down of a fused layer (after its attention)
-    hipError_t layer_fused_tail(int l, size_t m, bool o_done) {
+    // o (unless o_done), gate/up and down of a fused layer (after its
+    // attention); the down projection is left pending (for the next layer's
+    // fused decode launch) when that layer can take it
+    hipError_t layer_fused_tail(int l, size_t m, bool o_done, int& pending) {
         const int d = cfg.dim;
         const float eps = cfg.norm_eps;
         Layer& L = layers[l];
@@ -857,9 +895,13 @@ struct LlamaModel {
         // h = silu(gate) * up with [gate; up] = rms_norm(x) . Wgu^T (rows interleaved)
         e = launch_gemv_q4_0_fused_ex(L.gu.dev, L.gu.n, d, x, d, m, hb, 1, L.ffn_norm, eps, 2, stream);
         if (e != hipSuccess) return e;
-        // x += h . Wdown^T
-        return launch_gemv_q4_0_fused_ex(L.down.dev, L.down.n, cfg.ffn_dim, hb, cfg.ffn_dim, m, x, 0, nullptr,
-                                         0.0f, 1, stream);
+        // x += h . Wdown^T, now or in the next layer's launch
+        if (m == 1 && fused_attention && fused_down && l + 1 < cfg.n_layers && layers[l + 1].fused &&
+            !layers[l + 1].native) {
+            pending = l;
+            return hipSuccess;
+        }
+        return layer_down(l, m);
     }
 
     static bool kquant(const Mat& w) { return w.type == WType::Q4_K || w.type == WType::Q6_K; }
@@ -1038,10 +1080,18 @@ struct LlamaModel {
         hipError_t e = hipSuccess;
         if (embed && (e = launch_dequant_rows(emb.type, emb.dev, emb.n, emb.k, tokens, m, x, stream)) != hipSuccess)
             return e;
+        int pending = -1;  // a fused layer whose down projection has not run yet
         for (int l = 0; l < cfg.n_layers; l++) {
-            e = (m <= 4 && layers[l].fused && !layers[l].native) ? layer_fused(l, m) : layer_plain(l, m);
+            if (m <= 4 && layers[l].fused && !layers[l].native) {
+                e = layer_fused(l, m, pending);
+            } else {
+                if (pending >= 0 && (e = layer_down(pending, m)) != hipSuccess) return e;
+                pending = -1;
+                e = layer_plain(l, m);
+            }
             if (e != hipSuccess) return e;
         }
+        if (pending >= 0 && (e = layer_down(pending, m)) != hipSuccess) return e;
         // logits = rms_norm(x_last, norm) . Wout^T (the norm fused into the GEMV for Q4_0, Q4_K, Q6_K)
         if (fused_shapes && out.type == WType::Q4_0) {
             e = launch_gemv_q4_0_fused_ex(out.dev, out.n, d, x + (m - 1) * d, d, 1, logits, 1, final_norm, eps, 0,
@@ -1547,9 +1597,11 @@ rdl_status rdl_llama_generate_greedy(rdl_llama* model, const int32_t* prompt, si
 
 rdl_status rdl_llama_set_fused_attention(rdl_llama* model, int32_t enable) {
     if (!model) return api_fail(RDL_ERR_NULL_POINTER, "NULL model");
+    if (enable < 0 || enable > 2) return api_fail(RDL_ERR_INVALID_DATA, "fused-attention level %d (0, 1 or 2)", enable);
     rdl::LlamaModel& M = model->m;
-    if (M.fused_attention != (enable != 0)) {
+    if (M.fused_attention != (enable != 0) || M.fused_down != (enable == 2)) {
         M.fused_attention = enable != 0;
+        M.fused_down = enable == 2;
         // the captured decode step holds the other launches: capture again
         if (M.decode_exec) (void)hipGraphExecDestroy(M.decode_exec);
         if (M.decode_graph) (void)hipGraphDestroy(M.decode_graph);

@@ -252,13 +252,21 @@ hipError_t launch_gemv_q4_0_rope_kv(const uint8_t* w, size_t n, size_t k, const 
 // att W_o^T (W_o Q4_0, n_heads * hd columns), the attention outputs passing
 // through oxch (n_heads * hd tagged words, same rules as xch) instead of
 // att_out; the results equal the separate o launch's bit for bit.
+// With wd set as well, the launch starts with the previous layer's down
+// projection x_res[k] += h W_d^T (W_d Q4_0, k_d columns, h the SwiGLU row):
+// its results reach the q/k/v workgroups (whose weight loads run meanwhile)
+// and the o workgroups as tagged words through xx ([k], same rules as xch),
+// and x_res is written once, by the o projection; the results equal the
+// separate down launch's and this launch's without it bit for bit.
 // hipErrorInvalidValue for shapes it does not take (then use
 // launch_gemv_q4_0_rope_kv, the attention launch and the o launch).
 hipError_t launch_qkv_attention(const uint8_t* w, size_t n, size_t k, const float* x, float* y, const float* g,
                                 float eps, const int* pos, const float* cos_t, const float* sin_t, void* kc, void* vc,
                                 const int* kv_table, int n_heads, int n_kv, int hd, bool kv_f16, float* att_part,
                                 int nspan, int spans, int* att_cnt, float* att_out, uint64_t* xch, int* err,
-                                const uint8_t* wo, size_t n_o, float* x_res, uint64_t* oxch, hipStream_t s);
+                                const uint8_t* wo, size_t n_o, float* x_res, uint64_t* oxch, hipStream_t s,
+                                const uint8_t* wd = nullptr, size_t k_d = 0, const float* h = nullptr,
+                                uint64_t* xx = nullptr);
 
 // launch_gemv_q4_0_rope_kv for a Q4_K or Q6_K [Wq; Wk; Wv], or for the rows of
 // heads head0 .. head0 + n / hd - 1 of it (head0 = 0, or past the q heads:

@@ -45,7 +45,7 @@ _decl("rdl_llama_set_fused_attention", _i32, _p, _i32)
 
 
 class _PathCounts(C.Structure):
-    _fields_ = [(n, C.c_uint64) for n in ("fused_decode", "prefill_mfma", "prefill_rows", "attention")]
+    _fields_ = [(n, C.c_uint64) for n in ("fused_decode", "prefill_mfma", "prefill_rows", "attention", "fused_down")]
 
 
 _decl("rdl_llama_get_path_counts", _i32, _p, C.POINTER(_PathCounts))
@@ -156,9 +156,13 @@ class LlamaModel:
         check(lib.rdl_llama_position(self._h, C.byref(out)))
         return int(out.value)
 
-    def set_fused_attention(self, enable: bool) -> None:
-        """Decode steps' q/k/v projection, attention and o projection in one launch (default) or three."""
-        check(lib.rdl_llama_set_fused_attention(self._h, int(bool(enable))))
+    def set_fused_attention(self, level=1) -> None:
+        """Decode steps of fused layers: 1 (default, or True) q/k/v
+        projection, attention and o projection in one launch; 2 that launch
+        led by the previous layer's down projection; 0 (or False) q/k/v,
+        attention and o as three launches."""
+        level = 1 if level is True else 0 if level is False else int(level)
+        check(lib.rdl_llama_set_fused_attention(self._h, level))
 
     def set_native_q4_matmul(self, enabled: bool, layer: int = -1) -> None:
         """TransformerBlock::set_native_q4_matmul on one layer (layer=-1: all):
@@ -168,7 +172,8 @@ class LlamaModel:
 
     def path_counts(self) -> dict:
         """Attention launches enqueued so far, by kernel (host-side counts; a
-        captured decode graph counts once, at capture): fused_decode,
+        captured decode graph counts once, at capture): fused_decode (of
+        which fused_down were led by the previous layer's down projection),
         prefill_mfma, prefill_rows, attention."""
         c = _PathCounts()
         check(lib.rdl_llama_get_path_counts(self._h, C.byref(c)))

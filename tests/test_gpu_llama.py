@@ -239,6 +239,17 @@ def test_config5_shape_synthetic_weights(rq, gpu):
     assert m.path_counts()["fused_decode"] == c0["fused_decode"]
     for i, (f, u) in enumerate(zip(dec, dec3)):
         assert np.array_equal(f.view(np.uint32), u.view(np.uint32)), f"step {i}"
+    # (3) Each layer's down projection leading the next layer's fused launch
+    # (level 2; one workgroup a CU, the 256 down workgroups fill the device):
+    # the same logits, bit for bit.
+    m.reset()
+    m.set_fused_attention(2)
+    m.forward_with_cache(prompt)
+    dec2 = [m.decode_step(t) for t in a[:-1].tolist()]
+    m.set_fused_attention(1)
+    assert m.path_counts()["fused_down"] - c0["fused_down"] == len(dec2) * (cfg.n_layers - 1)
+    for i, (f, u) in enumerate(zip(dec, dec2)):
+        assert np.array_equal(f.view(np.uint32), u.view(np.uint32)), f"step {i} (level 2)"
 
 
 @pytest.mark.parametrize("kw", [
@@ -635,30 +646,39 @@ def test_fused_decode_two_rows_a_wave(rq, gpu, kv_f16, hd):
     attention launch two rows a wave and four block columns a lane
     (qkv_attention_kernel<KV, HD, 2, 4>): bit-equal to the q/k/v launch
     followed by the attention and o launches, and within the bar of the
-    oracle (f16 caches: K / V rounded alike), at 64+ cached keys."""
+    oracle (f16 caches: K / V rounded alike), at 64+ cached keys.  Also with
+    the first layer's down projection leading the second layer's launch
+    (level 2): 272 down workgroups ahead of 384 q/k/v workgroups that poll
+    its output (with head_dim 64 and an f16 cache two workgroups share a CU,
+    so the pollers start while the down workgroups still run)."""
     nh = 4096 // hd
     cfg = tiny_config(dim=4352, n_layers=2, n_heads=nh, n_kv_heads=nh // 4, head_dim=hd, ffn_dim=512,
                       vocab=320, max_seq=128, max_batch=64, kv_f16=kv_f16)
     print(f"case fused decode R=2 kv_f16={kv_f16} hd={hd}", flush=True)
     a, ref = build(cfg, seed=4352, centered=True)
     b, _ = build(cfg, seed=4352, centered=True)
+    c, _ = build(cfg, seed=4352, centered=True)
     b.set_fused_attention(False)
+    c.set_fused_attention(2)
     prompt = np.random.default_rng(4353).integers(0, cfg.vocab, 64)
-    la, lb = a.forward_with_cache(prompt), b.forward_with_cache(prompt)
+    la, lb, lc = a.forward_with_cache(prompt), b.forward_with_cache(prompt), c.forward_with_cache(prompt)
     want = ref.forward_with_cache(prompt)
     assert_close(la, want)
-    assert np.array_equal(la, lb)
-    c0 = a.path_counts()
+    assert np.array_equal(la, lb) and np.array_equal(la, lc)
+    c0, d0 = a.path_counts(), c.path_counts()
     tok = argmax(want)
     for _ in range(4):
-        la, lb = a.decode_step(tok), b.decode_step(tok)
+        la, lb, lc = a.decode_step(tok), b.decode_step(tok), c.decode_step(tok)
         want = ref.forward_with_cache([tok])
         assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+        assert np.array_equal(la.view(np.uint32), lc.view(np.uint32))
         assert_close(la, want)
         tok = argmax(want)
     assert a.path_counts()["fused_decode"] - c0["fused_decode"] == 4 * cfg.n_layers
+    assert c.path_counts()["fused_down"] - d0["fused_down"] == 4 * (cfg.n_layers - 1)
     assert b.path_counts()["fused_decode"] == 0
-    assert a.generate_greedy([tok], 5).tolist() == b.generate_greedy([tok], 5).tolist()
+    ga = a.generate_greedy([tok], 5).tolist()
+    assert ga == b.generate_greedy([tok], 5).tolist() == c.generate_greedy([tok], 5).tolist()
 
 
 def test_config5_head_grouping_against_oracle(rq, gpu):
@@ -784,26 +804,36 @@ def test_paged_cache_table_errors(rq, gpu):
     (dict(kv_f16=False, dim=128, n_heads=4, n_kv_heads=2, head_dim=64), 40),  # o input 256 > dim 128
 ])
 def test_fused_attention_equals_two_launches(rq, gpu, kw, n_prompt):
-    """Decode steps with the attention fused into the q/k/v launch give the
-    same logits, bit for bit, as the q/k/v launch followed by the attention
-    launch (eager steps and graph-replayed greedy steps; one to two spans of
-    512 keys)."""
+    """Decode steps with the attention fused into the q/k/v launch, with and
+    without the previous layer's down projection leading that launch, give
+    the same logits, bit for bit, as the q/k/v launch followed by the
+    attention launch (eager steps and graph-replayed greedy steps; one to two
+    spans of 512 keys)."""
     cfg = tiny_config(**kw)
     print(f"case fused attention {kw} prompt {n_prompt}", flush=True)
     a, _ = build(cfg, seed=61)
     b, _ = build(cfg, seed=61)
+    c, _ = build(cfg, seed=61)
     b.set_fused_attention(False)
+    c.set_fused_attention(2)
     prompt = np.random.default_rng(67).integers(0, cfg.vocab, n_prompt)
     for c0 in range(0, n_prompt, cfg.max_batch):
         la = a.forward_with_cache(prompt[c0:c0 + cfg.max_batch])
         lb = b.forward_with_cache(prompt[c0:c0 + cfg.max_batch])
-    assert np.array_equal(la, lb)
+        lc = c.forward_with_cache(prompt[c0:c0 + cfg.max_batch])
+    assert np.array_equal(la, lb) and np.array_equal(la, lc)
     tok = int(np.argmax(la))
+    p0 = c.path_counts()
     for _ in range(5):
-        la, lb = a.decode_step(tok), b.decode_step(tok)
+        la, lb, lc = a.decode_step(tok), b.decode_step(tok), c.decode_step(tok)
         assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+        assert np.array_equal(la.view(np.uint32), lc.view(np.uint32))
         tok = int(np.argmax(la))
-    assert a.generate_greedy([tok], 6).tolist() == b.generate_greedy([tok], 6).tolist()
+    p1 = c.path_counts()
+    assert p1["fused_down"] - p0["fused_down"] == 5 * (cfg.n_layers - 1)
+    assert a.path_counts()["fused_down"] == 0
+    ga = a.generate_greedy([tok], 6).tolist()
+    assert ga == b.generate_greedy([tok], 6).tolist() == c.generate_greedy([tok], 6).tolist()
 
 
 NATIVE_KIND = {"q4": "q4_native", "q4_1": "q4_1_native"}
