@@ -433,6 +433,25 @@ __device__ __forceinline__ float dot3(const uint32_t (&w)[8], const RF& x, int i
     const float t = fmaf((float)C, 1.0f / 256.0f, (float)B);
     return fmaf(t, 1.0f / 256.0f, (float)A);
 }
+// dot3(w, x, 0, 0, 0) with each digit's chain started by the three-address
+// v_dot4_i32_i8 on a zero accumulator (the compiler otherwise zeroes a
+// register for the two-address v_dot4c form: three moves a call)
+__device__ __forceinline__ int dot4z(uint32_t a, int b) {
+    int r;
+    asm("v_dot4_i32_i8 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+__device__ __forceinline__ float dot3z(const uint32_t (&w)[8], const RF& x) {
+    int A = dot4z(w[0], x.a0.x), B = dot4z(w[0], x.b0.x), C = dot4z(w[0], x.c0.x);
+    A = dot4(w[1], x.a0.y, A); A = dot4(w[2], x.a0.z, A); A = dot4(w[3], x.a0.w, A);
+    A = dot4(w[4], x.a1.x, A); A = dot4(w[5], x.a1.y, A); A = dot4(w[6], x.a1.z, A); A = dot4(w[7], x.a1.w, A);
+    B = dot4(w[1], x.b0.y, B); B = dot4(w[2], x.b0.z, B); B = dot4(w[3], x.b0.w, B);
+    B = dot4(w[4], x.b1.x, B); B = dot4(w[5], x.b1.y, B); B = dot4(w[6], x.b1.z, B); B = dot4(w[7], x.b1.w, B);
+    C = dot4(w[1], x.c0.y, C); C = dot4(w[2], x.c0.z, C); C = dot4(w[3], x.c0.w, C);
+    C = dot4(w[4], x.c1.x, C); C = dot4(w[5], x.c1.y, C); C = dot4(w[6], x.c1.z, C); C = dot4(w[7], x.c1.w, C);
+    const float t = fmaf((float)C, 1.0f / 256.0f, (float)B);
+    return fmaf(t, 1.0f / 256.0f, (float)A);
+}
 __device__ __forceinline__ int dot1(const uint32_t (&w)[8], const RN& x, int acc) {
     acc = dot4(w[0], x.q0.x, acc); acc = dot4(w[1], x.q0.y, acc);
     acc = dot4(w[2], x.q0.z, acc); acc = dot4(w[3], x.q0.w, acc);
@@ -1233,28 +1252,27 @@ __device__ __forceinline__ void store_slices(const float* rb, int r0, int n, flo
 // ---- Q4_K (float mode) ------------------------------------------------------------------
 // A unit is one 32-byte chunk of a super-block's nibbles: sub-block 2c (lo
 // nibbles) and 2c+1 (hi nibbles) of super-block sb (parser.rs:574-589).
-__device__ __forceinline__ void q4k_scale_min(const u32x4& h, int c, int& sc1, int& mn1, int& sc2,
-                                              int& mn2) {
-    // both forms, then a select: no branch on the lane's chunk index, so the
-    // rows of a wave stay one straight-line block each
-    const uint32_t j1 = 2 * (c & 1);  // byte of sub-block 2c within its group of four
-    // j < 4: sc = s[j] & 63, mn = s[j+4] & 63                        (parser.rs:565-566)
-    const uint32_t a_sc1 = (h.y >> (8 * j1)) & 63, a_sc2 = (h.y >> (8 * (j1 + 1))) & 63;
-    const uint32_t a_mn1 = (h.z >> (8 * j1)) & 63, a_mn2 = (h.z >> (8 * (j1 + 1))) & 63;
-    // j >= 4, i = j-4: sc = ((s[i]>>6)&3) | ((s[i+8]&0xF)<<2),
-    //                  mn = ((s[i+4]>>6)&3) | ((s[i+8]>>4)<<2)       (parser.rs:567-568)
-    const uint32_t si1 = h.y >> (8 * j1), si2 = h.y >> (8 * (j1 + 1));
-    const uint32_t ti1 = h.z >> (8 * j1), ti2 = h.z >> (8 * (j1 + 1));
-    const uint32_t ui1 = h.w >> (8 * j1), ui2 = h.w >> (8 * (j1 + 1));
-    const uint32_t b_sc1 = ((si1 >> 6) & 3) | ((ui1 & 0xF) << 2);
-    const uint32_t b_sc2 = ((si2 >> 6) & 3) | ((ui2 & 0xF) << 2);
-    const uint32_t b_mn1 = ((ti1 >> 6) & 3) | (((ui1 >> 4) & 0xF) << 2);
-    const uint32_t b_mn2 = ((ti2 >> 6) & 3) | (((ui2 >> 4) & 0xF) << 2);
-    const bool lo = c < 2;
-    sc1 = (int)(lo ? a_sc1 : b_sc1);
-    sc2 = (int)(lo ? a_sc2 : b_sc2);
-    mn1 = (int)(lo ? a_mn1 : b_mn1);
-    mn2 = (int)(lo ? a_mn2 : b_mn2);
+// The same four 6-bit values packed as bytes {sc1, sc2, mn1, mn2}, for a lane
+// whose chunk c is fixed: Q4kSel holds its byte selectors, so a row costs two
+// byte permutes and a few packed-byte operations (both forms, then a select).
+struct Q4kSel {
+    uint32_t p, w;  // v_perm selectors: {s[b], s[b+1], s[b+4], s[b+5]}, {s[b+8], s[b+9]} twice
+    uint32_t hi;    // all ones when c >= 2: the split form (parser.rs:567-568)
+};
+__device__ __forceinline__ Q4kSel q4k_sel(int c) {
+    const uint32_t b = 2 * (c & 1);
+    return Q4kSel{b | (b + 1) << 8 | (b + 4) << 16 | (b + 5) << 24, b | (b + 1) << 8 | b << 16 | (b + 1) << 24,
+                  c >= 2 ? ~0u : 0u};
+}
+__device__ __forceinline__ uint32_t q4k_scales4(const u32x4& h, const Q4kSel& q) {
+    const uint32_t p = perm(h.z, h.y, q.p);  // s[b], s[b+1] (scales), s[b+4], s[b+5] (mins)
+    const uint32_t w = perm(h.w, h.w, q.w);  // s[b+8], s[b+9], s[b+8], s[b+9]
+    // j < 4: the low 6 bits                                           (parser.rs:565-566)
+    const uint32_t lo = p & 0x3F3F3F3Fu;
+    // j >= 4: the top 2 bits of s[i] / s[i+4] and a nibble of s[i+8]  (parser.rs:567-568)
+    const uint32_t top = (p >> 6) & 0x03030303u;
+    const uint32_t nib = (w & 0x00000F0Fu) | ((w >> 4) & 0x0F0F0000u);
+    return ((top | (nib << 2)) & q.hi) | (lo & ~q.hi);  // a bit select, no branch
 }
 
 // Loads of Q4_K rows in flight ahead of the arithmetic (both Q4_K kernels).
@@ -1343,6 +1361,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_q4k_fused_kernel(const uint8_t* 
         const int sb = u >> 2, c = u & 3;
         const RF x1 = read_rf(lds4, nb, sb * 8 + 2 * c);
         const RF x2 = read_rf(lds4, nb, sb * 8 + 2 * c + 1);
+        const Q4kSel qs = q4k_sel(c);
+        const float s2h = x2.S * 0.0625f;  // the high nibbles enter as 16 (h - 8)
 #pragma unroll
         for (int r = 0; r < R; r++) {
             if (r + P0 < R) issue(r + P0);
@@ -1352,24 +1372,26 @@ __global__ __launch_bounds__(NW * 64) void gemv_q4k_fused_kernel(const uint8_t* 
             const int sl = r % NS;
             asm volatile("" : "+v"(hdr[sl]), "+v"(qa[sl]), "+v"(qb[sl]));
             const uint32_t raw[8] = {qa[sl].x, qa[sl].y, qa[sl].z, qa[sl].w, qb[sl].x, qb[sl].y, qb[sl].z, qb[sl].w};
+            // low nibbles as bytes 0..15; high nibbles h in place as the signed
+            // bytes 16 (h - 8) (one bitop3 a word), with sum h x = sum 16 (h - 8)
+            // x / 16 + 8 sum x
             uint32_t lo[8], hi[8];
 #pragma unroll
             for (int k = 0; k < 8; k++) {
                 lo[k] = raw[k] & NIB;
-                hi[k] = (raw[k] >> 4) & NIB;
+                hi[k] = (raw[k] & ~NIB) ^ 0x80808080u;
             }
             const float d = h2f(hdr[sl].x & 0xFFFFu);
             const float dmin = h2f(hdr[sl].x >> 16);
-            int sc1, mn1, sc2, mn2;
-            q4k_scale_min(hdr[sl], c, sc1, mn1, sc2, mn2);
+            const uint32_t sm = q4k_scales4(hdr[sl], qs);
             // element value (d*sc)*q - (dmin*mn)   (parser.rs:577-587)
-            const float d1 = d * (float)sc1, m1 = dmin * (float)mn1;
-            const float d2 = d * (float)sc2, m2 = dmin * (float)mn2;
+            const float d1 = d * (float)(sm & 0xFFu), m1 = dmin * (float)((sm >> 16) & 0xFFu);
+            const float d2 = d * (float)((sm >> 8) & 0xFFu), m2 = dmin * (float)(sm >> 24);
             float a = acc[r];
-            a = fmaf(d1 * x1.S, dot3(lo, x1, 0, 0, 0), a);
+            a = fmaf(d1 * x1.S, dot3z(lo, x1), a);
             a = fmaf(-m1, x1.xsum, a);
-            a = fmaf(d2 * x2.S, dot3(hi, x2, 0, 0, 0), a);
-            a = fmaf(-m2, x2.xsum, a);
+            a = fmaf(d2 * s2h, dot3z(hi, x2), a);
+            a = fmaf(fmaf(8.0f, d2, -m2), x2.xsum, a);
             acc[r] = a;
             if constexpr (R > 4) asm volatile("" : "+v"(acc[r]));  // row r done before row r + P0 + 1 issues
             __builtin_amdgcn_sched_barrier(0);  // one row at a time, in load order
@@ -1486,6 +1508,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_q4k_splitk_kernel(const uint8_t*
         const int sb = u >> 2, c = u & 3;
         const RF x1 = read_rf(lds4, nb, sb * 8 + 2 * c);
         const RF x2 = read_rf(lds4, nb, sb * 8 + 2 * c + 1);
+        const Q4kSel qs = q4k_sel(c);
+        const float s2h = x2.S * 0.0625f;  // the high nibbles enter as 16 (h - 8)
 #pragma unroll
         for (int r = 0; r < R; r++) {
             if (r + AH < R) issue(r + AH);
@@ -1494,24 +1518,26 @@ __global__ __launch_bounds__(NW * 64) void gemv_q4k_splitk_kernel(const uint8_t*
             // compiler from hoisting every row's scale work above the first dot)
             asm volatile("" : "+v"(hdr[r]), "+v"(qa[r]), "+v"(qb[r]));
             const uint32_t raw[8] = {qa[r].x, qa[r].y, qa[r].z, qa[r].w, qb[r].x, qb[r].y, qb[r].z, qb[r].w};
+            // low nibbles as bytes 0..15; high nibbles h in place as the signed
+            // bytes 16 (h - 8) (one bitop3 a word), with sum h x = sum 16 (h - 8)
+            // x / 16 + 8 sum x
             uint32_t lo[8], hi[8];
 #pragma unroll
             for (int k = 0; k < 8; k++) {
                 lo[k] = raw[k] & NIB;
-                hi[k] = (raw[k] >> 4) & NIB;
+                hi[k] = (raw[k] & ~NIB) ^ 0x80808080u;
             }
             const float d = h2f(hdr[r].x & 0xFFFFu);
             const float dmin = h2f(hdr[r].x >> 16);
-            int sc1, mn1, sc2, mn2;
-            q4k_scale_min(hdr[r], c, sc1, mn1, sc2, mn2);
+            const uint32_t sm = q4k_scales4(hdr[r], qs);
             // element value (d*sc)*q - (dmin*mn)   (parser.rs:577-587)
-            const float d1 = d * (float)sc1, m1 = dmin * (float)mn1;
-            const float d2 = d * (float)sc2, m2 = dmin * (float)mn2;
+            const float d1 = d * (float)(sm & 0xFFu), m1 = dmin * (float)((sm >> 16) & 0xFFu);
+            const float d2 = d * (float)((sm >> 8) & 0xFFu), m2 = dmin * (float)(sm >> 24);
             float a = acc[r];
-            a = fmaf(d1 * x1.S, dot3(lo, x1, 0, 0, 0), a);
+            a = fmaf(d1 * x1.S, dot3z(lo, x1), a);
             a = fmaf(-m1, x1.xsum, a);
-            a = fmaf(d2 * x2.S, dot3(hi, x2, 0, 0, 0), a);
-            a = fmaf(-m2, x2.xsum, a);
+            a = fmaf(d2 * s2h, dot3z(hi, x2), a);
+            a = fmaf(fmaf(8.0f, d2, -m2), x2.xsum, a);
             acc[r] = a;
             // one row at a time, in load order: row r's arithmetic runs while
             // the loads of rows r + 1 .. are still arriving
