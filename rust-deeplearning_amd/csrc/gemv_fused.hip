@@ -103,10 +103,10 @@ __device__ void prep_float_lds(const f32x4 (&xv)[PI], int nb, int* __restrict__ 
         if (j * NT >= nb * 8) break;  // uniform
         const int c = p >> 3, k = p & 7;
         const f32x4 v = xv[j];
-        const bool bad = !(isfinite(v.x) && isfinite(v.y) && isfinite(v.z) && isfinite(v.w));
-        float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-        amax = max8_f32(amax);
-        const int anybad = sum8_i32(bad ? 1 : 0);
+        // the block's largest magnitude; an Inf or NaN shows as bits >= 0x7F800000
+        const uint32_t ab = max8_u32(max(max(abs_bits(v.x), abs_bits(v.y)), max(abs_bits(v.z), abs_bits(v.w))));
+        const bool anybad = ab >= 0x7F800000u;
+        const float amax = __builtin_bit_cast(float, ab);
         // scale tiny blocks by 2^64 so that 8323072/amax stays finite (exact)
         // (the reciprocal's 1 ulp keeps |t| within 8323075, far inside the digits' range)
         const float pw = (amax < 0x1p-60f) ? 0x1p64f : 1.0f;
@@ -307,15 +307,13 @@ __device__ void prep_float4_lds(const f32x4 (&xv)[PI][2], const f32x4 (&av)[PI][
                 }
             }
         }
-        bool bad = false;
-        float amax = 0.0f;
+        // the block's largest magnitude; an Inf or NaN shows as bits >= 0x7F800000
+        uint32_t ab = 0;
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            bad |= !isfinite(v[i]);
-            amax = fmaxf(amax, fabsf(v[i]));
-        }
-        amax = max4_f32(amax);
-        const int anybad = sum4_i32(bad ? 1 : 0);
+        for (int i = 0; i < 8; i++) ab = max(ab, abs_bits(v[i]));
+        ab = max4_u32(ab);
+        const bool anybad = ab >= 0x7F800000u;
+        const float amax = __builtin_bit_cast(float, ab);
         // 7829364 / amax through the reciprocal (1 ulp): |t| <= 7829366, one
         // code inside the digits' range 0x777777 = 7829367
         const float pw = (amax < 0x1p-60f) ? 0x1p64f : 1.0f;

@@ -68,9 +68,12 @@ constexpr int DPP_QUAD_XOR2 = 0x4E;        // quad_perm [2,3,0,1]: lane i <- i^2
 constexpr int DPP_ROW_HALF_MIRROR = 0x141; // lane i <- 7-i within each 8 lanes
 constexpr int DPP_ROW_MIRROR = 0x140;      // lane i <- 15-i within each 16 lanes
 
+// Every pattern used here reads a lane of the same row, so no lane takes the
+// out-of-bounds value; bound_ctrl lets the compiler fold the move into the
+// instruction that consumes it (v_add_f32_dpp, v_max_u32_dpp, ...).
 template <int CTRL>
 __device__ __forceinline__ int dpp_i32(int v) {
-    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, true);
 }
 template <int CTRL>
 __device__ __forceinline__ float dpp_f32(float v) {
@@ -93,6 +96,19 @@ __device__ __forceinline__ float max4_f32(float v) {
     v = fmaxf(v, dpp_f32<DPP_QUAD_XOR1>(v));
     return fmaxf(v, dpp_f32<DPP_QUAD_XOR2>(v));
 }
+// Maximum of non-negative float bit patterns as unsigned integers: the same
+// order as the floats for finite values, and an Inf or NaN in the group
+// comes out on top (>= 0x7F800000), so one reduction gives both the largest
+// magnitude and whether the group holds a non-finite value.
+__device__ __forceinline__ uint32_t max4_u32(uint32_t v) {
+    v = max(v, (uint32_t)dpp_i32<DPP_QUAD_XOR1>((int)v));
+    return max(v, (uint32_t)dpp_i32<DPP_QUAD_XOR2>((int)v));
+}
+__device__ __forceinline__ uint32_t max8_u32(uint32_t v) {
+    v = max4_u32(v);
+    return max(v, (uint32_t)dpp_i32<DPP_ROW_HALF_MIRROR>((int)v));
+}
+__device__ __forceinline__ uint32_t abs_bits(float x) { return __builtin_bit_cast(uint32_t, x) & 0x7FFFFFFFu; }
 __device__ __forceinline__ int sum8_i32(int v) {
     v = sum4_i32(v);
     return v + dpp_i32<DPP_ROW_HALF_MIRROR>(v);
