@@ -366,12 +366,21 @@ __device__ __forceinline__ RF4 read_rf4(const i32x4* __restrict__ l4, int nb, in
     return r;
 }
 
+// The three-address v_dot8_i32_i4 on a zero accumulator: the first product
+// of a chain (the compiler otherwise zeroes a register for the two-address
+// v_dot8c form).
+__device__ __forceinline__ int dot8z(uint32_t a, int b) {
+    int r;
+    asm("v_dot8_i32_i4 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+
 // sum_j w_j * t_j for signed int4 weight nibbles w (four dwords), as a float.
 __device__ __forceinline__ float dot_i4(const uint32_t (&w)[4], const RF4& x) {
     int D[6];
 #pragma unroll
     for (int lv = 0; lv < 6; lv++) {
-        int a = __builtin_amdgcn_sdot8((int)w[0], x.lv[lv].x, 0, false);
+        int a = dot8z(w[0], x.lv[lv].x);
         a = __builtin_amdgcn_sdot8((int)w[1], x.lv[lv].y, a, false);
         a = __builtin_amdgcn_sdot8((int)w[2], x.lv[lv].z, a, false);
         D[lv] = __builtin_amdgcn_sdot8((int)w[3], x.lv[lv].w, a, false);
