@@ -523,7 +523,7 @@ struct BlockDot<(int)WType::Q8_0, false> {
 #pragma unroll
         for (int k = 0; k < 8; k++) q[k] = perm(w[k + 1], w[k], sel);
         const float d = h2f((w[0] >> dsh) & 0xFFFFu);
-        return (x.S * d) * dot3(q, x, 0, 0, 0);
+        return (x.S * d) * dot3z(q, x);
     }
 };
 template <>
@@ -537,7 +537,7 @@ struct BlockDot<(int)WType::Q4_1, false> {
             q[k + 4] = (w[k + 1] >> 4) & NIB;
         }
         const float d = h2f(w[0] & 0xFFFFu), m = h2f(w[0] >> 16);
-        return fmaf(x.S * d, dot3(q, x, 0, 0, 0), m * x.xsum);
+        return fmaf(x.S * d, dot3z(q, x), m * x.xsum);
     }
 };
 template <>
