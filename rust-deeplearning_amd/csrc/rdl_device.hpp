@@ -213,11 +213,16 @@ __device__ __forceinline__ uint32_t q6k_sel(uint32_t run) { return (run & 2) ? 0
 // The 32 codes (0..63) of a unit as 8 dwords of bytes (dword k: elements 4k..4k+3).
 __device__ __forceinline__ void q6k_codes(const uint32_t (&wl)[9], const uint32_t (&wh)[9], uint32_t sel, int t,
                                           uint32_t (&q)[8]) {
-    const uint32_t nsh = 4 * (uint32_t)(t >> 1), hsh = 2 * (uint32_t)t;
+    const uint32_t nsh = 4 * (uint32_t)(t >> 1);
+    // the 2-bit field at bits 2t, 2t+1 of each qh byte moves to bits 4, 5 by
+    // one rotation of the dword (right by 2t - 4, i.e. left by 4 - 2t): no bit
+    // that lands there crosses a byte
+    const uint32_t rot = (2 * (uint32_t)t + 28) & 31;
 #pragma unroll
     for (int k = 0; k < 8; k++) {
         const uint32_t lo = perm(wl[k + 1], wl[k], sel), hi = perm(wh[k + 1], wh[k], sel);
-        q[k] = ((lo >> nsh) & 0x0F0F0F0Fu) | (((hi >> hsh) & 0x03030303u) << 4);
+        const uint32_t h2 = __builtin_amdgcn_alignbit(hi, hi, rot) & 0x30303030u;
+        q[k] = ((lo >> nsh) & 0x0F0F0F0Fu) | h2;
     }
 }
 
