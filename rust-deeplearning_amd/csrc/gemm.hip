@@ -778,6 +778,19 @@ __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_kernel(
                     }
                 }
             }
+            if constexpr (!NATIVE && !SUMS && !Q6 && FI * FJ == 16 && KB == 1) {
+                // the 128 x 128 tile: each tile's two MFMAs followed by four
+                // VALU instructions (the previous tile's scale FMAs).  The
+                // scheduler otherwise issues all 32 of a block's MFMAs first,
+                // keeping every product live at once, and spills (256 -> 230
+                // VGPRs, no scratch; M = 2048 309-313 -> 323-326 TFLOP/s; the
+                // 128 x 64 tile measured 1-2 % slower with it)
+#pragma unroll
+                for (int p = 0; p < FI * FJ; p++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+                }
+            }
         }
     };
 
