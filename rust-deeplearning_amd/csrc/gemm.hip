@@ -299,8 +299,13 @@ struct GemmCfg {
     static constexpr int TJ = WJ * FJ * 16;
     static constexpr int TI = WI * FI * 16;
     static constexpr int CB = KB * KS;                      // blocks per chunk
-    // weight rows: 16 nibble bytes a block (Q6_K, Q8_0: 32 codes as bytes), padded
-    static constexpr int WNS = wf_bytes(WF) ? CB * 32 + 8 : Lds<CB>::WN_STRIDE;
+    // Q4_0 float mode, 128 x 128 tile: the weights staged as the MFMA's f16
+    // (q - 8) operands, converted once a chunk by the staging threads rather
+    // than by each of the WI waves that read a weight tile
+    static constexpr bool AF16 = !NATIVE && WF == WF_Q4_0 && FJ * FI == 16;
+    // weight rows: 16 nibble bytes a block (Q6_K, Q8_0: 32 codes as bytes;
+    // AF16: 32 f16 operands, the x rows' stride), padded
+    static constexpr int WNS = AF16 ? Lds<CB>::X_STRIDE : wf_bytes(WF) ? CB * 32 + 8 : Lds<CB>::WN_STRIDE;
     static constexpr int WN_BYTES = TJ * WNS;
     // Q4_0, Q8_0: the f16 d of each (row, block); Q4_K: f32 pairs {d sc,
     // 8 d sc - dmin mn}; Q6_K: {d sc0, d sc1} of the block's two sub-blocks;
@@ -642,9 +647,21 @@ __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_kernel(
                 lo.y = perm(r.w[u][2], r.w[u][1], sel);
                 hi.x = perm(r.w[u][3], r.w[u][2], sel);
                 hi.y = perm(w4, r.w[u][3], sel);
-                uint2* dst = reinterpret_cast<uint2*>(wn + jl * Lds<CB>::WN_STRIDE + bl * 16);
-                dst[0] = lo;
-                dst[1] = hi;
+                if constexpr (C::AF16) {
+                    // elements 8 g .. 8 g + 7 at 16 g: the low nibbles of bytes
+                    // 0-7, 8-15, then the high ones (rows or blocks past the
+                    // matrix: codes -8 with d = 0)
+                    constexpr uint32_t NIB = 0x0F0F0F0Fu;
+                    half8_t* dst = reinterpret_cast<half8_t*>(wn + jl * C::WNS + bl * 64);
+                    dst[0] = q_f16(lo.x & NIB, lo.y & NIB);
+                    dst[1] = q_f16(hi.x & NIB, hi.y & NIB);
+                    dst[2] = q_f16((lo.x >> 4) & NIB, (lo.y >> 4) & NIB);
+                    dst[3] = q_f16((hi.x >> 4) & NIB, (hi.y >> 4) & NIB);
+                } else {
+                    uint2* dst = reinterpret_cast<uint2*>(wn + jl * Lds<CB>::WN_STRIDE + bl * 16);
+                    dst[0] = lo;
+                    dst[1] = hi;
+                }
                 wd[bl * C::TJ + jl] = (uint16_t)dbits;  // block-major: a lane's four rows are adjacent
             }
         }
@@ -709,6 +726,8 @@ __global__ __launch_bounds__(WJ * WI * KS * 64) void gemm_q4_0_kernel(
                     // lane group g: codes (+ 128) of elements 8 g .. 8 g + 7
                     const uint2 c8 = *reinterpret_cast<const uint2*>(wn + (jt + r16) * C::WNS + bl * 32 + 8 * g);
                     aq[a] = q_f16<128>(c8.x, c8.y);
+                } else if constexpr (C::AF16) {
+                    aq[a] = *reinterpret_cast<const half8_t*>(wn + (jt + r16) * C::WNS + bl * 64 + 16 * g);
                 } else {
                     const uint2 nb8 = *reinterpret_cast<const uint2*>(wn + (jt + r16) * C::WNS + bl * 16 + 8 * (g & 1));
                     const uint32_t sh = (g >> 1) * 4;  // groups 2, 3: high nibbles
