@@ -1287,7 +1287,8 @@ constexpr int Q4K_AHEAD = 2;
 // gemv_q4k_splitk_kernel: rows issued before the activation prep, rows in
 // flight after it (4096 x 14336 on MI355X, us a launch: 2 / 2 9.80, 2 / 4
 // 9.72, 2 / 3 9.81, 1 / 2 10.30, 1 / 3 9.95, 1 / 4 9.87; 3 / 3 10.9 and 4 / 4
-// 12.6: weight loads ahead of the prep delay every CU's activation)
+// 12.6: weight loads ahead of the prep delay every CU's activation; with the
+// leaner dot and prep code since: 1 / 4 9.04, 2 / 4 8.88-8.91, 3 / 4 10.1)
 constexpr int Q4K_SPLIT_PRE = 2, Q4K_SPLIT_AHEAD = 4;
 
 // Q4_K rows of at most 64 units (K <= 4096): lane u takes unit u of R rows
