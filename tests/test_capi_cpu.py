@@ -15,6 +15,15 @@ def test_exports_every_declared_symbol(rq):
     assert not missing, missing
 
 
+def test_integration_names_every_declared_symbol(rq):
+    """The integration guide's entry point index covers every function
+    the headers declare (a new entry point needs its row there)."""
+    import os
+    doc = open(os.path.join(os.path.dirname(__file__), "..", "INTEGRATION.md")).read()
+    unnamed = [n for n in rq.declared_symbols() if n not in doc]
+    assert not unnamed, unnamed
+
+
 def test_status_strings(rq):
     for code in range(14):
         assert rq.lib.rdl_status_string(code)
